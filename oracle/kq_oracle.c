@@ -1,0 +1,376 @@
+/*
+ * kq_oracle.c -- CPU restatement of stratum's scalar k-quant routines.
+ *
+ * TEST INFRASTRUCTURE ONLY (see kq_oracle.h).  Build with
+ *   gcc -O2 -std=c11 -ffp-contract=off -fno-fast-math
+ * so that every binary32 product and sum rounds where the reference's C
+ * source rounds it (x86-64 without -mfma never contracts anyway).
+ *
+ * The arithmetic follows the reference statement by statement; the code
+ * is organised by 32- or 16-weight sub-block rather than by the
+ * reference's pointer walks.  Reference lines are cited per function.
+ */
+#define _GNU_SOURCE
+#include "kq_oracle.h"
+
+#include <pthread.h>
+#include <stdatomic.h>
+#include <stdlib.h>
+#include <string.h>
+
+int ko_block_bytes(int type) {
+    switch (type) {   /* stratum_gguf.h:57-79 */
+    case KO_Q2_K: return 84;
+    case KO_Q4_K: return 144;
+    case KO_Q6_K: return 210;
+    case KO_Q2K_NIB: return 148;
+    default: return 0;
+    }
+}
+
+static uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* Exact IEEE binary16 -> binary32 widening (stratum_q4k.h:24-55):
+ * zero, subnormal (renormalised), normal, inf and NaN (payload << 13). */
+float ko_fp16_to_fp32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    int e = (h >> 10) & 31;
+    uint32_t frac = h & 0x3ffu;
+    uint32_t bits;
+    if (e == 31) {
+        bits = sign | 0x7f800000u | (frac << 13);
+    } else if (e != 0) {
+        bits = sign | ((uint32_t)(e + 112) << 23) | (frac << 13);
+    } else if (frac == 0) {
+        bits = sign;
+    } else {
+        /* subnormal: shift the leading one up to bit 10 */
+        int shift = 0;
+        while (!(frac & 0x400u)) { frac <<= 1; shift++; }
+        bits = sign | ((uint32_t)(113 - shift) << 23) | ((frac & 0x3ffu) << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* 6-bit scale and min of Q4_K sub-block j (0..7) from the 12 packed bytes
+ * (stratum_q4k.h:57-65).  Sub-blocks 0..3 keep their low six bits in bytes
+ * 0..3 (scale) and 4..7 (min); sub-blocks 4..7 take a nibble from bytes
+ * 8..11 and their top two bits from the high bits of bytes 0..7. */
+void ko_q4k_scale_min(int j, const uint8_t* s, uint8_t* sc, uint8_t* m) {
+    if (j < 4) {
+        *sc = (uint8_t)(s[j] & 0x3f);
+        *m = (uint8_t)(s[4 + j] & 0x3f);
+    } else {
+        int t = j - 4;
+        *sc = (uint8_t)((s[8 + t] & 0x0f) | ((s[t] >> 6) << 4));
+        *m = (uint8_t)((s[8 + t] >> 4) | ((s[4 + t] >> 6) << 4));
+    }
+}
+
+/* ---------------------------------------------------------------- Q4_K */
+/* block_q4_K (stratum_q4k.h:16-22): d@0, dmin@2, scales[12]@4, qs[128]@16.
+ * Sub-block s (32 weights, positions 32s..32s+31) reads qs bytes
+ * 32*(s/2) .. +31, low nibble for even s, high nibble for odd s. */
+static inline int q4k_q(const uint8_t* blk, int s, int l) {
+    uint8_t b = blk[16 + 32 * (s >> 1) + l];
+    return (s & 1) ? (b >> 4) : (b & 0x0f);
+}
+
+static void q4k_dequant_block(const uint8_t* blk, float* y) {
+    /* stratum_q4k.h:67-84: y = fl(fl(d*sc)*q) - fl(dmin*m) */
+    const float d = ko_fp16_to_fp32(rd16(blk));
+    const float dmin = ko_fp16_to_fp32(rd16(blk + 2));
+    for (int s = 0; s < 8; s++) {
+        uint8_t sc, m;
+        ko_q4k_scale_min(s, blk + 4, &sc, &m);
+        const float ds = d * (float)sc;
+        const float dm = dmin * (float)m;
+        for (int l = 0; l < 32; l++) y[32 * s + l] = ds * (float)q4k_q(blk, s, l) - dm;
+    }
+}
+
+static double q4k_dot(const uint8_t* row, int K, const float* x) {
+    /* stratum_q4k.h:95-131 */
+    double dot = 0.0;
+    for (int b = 0; b < K / 256; b++) {
+        const uint8_t* blk = row + (size_t)b * 144;
+        const float* xb = x + (size_t)b * 256;
+        const float d = ko_fp16_to_fp32(rd16(blk));
+        const float dmin = ko_fp16_to_fp32(rd16(blk + 2));
+        for (int s = 0; s < 8; s++) {
+            uint8_t sc, m;
+            ko_q4k_scale_min(s, blk + 4, &sc, &m);
+            const float ds = d * (float)sc;
+            const float dm = dmin * (float)m;
+            float acc = 0.0f, xsum = 0.0f;
+            for (int l = 0; l < 32; l++) {
+                acc += (float)q4k_q(blk, s, l) * xb[32 * s + l];
+                xsum += xb[32 * s + l];
+            }
+            dot += (double)(ds * acc - dm * xsum);
+        }
+    }
+    return dot;
+}
+
+/* ---------------------------------------------------------------- Q6_K */
+/* block_q6_K (stratum_q6k.h:9-15): ql[128]@0, qh[64]@128, int8
+ * scales[16]@192, d@208.  Position p = 128h + 32t + l (h half, t 0..3,
+ * l 0..31): low four bits from ql[64h + l + 32(t&1)] (nibble t>>1), high
+ * two bits from qh[32h + l] bits 2t..2t+1, value minus 32; scale index
+ * 8h + 2t + l/16. */
+static inline int q6k_q(const uint8_t* blk, int h, int t, int l) {
+    uint8_t lo = blk[64 * h + l + 32 * (t & 1)];
+    uint8_t hi = blk[128 + 32 * h + l];
+    int q = ((lo >> (4 * (t >> 1))) & 0x0f) | (((hi >> (2 * t)) & 3) << 4);
+    return q - 32;
+}
+
+static void q6k_dequant_block(const uint8_t* blk, float* y) {
+    /* stratum_q6k.h:17-36: y = fl(fl(d*s)*q) */
+    const float d = ko_fp16_to_fp32(rd16(blk + 208));
+    const int8_t* sc = (const int8_t*)(blk + 192);
+    for (int h = 0; h < 2; h++)
+        for (int t = 0; t < 4; t++)
+            for (int l = 0; l < 32; l++)
+                y[128 * h + 32 * t + l] =
+                    d * (float)sc[8 * h + 2 * t + l / 16] * (float)q6k_q(blk, h, t, l);
+}
+
+static double q6k_dot(const uint8_t* row, int K, const float* x) {
+    /* stratum_q6k.h:38-73: eight binary32 sums of 16 products per half,
+     * then dot += ((double)d * (double)s) * (double)a in (is, t) order. */
+    double dot = 0.0;
+    for (int b = 0; b < K / 256; b++) {
+        const uint8_t* blk = row + (size_t)b * 210;
+        const float* xb = x + (size_t)b * 256;
+        const float d = ko_fp16_to_fp32(rd16(blk + 208));
+        const int8_t* sc = (const int8_t*)(blk + 192);
+        for (int h = 0; h < 2; h++) {
+            float a[4][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}, {0.0f, 0.0f}, {0.0f, 0.0f}};
+            for (int l = 0; l < 32; l++)
+                for (int t = 0; t < 4; t++)
+                    a[t][l / 16] += (float)q6k_q(blk, h, t, l) * xb[128 * h + 32 * t + l];
+            for (int is = 0; is < 2; is++)
+                for (int t = 0; t < 4; t++)
+                    dot += (double)d * (double)sc[8 * h + is + 2 * t] * a[t][is];
+        }
+    }
+    return dot;
+}
+
+/* ---------------------------------------------------------------- Q2_K */
+/* block_q2_K (stratum_q2k.h:8-14): scales[16]@0, qs[64]@16, d@80,
+ * dmin@82.  Group g = 8s + 2j + h (16 weights at 128s + 32j + 16h + l):
+ * q = (qs[32s + 16h + l] >> 2j) & 3, scale byte scales[g] (low nibble
+ * scale, high nibble min). */
+static inline int q2k_q(const uint8_t* blk, int g, int l) {
+    int s = g >> 3, j = (g >> 1) & 3, h = g & 1;
+    return (blk[16 + 32 * s + 16 * h + l] >> (2 * j)) & 3;
+}
+
+/* type 42 (tools_gguf_nib_convert.c:99-120; stratum_q2k_neon.h:265-291):
+ * scales[16]@0, nibbles[128]@16, d@144, dmin@146.  Position p lives in
+ * byte 16 + 16*(p/32) + p%16, low nibble when p%32 < 16, else high. */
+static inline int nib_q(const uint8_t* blk, int p) {
+    uint8_t b = blk[16 + 16 * (p >> 5) + (p & 15)];
+    return (p & 16) ? (b >> 4) : (b & 0x0f);
+}
+
+static inline int q2_pos(int g, int l) {
+    return 128 * (g >> 3) + 32 * ((g >> 1) & 3) + 16 * (g & 1) + l;
+}
+
+static void q2_dequant_block(const uint8_t* blk, int nib, float* y) {
+    /* stratum_q2k.h:16-42: y = fl(fl(d*sc)*q) - fl(dmin*m) */
+    const int doff = nib ? 144 : 80;
+    const float d = ko_fp16_to_fp32(rd16(blk + doff));
+    const float dmin = ko_fp16_to_fp32(rd16(blk + doff + 2));
+    for (int g = 0; g < 16; g++) {
+        const uint8_t scb = blk[g];
+        const float dl = d * (float)(scb & 0x0f);
+        const float ml = dmin * (float)(scb >> 4);
+        for (int l = 0; l < 16; l++) {
+            int p = q2_pos(g, l);
+            int q = nib ? nib_q(blk, p) : q2k_q(blk, g, l);
+            y[p] = dl * (float)q - ml;
+        }
+    }
+}
+
+static double q2_dot(const uint8_t* row, int K, const float* x, int nib) {
+    /* stratum_q2k.h:44-89, groups in (s, j, h) order */
+    const int bb = nib ? 148 : 84, doff = nib ? 144 : 80;
+    double dot = 0.0;
+    for (int b = 0; b < K / 256; b++) {
+        const uint8_t* blk = row + (size_t)b * bb;
+        const float* xb = x + (size_t)b * 256;
+        const float d = ko_fp16_to_fp32(rd16(blk + doff));
+        const float dmin = ko_fp16_to_fp32(rd16(blk + doff + 2));
+        for (int g = 0; g < 16; g++) {
+            const uint8_t scb = blk[g];
+            const float dl = d * (float)(scb & 0x0f);
+            const float ml = dmin * (float)(scb >> 4);
+            float qx = 0.0f, sx = 0.0f;
+            for (int l = 0; l < 16; l++) {
+                int p = q2_pos(g, l);
+                int q = nib ? nib_q(blk, p) : q2k_q(blk, g, l);
+                qx += (float)q * xb[p];
+                sx += xb[p];
+            }
+            dot += (double)(dl * qx - ml * sx);
+        }
+    }
+    return dot;
+}
+
+/* ------------------------------------------------------------ dispatch */
+void ko_dequant_row(int type, const uint8_t* row, int K, float* y) {
+    const int bb = ko_block_bytes(type);
+    for (int b = 0; b < K / 256; b++) {
+        const uint8_t* blk = row + (size_t)b * bb;
+        float* yb = y + (size_t)b * 256;
+        switch (type) {
+        case KO_Q4_K: q4k_dequant_block(blk, yb); break;
+        case KO_Q6_K: q6k_dequant_block(blk, yb); break;
+        case KO_Q2_K: q2_dequant_block(blk, 0, yb); break;
+        case KO_Q2K_NIB: q2_dequant_block(blk, 1, yb); break;
+        default: return;
+        }
+    }
+}
+
+double ko_dot_row_f64(int type, const uint8_t* row, int K, const float* x) {
+    switch (type) {
+    case KO_Q4_K: return q4k_dot(row, K, x);
+    case KO_Q6_K: return q6k_dot(row, K, x);
+    case KO_Q2_K: return q2_dot(row, K, x, 0);
+    case KO_Q2K_NIB: return q2_dot(row, K, x, 1);
+    default: return 0.0;
+    }
+}
+
+float ko_dot_row(int type, const uint8_t* row, int K, const float* x) {
+    return (float)ko_dot_row_f64(type, row, K, x);
+}
+
+/* --------------------------------------------------- threaded row split */
+/* Mirrors ST_PAR_ROWS (stratum_linear.h:201-228): workers pull 64-row
+ * tickets from an atomic counter; rows are independent, so the output does
+ * not depend on the thread count. */
+typedef struct {
+    int type, N, K, B;
+    size_t row_bytes;
+    const uint8_t* w;
+    const float* x;
+    const float* add;
+    float* y;
+    atomic_int next;
+} ko_job;
+
+static void* ko_worker(void* arg) {
+    ko_job* j = (ko_job*)arg;
+    for (;;) {
+        int s = atomic_fetch_add_explicit(&j->next, 64, memory_order_relaxed);
+        if (s >= j->N) break;
+        int e = s + 64 < j->N ? s + 64 : j->N;
+        for (int r = s; r < e; r++) {
+            const uint8_t* row = j->w + (size_t)r * j->row_bytes;
+            for (int b = 0; b < j->B; b++) {
+                float v = ko_dot_row(j->type, row, j->K, j->x + (size_t)b * j->K);
+                if (j->add) v = j->add[(size_t)b * j->N + r] + v;
+                j->y[(size_t)b * j->N + r] = v;
+            }
+        }
+    }
+    return NULL;
+}
+
+static int ko_run(ko_job* j, int nthreads) {
+    if (ko_block_bytes(j->type) == 0 || j->K % 256 != 0 || j->N < 0 || j->K < 0) return -1;
+    atomic_store(&j->next, 0);
+    if (nthreads <= 1) {
+        ko_worker(j);
+        return 0;
+    }
+    if (nthreads > 256) nthreads = 256;
+    pthread_t th[256];
+    int started = 0;
+    for (int t = 0; t < nthreads - 1; t++) {
+        if (pthread_create(&th[t], NULL, ko_worker, j) != 0) break;
+        started++;
+    }
+    ko_worker(j); /* the caller takes a share, as st_par_run does */
+    for (int t = 0; t < started; t++) pthread_join(th[t], NULL);
+    return 0;
+}
+
+int ko_gemv(int type, const uint8_t* w, const float* x, const float* add,
+            float* y, int N, int K, int nthreads) {
+    ko_job j;
+    j.type = type; j.N = N; j.K = K; j.B = 1;
+    j.row_bytes = (size_t)(K / 256) * (size_t)ko_block_bytes(type);
+    j.w = w; j.x = x; j.add = add; j.y = y;
+    return ko_run(&j, nthreads);
+}
+
+int ko_gemv_multix(int type, const uint8_t* w, const float* xs, float* ys,
+                   int B, int N, int K, int nthreads) {
+    ko_job j;
+    j.type = type; j.N = N; j.K = K; j.B = B;
+    j.row_bytes = (size_t)(K / 256) * (size_t)ko_block_bytes(type);
+    j.w = w; j.x = xs; j.add = NULL; j.y = ys;
+    return ko_run(&j, nthreads);
+}
+
+/* ------------------------------------------------------ type-42 layout */
+void ko_q2k_to_nib(const uint8_t* q2k, uint8_t* nib, int64_t nblocks) {
+    for (int64_t b = 0; b < nblocks; b++) {
+        const uint8_t* src = q2k + b * 84;
+        uint8_t* dst = nib + b * 148;
+        memcpy(dst, src, 16);            /* scales unchanged */
+        memset(dst + 16, 0, 128);
+        memcpy(dst + 144, src + 80, 4);  /* d, dmin moved to the tail */
+        for (int g = 0; g < 16; g++)
+            for (int l = 0; l < 16; l++) {
+                int p = q2_pos(g, l);
+                int q = q2k_q(src, g, l);
+                dst[16 + 16 * (p >> 5) + (p & 15)] |= (uint8_t)((p & 16) ? (q << 4) : q);
+            }
+    }
+}
+
+void ko_nib_to_q2k(const uint8_t* nib, uint8_t* q2k, int64_t nblocks) {
+    for (int64_t b = 0; b < nblocks; b++) {
+        const uint8_t* src = nib + b * 148;
+        uint8_t* dst = q2k + b * 84;
+        memcpy(dst, src, 16);
+        memset(dst + 16, 0, 64);
+        memcpy(dst + 80, src + 144, 4);
+        for (int g = 0; g < 16; g++)
+            for (int l = 0; l < 16; l++) {
+                int s = g >> 3, j = (g >> 1) & 3, h = g & 1;
+                int q = nib_q(src, q2_pos(g, l)) & 3;
+                dst[16 + 32 * s + 16 * h + l] |= (uint8_t)(q << (2 * j));
+            }
+    }
+}
+
+/* --------------------------------------------------------------- top-k */
+void ko_moe_topk(const float* w, int E, int K, int* sel, float* selw) {
+    /* stratum_arch_moe.inc.c:368-385: insertion into a descending list on
+     * strictly greater weight; an equal weight never displaces an earlier
+     * (lower-id) entry. */
+    for (int s = 0; s < K; s++) { sel[s] = -1; selw[s] = -1.0f; }
+    for (int e = 0; e < E; e++) {
+        int pos = -1;
+        for (int s = 0; s < K; s++)
+            if (w[e] > selw[s]) { pos = s; break; }
+        if (pos < 0) continue;
+        for (int s = K - 1; s > pos; s--) { sel[s] = sel[s - 1]; selw[s] = selw[s - 1]; }
+        sel[pos] = e;
+        selw[pos] = w[e];
+    }
+}

@@ -1,0 +1,84 @@
+/*
+ * kq_oracle.h -- CPU restatement of stratum's scalar k-quant routines.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (stratum_amd/, include/)
+ * links or calls this code; only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py use it, and only as the checker or as the
+ * timed CPU baseline.  It is compiled with strict IEEE binary32/binary64
+ * semantics (-O2 -ffp-contract=off -fno-fast-math), so every product and
+ * every sum is rounded exactly where the reference's C source rounds it.
+ *
+ * Reference functions restated here (paths under
+ * /root/reference/stratum/native/):
+ *   stratum_q4k.h:24-55   q4k_fp16_to_fp32        -> ko_fp16_to_fp32
+ *   stratum_q4k.h:57-65   q4k_get_scale_min       -> ko_q4k_scale_min
+ *   stratum_q4k.h:67-93   q4k_dequant_*_scalar    -> ko_dequant_row (Q4_K)
+ *   stratum_q4k.h:95-131  q4k_dot_row_scalar      -> ko_dot_row (Q4_K)
+ *   stratum_q6k.h:17-36   q6k_dequant_block_scalar-> ko_dequant_row (Q6_K)
+ *   stratum_q6k.h:38-73   q6k_dot_row_scalar      -> ko_dot_row (Q6_K)
+ *   stratum_q2k.h:16-42   q2k_dequant_block_scalar-> ko_dequant_row (Q2_K)
+ *   stratum_q2k.h:44-89   q2k_dot_row_scalar      -> ko_dot_row (Q2_K)
+ *   tools_gguf_nib_convert.c:99-120  Q2_K -> type 42 byte permutation
+ *                                     -> ko_q2k_to_nib / ko_nib_to_q2k
+ *   stratum_linear.h:201-228 ST_PAR_ROWS 64-row tickets -> ko_gemv threads
+ *   stratum_arch_moe.inc.c:368-385 moe_topk        -> ko_moe_topk
+ *
+ * Pinning (what checks each function, see tests/test_oracle_*.py):
+ *   - golden vectors in tests/golden/ written by the reference's own scalar
+ *     headers compiled from /root/reference (oracle/_ref), bit-exact;
+ *   - direct comparison against oracle/_ref when it is built;
+ *   - closed forms: exhaustive fp16 vs numpy.float16, exhaustive scale
+ *     decode, x = e_i gives the dequantized column, linearity checks, the
+ *     type-42 permutation round trip and value identity.
+ */
+#ifndef KQ_ORACLE_H
+#define KQ_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGML type ids (stratum_gguf.h:20-49). */
+enum {
+    KO_Q2_K = 10,
+    KO_Q4_K = 12,
+    KO_Q6_K = 14,
+    KO_Q2K_NIB = 42,
+};
+
+/* bytes per 256-weight super-block for a type; 0 for unsupported types */
+int ko_block_bytes(int type);
+
+float ko_fp16_to_fp32(uint16_t h);
+void ko_q4k_scale_min(int j, const uint8_t* scales, uint8_t* sc, uint8_t* m);
+
+/* one row of K weights (K % 256 == 0) */
+void ko_dequant_row(int type, const uint8_t* row, int K, float* y);
+float ko_dot_row(int type, const uint8_t* row, int K, const float* x);
+/* same sum, returned before the final (float) rounding */
+double ko_dot_row_f64(int type, const uint8_t* row, int K, const float* x);
+
+/* y[r] = dot(row r, x) for r < N; rows contiguous.  nthreads <= 1 runs on
+ * the calling thread; otherwise 64-row atomic tickets over pthreads.
+ * add != NULL gives y[r] = add[r] + dot (stratum_linear.h:568-632). */
+int ko_gemv(int type, const uint8_t* w, const float* x, const float* add,
+            float* y, int N, int K, int nthreads);
+
+/* B streams over one weight: ys[s*N + r] = dot(row r, xs[s*K ...]) */
+int ko_gemv_multix(int type, const uint8_t* w, const float* xs, float* ys,
+                   int B, int N, int K, int nthreads);
+
+/* type-42 permutation (148-byte blocks) and its inverse */
+void ko_q2k_to_nib(const uint8_t* q2k, uint8_t* nib, int64_t nblocks);
+void ko_nib_to_q2k(const uint8_t* nib, uint8_t* q2k, int64_t nblocks);
+
+/* top-k with strict '>' replacement: ties keep the lower expert id */
+void ko_moe_topk(const float* w, int E, int K, int* sel, float* selw);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,184 @@
+"""ctypes access to the CPU oracle (TEST INFRASTRUCTURE ONLY).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this module, and only as the checker or as the timed CPU baseline.
+
+  port()  -> oracle/liboracle.so      the repo's C restatement (kq_oracle.c)
+  ref()   -> oracle/_ref/libkqref.so  the reference's own scalar headers
+             compiled from /root/reference (None when not built)
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PORT_PATH = os.path.join(HERE, "liboracle.so")
+REF_PATH = os.path.join(HERE, "_ref", "libkqref.so")
+NIBCONV_PATH = os.path.join(HERE, "_ref", "nib_convert")
+
+_F = ctypes.POINTER(ctypes.c_float)
+_U8 = ctypes.POINTER(ctypes.c_uint8)
+
+
+def build(quiet: bool = True) -> None:
+    """make -C oracle (the reference part only where /root/reference exists)."""
+    out = subprocess.run(["make", "-C", HERE], capture_output=True, text=True)
+    if out.returncode != 0:
+        raise RuntimeError("oracle build failed:\n" + out.stdout + out.stderr)
+    if not quiet:
+        print(out.stdout)
+
+
+def _u8(a: np.ndarray):
+    assert a.dtype == np.uint8 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(_U8)
+
+
+def _f(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(_F)
+
+
+class Port:
+    """The restatement in oracle/kq_oracle.c."""
+
+    def __init__(self, path: str = PORT_PATH):
+        if not os.path.exists(path):
+            build()
+        L = ctypes.CDLL(path)
+        I = ctypes.c_int
+        L.ko_fp16_to_fp32.argtypes = [ctypes.c_uint16]
+        L.ko_fp16_to_fp32.restype = ctypes.c_float
+        L.ko_q4k_scale_min.argtypes = [I, _U8, _U8, _U8]
+        L.ko_dequant_row.argtypes = [I, _U8, I, _F]
+        L.ko_dot_row.argtypes = [I, _U8, I, _F]
+        L.ko_dot_row.restype = ctypes.c_float
+        L.ko_dot_row_f64.argtypes = [I, _U8, I, _F]
+        L.ko_dot_row_f64.restype = ctypes.c_double
+        L.ko_gemv.argtypes = [I, _U8, _F, _F, _F, I, I, I]
+        L.ko_gemv_multix.argtypes = [I, _U8, _F, _F, I, I, I, I]
+        L.ko_q2k_to_nib.argtypes = [_U8, _U8, ctypes.c_int64]
+        L.ko_nib_to_q2k.argtypes = [_U8, _U8, ctypes.c_int64]
+        L.ko_moe_topk.argtypes = [_F, I, I, ctypes.POINTER(ctypes.c_int), _F]
+        self.L = L
+
+    def fp16_to_fp32(self, h: int) -> float:
+        return self.L.ko_fp16_to_fp32(h)
+
+    def dequant(self, qtype: int, w: np.ndarray, nrows: int, K: int) -> np.ndarray:
+        y = np.empty(nrows * K, np.float32)
+        rb = w.size // nrows
+        for r in range(nrows):
+            self.L.ko_dequant_row(qtype, _u8(w[r * rb:(r + 1) * rb]), K,
+                                  y[r * K:(r + 1) * K].ctypes.data_as(_F))
+        return y
+
+    def gemv(self, qtype: int, w: np.ndarray, x: np.ndarray, N: int, K: int,
+             add: np.ndarray | None = None, threads: int = 1) -> np.ndarray:
+        y = np.empty(N, np.float32)
+        rc = self.L.ko_gemv(qtype, _u8(w), _f(x), _f(add) if add is not None else None,
+                            _f(y), N, K, threads)
+        assert rc == 0
+        return y
+
+    def gemv_rows(self, qtype: int, w: np.ndarray, x: np.ndarray, rows, K: int) -> np.ndarray:
+        """Oracle result for a subset of rows (large tensors)."""
+        rb = (K // 256) * {10: 84, 12: 144, 14: 210, 42: 148}[qtype]
+        out = np.empty(len(rows), np.float32)
+        for i, r in enumerate(rows):
+            seg = w[r * rb:(r + 1) * rb]
+            out[i] = self.L.ko_dot_row(qtype, _u8(seg), K, _f(x))
+        return out
+
+    def gemv_multix(self, qtype, w, xs, N, K, threads=1):
+        B = xs.shape[0]
+        ys = np.empty((B, N), np.float32)
+        assert self.L.ko_gemv_multix(qtype, _u8(w), _f(np.ascontiguousarray(xs)), _f(ys),
+                                     B, N, K, threads) == 0
+        return ys
+
+    def q2k_to_nib(self, q2k: np.ndarray) -> np.ndarray:
+        n = q2k.size // 84
+        out = np.empty(n * 148, np.uint8)
+        self.L.ko_q2k_to_nib(_u8(q2k), _u8(out), n)
+        return out
+
+    def nib_to_q2k(self, nib: np.ndarray) -> np.ndarray:
+        n = nib.size // 148
+        out = np.empty(n * 84, np.uint8)
+        self.L.ko_nib_to_q2k(_u8(nib), _u8(out), n)
+        return out
+
+    def topk(self, w: np.ndarray, k: int):
+        sel = (ctypes.c_int * k)()
+        selw = np.empty(k, np.float32)
+        self.L.ko_moe_topk(_f(w), w.size, k, sel, _f(selw))
+        return list(sel), selw
+
+
+class Ref:
+    """The reference's own scalar routines (oracle/_ref/libkqref.so)."""
+
+    def __init__(self, path: str = REF_PATH):
+        L = ctypes.CDLL(path)
+        I = ctypes.c_int
+        L.kqref_fp16_to_fp32.argtypes = [ctypes.c_uint16]
+        L.kqref_fp16_to_fp32.restype = ctypes.c_float
+        L.kqref_scale_min.argtypes = [I, _U8, _U8, _U8]
+        L.kqref_dequant_row.argtypes = [I, _U8, I, _F]
+        L.kqref_dot_row.argtypes = [I, _U8, I, _F]
+        L.kqref_dot_row.restype = ctypes.c_float
+        L.kqref_gemv.argtypes = [I, _U8, _F, _F, I, I, I, I]
+        self.L = L
+
+    def dequant(self, qtype: int, w: np.ndarray, nrows: int, K: int) -> np.ndarray:
+        y = np.empty(nrows * K, np.float32)
+        rb = w.size // nrows
+        for r in range(nrows):
+            assert self.L.kqref_dequant_row(qtype, _u8(w[r * rb:(r + 1) * rb]), K,
+                                            y[r * K:(r + 1) * K].ctypes.data_as(_F)) == 0
+        return y
+
+    def gemv(self, qtype: int, w: np.ndarray, x: np.ndarray, N: int, K: int,
+             threads: int = 1) -> np.ndarray:
+        y = np.empty(N, np.float32)
+        assert self.L.kqref_gemv(qtype, _u8(w), _f(x), _f(y), 1, N, K, threads) == 0
+        return y
+
+    def gemv_multix(self, qtype, w, xs, N, K, threads=1):
+        B = xs.shape[0]
+        ys = np.empty((B, N), np.float32)
+        assert self.L.kqref_gemv(qtype, _u8(w), _f(np.ascontiguousarray(xs)), _f(ys),
+                                 B, N, K, threads) == 0
+        return ys
+
+
+_port = None
+_ref = None
+
+
+def port() -> Port:
+    global _port
+    if _port is None:
+        _port = Port()
+    return _port
+
+
+def ref() -> Ref | None:
+    """The reference build, or None where /root/reference was not available."""
+    global _ref
+    if _ref is None and os.path.exists(REF_PATH):
+        _ref = Ref()
+    return _ref
+
+
+# ------------------------------------------------------------ tolerances
+def rel_err(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Per-element |a-b| / max(|b|, 1e-6): ASSERT_REL of quant_test.c:34-43."""
+    a = a.astype(np.float64)
+    b = b.astype(np.float64)
+    return np.abs(a - b) / np.maximum(np.abs(b), 1e-6)

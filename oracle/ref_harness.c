@@ -1,0 +1,106 @@
+/*
+ * ref_harness.c -- thin C-ABI around the reference's OWN scalar headers.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Built by oracle/Makefile, only when
+ * /root/reference is present, into oracle/_ref/libkqref.so with
+ *   -I/root/reference/stratum/native -O2 -ffp-contract=off -fno-fast-math
+ * No reference source is copied: the headers are #included where they
+ * lie.  The library is used to (a) pin oracle/kq_oracle.c bit for bit and
+ * to write the golden fixtures under tests/golden/, and (b) as the
+ * "reference" CPU baseline in bench.py (kind "reference").
+ *
+ * Exported functions wrap, without changing any arithmetic:
+ *   q4k_fp16_to_fp32, q4k_get_scale_min          (stratum_q4k.h:24-65)
+ *   q{4,6,2}k_dequant_block_scalar               (stratum_q4k.h:67, q6k.h:17, q2k.h:16)
+ *   q{4,6,2}k_dot_row_scalar                     (stratum_q4k.h:95, q6k.h:38, q2k.h:44)
+ * plus a pthread row split with 64-row tickets, as ST_PAR_ROWS does
+ * (stratum_linear.h:201-228) on a machine without NEON (stratum_linear.h:446-451).
+ */
+#define _GNU_SOURCE
+#include "stratum_q4k.h"
+#include "stratum_q6k.h"
+#include "stratum_q2k.h"
+
+#include <pthread.h>
+#include <stdatomic.h>
+#include <stdint.h>
+#include <string.h>
+
+float kqref_fp16_to_fp32(uint16_t h) { return q4k_fp16_to_fp32(h); }
+
+void kqref_scale_min(int j, const uint8_t* s, uint8_t* sc, uint8_t* m) {
+    q4k_get_scale_min(j, s, sc, m);
+}
+
+int kqref_block_bytes(int type) {
+    return type == 12 ? (int)sizeof(block_q4_K)
+         : type == 14 ? (int)sizeof(block_q6_K)
+         : type == 10 ? (int)sizeof(block_q2_K) : 0;
+}
+
+int kqref_dequant_row(int type, const uint8_t* row, int K, float* y) {
+    for (int b = 0; b < K / 256; b++) {
+        switch (type) {
+        case 12: q4k_dequant_block_scalar((const block_q4_K*)row + b, y + 256 * b); break;
+        case 14: q6k_dequant_block_scalar((const block_q6_K*)row + b, y + 256 * b); break;
+        case 10: q2k_dequant_block_scalar((const block_q2_K*)row + b, y + 256 * b); break;
+        default: return -1;
+        }
+    }
+    return 0;
+}
+
+float kqref_dot_row(int type, const uint8_t* row, int K, const float* x) {
+    switch (type) {
+    case 12: return q4k_dot_row_scalar((const block_q4_K*)row, K, x);
+    case 14: return q6k_dot_row_scalar((const block_q6_K*)row, K, x);
+    case 10: return q2k_dot_row_scalar((const block_q2_K*)row, K, x);
+    default: return 0.0f;
+    }
+}
+
+typedef struct {
+    int type, N, K, B;
+    size_t rb;
+    const uint8_t* w;
+    const float* x;
+    float* y;
+    atomic_int next;
+} kqref_job;
+
+static void* kqref_worker(void* a) {
+    kqref_job* j = (kqref_job*)a;
+    for (;;) {
+        int s = atomic_fetch_add_explicit(&j->next, 64, memory_order_relaxed);
+        if (s >= j->N) break;
+        int e = s + 64 < j->N ? s + 64 : j->N;
+        for (int r = s; r < e; r++)
+            for (int b = 0; b < j->B; b++)
+                j->y[(size_t)b * j->N + r] =
+                    kqref_dot_row(j->type, j->w + (size_t)r * j->rb, j->K,
+                                  j->x + (size_t)b * j->K);
+    }
+    return NULL;
+}
+
+/* ys[b*N + r] = row r . xs[b*K ...] for b < B, rows split over nthreads */
+int kqref_gemv(int type, const uint8_t* w, const float* xs, float* ys,
+               int B, int N, int K, int nthreads) {
+    int bb = kqref_block_bytes(type);
+    if (!bb || K % 256) return -1;
+    kqref_job j;
+    j.type = type; j.N = N; j.K = K; j.B = B;
+    j.rb = (size_t)(K / 256) * (size_t)bb;
+    j.w = w; j.x = xs; j.y = ys;
+    atomic_store(&j.next, 0);
+    if (nthreads > 256) nthreads = 256;
+    pthread_t th[256];
+    int started = 0;
+    for (int t = 0; t < nthreads - 1; t++) {
+        if (pthread_create(&th[t], NULL, kqref_worker, &j) != 0) break;
+        started++;
+    }
+    kqref_worker(&j);
+    for (int t = 0; t < started; t++) pthread_join(th[t], NULL);
+    return 0;
+}
