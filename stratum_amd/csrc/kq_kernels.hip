@@ -18,15 +18,18 @@
 // -ffp-contract=off and carries the pragma below so no mul+add fuses.
 //
 // Exact integer-to-float tricks used on the hot loop:
-//  * Q4_K / Q2_K / type-42 quants (0..15) go through v_cvt_pk_f32_fp8: an
-//    OCP E4M3 byte whose value is q (q < 16) is the subnormal/first-binade
-//    number q * 2^-9, so two quants convert per instruction.  x is staged
-//    pre-multiplied by 2^9 (exact), so fl(q*2^-9 * x*2^9) == fl(q*x).
+//  * Q4_K / Q2_K / type-42 quants are converted with v_cvt_f32_ubyte{0..3}
+//    straight from their packed bytes.  A quant that does not sit in the
+//    low bits of its byte is masked in place, so the byte holds q * 2^s
+//    (s = 4 for a high nibble, 2j for Q2_K's field j).  Since every
+//    partial sum then equals 2^s times the reference's partial sum exactly
+//    (power-of-two scaling commutes with binary32 rounding for these
+//    magnitudes), the factor is removed exactly by scaling d*sc by 2^-s.
 //  * Q6_K quants are assembled as the int8 byte 4*(q-32) and converted
 //    with a sign-extending byte select; the partial sums are then exactly
 //    4x the reference's, and the factor is folded into the exact binary64
 //    scale product d*s/4.
-// Both scalings are exact for every finite input with |x| < 2^118.
+// The scalings are exact for every finite input with |x| < 2^100.
 //
 // Work decomposition (all types).  A row of K weights is K/64 "chunks" of
 // 64 weights; a chunk is one lane's work and always lies inside one
@@ -54,10 +57,10 @@ constexpr int T_NIB = 42;
 constexpr int XPAD = 17;  // float4 slots per 64-weight chunk in LDS (16 + 1 pad)
 
 template <int TYPE> struct TypeInfo;
-template <> struct TypeInfo<T_Q4K> { static constexpr int BB = 144; static constexpr bool LINEAR = true;  static constexpr int XS_PER_CHUNK = 2; static constexpr float XSCALE = 512.0f; };
-template <> struct TypeInfo<T_Q6K> { static constexpr int BB = 210; static constexpr bool LINEAR = false; static constexpr int XS_PER_CHUNK = 0; static constexpr float XSCALE = 1.0f; };
-template <> struct TypeInfo<T_Q2K> { static constexpr int BB = 84;  static constexpr bool LINEAR = false; static constexpr int XS_PER_CHUNK = 4; static constexpr float XSCALE = 512.0f; };
-template <> struct TypeInfo<T_NIB> { static constexpr int BB = 148; static constexpr bool LINEAR = true;  static constexpr int XS_PER_CHUNK = 4; static constexpr float XSCALE = 512.0f; };
+template <> struct TypeInfo<T_Q4K> { static constexpr int BB = 144; static constexpr bool LINEAR = true;  static constexpr int XS_PER_CHUNK = 2; };
+template <> struct TypeInfo<T_Q6K> { static constexpr int BB = 210; static constexpr bool LINEAR = false; static constexpr int XS_PER_CHUNK = 0; };
+template <> struct TypeInfo<T_Q2K> { static constexpr int BB = 84;  static constexpr bool LINEAR = false; static constexpr int XS_PER_CHUNK = 4; };
+template <> struct TypeInfo<T_NIB> { static constexpr int BB = 148; static constexpr bool LINEAR = true;  static constexpr int XS_PER_CHUNK = 4; };
 
 struct GemvArgs {
     const uint8_t* w;    // row 0 of the tensor (device)
@@ -74,16 +77,29 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
     return (float)v;  // v_cvt_f32_f16: exact widening incl. subnormals
 }
 
-// two E4M3 bytes (low or high half-word of v) -> two floats q * 2^-9
-template <bool HI>
-__device__ __forceinline__ void fp8x2(uint32_t v, float& a, float& b) {
-    auto r = __builtin_amdgcn_cvt_pk_f32_fp8(v, HI);
-    a = r[0];
-    b = r[1];
+// the four bytes of v as floats (v_cvt_f32_ubyte0..3).  The empty asm
+// hides the masked value's known bits from the optimiser, which would
+// otherwise re-extract every field with v_bfe before converting.
+__device__ __forceinline__ void ubytes(uint32_t v, float& a, float& b, float& c, float& d) {
+    asm volatile("" : "+v"(v));
+    a = (float)(v & 0xffu);
+    b = (float)((v >> 8) & 0xffu);
+    c = (float)((v >> 16) & 0xffu);
+    d = (float)(v >> 24);
 }
 
 __device__ __forceinline__ uint32_t bfe(uint32_t v, uint32_t off, uint32_t w) {
     return __builtin_amdgcn_ubfe(v, off, w);
+}
+
+// v of the lane selected by DPP control CTRL (both 32-bit halves moved).
+// Used only with every lane of the 8-lane group active.
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const int lo = __double2loint(v), hi = __double2hiint(v);
+    const int l2 = __builtin_amdgcn_mov_dpp(lo, CTRL, 0xf, 0xf, false);
+    const int h2 = __builtin_amdgcn_mov_dpp(hi, CTRL, 0xf, 0xf, false);
+    return __hiloint2double(h2, l2);
 }
 
 // ------------------------------------------------------------------ LDS x
@@ -104,54 +120,83 @@ __device__ __forceinline__ void x_slot(int p, int& c, int& g) {
     }
 }
 
-// Stage x (one stream) into LDS: xl[c*XPAD + g] = x[...] * XSCALE, and the
-// per-sub-block plain sums the min terms need (sequential binary32, exactly
-// as the reference's xs1/xs2 and sx accumulators).
+// Staging of x (one stream) into LDS.
+//   stage_dma  -- x goes straight from global memory into the padded LDS
+//                 layout with global_load_lds_dwordx4 (lane i of a wave
+//                 writes 16 bytes at base + 16 i).  No registers are
+//                 involved, so every x load of the workgroup is issued back
+//                 to back right after the weight prefetch and the whole
+//                 staging costs about one memory latency;
+//   stage_sums -- after a barrier, the per-sub-block plain sums the min
+//                 terms need, read back from LDS (sequential binary32,
+//                 exactly as the reference's xs1/xs2 and sx accumulators).
+
+// global float4 index of LDS slot s (chunk c = s / XPAD, slot g = s % XPAD);
+// the pad slot (g == 16) is filled with a copy of slot 0 and never read
+template <bool LINEAR>
+__device__ __forceinline__ int x_src_of_slot(int s) {
+    const int c = s / XPAD;
+    int g = s - c * XPAD;
+    if (g == 16) g = 0;
+    if (LINEAR) return 16 * c + g;
+    // strided: chunk c = (block, half h, sub is); slot g = 4*run + l/4
+    const int bi = c >> 2, h = (c >> 1) & 1, is = c & 1;
+    return 64 * bi + 32 * h + 4 * is + 8 * (g >> 2) + (g & 3);
+}
+
 template <int TYPE>
-__device__ void stage_x(const float* __restrict__ x, int K, float4* xl, float* xs,
-                        int tid, int T) {
-    using TI = TypeInfo<TYPE>;
+__device__ __forceinline__ void stage_dma(const float* __restrict__ x, int K, int tid, int T,
+                                          float4* xl) {
+    const int total = (K >> 6) * XPAD;       // slots, pads included
+    const int wbase = tid & ~63;
     const float4* x4 = reinterpret_cast<const float4*>(x);
-    for (int i = tid; i < (K >> 2); i += T) {
-        float4 v = x4[i];
-        v.x *= TI::XSCALE; v.y *= TI::XSCALE; v.z *= TI::XSCALE; v.w *= TI::XSCALE;
-        int c, g;
-        x_slot<TI::LINEAR>(4 * i, c, g);
-        xl[c * XPAD + g] = v;
+    for (int s0 = 0; s0 < total; s0 += T) {
+        const int s = s0 + tid;
+        if (s < total) {
+            const float4* src = x4 + x_src_of_slot<TypeInfo<TYPE>::LINEAR>(s);
+            __builtin_amdgcn_global_load_lds(
+                src, (__attribute__((address_space(3))) void*)(xl + s0 + wbase), 16, 0, 0);
+        }
     }
+}
+
+template <int TYPE>
+__device__ __forceinline__ void stage_sums(int K, int tid, int T, const float4* xl, float* xs) {
     if (TYPE == T_Q4K) {
-        // xs[sb] = sum of the 32 x of sub-block sb (stratum_q4k.h:115-122)
+        // xs[sb] = sum of the 32 x of sub-block sb (stratum_q4k.h:115-122):
+        // chunk sb/2, float4 slots 8*(sb&1) .. +7 of the linear layout
         for (int sb = tid; sb < (K >> 5); sb += T) {
-            const float4* p = x4 + 8 * sb;
+            const float4* p = xl + (sb >> 1) * XPAD + 8 * (sb & 1);
             float s = 0.0f;
 #pragma unroll
             for (int k = 0; k < 8; k++) {
-                float4 v = p[k];
+                const float4 v = p[k];
                 s = s + v.x; s = s + v.y; s = s + v.z; s = s + v.w;
             }
             xs[sb] = s;
         }
     } else if (TYPE == T_Q2K || TYPE == T_NIB) {
-        // sums over 16-weight groups (stratum_q2k.h:65-68); stored at the
-        // chunk's slot: Q2_K chunk (block, s, h) holds groups j = 0..3,
-        // type-42 chunk u holds groups 4u..4u+3.
+        // sums over 16-weight groups (stratum_q2k.h:65-68), stored at the
+        // chunk's slot: Q2_K chunk (block, s, h) holds groups j = 0..3 (its
+        // float4 slots 4j..4j+3), type-42 chunk u holds groups 4u..4u+3.
         for (int gi = tid; gi < (K >> 4); gi += T) {
-            const float4* p = x4 + 4 * gi;
+            int c, j;
+            if (TYPE == T_NIB) {
+                c = gi >> 2;
+                j = gi & 3;
+            } else {
+                const int bi = gi >> 4, g16 = gi & 15;
+                c = 4 * bi + 2 * (g16 >> 3) + (g16 & 1);
+                j = (g16 >> 1) & 3;
+            }
+            const float4* p = xl + c * XPAD + 4 * j;
             float s = 0.0f;
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                float4 v = p[k];
+                const float4 v = p[k];
                 s = s + v.x; s = s + v.y; s = s + v.z; s = s + v.w;
             }
-            int slot;
-            if (TYPE == T_NIB) {
-                slot = gi;
-            } else {
-                const int bi = gi >> 4, g16 = gi & 15;
-                const int s2 = g16 >> 3, j = (g16 >> 1) & 3, h = g16 & 1;
-                slot = (4 * bi + 2 * s2 + h) * 4 + j;
-            }
-            xs[slot] = s;
+            xs[c * 4 + j] = s;
         }
     }
 }
@@ -191,9 +236,13 @@ __device__ __forceinline__ void load5(const uint8_t* p, uint32_t* o) {
 __device__ __forceinline__ RawQ6 load_q6k(const uint8_t* blk, int u) {
     RawQ6 r;
     const int h = u >> 1, is = u & 1;
-    const uintptr_t base = reinterpret_cast<uintptr_t>(blk);
-    r.sh = (uint32_t)(base & 3u) * 8u;
-    const uint8_t* b4 = reinterpret_cast<const uint8_t*>(base & ~uintptr_t(3));
+    // realign by pointer arithmetic (not through an integer) so the
+    // compiler keeps the global address space and emits global_load, not
+    // flat_load (flat loads also count against lgkmcnt, so every LDS wait
+    // would wait for the weight prefetch as well)
+    const uint32_t mis = (uint32_t)reinterpret_cast<uintptr_t>(blk) & 3u;
+    r.sh = mis * 8u;
+    const uint8_t* b4 = blk - mis;
     load5(b4 + 64 * h + 16 * is, r.l);
     load5(b4 + 64 * h + 32 + 16 * is, r.h);
     load5(b4 + 128 + 32 * h + 16 * is, r.q);
@@ -257,16 +306,16 @@ __device__ __forceinline__ double term_q4k(const RawQ4& r, int j, const float4* 
     const float d1 = d * (float)sc1, mm1 = dmin * (float)m1;
     const float d2 = d * (float)sc2, mm2 = dmin * (float)m2;
 
+    // high nibbles are converted in place (16 q), so a2 is 16x the
+    // reference's partial sum and d2 is used divided by 16 (both exact)
     float a1 = 0.0f, a2 = 0.0f;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
         const uint32_t v = k < 4 ? dw_of(r.qa, k) : dw_of(r.qb, k - 4);
-        const uint32_t vl = v & 0x0f0f0f0fu, vh = (v >> 4) & 0x0f0f0f0fu;
+        const uint32_t vl = v & 0x0f0f0f0fu, vh = v & 0xf0f0f0f0u;
         float l0, l1, l2, l3, h0, h1, h2, h3;
-        fp8x2<false>(vl, l0, l1);
-        fp8x2<true>(vl, l2, l3);
-        fp8x2<false>(vh, h0, h1);
-        fp8x2<true>(vh, h2, h3);
+        ubytes(vl, l0, l1, l2, l3);
+        ubytes(vh, h0, h1, h2, h3);
         const float4 xa = xc[k], xb = xc[8 + k];
         a1 = a1 + l0 * xa.x; a2 = a2 + h0 * xb.x;
         a1 = a1 + l1 * xa.y; a2 = a2 + h1 * xb.y;
@@ -274,7 +323,7 @@ __device__ __forceinline__ double term_q4k(const RawQ4& r, int j, const float4* 
         a1 = a1 + l3 * xa.w; a2 = a2 + h3 * xb.w;
     }
     const float t1 = d1 * a1 - mm1 * xs1;
-    const float t2 = d2 * a2 - mm2 * xs2;
+    const float t2 = (d2 * 0.0625f) * a2 - mm2 * xs2;
     return (double)t1 + (double)t2;
 }
 
@@ -334,22 +383,24 @@ __device__ __forceinline__ double term_q2k(const RawQ2& r, int u, const float4* 
     double acc = 0.0;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
+        // field j masked in place: bytes hold q * 4^j, so qx is 4^j times
+        // the reference's sum and dl is used divided by 4^j (exact)
         const float dl = d * (float)(sc[j] & 15u);
         const float ml = dmin * (float)(sc[j] >> 4);
+        const float inv = j == 0 ? 1.0f : j == 1 ? 0.25f : j == 2 ? 0.0625f : 0.015625f;
         float qx = 0.0f;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            const uint32_t v = (dw_of(r.q, k) >> (2 * j)) & 0x03030303u;
+            const uint32_t v = dw_of(r.q, k) & (0x03030303u << (2 * j));
             float q0, q1, q2, q3;
-            fp8x2<false>(v, q0, q1);
-            fp8x2<true>(v, q2, q3);
+            ubytes(v, q0, q1, q2, q3);
             const float4 xv = xc[4 * j + k];
             qx = qx + q0 * xv.x;
             qx = qx + q1 * xv.y;
             qx = qx + q2 * xv.z;
             qx = qx + q3 * xv.w;
         }
-        const float t = dl * qx - ml * sx[j];
+        const float t = (dl * inv) * qx - ml * sx[j];
         acc = acc + (double)t;
     }
     return acc;
@@ -368,21 +419,22 @@ __device__ __forceinline__ double term_nib(const RawNB& r, const float4* xc, con
         const float dl = d * (float)(scb & 15u);
         const float ml = dmin * (float)(scb >> 4);
         const uint4 src = (g < 2) ? r.qa : r.qb;
+        // high-nibble groups are converted in place (16 q): scale dl by 1/16
+        const float inv = (g & 1) ? 0.0625f : 1.0f;
         float qx = 0.0f;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             uint32_t v = dw_of(src, k);
-            v = (g & 1) ? ((v >> 4) & 0x0f0f0f0fu) : (v & 0x0f0f0f0fu);
+            v = (g & 1) ? (v & 0xf0f0f0f0u) : (v & 0x0f0f0f0fu);
             float q0, q1, q2, q3;
-            fp8x2<false>(v, q0, q1);
-            fp8x2<true>(v, q2, q3);
+            ubytes(v, q0, q1, q2, q3);
             const float4 xv = xc[4 * g + k];
             qx = qx + q0 * xv.x;
             qx = qx + q1 * xv.y;
             qx = qx + q2 * xv.z;
             qx = qx + q3 * xv.w;
         }
-        const float t = dl * qx - ml * sx[g];
+        const float t = (dl * inv) * qx - ml * sx[g];
         acc = acc + (double)t;
     }
     return acc;
@@ -436,8 +488,13 @@ __host__ __device__ inline int x_lds_bytes(int K) {
 }
 
 // ------------------------------------------------------------- the GEMV
-// One workgroup = R consecutive rows; see the header comment.
-template <int TYPE>
+// One workgroup = R consecutive rows; see the header comment.  Each lane
+// keeps DEPTH chunks in flight: the first DEPTH loads are issued before x
+// is staged (their latency overlaps the staging), then every computed
+// chunk's registers are refilled with the chunk DEPTH*T further on.
+// T (blockDim.x) is a multiple of 64, so a lane's chunk index modulo 4 --
+// its sub-block position inside the super-block -- never changes.
+template <int TYPE, int DEPTH>
 __global__ __launch_bounds__(1024) void kq_gemv_kernel(GemvArgs a) {
     using TI = TypeInfo<TYPE>;
     using C = Chunk<TYPE>;
@@ -452,37 +509,79 @@ __global__ __launch_bounds__(1024) void kq_gemv_kernel(GemvArgs a) {
     float* xs = reinterpret_cast<float*>(smem + NC * XPAD * 16);
     double* terms = reinterpret_cast<double*>(smem + x_lds_bytes<TYPE>(K));
 
-    stage_x<TYPE>(a.x, K, xl, xs, tid, T);
-    __syncthreads();
-
     const int nch = R * NC;
     const uint8_t* wb = a.w + (size_t)r0 * (size_t)(K >> 8) * TI::BB;
-    const int Tm = T % NC;
-    int f = tid;
-    int c = f % NC;
-    typename C::Raw cur;
-    if (f < nch) cur = C::load(wb + (size_t)(f >> 2) * TI::BB, f & 3);
-    for (; f < nch; f += T) {
-        const int fn = f + T;
-        typename C::Raw nxt;
-        if (fn < nch) nxt = C::load(wb + (size_t)(fn >> 2) * TI::BB, fn & 3);
-        terms[f] = C::term(cur, f & 3, xl + c * XPAD, xs, c);
-        c += Tm;
-        if (c >= NC) c -= NC;
-        cur = nxt;
+    const int u = tid & 3;
+
+    // Dynamic distribution: each wave grabs the next batch of 64
+    // consecutive chunks from an LDS counter, keeping DEPTH batches in
+    // flight.  Waves are not served fairly by the issue arbiter (the oldest
+    // wins), so a static split leaves a long tail with few waves, and so
+    // little memory parallelism, at the end; with batches the waves finish
+    // together.  A chunk's term does not depend on which wave computes it,
+    // so the result stays deterministic.  Loads are issued unconditionally
+    // (indices past the end are clamped to the last chunk) so the compiler
+    // can count outstanding loads exactly.
+    const int last = nch - 1;
+    const int lane = tid & 63;
+    int* next = reinterpret_cast<int*>(terms + nch);
+    if (tid == 0) *next = 64 * DEPTH * (T >> 6);
+    int base[DEPTH];
+    typename C::Raw buf[DEPTH];
+#pragma unroll
+    for (int k = 0; k < DEPTH; k++) {
+        base[k] = (k * (T >> 6) + (tid >> 6)) * 64;     // first batches: static
+        const int fk = min(base[k] + lane, last);
+        buf[k] = C::load(wb + (size_t)(fk >> 2) * TI::BB, u);
+    }
+
+    stage_dma<TYPE>(a.x, K, tid, T, xl);
+    __syncthreads();
+    if (TI::XS_PER_CHUNK) {
+        stage_sums<TYPE>(K, tid, T, xl, xs);
+        __syncthreads();
+    }
+
+    while (base[0] < nch) {
+#pragma unroll
+        for (int k = 0; k < DEPTH; k++) {
+            int nb = 0;
+            if (lane == 0) nb = atomicAdd(next, 64);
+            const int f = base[k] + lane;
+            if (base[k] < nch) {
+                const int c = f % NC;
+                const double t = C::term(buf[k], u, xl + c * XPAD, xs, c);
+                if (f < nch) terms[f] = t;
+            }
+            base[k] = __builtin_amdgcn_readfirstlane(nb);
+            const int fn = min(base[k] + lane, last);
+            buf[k] = C::load(wb + (size_t)(fn >> 2) * TI::BB, u);
+        }
     }
     __syncthreads();
 
-    // 16 lanes per row: lane p sums terms p, p+16, ... then a butterfly.
-    for (int task = tid; task < R * 16; task += T) {
-        const int rho = task >> 4, p = task & 15;
+    // Row reduction: L lanes per row (L = 8..64, as many as T allows), lane
+    // p sums terms p, p+L, ... in two interleaved partial sums, then a
+    // butterfly over the L lanes.  The order depends only on NC and L.
+    int L = 8;
+    while (L < 64 && 2 * L * R <= T) L *= 2;
+    for (int task = tid; task < R * L; task += T) {
+        const int rho = task / L, p = task & (L - 1);
         const double* tr = terms + rho * NC;
-        double s = 0.0;
-        for (int i = p; i < NC; i += 16) s = s + tr[i];
-        s = s + __shfl_xor(s, 8, 16);
-        s = s + __shfl_xor(s, 4, 16);
-        s = s + __shfl_xor(s, 2, 16);
-        s = s + __shfl_xor(s, 1, 16);
+        double s0 = 0.0, s1 = 0.0;
+        int i = p;
+        for (; i + L < NC; i += 2 * L) {
+            s0 = s0 + tr[i];
+            s1 = s1 + tr[i + L];
+        }
+        if (i < NC) s0 = s0 + tr[i];
+        double s = s0 + s1;
+        s = s + dpp_f64<0xB1>(s);    // quad_perm [1,0,3,2]: lane ^ 1
+        s = s + dpp_f64<0x4E>(s);    // quad_perm [2,3,0,1]: lane ^ 2
+        s = s + dpp_f64<0x141>(s);   // row_half_mirror: lane i <-> 7 - i (8 lanes)
+        if (L >= 16) s = s + dpp_f64<0x140>(s);   // row_mirror (16 lanes)
+        if (L >= 32) s = s + __shfl_xor(s, 16, 64);
+        if (L >= 64) s = s + __shfl_xor(s, 32, 64);
         if (p == 0) {
             float v = (float)s;
             if (a.add) v = a.add[r0 + rho] + v;
@@ -564,17 +663,33 @@ __global__ __launch_bounds__(256) void kq_dequant_kernel(const uint8_t* __restri
 }
 
 template <int TYPE>
-int launch_gemv(const GemvArgs& a, int grid, int threads, hipStream_t st) {
+int launch_gemv(const GemvArgs& a, int grid, int threads, int depth, hipStream_t st) {
     const int NC = a.K >> 6;
-    const size_t lds = (size_t)x_lds_bytes<TYPE>(a.K) + (size_t)a.rows_per_wg * NC * 8;
-    hipLaunchKernelGGL(kq_gemv_kernel<TYPE>, dim3(grid), dim3(threads), lds, st, a);
+    const size_t lds = (size_t)x_lds_bytes<TYPE>(a.K) + (size_t)a.rows_per_wg * NC * 8 + 16;
+    switch (depth) {
+    case 1: hipLaunchKernelGGL((kq_gemv_kernel<TYPE, 1>), dim3(grid), dim3(threads), lds, st, a); break;
+    case 2: hipLaunchKernelGGL((kq_gemv_kernel<TYPE, 2>), dim3(grid), dim3(threads), lds, st, a); break;
+    case 3: hipLaunchKernelGGL((kq_gemv_kernel<TYPE, 3>), dim3(grid), dim3(threads), lds, st, a); break;
+    case 4: hipLaunchKernelGGL((kq_gemv_kernel<TYPE, 4>), dim3(grid), dim3(threads), lds, st, a); break;
+    default: hipLaunchKernelGGL((kq_gemv_kernel<TYPE, 6>), dim3(grid), dim3(threads), lds, st, a); break;
+    }
     return (int)hipGetLastError();
+}
+
+template <int TYPE, int D>
+int set_lds1(int bytes) {
+    return (int)hipFuncSetAttribute(reinterpret_cast<const void*>(&kq_gemv_kernel<TYPE, D>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
 }
 
 template <int TYPE>
 int set_lds(int bytes) {
-    return (int)hipFuncSetAttribute(reinterpret_cast<const void*>(&kq_gemv_kernel<TYPE>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    int e = set_lds1<TYPE, 1>(bytes);
+    if (!e) e = set_lds1<TYPE, 2>(bytes);
+    if (!e) e = set_lds1<TYPE, 3>(bytes);
+    if (!e) e = set_lds1<TYPE, 4>(bytes);
+    if (!e) e = set_lds1<TYPE, 6>(bytes);
+    return e;
 }
 
 template <int TYPE>
@@ -601,7 +716,7 @@ long kqk_gemv_lds_bytes(int type, int K, int rows_per_wg) {
     case T_NIB: x = x_lds_bytes<T_NIB>(K); break;
     default: return -1;
     }
-    return x + (long)rows_per_wg * NC * 8;
+    return x + (long)rows_per_wg * NC * 8 + 16;
 }
 
 // Allows dynamic LDS up to `bytes` for every GEMV instantiation.
@@ -614,19 +729,20 @@ int kqk_set_max_lds(int bytes) {
 }
 
 // threads must be 256, 512 or 1024; rows_per_wg * (K/64) * 8 plus the x
-// staging must fit the LDS limit set above (checked by the caller).
+// staging must fit the LDS limit set above (checked by the caller); depth
+// (1..3) is the number of chunks each lane keeps in flight.
 int kqk_launch_gemv(int type, const void* w, const float* x, const float* add, float* y,
-                    int N, int K, int rows_per_wg, int threads, hipStream_t st) {
+                    int N, int K, int rows_per_wg, int threads, int depth, hipStream_t st) {
     GemvArgs a;
     a.w = static_cast<const uint8_t*>(w);
     a.x = x; a.add = add; a.y = y;
     a.N = N; a.K = K; a.rows_per_wg = rows_per_wg; a.B = 1;
     const int grid = (N + rows_per_wg - 1) / rows_per_wg;
     switch (type) {
-    case T_Q4K: return launch_gemv<T_Q4K>(a, grid, threads, st);
-    case T_Q6K: return launch_gemv<T_Q6K>(a, grid, threads, st);
-    case T_Q2K: return launch_gemv<T_Q2K>(a, grid, threads, st);
-    case T_NIB: return launch_gemv<T_NIB>(a, grid, threads, st);
+    case T_Q4K: return launch_gemv<T_Q4K>(a, grid, threads, depth, st);
+    case T_Q6K: return launch_gemv<T_Q6K>(a, grid, threads, depth, st);
+    case T_Q2K: return launch_gemv<T_Q2K>(a, grid, threads, depth, st);
+    case T_NIB: return launch_gemv<T_NIB>(a, grid, threads, depth, st);
     default: return -1;
     }
 }

@@ -24,7 +24,7 @@
 /* launchers (kq_kernels.hip) */
 long kqk_gemv_lds_bytes(int type, int K, int rows_per_wg);
 int kqk_launch_gemv(int type, const void* w, const float* x, const float* add, float* y,
-                    int N, int K, int rows_per_wg, int threads, hipStream_t st);
+                    int N, int K, int rows_per_wg, int threads, int depth, hipStream_t st);
 int kqk_launch_dequant(int type, const void* w, float* y, long nblocks, hipStream_t st);
 int kqk_set_max_lds(int bytes);
 
@@ -194,8 +194,9 @@ static const void* tensor_dev(const kq_tensor* w, int N, int K) {
 /* ----------------------------------------------------------- planning */
 /* One workgroup per CU, each owning ceil(N / n_cu) consecutive rows, as
  * long as x plus the per-chunk terms fit in LDS; workgroup size grows with
- * the chunks it owns.  KQ_ROWS_PER_WG / KQ_WG_THREADS override (tuning). */
-static int plan(int type, int N, int K, int* rows, int* threads) {
+ * the chunks it owns.  KQ_ROWS_PER_WG / KQ_WG_THREADS / KQ_DEPTH override
+ * (tuning). */
+static int plan(int type, int N, int K, int* rows, int* threads, int* depth) {
     const int NC = K / 64;
     const long xb = kqk_gemv_lds_bytes(type, K, 0);
     if (xb < 0) return kq_fail("type %d has no GEMV kernel", type);
@@ -209,13 +210,18 @@ static int plan(int type, int N, int K, int* rows, int* threads) {
     if (R < 1) R = 1;
     long chunks = R * NC;
     int T = chunks >= 4096 ? 1024 : chunks >= 1024 ? 512 : 256;
+
     const char* et = getenv("KQ_WG_THREADS");
     if (et) {
         int t = atoi(et);
         if (t == 256 || t == 512 || t == 1024) T = t;
     }
+    int D = 2;
+    const char* ed = getenv("KQ_DEPTH");
+    if (ed && atoi(ed) >= 1 && atoi(ed) <= 6) D = atoi(ed);
     *rows = (int)R;
     *threads = T;
+    *depth = D;
     return 0;
 }
 
@@ -235,9 +241,9 @@ int kq_gemv_dev(int type, const void* w, const float* x, const float* add, float
     if (check_shape(type, N, K) || kq_ready()) return -1;
     if (!w || !x || !y) return kq_fail("kq_gemv_dev: NULL pointer");
     if ((uintptr_t)x & 15) return kq_fail("kq_gemv_dev: x must be 16-byte aligned");
-    int R = 1, T = 256;
-    if (plan(type, N, K, &R, &T)) return -1;
-    int e = kqk_launch_gemv(type, w, x, add, y, N, K, R, T, pick(stream));
+    int R = 1, T = 256, D = 2;
+    if (plan(type, N, K, &R, &T, &D)) return -1;
+    int e = kqk_launch_gemv(type, w, x, add, y, N, K, R, T, D, pick(stream));
     if (e) return kq_fail("gemv launch: %s", hipGetErrorString((hipError_t)e));
     return 0;
 }
