@@ -119,6 +119,33 @@ int kq_gemv_dev(int type, const void* w, const float* x, const float* add, float
 int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,
                        int B, int N, int K, kq_stream stream);
 
+/* One segment of a batched launch: ngroups * rows_per_group rows of one
+ * type and row length K.  Rows [g*rows_per_group, (g+1)*rows_per_group)
+ * start at device address w[g] (separate bases: e.g. the selected MoE
+ * expert slices, stratum_arch_moe.inc.c:327-337) and read x, or, when
+ * x_stride != 0, x + g*x_stride.  y[i] (and add[i]) is segment row i. */
+#define KQ_MAX_SEGMENTS 8
+#define KQ_MAX_GROUPS 16
+typedef struct kq_segment {
+    int type;
+    int K;
+    int rows_per_group;
+    int ngroups;
+    const void* w[KQ_MAX_GROUPS];
+    const float* x;
+    int x_stride;
+    const float* add;
+    float* y;
+} kq_segment;
+
+/* Runs up to KQ_MAX_SEGMENTS segments in ONE launch, in order, each with
+ * the numerics of kq_gemv_dev.  Consecutive segments that read the same x
+ * (the same-input groups of st_q4k_group, stratum_linear.h:1086) stage it
+ * once.  No counterpart in the reference, which issues one call per tensor;
+ * it exists so a device-resident decode step pays one launch for several
+ * matvecs (a layer's QKV, gate+up, or a set of MoE expert slices). */
+int kq_gemv_segments_dev(const kq_segment* segs, int nseg, kq_stream stream);
+
 /* Bit-exact dequantization of nblocks consecutive blocks into 256*nblocks
  * floats (q4k_dequant_row_scalar and peers, stratum_q4k.h:67-93,
  * stratum_q6k.h:17-36, stratum_q2k.h:16-42). */

@@ -35,8 +35,44 @@ LIB_PATH = os.path.join(HERE, "libkqgemv.so")
 EXPORTS = (
     "kq_linear_init", "kq_register_region", "kq_device_ptr", "kq_linear_shutdown",
     "kq_last_error", "kq_linear_dispatch", "kq_linear_dispatch_add", "kq_linear_multix",
-    "kq_q4k_group", "kq_gemv_dev", "kq_gemv_multix_dev", "kq_dequant_dev", "kq_row_bytes",
+    "kq_q4k_group", "kq_gemv_dev", "kq_gemv_multix_dev", "kq_gemv_segments_dev",
+    "kq_dequant_dev", "kq_row_bytes",
 )
+
+MAX_SEGMENTS = 8
+MAX_GROUPS = 16
+
+
+class KqSegment(ctypes.Structure):
+    """kq_segment (include/kq_gemv.h): one segment of a batched launch."""
+
+    _fields_ = [
+        ("type", ctypes.c_int),
+        ("K", ctypes.c_int),
+        ("rows_per_group", ctypes.c_int),
+        ("ngroups", ctypes.c_int),
+        ("w", ctypes.c_void_p * MAX_GROUPS),
+        ("x", ctypes.c_void_p),
+        ("x_stride", ctypes.c_int),
+        ("add", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
+    ]
+
+
+def segment(qtype: int, K: int, rows_per_group: int, w_ptrs, x_ptr: int, y_ptr: int,
+            x_stride: int = 0, add_ptr: int | None = None) -> KqSegment:
+    s = KqSegment()
+    s.type = qtype
+    s.K = K
+    s.rows_per_group = rows_per_group
+    s.ngroups = len(w_ptrs)
+    for i, p in enumerate(w_ptrs):
+        s.w[i] = p
+    s.x = x_ptr
+    s.x_stride = x_stride
+    s.add = add_ptr
+    s.y = y_ptr
+    return s
 
 
 class KqTensor(ctypes.Structure):
@@ -99,6 +135,7 @@ def lib() -> ctypes.CDLL:
     L.kq_gemv_dev.argtypes = [I, P, P, P, P, I, I, P]
     L.kq_gemv_multix_dev.argtypes = [I, P, P, P, I, I, I, P]
     L.kq_dequant_dev.argtypes = [I, P, P, ctypes.c_int64, P]
+    L.kq_gemv_segments_dev.argtypes = [ctypes.POINTER(KqSegment), I, P]
     L.kq_row_bytes.argtypes = [I, I]
     L.kq_row_bytes.restype = ctypes.c_int64
     _LIB = L
@@ -178,6 +215,12 @@ def gemv_multix_dev(qtype: int, w_ptr: int, xs_ptr: int, ys_ptr: int, B: int, N:
                     K: int, stream: int | None = None) -> None:
     _check(lib().kq_gemv_multix_dev(qtype, w_ptr, xs_ptr, ys_ptr, B, N, K, stream),
            "kq_gemv_multix_dev")
+
+
+def gemv_segments_dev(segs: list[KqSegment], stream: int | None = None) -> None:
+    """One launch over up to 8 segments (kq_gemv_segments_dev)."""
+    arr = (KqSegment * len(segs))(*segs)
+    _check(lib().kq_gemv_segments_dev(arr, len(segs), stream), "kq_gemv_segments_dev")
 
 
 def dequant_dev(qtype: int, w_ptr: int, y_ptr: int, nblocks: int,

@@ -45,6 +45,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #pragma clang fp contract(off)
 
 namespace {
@@ -56,21 +58,14 @@ constexpr int T_NIB = 42;
 
 constexpr int XPAD = 17;  // float4 slots per 64-weight chunk in LDS (16 + 1 pad)
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 template <int TYPE> struct TypeInfo;
 template <> struct TypeInfo<T_Q4K> { static constexpr int BB = 144; static constexpr bool LINEAR = true;  static constexpr int XS_PER_CHUNK = 2; };
 template <> struct TypeInfo<T_Q6K> { static constexpr int BB = 210; static constexpr bool LINEAR = false; static constexpr int XS_PER_CHUNK = 0; };
 template <> struct TypeInfo<T_Q2K> { static constexpr int BB = 84;  static constexpr bool LINEAR = false; static constexpr int XS_PER_CHUNK = 4; };
 template <> struct TypeInfo<T_NIB> { static constexpr int BB = 148; static constexpr bool LINEAR = true;  static constexpr int XS_PER_CHUNK = 4; };
 
-struct GemvArgs {
-    const uint8_t* w;    // row 0 of the tensor (device)
-    const float* x;      // [B][K] activations (device)
-    const float* add;    // [B][N] residual or nullptr
-    float* y;            // [B][N] output
-    int N, K;
-    int rows_per_wg;     // rows owned by one workgroup
-    int B;               // streams (1 for the plain GEMV)
-};
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
     _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h);
@@ -88,6 +83,48 @@ __device__ __forceinline__ void ubytes(uint32_t v, float& a, float& b, float& c,
     d = (float)(v >> 24);
 }
 
+// fl(b * x) * 2^-149 for byte SEL (= b) of v: v_mul_f32 with an SDWA byte
+// select reads the zero-extended byte b as the binary32 bit pattern b,
+// i.e. the denormal b * 2^-149, and multiplies it exactly (fp32 denormals
+// are enabled).  With x pre-scaled so that every nonzero product lands in
+// the normal range, the rounded product is the reference's fl(b * x)
+// times a power of two -- one instruction instead of convert + multiply.
+template <int SEL>
+__device__ __forceinline__ float bmul(uint32_t v, float x) {
+    float r;
+    if (SEL == 0)
+        asm("v_mul_f32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0 src1_sel:DWORD"
+            : "=v"(r) : "v"(v), "v"(x));
+    else if (SEL == 1)
+        asm("v_mul_f32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1 src1_sel:DWORD"
+            : "=v"(r) : "v"(v), "v"(x));
+    else if (SEL == 2)
+        asm("v_mul_f32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2 src1_sel:DWORD"
+            : "=v"(r) : "v"(v), "v"(x));
+    else
+        asm("v_mul_f32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3 src1_sel:DWORD"
+            : "=v"(r) : "v"(v), "v"(x));
+    return r;
+}
+
+// The products of the four bytes of v with x.x .. x.w: exact conversion +
+// multiply (SC = false), or the scaled single-instruction form above.
+// x4 is read as one 128-bit LDS load (f32x4, a native vector type, keeps
+// the compiler from splitting it into 32-bit reads).
+
+template <bool SC>
+__device__ __forceinline__ void bmul4(uint32_t v, const float4* x4, float& p0, float& p1,
+                                      float& p2, float& p3) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(x4);
+    if (SC) {
+        p0 = bmul<0>(v, x.x); p1 = bmul<1>(v, x.y); p2 = bmul<2>(v, x.z); p3 = bmul<3>(v, x.w);
+    } else {
+        float a, b, c, d;
+        ubytes(v, a, b, c, d);
+        p0 = a * x.x; p1 = b * x.y; p2 = c * x.z; p3 = d * x.w;
+    }
+}
+
 __device__ __forceinline__ uint32_t bfe(uint32_t v, uint32_t off, uint32_t w) {
     return __builtin_amdgcn_ubfe(v, off, w);
 }
@@ -103,113 +140,172 @@ __device__ __forceinline__ double dpp_f64(double v) {
 }
 
 // ------------------------------------------------------------------ LDS x
-// Chunk index c and float4 slot g (0..15) of x position p (p % 4 == 0).
-//  LINEAR  (Q4_K, type 42): chunk = 64 consecutive weights.
+// x is staged once per workgroup in LDS, in a padded chunk-major layout:
+// chunk c (the 64 x values one lane's weights meet) occupies float4 slots
+// c*XPAD .. c*XPAD+15.
+//  LINEAR  (Q4_K, type 42): chunk = 64 consecutive x values.
 //  strided (Q6_K, Q2_K):    chunk = (block, half, 16-sub) = 4 runs of 16
-//                           weights spaced 32 apart, slot g = 4*run + l/4.
-template <bool LINEAR>
-__device__ __forceinline__ void x_slot(int p, int& c, int& g) {
-    if (LINEAR) {
-        c = p >> 6;
-        g = (p >> 2) & 15;
-    } else {
-        const int bi = p >> 8, pp = p & 255;
-        const int h = pp >> 7, t = (pp >> 5) & 3, is = (pp >> 4) & 1, q = (pp >> 2) & 3;
-        c = 4 * bi + 2 * h + is;
-        g = 4 * t + q;
+//                           values spaced 32 apart, slot g = 4*run + l/4.
+//
+// Staging goes through registers in "sum groups": runs of consecutive x
+// that one lane loads (128-bit loads), sums in the reference's sequential
+// binary32 order when the type has min terms (Q4_K: 32 values per
+// sub-block, stratum_q4k.h:115-122; Q2_K / type 42: 16 values,
+// stratum_q2k.h:65-68), scales, and writes to its LDS slots.  The first
+// round of x loads is issued before the weight prefetch and consumed after
+// it, so x arrives first and the weights' latency overlaps the staging.
+//
+// Scaled mode (Q4_K, Q2_K, type 42).  The byte-select multiply (bmul) needs
+// every nonzero product q * x' (q >= 1) in the binary32 normal range, so x
+// is staged as x' = x * 2^KSC.  Every product and partial sum is then the
+// reference's times the same power of two -- exactly, as long as nothing
+// overflows or lands below the normal range -- and the factor is folded into
+// the block scale at the end (d * sc * 2^(149-KSC) < 2^128).  That holds when
+// every finite nonzero x has 2^(23-KSC) <= |x| < 2^(116-KSC), which also
+// keeps Q6_K's 16-term sums of int8 * x' below 2^127 (so a Q6_K segment can
+// read a scaled x).  When some x falls outside (subnormal, or beyond 2^52),
+// the workgroup restages x unscaled and uses the convert-and-multiply path.
+constexpr int KSC = 64;
+constexpr uint32_t KSC_EMIN = 127 + 23 - KSC;    // smallest allowed biased exponent
+constexpr uint32_t KSC_EMAX = 127 + 116 - KSC;   // first disallowed biased exponent
+
+template <int TYPE> struct XGroup {
+    static constexpr int G4 = TYPE == T_Q4K ? 8 : 4;            // float4 per group
+    static constexpr bool SUMS = TypeInfo<TYPE>::XS_PER_CHUNK != 0;
+};
+
+// true when v is finite, nonzero and outside the scaled-mode window
+__device__ __forceinline__ bool out_of_window(float v) {
+    const uint32_t e = (__float_as_uint(v) & 0x7fffffffu) >> 23;
+    const bool zero = (__float_as_uint(v) & 0x7fffffffu) == 0u;
+    return !zero && e != 255u && (e < KSC_EMIN || e >= KSC_EMAX);
+}
+
+// LDS slot (within one x) of float4 q of group gi, and the xs index (within
+// one x) of the group's sum.
+template <int TYPE>
+__device__ __forceinline__ void group_place(int gi, int& slot0, int& xsi) {
+    if (TYPE == T_Q4K) {               // sub-block gi: chunk gi/2, slots 8*(gi&1)..
+        slot0 = (gi >> 1) * XPAD + 8 * (gi & 1);
+        xsi = gi;
+    } else if (TYPE == T_NIB) {        // 16-group gi: chunk gi/4, slots 4*(gi&3)..
+        slot0 = (gi >> 2) * XPAD + 4 * (gi & 3);
+        xsi = gi;                      // == 4 * chunk + (gi & 3)
+    } else {                           // strided: x positions 16 gi .. 16 gi + 15
+        const int p = 16 * gi, bi = p >> 8, pp = p & 255;
+        const int h = pp >> 7, t = (pp >> 5) & 3, is = (pp >> 4) & 1;
+        const int c = 4 * bi + 2 * h + is;
+        slot0 = c * XPAD + 4 * t;
+        xsi = 4 * c + t;
     }
 }
 
-// Staging of x (one stream) into LDS.
-//   stage_dma  -- x goes straight from global memory into the padded LDS
-//                 layout with global_load_lds_dwordx4 (lane i of a wave
-//                 writes 16 bytes at base + 16 i).  No registers are
-//                 involved, so every x load of the workgroup is issued back
-//                 to back right after the weight prefetch and the whole
-//                 staging costs about one memory latency;
-//   stage_sums -- after a barrier, the per-sub-block plain sums the min
-//                 terms need, read back from LDS (sequential binary32,
-//                 exactly as the reference's xs1/xs2 and sx accumulators).
-
-// global float4 index of LDS slot s (chunk c = s / XPAD, slot g = s % XPAD);
-// the pad slot (g == 16) is filled with a copy of slot 0 and never read
-template <bool LINEAR>
-__device__ __forceinline__ int x_src_of_slot(int s) {
-    const int c = s / XPAD;
-    int g = s - c * XPAD;
-    if (g == 16) g = 0;
-    if (LINEAR) return 16 * c + g;
-    // strided: chunk c = (block, half h, sub is); slot g = 4*run + l/4
-    const int bi = c >> 2, h = (c >> 1) & 1, is = c & 1;
-    return 64 * bi + 32 * h + 4 * is + 8 * (g >> 2) + (g & 3);
-}
-
 template <int TYPE>
-__device__ __forceinline__ void stage_dma(const float* __restrict__ x, int K, int tid, int T,
-                                          float4* xl) {
-    const int total = (K >> 6) * XPAD;       // slots, pads included
-    const int wbase = tid & ~63;
-    const float4* x4 = reinterpret_cast<const float4*>(x);
-    for (int s0 = 0; s0 < total; s0 += T) {
-        const int s = s0 + tid;
-        if (s < total) {
-            const float4* src = x4 + x_src_of_slot<TypeInfo<TYPE>::LINEAR>(s);
-            __builtin_amdgcn_global_load_lds(
-                src, (__attribute__((address_space(3))) void*)(xl + s0 + wbase), 16, 0, 0);
-        }
+struct XStage {
+    static constexpr int G4 = XGroup<TYPE>::G4;
+    const float* x;
+    int x_stride, per, total;          // groups per x, groups over all staged x
+    int NC;
+
+    __device__ __forceinline__ void load(int gidx, f32x4* v) const {
+        const int gc = min(gidx, total - 1);           // branch-free: clamped
+        const int gx = per == total ? 0 : gc / per;
+        const f32x4* src = reinterpret_cast<const f32x4*>(x + (size_t)gx * x_stride) +
+                           (size_t)(gc - gx * per) * G4;
+#pragma unroll
+        for (int q = 0; q < G4; q++) v[q] = src[q];
     }
-}
 
+    // writes group gidx (if it exists); returns "out of window" for it
+    __device__ __forceinline__ bool store(int gidx, const f32x4* v, bool scale, bool sums,
+                                          float4* xl, float* xs) const {
+        if (gidx >= total) return false;
+        const int gx = per == total ? 0 : gidx / per;
+        const int gi = gidx - gx * per;
+        int slot0, xsi;
+        group_place<TYPE>(gi, slot0, xsi);
+        f32x4* dst = reinterpret_cast<f32x4*>(xl) + gx * NC * XPAD + slot0;
+        bool bad = false;
+        float acc = 0.0f;
+#pragma unroll
+        for (int q = 0; q < G4; q++) {
+            const f32x4 w = v[q];
+            acc = acc + w.x; acc = acc + w.y; acc = acc + w.z; acc = acc + w.w;
+            bad |= out_of_window(w.x) | out_of_window(w.y) | out_of_window(w.z) |
+                   out_of_window(w.w);
+            f32x4 o = w;
+            if (scale) {
+                o.x = ldexpf(w.x, KSC); o.y = ldexpf(w.y, KSC);
+                o.z = ldexpf(w.z, KSC); o.w = ldexpf(w.w, KSC);
+            }
+            dst[q] = o;
+        }
+        if (XGroup<TYPE>::SUMS && sums) xs[gx * per + xsi] = acc;
+        return bad;
+    }
+};
+
+// Recomputes the per-group sums from an x already in LDS (for a segment
+// whose type needs sums laid out differently from the staging type's).
+// When the staged x is scaled by 2^ks, the sum of the scaled values is
+// scaled back: power-of-two scaling commutes with each binary32 addition
+// here (no overflow, and a sum below the normal range is exact), so the
+// result equals the unscaled sum.
 template <int TYPE>
-__device__ __forceinline__ void stage_sums(int K, int tid, int T, const float4* xl, float* xs) {
-    if (TYPE == T_Q4K) {
-        // xs[sb] = sum of the 32 x of sub-block sb (stratum_q4k.h:115-122):
-        // chunk sb/2, float4 slots 8*(sb&1) .. +7 of the linear layout
-        for (int sb = tid; sb < (K >> 5); sb += T) {
-            const float4* p = xl + (sb >> 1) * XPAD + 8 * (sb & 1);
-            float s = 0.0f;
+__device__ __forceinline__ void resum(int K, int ngx, int tid, int T, const float4* xl,
+                                      float* xs, int ks) {
+    constexpr int G4 = XGroup<TYPE>::G4;
+    const int per = K / (4 * G4), NC = K >> 6;
+    for (int t = tid; t < ngx * per; t += T) {
+        const int gx = t / per, gi = t - gx * per;
+        int slot0, xsi;
+        group_place<TYPE>(gi, slot0, xsi);
+        const f32x4* p = reinterpret_cast<const f32x4*>(xl) + gx * NC * XPAD + slot0;
+        float acc = 0.0f;
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const float4 v = p[k];
-                s = s + v.x; s = s + v.y; s = s + v.z; s = s + v.w;
-            }
-            xs[sb] = s;
+        for (int q = 0; q < G4; q++) {
+            const f32x4 v = p[q];
+            acc = acc + v.x; acc = acc + v.y; acc = acc + v.z; acc = acc + v.w;
         }
-    } else if (TYPE == T_Q2K || TYPE == T_NIB) {
-        // sums over 16-weight groups (stratum_q2k.h:65-68), stored at the
-        // chunk's slot: Q2_K chunk (block, s, h) holds groups j = 0..3 (its
-        // float4 slots 4j..4j+3), type-42 chunk u holds groups 4u..4u+3.
-        for (int gi = tid; gi < (K >> 4); gi += T) {
-            int c, j;
-            if (TYPE == T_NIB) {
-                c = gi >> 2;
-                j = gi & 3;
-            } else {
-                const int bi = gi >> 4, g16 = gi & 15;
-                c = 4 * bi + 2 * (g16 >> 3) + (g16 & 1);
-                j = (g16 >> 1) & 3;
-            }
-            const float4* p = xl + c * XPAD + 4 * j;
-            float s = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const float4 v = p[k];
-                s = s + v.x; s = s + v.y; s = s + v.z; s = s + v.w;
-            }
-            xs[c * 4 + j] = s;
-        }
+        xs[gx * per + xsi] = ks ? ldexpf(acc, -ks) : acc;
     }
 }
 
 // ------------------------------------------------------------ raw loads
-// 4-byte-aligned 128-bit vector: Q6_K/Q2_K/type-42 blocks are only dword
-// aligned; global_load_dwordx4 needs dword alignment only.
+// Weight bytes are read through explicit global-address-space pointers.
+// A generic pointer (e.g. one read back from the LDS weight-base table)
+// would make the compiler emit FLAT loads, which count against lgkmcnt as
+// well as vmcnt: every LDS wait in the loop would then also wait for the
+// whole weight prefetch.
+#define KQ_GLOBAL __attribute__((address_space(1)))
+typedef const uint8_t KQ_GLOBAL* wptr;
+
+__device__ __forceinline__ wptr to_global(const uint8_t* p) { return (wptr)p; }
+
+// 128-bit vectors: 16-byte aligned (Q4_K blocks are 144 B) and 4-byte
+// aligned (Q6_K/Q2_K/type-42 blocks are only dword aligned;
+// global_load_dwordx4 needs dword alignment only).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u32x2a __attribute__((ext_vector_type(2), aligned(4)));
 
-__device__ __forceinline__ uint4 ld16a4(const uint8_t* p) {
-    const u32x4a v = *reinterpret_cast<const u32x4a*>(p);
+__device__ __forceinline__ uint4 ld16(wptr p) {
+    const u32x4 v = *reinterpret_cast<const KQ_GLOBAL u32x4*>(p);
     return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint4 ld16a4(wptr p) {
+    const u32x4a v = *reinterpret_cast<const KQ_GLOBAL u32x4a*>(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ld8a4(wptr p) {
+    const u32x2a v = *reinterpret_cast<const KQ_GLOBAL u32x2a*>(p);
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint32_t ld4(wptr p) {
+    return *reinterpret_cast<const KQ_GLOBAL uint32_t*>(p);
+}
+__device__ __forceinline__ uint32_t ld2(wptr p) {
+    return *reinterpret_cast<const KQ_GLOBAL uint16_t*>(p);
 }
 
 struct RawQ4 { uint4 hd, qa, qb; };
@@ -217,60 +313,56 @@ struct RawQ6 { uint32_t l[5], h[5], q[5], s[3], d; uint32_t sh; };
 struct RawQ2 { uint4 q; uint2 s; uint32_t dd; };
 struct RawNB { uint4 qa, qb; uint32_t s, dd; };
 
-__device__ __forceinline__ RawQ4 load_q4k(const uint8_t* blk, int j) {
+__device__ __forceinline__ RawQ4 load_q4k(wptr blk, int j) {
     RawQ4 r;
-    r.hd = *reinterpret_cast<const uint4*>(blk);
-    r.qa = *reinterpret_cast<const uint4*>(blk + 16 + 32 * j);
-    r.qb = *reinterpret_cast<const uint4*>(blk + 32 + 32 * j);
+    r.hd = ld16(blk);
+    r.qa = ld16(blk + 16 + 32 * j);
+    r.qb = ld16(blk + 32 + 32 * j);
     return r;
 }
 
 // Q6_K blocks are 210 B, so odd blocks start 2 bytes off a dword.  Loads
 // are dword-aligned and realigned with v_alignbit (shift 0 or 16).
-__device__ __forceinline__ void load5(const uint8_t* p, uint32_t* o) {
+__device__ __forceinline__ void load5(wptr p, uint32_t* o) {
     const uint4 v = ld16a4(p);
     o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
-    o[4] = reinterpret_cast<const uint32_t*>(p)[4];
+    o[4] = ld4(p + 16);
 }
 
-__device__ __forceinline__ RawQ6 load_q6k(const uint8_t* blk, int u) {
+__device__ __forceinline__ RawQ6 load_q6k(wptr blk, int u) {
     RawQ6 r;
     const int h = u >> 1, is = u & 1;
-    // realign by pointer arithmetic (not through an integer) so the
-    // compiler keeps the global address space and emits global_load, not
-    // flat_load (flat loads also count against lgkmcnt, so every LDS wait
-    // would wait for the weight prefetch as well)
+    // realign by pointer arithmetic, which keeps the global address space
     const uint32_t mis = (uint32_t)reinterpret_cast<uintptr_t>(blk) & 3u;
     r.sh = mis * 8u;
-    const uint8_t* b4 = blk - mis;
+    const wptr b4 = blk - mis;
     load5(b4 + 64 * h + 16 * is, r.l);
     load5(b4 + 64 * h + 32 + 16 * is, r.h);
     load5(b4 + 128 + 32 * h + 16 * is, r.q);
     // scales: 8 bytes from 192 + 8h.  A third dword is needed only when the
     // block is 2 bytes off; when aligned, dword 1 is re-read instead so the
     // last block of a tensor never reads past its 210 bytes.
-    const uint32_t* sp = reinterpret_cast<const uint32_t*>(b4 + 192 + 8 * h);
-    r.s[0] = sp[0]; r.s[1] = sp[1]; r.s[2] = sp[r.sh ? 2 : 1];
-    r.d = *reinterpret_cast<const uint16_t*>(blk + 208);
+    const wptr sp = b4 + 192 + 8 * h;
+    r.s[0] = ld4(sp); r.s[1] = ld4(sp + 4); r.s[2] = ld4(sp + (r.sh ? 8 : 4));
+    r.d = ld2(blk + 208);
     return r;
 }
 
-__device__ __forceinline__ RawQ2 load_q2k(const uint8_t* blk, int u) {
+__device__ __forceinline__ RawQ2 load_q2k(wptr blk, int u) {
     RawQ2 r;
     const int s = u >> 1, h = u & 1;
     r.q = ld16a4(blk + 16 + 32 * s + 16 * h);
-    const u32x2a sv = *reinterpret_cast<const u32x2a*>(blk + 8 * s);
-    r.s = make_uint2(sv.x, sv.y);
-    r.dd = *reinterpret_cast<const uint32_t*>(blk + 80);
+    r.s = ld8a4(blk + 8 * s);
+    r.dd = ld4(blk + 80);
     return r;
 }
 
-__device__ __forceinline__ RawNB load_nib(const uint8_t* blk, int u) {
+__device__ __forceinline__ RawNB load_nib(wptr blk, int u) {
     RawNB r;
     r.qa = ld16a4(blk + 16 + 32 * u);
     r.qb = ld16a4(blk + 32 + 32 * u);
-    r.s = *reinterpret_cast<const uint32_t*>(blk + 4 * u);
-    r.dd = *reinterpret_cast<const uint32_t*>(blk + 144);
+    r.s = ld4(blk + 4 * u);
+    r.dd = ld4(blk + 144);
     return r;
 }
 
@@ -283,8 +375,10 @@ __device__ __forceinline__ uint32_t dw_of(const uint4& v, int k) {
 }
 
 // Q4_K chunk j of a block: sub-blocks 2j (low nibbles) and 2j+1 (high).
+// SC: x is scaled by 2^k and f = 2^(149-k) (see bmul); otherwise f = 1.
+template <bool SC>
 __device__ __forceinline__ double term_q4k(const RawQ4& r, int j, const float4* xc,
-                                           float xs1, float xs2) {
+                                           float xs1, float xs2, float f) {
     const float d = f16_bits_to_f32(r.hd.x & 0xffffu);
     const float dmin = f16_bits_to_f32(r.hd.x >> 16);
     // 6-bit scale/min decode (stratum_q4k.h:57-65) for sub-blocks 2j, 2j+1.
@@ -306,24 +400,29 @@ __device__ __forceinline__ double term_q4k(const RawQ4& r, int j, const float4* 
     const float d1 = d * (float)sc1, mm1 = dmin * (float)m1;
     const float d2 = d * (float)sc2, mm2 = dmin * (float)m2;
 
-    // high nibbles are converted in place (16 q), so a2 is 16x the
-    // reference's partial sum and d2 is used divided by 16 (both exact)
+    // high nibbles are used in place (16 q), so a2 is 16x the reference's
+    // partial sum and d2 is used divided by 16 (both exact)
     float a1 = 0.0f, a2 = 0.0f;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
         const uint32_t v = k < 4 ? dw_of(r.qa, k) : dw_of(r.qb, k - 4);
         const uint32_t vl = v & 0x0f0f0f0fu, vh = v & 0xf0f0f0f0u;
         float l0, l1, l2, l3, h0, h1, h2, h3;
-        ubytes(vl, l0, l1, l2, l3);
-        ubytes(vh, h0, h1, h2, h3);
-        const float4 xa = xc[k], xb = xc[8 + k];
-        a1 = a1 + l0 * xa.x; a2 = a2 + h0 * xb.x;
-        a1 = a1 + l1 * xa.y; a2 = a2 + h1 * xb.y;
-        a1 = a1 + l2 * xa.z; a2 = a2 + h2 * xb.z;
-        a1 = a1 + l3 * xa.w; a2 = a2 + h3 * xb.w;
+        bmul4<SC>(vl, xc + k, l0, l1, l2, l3);
+        bmul4<SC>(vh, xc + 8 + k, h0, h1, h2, h3);
+        a1 = a1 + l0; a2 = a2 + h0;
+        a1 = a1 + l1; a2 = a2 + h1;
+        a1 = a1 + l2; a2 = a2 + h2;
+        a1 = a1 + l3; a2 = a2 + h3;
+        // keep the x reads of later steps from being hoisted all at once
+        // (64 registers): schedule as "2 LDS reads, then 18 VALU" per step
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 18, 0);
     }
-    const float t1 = d1 * a1 - mm1 * xs1;
-    const float t2 = (d2 * 0.0625f) * a2 - mm2 * xs2;
+    const float d1s = SC ? d1 * f : d1;
+    const float d2s = d2 * (SC ? f * 0.0625f : 0.0625f);
+    const float t1 = d1s * a1 - mm1 * xs1;
+    const float t2 = d2s * a2 - mm2 * xs2;
     return (double)t1 + (double)t2;
 }
 
@@ -332,7 +431,8 @@ __device__ __forceinline__ float i8f(uint32_t v, int e) {
 }
 
 // Q6_K chunk (half h, sub is): four 16-weight sums a_t, t = 0..3.
-__device__ __forceinline__ double term_q6k(const RawQ6& r, int u, const float4* xc) {
+// f6 = 2^(-2-k) when x is scaled by 2^k (k = 0: unscaled).
+__device__ __forceinline__ double term_q6k(const RawQ6& r, int u, const float4* xc, double f6) {
     const int is = u & 1;
     const uint32_t sh = r.sh;
     float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -360,7 +460,7 @@ __device__ __forceinline__ double term_q6k(const RawQ6& r, int u, const float4* 
     const uint32_t S0 = __builtin_amdgcn_alignbit(r.s[1], r.s[0], sh);
     const uint32_t S1 = __builtin_amdgcn_alignbit(r.s[2], r.s[1], sh);
     const uint32_t dh = r.d;
-    const double dq = (double)f16_bits_to_f32(dh) * 0.25;  // exact
+    const double dq = (double)f16_bits_to_f32(dh) * f6;  // exact
     const uint32_t Sa = is ? (S0 >> 8) : S0;
     const uint32_t Sb = is ? (S1 >> 8) : S1;
     const double t0 = (dq * (double)(int8_t)(uint8_t)(Sa)) * (double)a[0];
@@ -371,8 +471,9 @@ __device__ __forceinline__ double term_q6k(const RawQ6& r, int u, const float4* 
 }
 
 // Q2_K chunk (half s, 16-sub h): groups j = 0..3, q = (qs >> 2j) & 3.
+template <bool SC>
 __device__ __forceinline__ double term_q2k(const RawQ2& r, int u, const float4* xc,
-                                           const float4 xs4) {
+                                           const float4 xs4, float f) {
     const int h = u & 1;
     const float d = f16_bits_to_f32(r.dd & 0xffffu);
     const float dmin = f16_bits_to_f32(r.dd >> 16);
@@ -392,15 +493,14 @@ __device__ __forceinline__ double term_q2k(const RawQ2& r, int u, const float4* 
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const uint32_t v = dw_of(r.q, k) & (0x03030303u << (2 * j));
-            float q0, q1, q2, q3;
-            ubytes(v, q0, q1, q2, q3);
-            const float4 xv = xc[4 * j + k];
-            qx = qx + q0 * xv.x;
-            qx = qx + q1 * xv.y;
-            qx = qx + q2 * xv.z;
-            qx = qx + q3 * xv.w;
+            float p0, p1, p2, p3;
+            bmul4<SC>(v, xc + 4 * j + k, p0, p1, p2, p3);
+            qx = qx + p0;
+            qx = qx + p1;
+            qx = qx + p2;
+            qx = qx + p3;
         }
-        const float t = (dl * inv) * qx - ml * sx[j];
+        const float t = (dl * (SC ? inv * f : inv)) * qx - ml * sx[j];
         acc = acc + (double)t;
     }
     return acc;
@@ -408,7 +508,9 @@ __device__ __forceinline__ double term_q2k(const RawQ2& r, int u, const float4* 
 
 // type-42 chunk u: 64 consecutive weights = groups 4u..4u+3; group g's
 // 16 values are the low (g even) or high (g odd) nibbles of 16 bytes.
-__device__ __forceinline__ double term_nib(const RawNB& r, const float4* xc, const float4 xs4) {
+template <bool SC>
+__device__ __forceinline__ double term_nib(const RawNB& r, const float4* xc, const float4 xs4,
+                                           float f) {
     const float d = f16_bits_to_f32(r.dd & 0xffffu);
     const float dmin = f16_bits_to_f32(r.dd >> 16);
     const float sx[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
@@ -426,15 +528,14 @@ __device__ __forceinline__ double term_nib(const RawNB& r, const float4* xc, con
         for (int k = 0; k < 4; k++) {
             uint32_t v = dw_of(src, k);
             v = (g & 1) ? (v & 0xf0f0f0f0u) : (v & 0x0f0f0f0fu);
-            float q0, q1, q2, q3;
-            ubytes(v, q0, q1, q2, q3);
-            const float4 xv = xc[4 * g + k];
-            qx = qx + q0 * xv.x;
-            qx = qx + q1 * xv.y;
-            qx = qx + q2 * xv.z;
-            qx = qx + q3 * xv.w;
+            float p0, p1, p2, p3;
+            bmul4<SC>(v, xc + 4 * g + k, p0, p1, p2, p3);
+            qx = qx + p0;
+            qx = qx + p1;
+            qx = qx + p2;
+            qx = qx + p3;
         }
-        const float t = (dl * inv) * qx - ml * sx[g];
+        const float t = (dl * (SC ? inv * f : inv)) * qx - ml * sx[g];
         acc = acc + (double)t;
     }
     return acc;
@@ -445,119 +546,265 @@ template <int TYPE> struct Chunk;
 
 template <> struct Chunk<T_Q4K> {
     using Raw = RawQ4;
-    static __device__ __forceinline__ Raw load(const uint8_t* blk, int u) { return load_q4k(blk, u); }
+    static __device__ __forceinline__ Raw load(wptr blk, int u) { return load_q4k(blk, u); }
+    static __device__ __forceinline__ void drain(const Raw& r) {
+        asm volatile("" ::"v"(r.hd.x), "v"(r.qa.x), "v"(r.qb.x));
+    }
+    template <bool SC>
     static __device__ __forceinline__ double term(const Raw& r, int u, const float4* xc,
-                                                  const float* xs, int c) {
+                                                  const float* xs, int c, float f, double) {
         const float2 s = reinterpret_cast<const float2*>(xs)[c];
-        return term_q4k(r, u, xc, s.x, s.y);
+        return term_q4k<SC>(r, u, xc, s.x, s.y, f);
     }
 };
 template <> struct Chunk<T_Q6K> {
     using Raw = RawQ6;
-    static __device__ __forceinline__ Raw load(const uint8_t* blk, int u) { return load_q6k(blk, u); }
+    static __device__ __forceinline__ Raw load(wptr blk, int u) { return load_q6k(blk, u); }
+    static __device__ __forceinline__ void drain(const Raw& r) {
+        asm volatile("" ::"v"(r.l[0]), "v"(r.l[4]), "v"(r.h[0]), "v"(r.h[4]), "v"(r.q[0]),
+                     "v"(r.q[4]), "v"(r.s[0]), "v"(r.s[1]), "v"(r.s[2]), "v"(r.d));
+    }
+    template <bool SC>
     static __device__ __forceinline__ double term(const Raw& r, int u, const float4* xc,
-                                                  const float*, int) {
-        return term_q6k(r, u, xc);
+                                                  const float*, int, float, double f6) {
+        return term_q6k(r, u, xc, f6);
     }
 };
 template <> struct Chunk<T_Q2K> {
     using Raw = RawQ2;
-    static __device__ __forceinline__ Raw load(const uint8_t* blk, int u) { return load_q2k(blk, u); }
+    static __device__ __forceinline__ Raw load(wptr blk, int u) { return load_q2k(blk, u); }
+    static __device__ __forceinline__ void drain(const Raw& r) {
+        asm volatile("" ::"v"(r.q.x), "v"(r.s.x), "v"(r.dd));
+    }
+    template <bool SC>
     static __device__ __forceinline__ double term(const Raw& r, int u, const float4* xc,
-                                                  const float* xs, int c) {
-        return term_q2k(r, u, xc, reinterpret_cast<const float4*>(xs)[c]);
+                                                  const float* xs, int c, float f, double) {
+        return term_q2k<SC>(r, u, xc, reinterpret_cast<const float4*>(xs)[c], f);
     }
 };
 template <> struct Chunk<T_NIB> {
     using Raw = RawNB;
-    static __device__ __forceinline__ Raw load(const uint8_t* blk, int u) { return load_nib(blk, u); }
+    static __device__ __forceinline__ Raw load(wptr blk, int u) { return load_nib(blk, u); }
+    static __device__ __forceinline__ void drain(const Raw& r) {
+        asm volatile("" ::"v"(r.qa.x), "v"(r.qb.x), "v"(r.s), "v"(r.dd));
+    }
+    template <bool SC>
     static __device__ __forceinline__ double term(const Raw& r, int, const float4* xc,
-                                                  const float* xs, int c) {
-        return term_nib(r, xc, reinterpret_cast<const float4*>(xs)[c]);
+                                                  const float* xs, int c, float f, double) {
+        return term_nib<SC>(r, xc, reinterpret_cast<const float4*>(xs)[c], f);
     }
 };
 
-template <int TYPE>
-__host__ __device__ constexpr int xs_floats_per_chunk() { return TypeInfo<TYPE>::XS_PER_CHUNK; }
+// ------------------------------------------------------------- the GEMV
+// One persistent launch runs a list of segments.  A segment is a tensor of
+// N = ngroups * Ng rows of one type and row length K; rows of group g live
+// at w[g] + row * row_bytes (separate weight bases: the MoE expert slices),
+// and use the shared x or, when x_stride != 0, their own x at x + g *
+// x_stride.  y and add are indexed by the segment row g * Ng + row.
+//
+// Workgroup b of G owns rows b, b + G, b + 2G, ... of every segment, so at
+// any moment all workgroups stream neighbouring rows (DRAM locality).  Its
+// R rows are R * NC chunks of 64 weights; the waves take batches of 64
+// consecutive chunks (first batch static, then from an LDS counter: the
+// issue arbiter favours old waves, and a static split would leave a long,
+// poorly overlapped tail).  Each chunk's binary64 term goes to LDS; after
+// a barrier, L lanes per row reduce that row's terms in a fixed order, so
+// the result depends on nothing but the inputs.
+//
+// x is staged once per segment, or not at all when the segment uses the
+// same x (same pointer, K and layout) as the previous one: the same-input
+// groups (QKV, gate+up).
+constexpr int MAXSEG = 8;
+constexpr int MAXG = 16;
 
-// LDS bytes for x staging of one stream
-template <int TYPE>
-__host__ __device__ inline int x_lds_bytes(int K) {
-    const int NC = K >> 6;
-    return NC * XPAD * 16 + NC * xs_floats_per_chunk<TYPE>() * 4;
+// The fields a segment needs first come first (one 64-byte scalar load
+// with w[0]); the other weight bases follow.
+struct Seg {
+    const float* x;
+    const float* add;
+    float* y;
+    int type, K, N, Ng, ngroups, x_stride;
+    uint32_t ng_m;     // magic multiplier for division by Ng (0: Ng == 1)
+    int ng_l;          // its shift
+    uint32_t nc_m;     // the same for division by NC = K / 64
+    int nc_l;
+    const uint8_t* w[MAXG];
+};
+
+// Issues the scalar loads of a segment's leading fields together and waits
+// for them once: used as they are needed, the fields would be fetched in
+// several dependent round trips to the kernel-argument memory.
+__device__ __forceinline__ void prefetch_seg(const Seg& S) {
+    asm volatile("" ::"s"(S.x), "s"(S.add), "s"(S.y), "s"(S.type), "s"(S.K), "s"(S.N),
+                 "s"(S.Ng), "s"(S.ngroups), "s"(S.x_stride), "s"(S.ng_m), "s"(S.ng_l),
+                 "s"(S.nc_m), "s"(S.nc_l), "s"(S.w[0]));
 }
 
-// ------------------------------------------------------------- the GEMV
-// One workgroup = R consecutive rows; see the header comment.  Each lane
-// keeps DEPTH chunks in flight: the first DEPTH loads are issued before x
-// is staged (their latency overlaps the staging), then every computed
-// chunk's registers are refilled with the chunk DEPTH*T further on.
-// T (blockDim.x) is a multiple of 64, so a lane's chunk index modulo 4 --
-// its sub-block position inside the super-block -- never changes.
-template <int TYPE, int DEPTH>
-__global__ __launch_bounds__(1024) void kq_gemv_kernel(GemvArgs a) {
+struct SegsArg {
+    Seg s[MAXSEG];
+    int nseg;
+    int threads;       // blockDim.x and gridDim.x, passed as plain arguments:
+    int grid;          // the built-ins are read through a dependent load chain
+    int xs_off;        // LDS byte offsets of the xs, terms and scratch regions
+    int terms_off;
+    int scr_off;
+};
+
+// n / d for the divisor encoded by (m, l): the invariant-integer division
+// of Granlund and Montgomery (1994), valid for every 32-bit n.
+__device__ __forceinline__ uint32_t div_magic(uint32_t n, uint32_t m, int l) {
+    if (m == 0) return n;
+    const uint32_t t = __umulhi(m, n);
+    return (t + ((n - t) >> 1)) >> (l - 1);
+}
+
+// What the LDS x region currently holds: x (pointer, K, groups, layout),
+// which type's per-group sums are in the xs region (0: none), the scale
+// exponent of the staged values (0 or KSC) and whether some x fell outside
+// the scaled-mode window.
+struct Staged {
+    const float* x;
+    int K, layout, ngx, sums, k;
+    bool bad;
+};
+
+// LDS scratch: per-segment batch counters, per-wave flags, weight-base table
+constexpr int SCR_FLAGS = 4 * MAXSEG;
+constexpr int SCR_WTAB = SCR_FLAGS + 4 * 16;
+constexpr int SCR_BYTES = SCR_WTAB + 8 * MAXG;
+
+template <int TYPE, int DEPTH, bool GROUPED>
+__device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st, uint8_t* smem) {
     using TI = TypeInfo<TYPE>;
     using C = Chunk<TYPE>;
-    extern __shared__ __align__(16) uint8_t smem[];
-    const int tid = threadIdx.x, T = blockDim.x;
-    const int K = a.K, NC = K >> 6;
-    const int r0 = blockIdx.x * a.rows_per_wg;
-    const int R = min(a.rows_per_wg, a.N - r0);
-    if (R <= 0) return;
-
-    float4* xl = reinterpret_cast<float4*>(smem);
-    float* xs = reinterpret_cast<float*>(smem + NC * XPAD * 16);
-    double* terms = reinterpret_cast<double*>(smem + x_lds_bytes<TYPE>(K));
-
+    const int tid = threadIdx.x, T = A.threads, lane = tid & 63, wave = tid >> 6;
+    const int b = blockIdx.x, G = A.grid;
+    const int K = S.K, NC = K >> 6, N = S.N;
+    const int R = N > b ? (N - b + G - 1) / G : 0;
+    if (R == 0) return;                       // uniform over the workgroup
     const int nch = R * NC;
-    const uint8_t* wb = a.w + (size_t)r0 * (size_t)(K >> 8) * TI::BB;
-    const int u = tid & 3;
-
-    // Dynamic distribution: each wave grabs the next batch of 64
-    // consecutive chunks from an LDS counter, keeping DEPTH batches in
-    // flight.  Waves are not served fairly by the issue arbiter (the oldest
-    // wins), so a static split leaves a long tail with few waves, and so
-    // little memory parallelism, at the end; with batches the waves finish
-    // together.  A chunk's term does not depend on which wave computes it,
-    // so the result stays deterministic.  Loads are issued unconditionally
-    // (indices past the end are clamped to the last chunk) so the compiler
-    // can count outstanding loads exactly.
     const int last = nch - 1;
-    const int lane = tid & 63;
-    int* next = reinterpret_cast<int*>(terms + nch);
-    if (tid == 0) *next = 64 * DEPTH * (T >> 6);
-    int base[DEPTH];
+    const int u = tid & 3;
+    const size_t rbytes = (size_t)(K >> 8) * TI::BB;
+    float4* xl = reinterpret_cast<float4*>(smem);
+    float* xs = reinterpret_cast<float*>(smem + A.xs_off);
+    double* terms = reinterpret_cast<double*>(smem + A.terms_off);
+    int* next = reinterpret_cast<int*>(smem + A.scr_off) + seg;
+    int* flags = reinterpret_cast<int*>(smem + A.scr_off + SCR_FLAGS);
+    const uint8_t** wtab = reinterpret_cast<const uint8_t**>(smem + A.scr_off + SCR_WTAB);
+    const int ngx = S.x_stride ? S.ngroups : 1;
+
+    // Chunk f = base + lane of the workgroup's range (clamped to the last
+    // one): its local row rho, column chunk c, staged-x chunk cx and weight
+    // address.  Branch-free, so the loads that follow are unconditional and
+    // the compiler can count the outstanding ones exactly.
+    auto locate = [&](int base, int& cx) -> wptr {
+        const uint32_t f = (uint32_t)min(base + lane, last);
+        const uint32_t rho = div_magic(f, S.nc_m, S.nc_l);
+        const uint32_t c = f - rho * (uint32_t)NC;
+        const uint32_t r = (uint32_t)b + (uint32_t)G * rho;
+        if (GROUPED) {
+            const uint32_t g = div_magic(r, S.ng_m, S.ng_l);
+            cx = (S.x_stride ? (int)g * NC : 0) + (int)c;
+            return to_global(wtab[g]) + (size_t)(r - g * (uint32_t)S.Ng) * rbytes +
+                   (size_t)(c >> 2) * TI::BB;
+        }
+        cx = (int)c;
+        return to_global(S.w[0]) + (size_t)r * rbytes + (size_t)(c >> 2) * TI::BB;
+    };
+
+    // x staging decision: SC types stage x scaled, Q6_K unscaled; a Q6_K
+    // segment can read a scaled x, an SC type restages an unscaled one
+    // unless the window already failed for it.
+    constexpr bool SCTYPE = TYPE != T_Q6K;
+    const bool same_x = st.x == S.x && st.K == K && st.layout == (int)TI::LINEAR && st.ngx == ngx;
+    const bool restage = !same_x || (SCTYPE && st.k == 0 && !st.bad);
+    constexpr int G4 = XGroup<TYPE>::G4;
+    const XStage<TYPE> xg = {S.x, S.x_stride, K / (4 * G4), ngx * (K / (4 * G4)), NC};
+    f32x4 xv[G4];
+    if (restage) xg.load(tid, xv);            // first round of x, ahead of the weights
+
+    if (GROUPED) {
+        // each wave writes the weight-base table itself (identical values),
+        // so its own reads below need no barrier
+        const uint8_t* wv = S.w[0];
+#pragma unroll
+        for (int g = 1; g < MAXG; g++)
+            if (lane == g) wv = S.w[g];
+        if (lane < S.ngroups) wtab[lane] = wv;
+    }
+
+    // first DEPTH batches: static (wave w takes chunks 64w .., then
+    // 64(W + w) ..); their latency overlaps the staging
+    int base[DEPTH], cx[DEPTH];
     typename C::Raw buf[DEPTH];
 #pragma unroll
     for (int k = 0; k < DEPTH; k++) {
-        base[k] = (k * (T >> 6) + (tid >> 6)) * 64;     // first batches: static
-        const int fk = min(base[k] + lane, last);
-        buf[k] = C::load(wb + (size_t)(fk >> 2) * TI::BB, u);
+        base[k] = (k * (T >> 6) + wave) * 64;
+        buf[k] = C::load(locate(base[k], cx[k]), u);
     }
 
-    stage_dma<TYPE>(a.x, K, tid, T, xl);
-    __syncthreads();
-    if (TI::XS_PER_CHUNK) {
-        stage_sums<TYPE>(K, tid, T, xl, xs);
-        __syncthreads();
-    }
-
-    while (base[0] < nch) {
-#pragma unroll
-        for (int k = 0; k < DEPTH; k++) {
-            int nb = 0;
-            if (lane == 0) nb = atomicAdd(next, 64);
-            const int f = base[k] + lane;
-            if (base[k] < nch) {
-                const int c = f % NC;
-                const double t = C::term(buf[k], u, xl + c * XPAD, xs, c);
-                if (f < nch) terms[f] = t;
-            }
-            base[k] = __builtin_amdgcn_readfirstlane(nb);
-            const int fn = min(base[k] + lane, last);
-            buf[k] = C::load(wb + (size_t)(fn >> 2) * TI::BB, u);
+    if (restage) {
+        bool bad = xg.store(tid, xv, SCTYPE, true, xl, xs);
+        for (int gi = tid + T; gi < xg.total; gi += T) {
+            xg.load(gi, xv);
+            bad |= xg.store(gi, xv, SCTYPE, true, xl, xs);
         }
+        if (lane == 0) flags[wave] = __ballot(bad) != 0ull;
+        __syncthreads();
+        int any = 0;
+        for (int i = 0; i < (T >> 6); i++) any |= flags[i];
+        st.x = S.x; st.K = K; st.layout = (int)TI::LINEAR; st.ngx = ngx;
+        st.sums = TI::XS_PER_CHUNK ? TYPE : 0;
+        st.k = SCTYPE ? KSC : 0;
+        st.bad = SCTYPE && any;
+        if (st.bad) {                         // the same in every workgroup
+            for (int gi = tid; gi < xg.total; gi += T) {
+                xg.load(gi, xv);
+                xg.store(gi, xv, false, false, xl, xs);
+            }
+            __syncthreads();
+            st.k = 0;
+        }
+    } else if (TI::XS_PER_CHUNK && st.sums != TYPE) {   // sums are laid out per type
+        resum<TYPE>(K, ngx, tid, T, xl, xs, st.k);
+        __syncthreads();
+        st.sums = TYPE;
     }
+    const float f = st.k ? ldexpf(1.0f, 149 - st.k) : 1.0f;
+    const double f6 = ldexp(0.25, -st.k);
+
+    // Each wave keeps DEPTH batches in flight: a computed batch's registers
+    // are refilled at once with the next batch from the counter.  Batches
+    // are handed out in increasing order, so base[0] < base[1] < ...
+    auto sweep = [&](auto scaled) {
+        constexpr bool SC = decltype(scaled)::value;
+        while (base[0] < nch) {
+#pragma unroll
+            for (int k = 0; k < DEPTH; k++) {
+                int nb = 0;
+                if (lane == 0) nb = atomicAdd(next, 64);
+                if (base[k] < nch) {                 // uniform over the wave
+                    const int fi = base[k] + lane;
+                    const double t = C::template term<SC>(buf[k], u, xl + cx[k] * XPAD, xs, cx[k],
+                                                          f, f6);
+                    if (fi < nch) terms[fi] = t;
+                }
+                base[k] = __builtin_amdgcn_readfirstlane(nb);
+                buf[k] = C::load(locate(base[k], cx[k]), u);
+            }
+        }
+        // the last refill is past the end: wait for it here, so no load is
+        // outstanding into the next segment (the compiler would otherwise
+        // wait for all loads where the next segment reuses the registers,
+        // including that segment's x loads)
+#pragma unroll
+        for (int k = 0; k < DEPTH; k++) C::drain(buf[k]);
+    };
+    if (SCTYPE && st.k > 0)
+        sweep(std::integral_constant<bool, true>());
+    else
+        sweep(std::integral_constant<bool, false>());
     __syncthreads();
 
     // Row reduction: L lanes per row (L = 8..64, as many as T allows), lane
@@ -583,10 +830,63 @@ __global__ __launch_bounds__(1024) void kq_gemv_kernel(GemvArgs a) {
         if (L >= 32) s = s + __shfl_xor(s, 16, 64);
         if (L >= 64) s = s + __shfl_xor(s, 32, 64);
         if (p == 0) {
+            const int r = b + G * rho;
             float v = (float)s;
-            if (a.add) v = a.add[r0 + rho] + v;
-            a.y[r0 + rho] = v;
+            if (S.add) v = S.add[r] + v;
+            S.y[r] = v;
         }
+    }
+    // Wait for the y stores here: a store keeps its data registers busy
+    // until it completes, and the next segment's first writes to those
+    // registers would otherwise wait for every outstanding load -- its x.
+    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
+    __syncthreads();
+}
+
+// TYPES is a bit set of the types the launch contains (bit 0 Q4_K, 1 Q6_K,
+// 2 Q2_K, 3 type 42): the host launches the instantiation with only the
+// types present, so a single-type launch carries one type's code and the
+// register allocation is not constrained by the others.
+constexpr int TB_Q4K = 1, TB_Q6K = 2, TB_Q2K = 4, TB_NIB = 8, TB_ALL = 15;
+
+template <int DEPTH, int TYPES>
+__global__ __launch_bounds__(1024) void kq_segs_kernel(SegsArg A) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    asm volatile("" ::"s"(A.nseg), "s"(A.threads), "s"(A.grid), "s"(A.xs_off),
+                 "s"(A.terms_off), "s"(A.scr_off));
+    prefetch_seg(A.s[0]);
+    // batch counters of every segment (the first segment that runs stages
+    // x, and its barrier orders these writes before any batch is taken)
+    if (threadIdx.x < (unsigned)A.nseg)
+        reinterpret_cast<int*>(smem + A.scr_off)[threadIdx.x] = 64 * DEPTH * (A.threads >> 6);
+    Staged st = {nullptr, 0, -1, 0, 0, 0, false};
+    // a single-type instantiation does not read the segment types (the host
+    // launches it only for segment lists of that type)
+    constexpr bool SINGLE = TYPES == TB_Q4K || TYPES == TB_Q6K || TYPES == TB_Q2K || TYPES == TB_NIB;
+    for (int i = 0; i < A.nseg; i++) {
+        const Seg& S = A.s[i];
+        if (i) prefetch_seg(S);
+        const bool grp = S.ngroups > 1;
+        if (SINGLE) {
+            constexpr int TY = TYPES == TB_Q4K ? T_Q4K : TYPES == TB_Q6K ? T_Q6K
+                             : TYPES == TB_Q2K ? T_Q2K : T_NIB;
+            if (grp) run_segment<TY, DEPTH, true>(S, A, i, st, smem);
+            else run_segment<TY, DEPTH, false>(S, A, i, st, smem);
+            continue;
+        }
+#define KQ_RUN(T_, TB_)                                                        \
+        if (TYPES & TB_) {                                                     \
+            if (grp) run_segment<T_, DEPTH, true>(S, A, i, st, smem);          \
+            else run_segment<T_, DEPTH, false>(S, A, i, st, smem);             \
+        }
+        switch (S.type) {
+        case T_Q4K: KQ_RUN(T_Q4K, TB_Q4K) break;
+        case T_Q6K: KQ_RUN(T_Q6K, TB_Q6K) break;
+        case T_Q2K: KQ_RUN(T_Q2K, TB_Q2K) break;
+        case T_NIB: KQ_RUN(T_NIB, TB_NIB) break;
+        default: break;
+        }
+#undef KQ_RUN
     }
 }
 
@@ -598,14 +898,14 @@ __global__ __launch_bounds__(256) void kq_dequant_kernel(const uint8_t* __restri
     using TI = TypeInfo<TYPE>;
     const long f = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (f >= nchunks) return;
-    const uint8_t* blk = w + (size_t)(f >> 2) * TI::BB;
+    const wptr blk = to_global(w) + (size_t)(f >> 2) * TI::BB;
     const int u = (int)(f & 3);
     float* yb = y + (size_t)(f >> 2) * 256;
     if (TYPE == T_Q4K) {
         const RawQ4 r = load_q4k(blk, u);
         const float d = f16_bits_to_f32(r.hd.x & 0xffffu);
         const float dmin = f16_bits_to_f32(r.hd.x >> 16);
-        const uint8_t* s = blk + 4;
+        const wptr s = blk + 4;
 #pragma unroll
         for (int half = 0; half < 2; half++) {
             const int sb = 2 * u + half;
@@ -663,36 +963,6 @@ __global__ __launch_bounds__(256) void kq_dequant_kernel(const uint8_t* __restri
 }
 
 template <int TYPE>
-int launch_gemv(const GemvArgs& a, int grid, int threads, int depth, hipStream_t st) {
-    const int NC = a.K >> 6;
-    const size_t lds = (size_t)x_lds_bytes<TYPE>(a.K) + (size_t)a.rows_per_wg * NC * 8 + 16;
-    switch (depth) {
-    case 1: hipLaunchKernelGGL((kq_gemv_kernel<TYPE, 1>), dim3(grid), dim3(threads), lds, st, a); break;
-    case 2: hipLaunchKernelGGL((kq_gemv_kernel<TYPE, 2>), dim3(grid), dim3(threads), lds, st, a); break;
-    case 3: hipLaunchKernelGGL((kq_gemv_kernel<TYPE, 3>), dim3(grid), dim3(threads), lds, st, a); break;
-    case 4: hipLaunchKernelGGL((kq_gemv_kernel<TYPE, 4>), dim3(grid), dim3(threads), lds, st, a); break;
-    default: hipLaunchKernelGGL((kq_gemv_kernel<TYPE, 6>), dim3(grid), dim3(threads), lds, st, a); break;
-    }
-    return (int)hipGetLastError();
-}
-
-template <int TYPE, int D>
-int set_lds1(int bytes) {
-    return (int)hipFuncSetAttribute(reinterpret_cast<const void*>(&kq_gemv_kernel<TYPE, D>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-}
-
-template <int TYPE>
-int set_lds(int bytes) {
-    int e = set_lds1<TYPE, 1>(bytes);
-    if (!e) e = set_lds1<TYPE, 2>(bytes);
-    if (!e) e = set_lds1<TYPE, 3>(bytes);
-    if (!e) e = set_lds1<TYPE, 4>(bytes);
-    if (!e) e = set_lds1<TYPE, 6>(bytes);
-    return e;
-}
-
-template <int TYPE>
 int launch_dequant(const uint8_t* w, float* y, long nblocks, hipStream_t st) {
     const long nch = nblocks * 4;
     const long grid = (nch + 255) / 256;
@@ -705,46 +975,106 @@ int launch_dequant(const uint8_t* w, float* y, long nblocks, hipStream_t st) {
 // ------------------------------------------------------------ C launchers
 extern "C" {
 
-// LDS bytes the GEMV kernel needs for a given type, K and rows per group.
-long kqk_gemv_lds_bytes(int type, int K, int rows_per_wg) {
-    const long NC = K >> 6;
-    long x;
+// Host view of one segment (plain C layout, see kq_linear.c).
+struct kqk_seg {
+    const void* w[MAXG];
+    const float* x;
+    const float* add;
+    float* y;
+    int type, K, N, Ng, ngroups, x_stride;
+};
+
+static int xs_per_chunk(int type) {
     switch (type) {
-    case T_Q4K: x = x_lds_bytes<T_Q4K>(K); break;
-    case T_Q6K: x = x_lds_bytes<T_Q6K>(K); break;
-    case T_Q2K: x = x_lds_bytes<T_Q2K>(K); break;
-    case T_NIB: x = x_lds_bytes<T_NIB>(K); break;
+    case T_Q4K: return TypeInfo<T_Q4K>::XS_PER_CHUNK;
+    case T_Q6K: return TypeInfo<T_Q6K>::XS_PER_CHUNK;
+    case T_Q2K: return TypeInfo<T_Q2K>::XS_PER_CHUNK;
+    case T_NIB: return TypeInfo<T_NIB>::XS_PER_CHUNK;
     default: return -1;
     }
-    return x + (long)rows_per_wg * NC * 8 + 16;
 }
 
-// Allows dynamic LDS up to `bytes` for every GEMV instantiation.
+static void magic_for(uint32_t d, uint32_t& m, int& l) {
+    if (d <= 1) { m = 0; l = 0; return; }
+    l = 0;
+    while ((1ull << l) < d) l++;
+    m = (uint32_t)(((1ull << 32) * ((1ull << l) - d)) / d + 1);
+}
+
+// LDS plan of a segment list for `grid` workgroups: x region, xs region and
+// term region sized for the largest segment.  Returns total bytes or -1.
+long kqk_segs_lds(const kqk_seg* segs, int nseg, int grid, int* xs_off, int* terms_off,
+                  int* scr_off) {
+    long xl = 0, xsb = 0, tb = 0;
+    for (int i = 0; i < nseg; i++) {
+        const kqk_seg& g = segs[i];
+        const int xpc = xs_per_chunk(g.type);
+        if (xpc < 0 || g.K <= 0 || (g.K & 255) || g.ngroups < 1 || g.ngroups > MAXG ||
+            g.N != g.Ng * g.ngroups)
+            return -1;
+        const long NC = g.K >> 6;
+        const long ngx = g.x_stride ? g.ngroups : 1;
+        xl = xl > ngx * NC * XPAD * 16 ? xl : ngx * NC * XPAD * 16;
+        xsb = xsb > ngx * NC * xpc * 4 ? xsb : ngx * NC * xpc * 4;
+        const long R = (g.N + grid - 1) / grid;
+        tb = tb > R * NC * 8 ? tb : R * NC * 8;
+    }
+    xsb = (xsb + 15) & ~15L;
+    *xs_off = (int)xl;
+    *terms_off = (int)(xl + xsb);
+    *scr_off = (int)(xl + xsb + tb);
+    return xl + xsb + tb + SCR_BYTES;
+}
+
+// Every instantiation, indexed by [depth - 1][type set].
+#define KQ_SEGS_ROW(D)                                                                  \
+    {&kq_segs_kernel<D, TB_Q4K>, &kq_segs_kernel<D, TB_Q6K>, &kq_segs_kernel<D, TB_Q2K>, \
+     &kq_segs_kernel<D, TB_NIB>, &kq_segs_kernel<D, TB_ALL>}
+typedef void (*segs_fn)(SegsArg);
+static const segs_fn k_segs[2][5] = {KQ_SEGS_ROW(1), KQ_SEGS_ROW(2)};
+#undef KQ_SEGS_ROW
+
 int kqk_set_max_lds(int bytes) {
-    int e = set_lds<T_Q4K>(bytes);
-    if (!e) e = set_lds<T_Q6K>(bytes);
-    if (!e) e = set_lds<T_Q2K>(bytes);
-    if (!e) e = set_lds<T_NIB>(bytes);
-    return e;
+    for (int d = 0; d < 2; d++)
+        for (int t = 0; t < 5; t++) {
+            const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_segs[d][t]),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+            if (e != hipSuccess) return (int)e;
+        }
+    return 0;
 }
 
-// threads must be 256, 512 or 1024; rows_per_wg * (K/64) * 8 plus the x
-// staging must fit the LDS limit set above (checked by the caller); depth
-// (1..3) is the number of chunks each lane keeps in flight.
-int kqk_launch_gemv(int type, const void* w, const float* x, const float* add, float* y,
-                    int N, int K, int rows_per_wg, int threads, int depth, hipStream_t st) {
-    GemvArgs a;
-    a.w = static_cast<const uint8_t*>(w);
-    a.x = x; a.add = add; a.y = y;
-    a.N = N; a.K = K; a.rows_per_wg = rows_per_wg; a.B = 1;
-    const int grid = (N + rows_per_wg - 1) / rows_per_wg;
-    switch (type) {
-    case T_Q4K: return launch_gemv<T_Q4K>(a, grid, threads, depth, st);
-    case T_Q6K: return launch_gemv<T_Q6K>(a, grid, threads, depth, st);
-    case T_Q2K: return launch_gemv<T_Q2K>(a, grid, threads, depth, st);
-    case T_NIB: return launch_gemv<T_NIB>(a, grid, threads, depth, st);
-    default: return -1;
+// One launch over nseg (<= 8) segments; grid workgroups of `threads`
+// (a multiple of 64, at most 1024), `depth` (1 or 2) batches in flight per
+// wave (a third would not fit the 128 VGPRs a 1024-lane workgroup allows).
+int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int depth,
+                    long lds_bytes, int xs_off, int terms_off, int scr_off, hipStream_t st) {
+    if (nseg < 1 || nseg > MAXSEG || threads < 64 || threads > 1024 || (threads & 63) ||
+        depth < 1 || depth > 2)
+        return (int)hipErrorInvalidValue;
+    SegsArg A;
+    A.nseg = nseg;
+    A.xs_off = xs_off;
+    A.terms_off = terms_off;
+    A.scr_off = scr_off;
+    A.threads = threads;
+    A.grid = grid;
+    int set = 0;
+    for (int i = 0; i < nseg; i++) {
+        Seg& d = A.s[i];
+        const kqk_seg& h = segs[i];
+        for (int g = 0; g < MAXG; g++)
+            d.w[g] = static_cast<const uint8_t*>(g < h.ngroups ? h.w[g] : h.w[0]);
+        d.x = h.x; d.add = h.add; d.y = h.y;
+        d.type = h.type; d.K = h.K; d.N = h.N; d.Ng = h.Ng; d.ngroups = h.ngroups;
+        d.x_stride = h.x_stride;
+        magic_for((uint32_t)h.Ng, d.ng_m, d.ng_l);
+        magic_for((uint32_t)(h.K >> 6), d.nc_m, d.nc_l);
+        set |= h.type == T_Q4K ? TB_Q4K : h.type == T_Q6K ? TB_Q6K : h.type == T_Q2K ? TB_Q2K : TB_NIB;
     }
+    const int t = set == TB_Q4K ? 0 : set == TB_Q6K ? 1 : set == TB_Q2K ? 2 : set == TB_NIB ? 3 : 4;
+    hipLaunchKernelGGL(k_segs[depth - 1][t], dim3(grid), dim3(threads), (size_t)lds_bytes, st, A);
+    return (int)hipGetLastError();
 }
 
 int kqk_launch_dequant(int type, const void* w, float* y, long nblocks, hipStream_t st) {

@@ -22,9 +22,17 @@
 #include <string.h>
 
 /* launchers (kq_kernels.hip) */
-long kqk_gemv_lds_bytes(int type, int K, int rows_per_wg);
-int kqk_launch_gemv(int type, const void* w, const float* x, const float* add, float* y,
-                    int N, int K, int rows_per_wg, int threads, int depth, hipStream_t st);
+typedef struct {
+    const void* w[KQ_MAX_GROUPS];
+    const float* x;
+    const float* add;
+    float* y;
+    int type, K, N, Ng, ngroups, x_stride;
+} kqk_seg;
+long kqk_segs_lds(const kqk_seg* segs, int nseg, int grid, int* xs_off, int* terms_off,
+                  int* scr_off);
+int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int depth,
+                    long lds_bytes, int xs_off, int terms_off, int scr_off, hipStream_t st);
 int kqk_launch_dequant(int type, const void* w, float* y, long nblocks, hipStream_t st);
 int kqk_set_max_lds(int bytes);
 
@@ -192,40 +200,68 @@ static const void* tensor_dev(const kq_tensor* w, int N, int K) {
 }
 
 /* ----------------------------------------------------------- planning */
-/* One workgroup per CU, each owning ceil(N / n_cu) consecutive rows, as
- * long as x plus the per-chunk terms fit in LDS; workgroup size grows with
- * the chunks it owns.  KQ_ROWS_PER_WG / KQ_WG_THREADS / KQ_DEPTH override
- * (tuning). */
-static int plan(int type, int N, int K, int* rows, int* threads, int* depth) {
-    const int NC = K / 64;
-    const long xb = kqk_gemv_lds_bytes(type, K, 0);
-    if (xb < 0) return kq_fail("type %d has no GEMV kernel", type);
-    const long cap = (long)g_kq.lds_max - 256;
-    long rmax = (cap - xb) / ((long)NC * 8);
-    if (rmax < 1) return kq_fail("K=%d needs %ld bytes of LDS for x (max %ld)", K, xb, cap);
-    long R = (N + g_kq.n_cu - 1) / g_kq.n_cu;
-    const char* er = getenv("KQ_ROWS_PER_WG");
-    if (er && atoi(er) > 0) R = atoi(er);
-    if (R > rmax) R = rmax;
-    if (R < 1) R = 1;
-    long chunks = R * NC;
-    int T = chunks >= 4096 ? 1024 : chunks >= 1024 ? 512 : 256;
+/* One persistent workgroup per CU (KQ_GRID overrides).  The workgroup
+ * size follows the largest per-workgroup share of 64-weight chunks over the
+ * segments: enough waves to keep each CU's memory pipe busy without many
+ * idle lanes on small tensors (KQ_WG_THREADS overrides: 256, 512 or
+ * 1024).  Each wave keeps one batch of loads in flight (KQ_DEPTH=2: two;
+ * a second batch costs more registers than the overlap it buys). */
+static int plan_grid(void) {
+    const char* e = getenv("KQ_GRID");
+    int g = e && atoi(e) > 0 ? atoi(e) : g_kq.n_cu;
+    return g;
+}
 
-    const char* et = getenv("KQ_WG_THREADS");
-    if (et) {
-        int t = atoi(et);
-        if (t == 256 || t == 512 || t == 1024) T = t;
+static int plan_threads(const kqk_seg* segs, int nseg, int grid) {
+    const char* e = getenv("KQ_WG_THREADS");
+    if (e) {
+        const int t = atoi(e);
+        if (t == 256 || t == 512 || t == 1024) return t;
     }
-    int D = 2;
-    const char* ed = getenv("KQ_DEPTH");
-    if (ed && atoi(ed) >= 1 && atoi(ed) <= 6) D = atoi(ed);
-    *rows = (int)R;
-    *threads = T;
-    *depth = D;
+    long chunks = 0;
+    for (int i = 0; i < nseg; i++) {
+        const long c = (long)((segs[i].N + grid - 1) / grid) * (segs[i].K / 64);
+        if (c > chunks) chunks = c;
+    }
+    return chunks >= 4096 ? 1024 : chunks >= 1024 ? 512 : 256;
+}
+
+static int plan_depth(void) {
+    const char* e = getenv("KQ_DEPTH");
+    const int d = e ? atoi(e) : 1;
+    return d == 2 ? 2 : 1;
+}
+
+static int launch_segs(const kqk_seg* segs, int nseg, hipStream_t st) {
+    const int grid = plan_grid(), threads = plan_threads(segs, nseg, grid);
+    int xs_off = 0, terms_off = 0, scr_off = 0;
+    long lds = kqk_segs_lds(segs, nseg, grid, &xs_off, &terms_off, &scr_off);
+    if (lds < 0) return kq_fail("invalid segment list");
+    if (lds > g_kq.lds_max)
+        return kq_fail("segments need %ld bytes of LDS (max %d): split the rows", lds,
+                       g_kq.lds_max);
+    int e = kqk_launch_segs(segs, nseg, grid, threads, plan_depth(), lds, xs_off, terms_off,
+                            scr_off, st);
+    if (e) return kq_fail("gemv launch: %s", hipGetErrorString((hipError_t)e));
     return 0;
 }
 
-/* NULL is the null (default) stream, as in the HIP runtime itself. */
+/* Largest row count one launch can give a single segment (LDS limit):
+ * the x and xs regions are fixed, the term region grows with the rows per
+ * workgroup. */
+static int max_rows_per_launch(const kqk_seg* proto) {
+    const int grid = plan_grid();
+    kqk_seg t = *proto;
+    t.N = t.Ng = 1;
+    int a, b2, c;
+    const long fixed = kqk_segs_lds(&t, 1, grid, &a, &b2, &c) - (long)(t.K / 64) * 8;
+    const long per_row = (long)(t.K / 64) * 8;
+    long rows = (g_kq.lds_max - fixed) / per_row;      /* rows per workgroup */
+    if (rows < 1) rows = 1;
+    long n = rows * grid;
+    return n > 0x40000000L ? 0x40000000 : (int)n;
+}
+
 static hipStream_t pick(kq_stream s) { return (hipStream_t)s; }
 
 static int check_shape(int type, int N, int K) {
@@ -241,11 +277,47 @@ int kq_gemv_dev(int type, const void* w, const float* x, const float* add, float
     if (check_shape(type, N, K) || kq_ready()) return -1;
     if (!w || !x || !y) return kq_fail("kq_gemv_dev: NULL pointer");
     if ((uintptr_t)x & 15) return kq_fail("kq_gemv_dev: x must be 16-byte aligned");
-    int R = 1, T = 256, D = 2;
-    if (plan(type, N, K, &R, &T, &D)) return -1;
-    int e = kqk_launch_gemv(type, w, x, add, y, N, K, R, T, D, pick(stream));
-    if (e) return kq_fail("gemv launch: %s", hipGetErrorString((hipError_t)e));
+    kqk_seg sg;
+    memset(&sg, 0, sizeof sg);
+    sg.type = type; sg.K = K; sg.ngroups = 1; sg.x = x;
+    sg.N = sg.Ng = N;
+    const int maxr = max_rows_per_launch(&sg);
+    const int64_t rb = kq_row_bytes(type, K);
+    for (int r0 = 0; r0 < N; r0 += maxr) {       /* one launch unless LDS runs out */
+        const int n = N - r0 < maxr ? N - r0 : maxr;
+        sg.w[0] = (const uint8_t*)w + (size_t)r0 * (size_t)rb;
+        sg.add = add ? add + r0 : NULL;
+        sg.y = y + r0;
+        sg.N = sg.Ng = n;
+        if (launch_segs(&sg, 1, pick(stream))) return -1;
+    }
     return 0;
+}
+
+int kq_gemv_segments_dev(const kq_segment* segs, int nseg, kq_stream stream) {
+    if (nseg < 1 || nseg > KQ_MAX_SEGMENTS) return kq_fail("kq_gemv_segments_dev: nseg=%d", nseg);
+    if (!segs || kq_ready()) return segs ? -1 : kq_fail("kq_gemv_segments_dev: NULL");
+    kqk_seg h[KQ_MAX_SEGMENTS];
+    memset(h, 0, sizeof h);
+    for (int i = 0; i < nseg; i++) {
+        const kq_segment* s = &segs[i];
+        if (s->ngroups < 1 || s->ngroups > KQ_MAX_GROUPS)
+            return kq_fail("segment %d: ngroups=%d", i, s->ngroups);
+        if (check_shape(s->type, s->rows_per_group, s->K)) return -1;
+        if (!s->x || !s->y) return kq_fail("segment %d: NULL x or y", i);
+        if (((uintptr_t)s->x & 15) || (s->x_stride & 3))
+            return kq_fail("segment %d: x must be 16-byte aligned", i);
+        if ((int64_t)s->rows_per_group * s->ngroups > 0x7fffffff)
+            return kq_fail("segment %d: too many rows", i);
+        for (int g = 0; g < s->ngroups; g++) {
+            if (!s->w[g]) return kq_fail("segment %d: NULL weights for group %d", i, g);
+            h[i].w[g] = s->w[g];
+        }
+        h[i].type = s->type; h[i].K = s->K; h[i].Ng = s->rows_per_group;
+        h[i].ngroups = s->ngroups; h[i].N = s->rows_per_group * s->ngroups;
+        h[i].x = s->x; h[i].x_stride = s->x_stride; h[i].add = s->add; h[i].y = s->y;
+    }
+    return launch_segs(h, nseg, pick(stream));
 }
 
 int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,
@@ -328,7 +400,34 @@ int kq_q4k_group(const float* x, int K,
     float* ys[3] = {y0, y1, y2};
     const int Ns[3] = {N0, N1, N2};
     const int nw = w2 ? 3 : 2;
-    for (int i = 0; i < nw; i++)
-        if (kq_linear_dispatch(ws[i], x, ys[i], Ns[i], K)) return -1;
-    return 0;
+    if (kq_ready()) return -1;
+    size_t ytot = 0;
+    kq_segment sg[3];
+    memset(sg, 0, sizeof sg);
+    for (int i = 0; i < nw; i++) {
+        if (!ws[i]) return kq_fail("kq_q4k_group: NULL tensor");
+        if (check_shape((int)ws[i]->type, Ns[i], K)) return -1;
+        const void* dw = tensor_dev(ws[i], Ns[i], K);
+        if (!dw) return -1;
+        sg[i].type = (int)ws[i]->type; sg[i].K = K; sg[i].rows_per_group = Ns[i];
+        sg[i].ngroups = 1; sg[i].w[0] = dw;
+        ytot += (size_t)Ns[i];
+    }
+    if (grow(&g_kq.d_x, &g_kq.cap_x, (size_t)K) || grow(&g_kq.d_y, &g_kq.cap_y, ytot)) return -1;
+    if (h2d(g_kq.d_x, x, (size_t)K)) return -1;
+    size_t off = 0;
+    for (int i = 0; i < nw; i++) {
+        sg[i].x = g_kq.d_x;
+        sg[i].y = g_kq.d_y + off;
+        off += (size_t)Ns[i];
+    }
+    if (kq_gemv_segments_dev(sg, nw, g_kq.stream)) return -1;
+    off = 0;
+    for (int i = 0; i < nw; i++) {
+        if (hip_ok(hipMemcpyAsync(ys[i], g_kq.d_y + off, (size_t)Ns[i] * sizeof(float),
+                                  hipMemcpyDeviceToHost, g_kq.stream), "copy y out"))
+            return -1;
+        off += (size_t)Ns[i];
+    }
+    return hip_ok(hipStreamSynchronize(g_kq.stream), "synchronize");
 }

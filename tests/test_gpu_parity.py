@@ -159,7 +159,7 @@ def test_gemv_27b_shape_sampled(port, qtype, N, Kd, monkeypatch):
                                      [0, 1, N - 2, N - 1]]))
     check_close(y[rows], port.gemv_rows(qtype, w, x, rows, Kd), f"27b {qtype} {N}x{Kd}")
     assert same_values(gpu_gemv(qtype, w, x, N, Kd), y)
-    monkeypatch.setenv("KQ_ROWS_PER_WG", "7")
+    monkeypatch.setenv("KQ_GRID", "37")
     monkeypatch.setenv("KQ_WG_THREADS", "256")
     assert same_values(gpu_gemv(qtype, w, x, N, Kd), y)
 
@@ -197,3 +197,65 @@ def test_host_abi_dispatch_multix_group(port):
     bad = K.make_tensor(12, 512, Kd, blob.size - 100)
     y = np.empty(512, np.float32)
     assert K.lib().kq_linear_dispatch(ctypes.byref(bad), K._fptr(x), K._fptr(y), 512, Kd) == -1
+
+
+# ------------------------------------------------------- batched segments
+def test_segments_layer_set_matches_single_launches(port):
+    """A layer's matvecs in ONE launch (kq_gemv_segments_dev): each output is
+    bit-identical to its own kq_gemv_dev launch, and matches the oracle."""
+    H, F, Q, KV = 1024, 3072, 2048, 512
+    specs = [("q", 12, Q, H, "h"), ("k", 12, KV, H, "h"), ("v", 14, KV, H, "h"),
+             ("gate", 12, F, H, "h"), ("up", 10, F, H, "h"),
+             ("o", 12, H, Q, "a"), ("down", 14, H, F, "f"), ("extra", 42, 256, F, "f")]
+    xs = {"h": synth.gaussian(synth.rng(1), H), "a": synth.gaussian(synth.rng(2), Q),
+          "f": synth.gaussian(synth.rng(3), F)}
+    dx = {k: dev(v) for k, v in xs.items()}
+    ws, dws, dys, segs = {}, {}, {}, []
+    for i, (name, t, N, Kd, xn) in enumerate(specs):
+        ws[name] = synth.tensor(t, N, Kd, 70 + i)
+        dws[name] = dev(ws[name])
+        dys[name] = torch.empty(N, dtype=torch.float32, device="cuda")
+        segs.append(K.segment(t, Kd, N, [dws[name].data_ptr()], dx[xn].data_ptr(),
+                              dys[name].data_ptr()))
+    K.gemv_segments_dev(segs, stream=stream())
+    torch.cuda.synchronize()
+    for name, t, N, Kd, xn in specs:
+        got = dys[name].cpu().numpy()
+        single = gpu_gemv(t, ws[name], xs[xn], N, Kd)
+        assert same_values(got, single), name
+        check_close(got, port.gemv(t, ws[name], xs[xn], N, Kd, threads=8), f"seg {name}")
+
+
+def test_segments_groups_expert_slices(port):
+    """MoE-style segments: groups with separate weight bases; gate/up share
+    x, down uses one x per group (x_stride)."""
+    H, F, E = 512, 768, 5
+    r = np.random.default_rng(9)
+    x = synth.gaussian(synth.rng(4), H)
+    gate = [synth.tensor(12, F, H, 100 + e) for e in range(E)]
+    down = [synth.tensor(12, H, F, 200 + e) for e in range(E)]
+    a = np.stack([synth.gaussian(synth.rng(300 + e), F) for e in range(E)])
+    dgate = [dev(g) for g in gate]
+    ddown = [dev(d) for d in down]
+    dx, da = dev(x), dev(a.reshape(-1))
+    yg = torch.empty(E * F, dtype=torch.float32, device="cuda")
+    yd = torch.empty(E * H, dtype=torch.float32, device="cuda")
+    add = synth.gaussian(synth.rng(5), E * H)
+    dadd = dev(add)
+    segs = [K.segment(12, H, F, [t.data_ptr() for t in dgate], dx.data_ptr(), yg.data_ptr()),
+            K.segment(12, F, H, [t.data_ptr() for t in ddown], da.data_ptr(), yd.data_ptr(),
+                      x_stride=F, add_ptr=dadd.data_ptr())]
+    K.gemv_segments_dev(segs, stream=stream())
+    torch.cuda.synchronize()
+    g_out = yg.cpu().numpy().reshape(E, F)
+    d_out = yd.cpu().numpy().reshape(E, H)
+    for e in range(E):
+        check_close(g_out[e], port.gemv(12, gate[e], x, F, H), f"gate e{e}")
+        check_close(d_out[e], port.gemv(12, down[e], a[e], H, F, add=add[e * H:(e + 1) * H]),
+                    f"down e{e}")
+
+
+def test_segments_rejects_bad_input():
+    bad = K.segment(12, 1000, 16, [0], 0, 0)
+    with pytest.raises(RuntimeError):
+        K.gemv_segments_dev([bad])
