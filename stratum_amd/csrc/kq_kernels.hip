@@ -750,7 +750,8 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
             xg.load(gi, xv);
             bad |= xg.store(gi, xv, SCTYPE, true, xl, xs);
         }
-        if (lane == 0) flags[wave] = __ballot(bad) != 0ull;
+        const bool wave_bad = __ballot(bad) != 0ull;   // with every lane active
+        if (lane == 0) flags[wave] = wave_bad;
         __syncthreads();
         int any = 0;
         for (int i = 0; i < (T >> 6); i++) any |= flags[i];

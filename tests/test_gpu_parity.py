@@ -259,3 +259,65 @@ def test_segments_rejects_bad_input():
     bad = K.segment(12, 1000, 16, [0], 0, 0)
     with pytest.raises(RuntimeError):
         K.gemv_segments_dev([bad])
+
+
+# ----------------------------------------------------- scaled-x window
+# Q4_K, Q2_K and type 42 run on x scaled by 2^64 when every finite nonzero
+# |x| lies in [2^-41, 2^52); otherwise the workgroups restage x unscaled and
+# take the convert path.  Both must give the reference's values.
+WINDOW_CASES = {
+    "low-edge-in": [2.0 ** -41, -(2.0 ** -41)],
+    "low-edge-out": [2.0 ** -42],
+    "high-edge-in": [np.float32(2.0 ** 52) - np.float32(2.0 ** 28), -(2.0 ** 51)],
+    "high-edge-out": [2.0 ** 52],
+    "subnormal": [1e-40],
+    "zeros-inf-nan": [0.0, -0.0, np.inf, np.nan],
+}
+
+
+@pytest.mark.parametrize("case", sorted(WINDOW_CASES))
+@pytest.mark.parametrize("qtype", [12, 10, 42, 14])
+def test_gemv_x_window_edges(port, qtype, case):
+    N, Kd = 96, 1024
+    w = synth.tensor(qtype, N, Kd, 500 + qtype)
+    x = synth.gaussian(synth.rng(501), Kd)
+    special = np.asarray(WINDOW_CASES[case], np.float32)
+    x[7:7 + special.size] = special
+    x[900:900 + special.size] = special[::-1]
+    check_close(gpu_gemv(qtype, w, x, N, Kd), port.gemv(qtype, w, x, N, Kd),
+                f"{K.TYPE_NAMES[qtype]} window {case}")
+
+
+@pytest.mark.parametrize("qtype", [12, 10, 42])
+def test_gemv_x_all_below_window(port, qtype):
+    """Every x near 2^-45: scaled products would fall below the binary32
+    normal range and lose bits, so only the unscaled fallback matches."""
+    N, Kd = 64, 1024
+    w = synth.tensor(qtype, N, Kd, 520 + qtype)
+    x = (synth.gaussian(synth.rng(521), Kd) * np.float32(2.0 ** -45)).astype(np.float32)
+    check_close(gpu_gemv(qtype, w, x, N, Kd), port.gemv(qtype, w, x, N, Kd),
+                f"{K.TYPE_NAMES[qtype]} x ~ 2^-45")
+
+
+@pytest.mark.parametrize("wide", [False, True])
+def test_segments_shared_x_across_types(port, wide):
+    """Segments that share one x in different ways: sums recomputed from a
+    scaled x (Q4_K -> type 42), Q6_K reading a scaled x, and -- with one x
+    value outside the window -- every type on the unscaled fallback."""
+    H = 1024
+    x = synth.gaussian(synth.rng(600), H)
+    if wide:
+        x[33] = 2.0 ** 60
+    specs = [(12, 256), (42, 192), (10, 128), (14, 320), (10, 64), (12, 96)]
+    dx = dev(x)
+    ws, dws, dys, segs = [], [], [], []
+    for i, (t, N) in enumerate(specs):
+        ws.append(synth.tensor(t, N, H, 610 + i))
+        dws.append(dev(ws[-1]))
+        dys.append(torch.empty(N, dtype=torch.float32, device="cuda"))
+        segs.append(K.segment(t, H, N, [dws[-1].data_ptr()], dx.data_ptr(), dys[-1].data_ptr()))
+    K.gemv_segments_dev(segs, stream=stream())
+    torch.cuda.synchronize()
+    for i, (t, N) in enumerate(specs):
+        check_close(dys[i].cpu().numpy(), port.gemv(t, ws[i], x, N, H),
+                    f"shared x seg {i} {K.TYPE_NAMES[t]} wide={wide}")
