@@ -45,7 +45,6 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include <type_traits>
 
 #pragma clang fp contract(off)
 
@@ -403,21 +402,37 @@ __device__ __forceinline__ double term_q4k(const RawQ4& r, int j, const float4* 
     // high nibbles are used in place (16 q), so a2 is 16x the reference's
     // partial sum and d2 is used divided by 16 (both exact)
     float a1 = 0.0f, a2 = 0.0f;
+    if (SC) {
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-        const uint32_t v = k < 4 ? dw_of(r.qa, k) : dw_of(r.qb, k - 4);
-        const uint32_t vl = v & 0x0f0f0f0fu, vh = v & 0xf0f0f0f0u;
-        float l0, l1, l2, l3, h0, h1, h2, h3;
-        bmul4<SC>(vl, xc + k, l0, l1, l2, l3);
-        bmul4<SC>(vh, xc + 8 + k, h0, h1, h2, h3);
-        a1 = a1 + l0; a2 = a2 + h0;
-        a1 = a1 + l1; a2 = a2 + h1;
-        a1 = a1 + l2; a2 = a2 + h2;
-        a1 = a1 + l3; a2 = a2 + h3;
-        // keep the x reads of later steps from being hoisted all at once
-        // (64 registers): schedule as "2 LDS reads, then 18 VALU" per step
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 18, 0);
+        for (int k = 0; k < 8; k++) {
+            const uint32_t v = k < 4 ? dw_of(r.qa, k) : dw_of(r.qb, k - 4);
+            const uint32_t vl = v & 0x0f0f0f0fu, vh = v & 0xf0f0f0f0u;
+            float l0, l1, l2, l3, h0, h1, h2, h3;
+            bmul4<true>(vl, xc + k, l0, l1, l2, l3);
+            bmul4<true>(vh, xc + 8 + k, h0, h1, h2, h3);
+            a1 = a1 + l0; a2 = a2 + h0;
+            a1 = a1 + l1; a2 = a2 + h1;
+            a1 = a1 + l2; a2 = a2 + h2;
+            a1 = a1 + l3; a2 = a2 + h3;
+        }
+    } else {
+        // exact convert path for x outside the window (rare): a rolled loop,
+        // the packed words rotating through q0, so that its registers do not
+        // raise the register count of the whole kernel
+        uint32_t q0 = r.qa.x, q1 = r.qa.y, q2 = r.qa.z, q3 = r.qa.w;
+        uint32_t q4 = r.qb.x, q5 = r.qb.y, q6 = r.qb.z, q7 = r.qb.w;
+#pragma unroll 1
+        for (int k = 0; k < 8; k++) {
+            const uint32_t v = q0;
+            q0 = q1; q1 = q2; q2 = q3; q3 = q4; q4 = q5; q5 = q6; q6 = q7; q7 = v;
+            float l0, l1, l2, l3, h0, h1, h2, h3;
+            bmul4<false>(v & 0x0f0f0f0fu, xc + k, l0, l1, l2, l3);
+            bmul4<false>(v & 0xf0f0f0f0u, xc + 8 + k, h0, h1, h2, h3);
+            a1 = a1 + l0; a2 = a2 + h0;
+            a1 = a1 + l1; a2 = a2 + h1;
+            a1 = a1 + l2; a2 = a2 + h2;
+            a1 = a1 + l3; a2 = a2 + h3;
+        }
     }
     const float d1s = SC ? d1 * f : d1;
     const float d2s = d2 * (SC ? f * 0.0625f : 0.0625f);
@@ -479,29 +494,58 @@ __device__ __forceinline__ double term_q2k(const RawQ2& r, int u, const float4* 
     const float dmin = f16_bits_to_f32(r.dd >> 16);
     const uint32_t S0 = h ? (r.s.x >> 8) : r.s.x;   // bytes h, h+2
     const uint32_t S1 = h ? (r.s.y >> 8) : r.s.y;   // bytes h+4, h+6
-    const uint32_t sc[4] = {S0 & 0xffu, (S0 >> 16) & 0xffu, S1 & 0xffu, (S1 >> 16) & 0xffu};
-    const float sx[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
     double acc = 0.0;
+    if (SC) {
+        const uint32_t sc[4] = {S0 & 0xffu, (S0 >> 16) & 0xffu, S1 & 0xffu, (S1 >> 16) & 0xffu};
+        const float sx[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        // field j masked in place: bytes hold q * 4^j, so qx is 4^j times
-        // the reference's sum and dl is used divided by 4^j (exact)
-        const float dl = d * (float)(sc[j] & 15u);
-        const float ml = dmin * (float)(sc[j] >> 4);
-        const float inv = j == 0 ? 1.0f : j == 1 ? 0.25f : j == 2 ? 0.0625f : 0.015625f;
-        float qx = 0.0f;
+        for (int j = 0; j < 4; j++) {
+            // field j masked in place: bytes hold q * 4^j, so qx is 4^j times
+            // the reference's sum and dl is used divided by 4^j (exact)
+            const float dl = d * (float)(sc[j] & 15u);
+            const float ml = dmin * (float)(sc[j] >> 4);
+            const float inv = j == 0 ? 1.0f : j == 1 ? 0.25f : j == 2 ? 0.0625f : 0.015625f;
+            float qx = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const uint32_t v = dw_of(r.q, k) & (0x03030303u << (2 * j));
-            float p0, p1, p2, p3;
-            bmul4<SC>(v, xc + 4 * j + k, p0, p1, p2, p3);
-            qx = qx + p0;
-            qx = qx + p1;
-            qx = qx + p2;
-            qx = qx + p3;
+            for (int k = 0; k < 4; k++) {
+                const uint32_t v = dw_of(r.q, k) & (0x03030303u << (2 * j));
+                float p0, p1, p2, p3;
+                bmul4<true>(v, xc + 4 * j + k, p0, p1, p2, p3);
+                qx = qx + p0;
+                qx = qx + p1;
+                qx = qx + p2;
+                qx = qx + p3;
+            }
+            const float t = (dl * (inv * f)) * qx - ml * sx[j];
+            acc = acc + (double)t;
         }
-        const float t = (dl * (SC ? inv * f : inv)) * qx - ml * sx[j];
-        acc = acc + (double)t;
+    } else {
+        // exact convert path (x outside the window): rolled over j, with
+        // the scale bytes, x sums and 1/4^j rotating through the first slot
+        uint32_t s0 = S0 & 0xffu, s1 = (S0 >> 16) & 0xffu, s2 = S1 & 0xffu, s3 = (S1 >> 16) & 0xffu;
+        float x0 = xs4.x, x1 = xs4.y, x2 = xs4.z, x3 = xs4.w;
+        float inv = 1.0f;
+#pragma unroll 1
+        for (int j = 0; j < 4; j++) {
+            const float dl = d * (float)(s0 & 15u);
+            const float ml = dmin * (float)(s0 >> 4);
+            const uint32_t m = 0x03030303u << (2 * j);
+            float qx = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                float p0, p1, p2, p3;
+                bmul4<false>(dw_of(r.q, k) & m, xc + 4 * j + k, p0, p1, p2, p3);
+                qx = qx + p0;
+                qx = qx + p1;
+                qx = qx + p2;
+                qx = qx + p3;
+            }
+            const float t = (dl * inv) * qx - ml * x0;
+            acc = acc + (double)t;
+            s0 = s1; s1 = s2; s2 = s3;
+            x0 = x1; x1 = x2; x2 = x3;
+            inv = inv * 0.25f;
+        }
     }
     return acc;
 }
@@ -513,30 +557,64 @@ __device__ __forceinline__ double term_nib(const RawNB& r, const float4* xc, con
                                            float f) {
     const float d = f16_bits_to_f32(r.dd & 0xffffu);
     const float dmin = f16_bits_to_f32(r.dd >> 16);
-    const float sx[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
     double acc = 0.0;
+    if (SC) {
+        const float sx[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
 #pragma unroll
-    for (int g = 0; g < 4; g++) {
-        const uint32_t scb = (r.s >> (8 * g)) & 0xffu;
-        const float dl = d * (float)(scb & 15u);
-        const float ml = dmin * (float)(scb >> 4);
-        const uint4 src = (g < 2) ? r.qa : r.qb;
-        // high-nibble groups are converted in place (16 q): scale dl by 1/16
-        const float inv = (g & 1) ? 0.0625f : 1.0f;
-        float qx = 0.0f;
+        for (int g = 0; g < 4; g++) {
+            const uint32_t scb = (r.s >> (8 * g)) & 0xffu;
+            const float dl = d * (float)(scb & 15u);
+            const float ml = dmin * (float)(scb >> 4);
+            const uint4 src = (g < 2) ? r.qa : r.qb;
+            // high-nibble groups are used in place (16 q): scale dl by 1/16
+            const float inv = (g & 1) ? 0.0625f : 1.0f;
+            float qx = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            uint32_t v = dw_of(src, k);
-            v = (g & 1) ? (v & 0xf0f0f0f0u) : (v & 0x0f0f0f0fu);
-            float p0, p1, p2, p3;
-            bmul4<SC>(v, xc + 4 * g + k, p0, p1, p2, p3);
-            qx = qx + p0;
-            qx = qx + p1;
-            qx = qx + p2;
-            qx = qx + p3;
+            for (int k = 0; k < 4; k++) {
+                uint32_t v = dw_of(src, k);
+                v = (g & 1) ? (v & 0xf0f0f0f0u) : (v & 0x0f0f0f0fu);
+                float p0, p1, p2, p3;
+                bmul4<true>(v, xc + 4 * g + k, p0, p1, p2, p3);
+                qx = qx + p0;
+                qx = qx + p1;
+                qx = qx + p2;
+                qx = qx + p3;
+            }
+            const float t = (dl * (inv * f)) * qx - ml * sx[g];
+            acc = acc + (double)t;
         }
-        const float t = (dl * (SC ? inv * f : inv)) * qx - ml * sx[g];
-        acc = acc + (double)t;
+    } else {
+        // exact convert path (x outside the window): rolled over g, with the
+        // packed words and x sums rotating through the first slots
+        uint32_t w0 = r.qa.x, w1 = r.qa.y, w2 = r.qa.z, w3 = r.qa.w;
+        uint32_t w4 = r.qb.x, w5 = r.qb.y, w6 = r.qb.z, w7 = r.qb.w;
+        float x0 = xs4.x, x1 = xs4.y, x2 = xs4.z, x3 = xs4.w;
+        uint32_t sc = r.s;
+#pragma unroll 1
+        for (int g = 0; g < 4; g++) {
+            const float dl = d * (float)(sc & 15u);
+            const float ml = dmin * (float)((sc >> 4) & 15u);
+            const bool hi = g & 1;
+            const uint32_t m = hi ? 0xf0f0f0f0u : 0x0f0f0f0fu;
+            float qx = 0.0f;
+            const uint32_t v4[4] = {w0, w1, w2, w3};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                float p0, p1, p2, p3;
+                bmul4<false>(v4[k] & m, xc + 4 * g + k, p0, p1, p2, p3);
+                qx = qx + p0;
+                qx = qx + p1;
+                qx = qx + p2;
+                qx = qx + p3;
+            }
+            const float t = (dl * (hi ? 0.0625f : 1.0f)) * qx - ml * x0;
+            acc = acc + (double)t;
+            if (hi) {                    // next pair of groups reads qb
+                w0 = w4; w1 = w5; w2 = w6; w3 = w7;
+            }
+            sc >>= 8;
+            x0 = x1; x1 = x2; x2 = x3;
+        }
     }
     return acc;
 }
@@ -673,6 +751,67 @@ constexpr int SCR_FLAGS = 4 * MAXSEG;
 constexpr int SCR_WTAB = SCR_FLAGS + 4 * 16;
 constexpr int SCR_BYTES = SCR_WTAB + 8 * MAXG;
 
+// Where chunk f = base + lane of a workgroup's range lives: its local row
+// rho, column chunk c, staged-x chunk cx and weight address (f clamped to
+// the last chunk).  Branch-free, so the loads that follow are unconditional
+// and the compiler can count the outstanding ones exactly.
+template <int TYPE, bool GROUPED>
+struct Walk {
+    const uint8_t* w0;
+    const uint8_t* const* wtab;    // LDS table of the group bases (GROUPED)
+    uint32_t nc_m, ng_m;
+    int nc_l, ng_l, Ng, x_stride, NC, b, G, lane, last;
+    size_t rbytes;
+
+    __device__ __forceinline__ wptr locate(int base, int& cx) const {
+        const uint32_t f = (uint32_t)min(base + lane, last);
+        const uint32_t rho = div_magic(f, nc_m, nc_l);
+        const uint32_t c = f - rho * (uint32_t)NC;
+        const uint32_t r = (uint32_t)b + (uint32_t)G * rho;
+        if (GROUPED) {
+            const uint32_t g = div_magic(r, ng_m, ng_l);
+            cx = (x_stride ? (int)g * NC : 0) + (int)c;
+            return to_global(wtab[g]) + (size_t)(r - g * (uint32_t)Ng) * rbytes +
+                   (size_t)(c >> 2) * TypeInfo<TYPE>::BB;
+        }
+        cx = (int)c;
+        return to_global(w0) + (size_t)r * rbytes + (size_t)(c >> 2) * TypeInfo<TYPE>::BB;
+    }
+};
+
+// The batch loop.  Each wave keeps DEPTH batches in flight: a computed
+// batch's registers are refilled at once with the next batch from the
+// counter.  Batches are handed out in increasing order, so base[0] <
+// base[1] < ...; the first DEPTH batches are static (set by the caller).
+template <int TYPE, int DEPTH, bool GROUPED, bool SC>
+__device__ __forceinline__ void sweep(const Walk<TYPE, GROUPED>& W, int nch, int u, int* next,
+                                      const float4* xl, const float* xs, double* terms, float f,
+                                      double f6, int* base, int* cx,
+                                      typename Chunk<TYPE>::Raw* buf) {
+    using C = Chunk<TYPE>;
+    while (base[0] < nch) {
+#pragma unroll
+        for (int k = 0; k < DEPTH; k++) {
+            int nb = 0;
+            if (W.lane == 0) nb = atomicAdd(next, 64);
+            if (base[k] < nch) {                 // uniform over the wave
+                const int fi = base[k] + W.lane;
+                const double t = C::template term<SC>(buf[k], u, xl + cx[k] * XPAD, xs, cx[k],
+                                                      f, f6);
+                if (fi < nch) terms[fi] = t;
+            }
+            base[k] = __builtin_amdgcn_readfirstlane(nb);
+            buf[k] = C::load(W.locate(base[k], cx[k]), u);
+        }
+    }
+    // the last refill is past the end: wait for it here, so no load is
+    // outstanding into the next segment (the compiler would otherwise wait
+    // for all loads where the next segment reuses the registers, including
+    // that segment's x loads)
+#pragma unroll
+    for (int k = 0; k < DEPTH; k++) C::drain(buf[k]);
+}
+
 template <int TYPE, int DEPTH, bool GROUPED>
 __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st, uint8_t* smem) {
     using TI = TypeInfo<TYPE>;
@@ -694,24 +833,8 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
     const uint8_t** wtab = reinterpret_cast<const uint8_t**>(smem + A.scr_off + SCR_WTAB);
     const int ngx = S.x_stride ? S.ngroups : 1;
 
-    // Chunk f = base + lane of the workgroup's range (clamped to the last
-    // one): its local row rho, column chunk c, staged-x chunk cx and weight
-    // address.  Branch-free, so the loads that follow are unconditional and
-    // the compiler can count the outstanding ones exactly.
-    auto locate = [&](int base, int& cx) -> wptr {
-        const uint32_t f = (uint32_t)min(base + lane, last);
-        const uint32_t rho = div_magic(f, S.nc_m, S.nc_l);
-        const uint32_t c = f - rho * (uint32_t)NC;
-        const uint32_t r = (uint32_t)b + (uint32_t)G * rho;
-        if (GROUPED) {
-            const uint32_t g = div_magic(r, S.ng_m, S.ng_l);
-            cx = (S.x_stride ? (int)g * NC : 0) + (int)c;
-            return to_global(wtab[g]) + (size_t)(r - g * (uint32_t)S.Ng) * rbytes +
-                   (size_t)(c >> 2) * TI::BB;
-        }
-        cx = (int)c;
-        return to_global(S.w[0]) + (size_t)r * rbytes + (size_t)(c >> 2) * TI::BB;
-    };
+    const Walk<TYPE, GROUPED> W = {S.w[0], wtab, S.nc_m, S.ng_m, S.nc_l, S.ng_l, S.Ng,
+                                   S.x_stride, NC, b, G, lane, last, rbytes};
 
     // x staging decision: SC types stage x scaled, Q6_K unscaled; a Q6_K
     // segment can read a scaled x, an SC type restages an unscaled one
@@ -741,7 +864,7 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
 #pragma unroll
     for (int k = 0; k < DEPTH; k++) {
         base[k] = (k * (T >> 6) + wave) * 64;
-        buf[k] = C::load(locate(base[k], cx[k]), u);
+        buf[k] = C::load(W.locate(base[k], cx[k]), u);
     }
 
     if (restage) {
@@ -775,37 +898,10 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
     const float f = st.k ? ldexpf(1.0f, 149 - st.k) : 1.0f;
     const double f6 = ldexp(0.25, -st.k);
 
-    // Each wave keeps DEPTH batches in flight: a computed batch's registers
-    // are refilled at once with the next batch from the counter.  Batches
-    // are handed out in increasing order, so base[0] < base[1] < ...
-    auto sweep = [&](auto scaled) {
-        constexpr bool SC = decltype(scaled)::value;
-        while (base[0] < nch) {
-#pragma unroll
-            for (int k = 0; k < DEPTH; k++) {
-                int nb = 0;
-                if (lane == 0) nb = atomicAdd(next, 64);
-                if (base[k] < nch) {                 // uniform over the wave
-                    const int fi = base[k] + lane;
-                    const double t = C::template term<SC>(buf[k], u, xl + cx[k] * XPAD, xs, cx[k],
-                                                          f, f6);
-                    if (fi < nch) terms[fi] = t;
-                }
-                base[k] = __builtin_amdgcn_readfirstlane(nb);
-                buf[k] = C::load(locate(base[k], cx[k]), u);
-            }
-        }
-        // the last refill is past the end: wait for it here, so no load is
-        // outstanding into the next segment (the compiler would otherwise
-        // wait for all loads where the next segment reuses the registers,
-        // including that segment's x loads)
-#pragma unroll
-        for (int k = 0; k < DEPTH; k++) C::drain(buf[k]);
-    };
     if (SCTYPE && st.k > 0)
-        sweep(std::integral_constant<bool, true>());
+        sweep<TYPE, DEPTH, GROUPED, true>(W, nch, u, next, xl, xs, terms, f, f6, base, cx, buf);
     else
-        sweep(std::integral_constant<bool, false>());
+        sweep<TYPE, DEPTH, GROUPED, false>(W, nch, u, next, xl, xs, terms, f, f6, base, cx, buf);
     __syncthreads();
 
     // Row reduction: L lanes per row (L = 8..64, as many as T allows), lane

@@ -204,8 +204,9 @@ static const void* tensor_dev(const kq_tensor* w, int N, int K) {
  * size follows the largest per-workgroup share of 64-weight chunks over the
  * segments: enough waves to keep each CU's memory pipe busy without many
  * idle lanes on small tensors (KQ_WG_THREADS overrides: 256, 512 or
- * 1024).  Each wave keeps one batch of loads in flight (KQ_DEPTH=2: two;
- * a second batch costs more registers than the overlap it buys). */
+ * 1024).  Each wave keeps one batch of loads in flight, two when the
+ * workgroup has fewer than 16 waves to hide the memory latency with
+ * (KQ_DEPTH overrides: 1 or 2). */
 static int plan_grid(void) {
     const char* e = getenv("KQ_GRID");
     int g = e && atoi(e) > 0 ? atoi(e) : g_kq.n_cu;
@@ -226,10 +227,10 @@ static int plan_threads(const kqk_seg* segs, int nseg, int grid) {
     return chunks >= 4096 ? 1024 : chunks >= 1024 ? 512 : 256;
 }
 
-static int plan_depth(void) {
+static int plan_depth(int threads) {
     const char* e = getenv("KQ_DEPTH");
-    const int d = e ? atoi(e) : 1;
-    return d == 2 ? 2 : 1;
+    if (e) return atoi(e) == 2 ? 2 : 1;
+    return threads < 1024 ? 2 : 1;
 }
 
 static int launch_segs(const kqk_seg* segs, int nseg, hipStream_t st) {
@@ -240,7 +241,7 @@ static int launch_segs(const kqk_seg* segs, int nseg, hipStream_t st) {
     if (lds > g_kq.lds_max)
         return kq_fail("segments need %ld bytes of LDS (max %d): split the rows", lds,
                        g_kq.lds_max);
-    int e = kqk_launch_segs(segs, nseg, grid, threads, plan_depth(), lds, xs_off, terms_off,
+    int e = kqk_launch_segs(segs, nseg, grid, threads, plan_depth(threads), lds, xs_off, terms_off,
                             scr_off, st);
     if (e) return kq_fail("gemv launch: %s", hipGetErrorString((hipError_t)e));
     return 0;
