@@ -1,20 +1,27 @@
 #!/usr/bin/env python3
 """k-quant GEMV on one MI355X: HBM GB/s, fraction of peak, µs per layer set.
 
-Workload (where the ≥70 % north-star target is
+Workload (where the >=70 % north-star target is
 quoted): the seven batch-1 matvecs of one 27B-class dense decode layer,
 hidden 5120 --
   Q 5120->6144, K/V 5120->1024, O 6144->5120, gate/up 5120->17408 in Q4_K,
   down 17408->5120 in Q6_K --
 on seeded synthetic super-blocks and x ~ N(0,1) (stratum_amd.synth).
-A step is one pass over the layer set: 7 GEMV launches, each reading its
-weights from HBM.  Four device copies of the layer's weights (860 MB) are
-rotated so no step finds its weights in the 256 MB MALL or the L2s.
+
+A step is one pass over the layer set as a decode loop issues it: one
+kq_gemv_segments_dev launch per group of matvecs that share an input and
+have no dependency between them -- [Q, K, V], [O], [gate, up], [down] --
+each launch reading its weights from HBM.  (The 7-launch form, one
+kq_gemv_dev per tensor as the reference calls st_linear_dispatch, is timed
+too and reported as "separate_launches".)  Four device copies of the
+layer's weights (860 MB) are rotated so no step finds its weights in the
+256 MB MALL or the L2s.
 
 value = algorithmic bytes of the layer set / measured time per step, with
 algorithmic bytes per matvec = N*(K/256)*block_bytes + 4K + 4N.
-roofline: the dominant kernel (ffn_gate, Q4_K 17408x5120) timed per launch
-with HIP events on the stream it runs on.
+roofline: the dominant launch ([gate, up], kernel kq_segs_kernel<1, 1>)
+timed per launch with HIP events on the stream it runs on; traffic from
+profiles/traffic.json (rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated).
 cpu_baseline: the reference's own scalar routines (oracle/_ref) -- or the
 repo's restatement when that build is absent -- on the host cores, over a
 bounded number of passes of the same layer set.
@@ -24,6 +31,7 @@ bounded number of passes of the same layer set.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -51,7 +59,15 @@ LAYER_27B = [
     ("ffn_down", KQ.TYPE_Q6_K, 5120, 17408, "ff"),
 ]
 X_LEN = {"h": 5120, "attn": 6144, "ff": 17408}
-DOMINANT = "ffn_gate"
+# launches of one step: matvecs that share x and do not depend on each other
+GROUPS = [
+    ("attn_qkv", ["attn_q", "attn_k", "attn_v"]),
+    ("attn_output", ["attn_output"]),
+    ("ffn_gate_up", ["ffn_gate", "ffn_up"]),
+    ("ffn_down", ["ffn_down"]),
+]
+DOMINANT = "ffn_gate_up"
+DOMINANT_KERNEL = "kq_segs_kernel<1, 1>"
 COPIES = 4
 
 
@@ -98,6 +114,13 @@ def cpu_baseline(weights: dict, xs: dict) -> dict:
     }
 
 
+def load_traffic() -> dict | None:
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    return json.load(open(path)).get(DOMINANT)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -105,6 +128,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--kernel-reps", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run 5 copies of 64 MiB (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -117,9 +142,10 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
     torch.cuda.set_device(0)
-    KQ.lib()  # fails loudly when the HIP library is missing
+    L = KQ.lib()  # fails loudly when the HIP library is missing
 
     # ---- inputs: one seeded copy on the host, COPIES rotated on the device
+    spec = {name: (t, N, K, xn) for name, t, N, K, xn in LAYER_27B}
     host_w, offs, total = {}, {}, 0
     for i, (name, t, N, K, _) in enumerate(LAYER_27B):
         host_w[name] = synth.tensor(t, N, K, seed=1000 + i)
@@ -135,55 +161,79 @@ def main() -> int:
     ys = {name: torch.empty(N, dtype=torch.float32, device="cuda") for name, _, N, _, _ in LAYER_27B}
     stream = torch.cuda.current_stream()
     sh = stream.cuda_stream
-    L = KQ.lib()
-    plan = [(t, N, K, offs[name], xs[xn].data_ptr(), ys[name].data_ptr(), name)
-            for name, t, N, K, xn in LAYER_27B]
 
-    def launch(copy, t, N, K, off, xp, yp):
-        rc = L.kq_gemv_dev(t, copy.data_ptr() + off, xp, None, yp, N, K, sh)
-        if rc != 0:
+    # segment arrays of every (copy, group), built once
+    seg_arrays = []
+    for c in copies:
+        per_group = []
+        for _, members in GROUPS:
+            segs = [KQ.segment(spec[m][0], spec[m][2], spec[m][1], [c.data_ptr() + offs[m]],
+                               xs[spec[m][3]].data_ptr(), ys[m].data_ptr()) for m in members]
+            per_group.append(((KQ.KqSegment * len(segs))(*segs), len(segs)))
+        seg_arrays.append(per_group)
+
+    def launch_group(copy_i, g):
+        arr, n = seg_arrays[copy_i][g]
+        if L.kq_gemv_segments_dev(arr, n, sh) != 0:
             raise RuntimeError(L.kq_last_error().decode())
 
     def step(i):
+        for g in range(len(GROUPS)):
+            launch_group(i % COPIES, g)
+
+    def step_separate(i):
         c = copies[i % COPIES]
-        for t, N, K, off, xp, yp, _ in plan:
-            launch(c, t, N, K, off, xp, yp)
+        for name, t, N, K, xn in LAYER_27B:
+            if L.kq_gemv_dev(t, c.data_ptr() + offs[name], xs[xn].data_ptr(), None,
+                             ys[name].data_ptr(), N, K, sh) != 0:
+                raise RuntimeError(L.kq_last_error().decode())
 
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for i in range(args.steps):
-        step(i)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms_per_step = e0.elapsed_time(e1) / args.steps
+    def timed(fn, steps, warmup):
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        w0 = time.perf_counter()
+        e0.record(stream)
+        for i in range(steps):
+            fn(i)
+        e1.record(stream)
+        enqueue_s = time.perf_counter() - w0
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps, enqueue_s / steps * 1e3
+
     set_bytes = sum(algo_bytes(t, N, K) for _, t, N, K, _ in LAYER_27B)
+    ms_per_step, enq_ms = timed(step, args.steps, args.warmup)
     gbs = set_bytes / (ms_per_step * 1e-3) / 1e9
+    sep_ms, sep_enq_ms = timed(step_separate, args.steps, args.warmup)
 
-    # ---- per-kernel durations (events around each launch, same stream)
-    per_kernel = {}
-    for t, N, K, off, xp, yp, name in plan:
+    # ---- per-launch durations (events around each launch, same stream)
+    per_launch = {}
+    for g, (gname, members) in enumerate(GROUPS):
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                for _ in range(args.kernel_reps)]
         for i in range(4):
-            launch(copies[i % COPIES], t, N, K, off, xp, yp)
+            launch_group(i % COPIES, g)
         for i, (a, b) in enumerate(evs):
             a.record(stream)
-            launch(copies[(i + 1) % COPIES], t, N, K, off, xp, yp)
+            launch_group((i + 1) % COPIES, g)
             b.record(stream)
         torch.cuda.synchronize()
         us = float(np.mean([a.elapsed_time(b) for a, b in evs])) * 1e3
-        per_kernel[name] = {"us": round(us, 2),
-                            "GB/s": round(algo_bytes(t, N, K) / (us * 1e-6) / 1e9, 1)}
-    dom = next(x for x in LAYER_27B if x[0] == DOMINANT)
-    dom_us = per_kernel[DOMINANT]["us"]
-    achieved = algo_bytes(dom[1], dom[2], dom[3]) / (dom_us * 1e-6) / 1e9
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "traffic.json")
-    if os.path.exists(tpath):
-        traffic = json.load(open(tpath)).get("q4k_gemv_27b_gate", {}).get("hbm_bytes_per_launch")
+        nbytes = sum(algo_bytes(spec[m][0], spec[m][1], spec[m][2]) for m in members)
+        per_launch[gname] = {"us": round(us, 2), "bytes": nbytes,
+                             "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    dom = per_launch[DOMINANT]
+    achieved = dom["bytes"] / (dom["us"] * 1e-6) / 1e9
+    tr = load_traffic()
+    traffic = tr.get("hbm_bytes_per_launch") if tr else None
+
+    if args.copy_calibration:
+        src = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
 
     out = {
         "metric": METRIC,
@@ -197,21 +247,27 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic",
+        "data": "synthetic (seeded k-quant super-blocks, x ~ N(0,1))",
         "config": {
             "workload": "27B-class dense decode layer matvec set, batch 1 (BASELINE configs[2]): "
-                        "Q/K/V/O/gate/up Q4_K, down Q6_K, hidden 5120, ffn 17408",
+                        "Q/K/V/O/gate/up Q4_K, down Q6_K, hidden 5120, ffn 17408; launches "
+                        "[Q,K,V] [O] [gate,up] [down]",
             "layer_set_bytes": set_bytes,
             "weight_copies_rotated": COPIES,
-            "launches_per_step": len(LAYER_27B),
+            "launches_per_step": len(GROUPS),
         },
         "us_per_layer_set": round(ms_per_step * 1e3, 2),
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
-        "per_kernel": per_kernel,
+        "host_enqueue_us_per_step": round(enq_ms * 1e3, 1),
+        "separate_launches": {"launches_per_step": len(LAYER_27B),
+                              "us_per_layer_set": round(sep_ms * 1e3, 2),
+                              "GB/s": round(set_bytes / (sep_ms * 1e-3) / 1e9, 1),
+                              "host_enqueue_us_per_step": round(sep_enq_ms * 1e3, 1)},
+        "per_launch": per_launch,
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
-            "kernel": "kq_gemv_kernel<Q4_K> ffn_gate 17408x5120",
+            "kernel": f"{DOMINANT_KERNEL}: ffn_gate + ffn_up (Q4_K 2 x 17408x5120) in one launch",
         },
         "cpu_baseline": None,
     }

@@ -173,11 +173,11 @@ template <int TYPE> struct XGroup {
     static constexpr bool SUMS = TypeInfo<TYPE>::XS_PER_CHUNK != 0;
 };
 
-// true when v is finite, nonzero and outside the scaled-mode window
-__device__ __forceinline__ bool out_of_window(float v) {
+// 1 when v is finite, nonzero and outside the scaled-mode window
+__device__ __forceinline__ uint32_t out_of_window(float v) {
     const uint32_t e = (__float_as_uint(v) & 0x7fffffffu) >> 23;
     const bool zero = (__float_as_uint(v) & 0x7fffffffu) == 0u;
-    return !zero && e != 255u && (e < KSC_EMIN || e >= KSC_EMAX);
+    return (!zero && e != 255u && (e < KSC_EMIN || e >= KSC_EMAX)) ? 1u : 0u;
 }
 
 // LDS slot (within one x) of float4 q of group gi, and the xs index (within
@@ -224,7 +224,7 @@ struct XStage {
         int slot0, xsi;
         group_place<TYPE>(gi, slot0, xsi);
         f32x4* dst = reinterpret_cast<f32x4*>(xl) + gx * NC * XPAD + slot0;
-        bool bad = false;
+        uint32_t bad = 0;
         float acc = 0.0f;
 #pragma unroll
         for (int q = 0; q < G4; q++) {
@@ -240,7 +240,7 @@ struct XStage {
             dst[q] = o;
         }
         if (XGroup<TYPE>::SUMS && sums) xs[gx * per + xsi] = acc;
-        return bad;
+        return bad != 0;
     }
 };
 
@@ -695,27 +695,34 @@ template <> struct Chunk<T_NIB> {
 constexpr int MAXSEG = 8;
 constexpr int MAXG = 16;
 
-// The fields a segment needs first come first (one 64-byte scalar load
-// with w[0]); the other weight bases follow.
+// A segment: N rows of one type and row length K, made of nparts parts.
+// Part p holds rows [start[p], start[p+1]) at weight base w[p], writes
+// y[p][row - start[p]] (plus add[p][...] when add[p] != nullptr) and reads
+// x, or x + p * x_stride when x_stride != 0.  One part is a plain tensor;
+// several parts are the matvecs of a same-input group (Q/K/V, gate/up)
+// merged into one row space, or the selected experts of an MoE layer.
+// The fields a segment needs first come first (one scalar load).
 struct Seg {
     const float* x;
-    const float* add;
-    float* y;
-    int type, K, N, Ng, ngroups, x_stride;
-    uint32_t ng_m;     // magic multiplier for division by Ng (0: Ng == 1)
-    int ng_l;          // its shift
+    int type, K, N, nparts, x_stride;
+    int pn;            // rows per part when every part has the same count, else 0
+    uint32_t pn_m;     // magic multiplier for division by pn (0: pn <= 1)
+    int pn_l;          // its shift
     uint32_t nc_m;     // the same for division by NC = K / 64
     int nc_l;
     const uint8_t* w[MAXG];
+    float* y[MAXG];
+    const float* add[MAXG];
+    int start[MAXG];
 };
 
 // Issues the scalar loads of a segment's leading fields together and waits
 // for them once: used as they are needed, the fields would be fetched in
 // several dependent round trips to the kernel-argument memory.
 __device__ __forceinline__ void prefetch_seg(const Seg& S) {
-    asm volatile("" ::"s"(S.x), "s"(S.add), "s"(S.y), "s"(S.type), "s"(S.K), "s"(S.N),
-                 "s"(S.Ng), "s"(S.ngroups), "s"(S.x_stride), "s"(S.ng_m), "s"(S.ng_l),
-                 "s"(S.nc_m), "s"(S.nc_l), "s"(S.w[0]));
+    asm volatile("" ::"s"(S.x), "s"(S.type), "s"(S.K), "s"(S.N), "s"(S.nparts),
+                 "s"(S.x_stride), "s"(S.pn), "s"(S.pn_m), "s"(S.pn_l), "s"(S.nc_m), "s"(S.nc_l),
+                 "s"(S.w[0]), "s"(S.y[0]), "s"(S.add[0]));
 }
 
 struct SegsArg {
@@ -746,36 +753,73 @@ struct Staged {
     bool bad;
 };
 
-// LDS scratch: per-segment batch counters, per-wave flags, weight-base table
+// LDS scratch: per-segment batch counters, per-wave flags, part tables
 constexpr int SCR_FLAGS = 4 * MAXSEG;
-constexpr int SCR_WTAB = SCR_FLAGS + 4 * 16;
-constexpr int SCR_BYTES = SCR_WTAB + 8 * MAXG;
+constexpr int SCR_TABS = SCR_FLAGS + 4 * 16;
+constexpr int SCR_BYTES = SCR_TABS + 3 * 8 * MAXG;
 
-// Where chunk f = base + lane of a workgroup's range lives: its local row
-// rho, column chunk c, staged-x chunk cx and weight address (f clamped to
-// the last chunk).  Branch-free, so the loads that follow are unconditional
-// and the compiler can count the outstanding ones exactly.
-template <int TYPE, bool GROUPED>
+// Part layout of a segment: one part; up to 4 parts of any sizes (a merged
+// same-input group: the part of a row by comparing with the part starts,
+// its base by selection); or up to 16 equal parts (MoE experts: the part of
+// a row by division, its base from an LDS table).
+constexpr int PM_ONE = 0, PM_LIST = 1, PM_EQUAL = 2;
+constexpr int LIST_MAX = 4;
+
+template <typename V>
+__device__ __forceinline__ V pick4(uint32_t g, V v0, V v1, V v2, V v3) {
+    return g == 0 ? v0 : g == 1 ? v1 : g == 2 ? v2 : v3;
+}
+
+// Part g and part-local row rg of segment row r.
+template <int PM>
+__device__ __forceinline__ uint32_t part_of(const Seg& S, uint32_t r, uint32_t& rg) {
+    if (PM == PM_ONE) {
+        rg = r;
+        return 0;
+    }
+    uint32_t g;
+    if (PM == PM_EQUAL) {
+        g = div_magic(r, S.pn_m, S.pn_l);
+        rg = r - g * (uint32_t)S.pn;
+        return g;
+    }
+    g = 0;
+#pragma unroll
+    for (int i = 1; i < LIST_MAX; i++) g += (i < S.nparts && r >= (uint32_t)S.start[i]) ? 1u : 0u;
+    rg = r - (uint32_t)pick4(g, S.start[0], S.start[1], S.start[2], S.start[3]);
+    return g;
+}
+
+// weight base of part g (the LDS table holds the PM_EQUAL bases)
+template <int PM>
+__device__ __forceinline__ const uint8_t* part_w(const Seg& S, uint32_t g,
+                                                 const uint8_t* const* wtab) {
+    if (PM == PM_ONE) return S.w[0];
+    if (PM == PM_LIST) return pick4(g, S.w[0], S.w[1], S.w[2], S.w[3]);
+    return wtab[g];
+}
+
+// Where chunk f = base + lane of a workgroup's range lives: its staged-x
+// chunk cx and weight address (f clamped to the last chunk).  Branch-free,
+// so the loads that follow are unconditional and the compiler can count the
+// outstanding ones exactly.
+template <int TYPE, int PM>
 struct Walk {
-    const uint8_t* w0;
-    const uint8_t* const* wtab;    // LDS table of the group bases (GROUPED)
-    uint32_t nc_m, ng_m;
-    int nc_l, ng_l, Ng, x_stride, NC, b, G, lane, last;
+    const Seg* S;
+    const uint8_t* const* wtab;
+    int NC, b, G, lane, last;
     size_t rbytes;
 
     __device__ __forceinline__ wptr locate(int base, int& cx) const {
         const uint32_t f = (uint32_t)min(base + lane, last);
-        const uint32_t rho = div_magic(f, nc_m, nc_l);
+        const uint32_t rho = div_magic(f, S->nc_m, S->nc_l);
         const uint32_t c = f - rho * (uint32_t)NC;
         const uint32_t r = (uint32_t)b + (uint32_t)G * rho;
-        if (GROUPED) {
-            const uint32_t g = div_magic(r, ng_m, ng_l);
-            cx = (x_stride ? (int)g * NC : 0) + (int)c;
-            return to_global(wtab[g]) + (size_t)(r - g * (uint32_t)Ng) * rbytes +
-                   (size_t)(c >> 2) * TypeInfo<TYPE>::BB;
-        }
-        cx = (int)c;
-        return to_global(w0) + (size_t)r * rbytes + (size_t)(c >> 2) * TypeInfo<TYPE>::BB;
+        uint32_t rg;
+        const uint32_t g = part_of<PM>(*S, r, rg);
+        cx = (PM != PM_ONE && S->x_stride ? (int)g * NC : 0) + (int)c;
+        return to_global(part_w<PM>(*S, g, wtab)) + (size_t)rg * rbytes +
+               (size_t)(c >> 2) * TypeInfo<TYPE>::BB;
     }
 };
 
@@ -783,8 +827,8 @@ struct Walk {
 // batch's registers are refilled at once with the next batch from the
 // counter.  Batches are handed out in increasing order, so base[0] <
 // base[1] < ...; the first DEPTH batches are static (set by the caller).
-template <int TYPE, int DEPTH, bool GROUPED, bool SC>
-__device__ __forceinline__ void sweep(const Walk<TYPE, GROUPED>& W, int nch, int u, int* next,
+template <int TYPE, int DEPTH, int PM, bool SC>
+__device__ __forceinline__ void sweep(const Walk<TYPE, PM>& W, int nch, int u, int* next,
                                       const float4* xl, const float* xs, double* terms, float f,
                                       double f6, int* base, int* cx,
                                       typename Chunk<TYPE>::Raw* buf) {
@@ -812,7 +856,7 @@ __device__ __forceinline__ void sweep(const Walk<TYPE, GROUPED>& W, int nch, int
     for (int k = 0; k < DEPTH; k++) C::drain(buf[k]);
 }
 
-template <int TYPE, int DEPTH, bool GROUPED>
+template <int TYPE, int DEPTH, int PM>
 __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st, uint8_t* smem) {
     using TI = TypeInfo<TYPE>;
     using C = Chunk<TYPE>;
@@ -830,11 +874,30 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
     double* terms = reinterpret_cast<double*>(smem + A.terms_off);
     int* next = reinterpret_cast<int*>(smem + A.scr_off) + seg;
     int* flags = reinterpret_cast<int*>(smem + A.scr_off + SCR_FLAGS);
-    const uint8_t** wtab = reinterpret_cast<const uint8_t**>(smem + A.scr_off + SCR_WTAB);
-    const int ngx = S.x_stride ? S.ngroups : 1;
+    const uint8_t** wtab = reinterpret_cast<const uint8_t**>(smem + A.scr_off + SCR_TABS);
+    float** ytab = reinterpret_cast<float**>(smem + A.scr_off + SCR_TABS + 8 * MAXG);
+    const float** atab = reinterpret_cast<const float**>(smem + A.scr_off + SCR_TABS + 16 * MAXG);
+    const int ngx = (PM != PM_ONE && S.x_stride) ? S.nparts : 1;
 
-    const Walk<TYPE, GROUPED> W = {S.w[0], wtab, S.nc_m, S.ng_m, S.nc_l, S.ng_l, S.Ng,
-                                   S.x_stride, NC, b, G, lane, last, rbytes};
+    if (PM == PM_EQUAL) {
+        // each wave writes the part tables itself (identical values), so its
+        // own reads need no barrier
+        const uint8_t* wv = S.w[0];
+        float* yv = S.y[0];
+        const float* av = S.add[0];
+#pragma unroll
+        for (int g = 1; g < MAXG; g++) {
+            wv = lane == g ? S.w[g] : wv;
+            yv = lane == g ? S.y[g] : yv;
+            av = lane == g ? S.add[g] : av;
+        }
+        if (lane < S.nparts) {
+            wtab[lane] = wv;
+            ytab[lane] = yv;
+            atab[lane] = av;
+        }
+    }
+    const Walk<TYPE, PM> W = {&S, wtab, NC, b, G, lane, last, rbytes};
 
     // x staging decision: SC types stage x scaled, Q6_K unscaled; a Q6_K
     // segment can read a scaled x, an SC type restages an unscaled one
@@ -846,16 +909,6 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
     const XStage<TYPE> xg = {S.x, S.x_stride, K / (4 * G4), ngx * (K / (4 * G4)), NC};
     f32x4 xv[G4];
     if (restage) xg.load(tid, xv);            // first round of x, ahead of the weights
-
-    if (GROUPED) {
-        // each wave writes the weight-base table itself (identical values),
-        // so its own reads below need no barrier
-        const uint8_t* wv = S.w[0];
-#pragma unroll
-        for (int g = 1; g < MAXG; g++)
-            if (lane == g) wv = S.w[g];
-        if (lane < S.ngroups) wtab[lane] = wv;
-    }
 
     // first DEPTH batches: static (wave w takes chunks 64w .., then
     // 64(W + w) ..); their latency overlaps the staging
@@ -899,9 +952,9 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
     const double f6 = ldexp(0.25, -st.k);
 
     if (SCTYPE && st.k > 0)
-        sweep<TYPE, DEPTH, GROUPED, true>(W, nch, u, next, xl, xs, terms, f, f6, base, cx, buf);
+        sweep<TYPE, DEPTH, PM, true>(W, nch, u, next, xl, xs, terms, f, f6, base, cx, buf);
     else
-        sweep<TYPE, DEPTH, GROUPED, false>(W, nch, u, next, xl, xs, terms, f, f6, base, cx, buf);
+        sweep<TYPE, DEPTH, PM, false>(W, nch, u, next, xl, xs, terms, f, f6, base, cx, buf);
     __syncthreads();
 
     // Row reduction: L lanes per row (L = 8..64, as many as T allows), lane
@@ -927,10 +980,23 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
         if (L >= 32) s = s + __shfl_xor(s, 16, 64);
         if (L >= 64) s = s + __shfl_xor(s, 32, 64);
         if (p == 0) {
-            const int r = b + G * rho;
+            uint32_t rg;
+            const uint32_t g = part_of<PM>(S, (uint32_t)(b + G * rho), rg);
+            float* y;
+            const float* add;
+            if (PM == PM_ONE) {
+                y = S.y[0];
+                add = S.add[0];
+            } else if (PM == PM_LIST) {
+                y = pick4(g, S.y[0], S.y[1], S.y[2], S.y[3]);
+                add = pick4(g, S.add[0], S.add[1], S.add[2], S.add[3]);
+            } else {
+                y = ytab[g];
+                add = atab[g];
+            }
             float v = (float)s;
-            if (S.add) v = S.add[r] + v;
-            S.y[r] = v;
+            if (add) v = add[rg] + v;
+            y[rg] = v;
         }
     }
     // Wait for the y stores here: a store keeps its data registers busy
@@ -963,24 +1029,22 @@ __global__ __launch_bounds__(1024) void kq_segs_kernel(SegsArg A) {
     for (int i = 0; i < A.nseg; i++) {
         const Seg& S = A.s[i];
         if (i) prefetch_seg(S);
-        const bool grp = S.ngroups > 1;
+        const int pm = S.nparts == 1 ? PM_ONE : S.nparts <= LIST_MAX ? PM_LIST : PM_EQUAL;
+#define KQ_RUN(T_)                                                             \
+        if (pm == PM_ONE) run_segment<T_, DEPTH, PM_ONE>(S, A, i, st, smem);   \
+        else if (pm == PM_LIST) run_segment<T_, DEPTH, PM_LIST>(S, A, i, st, smem); \
+        else run_segment<T_, DEPTH, PM_EQUAL>(S, A, i, st, smem);
         if (SINGLE) {
             constexpr int TY = TYPES == TB_Q4K ? T_Q4K : TYPES == TB_Q6K ? T_Q6K
                              : TYPES == TB_Q2K ? T_Q2K : T_NIB;
-            if (grp) run_segment<TY, DEPTH, true>(S, A, i, st, smem);
-            else run_segment<TY, DEPTH, false>(S, A, i, st, smem);
+            KQ_RUN(TY)
             continue;
         }
-#define KQ_RUN(T_, TB_)                                                        \
-        if (TYPES & TB_) {                                                     \
-            if (grp) run_segment<T_, DEPTH, true>(S, A, i, st, smem);          \
-            else run_segment<T_, DEPTH, false>(S, A, i, st, smem);             \
-        }
         switch (S.type) {
-        case T_Q4K: KQ_RUN(T_Q4K, TB_Q4K) break;
-        case T_Q6K: KQ_RUN(T_Q6K, TB_Q6K) break;
-        case T_Q2K: KQ_RUN(T_Q2K, TB_Q2K) break;
-        case T_NIB: KQ_RUN(T_NIB, TB_NIB) break;
+        case T_Q4K: if (TYPES & TB_Q4K) { KQ_RUN(T_Q4K) } break;
+        case T_Q6K: if (TYPES & TB_Q6K) { KQ_RUN(T_Q6K) } break;
+        case T_Q2K: if (TYPES & TB_Q2K) { KQ_RUN(T_Q2K) } break;
+        case T_NIB: if (TYPES & TB_NIB) { KQ_RUN(T_NIB) } break;
         default: break;
         }
 #undef KQ_RUN
@@ -1072,14 +1136,23 @@ int launch_dequant(const uint8_t* w, float* y, long nblocks, hipStream_t st) {
 // ------------------------------------------------------------ C launchers
 extern "C" {
 
-// Host view of one segment (plain C layout, see kq_linear.c).
+// Host view of one segment (plain C layout, mirrored in kq_linear.c):
+// nparts parts, part p = rows [start[p], start[p] + rows[p]) at w[p],
+// writing y[p] (+ add[p]); x, or x + p * x_stride when x_stride != 0.
 struct kqk_seg {
     const void* w[MAXG];
+    float* y[MAXG];
+    const float* add[MAXG];
+    int rows[MAXG];
     const float* x;
-    const float* add;
-    float* y;
-    int type, K, N, Ng, ngroups, x_stride;
+    int type, K, nparts, x_stride;
 };
+
+static long seg_rows(const kqk_seg& g) {
+    long n = 0;
+    for (int p = 0; p < g.nparts; p++) n += g.rows[p];
+    return n;
+}
 
 static int xs_per_chunk(int type) {
     switch (type) {
@@ -1106,14 +1179,21 @@ long kqk_segs_lds(const kqk_seg* segs, int nseg, int grid, int* xs_off, int* ter
     for (int i = 0; i < nseg; i++) {
         const kqk_seg& g = segs[i];
         const int xpc = xs_per_chunk(g.type);
-        if (xpc < 0 || g.K <= 0 || (g.K & 255) || g.ngroups < 1 || g.ngroups > MAXG ||
-            g.N != g.Ng * g.ngroups)
+        if (xpc < 0 || g.K <= 0 || (g.K & 255) || g.nparts < 1 || g.nparts > MAXG)
             return -1;
+        bool equal = true;
+        for (int p = 0; p < g.nparts; p++) {
+            if (g.rows[p] < 1) return -1;
+            equal = equal && g.rows[p] == g.rows[0];
+        }
+        if (g.nparts > LIST_MAX && !equal) return -1;   // many parts must be equal
+        const long N = seg_rows(g);
+        if (N > 0x7fffffffL) return -1;
         const long NC = g.K >> 6;
-        const long ngx = g.x_stride ? g.ngroups : 1;
+        const long ngx = g.x_stride && g.nparts > 1 ? g.nparts : 1;
         xl = xl > ngx * NC * XPAD * 16 ? xl : ngx * NC * XPAD * 16;
         xsb = xsb > ngx * NC * xpc * 4 ? xsb : ngx * NC * xpc * 4;
-        const long R = (g.N + grid - 1) / grid;
+        const long R = (N + grid - 1) / grid;
         tb = tb > R * NC * 8 ? tb : R * NC * 8;
     }
     xsb = (xsb + 15) & ~15L;
@@ -1160,16 +1240,29 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
     for (int i = 0; i < nseg; i++) {
         Seg& d = A.s[i];
         const kqk_seg& h = segs[i];
-        for (int g = 0; g < MAXG; g++)
-            d.w[g] = static_cast<const uint8_t*>(g < h.ngroups ? h.w[g] : h.w[0]);
-        d.x = h.x; d.add = h.add; d.y = h.y;
-        d.type = h.type; d.K = h.K; d.N = h.N; d.Ng = h.Ng; d.ngroups = h.ngroups;
-        d.x_stride = h.x_stride;
-        magic_for((uint32_t)h.Ng, d.ng_m, d.ng_l);
+        int start = 0;
+        bool equal = true;
+        for (int g = 0; g < MAXG; g++) {
+            const int q = g < h.nparts ? g : 0;      // unused slots repeat part 0
+            d.w[g] = static_cast<const uint8_t*>(h.w[q]);
+            d.y[g] = h.y[q];
+            d.add[g] = h.add[q];
+            d.start[g] = g < h.nparts ? start : 0;
+            if (g < h.nparts) {
+                start += h.rows[g];
+                equal = equal && h.rows[g] == h.rows[0];
+            }
+        }
+        d.x = h.x;
+        d.type = h.type; d.K = h.K; d.N = start; d.nparts = h.nparts;
+        d.x_stride = h.nparts > 1 ? h.x_stride : 0;
+        d.pn = equal ? h.rows[0] : 0;
+        magic_for((uint32_t)(equal ? h.rows[0] : 1), d.pn_m, d.pn_l);
         magic_for((uint32_t)(h.K >> 6), d.nc_m, d.nc_l);
         set |= h.type == T_Q4K ? TB_Q4K : h.type == T_Q6K ? TB_Q6K : h.type == T_Q2K ? TB_Q2K : TB_NIB;
     }
     const int t = set == TB_Q4K ? 0 : set == TB_Q6K ? 1 : set == TB_Q2K ? 2 : set == TB_NIB ? 3 : 4;
+    if (t == 4) depth = 1;   // the all-types kernel fits 128 VGPRs at depth 1 only
     hipLaunchKernelGGL(k_segs[depth - 1][t], dim3(grid), dim3(threads), (size_t)lds_bytes, st, A);
     return (int)hipGetLastError();
 }

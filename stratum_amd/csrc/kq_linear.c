@@ -21,14 +21,18 @@
 #include <stdlib.h>
 #include <string.h>
 
-/* launchers (kq_kernels.hip) */
+/* launchers (kq_kernels.hip).  A launcher segment has nparts parts; part p
+ * is rows[p] rows at w[p] writing y[p] (+ add[p]), reading x, or
+ * x + p * x_stride when x_stride != 0. */
 typedef struct {
     const void* w[KQ_MAX_GROUPS];
+    float* y[KQ_MAX_GROUPS];
+    const float* add[KQ_MAX_GROUPS];
+    int rows[KQ_MAX_GROUPS];
     const float* x;
-    const float* add;
-    float* y;
-    int type, K, N, Ng, ngroups, x_stride;
+    int type, K, nparts, x_stride;
 } kqk_seg;
+#define KQK_LIST_MAX 4   /* parts of unequal sizes one launcher segment takes */
 long kqk_segs_lds(const kqk_seg* segs, int nseg, int grid, int* xs_off, int* terms_off,
                   int* scr_off);
 int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int depth,
@@ -221,7 +225,9 @@ static int plan_threads(const kqk_seg* segs, int nseg, int grid) {
     }
     long chunks = 0;
     for (int i = 0; i < nseg; i++) {
-        const long c = (long)((segs[i].N + grid - 1) / grid) * (segs[i].K / 64);
+        long n = 0;
+        for (int p = 0; p < segs[i].nparts; p++) n += segs[i].rows[p];
+        const long c = ((n + grid - 1) / grid) * (segs[i].K / 64);
         if (c > chunks) chunks = c;
     }
     return chunks >= 4096 ? 1024 : chunks >= 1024 ? 512 : 256;
@@ -253,7 +259,8 @@ static int launch_segs(const kqk_seg* segs, int nseg, hipStream_t st) {
 static int max_rows_per_launch(const kqk_seg* proto) {
     const int grid = plan_grid();
     kqk_seg t = *proto;
-    t.N = t.Ng = 1;
+    t.nparts = 1;
+    t.rows[0] = 1;
     int a, b2, c;
     const long fixed = kqk_segs_lds(&t, 1, grid, &a, &b2, &c) - (long)(t.K / 64) * 8;
     const long per_row = (long)(t.K / 64) * 8;
@@ -280,18 +287,41 @@ int kq_gemv_dev(int type, const void* w, const float* x, const float* add, float
     if ((uintptr_t)x & 15) return kq_fail("kq_gemv_dev: x must be 16-byte aligned");
     kqk_seg sg;
     memset(&sg, 0, sizeof sg);
-    sg.type = type; sg.K = K; sg.ngroups = 1; sg.x = x;
-    sg.N = sg.Ng = N;
+    sg.type = type; sg.K = K; sg.nparts = 1; sg.x = x;
     const int maxr = max_rows_per_launch(&sg);
     const int64_t rb = kq_row_bytes(type, K);
     for (int r0 = 0; r0 < N; r0 += maxr) {       /* one launch unless LDS runs out */
         const int n = N - r0 < maxr ? N - r0 : maxr;
         sg.w[0] = (const uint8_t*)w + (size_t)r0 * (size_t)rb;
-        sg.add = add ? add + r0 : NULL;
-        sg.y = y + r0;
-        sg.N = sg.Ng = n;
+        sg.add[0] = add ? add + r0 : NULL;
+        sg.y[0] = y + r0;
+        sg.rows[0] = n;
         if (launch_segs(&sg, 1, pick(stream))) return -1;
     }
+    return 0;
+}
+
+/* Consecutive single-group segments with the same type, K and x are merged
+ * into one launcher segment of up to KQK_LIST_MAX parts (while the list
+ * still fits the LDS): they are then one row space, swept and reduced
+ * together -- one pass of the batch loop instead of one per tensor.  Each
+ * row's arithmetic does not change. */
+static int try_merge(kqk_seg* h, int nh, const kq_segment* s, int grid) {
+    kqk_seg* prev = &h[nh - 1];
+    if (s->ngroups != 1 || prev->type != s->type || prev->K != s->K || prev->x != s->x ||
+        prev->x_stride != 0 || prev->nparts >= KQK_LIST_MAX)
+        return 0;
+    const kqk_seg keep = *prev;
+    const int p = prev->nparts;
+    prev->w[p] = s->w[0];
+    prev->y[p] = s->y;
+    prev->add[p] = s->add;
+    prev->rows[p] = s->rows_per_group;
+    prev->nparts = p + 1;
+    int a, b, c;
+    const long lds = kqk_segs_lds(h, nh, grid, &a, &b, &c);
+    if (lds > 0 && lds <= g_kq.lds_max) return 1;
+    *prev = keep;
     return 0;
 }
 
@@ -300,6 +330,8 @@ int kq_gemv_segments_dev(const kq_segment* segs, int nseg, kq_stream stream) {
     if (!segs || kq_ready()) return segs ? -1 : kq_fail("kq_gemv_segments_dev: NULL");
     kqk_seg h[KQ_MAX_SEGMENTS];
     memset(h, 0, sizeof h);
+    int nh = 0;
+    const int grid = plan_grid();
     for (int i = 0; i < nseg; i++) {
         const kq_segment* s = &segs[i];
         if (s->ngroups < 1 || s->ngroups > KQ_MAX_GROUPS)
@@ -310,15 +342,20 @@ int kq_gemv_segments_dev(const kq_segment* segs, int nseg, kq_stream stream) {
             return kq_fail("segment %d: x must be 16-byte aligned", i);
         if ((int64_t)s->rows_per_group * s->ngroups > 0x7fffffff)
             return kq_fail("segment %d: too many rows", i);
-        for (int g = 0; g < s->ngroups; g++) {
+        for (int g = 0; g < s->ngroups; g++)
             if (!s->w[g]) return kq_fail("segment %d: NULL weights for group %d", i, g);
-            h[i].w[g] = s->w[g];
+        if (nh > 0 && try_merge(h, nh, s, grid)) continue;
+        kqk_seg* t = &h[nh++];
+        for (int g = 0; g < s->ngroups; g++) {
+            t->w[g] = s->w[g];
+            t->y[g] = s->y + (size_t)g * s->rows_per_group;
+            t->add[g] = s->add ? s->add + (size_t)g * s->rows_per_group : NULL;
+            t->rows[g] = s->rows_per_group;
         }
-        h[i].type = s->type; h[i].K = s->K; h[i].Ng = s->rows_per_group;
-        h[i].ngroups = s->ngroups; h[i].N = s->rows_per_group * s->ngroups;
-        h[i].x = s->x; h[i].x_stride = s->x_stride; h[i].add = s->add; h[i].y = s->y;
+        t->type = s->type; t->K = s->K; t->nparts = s->ngroups;
+        t->x = s->x; t->x_stride = s->ngroups > 1 ? s->x_stride : 0;
     }
-    return launch_segs(h, nseg, pick(stream));
+    return launch_segs(h, nh, pick(stream));
 }
 
 int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,

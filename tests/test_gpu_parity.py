@@ -321,3 +321,39 @@ def test_segments_shared_x_across_types(port, wide):
     for i, (t, N) in enumerate(specs):
         check_close(dys[i].cpu().numpy(), port.gemv(t, ws[i], x, N, H),
                     f"shared x seg {i} {K.TYPE_NAMES[t]} wide={wide}")
+
+
+def test_segments_merged_same_input_parts(port):
+    """Same-input single-tensor segments are merged into one row space of up
+    to 4 parts of any sizes (then a new one starts); groups of 3 experts with
+    one x each run as parts too.  Every output matches its own launch."""
+    H = 768
+    x = synth.gaussian(synth.rng(700), H)
+    dx = dev(x)
+    sizes = [100, 37, 300, 64, 5, 129]
+    ws = [synth.tensor(12, n, H, 710 + i) for i, n in enumerate(sizes)]
+    dws = [dev(w) for w in ws]
+    dys = [torch.empty(n, dtype=torch.float32, device="cuda") for n in sizes]
+    add = synth.gaussian(synth.rng(701), sizes[2])
+    dadd = dev(add)
+    segs = [K.segment(12, H, n, [dws[i].data_ptr()], dx.data_ptr(), dys[i].data_ptr(),
+                      add_ptr=dadd.data_ptr() if i == 2 else None)
+            for i, n in enumerate(sizes)]
+    E, F = 3, 512
+    ex = [synth.tensor(14, F, H, 720 + e) for e in range(E)]
+    dex = [dev(t) for t in ex]
+    xe = np.stack([synth.gaussian(synth.rng(730 + e), H) for e in range(E)])
+    dxe = dev(xe.reshape(-1))
+    ye = torch.empty(E * F, dtype=torch.float32, device="cuda")
+    segs.append(K.segment(14, H, F, [t.data_ptr() for t in dex], dxe.data_ptr(), ye.data_ptr(),
+                          x_stride=H))
+    K.gemv_segments_dev(segs, stream=stream())
+    torch.cuda.synchronize()
+    for i, n in enumerate(sizes):
+        got = dys[i].cpu().numpy()
+        a = add if i == 2 else None
+        assert same_values(got, gpu_gemv(12, ws[i], x, n, H, add=a)), f"part {i}"
+        check_close(got, port.gemv(12, ws[i], x, n, H, add=a), f"merged part {i} ({n} rows)")
+    got = ye.cpu().numpy().reshape(E, F)
+    for e in range(E):
+        check_close(got[e], port.gemv(14, ex[e], xe[e], F, H), f"expert part {e}")
