@@ -128,6 +128,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--kernel-reps", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--skip-separate", action="store_true",
+                    help="do not time the 7-launch form (profiling runs: then every "
+                         "kq_segs_kernel<1, 1> dispatch is the dominant launch)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 5 copies of 64 MiB (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -205,21 +208,22 @@ def main() -> int:
     set_bytes = sum(algo_bytes(t, N, K) for _, t, N, K, _ in LAYER_27B)
     ms_per_step, enq_ms = timed(step, args.steps, args.warmup)
     gbs = set_bytes / (ms_per_step * 1e-3) / 1e9
-    sep_ms, sep_enq_ms = timed(step_separate, args.steps, args.warmup)
+    sep_ms, sep_enq_ms = (None, None) if args.skip_separate else \
+        timed(step_separate, args.steps, args.warmup)
 
-    # ---- per-launch durations (events around each launch, same stream)
+    # ---- per-launch durations: HIP events on the launch stream around
+    # kernel_reps back-to-back launches of one group (rotating copies)
     per_launch = {}
     for g, (gname, members) in enumerate(GROUPS):
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-               for _ in range(args.kernel_reps)]
         for i in range(4):
             launch_group(i % COPIES, g)
-        for i, (a, b) in enumerate(evs):
-            a.record(stream)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for i in range(args.kernel_reps):
             launch_group((i + 1) % COPIES, g)
-            b.record(stream)
+        b.record(stream)
         torch.cuda.synchronize()
-        us = float(np.mean([a.elapsed_time(b) for a, b in evs])) * 1e3
+        us = a.elapsed_time(b) * 1e3 / args.kernel_reps
         nbytes = sum(algo_bytes(spec[m][0], spec[m][1], spec[m][2]) for m in members)
         per_launch[gname] = {"us": round(us, 2), "bytes": nbytes,
                              "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1)}
@@ -259,10 +263,11 @@ def main() -> int:
         "us_per_layer_set": round(ms_per_step * 1e3, 2),
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "host_enqueue_us_per_step": round(enq_ms * 1e3, 1),
-        "separate_launches": {"launches_per_step": len(LAYER_27B),
-                              "us_per_layer_set": round(sep_ms * 1e3, 2),
-                              "GB/s": round(set_bytes / (sep_ms * 1e-3) / 1e9, 1),
-                              "host_enqueue_us_per_step": round(sep_enq_ms * 1e3, 1)},
+        "separate_launches": None if sep_ms is None else {
+            "launches_per_step": len(LAYER_27B),
+            "us_per_layer_set": round(sep_ms * 1e3, 2),
+            "GB/s": round(set_bytes / (sep_ms * 1e-3) / 1e9, 1),
+            "host_enqueue_us_per_step": round(sep_enq_ms * 1e3, 1)},
         "per_launch": per_launch,
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
