@@ -165,19 +165,22 @@ __device__ __forceinline__ double dpp_f64(double v) {
 // read a scaled x).  When some x falls outside (subnormal, or beyond 2^52),
 // the workgroup restages x unscaled and uses the convert-and-multiply path.
 constexpr int KSC = 64;
-constexpr uint32_t KSC_EMIN = 127 + 23 - KSC;    // smallest allowed biased exponent
-constexpr uint32_t KSC_EMAX = 127 + 116 - KSC;   // first disallowed biased exponent
+// window test on frexp exponents (|v| in [2^(e-1), 2^e)): allowed
+// e in [24 - KSC, 117 - KSC); frexp gives 0 for zero, inf and NaN, which are
+// allowed too.  out_of_window(v) = (e - (24 - KSC)) as unsigned >= KSC_SPAN.
+constexpr int KSC_ELO = 24 - KSC;
+constexpr uint32_t KSC_SPAN = 117 - 24;
 
 template <int TYPE> struct XGroup {
     static constexpr int G4 = TYPE == T_Q4K ? 8 : 4;            // float4 per group
     static constexpr bool SUMS = TypeInfo<TYPE>::XS_PER_CHUNK != 0;
 };
 
-// 1 when v is finite, nonzero and outside the scaled-mode window
-__device__ __forceinline__ uint32_t out_of_window(float v) {
-    const uint32_t e = (__float_as_uint(v) & 0x7fffffffu) >> 23;
-    const bool zero = (__float_as_uint(v) & 0x7fffffffu) == 0u;
-    return (!zero && e != 255u && (e < KSC_EMIN || e >= KSC_EMAX)) ? 1u : 0u;
+// (e - KSC_ELO) as unsigned: >= KSC_SPAN when v is finite, nonzero and
+// outside the scaled-mode window (v_frexp_exp_i32_f32 returns 0 for zero,
+// infinities and NaN)
+__device__ __forceinline__ uint32_t window_dist(float v) {
+    return (uint32_t)(__builtin_amdgcn_frexp_expf(v) - KSC_ELO);
 }
 
 // LDS slot (within one x) of float4 q of group gi, and the xs index (within
@@ -224,14 +227,14 @@ struct XStage {
         int slot0, xsi;
         group_place<TYPE>(gi, slot0, xsi);
         f32x4* dst = reinterpret_cast<f32x4*>(xl) + gx * NC * XPAD + slot0;
-        uint32_t bad = 0;
+        uint32_t dist = 0;
         float acc = 0.0f;
 #pragma unroll
         for (int q = 0; q < G4; q++) {
             const f32x4 w = v[q];
             acc = acc + w.x; acc = acc + w.y; acc = acc + w.z; acc = acc + w.w;
-            bad |= out_of_window(w.x) | out_of_window(w.y) | out_of_window(w.z) |
-                   out_of_window(w.w);
+            dist = max(max(dist, window_dist(w.x)), window_dist(w.y));
+            dist = max(max(dist, window_dist(w.z)), window_dist(w.w));
             f32x4 o = w;
             if (scale) {
                 o.x = ldexpf(w.x, KSC); o.y = ldexpf(w.y, KSC);
@@ -240,7 +243,7 @@ struct XStage {
             dst[q] = o;
         }
         if (XGroup<TYPE>::SUMS && sums) xs[gx * per + xsi] = acc;
-        return bad != 0;
+        return dist >= KSC_SPAN;
     }
 };
 
@@ -857,7 +860,8 @@ __device__ __forceinline__ void sweep(const Walk<TYPE, PM>& W, int nch, int u, i
 }
 
 template <int TYPE, int DEPTH, int PM>
-__device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st, uint8_t* smem) {
+__device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st, uint8_t* smem,
+                            bool last_seg) {
     using TI = TypeInfo<TYPE>;
     using C = Chunk<TYPE>;
     const int tid = threadIdx.x, T = A.threads, lane = tid & 63, wave = tid >> 6;
@@ -957,28 +961,22 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
         sweep<TYPE, DEPTH, PM, false>(W, nch, u, next, xl, xs, terms, f, f6, base, cx, buf);
     __syncthreads();
 
-    // Row reduction: L lanes per row (L = 8..64, as many as T allows), lane
-    // p sums terms p, p+L, ... in two interleaved partial sums, then a
-    // butterfly over the L lanes.  The order depends only on NC and L.
-    int L = 8;
-    while (L < 64 && 2 * L * R <= T) L *= 2;
-    for (int task = tid; task < R * L; task += T) {
-        const int rho = task / L, p = task & (L - 1);
+    // Row reduction, in one fixed order that depends on NC only (so the
+    // result does not depend on the grid, the workgroup size or how rows
+    // are batched, and the multi-stream kernel reproduces it): 8 lanes per
+    // row, lane p sums the terms of chunks p, p+8, p+16, ... in increasing
+    // order (binary64, from 0), then
+    //   y = ((P0 + P1) + (P2 + P3)) + ((P4 + P5) + (P6 + P7))
+    // by a butterfly (each addition is commutative, so every lane of the
+    // group ends with the same bits).
+    for (int task = tid; task < R * 8; task += T) {
+        const int rho = task >> 3, p = task & 7;
         const double* tr = terms + rho * NC;
-        double s0 = 0.0, s1 = 0.0;
-        int i = p;
-        for (; i + L < NC; i += 2 * L) {
-            s0 = s0 + tr[i];
-            s1 = s1 + tr[i + L];
-        }
-        if (i < NC) s0 = s0 + tr[i];
-        double s = s0 + s1;
+        double s = 0.0;
+        for (int i = p; i < NC; i += 8) s = s + tr[i];
         s = s + dpp_f64<0xB1>(s);    // quad_perm [1,0,3,2]: lane ^ 1
         s = s + dpp_f64<0x4E>(s);    // quad_perm [2,3,0,1]: lane ^ 2
         s = s + dpp_f64<0x141>(s);   // row_half_mirror: lane i <-> 7 - i (8 lanes)
-        if (L >= 16) s = s + dpp_f64<0x140>(s);   // row_mirror (16 lanes)
-        if (L >= 32) s = s + __shfl_xor(s, 16, 64);
-        if (L >= 64) s = s + __shfl_xor(s, 32, 64);
         if (p == 0) {
             uint32_t rg;
             const uint32_t g = part_of<PM>(S, (uint32_t)(b + G * rho), rg);
@@ -999,9 +997,11 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
             y[rg] = v;
         }
     }
-    // Wait for the y stores here: a store keeps its data registers busy
-    // until it completes, and the next segment's first writes to those
-    // registers would otherwise wait for every outstanding load -- its x.
+    if (last_seg) return;
+    // Before the next segment: wait for the y stores here (a store keeps its
+    // data registers busy until it completes, and the next segment's first
+    // writes to those registers would otherwise wait for every outstanding
+    // load -- its x), and let every wave finish with the LDS.
     __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
     __syncthreads();
 }
@@ -1012,42 +1012,50 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
 // register allocation is not constrained by the others.
 constexpr int TB_Q4K = 1, TB_Q6K = 2, TB_Q2K = 4, TB_NIB = 8, TB_ALL = 15;
 
-template <int DEPTH, int TYPES>
+// MULTI = false: the launch has exactly one segment (no segment loop, so
+// no state flows between segments and the compiler's wait analysis stays
+// exact; most launches are this).
+template <int DEPTH, int TYPES, bool MULTI>
 __global__ __launch_bounds__(1024) void kq_segs_kernel(SegsArg A) {
     extern __shared__ __align__(16) uint8_t smem[];
     asm volatile("" ::"s"(A.nseg), "s"(A.threads), "s"(A.grid), "s"(A.xs_off),
                  "s"(A.terms_off), "s"(A.scr_off));
     prefetch_seg(A.s[0]);
+    const int nseg = MULTI ? A.nseg : 1;
     // batch counters of every segment (the first segment that runs stages
     // x, and its barrier orders these writes before any batch is taken)
-    if (threadIdx.x < (unsigned)A.nseg)
+    if (threadIdx.x < (unsigned)nseg)
         reinterpret_cast<int*>(smem + A.scr_off)[threadIdx.x] = 64 * DEPTH * (A.threads >> 6);
     Staged st = {nullptr, 0, -1, 0, 0, 0, false};
     // a single-type instantiation does not read the segment types (the host
     // launches it only for segment lists of that type)
     constexpr bool SINGLE = TYPES == TB_Q4K || TYPES == TB_Q6K || TYPES == TB_Q2K || TYPES == TB_NIB;
-    for (int i = 0; i < A.nseg; i++) {
+    for (int i = 0; i < nseg; i++) {
         const Seg& S = A.s[i];
         if (i) prefetch_seg(S);
         const int pm = S.nparts == 1 ? PM_ONE : S.nparts <= LIST_MAX ? PM_LIST : PM_EQUAL;
-#define KQ_RUN(T_)                                                             \
-        if (pm == PM_ONE) run_segment<T_, DEPTH, PM_ONE>(S, A, i, st, smem);   \
-        else if (pm == PM_LIST) run_segment<T_, DEPTH, PM_LIST>(S, A, i, st, smem); \
-        else run_segment<T_, DEPTH, PM_EQUAL>(S, A, i, st, smem);
+        const bool last = i == nseg - 1;
+#define KQ_RUN(T_)                                                                   \
+        if (pm == PM_ONE) run_segment<T_, DEPTH, PM_ONE>(S, A, i, st, smem, last);   \
+        else if (pm == PM_LIST) run_segment<T_, DEPTH, PM_LIST>(S, A, i, st, smem, last); \
+        else run_segment<T_, DEPTH, PM_EQUAL>(S, A, i, st, smem, last);
         if (SINGLE) {
             constexpr int TY = TYPES == TB_Q4K ? T_Q4K : TYPES == TB_Q6K ? T_Q6K
                              : TYPES == TB_Q2K ? T_Q2K : T_NIB;
             KQ_RUN(TY)
-            continue;
-        }
-        switch (S.type) {
-        case T_Q4K: if (TYPES & TB_Q4K) { KQ_RUN(T_Q4K) } break;
-        case T_Q6K: if (TYPES & TB_Q6K) { KQ_RUN(T_Q6K) } break;
-        case T_Q2K: if (TYPES & TB_Q2K) { KQ_RUN(T_Q2K) } break;
-        case T_NIB: if (TYPES & TB_NIB) { KQ_RUN(T_NIB) } break;
-        default: break;
+        } else {
+            switch (S.type) {
+            case T_Q4K: if (TYPES & TB_Q4K) { KQ_RUN(T_Q4K) } break;
+            case T_Q6K: if (TYPES & TB_Q6K) { KQ_RUN(T_Q6K) } break;
+            case T_Q2K: if (TYPES & TB_Q2K) { KQ_RUN(T_Q2K) } break;
+            case T_NIB: if (TYPES & TB_NIB) { KQ_RUN(T_NIB) } break;
+            default: break;
+            }
         }
 #undef KQ_RUN
+        // leave straight from the last segment: its y stores may still be
+        // in flight, and only the other paths return to the loop head
+        if (last) break;
     }
 }
 
@@ -1203,21 +1211,25 @@ long kqk_segs_lds(const kqk_seg* segs, int nseg, int grid, int* xs_off, int* ter
     return xl + xsb + tb + SCR_BYTES;
 }
 
-// Every instantiation, indexed by [depth - 1][type set].
-#define KQ_SEGS_ROW(D)                                                                  \
-    {&kq_segs_kernel<D, TB_Q4K>, &kq_segs_kernel<D, TB_Q6K>, &kq_segs_kernel<D, TB_Q2K>, \
-     &kq_segs_kernel<D, TB_NIB>, &kq_segs_kernel<D, TB_ALL>}
+// Every instantiation, indexed by [multi][depth - 1][type set].
+#define KQ_SEGS_ROW(D, M)                                                       \
+    {&kq_segs_kernel<D, TB_Q4K, M>, &kq_segs_kernel<D, TB_Q6K, M>,              \
+     &kq_segs_kernel<D, TB_Q2K, M>, &kq_segs_kernel<D, TB_NIB, M>,              \
+     &kq_segs_kernel<D, TB_ALL, M>}
 typedef void (*segs_fn)(SegsArg);
-static const segs_fn k_segs[2][5] = {KQ_SEGS_ROW(1), KQ_SEGS_ROW(2)};
+static const segs_fn k_segs[2][2][5] = {{KQ_SEGS_ROW(1, false), KQ_SEGS_ROW(2, false)},
+                                        {KQ_SEGS_ROW(1, true), KQ_SEGS_ROW(2, true)}};
 #undef KQ_SEGS_ROW
 
 int kqk_set_max_lds(int bytes) {
-    for (int d = 0; d < 2; d++)
-        for (int t = 0; t < 5; t++) {
-            const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_segs[d][t]),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-            if (e != hipSuccess) return (int)e;
-        }
+    for (int m = 0; m < 2; m++)
+        for (int d = 0; d < 2; d++)
+            for (int t = 0; t < 5; t++) {
+                const hipError_t e =
+                    hipFuncSetAttribute(reinterpret_cast<const void*>(k_segs[m][d][t]),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+                if (e != hipSuccess) return (int)e;
+            }
     return 0;
 }
 
@@ -1263,7 +1275,8 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
     }
     const int t = set == TB_Q4K ? 0 : set == TB_Q6K ? 1 : set == TB_Q2K ? 2 : set == TB_NIB ? 3 : 4;
     if (t == 4) depth = 1;   // the all-types kernel fits 128 VGPRs at depth 1 only
-    hipLaunchKernelGGL(k_segs[depth - 1][t], dim3(grid), dim3(threads), (size_t)lds_bytes, st, A);
+    hipLaunchKernelGGL(k_segs[nseg > 1][depth - 1][t], dim3(grid), dim3(threads),
+                       (size_t)lds_bytes, st, A);
     return (int)hipGetLastError();
 }
 

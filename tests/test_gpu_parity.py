@@ -288,15 +288,22 @@ def test_gemv_x_window_edges(port, qtype, case):
                 f"{K.TYPE_NAMES[qtype]} window {case}")
 
 
+@pytest.mark.parametrize("scale", [2.0 ** -45, 2.0 ** -135])
 @pytest.mark.parametrize("qtype", [12, 10, 42])
-def test_gemv_x_all_below_window(port, qtype):
-    """Every x near 2^-45: scaled products would fall below the binary32
-    normal range and lose bits, so only the unscaled fallback matches."""
+def test_gemv_x_all_below_window(port, qtype, scale):
+    """Every x near 2^-45 (normal) or 2^-135 (subnormal): scaled products
+    would fall below the binary32 normal range and lose bits or vanish, so
+    only the unscaled fallback matches."""
     N, Kd = 64, 1024
     w = synth.tensor(qtype, N, Kd, 520 + qtype)
-    x = (synth.gaussian(synth.rng(521), Kd) * np.float32(2.0 ** -45)).astype(np.float32)
-    check_close(gpu_gemv(qtype, w, x, N, Kd), port.gemv(qtype, w, x, N, Kd),
-                f"{K.TYPE_NAMES[qtype]} x ~ 2^-45")
+    x = (synth.gaussian(synth.rng(521), Kd).astype(np.float64) * scale).astype(np.float32)
+    assert np.count_nonzero(x) > Kd // 2
+    got, want = gpu_gemv(qtype, w, x, N, Kd), port.gemv(qtype, w, x, N, Kd)
+    check_close(got, want, f"{K.TYPE_NAMES[qtype]} x ~ {scale:.1e}")
+    # |y| is far below the 1e-6 floor of the relative bound, which then
+    # cannot tell a wrong result; the binary64 sums of these few binary32
+    # terms are exact, so the results must be bit-identical
+    assert same_values(got, want), f"{K.TYPE_NAMES[qtype]} x ~ {scale:.1e} not bit-identical"
 
 
 @pytest.mark.parametrize("wide", [False, True])
