@@ -19,7 +19,7 @@ layer's weights (860 MB) are rotated so no step finds its weights in the
 
 value = algorithmic bytes of the layer set / measured time per step, with
 algorithmic bytes per matvec = N*(K/256)*block_bytes + 4K + 4N.
-roofline: the dominant launch ([gate, up], kernel kq_segs_kernel<1, 1>)
+roofline: the dominant launch ([gate, up], kernel kq_segs_kernel<1, 1, false>)
 timed per launch with HIP events on the stream it runs on; traffic from
 profiles/traffic.json (rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated).
 cpu_baseline: the reference's own scalar routines (oracle/_ref) -- or the
@@ -67,7 +67,7 @@ GROUPS = [
     ("ffn_down", ["ffn_down"]),
 ]
 DOMINANT = "ffn_gate_up"
-DOMINANT_KERNEL = "kq_segs_kernel<1, 1>"
+DOMINANT_KERNEL = "kq_segs_kernel<1, 1, false>"
 COPIES = 4
 
 
@@ -130,7 +130,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-separate", action="store_true",
                     help="do not time the 7-launch form (profiling runs: then every "
-                         "kq_segs_kernel<1, 1> dispatch is the dominant launch)")
+                         "kq_segs_kernel<1, 1, false> dispatch is the dominant launch)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 5 copies of 64 MiB (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
