@@ -378,7 +378,9 @@ __device__ __forceinline__ uint32_t dw_of(const uint4& v, int k) {
 
 // Q4_K chunk j of a block: sub-blocks 2j (low nibbles) and 2j+1 (high).
 // SC: x is scaled by 2^k and f = 2^(149-k) (see bmul); otherwise f = 1.
-template <bool SC>
+// LOWREG: a scheduling fence every few steps keeps the x reads from being
+// hoisted all at once (the multi-stream kernel's register budget).
+template <bool SC, bool LOWREG = false>
 __device__ __forceinline__ double term_q4k(const RawQ4& r, int j, const float4* xc,
                                            float xs1, float xs2, float f) {
     const float d = f16_bits_to_f32(r.hd.x & 0xffffu);
@@ -417,6 +419,7 @@ __device__ __forceinline__ double term_q4k(const RawQ4& r, int j, const float4* 
             a1 = a1 + l1; a2 = a2 + h1;
             a1 = a1 + l2; a2 = a2 + h2;
             a1 = a1 + l3; a2 = a2 + h3;
+            if (LOWREG && (k & 1)) __builtin_amdgcn_sched_barrier(0);
         }
     } else {
         // exact convert path for x outside the window (rare): a rolled loop,
@@ -450,6 +453,7 @@ __device__ __forceinline__ float i8f(uint32_t v, int e) {
 
 // Q6_K chunk (half h, sub is): four 16-weight sums a_t, t = 0..3.
 // f6 = 2^(-2-k) when x is scaled by 2^k (k = 0: unscaled).
+template <bool LOWREG = false>
 __device__ __forceinline__ double term_q6k(const RawQ6& r, int u, const float4* xc, double f6) {
     const int is = u & 1;
     const uint32_t sh = r.sh;
@@ -473,6 +477,7 @@ __device__ __forceinline__ double term_q6k(const RawQ6& r, int u, const float4* 
             a[t] = a[t] + i8f(y[t], 2) * xv.z;
             a[t] = a[t] + i8f(y[t], 3) * xv.w;
         }
+        if (LOWREG) __builtin_amdgcn_sched_barrier(0);
     }
     // scales s[8h + is + 2t] sit at bytes is + 2t of the realigned pair
     const uint32_t S0 = __builtin_amdgcn_alignbit(r.s[1], r.s[0], sh);
@@ -489,7 +494,7 @@ __device__ __forceinline__ double term_q6k(const RawQ6& r, int u, const float4* 
 }
 
 // Q2_K chunk (half s, 16-sub h): groups j = 0..3, q = (qs >> 2j) & 3.
-template <bool SC>
+template <bool SC, bool LOWREG = false>
 __device__ __forceinline__ double term_q2k(const RawQ2& r, int u, const float4* xc,
                                            const float4 xs4, float f) {
     const int h = u & 1;
@@ -521,6 +526,7 @@ __device__ __forceinline__ double term_q2k(const RawQ2& r, int u, const float4* 
             }
             const float t = (dl * (inv * f)) * qx - ml * sx[j];
             acc = acc + (double)t;
+            if (LOWREG) __builtin_amdgcn_sched_barrier(0);
         }
     } else {
         // exact convert path (x outside the window): rolled over j, with
@@ -555,7 +561,7 @@ __device__ __forceinline__ double term_q2k(const RawQ2& r, int u, const float4* 
 
 // type-42 chunk u: 64 consecutive weights = groups 4u..4u+3; group g's
 // 16 values are the low (g even) or high (g odd) nibbles of 16 bytes.
-template <bool SC>
+template <bool SC, bool LOWREG = false>
 __device__ __forceinline__ double term_nib(const RawNB& r, const float4* xc, const float4 xs4,
                                            float f) {
     const float d = f16_bits_to_f32(r.dd & 0xffffu);
@@ -585,6 +591,7 @@ __device__ __forceinline__ double term_nib(const RawNB& r, const float4* xc, con
             }
             const float t = (dl * (inv * f)) * qx - ml * sx[g];
             acc = acc + (double)t;
+            if (LOWREG) __builtin_amdgcn_sched_barrier(0);
         }
     } else {
         // exact convert path (x outside the window): rolled over g, with the
@@ -631,11 +638,11 @@ template <> struct Chunk<T_Q4K> {
     static __device__ __forceinline__ void drain(const Raw& r) {
         asm volatile("" ::"v"(r.hd.x), "v"(r.qa.x), "v"(r.qb.x));
     }
-    template <bool SC>
+    template <bool SC, bool LOWREG = false>
     static __device__ __forceinline__ double term(const Raw& r, int u, const float4* xc,
                                                   const float* xs, int c, float f, double) {
         const float2 s = reinterpret_cast<const float2*>(xs)[c];
-        return term_q4k<SC>(r, u, xc, s.x, s.y, f);
+        return term_q4k<SC, LOWREG>(r, u, xc, s.x, s.y, f);
     }
 };
 template <> struct Chunk<T_Q6K> {
@@ -645,10 +652,10 @@ template <> struct Chunk<T_Q6K> {
         asm volatile("" ::"v"(r.l[0]), "v"(r.l[4]), "v"(r.h[0]), "v"(r.h[4]), "v"(r.q[0]),
                      "v"(r.q[4]), "v"(r.s[0]), "v"(r.s[1]), "v"(r.s[2]), "v"(r.d));
     }
-    template <bool SC>
+    template <bool SC, bool LOWREG = false>
     static __device__ __forceinline__ double term(const Raw& r, int u, const float4* xc,
                                                   const float*, int, float, double f6) {
-        return term_q6k(r, u, xc, f6);
+        return term_q6k<LOWREG>(r, u, xc, f6);
     }
 };
 template <> struct Chunk<T_Q2K> {
@@ -657,10 +664,10 @@ template <> struct Chunk<T_Q2K> {
     static __device__ __forceinline__ void drain(const Raw& r) {
         asm volatile("" ::"v"(r.q.x), "v"(r.s.x), "v"(r.dd));
     }
-    template <bool SC>
+    template <bool SC, bool LOWREG = false>
     static __device__ __forceinline__ double term(const Raw& r, int u, const float4* xc,
                                                   const float* xs, int c, float f, double) {
-        return term_q2k<SC>(r, u, xc, reinterpret_cast<const float4*>(xs)[c], f);
+        return term_q2k<SC, LOWREG>(r, u, xc, reinterpret_cast<const float4*>(xs)[c], f);
     }
 };
 template <> struct Chunk<T_NIB> {
@@ -669,10 +676,10 @@ template <> struct Chunk<T_NIB> {
     static __device__ __forceinline__ void drain(const Raw& r) {
         asm volatile("" ::"v"(r.qa.x), "v"(r.qb.x), "v"(r.s), "v"(r.dd));
     }
-    template <bool SC>
+    template <bool SC, bool LOWREG = false>
     static __device__ __forceinline__ double term(const Raw& r, int, const float4* xc,
                                                   const float* xs, int c, float f, double) {
-        return term_nib<SC>(r, xc, reinterpret_cast<const float4*>(xs)[c], f);
+        return term_nib<SC, LOWREG>(r, xc, reinterpret_cast<const float4*>(xs)[c], f);
     }
 };
 
@@ -1059,6 +1066,225 @@ __global__ __launch_bounds__(1024) void kq_segs_kernel(SegsArg A) {
     }
 }
 
+// ------------------------------------------------------------ multi-stream
+// y_s = W . x_s for B streams (STRATUM_MULTISEQ) with one pass over W.
+// Each stream's result is bit-identical to the single-stream kernel's: the
+// same chunk terms (same arithmetic, same x scaling rule) and the same
+// reduction (8 partial sums over chunks p, p+8, ... in order, combined
+// pairwise).  Here the partials live in registers: lane (row, p, stream
+// group) walks chunks p, p+8, p+16, ... of its row and accumulates BS
+// streams, so a wave covers 8 consecutive chunks (2 super-blocks) of 8 rows
+// and the 8 rows read the same x values (LDS broadcast).
+//  * prologue: the per-sub-block sums of every stream (for the min terms)
+//    and the window vote over all x, once;
+//  * x is staged tile by tile (8 chunks = 512 values of every stream,
+//    double-buffered, a few float4 per lane) while the next tile's weights
+//    are already in flight.
+struct MultixArg {
+    const uint8_t* w;
+    const float* xs;      // B x K, stream s at xs + s*K
+    float* ys;            // B x N
+    int B, N, K, NG;      // NG stream groups of BS streams
+    int threads, grid;
+    int xl_bytes;         // LDS bytes of one x tile buffer (all streams)
+    int sums_bytes;       // LDS bytes of the sums of all streams
+};
+
+// LDS slot (chunk-major, XPAD per chunk) of the float4 at x position 4q
+// (q = 0..127) of a 512-value tile
+template <bool LINEAR>
+__device__ __forceinline__ int tile_slot(int q) {
+    const int pos = 4 * q;
+    if (LINEAR) return (pos >> 6) * XPAD + ((pos >> 2) & 15);
+    const int bi = pos >> 8, pp = pos & 255;
+    const int h = pp >> 7, t = (pp >> 5) & 3, is = (pp >> 4) & 1, qq = (pp >> 2) & 3;
+    return (4 * bi + 2 * h + is) * XPAD + 4 * t + qq;
+}
+
+template <int TYPE, int BS>
+__global__ __launch_bounds__(512) void kq_multix_kernel(MultixArg A) {
+    using TI = TypeInfo<TYPE>;
+    using C = Chunk<TYPE>;
+    constexpr int G4 = XGroup<TYPE>::G4;
+    constexpr bool SCTYPE = TYPE != T_Q6K;
+    constexpr int XPT = 4;                        // tile float4 per lane per round
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, T = A.threads, lane = tid & 63, wave = tid >> 6;
+    const int b = blockIdx.x, G = A.grid;
+    const int K = A.K, NC = K >> 6, N = A.N, B = A.B;
+    const int R = N > b ? (N - b + G - 1) / G : 0;
+    if (R == 0) return;                         // uniform over the workgroup
+    const int steps = (NC + 7) >> 3;
+    const size_t rbytes = (size_t)(K >> 8) * TI::BB;
+
+    // LDS: two x tile buffers [B][8 * XPAD] float4, the sums of all streams
+    // [B][K / (4 G4)], per-wave flags
+    float4* xt0 = reinterpret_cast<float4*>(smem);
+    float4* xt1 = reinterpret_cast<float4*>(smem + A.xl_bytes);
+    float* sums = reinterpret_cast<float*>(smem + 2 * A.xl_bytes);
+    int* flags = reinterpret_cast<int*>(smem + 2 * A.xl_bytes + A.sums_bytes);
+    const int per = K / (4 * G4);               // sum groups per stream
+
+    // lane role: p = chunk phase, g = stream group, rl = row of the pass.
+    // The workgroup's R rows go in `passes` passes of up to RP rows (each
+    // pass sweeps K once; the weights of every row are read once).
+    const int p = tid & 7;
+    const int g = (tid >> 3) % A.NG;
+    const int rl = (tid >> 3) / A.NG;
+    const int lanes_rows = T / (8 * A.NG);
+    const int passes = (R + lanes_rows - 1) / lanes_rows;
+    const int RP = (R + passes - 1) / passes;
+    const int u = p & 3;
+    const int s0 = g * BS;
+
+    // prologue: the sums of every stream and the window vote over all x
+    uint32_t dist = 0;
+    for (int q = tid; q < B * per; q += T) {
+        const int sidx = q / per, gi = q - sidx * per;
+        const f32x4* src = reinterpret_cast<const f32x4*>(A.xs + (size_t)sidx * K) + (size_t)gi * G4;
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < G4; k++) {
+            const f32x4 w = src[k];
+            acc = acc + w.x; acc = acc + w.y; acc = acc + w.z; acc = acc + w.w;
+            dist = max(max(dist, window_dist(w.x)), window_dist(w.y));
+            dist = max(max(dist, window_dist(w.z)), window_dist(w.w));
+        }
+        if (XGroup<TYPE>::SUMS) {
+            int slot0, xsi;
+            group_place<TYPE>(gi, slot0, xsi);
+            sums[sidx * per + xsi] = acc;
+        }
+    }
+    const bool wave_bad = __ballot(dist >= KSC_SPAN) != 0ull;
+    if (lane == 0) flags[wave] = wave_bad;
+    __syncthreads();
+    int any = 0;
+    for (int i = 0; i < (T >> 6); i++) any |= flags[i];
+    const bool sc = SCTYPE && !any;             // the same in every workgroup
+
+    // tile staging by float4 (lane t takes float4 t, t + T, ...)
+    const int tq = B * 128;                     // float4 per tile
+    auto tload = [&](int tile, int r, f32x4* v) {
+#pragma unroll
+        for (int k = 0; k < XPT; k++) {
+            const int q = min(tid + (r * XPT + k) * T, tq - 1);
+            const int sidx = q >> 7;
+            // positions past K (a last tile of fewer than 8 chunks) read the
+            // stream's last float4 instead: those slots are never used
+            const int pos = min(512 * tile + 4 * (q & 127), K - 4);
+            v[k] = *reinterpret_cast<const f32x4*>(A.xs + (size_t)sidx * K + pos);
+        }
+    };
+    auto tstore = [&](int r, const f32x4* v, float4* xt) {
+#pragma unroll
+        for (int k = 0; k < XPT; k++) {
+            const int q = tid + (r * XPT + k) * T;
+            if (q < tq) {
+                f32x4 o = v[k];
+                if (sc) {
+                    o.x = ldexpf(o.x, KSC); o.y = ldexpf(o.y, KSC);
+                    o.z = ldexpf(o.z, KSC); o.w = ldexpf(o.w, KSC);
+                }
+                reinterpret_cast<f32x4*>(xt)[(q >> 7) * 8 * XPAD + tile_slot<TI::LINEAR>(q & 127)] = o;
+            }
+        }
+    };
+    const int rounds = (tq + XPT * T - 1) / (XPT * T);
+    const float f = ldexpf(1.0f, 149 - KSC);
+    const double f6 = ldexp(0.25, sc ? -KSC : 0);
+    f32x4 xv[XPT];
+
+    for (int pass = 0; pass < passes; pass++) {
+        const int rho = pass * RP + rl;
+        const bool active = rl < RP && rho < R;
+        const int row = b + G * min(rho, R - 1);
+        const wptr wrow = to_global(A.w) + (size_t)row * rbytes;
+        typename C::Raw cur = C::load(wrow + (size_t)(min(p, NC - 1) >> 2) * TI::BB, u);
+        for (int r = 0; r < rounds; r++) {
+            tload(0, r, xv);
+            tstore(r, xv, xt0);
+        }
+        __syncthreads();
+
+        double part[BS];
+#pragma unroll
+        for (int s = 0; s < BS; s++) part[s] = 0.0;
+
+        for (int i = 0; i < steps; i++) {
+            float4* xc0 = (i & 1) ? xt1 : xt0;
+            float4* xn = (i & 1) ? xt0 : xt1;
+            const bool more = i + 1 < steps;
+            if (more) tload(i + 1, 0, xv);      // next tile's x, then its weights
+            const int cn = min(8 * (i + 1) + p, NC - 1);
+            const typename C::Raw nxt = C::load(wrow + (size_t)(cn >> 2) * TI::BB, u);
+            const int c = 8 * i + p;
+            if (active && c < NC) {
+                // one stream at a time (a scheduling fence between streams
+                // keeps the compiler from interleaving them)
+                if (sc) {
+#pragma unroll
+                    for (int s = 0; s < BS; s++) {
+                        if (s0 + s < B) {
+                            const float4* xc = xc0 + (s0 + s) * 8 * XPAD + p * XPAD;
+                            const float* xs = sums + (s0 + s) * per;
+                            part[s] = part[s] + C::template term<true, true>(cur, u, xc, xs, c, f, f6);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                } else {
+#pragma unroll
+                    for (int s = 0; s < BS; s++) {
+                        if (s0 + s < B) {
+                            const float4* xc = xc0 + (s0 + s) * 8 * XPAD + p * XPAD;
+                            const float* xs = sums + (s0 + s) * per;
+                            part[s] = part[s] + C::template term<false, true>(cur, u, xc, xs, c, 1.0f, f6);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+            }
+            cur = nxt;
+            if (more) {
+                tstore(0, xv, xn);
+                for (int r = 1; r < rounds; r++) {
+                    tload(i + 1, r, xv);
+                    tstore(r, xv, xn);
+                }
+            }
+            __syncthreads();                    // next tile written, this tile's reads done
+        }
+        C::drain(cur);
+
+        // ((P0 + P1) + (P2 + P3)) + ((P4 + P5) + (P6 + P7)) per stream, as
+        // the single-stream reduction
+#pragma unroll
+        for (int s = 0; s < BS; s++) {
+            double v = part[s];
+            v = v + dpp_f64<0xB1>(v);
+            v = v + dpp_f64<0x4E>(v);
+            v = v + dpp_f64<0x141>(v);
+            part[s] = v;
+        }
+        if (active && p == 0) {
+#pragma unroll
+            for (int s = 0; s < BS; s++)
+                if (s0 + s < B) A.ys[(size_t)(s0 + s) * N + row] = (float)part[s];
+        }
+    }
+}
+
+template <int TYPE>
+int launch_multix_t(const MultixArg& a, int bs, long lds, hipStream_t st) {
+    switch (bs) {
+    case 1: hipLaunchKernelGGL((kq_multix_kernel<TYPE, 1>), dim3(a.grid), dim3(a.threads), (size_t)lds, st, a); break;
+    case 2: hipLaunchKernelGGL((kq_multix_kernel<TYPE, 2>), dim3(a.grid), dim3(a.threads), (size_t)lds, st, a); break;
+    case 4: hipLaunchKernelGGL((kq_multix_kernel<TYPE, 4>), dim3(a.grid), dim3(a.threads), (size_t)lds, st, a); break;
+    default: hipLaunchKernelGGL((kq_multix_kernel<TYPE, 8>), dim3(a.grid), dim3(a.threads), (size_t)lds, st, a); break;
+    }
+    return (int)hipGetLastError();
+}
+
 // --------------------------------------------------------------- dequant
 // Bit-exact dequantization, one lane per 64-weight chunk (64 floats out).
 template <int TYPE>
@@ -1278,6 +1504,67 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
     hipLaunchKernelGGL(k_segs[nseg > 1][depth - 1][t], dim3(grid), dim3(threads),
                        (size_t)lds_bytes, st, A);
     return (int)hipGetLastError();
+}
+
+// Multi-stream launch plan (B <= 16 per launch): BS = streams per lane
+// (the next power of two >= B, at most 8), NG = ceil(B / BS) lane groups
+// per row; a workgroup takes up to 512 lanes, 8 * NG per row in flight, and
+// goes over its rows in as few passes as that allows.  Returns the LDS
+// bytes, or -1.
+long kqk_multix_plan(int type, int B, int N, int K, int grid, int* threads, int* bs,
+                     int* xl_bytes, int* sums_bytes) {
+    const int xpc = xs_per_chunk(type);
+    if (xpc < 0 || B < 1 || B > 16 || N < 1 || K <= 0 || (K & 255) || grid < 1) return -1;
+    const int BS = B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8;
+    const int NG = (B + BS - 1) / BS;
+    const long R = (N + grid - 1) / grid;
+    long rows = 512 / (8 * NG);                 // rows in flight per pass
+    const long passes = (R + rows - 1) / rows;
+    rows = (R + passes - 1) / passes;
+    const long lanes = 8 * rows * NG;
+    *threads = (int)((lanes + 63) / 64 * 64);
+    *bs = BS;
+    *xl_bytes = B * 8 * XPAD * 16;
+    *sums_bytes = (int)(((long)B * (K / 64) * xpc * 4 + 15) & ~15L);
+    return 2L * *xl_bytes + *sums_bytes + 64;
+}
+
+int kqk_multix_set_max_lds(int bytes) {
+#define KQ_MX_ATTR(T_)                                                                    \
+    {&kq_multix_kernel<T_, 1>, &kq_multix_kernel<T_, 2>, &kq_multix_kernel<T_, 4>,      \
+     &kq_multix_kernel<T_, 8>}
+    typedef void (*mx_fn)(MultixArg);
+    const mx_fn fns[4][4] = {KQ_MX_ATTR(T_Q4K), KQ_MX_ATTR(T_Q6K), KQ_MX_ATTR(T_Q2K),
+                             KQ_MX_ATTR(T_NIB)};
+#undef KQ_MX_ATTR
+    for (int t = 0; t < 4; t++)
+        for (int i = 0; i < 4; i++) {
+            const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fns[t][i]),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+            if (e != hipSuccess) return (int)e;
+        }
+    return 0;
+}
+
+// B streams (xs: B x K contiguous, ys: B x N) in one pass over the weights.
+int kqk_launch_multix(int type, const void* w, const float* xs, float* ys, int B, int N, int K,
+                      int grid, hipStream_t st) {
+    int threads = 0, bs = 0, xlb = 0, smb = 0;
+    const long lds = kqk_multix_plan(type, B, N, K, grid, &threads, &bs, &xlb, &smb);
+    if (lds < 0) return (int)hipErrorInvalidValue;
+    MultixArg a;
+    a.w = static_cast<const uint8_t*>(w);
+    a.xs = xs;
+    a.ys = ys;
+    a.B = B; a.N = N; a.K = K; a.NG = (B + bs - 1) / bs;
+    a.threads = threads; a.grid = grid; a.xl_bytes = xlb; a.sums_bytes = smb;
+    switch (type) {
+    case T_Q4K: return launch_multix_t<T_Q4K>(a, bs, lds, st);
+    case T_Q6K: return launch_multix_t<T_Q6K>(a, bs, lds, st);
+    case T_Q2K: return launch_multix_t<T_Q2K>(a, bs, lds, st);
+    case T_NIB: return launch_multix_t<T_NIB>(a, bs, lds, st);
+    default: return (int)hipErrorInvalidValue;
+    }
 }
 
 int kqk_launch_dequant(int type, const void* w, float* y, long nblocks, hipStream_t st) {

@@ -39,6 +39,11 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
                     long lds_bytes, int xs_off, int terms_off, int scr_off, hipStream_t st);
 int kqk_launch_dequant(int type, const void* w, float* y, long nblocks, hipStream_t st);
 int kqk_set_max_lds(int bytes);
+long kqk_multix_plan(int type, int B, int N, int K, int grid, int* threads, int* bs,
+                     int* xl_bytes, int* sums_bytes);
+int kqk_launch_multix(int type, const void* w, const float* xs, float* ys, int B, int N, int K,
+                      int grid, hipStream_t st);
+int kqk_multix_set_max_lds(int bytes);
 
 #define KQ_MAX_REGIONS 16
 
@@ -114,7 +119,8 @@ static int kq_ready(void) {
     g_kq.device = dev;
     g_kq.n_cu = ncu > 0 ? ncu : 1;
     g_kq.lds_max = lds > 0 ? lds : 65536;
-    if (kqk_set_max_lds(g_kq.lds_max) != 0) return kq_fail("cannot raise the LDS limit");
+    if (kqk_set_max_lds(g_kq.lds_max) != 0 || kqk_multix_set_max_lds(g_kq.lds_max) != 0)
+        return kq_fail("cannot raise the LDS limit");
     g_kq.ready = 1;
     return 0;
 }
@@ -358,12 +364,37 @@ int kq_gemv_segments_dev(const kq_segment* segs, int nseg, kq_stream stream) {
     return launch_segs(h, nh, pick(stream));
 }
 
+/* B streams with one pass over the weights per group of up to 16 streams
+ * (the multi-stream kernel); each stream's y equals its single-stream
+ * result bit for bit. */
 int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,
                        int B, int N, int K, kq_stream stream) {
     if (B < 1) return kq_fail("kq_gemv_multix_dev: B=%d", B);
-    for (int s = 0; s < B; s++)
-        if (kq_gemv_dev(type, w, xs + (size_t)s * K, NULL, ys + (size_t)s * N, N, K, stream))
-            return -1;
+    if (check_shape(type, N, K) || kq_ready()) return -1;
+    if (!w || !xs || !ys) return kq_fail("kq_gemv_multix_dev: NULL pointer");
+    if ((uintptr_t)xs & 15) return kq_fail("kq_gemv_multix_dev: xs must be 16-byte aligned");
+    if (B == 1) return kq_gemv_dev(type, w, xs, NULL, ys, N, K, stream);
+    const int grid = plan_grid();
+    for (int s0 = 0; s0 < B; ) {
+        int nb = B - s0 < 16 ? B - s0 : 16;
+        int t, bs, xlb, smb;
+        long lds = kqk_multix_plan(type, nb, N, K, grid, &t, &bs, &xlb, &smb);
+        while (nb > 1 && (lds < 0 || lds > g_kq.lds_max)) {
+            nb = (nb + 1) / 2;
+            lds = kqk_multix_plan(type, nb, N, K, grid, &t, &bs, &xlb, &smb);
+        }
+        if (lds < 0 || lds > g_kq.lds_max) {
+            /* x too long for even one stream's tiles: single-stream launches */
+            if (kq_gemv_dev(type, w, xs + (size_t)s0 * K, NULL, ys + (size_t)s0 * N, N, K, stream))
+                return -1;
+            s0 += 1;
+            continue;
+        }
+        const int e = kqk_launch_multix(type, w, xs + (size_t)s0 * K, ys + (size_t)s0 * N, nb, N,
+                                        K, grid, pick(stream));
+        if (e) return kq_fail("multix launch: %s", hipGetErrorString((hipError_t)e));
+        s0 += nb;
+    }
     return 0;
 }
 

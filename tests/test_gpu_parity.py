@@ -364,3 +364,59 @@ def test_segments_merged_same_input_parts(port):
     got = ye.cpu().numpy().reshape(E, F)
     for e in range(E):
         check_close(got[e], port.gemv(14, ex[e], xe[e], F, H), f"expert part {e}")
+
+
+# ------------------------------------------------------------ multi-stream
+def gpu_multix(qtype, w, xs, N, Kd):
+    B = xs.shape[0]
+    dw, dx = dev(w), dev(xs.reshape(-1))
+    dy = torch.empty(B * N, dtype=torch.float32, device="cuda")
+    K.gemv_multix_dev(qtype, dw.data_ptr(), dx.data_ptr(), dy.data_ptr(), B, N, Kd, stream=stream())
+    torch.cuda.synchronize()
+    return dy.cpu().numpy().reshape(B, N)
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("B,N,Kd", [(2, 300, 1024), (3, 129, 768), (8, 96, 3072),
+                                    (16, 64, 1024), (19, 40, 2048)])
+def test_multix_bit_identical_to_single_stream(port, qtype, B, N, Kd):
+    """One weight pass for B streams: every stream equals its own
+    single-stream launch bit for bit, and the oracle within the bound."""
+    w = synth.tensor(qtype, N, Kd, 800 + qtype + B)
+    xs = np.stack([synth.gaussian(synth.rng(810 + s), Kd) for s in range(B)])
+    got = gpu_multix(qtype, w, xs, N, Kd)
+    for s in range(B):
+        assert same_values(got[s], gpu_gemv(qtype, w, xs[s], N, Kd)), f"stream {s}"
+    for s in (0, B - 1):
+        check_close(got[s], port.gemv(qtype, w, xs[s], N, Kd), f"multix {K.TYPE_NAMES[qtype]} B={B} s={s}")
+
+
+@pytest.mark.parametrize("qtype", [12, 10, 14])
+def test_multix_window_fallback(port, qtype):
+    """One stream with a value outside the scaled window sends the launch to
+    the exact path; every stream still equals its single-stream result."""
+    N, Kd, B = 80, 1024, 4
+    w = synth.tensor(qtype, N, Kd, 830 + qtype)
+    xs = np.stack([synth.gaussian(synth.rng(840 + s), Kd) for s in range(B)])
+    xs[2, 17] = 2.0 ** 60
+    got = gpu_multix(qtype, w, xs, N, Kd)
+    for s in range(B):
+        assert same_values(got[s], gpu_gemv(qtype, w, xs[s], N, Kd)), f"stream {s}"
+        check_close(got[s], port.gemv(qtype, w, xs[s], N, Kd), f"multix window s={s}")
+
+
+@pytest.mark.parametrize("qtype,N,Kd", [(12, 17408, 5120), (14, 5120, 17408)])
+def test_multix_27b_sampled(port, qtype, N, Kd):
+    """27B gate / down with B = 8: sampled rows against the oracle, all rows
+    against single-stream launches."""
+    B = 8
+    w = synth.tensor(qtype, N, Kd, 850 + qtype)
+    xs = np.stack([synth.gaussian(synth.rng(860 + s), Kd) for s in range(B)])
+    got = gpu_multix(qtype, w, xs, N, Kd)
+    rows = np.random.default_rng(3).choice(N, 256, replace=False)
+    rb = K.lib().kq_row_bytes(qtype, Kd)
+    sub = np.concatenate([w[r * rb:(r + 1) * rb] for r in rows])
+    for s in (0, 5):
+        assert same_values(got[s], gpu_gemv(qtype, w, xs[s], N, Kd)), f"stream {s}"
+        check_close(got[s][rows], port.gemv(qtype, sub, xs[s], len(rows), Kd),
+                    f"multix 27B {K.TYPE_NAMES[qtype]} s={s}")
