@@ -138,6 +138,37 @@ __device__ __forceinline__ double dpp_f64(double v) {
     return __hiloint2double(h2, l2);
 }
 
+// The row reduction's phase count: a row's chunk terms are summed as G
+// partials (partial p: chunks p, p+G, ... in order, binary64 from 0),
+// combined by the pairwise tree below.  G depends on the row length only
+// (8, or 32 for rows longer than 128 chunks, whose long chains would
+// otherwise leave few lanes per row busy), so every kernel reproduces it.
+__host__ __device__ __forceinline__ int kq_phases(int NC) { return NC > 128 ? 32 : 8; }
+
+// v of lane ^ 16 (both halves)
+__device__ __forceinline__ double xor16_f64(double v) {
+    const int lo = __shfl_xor(__double2loint(v), 16);
+    const int hi = __shfl_xor(__double2hiint(v), 16);
+    return __hiloint2double(hi, lo);
+}
+
+// Pairwise tree over the G = 8 or 32 partials held by consecutive lanes
+// (every lane of the group active):
+//   8: ((P0 + P1) + (P2 + P3)) + ((P4 + P5) + (P6 + P7))
+//  32: ((S0 + S1) + (S2 + S3)) over the 8-lane sums S0..S3.
+// A butterfly: each addition is commutative, so every lane of the group
+// ends with the same bits.
+__device__ __forceinline__ double phase_tree(double s, int G) {
+    s = s + dpp_f64<0xB1>(s);    // quad_perm [1,0,3,2]: lane ^ 1
+    s = s + dpp_f64<0x4E>(s);    // quad_perm [2,3,0,1]: lane ^ 2
+    s = s + dpp_f64<0x141>(s);   // row_half_mirror: lane i <-> 7 - i (8 lanes)
+    if (G == 32) {
+        s = s + dpp_f64<0x140>(s);   // row_mirror: 8-lane halves of a 16-lane row
+        s = s + xor16_f64(s);        // 16-lane rows 0 <-> 1, 2 <-> 3
+    }
+    return s;
+}
+
 // ------------------------------------------------------------------ LDS x
 // x is staged once per workgroup in LDS, in a padded chunk-major layout:
 // chunk c (the 64 x values one lane's weights meet) occupies float4 slots
@@ -378,8 +409,9 @@ __device__ __forceinline__ uint32_t dw_of(const uint4& v, int k) {
 
 // Q4_K chunk j of a block: sub-blocks 2j (low nibbles) and 2j+1 (high).
 // SC: x is scaled by 2^k and f = 2^(149-k) (see bmul); otherwise f = 1.
-// LOWREG: a scheduling fence every few steps keeps the x reads from being
-// hoisted all at once (the multi-stream kernel's register budget).
+// LOWREG: a fence every few steps (the partial sums pinned in registers,
+// then a scheduling barrier) keeps the x reads and products from being
+// hoisted all at once (the multi-x kernel's register budget).
 template <bool SC, bool LOWREG = false>
 __device__ __forceinline__ double term_q4k(const RawQ4& r, int j, const float4* xc,
                                            float xs1, float xs2, float f) {
@@ -419,7 +451,10 @@ __device__ __forceinline__ double term_q4k(const RawQ4& r, int j, const float4* 
             a1 = a1 + l1; a2 = a2 + h1;
             a1 = a1 + l2; a2 = a2 + h2;
             a1 = a1 + l3; a2 = a2 + h3;
-            if (LOWREG && (k & 1)) __builtin_amdgcn_sched_barrier(0);
+            if (LOWREG && (k & 1)) {
+                asm volatile("" : "+v"(a1), "+v"(a2));
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     } else {
         // exact convert path for x outside the window (rare): a rolled loop,
@@ -453,32 +488,24 @@ __device__ __forceinline__ float i8f(uint32_t v, int e) {
 
 // Q6_K chunk (half h, sub is): four 16-weight sums a_t, t = 0..3.
 // f6 = 2^(-2-k) when x is scaled by 2^k (k = 0: unscaled).
-template <bool LOWREG = false>
-__device__ __forceinline__ double term_q6k(const RawQ6& r, int u, const float4* xc, double f6) {
+// The four words of step k (16 weights of each of the 4 runs of the chunk):
+// byte = ((q ^ 0x20) << 2) = int8 4*(q - 32), q = lo4 | hi2 << 4.
+__device__ __forceinline__ void q6k_words(const RawQ6& r, int k, uint32_t (&y)[4]) {
+    const uint32_t sh = r.sh;
+    const uint32_t L = __builtin_amdgcn_alignbit(r.l[k + 1], r.l[k], sh);
+    const uint32_t H = __builtin_amdgcn_alignbit(r.h[k + 1], r.h[k], sh);
+    const uint32_t Q = __builtin_amdgcn_alignbit(r.q[k + 1], r.q[k], sh) ^ 0xaaaaaaaau;
+    y[0] = ((L << 2) & 0x3c3c3c3cu) | ((Q << 6) & 0xc0c0c0c0u);
+    y[1] = ((H << 2) & 0x3c3c3c3cu) | ((Q << 4) & 0xc0c0c0c0u);
+    y[2] = ((L >> 2) & 0x3c3c3c3cu) | ((Q << 2) & 0xc0c0c0c0u);
+    y[3] = ((H >> 2) & 0x3c3c3c3cu) | (Q & 0xc0c0c0c0u);
+}
+
+// The chunk term from the four 16-weight sums: d * s[t] * a_t in binary64.
+__device__ __forceinline__ double q6k_combine(const RawQ6& r, int u, const float (&a)[4],
+                                              double f6) {
     const int is = u & 1;
     const uint32_t sh = r.sh;
-    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const uint32_t L = __builtin_amdgcn_alignbit(r.l[k + 1], r.l[k], sh);
-        const uint32_t H = __builtin_amdgcn_alignbit(r.h[k + 1], r.h[k], sh);
-        const uint32_t Q = __builtin_amdgcn_alignbit(r.q[k + 1], r.q[k], sh) ^ 0xaaaaaaaau;
-        // byte = ((q ^ 0x20) << 2) = int8 4*(q - 32), q = lo4 | hi2 << 4
-        uint32_t y[4];
-        y[0] = ((L << 2) & 0x3c3c3c3cu) | ((Q << 6) & 0xc0c0c0c0u);
-        y[1] = ((H << 2) & 0x3c3c3c3cu) | ((Q << 4) & 0xc0c0c0c0u);
-        y[2] = ((L >> 2) & 0x3c3c3c3cu) | ((Q << 2) & 0xc0c0c0c0u);
-        y[3] = ((H >> 2) & 0x3c3c3c3cu) | (Q & 0xc0c0c0c0u);
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const float4 xv = xc[4 * t + k];
-            a[t] = a[t] + i8f(y[t], 0) * xv.x;
-            a[t] = a[t] + i8f(y[t], 1) * xv.y;
-            a[t] = a[t] + i8f(y[t], 2) * xv.z;
-            a[t] = a[t] + i8f(y[t], 3) * xv.w;
-        }
-        if (LOWREG) __builtin_amdgcn_sched_barrier(0);
-    }
     // scales s[8h + is + 2t] sit at bytes is + 2t of the realigned pair
     const uint32_t S0 = __builtin_amdgcn_alignbit(r.s[1], r.s[0], sh);
     const uint32_t S1 = __builtin_amdgcn_alignbit(r.s[2], r.s[1], sh);
@@ -491,6 +518,75 @@ __device__ __forceinline__ double term_q6k(const RawQ6& r, int u, const float4* 
     const double t2 = (dq * (double)(int8_t)(uint8_t)(Sb)) * (double)a[2];
     const double t3 = (dq * (double)(int8_t)(uint8_t)(Sb >> 16)) * (double)a[3];
     return (t0 + t1) + (t2 + t3);
+}
+
+// Q6_K chunk (half h, sub is): four 16-weight sums a_t, t = 0..3.
+// f6 = 2^(-2-k) when x is scaled by 2^k (k = 0: unscaled).
+template <bool LOWREG = false>
+__device__ __forceinline__ double term_q6k(const RawQ6& r, int u, const float4* xc, double f6) {
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        uint32_t y[4];
+        q6k_words(r, k, y);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const float4 xv = xc[4 * t + k];
+            a[t] = a[t] + i8f(y[t], 0) * xv.x;
+            a[t] = a[t] + i8f(y[t], 1) * xv.y;
+            a[t] = a[t] + i8f(y[t], 2) * xv.z;
+            a[t] = a[t] + i8f(y[t], 3) * xv.w;
+        }
+        if (LOWREG) {
+            asm volatile("" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    return q6k_combine(r, u, a, f6);
+}
+
+// The Q6_K chunk terms of S members at once (the multi-x kernel): each
+// step's 16 conversions are shared by the members, and fences bound the
+// live ranges (converted quants, x, partial sums).  Member s's term is
+// term_q6k's for xc[s], operation for operation; members with !ok[s] are
+// skipped.
+template <int S>
+__device__ __forceinline__ void mx_term_q6k(const RawQ6& r, int u, const float4* const (&xc)[S],
+                                            const bool (&ok)[S], double f6, double (&part)[S]) {
+    float a[S][4];
+#pragma unroll
+    for (int s = 0; s < S; s++) a[s][0] = a[s][1] = a[s][2] = a[s][3] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        uint32_t y[4];
+        q6k_words(r, k, y);
+        float q[16];
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) q[4 * t + e] = i8f(y[t], e);
+        asm volatile("" : "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]), "+v"(q[4]),
+                     "+v"(q[5]), "+v"(q[6]), "+v"(q[7]), "+v"(q[8]), "+v"(q[9]), "+v"(q[10]),
+                     "+v"(q[11]), "+v"(q[12]), "+v"(q[13]), "+v"(q[14]), "+v"(q[15]));
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            if (ok[s]) {
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const float4 xv = xc[s][4 * t + k];
+                    a[s][t] = a[s][t] + q[4 * t + 0] * xv.x;
+                    a[s][t] = a[s][t] + q[4 * t + 1] * xv.y;
+                    a[s][t] = a[s][t] + q[4 * t + 2] * xv.z;
+                    a[s][t] = a[s][t] + q[4 * t + 3] * xv.w;
+                }
+                asm volatile("" : "+v"(a[s][0]), "+v"(a[s][1]), "+v"(a[s][2]), "+v"(a[s][3]));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < S; s++)
+        if (ok[s]) part[s] = part[s] + q6k_combine(r, u, a[s], f6);
 }
 
 // Q2_K chunk (half s, 16-sub h): groups j = 0..3, q = (qs >> 2j) & 3.
@@ -526,7 +622,10 @@ __device__ __forceinline__ double term_q2k(const RawQ2& r, int u, const float4* 
             }
             const float t = (dl * (inv * f)) * qx - ml * sx[j];
             acc = acc + (double)t;
-            if (LOWREG) __builtin_amdgcn_sched_barrier(0);
+            if (LOWREG) {
+                asm volatile("" : "+v"(acc));
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     } else {
         // exact convert path (x outside the window): rolled over j, with
@@ -591,7 +690,10 @@ __device__ __forceinline__ double term_nib(const RawNB& r, const float4* xc, con
             }
             const float t = (dl * (inv * f)) * qx - ml * sx[g];
             acc = acc + (double)t;
-            if (LOWREG) __builtin_amdgcn_sched_barrier(0);
+            if (LOWREG) {
+                asm volatile("" : "+v"(acc));
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     } else {
         // exact convert path (x outside the window): rolled over g, with the
@@ -970,20 +1072,17 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
 
     // Row reduction, in one fixed order that depends on NC only (so the
     // result does not depend on the grid, the workgroup size or how rows
-    // are batched, and the multi-stream kernel reproduces it): 8 lanes per
-    // row, lane p sums the terms of chunks p, p+8, p+16, ... in increasing
-    // order (binary64, from 0), then
-    //   y = ((P0 + P1) + (P2 + P3)) + ((P4 + P5) + (P6 + P7))
-    // by a butterfly (each addition is commutative, so every lane of the
-    // group ends with the same bits).
-    for (int task = tid; task < R * 8; task += T) {
-        const int rho = task >> 3, p = task & 7;
+    // are batched, and the multi-x kernel reproduces it): GP = kq_phases(NC)
+    // lanes per row, lane p sums the terms of chunks p, p+GP, ... in
+    // increasing order (binary64, from 0), then phase_tree.  GP divides 64
+    // and R * GP is a multiple of GP, so each lane group is entirely active.
+    const int GP = kq_phases(NC), lgp = GP == 32 ? 5 : 3;
+    for (int task = tid; task < R * GP; task += T) {
+        const int rho = task >> lgp, p = task & (GP - 1);
         const double* tr = terms + rho * NC;
         double s = 0.0;
-        for (int i = p; i < NC; i += 8) s = s + tr[i];
-        s = s + dpp_f64<0xB1>(s);    // quad_perm [1,0,3,2]: lane ^ 1
-        s = s + dpp_f64<0x4E>(s);    // quad_perm [2,3,0,1]: lane ^ 2
-        s = s + dpp_f64<0x141>(s);   // row_half_mirror: lane i <-> 7 - i (8 lanes)
+        for (int i = p; i < NC; i += GP) s = s + tr[i];
+        s = phase_tree(s, GP);
         if (p == 0) {
             uint32_t rg;
             const uint32_t g = part_of<PM>(S, (uint32_t)(b + G * rho), rg);
@@ -1066,222 +1165,357 @@ __global__ __launch_bounds__(1024) void kq_segs_kernel(SegsArg A) {
     }
 }
 
-// ------------------------------------------------------------ multi-stream
-// y_s = W . x_s for B streams (STRATUM_MULTISEQ) with one pass over W.
-// Each stream's result is bit-identical to the single-stream kernel's: the
-// same chunk terms (same arithmetic, same x scaling rule) and the same
-// reduction (8 partial sums over chunks p, p+8, ... in order, combined
-// pairwise).  Here the partials live in registers: lane (row, p, stream
-// group) walks chunks p, p+8, p+16, ... of its row and accumulates BS
-// streams, so a wave covers 8 consecutive chunks (2 super-blocks) of 8 rows
-// and the 8 rows read the same x values (LDS broadcast).
-//  * prologue: the per-sub-block sums of every stream (for the min terms)
-//    and the window vote over all x, once;
-//  * x is staged tile by tile (8 chunks = 512 values of every stream,
-//    double-buffered, a few float4 per lane) while the next tile's weights
-//    are already in flight.
-struct MultixArg {
-    const uint8_t* w;
-    const float* xs;      // B x K, stream s at xs + s*K
-    float* ys;            // B x N
-    int B, N, K, NG;      // NG stream groups of BS streams
-    int threads, grid;
-    int xl_bytes;         // LDS bytes of one x tile buffer (all streams)
-    int sums_bytes;       // LDS bytes of the sums of all streams
+// ------------------------------------------------------------- multi-x
+// y_j = W_g . x_j for the members j of each group g, with one pass over the
+// group's weight rows: STRATUM_MULTISEQ (one group, B members) and the MoE
+// gather (one group per selected expert, its routed tokens as members).
+// Each member's result is bit-identical to the single-stream kernel's for
+// the same row and x: the same chunk terms (same arithmetic, same x scaling
+// rule) and the same reduction (GP = kq_phases(K/64) partial sums over
+// chunks p, p+GP, ... in order, combined by phase_tree).
+//
+// Work.  A group's rows are cut into items of RB rows; workgroup b takes
+// items b, b+G, ...  Within an item a task is (group of 64/GP rows,
+// subgroup of S members): a wave's 64 lanes are the rows x GP chunk phases
+// (lane p takes chunks p, p+GP, ... of its row, like the single-stream
+// reduction), and each weight load serves the S members.  Tasks go
+// round-robin over the waves (task t to wave t % W, at most MX_TW per
+// wave), so the four SIMDs of a CU carry equal task counts whatever the row
+// count.  Per wave the (step, task) sequence runs with the next unit's
+// weights in flight.
+// x.  The members' x is staged in LDS in the single-stream kernel's
+// chunk-major layout, whole when it fits, else in double-buffered tiles of
+// TC chunks (a multiple of GP) staged while the previous tile is consumed.
+// A prologue pass over x gives the per-sub-block sums (min terms) and the
+// scaled-mode window vote.  Members are staged mch (<= MX_MC) at a time;
+// each such member chunk is one more pass over the item's rows (from L2).
+constexpr int MX_MAXM = 64;   // members per group
+constexpr int MX_MC = 16;     // members staged together, at most
+constexpr int MX_TW = 4;      // tasks per wave, at most
+
+struct MxGroup {
+    const uint8_t* w;         // row r at w + r * row_bytes
+    int M;                    // members, 1..MX_MAXM
+    int pad_;
+    int xi[MX_MAXM];          // member j reads x = X + xi[j] * x_stride
+    int yi[MX_MAXM];          // and writes y = Y + yi[j] * y_stride
 };
 
-// LDS slot (chunk-major, XPAD per chunk) of the float4 at x position 4q
-// (q = 0..127) of a 512-value tile
+struct MxArg {
+    const uint8_t* w;         // inline group (gdev == nullptr): weights and
+    int M;                    // members j = 0..M-1 (xi = yi = j)
+    int N, K;
+    const MxGroup* gdev;      // else groups in device memory, *ngdev of them
+    const int* ngdev;
+    const float* X;
+    float* Y;
+    long x_stride, y_stride;  // floats
+    int RB, nblk;             // rows per item, items per group
+    int threads, grid;
+    int mch;                  // members staged together
+    int TC;                   // chunks per x tile; >= K/64: x staged whole
+    int sums_bytes;           // LDS bytes of the sums of mch members
+    int xt_bytes;             // LDS bytes of one x buffer
+};
+
+// LDS slot of the float4 at tile-relative x position pos (a multiple of 4;
+// tiles start on super-block boundaries)
 template <bool LINEAR>
-__device__ __forceinline__ int tile_slot(int q) {
-    const int pos = 4 * q;
+__device__ __forceinline__ int tile_slot(int pos) {
     if (LINEAR) return (pos >> 6) * XPAD + ((pos >> 2) & 15);
     const int bi = pos >> 8, pp = pos & 255;
     const int h = pp >> 7, t = (pp >> 5) & 3, is = (pp >> 4) & 1, qq = (pp >> 2) & 3;
     return (4 * bi + 2 * h + is) * XPAD + 4 * t + qq;
 }
 
-template <int TYPE, int BS>
-__global__ __launch_bounds__(512) void kq_multix_kernel(MultixArg A) {
+// One wave's tasks (wave-uniform: scalar registers).  Task k covers rows
+// r0 + RPT grp[k] .. + RPT-1 (the lane's row: lane >> lgp) and members
+// sg[k]*S .. +S-1.
+struct MxTasks {
+    int grp[MX_TW];
+    int sg[MX_TW];
+    int ntw;                  // tasks of this wave
+    int r0, rows;             // the item's rows
+    int GP, lgp, RPT;         // phases, log2, rows per task
+};
+
+// The step/task sweep of one member chunk: tiles, steps, tasks.  SC: x is
+// staged scaled (byte-select products); else unscaled (exact convert path).
+template <int TYPE, int S, bool WHOLE, bool SC>
+__device__ __forceinline__ void mx_sweep(const MxArg& A, const MxTasks& tk, wptr gw,
+                                         double (&part)[MX_TW][S], int MC, int mc0,
+                                         const int* d_xi, const float* sums, float4* xb0,
+                                         float4* xb1, int TC, int ntile) {
     using TI = TypeInfo<TYPE>;
     using C = Chunk<TYPE>;
-    constexpr int G4 = XGroup<TYPE>::G4;
-    constexpr bool SCTYPE = TYPE != T_Q6K;
-    constexpr int XPT = 4;                        // tile float4 per lane per round
-    extern __shared__ __align__(16) uint8_t smem[];
-    const int tid = threadIdx.x, T = A.threads, lane = tid & 63, wave = tid >> 6;
-    const int b = blockIdx.x, G = A.grid;
-    const int K = A.K, NC = K >> 6, N = A.N, B = A.B;
-    const int R = N > b ? (N - b + G - 1) / G : 0;
-    if (R == 0) return;                         // uniform over the workgroup
-    const int steps = (NC + 7) >> 3;
+    const int tid = threadIdx.x, T = A.threads, GP = tk.GP;
+    const int p = tid & (GP - 1), u = p & 3, lrow = (tid & 63) >> tk.lgp;
+    const int K = A.K, NC = K >> 6, nstep = (NC + GP - 1) >> tk.lgp, nsub = TC >> tk.lgp;
+    const int xmem = TC * XPAD;                   // float4 per member in a buffer
+    const int per2 = K / (4 * XGroup<TYPE>::G4);  // sums per member
+    const int tq = MC * TC * 16;                  // float4 per tile
+    const float f = SC ? ldexpf(1.0f, 149 - KSC) : 1.0f;
+    const double f6 = 0.25;                       // Q6_K x is never scaled here
     const size_t rbytes = (size_t)(K >> 8) * TI::BB;
 
-    // LDS: two x tile buffers [B][8 * XPAD] float4, the sums of all streams
-    // [B][K / (4 G4)], per-wave flags
-    float4* xt0 = reinterpret_cast<float4*>(smem);
-    float4* xt1 = reinterpret_cast<float4*>(smem + A.xl_bytes);
-    float* sums = reinterpret_cast<float*>(smem + 2 * A.xl_bytes);
-    int* flags = reinterpret_cast<int*>(smem + 2 * A.xl_bytes + A.sums_bytes);
-    const int per = K / (4 * G4);               // sum groups per stream
-
-    // lane role: p = chunk phase, g = stream group, rl = row of the pass.
-    // The workgroup's R rows go in `passes` passes of up to RP rows (each
-    // pass sweeps K once; the weights of every row are read once).
-    const int p = tid & 7;
-    const int g = (tid >> 3) % A.NG;
-    const int rl = (tid >> 3) / A.NG;
-    const int lanes_rows = T / (8 * A.NG);
-    const int passes = (R + lanes_rows - 1) / lanes_rows;
-    const int RP = (R + passes - 1) / passes;
-    const int u = p & 3;
-    const int s0 = g * BS;
-
-    // prologue: the sums of every stream and the window vote over all x
-    uint32_t dist = 0;
-    for (int q = tid; q < B * per; q += T) {
-        const int sidx = q / per, gi = q - sidx * per;
-        const f32x4* src = reinterpret_cast<const f32x4*>(A.xs + (size_t)sidx * K) + (size_t)gi * G4;
-        float acc = 0.0f;
+    auto tile_load = [&](int ti, f32x4* v) {
 #pragma unroll
-        for (int k = 0; k < G4; k++) {
-            const f32x4 w = src[k];
-            acc = acc + w.x; acc = acc + w.y; acc = acc + w.z; acc = acc + w.w;
-            dist = max(max(dist, window_dist(w.x)), window_dist(w.y));
-            dist = max(max(dist, window_dist(w.z)), window_dist(w.w));
-        }
-        if (XGroup<TYPE>::SUMS) {
-            int slot0, xsi;
-            group_place<TYPE>(gi, slot0, xsi);
-            sums[sidx * per + xsi] = acc;
-        }
-    }
-    const bool wave_bad = __ballot(dist >= KSC_SPAN) != 0ull;
-    if (lane == 0) flags[wave] = wave_bad;
-    __syncthreads();
-    int any = 0;
-    for (int i = 0; i < (T >> 6); i++) any |= flags[i];
-    const bool sc = SCTYPE && !any;             // the same in every workgroup
-
-    // tile staging by float4 (lane t takes float4 t, t + T, ...)
-    const int tq = B * 128;                     // float4 per tile
-    auto tload = [&](int tile, int r, f32x4* v) {
-#pragma unroll
-        for (int k = 0; k < XPT; k++) {
-            const int q = min(tid + (r * XPT + k) * T, tq - 1);
-            const int sidx = q >> 7;
-            // positions past K (a last tile of fewer than 8 chunks) read the
-            // stream's last float4 instead: those slots are never used
-            const int pos = min(512 * tile + 4 * (q & 127), K - 4);
-            v[k] = *reinterpret_cast<const f32x4*>(A.xs + (size_t)sidx * K + pos);
+        for (int r = 0; r < 2; r++) {
+            const int q = min(tid + r * T, tq - 1);
+            const int j = q / (TC * 16), w4 = q - j * (TC * 16);
+            // positions past K (a last tile of fewer chunks) read the
+            // member's last float4 instead: those slots are never used
+            const int pos = min(ti * TC * 64 + 4 * w4, K - 4);
+            v[r] = *reinterpret_cast<const f32x4*>(A.X + (size_t)d_xi[mc0 + j] * A.x_stride + pos);
         }
     };
-    auto tstore = [&](int r, const f32x4* v, float4* xt) {
+    auto tile_store = [&](const f32x4* v, float4* xb) {
 #pragma unroll
-        for (int k = 0; k < XPT; k++) {
-            const int q = tid + (r * XPT + k) * T;
+        for (int r = 0; r < 2; r++) {
+            const int q = tid + r * T;
             if (q < tq) {
-                f32x4 o = v[k];
-                if (sc) {
+                const int j = q / (TC * 16), w4 = q - j * (TC * 16);
+                f32x4 o = v[r];
+                if (SC) {
                     o.x = ldexpf(o.x, KSC); o.y = ldexpf(o.y, KSC);
                     o.z = ldexpf(o.z, KSC); o.w = ldexpf(o.w, KSC);
                 }
-                reinterpret_cast<f32x4*>(xt)[(q >> 7) * 8 * XPAD + tile_slot<TI::LINEAR>(q & 127)] = o;
+                reinterpret_cast<f32x4*>(xb)[j * xmem + tile_slot<TI::LINEAR>(4 * w4)] = o;
             }
         }
     };
-    const int rounds = (tq + XPT * T - 1) / (XPT * T);
-    const float f = ldexpf(1.0f, 149 - KSC);
-    const double f6 = ldexp(0.25, sc ? -KSC : 0);
-    f32x4 xv[XPT];
+    // the lane's row of task k (clamped into the item) and its weights
+    auto wrow = [&](int k) {
+        return gw + (size_t)(tk.r0 + min(tk.RPT * tk.grp[k] + lrow, tk.rows - 1)) * rbytes;
+    };
 
-    for (int pass = 0; pass < passes; pass++) {
-        const int rho = pass * RP + rl;
-        const bool active = rl < RP && rho < R;
-        const int row = b + G * min(rho, R - 1);
-        const wptr wrow = to_global(A.w) + (size_t)row * rbytes;
-        typename C::Raw cur = C::load(wrow + (size_t)(min(p, NC - 1) >> 2) * TI::BB, u);
-        for (int r = 0; r < rounds; r++) {
-            tload(0, r, xv);
-            tstore(r, xv, xt0);
-        }
+    f32x4 xv[2];
+    if (!WHOLE) {                                 // tile 0, synchronously
+        tile_load(0, xv);
+        tile_store(xv, xb0);
         __syncthreads();
-
-        double part[BS];
+    }
+    typename C::Raw nxt = C::load(wrow(0) + (size_t)(min(p, NC - 1) >> 2) * TI::BB, u);
+    for (int ti = 0; ti < ntile; ti++) {
+        const float4* xcur = (ti & 1) ? xb1 : xb0;
+        const bool more = !WHOLE && ti + 1 < ntile;
+        if (more) tile_load(ti + 1, xv);
+        for (int j = 0; j < nsub; j++) {
+            const int st = ti * nsub + j;
+            if (st >= nstep) break;
+            const int c = GP * st + p, cl = GP * j + p;
+            // The loads are unconditional (a wave with fewer than MX_TW tasks
+            // re-reads its next step's first unit): a load under a branch
+            // would join with the old value and force a copy that waits for
+            // it, serializing the prefetch.
 #pragma unroll
-        for (int s = 0; s < BS; s++) part[s] = 0.0;
-
-        for (int i = 0; i < steps; i++) {
-            float4* xc0 = (i & 1) ? xt1 : xt0;
-            float4* xn = (i & 1) ? xt0 : xt1;
-            const bool more = i + 1 < steps;
-            if (more) tload(i + 1, 0, xv);      // next tile's x, then its weights
-            const int cn = min(8 * (i + 1) + p, NC - 1);
-            const typename C::Raw nxt = C::load(wrow + (size_t)(cn >> 2) * TI::BB, u);
-            const int c = 8 * i + p;
-            if (active && c < NC) {
-                // one stream at a time (a scheduling fence between streams
-                // keeps the compiler from interleaving them)
-                if (sc) {
+            for (int k = 0; k < MX_TW; k++) {
+                const typename C::Raw cur = nxt;
+                // the next unit: task k+1 of this step, or task 0 of the next
+                const bool wrap = k + 1 >= tk.ntw;
+                const wptr wn = wrow(wrap ? 0 : (k + 1 < MX_TW ? k + 1 : 0));
+                const int cn = min(GP * (st + (wrap ? 1 : 0)) + p, NC - 1);
+                nxt = C::load(wn + (size_t)(cn >> 2) * TI::BB, u);
+                if (k < tk.ntw && tk.RPT * tk.grp[k] + lrow < tk.rows && c < NC) {
+                    if constexpr (TYPE == T_Q6K) {
+                        const float4* xc[S];
+                        bool ok[S];
 #pragma unroll
-                    for (int s = 0; s < BS; s++) {
-                        if (s0 + s < B) {
-                            const float4* xc = xc0 + (s0 + s) * 8 * XPAD + p * XPAD;
-                            const float* xs = sums + (s0 + s) * per;
-                            part[s] = part[s] + C::template term<true, true>(cur, u, xc, xs, c, f, f6);
+                        for (int s = 0; s < S; s++) {
+                            const int m = tk.sg[k] * S + s;
+                            ok[s] = m < MC;
+                            xc[s] = xcur + min(m, MC - 1) * xmem + cl * XPAD;
                         }
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
-                } else {
+                        mx_term_q6k<S>(cur, u, xc, ok, f6, part[k]);
+                    } else {
 #pragma unroll
-                    for (int s = 0; s < BS; s++) {
-                        if (s0 + s < B) {
-                            const float4* xc = xc0 + (s0 + s) * 8 * XPAD + p * XPAD;
-                            const float* xs = sums + (s0 + s) * per;
-                            part[s] = part[s] + C::template term<false, true>(cur, u, xc, xs, c, 1.0f, f6);
+                        for (int s = 0; s < S; s++) {
+                            const int m = tk.sg[k] * S + s;
+                            if (m < MC) {
+                                const float4* xc = xcur + m * xmem + cl * XPAD;
+                                const float* xs = sums + m * per2;
+                                part[k][s] = part[k][s] +
+                                             C::template term<SC, true>(cur, u, xc, xs, c, f, f6);
+                            }
                         }
-                        __builtin_amdgcn_sched_barrier(0);
                     }
                 }
             }
-            cur = nxt;
-            if (more) {
-                tstore(0, xv, xn);
-                for (int r = 1; r < rounds; r++) {
-                    tload(i + 1, r, xv);
-                    tstore(r, xv, xn);
+        }
+        if (more) {
+            tile_store(xv, (ti & 1) ? xb0 : xb1);
+            __syncthreads();                      // next tile in; this tile's reads done
+        }
+    }
+    C::drain(nxt);
+}
+
+template <int TYPE, int S, bool WHOLE>
+__global__ __launch_bounds__(1024) void kq_mx_kernel(MxArg A) {
+    using TI = TypeInfo<TYPE>;
+    constexpr int G4 = XGroup<TYPE>::G4;
+    constexpr bool SCTYPE = TYPE != T_Q6K;
+    constexpr bool SUMS = XGroup<TYPE>::SUMS;
+    extern __shared__ __align__(16) uint8_t smem[];
+    // the wave index in a scalar register: task choice and the task loop's
+    // branches are then scalar (no exec masking around the weight loads)
+    const int tid = threadIdx.x, T = A.threads, lane = tid & 63, W = T >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int K = A.K, NC = K >> 6, N = A.N;
+    const int per = K / (4 * G4);
+    const int GP = kq_phases(NC), lgp = GP == 32 ? 5 : 3, RPT = 64 / GP;
+    const int TC = WHOLE ? (NC + GP - 1) & -GP : A.TC;
+    const int ntile = WHOLE ? 1 : (NC + TC - 1) / TC;
+    const int xmem = TC * XPAD;
+
+    // LDS: member tables, flags, sums [mch][per], x buffer(s)
+    int* d_xi = reinterpret_cast<int*>(smem);
+    int* d_yi = d_xi + MX_MAXM;
+    int* flags = d_yi + MX_MAXM;
+    float* sums = reinterpret_cast<float*>(flags + 16);
+    float4* xb0 = reinterpret_cast<float4*>(smem + 8 * MX_MAXM + 64 + A.sums_bytes);
+    float4* xb1 = reinterpret_cast<float4*>(reinterpret_cast<uint8_t*>(xb0) + A.xt_bytes);
+
+    const int ng = A.gdev ? *A.ngdev : 1;
+    const int nitems = ng * A.nblk;
+    for (int item = blockIdx.x; item < nitems; item += A.grid) {
+        const int g = item / A.nblk, blk = item - g * A.nblk;
+        const int r0 = blk * A.RB, rows = min(A.RB, N - r0);
+        const uint8_t* gw;
+        int M;
+        __syncthreads();                          // the previous item's table reads are done
+        if (A.gdev) {
+            const MxGroup* Gd = A.gdev + g;
+            gw = Gd->w;
+            M = min(Gd->M, MX_MAXM);
+            for (int j = tid; j < M; j += T) { d_xi[j] = Gd->xi[j]; d_yi[j] = Gd->yi[j]; }
+        } else {
+            gw = A.w;
+            M = A.M;
+            for (int j = tid; j < M; j += T) { d_xi[j] = j; d_yi[j] = j; }
+        }
+        for (int mc0 = 0; mc0 < M; mc0 += A.mch) {
+            const int MC = min(A.mch, M - mc0);
+            __syncthreads();                      // tables in; the previous chunk's LDS reads done
+
+            // prologue: sums, window vote, and x itself when staged whole
+            uint32_t dist = 0;
+            if (SUMS || WHOLE) {
+                for (int q = tid; q < MC * per; q += T) {
+                    const int j = q / per, gi = q - j * per;
+                    const f32x4* src = reinterpret_cast<const f32x4*>(
+                                           A.X + (size_t)d_xi[mc0 + j] * A.x_stride) +
+                                       (size_t)gi * G4;
+                    f32x4 v[G4];
+#pragma unroll
+                    for (int k = 0; k < G4; k++) v[k] = src[k];
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < G4; k++) {
+                        acc = acc + v[k].x; acc = acc + v[k].y; acc = acc + v[k].z; acc = acc + v[k].w;
+                        dist = max(max(dist, window_dist(v[k].x)), window_dist(v[k].y));
+                        dist = max(max(dist, window_dist(v[k].z)), window_dist(v[k].w));
+                    }
+                    int slot0, xsi;
+                    group_place<TYPE>(gi, slot0, xsi);
+                    if (SUMS) sums[j * per + xsi] = acc;
+                    if (WHOLE) {
+                        f32x4* dst = reinterpret_cast<f32x4*>(xb0) + j * xmem + slot0;
+#pragma unroll
+                        for (int k = 0; k < G4; k++) {
+                            f32x4 o = v[k];
+                            if (SCTYPE) {
+                                o.x = ldexpf(o.x, KSC); o.y = ldexpf(o.y, KSC);
+                                o.z = ldexpf(o.z, KSC); o.w = ldexpf(o.w, KSC);
+                            }
+                            dst[k] = o;
+                        }
+                    }
                 }
             }
-            __syncthreads();                    // next tile written, this tile's reads done
-        }
-        C::drain(cur);
+            bool sc = false;
+            if (SCTYPE) {
+                const bool wave_bad = __ballot(dist >= KSC_SPAN) != 0ull;
+                if (lane == 0) flags[wave] = wave_bad;
+                __syncthreads();
+                int any = 0;
+                for (int i = 0; i < W; i++) any |= flags[i];
+                sc = !any;                        // uniform over the workgroup
+                if (WHOLE && any) {               // restage unscaled
+                    for (int q = tid; q < MC * per; q += T) {
+                        const int j = q / per, gi = q - j * per;
+                        const f32x4* src = reinterpret_cast<const f32x4*>(
+                                               A.X + (size_t)d_xi[mc0 + j] * A.x_stride) +
+                                           (size_t)gi * G4;
+                        int slot0, xsi;
+                        group_place<TYPE>(gi, slot0, xsi);
+                        f32x4* dst = reinterpret_cast<f32x4*>(xb0) + j * xmem + slot0;
+#pragma unroll
+                        for (int k = 0; k < G4; k++) dst[k] = src[k];
+                    }
+                    __syncthreads();
+                }
+            } else {
+                __syncthreads();
+            }
 
-        // ((P0 + P1) + (P2 + P3)) + ((P4 + P5) + (P6 + P7)) per stream, as
-        // the single-stream reduction
+            // this wave's tasks t = wave + k * W
+            const int nsg = (MC + S - 1) / S;
+            const int ntask = ((rows + RPT - 1) / RPT) * nsg;
+            MxTasks tk;
+            tk.ntw = wave < ntask ? min(MX_TW, (ntask - wave + W - 1) / W) : 0;
+            tk.r0 = r0;
+            tk.rows = rows;
+            tk.GP = GP;
+            tk.lgp = lgp;
+            tk.RPT = RPT;
 #pragma unroll
-        for (int s = 0; s < BS; s++) {
-            double v = part[s];
-            v = v + dpp_f64<0xB1>(v);
-            v = v + dpp_f64<0x4E>(v);
-            v = v + dpp_f64<0x141>(v);
-            part[s] = v;
-        }
-        if (active && p == 0) {
+            for (int k = 0; k < MX_TW; k++) {
+                const int t = wave + k * W;
+                tk.grp[k] = t / nsg;
+                tk.sg[k] = t - tk.grp[k] * nsg;
+            }
+            double part[MX_TW][S];
 #pragma unroll
-            for (int s = 0; s < BS; s++)
-                if (s0 + s < B) A.ys[(size_t)(s0 + s) * N + row] = (float)part[s];
+            for (int k = 0; k < MX_TW; k++)
+#pragma unroll
+                for (int s = 0; s < S; s++) part[k][s] = 0.0;
+
+            if (sc)
+                mx_sweep<TYPE, S, WHOLE, SCTYPE>(A, tk, to_global(gw), part, MC, mc0, d_xi, sums,
+                                                 xb0, xb1, TC, ntile);
+            else
+                mx_sweep<TYPE, S, WHOLE, false>(A, tk, to_global(gw), part, MC, mc0, d_xi, sums,
+                                                xb0, xb1, TC, ntile);
+
+            // phase_tree per member (every lane of the wave takes part)
+#pragma unroll
+            for (int k = 0; k < MX_TW; k++) {
+                if (k < tk.ntw) {
+#pragma unroll
+                    for (int s = 0; s < S; s++) {
+                        const double v = phase_tree(part[k][s], GP);
+                        const int m = tk.sg[k] * S + s;
+                        const int rr = RPT * tk.grp[k] + (lane >> lgp);
+                        if (rr < rows && (lane & (GP - 1)) == 0 && m < MC)
+                            A.Y[(size_t)d_yi[mc0 + m] * A.y_stride + r0 + rr] = (float)v;
+                    }
+                }
+            }
         }
     }
 }
 
 template <int TYPE>
-int launch_multix_t(const MultixArg& a, int bs, long lds, hipStream_t st) {
-    switch (bs) {
-    case 1: hipLaunchKernelGGL((kq_multix_kernel<TYPE, 1>), dim3(a.grid), dim3(a.threads), (size_t)lds, st, a); break;
-    case 2: hipLaunchKernelGGL((kq_multix_kernel<TYPE, 2>), dim3(a.grid), dim3(a.threads), (size_t)lds, st, a); break;
-    case 4: hipLaunchKernelGGL((kq_multix_kernel<TYPE, 4>), dim3(a.grid), dim3(a.threads), (size_t)lds, st, a); break;
-    default: hipLaunchKernelGGL((kq_multix_kernel<TYPE, 8>), dim3(a.grid), dim3(a.threads), (size_t)lds, st, a); break;
+int launch_mx_t(const MxArg& a, int s, bool whole, long lds, hipStream_t st) {
+#define KQ_MX_GO(S_, W_) \
+    hipLaunchKernelGGL((kq_mx_kernel<TYPE, S_, W_>), dim3(a.grid), dim3(a.threads), (size_t)lds, st, a)
+    if (whole) {
+        if (s == 1) KQ_MX_GO(1, true); else KQ_MX_GO(2, true);
+    } else {
+        if (s == 1) KQ_MX_GO(1, false); else KQ_MX_GO(2, false);
     }
+#undef KQ_MX_GO
     return (int)hipGetLastError();
 }
 
@@ -1506,34 +1740,92 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
     return (int)hipGetLastError();
 }
 
-// Multi-stream launch plan (B <= 16 per launch): BS = streams per lane
-// (the next power of two >= B, at most 8), NG = ceil(B / BS) lane groups
-// per row; a workgroup takes up to 512 lanes, 8 * NG per row in flight, and
-// goes over its rows in as few passes as that allows.  Returns the LDS
-// bytes, or -1.
-long kqk_multix_plan(int type, int B, int N, int K, int grid, int* threads, int* bs,
-                     int* xl_bytes, int* sums_bytes) {
+// Multi-x launch plan for groups of N x K rows with at most mmax members
+// and at most ngmax groups.  plan[]: 0 threads, 1 S (members per weight
+// load), 2 RB (rows per item), 3 nblk (items per group), 4 TC (chunks per x
+// tile), 5 sums bytes, 6 x buffer bytes, 7 mch (members staged together).
+// Returns the LDS bytes, or -1.
+//
+// The choice comes from a small cost model, in instruction issues of the
+// busiest SIMD: item rounds x member chunks x (steps x task-step cost +
+// per-item and per-tile overheads).  Tasks t go to SIMD t % 4; a task-step
+// costs c0 (shared by the S members) + S c1 (per member) issues, per-type
+// counts from the generated code; a SIMD with fewer than 3 tasks is
+// latency-bound and taken as 3.
+long kqk_mx_plan(int type, int N, int K, int mmax, int ngmax, int grid, int lds_max, int* plan) {
     const int xpc = xs_per_chunk(type);
-    if (xpc < 0 || B < 1 || B > 16 || N < 1 || K <= 0 || (K & 255) || grid < 1) return -1;
-    const int BS = B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8;
-    const int NG = (B + BS - 1) / BS;
-    const long R = (N + grid - 1) / grid;
-    long rows = 512 / (8 * NG);                 // rows in flight per pass
-    const long passes = (R + rows - 1) / rows;
-    rows = (R + passes - 1) / passes;
-    const long lanes = 8 * rows * NG;
-    *threads = (int)((lanes + 63) / 64 * 64);
-    *bs = BS;
-    *xl_bytes = B * 8 * XPAD * 16;
-    *sums_bytes = (int)(((long)B * (K / 64) * xpc * 4 + 15) & ~15L);
-    return 2L * *xl_bytes + *sums_bytes + 64;
+    if (xpc < 0 || mmax < 1 || mmax > MX_MAXM || ngmax < 1 || N < 1 || K <= 0 || (K & 255) ||
+        grid < 1)
+        return -1;
+    const int T = 1024, W = T / 64;
+    const int NC = K >> 6, GP = kq_phases(NC), RPT = 64 / GP;
+    const int NCg = (NC + GP - 1) / GP * GP, nstep = NCg / GP;
+    const int G4 = type == T_Q4K ? 8 : 4;
+    const long per = K / (4 * G4);
+    const long head = 8L * MX_MAXM + 64;
+    const double c0 = type == T_Q4K ? 45 : type == T_Q6K ? 170 : type == T_Q2K ? 30 : 35;
+    const double c1 = type == T_Q6K ? 140 : 150;
+    // per-pass and per-tile overheads, fitted to timings of the 27B gate
+    // and down shapes (a pass stages x and ramps the weight stream up)
+    const double item_cost = 20000, tile_cost = 500;
+    double best = 1e300;
+    long best_lds = -1;
+    const int m0 = mmax < MX_MC ? mmax : MX_MC;
+    for (int mch = m0; mch >= 1; mch = mch > 1 ? (mch + 1) / 2 : 0) {
+        const long sums = xpc ? ((long)mch * per * 4 + 15) & ~15L : 0;
+        const long whole = (long)mch * NCg * XPAD * 16;
+        long xt, lds;
+        int TC;
+        if (head + sums + whole <= lds_max) {
+            TC = NCg;
+            xt = whole;
+            lds = head + sums + xt;
+        } else {
+            TC = 0;
+            for (int tc = GP; tc < NCg; tc += GP) {
+                if (head + sums + 2L * mch * tc * XPAD * 16 > lds_max || mch * tc * 16 > 2 * T) break;
+                TC = tc;
+            }
+            if (TC == 0) continue;
+            xt = (long)mch * TC * XPAD * 16;
+            lds = head + sums + 2 * xt;
+        }
+        const int ntile = (NC + TC - 1) / TC;
+        const int nmc = (mmax + mch - 1) / mch;
+        for (int S = 1; S <= 2; S++) {
+            if (S > 1 && S > mch) break;
+            const int nsg = (mch + S - 1) / S;
+            const int maxgrp = W * MX_TW / nsg;
+            if (maxgrp < 1) continue;
+            const int nblk0 = (N + RPT * maxgrp - 1) / (RPT * maxgrp);
+            for (int nblk = nblk0; nblk <= N && nblk <= 4096; nblk++) {
+                const int RB = (N + nblk - 1) / nblk;
+                if (nblk > nblk0 && (N + RB - 1) / RB != nblk) continue;
+                const int ntask = ((RB + RPT - 1) / RPT) * nsg;
+                if (ntask > W * MX_TW) continue;
+                const long items = (long)ngmax * nblk;
+                const long rounds = (items + grid - 1) / grid;
+                const int simd = (ntask + 3) / 4;
+                const double step = (simd < 3 ? 3 : simd) * (c0 + S * c1);
+                const double cost =
+                    (double)rounds * nmc * (step * nstep + item_cost + (ntile - 1) * tile_cost);
+                if (cost <= best) {             // ties: the later (more items, or fewer
+                    best = cost;                // members per load) choice
+                    best_lds = lds;
+                    plan[0] = T; plan[1] = S; plan[2] = RB; plan[3] = nblk; plan[4] = TC;
+                    plan[5] = (int)sums; plan[6] = (int)xt; plan[7] = mch;
+                }
+            }
+        }
+    }
+    return best_lds;
 }
 
-int kqk_multix_set_max_lds(int bytes) {
-#define KQ_MX_ATTR(T_)                                                                    \
-    {&kq_multix_kernel<T_, 1>, &kq_multix_kernel<T_, 2>, &kq_multix_kernel<T_, 4>,      \
-     &kq_multix_kernel<T_, 8>}
-    typedef void (*mx_fn)(MultixArg);
+int kqk_mx_set_max_lds(int bytes) {
+#define KQ_MX_ATTR(T_)                                                                  \
+    {&kq_mx_kernel<T_, 1, true>, &kq_mx_kernel<T_, 2, true>, &kq_mx_kernel<T_, 1, false>, \
+     &kq_mx_kernel<T_, 2, false>}
+    typedef void (*mx_fn)(MxArg);
     const mx_fn fns[4][4] = {KQ_MX_ATTR(T_Q4K), KQ_MX_ATTR(T_Q6K), KQ_MX_ATTR(T_Q2K),
                              KQ_MX_ATTR(T_NIB)};
 #undef KQ_MX_ATTR
@@ -1546,23 +1838,29 @@ int kqk_multix_set_max_lds(int bytes) {
     return 0;
 }
 
-// B streams (xs: B x K contiguous, ys: B x N) in one pass over the weights.
-int kqk_launch_multix(int type, const void* w, const float* xs, float* ys, int B, int N, int K,
-                      int grid, hipStream_t st) {
-    int threads = 0, bs = 0, xlb = 0, smb = 0;
-    const long lds = kqk_multix_plan(type, B, N, K, grid, &threads, &bs, &xlb, &smb);
-    if (lds < 0) return (int)hipErrorInvalidValue;
-    MultixArg a;
+// One multi-x launch.  Inline group (gdev == NULL): weights w, members
+// j = 0..M-1 with x_j = X + j * x_stride and y_j = Y + j * y_stride.  Else
+// *ngdev groups of MxGroup layout at gdev (device memory).
+int kqk_launch_mx(int type, const int* plan, long lds, int grid, const void* w, int M,
+                  const void* gdev, const int* ngdev, const float* X, long x_stride, float* Y,
+                  long y_stride, int N, int K, hipStream_t st) {
+    MxArg a;
     a.w = static_cast<const uint8_t*>(w);
-    a.xs = xs;
-    a.ys = ys;
-    a.B = B; a.N = N; a.K = K; a.NG = (B + bs - 1) / bs;
-    a.threads = threads; a.grid = grid; a.xl_bytes = xlb; a.sums_bytes = smb;
+    a.M = M;
+    a.N = N; a.K = K;
+    a.gdev = static_cast<const MxGroup*>(gdev);
+    a.ngdev = ngdev;
+    a.X = X; a.Y = Y;
+    a.x_stride = x_stride; a.y_stride = y_stride;
+    a.RB = plan[2]; a.nblk = plan[3];
+    a.threads = plan[0]; a.grid = grid;
+    a.TC = plan[4]; a.sums_bytes = plan[5]; a.xt_bytes = plan[6]; a.mch = plan[7];
+    const bool whole = a.TC >= (K >> 6);
     switch (type) {
-    case T_Q4K: return launch_multix_t<T_Q4K>(a, bs, lds, st);
-    case T_Q6K: return launch_multix_t<T_Q6K>(a, bs, lds, st);
-    case T_Q2K: return launch_multix_t<T_Q2K>(a, bs, lds, st);
-    case T_NIB: return launch_multix_t<T_NIB>(a, bs, lds, st);
+    case T_Q4K: return launch_mx_t<T_Q4K>(a, plan[1], whole, lds, st);
+    case T_Q6K: return launch_mx_t<T_Q6K>(a, plan[1], whole, lds, st);
+    case T_Q2K: return launch_mx_t<T_Q2K>(a, plan[1], whole, lds, st);
+    case T_NIB: return launch_mx_t<T_NIB>(a, plan[1], whole, lds, st);
     default: return (int)hipErrorInvalidValue;
     }
 }

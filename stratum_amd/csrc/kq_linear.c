@@ -39,11 +39,16 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
                     long lds_bytes, int xs_off, int terms_off, int scr_off, hipStream_t st);
 int kqk_launch_dequant(int type, const void* w, float* y, long nblocks, hipStream_t st);
 int kqk_set_max_lds(int bytes);
-long kqk_multix_plan(int type, int B, int N, int K, int grid, int* threads, int* bs,
-                     int* xl_bytes, int* sums_bytes);
-int kqk_launch_multix(int type, const void* w, const float* xs, float* ys, int B, int N, int K,
-                      int grid, hipStream_t st);
-int kqk_multix_set_max_lds(int bytes);
+/* multi-x launcher: plan[] = threads, S, RB, nblk, TC, sums bytes, x buffer
+ * bytes, members staged together (kqk_mx_plan returns the LDS bytes, or
+ * -1); gdev == NULL launches one inline group of M members (x_j = X + j
+ * x_stride, y_j = Y + j y_stride) */
+#define KQK_MX_PLAN 8
+long kqk_mx_plan(int type, int N, int K, int mmax, int ngmax, int grid, int lds_max, int* plan);
+int kqk_launch_mx(int type, const int* plan, long lds, int grid, const void* w, int M,
+                  const void* gdev, const int* ngdev, const float* X, long x_stride, float* Y,
+                  long y_stride, int N, int K, hipStream_t st);
+int kqk_mx_set_max_lds(int bytes);
 
 #define KQ_MAX_REGIONS 16
 
@@ -119,7 +124,7 @@ static int kq_ready(void) {
     g_kq.device = dev;
     g_kq.n_cu = ncu > 0 ? ncu : 1;
     g_kq.lds_max = lds > 0 ? lds : 65536;
-    if (kqk_set_max_lds(g_kq.lds_max) != 0 || kqk_multix_set_max_lds(g_kq.lds_max) != 0)
+    if (kqk_set_max_lds(g_kq.lds_max) != 0 || kqk_mx_set_max_lds(g_kq.lds_max) != 0)
         return kq_fail("cannot raise the LDS limit");
     g_kq.ready = 1;
     return 0;
@@ -364,9 +369,9 @@ int kq_gemv_segments_dev(const kq_segment* segs, int nseg, kq_stream stream) {
     return launch_segs(h, nh, pick(stream));
 }
 
-/* B streams with one pass over the weights per group of up to 16 streams
- * (the multi-stream kernel); each stream's y equals its single-stream
- * result bit for bit. */
+/* B streams with one pass over the weights per group of up to 64 streams
+ * (the multi-x kernel); each stream's y equals its single-stream result bit
+ * for bit. */
 int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,
                        int B, int N, int K, kq_stream stream) {
     if (B < 1) return kq_fail("kq_gemv_multix_dev: B=%d", B);
@@ -376,23 +381,20 @@ int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,
     if (B == 1) return kq_gemv_dev(type, w, xs, NULL, ys, N, K, stream);
     const int grid = plan_grid();
     for (int s0 = 0; s0 < B; ) {
-        int nb = B - s0 < 16 ? B - s0 : 16;
-        int t, bs, xlb, smb;
-        long lds = kqk_multix_plan(type, nb, N, K, grid, &t, &bs, &xlb, &smb);
-        while (nb > 1 && (lds < 0 || lds > g_kq.lds_max)) {
-            nb = (nb + 1) / 2;
-            lds = kqk_multix_plan(type, nb, N, K, grid, &t, &bs, &xlb, &smb);
+        const int nb = B - s0 < 64 ? B - s0 : 64;
+        int plan[KQK_MX_PLAN];
+        const long lds = kqk_mx_plan(type, N, K, nb, 1, grid, g_kq.lds_max, plan);
+        if (lds < 0) {
+            /* x too long to stage even in 8-chunk tiles: single-stream launches */
+            for (int s = s0; s < s0 + nb; s++)
+                if (kq_gemv_dev(type, w, xs + (size_t)s * K, NULL, ys + (size_t)s * N, N, K, stream))
+                    return -1;
+        } else {
+            const int e = kqk_launch_mx(type, plan, lds, grid, w, nb, NULL, NULL,
+                                        xs + (size_t)s0 * K, K, ys + (size_t)s0 * N, N, N, K,
+                                        pick(stream));
+            if (e) return kq_fail("multix launch: %s", hipGetErrorString((hipError_t)e));
         }
-        if (lds < 0 || lds > g_kq.lds_max) {
-            /* x too long for even one stream's tiles: single-stream launches */
-            if (kq_gemv_dev(type, w, xs + (size_t)s0 * K, NULL, ys + (size_t)s0 * N, N, K, stream))
-                return -1;
-            s0 += 1;
-            continue;
-        }
-        const int e = kqk_launch_multix(type, w, xs + (size_t)s0 * K, ys + (size_t)s0 * N, nb, N,
-                                        K, grid, pick(stream));
-        if (e) return kq_fail("multix launch: %s", hipGetErrorString((hipError_t)e));
         s0 += nb;
     }
     return 0;

@@ -405,6 +405,32 @@ def test_multix_window_fallback(port, qtype):
         check_close(got[s], port.gemv(qtype, w, xs[s], N, Kd), f"multix window s={s}")
 
 
+@pytest.mark.parametrize("qtype", [12, 10, 14, 42])
+def test_multix_tiled_window_fallback(port, qtype):
+    """x too long to stage whole (tiles of a few chunks), with one stream
+    outside the scaled window: the tiled exact path, still bit-identical."""
+    N, Kd, B = 200, 5120, 8
+    w = synth.tensor(qtype, N, Kd, 870 + qtype)
+    xs = np.stack([synth.gaussian(synth.rng(880 + s), Kd) for s in range(B)])
+    xs[5, 4097] = -(2.0 ** 61)
+    got = gpu_multix(qtype, w, xs, N, Kd)
+    for s in range(B):
+        assert same_values(got[s], gpu_gemv(qtype, w, xs[s], N, Kd)), f"stream {s}"
+    check_close(got[5], port.gemv(qtype, w, xs[5], N, Kd), "tiled window s=5")
+
+
+@pytest.mark.parametrize("B", [17, 40, 64, 70])
+def test_multix_member_chunks(port, B):
+    """More than 16 streams: members staged 16 at a time within one weight
+    pass (and more than 64 in two launches)."""
+    qtype, N, Kd = 12, 100, 1024
+    w = synth.tensor(qtype, N, Kd, 890 + B)
+    xs = np.stack([synth.gaussian(synth.rng(900 + s), Kd) for s in range(B)])
+    got = gpu_multix(qtype, w, xs, N, Kd)
+    for s in range(B):
+        assert same_values(got[s], gpu_gemv(qtype, w, xs[s], N, Kd)), f"stream {s}"
+
+
 @pytest.mark.parametrize("qtype,N,Kd", [(12, 17408, 5120), (14, 5120, 17408)])
 def test_multix_27b_sampled(port, qtype, N, Kd):
     """27B gate / down with B = 8: sampled rows against the oracle, all rows
