@@ -154,6 +154,102 @@ int kq_dequant_dev(int type, const void* w, float* y, int64_t nblocks, kq_stream
 /* Bytes of one row of K weights of `type` (K/256 blocks), or -1. */
 int64_t kq_row_bytes(int type, int K);
 
+/* ----------------------------------------------------------- MoE gather
+ * Expert-stacked tensors (GGUF [K_in, N_out, E]: expert e's slice is bytes
+ * [offset + e*slice, +slice)) and .moep packs (per layer and expert, the
+ * gate|up|down slices contiguous), as addressed by
+ * stratum_arch_moe.inc.c:220-337, and the routed expert GEMVs of
+ * moe_forward_block / moe_forward_b (:605-755, :817-1267). */
+
+#define KQ_MOE_MAX_EXPERTS 4096
+#define KQ_MOE_MAX_TOKENS 64
+
+/* Bytes of one expert slice of a stacked tensor.  Replaces moe_slice_bytes
+ * (stratum_arch_moe.inc.c:220-238): nbytes / (nelem / (K_in * N_out)), the
+ * block size formula when nbytes or nelem is unset, and the fixed formulas
+ * of the W16 types 43 and 44.  -1 for an unknown type without sizes. */
+int64_t kq_moe_slice_bytes(const kq_tensor* t, int K_in, int N_out);
+
+/* Descriptor of one expert slice: *dst = *t with nelem = K_in * N_out,
+ * nbytes = slice and offset moved to expert e's slice of the stacked
+ * tensor or, when slice_host != NULL, to that host address (a pack slice)
+ * relative to base.  Replaces moe_bind_slice (stratum_arch_moe.inc.c:327-337);
+ * the result goes to kq_linear_dispatch like any tensor. */
+void kq_moe_bind_slice(kq_tensor* dst, const kq_tensor* t, int e, int64_t slice, int N_out,
+                       int K_in, const uint8_t* slice_host, const uint8_t* base);
+
+/* The .moep header (MoePackHdr, stratum_arch_moe.inc.c:245-259): packed,
+ * little-endian, 68 bytes. */
+#pragma pack(push, 1)
+typedef struct kq_moe_pack_hdr {
+    char     magic[4];
+    uint32_t version, n_layers, n_experts, n_embed, n_ff;
+    uint32_t gate_type, up_type, down_type;
+    uint64_t gate_slice, up_slice, down_slice, data_off;
+} kq_moe_pack_hdr;
+#pragma pack(pop)
+
+/* A validated pack mapping. */
+typedef struct kq_moe_pack {
+    const uint8_t* base;
+    size_t size;
+    uint64_t data_off, gate_slice, up_slice, down_slice, stride;
+    uint32_t n_layers, n_experts;
+} kq_moe_pack;
+
+/* Checks a pack mapped at [base, base+size) against the model, with the
+ * header tests of moe_pack_load (stratum_arch_moe.inc.c:506-525: magic,
+ * version, shape, types, slice sizes from the stacked tensors, data_off and
+ * total size), and fills *out.  0, or -1 when the pack does not match.
+ * The sampled byte comparison the reference then runs against the GGUF
+ * (:535-560) is the caller's (it reads both host mappings). */
+int kq_moe_pack_open(const uint8_t* base, size_t size, int n_layers, int n_experts, int n_embed,
+                     int n_ff, const kq_tensor* gate, const kq_tensor* up,
+                     const kq_tensor* down, kq_moe_pack* out);
+
+/* Host address of layer li, expert e, tensor which (0 gate, 1 up, 2 down)
+ * in the pack.  Replaces moe_pack_which (stratum_arch_moe.inc.c:307-313). */
+const uint8_t* kq_moe_pack_which(const kq_moe_pack* p, int li, int e, int which);
+
+/* Top-K experts of one token's router weights w[0..E): sel[s], selw[s] for
+ * s < K in decreasing weight, equal weights in increasing expert id, slots
+ * without an expert (w <= -1) left (-1, -1.0f).  Replaces moe_topk
+ * (stratum_arch_moe.inc.c:368-385); host code, as in the reference. */
+void kq_moe_topk(const float* w, int E, int K, int* sel, float* selw);
+
+/* The same selection on the device for B tokens: probs is B x E (row per
+ * token), sel and selw are B x k.  E <= KQ_MOE_MAX_EXPERTS.  0 or -1. */
+int kq_moe_topk_dev(const float* probs, int B, int E, int k, int* sel, float* selw,
+                    kq_stream stream);
+
+/* One routed expert GEMV of a layer: for every member m = s*k + r (token s,
+ * rank r) with expert e = sel[m] and every tensor t < ntensors,
+ *   y[t][m*n_out .. +n_out) = W_t(e) . x[(m / x_div)*k_in .. +k_in)
+ * where W_t(e) starts at w[t] + e * expert_stride (the stacked slice, or
+ * the pack stride).  Gate and up (ntensors 2, x_div k: one x per token)
+ * share one launch; down is ntensors 1, x_div 1 (one activation per
+ * member).  Each member's y equals kq_gemv_dev on its slice bit for bit.
+ * All pointers are device pointers; sel is read on the device (entries
+ * outside [0, E) are clamped into it for B == 1 and skipped for B > 1;
+ * their y is unspecified, as the reference skips sel < 0 ranks,
+ * stratum_arch_moe.inc.c:722-725).  B == 1 runs the single-stream kernel
+ * with the expert bases resolved on the device; B > 1 builds the distinct
+ * experts' member lists on the device (moe_forward_b's grouping,
+ * stratum_arch_moe.inc.c:1130-1205) and streams each selected slice once
+ * for all of its tokens.  B <= KQ_MOE_MAX_TOKENS, k <= KQ_MAX_GROUPS.  No
+ * counterpart as one call in the reference, which dispatches per slice
+ * (moe_dispatch_slice / moe_multix_slice, :596-603, :808-815). */
+typedef struct kq_moe_op {
+    int type, n_out, k_in;
+    int ntensors;
+    const void* w[2];
+    int64_t expert_stride;
+    const float* x;
+    int x_div;
+    float* y[2];
+} kq_moe_op;
+int kq_moe_gemv_dev(const kq_moe_op* op, const int* sel, int B, int k, int E, kq_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -176,6 +176,37 @@ def ref() -> Ref | None:
     return _ref
 
 
+# ------------------------------------------------------------ MoE addressing
+# Integer restatements of the expert-slice and pack addressing (pure
+# arithmetic, so plain Python).
+
+BLOCK_BYTES = {10: 84, 12: 144, 14: 210, 42: 148}
+
+
+def moe_slice_bytes(qtype: int, nelem: int, nbytes: int, K_in: int, N_out: int) -> int:
+    """stratum_arch_moe.inc.c:220-238."""
+    if qtype == 43:
+        return N_out * K_in * 2 + N_out * (K_in // 256) * 8 + N_out * (K_in // 32) * 2
+    if qtype == 44:
+        return N_out * K_in * 2 + N_out * (K_in // 256) * 8
+    one = K_in * N_out
+    if nbytes <= 0 or nelem <= 0:
+        return one // 256 * BLOCK_BYTES[qtype]      # gguf_tensor_bytes of one slice
+    e_all = max(1, nelem // one)
+    return nbytes // e_all
+
+
+def moe_pack_offset(data_off: int, n_experts: int, gate: int, up: int, down: int,
+                    li: int, e: int, which: int) -> int:
+    """moe_pack_which, stratum_arch_moe.inc.c:307-313 (stride = gate+up+down)."""
+    off = data_off + (li * n_experts + e) * (gate + up + down)
+    if which == 1:
+        off += gate
+    elif which == 2:
+        off += gate + up
+    return off
+
+
 # ------------------------------------------------------------ tolerances
 def rel_err(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     """Per-element |a-b| / max(|b|, 1e-6): ASSERT_REL of quant_test.c:34-43."""

@@ -10,6 +10,10 @@ wrappers with the reference's argument meaning:
   linear_dispatch_add(w, x, add, ..) st_linear_dispatch_add (stratum_linear.h:568)
   linear_multix(w, xs, N, K)         st_linear_multix     (stratum_linear.h:715)
   q4k_group(x, K, (w, N), ...)       st_q4k_group         (stratum_linear.h:1086)
+  moe_slice_bytes / moe_bind_slice   (stratum_arch_moe.inc.c:220-238, 327-337)
+  moe_pack_open / moe_pack_which     (stratum_arch_moe.inc.c:245-313, 506-525)
+  moe_topk, moe_topk_dev             moe_topk (stratum_arch_moe.inc.c:368-385)
+  moe_gemv_dev(op, sel, B, k, E)     the routed expert GEMVs (:596-603, 808-815, 1135-1205)
 
 There is no CPU fallback: if the library is missing, ``lib()`` raises.
 """
@@ -36,7 +40,9 @@ EXPORTS = (
     "kq_linear_init", "kq_register_region", "kq_device_ptr", "kq_linear_shutdown",
     "kq_last_error", "kq_linear_dispatch", "kq_linear_dispatch_add", "kq_linear_multix",
     "kq_q4k_group", "kq_gemv_dev", "kq_gemv_multix_dev", "kq_gemv_segments_dev",
-    "kq_dequant_dev", "kq_row_bytes",
+    "kq_dequant_dev", "kq_row_bytes", "kq_moe_slice_bytes", "kq_moe_bind_slice",
+    "kq_moe_pack_open", "kq_moe_pack_which", "kq_moe_topk", "kq_moe_topk_dev",
+    "kq_moe_gemv_dev",
 )
 
 MAX_SEGMENTS = 8
@@ -106,6 +112,53 @@ def make_tensor(qtype: int, N: int, K: int, offset: int, name: bytes = b"w") -> 
     return t
 
 
+class KqMoePackHdr(ctypes.Structure):
+    """kq_moe_pack_hdr == MoePackHdr (stratum_arch_moe.inc.c:245-259), packed."""
+
+    _pack_ = 1
+    _fields_ = [("magic", ctypes.c_char * 4)] + [
+        (n, ctypes.c_uint32) for n in ("version", "n_layers", "n_experts", "n_embed", "n_ff",
+                                       "gate_type", "up_type", "down_type")] + [
+        (n, ctypes.c_uint64) for n in ("gate_slice", "up_slice", "down_slice", "data_off")]
+
+
+class KqMoePack(ctypes.Structure):
+    """kq_moe_pack: a validated pack mapping."""
+
+    _fields_ = [("base", ctypes.c_void_p), ("size", ctypes.c_size_t)] + [
+        (n, ctypes.c_uint64) for n in ("data_off", "gate_slice", "up_slice", "down_slice",
+                                       "stride")] + [
+        ("n_layers", ctypes.c_uint32), ("n_experts", ctypes.c_uint32)]
+
+
+class KqMoeOp(ctypes.Structure):
+    """kq_moe_op: one routed expert GEMV (gate+up, or down) of a layer."""
+
+    _fields_ = [
+        ("type", ctypes.c_int), ("n_out", ctypes.c_int), ("k_in", ctypes.c_int),
+        ("ntensors", ctypes.c_int),
+        ("w", ctypes.c_void_p * 2),
+        ("expert_stride", ctypes.c_int64),
+        ("x", ctypes.c_void_p),
+        ("x_div", ctypes.c_int),
+        ("y", ctypes.c_void_p * 2),
+    ]
+
+
+def moe_op(qtype: int, n_out: int, k_in: int, w_ptrs, expert_stride: int, x_ptr: int,
+           x_div: int, y_ptrs) -> KqMoeOp:
+    op = KqMoeOp()
+    op.type, op.n_out, op.k_in, op.ntensors = qtype, n_out, k_in, len(w_ptrs)
+    for i, p in enumerate(w_ptrs):
+        op.w[i] = p
+    for i, p in enumerate(y_ptrs):
+        op.y[i] = p
+    op.expert_stride = expert_stride
+    op.x = x_ptr
+    op.x_div = x_div
+    return op
+
+
 _LIB = None
 
 
@@ -138,6 +191,18 @@ def lib() -> ctypes.CDLL:
     L.kq_gemv_segments_dev.argtypes = [ctypes.POINTER(KqSegment), I, P]
     L.kq_row_bytes.argtypes = [I, I]
     L.kq_row_bytes.restype = ctypes.c_int64
+    L.kq_moe_slice_bytes.argtypes = [TP, I, I]
+    L.kq_moe_slice_bytes.restype = ctypes.c_int64
+    L.kq_moe_bind_slice.argtypes = [TP, TP, I, ctypes.c_int64, I, I, P, P]
+    L.kq_moe_bind_slice.restype = None
+    L.kq_moe_pack_open.argtypes = [P, ctypes.c_size_t, I, I, I, I, TP, TP, TP,
+                                   ctypes.POINTER(KqMoePack)]
+    L.kq_moe_pack_which.argtypes = [ctypes.POINTER(KqMoePack), I, I, I]
+    L.kq_moe_pack_which.restype = P
+    L.kq_moe_topk.argtypes = [F, I, I, ctypes.POINTER(ctypes.c_int), F]
+    L.kq_moe_topk.restype = None
+    L.kq_moe_topk_dev.argtypes = [P, I, I, I, P, P, P]
+    L.kq_moe_gemv_dev.argtypes = [ctypes.POINTER(KqMoeOp), P, I, I, I, P]
     _LIB = L
     return L
 
@@ -226,3 +291,47 @@ def gemv_segments_dev(segs: list[KqSegment], stream: int | None = None) -> None:
 def dequant_dev(qtype: int, w_ptr: int, y_ptr: int, nblocks: int,
                 stream: int | None = None) -> None:
     _check(lib().kq_dequant_dev(qtype, w_ptr, y_ptr, nblocks, stream), "kq_dequant_dev")
+
+
+def moe_slice_bytes(t: KqTensor, K_in: int, N_out: int) -> int:
+    return lib().kq_moe_slice_bytes(ctypes.byref(t), K_in, N_out)
+
+
+def moe_bind_slice(t: KqTensor, e: int, slice_bytes: int, N_out: int, K_in: int,
+                   slice_host: int | None = None, base: int | None = None) -> KqTensor:
+    d = KqTensor()
+    lib().kq_moe_bind_slice(ctypes.byref(d), ctypes.byref(t), e, slice_bytes, N_out, K_in,
+                            slice_host, base)
+    return d
+
+
+def moe_pack_open(blob: np.ndarray, n_layers: int, n_experts: int, n_embed: int, n_ff: int,
+                  gate: KqTensor, up: KqTensor, down: KqTensor) -> KqMoePack:
+    pk = KqMoePack()
+    _check(lib().kq_moe_pack_open(blob.ctypes.data, blob.nbytes, n_layers, n_experts, n_embed,
+                                  n_ff, ctypes.byref(gate), ctypes.byref(up), ctypes.byref(down),
+                                  ctypes.byref(pk)), "kq_moe_pack_open")
+    return pk
+
+
+def moe_pack_which(pk: KqMoePack, li: int, e: int, which: int) -> int:
+    """Byte offset from the pack base of (layer li, expert e, tensor which)."""
+    return lib().kq_moe_pack_which(ctypes.byref(pk), li, e, which) - pk.base
+
+
+def moe_topk(w: np.ndarray, k: int) -> tuple[list[int], np.ndarray]:
+    sel = (ctypes.c_int * k)()
+    selw = np.empty(k, np.float32)
+    lib().kq_moe_topk(_fptr(w), len(w), k, sel, _fptr(selw))
+    return list(sel), selw
+
+
+def moe_topk_dev(probs_ptr: int, B: int, E: int, k: int, sel_ptr: int, selw_ptr: int,
+                 stream: int | None = None) -> None:
+    _check(lib().kq_moe_topk_dev(probs_ptr, B, E, k, sel_ptr, selw_ptr, stream),
+           "kq_moe_topk_dev")
+
+
+def moe_gemv_dev(op: KqMoeOp, sel_ptr: int, B: int, k: int, E: int,
+                 stream: int | None = None) -> None:
+    _check(lib().kq_moe_gemv_dev(ctypes.byref(op), sel_ptr, B, k, E, stream), "kq_moe_gemv_dev")

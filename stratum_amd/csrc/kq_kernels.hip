@@ -826,6 +826,12 @@ struct Seg {
     float* y[MAXG];
     const float* add[MAXG];
     int start[MAXG];
+    // MoE gather (nullptr: unused): part p's weights are w[p] plus
+    // sel[p % ksel] expert strides, the expert index read on the device
+    // (clamped to [0, emax))
+    const int* sel;
+    long estride;
+    int ksel, emax;
 };
 
 // Issues the scalar loads of a segment's leading fields together and waits
@@ -1005,6 +1011,10 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
             av = lane == g ? S.add[g] : av;
         }
         if (lane < S.nparts) {
+            if (S.sel) {                          // the expert chosen on the device
+                const int e = min(max(S.sel[lane % S.ksel], 0), S.emax - 1);
+                wv += (size_t)e * S.estride;
+            }
             wtab[lane] = wv;
             ytab[lane] = yv;
             atab[lane] = av;
@@ -1139,7 +1149,8 @@ __global__ __launch_bounds__(1024) void kq_segs_kernel(SegsArg A) {
     for (int i = 0; i < nseg; i++) {
         const Seg& S = A.s[i];
         if (i) prefetch_seg(S);
-        const int pm = S.nparts == 1 ? PM_ONE : S.nparts <= LIST_MAX ? PM_LIST : PM_EQUAL;
+        const int pm = S.sel ? PM_EQUAL
+                     : S.nparts == 1 ? PM_ONE : S.nparts <= LIST_MAX ? PM_LIST : PM_EQUAL;
         const bool last = i == nseg - 1;
 #define KQ_RUN(T_)                                                                   \
         if (pm == PM_ONE) run_segment<T_, DEPTH, PM_ONE>(S, A, i, st, smem, last);   \
@@ -1195,10 +1206,11 @@ constexpr int MX_TW = 4;      // tasks per wave, at most
 
 struct MxGroup {
     const uint8_t* w;         // row r at w + r * row_bytes
+    float* y;                 // member j writes y + yi[j] * y_stride
     int M;                    // members, 1..MX_MAXM
     int pad_;
     int xi[MX_MAXM];          // member j reads x = X + xi[j] * x_stride
-    int yi[MX_MAXM];          // and writes y = Y + yi[j] * y_stride
+    int yi[MX_MAXM];
 };
 
 struct MxArg {
@@ -1382,15 +1394,18 @@ __global__ __launch_bounds__(1024) void kq_mx_kernel(MxArg A) {
         const int g = item / A.nblk, blk = item - g * A.nblk;
         const int r0 = blk * A.RB, rows = min(A.RB, N - r0);
         const uint8_t* gw;
+        float* Yb;
         int M;
         __syncthreads();                          // the previous item's table reads are done
         if (A.gdev) {
             const MxGroup* Gd = A.gdev + g;
             gw = Gd->w;
+            Yb = Gd->y;
             M = min(Gd->M, MX_MAXM);
             for (int j = tid; j < M; j += T) { d_xi[j] = Gd->xi[j]; d_yi[j] = Gd->yi[j]; }
         } else {
             gw = A.w;
+            Yb = A.Y;
             M = A.M;
             for (int j = tid; j < M; j += T) { d_xi[j] = j; d_yi[j] = j; }
         }
@@ -1498,7 +1513,7 @@ __global__ __launch_bounds__(1024) void kq_mx_kernel(MxArg A) {
                         const int m = tk.sg[k] * S + s;
                         const int rr = RPT * tk.grp[k] + (lane >> lgp);
                         if (rr < rows && (lane & (GP - 1)) == 0 && m < MC)
-                            A.Y[(size_t)d_yi[mc0 + m] * A.y_stride + r0 + rr] = (float)v;
+                            Yb[(size_t)d_yi[mc0 + m] * A.y_stride + r0 + rr] = (float)v;
                     }
                 }
             }
@@ -1517,6 +1532,121 @@ int launch_mx_t(const MxArg& a, int s, bool whole, long lds, hipStream_t st) {
     }
 #undef KQ_MX_GO
     return (int)hipGetLastError();
+}
+
+// ------------------------------------------------------------ MoE routing
+// Top-k per token (moe_topk, stratum_arch_moe.inc.c:368-385): slots start
+// at (sel -1, weight -1.0f) and expert e, in increasing e, displaces the
+// first slot whose weight it beats strictly.  The result is the k largest
+// weights in decreasing order, equal weights in increasing expert order,
+// counting only weights > -1 (NaN never beats anything); missing slots
+// stay (-1, -1.0f).  One wave per token: k rounds of a wave argmax over the
+// eligible experts (ties to the lower index).
+__global__ __launch_bounds__(256) void kq_moe_topk_kernel(const float* probs, int B, int E, int k,
+                                                         int* sel, float* selw) {
+    const int lane = threadIdx.x & 63;
+    const int tok = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (tok >= B) return;                      // uniform over the wave
+    const float* w = probs + (size_t)tok * E;
+    uint64_t taken = 0;                        // experts lane + 64 i already chosen, bit i
+    for (int r = 0; r < k; r++) {
+        float bv = -1.0f;
+        int be = 0x7fffffff;
+        for (int i = 0, e = lane; e < E; i++, e += 64) {
+            const float v = w[e];
+            const bool free_ = !((taken >> i) & 1);     // E <= 4096: i < 64
+            if (free_ && v > bv) { bv = v; be = e; }   // first (lowest) e wins ties in a lane
+        }
+        // wave argmax: larger weight, then lower expert
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float ov = __shfl_xor(bv, off);
+            const int oe = __shfl_xor(be, off);
+            if (ov > bv || (ov == bv && oe < be)) { bv = ov; be = oe; }
+        }
+        const bool found = be != 0x7fffffff;
+        if (lane == 0) {
+            sel[(size_t)tok * k + r] = found ? be : -1;
+            selw[(size_t)tok * k + r] = found ? bv : -1.0f;
+        }
+        if (found && (be & 63) == lane) taken |= 1ull << (be >> 6);
+    }
+}
+
+// Expert groups of the selected (token, rank) members, in increasing expert
+// order (moe_forward_b's member lists, stratum_arch_moe.inc.c:1130-1140):
+// for each distinct expert e, one MxGroup per tensor t with the members m
+// (in increasing m) that chose e: weights w[t] + e * estride, x row
+// m / x_div, output row m of y[t].  One workgroup; *ng = nt * distinct.
+struct MoeGroupArg {
+    const int* sel;
+    int nm, E, nt, x_div;          // members (B * k), experts, tensors, x divisor
+    const uint8_t* w[2];
+    float* y[2];
+    long estride;
+    MxGroup* groups;
+    int* ng;
+};
+
+__global__ __launch_bounds__(1024) void kq_moe_group_kernel(MoeGroupArg a) {
+    extern __shared__ __align__(16) int lds_i[];
+    int* cnt = lds_i;                 // [E]
+    int* gid = cnt + a.E;             // [E] group index of expert e
+    int* ms = gid + a.E;              // [nm] the members' experts
+    __shared__ int wsum[16];
+    const int tid = threadIdx.x, T = blockDim.x, lane = tid & 63, wave = tid >> 6;
+    for (int e = tid; e < a.E; e += T) cnt[e] = 0;
+    __syncthreads();
+    for (int m = tid; m < a.nm; m += T) {
+        const int e = a.sel[m];
+        const int ok = e >= 0 && e < a.E;
+        ms[m] = ok ? e : -1;
+        if (ok) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    // exclusive scan of (cnt[e] > 0) over e: each thread a run of experts
+    const int run = (a.E + T - 1) / T, e0 = tid * run, e1 = min(a.E, e0 + run);
+    int local = 0;
+    for (int e = e0; e < e1; e++) local += cnt[e] > 0;
+    int incl = local;
+    for (int off = 1; off < 64; off <<= 1) {
+        const int o = __shfl_up(incl, off);
+        if (lane >= off) incl += o;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int before = incl - local;
+    for (int i = 0; i < wave; i++) before += wsum[i];
+    for (int e = e0; e < e1; e++) {
+        gid[e] = before;
+        before += cnt[e] > 0;
+    }
+    int nd = 0;
+    for (int i = 0; i < (T >> 6); i++) nd += wsum[i];
+    __syncthreads();
+    if (tid == 0) *a.ng = a.nt * nd;
+    // one thread per distinct expert collects its members in increasing m
+    for (int e = tid; e < a.E; e += T) {
+        const int c = cnt[e];
+        if (c == 0) continue;
+        for (int t = 0; t < a.nt; t++) {
+            MxGroup* G = a.groups + (size_t)t * nd + gid[e];
+            G->w = a.w[t] + (size_t)e * a.estride;
+            G->y = a.y[t];
+            G->M = min(c, MX_MAXM);
+            G->pad_ = 0;
+        }
+        int j = 0;
+        for (int m = 0; m < a.nm && j < MX_MAXM; m++) {
+            if (ms[m] != e) continue;
+            for (int t = 0; t < a.nt; t++) {
+                MxGroup* G = a.groups + (size_t)t * nd + gid[e];
+                G->xi[j] = m / a.x_div;
+                G->yi[j] = m;
+            }
+            j++;
+        }
+    }
 }
 
 // --------------------------------------------------------------- dequant
@@ -1614,6 +1744,9 @@ struct kqk_seg {
     int rows[MAXG];
     const float* x;
     int type, K, nparts, x_stride;
+    const int* sel;          // MoE gather (NULL: none), as in Seg
+    long estride;
+    int ksel, emax;
 };
 
 static long seg_rows(const kqk_seg& g) {
@@ -1726,6 +1859,10 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
             }
         }
         d.x = h.x;
+        d.sel = h.sel;
+        d.estride = h.estride;
+        d.ksel = h.ksel > 0 ? h.ksel : 1;
+        d.emax = h.emax > 0 ? h.emax : 1;
         d.type = h.type; d.K = h.K; d.N = start; d.nparts = h.nparts;
         d.x_stride = h.nparts > 1 ? h.x_stride : 0;
         d.pn = equal ? h.rows[0] : 0;
@@ -1863,6 +2000,35 @@ int kqk_launch_mx(int type, const int* plan, long lds, int grid, const void* w, 
     case T_NIB: return launch_mx_t<T_NIB>(a, plan[1], whole, lds, st);
     default: return (int)hipErrorInvalidValue;
     }
+}
+
+// MoE: top-k per token (E <= 4096), and the expert groups of a selection
+int kqk_launch_moe_topk(const float* probs, int B, int E, int k, int* sel, float* selw,
+                        hipStream_t st) {
+    if (B < 1 || E < 1 || E > 4096 || k < 1) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(kq_moe_topk_kernel, dim3((B + 3) / 4), dim3(256), 0, st, probs, B, E, k,
+                       sel, selw);
+    return (int)hipGetLastError();
+}
+
+long kqk_mx_group_bytes(void) { return (long)sizeof(MxGroup); }
+
+int kqk_launch_moe_group(const int* sel, int nm, int E, int nt, int x_div, const void* w0,
+                         const void* w1, float* y0, float* y1, long estride, void* groups,
+                         int* ng, hipStream_t st) {
+    if (nm < 1 || E < 1 || E > 4096 || nt < 1 || nt > 2 || x_div < 1) return (int)hipErrorInvalidValue;
+    MoeGroupArg a;
+    a.sel = sel; a.nm = nm; a.E = E; a.nt = nt; a.x_div = x_div;
+    a.w[0] = static_cast<const uint8_t*>(w0);
+    a.w[1] = static_cast<const uint8_t*>(nt > 1 ? w1 : w0);
+    a.y[0] = y0;
+    a.y[1] = nt > 1 ? y1 : y0;
+    a.estride = estride;
+    a.groups = static_cast<MxGroup*>(groups);
+    a.ng = ng;
+    const size_t lds = (size_t)(2 * E + nm) * sizeof(int);
+    hipLaunchKernelGGL(kq_moe_group_kernel, dim3(1), dim3(1024), lds, st, a);
+    return (int)hipGetLastError();
 }
 
 int kqk_launch_dequant(int type, const void* w, float* y, long nblocks, hipStream_t st) {

@@ -31,6 +31,9 @@ typedef struct {
     int rows[KQ_MAX_GROUPS];
     const float* x;
     int type, K, nparts, x_stride;
+    const int* sel;          /* MoE gather: part p uses expert sel[p % ksel] */
+    long estride;            /* bytes per expert */
+    int ksel, emax;
 } kqk_seg;
 #define KQK_LIST_MAX 4   /* parts of unequal sizes one launcher segment takes */
 long kqk_segs_lds(const kqk_seg* segs, int nseg, int grid, int* xs_off, int* terms_off,
@@ -49,6 +52,13 @@ int kqk_launch_mx(int type, const int* plan, long lds, int grid, const void* w, 
                   const void* gdev, const int* ngdev, const float* X, long x_stride, float* Y,
                   long y_stride, int N, int K, hipStream_t st);
 int kqk_mx_set_max_lds(int bytes);
+/* MoE: top-k per token; the expert groups (MxGroup records) of a selection */
+int kqk_launch_moe_topk(const float* probs, int B, int E, int k, int* sel, float* selw,
+                        hipStream_t st);
+long kqk_mx_group_bytes(void);
+int kqk_launch_moe_group(const int* sel, int nm, int E, int nt, int x_div, const void* w0,
+                         const void* w1, float* y0, float* y1, long estride, void* groups,
+                         int* ng, hipStream_t st);
 
 #define KQ_MAX_REGIONS 16
 
@@ -71,6 +81,7 @@ typedef struct {
     float* d_x; size_t cap_x;
     float* d_y; size_t cap_y;
     float* d_a; size_t cap_a;
+    float* d_moe; size_t cap_moe;   /* MoE expert groups + their count */
     char err[512];
 } kq_state;
 
@@ -184,6 +195,7 @@ void kq_linear_shutdown(void) {
     if (g_kq.d_x) (void)hipFree(g_kq.d_x);
     if (g_kq.d_y) (void)hipFree(g_kq.d_y);
     if (g_kq.d_a) (void)hipFree(g_kq.d_a);
+    if (g_kq.d_moe) (void)hipFree(g_kq.d_moe);
     if (g_kq.ready && g_kq.stream) (void)hipStreamDestroy(g_kq.stream);
     memset(&g_kq, 0, sizeof g_kq);
 }
@@ -501,4 +513,164 @@ int kq_q4k_group(const float* x, int K,
         off += (size_t)Ns[i];
     }
     return hip_ok(hipStreamSynchronize(g_kq.stream), "synchronize");
+}
+
+/* ------------------------------------------------------------ MoE gather */
+
+int64_t kq_moe_slice_bytes(const kq_tensor* t, int K_in, int N_out) {
+    /* stratum_arch_moe.inc.c:220-238 */
+    if (!t || K_in <= 0 || N_out <= 0) return -1;
+    if (t->type == 43)   /* Q4K_W16: w16 + d/dm per 256 + m16 */
+        return (int64_t)N_out * K_in * 2 + (int64_t)N_out * (K_in / 256) * 8 +
+               (int64_t)N_out * (K_in / 32) * 2;
+    if (t->type == 44)   /* Q6K_W16: the same without the m16 section */
+        return (int64_t)N_out * K_in * 2 + (int64_t)N_out * (K_in / 256) * 8;
+    const int64_t one = (int64_t)K_in * N_out;
+    if (t->nbytes <= 0 || t->nelem <= 0) {
+        const int bb = block_bytes((int)t->type);
+        return bb ? one / 256 * bb : -1;
+    }
+    int64_t e_all = t->nelem / one;
+    if (e_all < 1) e_all = 1;
+    return t->nbytes / e_all;
+}
+
+void kq_moe_bind_slice(kq_tensor* dst, const kq_tensor* t, int e, int64_t slice, int N_out,
+                       int K_in, const uint8_t* slice_host, const uint8_t* base) {
+    /* stratum_arch_moe.inc.c:327-337 */
+    *dst = *t;
+    dst->nelem = (int64_t)K_in * N_out;
+    dst->nbytes = slice;
+    dst->offset = slice_host ? (uint64_t)(slice_host - base)
+                             : t->offset + (uint64_t)e * (uint64_t)slice;
+}
+
+int kq_moe_pack_open(const uint8_t* base, size_t size, int n_layers, int n_experts, int n_embed,
+                     int n_ff, const kq_tensor* gate, const kq_tensor* up, const kq_tensor* down,
+                     kq_moe_pack* out) {
+    /* the header checks of moe_pack_load (stratum_arch_moe.inc.c:506-525) */
+    kq_moe_pack_hdr h;
+    if (!base || !out || !gate || !up || !down) return kq_fail("kq_moe_pack_open: NULL argument");
+    if (size < sizeof h) return kq_fail("MOE_PACK: not a pack file");
+    memcpy(&h, base, sizeof h);
+    const int64_t gsb = kq_moe_slice_bytes(gate, n_embed, n_ff);
+    const int64_t usb = kq_moe_slice_bytes(up, n_embed, n_ff);
+    const int64_t dsb = kq_moe_slice_bytes(down, n_ff, n_embed);
+    int ok = memcmp(h.magic, "MOEP", 4) == 0 && h.version == 1 &&
+             (int)h.n_layers == n_layers && (int)h.n_experts == n_experts &&
+             (int)h.n_embed == n_embed && (int)h.n_ff == n_ff && h.gate_type == gate->type &&
+             h.up_type == up->type && h.down_type == down->type &&
+             h.gate_slice == (uint64_t)gsb && h.up_slice == (uint64_t)usb &&
+             h.down_slice == (uint64_t)dsb && h.data_off >= sizeof h && h.data_off < size;
+    const uint64_t stride = h.gate_slice + h.up_slice + h.down_slice;
+    const uint64_t need = h.data_off + (uint64_t)n_layers * (uint64_t)n_experts * stride;
+    if (ok && need > size) ok = 0;
+    if (!ok) return kq_fail("MOE_PACK: the pack does not match this model");
+    out->base = base;
+    out->size = size;
+    out->data_off = h.data_off;
+    out->gate_slice = h.gate_slice;
+    out->up_slice = h.up_slice;
+    out->down_slice = h.down_slice;
+    out->stride = stride;
+    out->n_layers = h.n_layers;
+    out->n_experts = h.n_experts;
+    return 0;
+}
+
+const uint8_t* kq_moe_pack_which(const kq_moe_pack* p, int li, int e, int which) {
+    /* stratum_arch_moe.inc.c:307-313 */
+    uint64_t off = p->data_off + ((uint64_t)li * (uint64_t)p->n_experts + (uint64_t)e) * p->stride;
+    if (which == 1) off += p->gate_slice;
+    else if (which == 2) off += p->gate_slice + p->up_slice;
+    return p->base + off;
+}
+
+void kq_moe_topk(const float* w, int E, int K, int* sel, float* selw) {
+    /* stratum_arch_moe.inc.c:368-385: insertion on a strictly greater
+     * weight, so equal weights keep the lower expert id first */
+    for (int s = 0; s < K; s++) { sel[s] = -1; selw[s] = -1.0f; }
+    for (int e = 0; e < E; e++) {
+        const float ww = w[e];
+        for (int s = 0; s < K; s++) {
+            if (ww > selw[s]) {
+                for (int t2 = K - 1; t2 > s; t2--) {
+                    sel[t2] = sel[t2 - 1];
+                    selw[t2] = selw[t2 - 1];
+                }
+                sel[s] = e;
+                selw[s] = ww;
+                break;
+            }
+        }
+    }
+}
+
+int kq_moe_topk_dev(const float* probs, int B, int E, int k, int* sel, float* selw,
+                    kq_stream stream) {
+    if (kq_ready()) return -1;
+    if (!probs || !sel || !selw) return kq_fail("kq_moe_topk_dev: NULL pointer");
+    if (B < 1 || E < 1 || E > KQ_MOE_MAX_EXPERTS || k < 1 || k > E)
+        return kq_fail("kq_moe_topk_dev: B=%d E=%d k=%d", B, E, k);
+    const int e = kqk_launch_moe_topk(probs, B, E, k, sel, selw, pick(stream));
+    if (e) return kq_fail("moe top-k launch: %s", hipGetErrorString((hipError_t)e));
+    return 0;
+}
+
+int kq_moe_gemv_dev(const kq_moe_op* op, const int* sel, int B, int k, int E, kq_stream stream) {
+    if (!op || !sel) return kq_fail("kq_moe_gemv_dev: NULL argument");
+    if (check_shape(op->type, op->n_out, op->k_in) || kq_ready()) return -1;
+    const int nt = op->ntensors;
+    if (nt < 1 || nt > 2) return kq_fail("kq_moe_gemv_dev: ntensors=%d", nt);
+    if (B < 1 || B > KQ_MOE_MAX_TOKENS || k < 1 || k > KQ_MAX_GROUPS || E < 1 ||
+        E > KQ_MOE_MAX_EXPERTS)
+        return kq_fail("kq_moe_gemv_dev: B=%d k=%d E=%d", B, k, E);
+    if (op->x_div != 1 && op->x_div != k)
+        return kq_fail("kq_moe_gemv_dev: x_div must be 1 or k");
+    if (!op->x || ((uintptr_t)op->x & 15)) return kq_fail("kq_moe_gemv_dev: x NULL or unaligned");
+    const int64_t rb = kq_row_bytes(op->type, op->k_in);
+    if (op->expert_stride < rb * op->n_out)
+        return kq_fail("kq_moe_gemv_dev: expert_stride below the slice size");
+    for (int t = 0; t < nt; t++)
+        if (!op->w[t] || !op->y[t]) return kq_fail("kq_moe_gemv_dev: NULL w or y");
+    hipStream_t st = pick(stream);
+    if (B == 1) {
+        /* one token: the single-stream kernel, part r of tensor t on expert
+         * sel[r] (read on the device) */
+        kqk_seg h[2];
+        memset(h, 0, sizeof h);
+        for (int t = 0; t < nt; t++) {
+            for (int r = 0; r < k; r++) {
+                h[t].w[r] = op->w[t];
+                h[t].y[r] = op->y[t] + (size_t)r * op->n_out;
+                h[t].rows[r] = op->n_out;
+            }
+            h[t].type = op->type; h[t].K = op->k_in; h[t].nparts = k;
+            h[t].x = op->x;
+            h[t].x_stride = op->x_div == 1 && k > 1 ? op->k_in : 0;
+            h[t].sel = sel;
+            h[t].estride = (long)op->expert_stride;
+            h[t].ksel = k;
+            h[t].emax = E;
+        }
+        return launch_segs(h, nt, st);
+    }
+    /* several tokens: expert groups built on the device, then one weight
+     * pass per selected expert for all of its tokens */
+    const int nm = B * k, ngmax = nt * (E < nm ? E : nm);
+    const size_t gbytes = (size_t)kqk_mx_group_bytes();
+    if (grow(&g_kq.d_moe, &g_kq.cap_moe, (ngmax * gbytes + 64) / sizeof(float) + 1)) return -1;
+    void* groups = g_kq.d_moe;
+    int* ng = (int*)((uint8_t*)g_kq.d_moe + ngmax * gbytes);
+    int e = kqk_launch_moe_group(sel, nm, E, nt, op->x_div, op->w[0], op->w[nt - 1], op->y[0],
+                                 op->y[nt - 1], (long)op->expert_stride, groups, ng, st);
+    if (e) return kq_fail("moe group launch: %s", hipGetErrorString((hipError_t)e));
+    const int grid = plan_grid();
+    int plan[KQK_MX_PLAN];
+    const long lds = kqk_mx_plan(op->type, op->n_out, op->k_in, B, ngmax, grid, g_kq.lds_max, plan);
+    if (lds < 0) return kq_fail("kq_moe_gemv_dev: no launch plan for K=%d", op->k_in);
+    e = kqk_launch_mx(op->type, plan, lds, grid, NULL, 0, groups, ng, op->x, op->k_in, NULL,
+                      op->n_out, op->n_out, op->k_in, st);
+    if (e) return kq_fail("moe gemv launch: %s", hipGetErrorString((hipError_t)e));
+    return 0;
 }

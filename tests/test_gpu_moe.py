@@ -1,0 +1,229 @@
+"""GPU parity of the MoE gather (through the C ABI): device top-k against
+the oracle's moe_topk, and the routed expert GEMVs against the
+single-stream GEMV of each selected slice (bit for bit) and the oracle
+(within the GEMV bound), for one token and for batches whose tokens share
+experts (stratum_arch_moe.inc.c:605-755, 817-1267)."""
+import numpy as np
+import pytest
+
+import stratum_amd as K
+from conftest import same_values
+from oracle import oracle as O
+from stratum_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    K.lib()
+    yield
+    torch.cuda.synchronize()
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def softmax_rows(logits):
+    z = logits - logits.max(axis=1, keepdims=True)
+    p = np.exp(z.astype(np.float64))
+    return (p / p.sum(axis=1, keepdims=True)).astype(np.float32)
+
+
+def gpu_topk(probs, k):
+    B, E = probs.shape
+    dp = dev(probs)
+    sel = torch.empty(B * k, dtype=torch.int32, device="cuda")
+    selw = torch.empty(B * k, dtype=torch.float32, device="cuda")
+    K.moe_topk_dev(dp.data_ptr(), B, E, k, sel.data_ptr(), selw.data_ptr(), stream())
+    torch.cuda.synchronize()
+    return sel.cpu().numpy().reshape(B, k), selw.cpu().numpy().reshape(B, k)
+
+
+@pytest.mark.parametrize("B,E,k", [(16, 128, 8), (1, 128, 8), (5, 100, 6), (3, 4096, 8),
+                                   (2, 5, 5), (4, 64, 1)])
+def test_topk_dev_matches_oracle(port, B, E, k):
+    r = np.random.default_rng(B * 1000 + E + k)
+    probs = softmax_rows(r.standard_normal((B, E)).astype(np.float32))
+    sel, selw = gpu_topk(probs, k)
+    for s in range(B):
+        ws, ww = port.topk(probs[s], k)
+        assert list(sel[s]) == ws, s
+        assert same_values(selw[s], ww), s
+
+
+def test_topk_dev_ties_and_ineligible(port):
+    """Equal weights keep the lower expert first; weights <= -1 and NaN are
+    never chosen; missing slots are (-1, -1.0f)."""
+    rows = [
+        np.array([0.1, 0.3, 0.3, 0.2, 0.3, 0.05] + [0.0] * 94, np.float32),
+        np.full(100, 0.125, np.float32),
+        np.array([-2.0, -1.0, -0.5, np.nan, 0.0, -0.0] + [-1.0] * 94, np.float32),
+        np.array([-3.0] * 99 + [-1.0], np.float32),
+    ]
+    probs = np.stack(rows)
+    for k in (1, 3, 8):
+        sel, selw = gpu_topk(probs, k)
+        for s in range(len(rows)):
+            ws, ww = port.topk(probs[s], k)
+            assert list(sel[s]) == ws, (s, k)
+            assert same_values(selw[s], ww), (s, k)
+
+
+def experts(qtype, n_exp, N_out, K_in, seed):
+    """Stacked expert tensor: expert e's slice is rows [e*N_out, (e+1)*N_out)."""
+    return synth.tensor(qtype, n_exp * N_out, K_in, seed)
+
+
+def single(qtype, w_slice, x, N, K_in):
+    dw, dx = dev(w_slice), dev(x)
+    dy = torch.empty(N, dtype=torch.float32, device="cuda")
+    K.gemv_dev(qtype, dw.data_ptr(), dx.data_ptr(), dy.data_ptr(), N, K_in, stream=stream())
+    torch.cuda.synchronize()
+    return dy.cpu().numpy()
+
+
+def run_moe(qtype, wts, sel, x, x_div, B, k, n_exp, N_out, K_in, stride=None, w_off=None):
+    """kq_moe_gemv_dev over the stacked tensors wts (or one buffer with
+    per-tensor offsets w_off and expert stride `stride`)."""
+    nt = len(wts) if w_off is None else len(w_off)
+    if w_off is None:
+        dws = [dev(w) for w in wts]
+        ptrs = [d.data_ptr() for d in dws]
+        stride = N_out * K.lib().kq_row_bytes(qtype, K_in)
+    else:
+        dws = [dev(wts[0])]
+        ptrs = [dws[0].data_ptr() + o for o in w_off]
+    dx = dev(x)
+    ys = [torch.full((B * k * N_out,), float("nan"), dtype=torch.float32, device="cuda")
+          for _ in range(nt)]
+    dsel = dev(np.asarray(sel, np.int32).reshape(-1))
+    op = K.moe_op(qtype, N_out, K_in, ptrs, stride, dx.data_ptr(), x_div,
+                  [y.data_ptr() for y in ys])
+    K.moe_gemv_dev(op, dsel.data_ptr(), B, k, n_exp, stream())
+    torch.cuda.synchronize()
+    return [y.cpu().numpy().reshape(B * k, N_out) for y in ys]
+
+
+def check_members(port, qtype, wts, sel, x, x_div, got, N_out, K_in, n_oracle=3):
+    rb = K.lib().kq_row_bytes(qtype, K_in)
+    sl = N_out * rb
+    sel = np.asarray(sel).reshape(-1)
+    checked = 0
+    for t, w in enumerate(wts):
+        for m, e in enumerate(sel):
+            if e < 0:
+                continue
+            xm = x[(m // x_div) * K_in:(m // x_div + 1) * K_in]
+            ws = w[e * sl:(e + 1) * sl]
+            assert same_values(got[t][m], single(qtype, ws, xm, N_out, K_in)), (t, m, e)
+            if checked < n_oracle:
+                want = port.gemv(qtype, ws, xm, N_out, K_in)
+                err = O.rel_err(got[t][m], want).max()
+                assert err <= 1e-5, (t, m, e, err)
+                checked += 1
+
+
+@pytest.mark.parametrize("qtype", [12, 14])
+def test_moe_one_token_gate_up_and_down(port, qtype):
+    """Batch 1: gate and up (one x) in one launch, down (one activation per
+    rank) in another; each rank's output equals its slice's single GEMV."""
+    n_exp, H, F, k = 32, 512, 256, 8
+    gate, up = experts(qtype, n_exp, F, H, 1), experts(qtype, n_exp, F, H, 2)
+    down = experts(qtype, n_exp, H, F, 3)
+    r = np.random.default_rng(4)
+    sel = r.choice(n_exp, k, replace=False).astype(np.int32)
+    x = synth.gaussian(r, H)
+    got = run_moe(qtype, [gate, up], sel, x, k, 1, k, n_exp, F, H)
+    check_members(port, qtype, [gate, up], sel, x, k, got, F, H)
+    act = np.stack([synth.gaussian(r, F) for _ in range(k)]).reshape(-1)
+    got = run_moe(qtype, [down], sel, act, 1, 1, k, n_exp, H, F)
+    check_members(port, qtype, [down], sel, act, 1, got, H, F)
+
+
+@pytest.mark.parametrize("qtype", [12, 14, 10])
+@pytest.mark.parametrize("B,n_exp", [(16, 32), (16, 128), (3, 8), (64, 16)])
+def test_moe_batch_grouped(port, qtype, B, n_exp):
+    """Batches whose tokens share experts: each selected slice is streamed
+    once for all its tokens; every member still equals its single GEMV."""
+    H, F, k = 512, 256, min(8, n_exp)
+    gate, up = experts(qtype, n_exp, F, H, 11), experts(qtype, n_exp, F, H, 12)
+    down = experts(qtype, n_exp, H, F, 13)
+    r = np.random.default_rng(B + n_exp)
+    probs = softmax_rows(r.standard_normal((B, n_exp)).astype(np.float32))
+    sel = np.stack([port.topk(probs[s], k)[0] for s in range(B)]).astype(np.int32)
+    x = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
+    got = run_moe(qtype, [gate, up], sel, x, k, B, k, n_exp, F, H)
+    check_members(port, qtype, [gate, up], sel, x, k, got, F, H)
+    act = np.stack([synth.gaussian(r, F) for _ in range(B * k)]).reshape(-1)
+    got = run_moe(qtype, [down], sel, act, 1, B, k, n_exp, H, F)
+    check_members(port, qtype, [down], sel, act, 1, got, H, F)
+
+
+def test_moe_pack_layout_and_unselected_slots(port):
+    """Expert slices in a pack (gate|up|down per expert, stride = their sum),
+    with some ranks unselected (sel -1): the selected ranks are exact."""
+    qtype, n_exp, H, F, B, k = 12, 12, 512, 256, 6, 4
+    rb_g = K.lib().kq_row_bytes(qtype, H)
+    rb_d = K.lib().kq_row_bytes(qtype, F)
+    gsl, dsl = F * rb_g, H * rb_d
+    stride = 2 * gsl + dsl
+    gate, up = experts(qtype, n_exp, F, H, 21), experts(qtype, n_exp, F, H, 22)
+    down = experts(qtype, n_exp, H, F, 23)
+    pack = np.concatenate([np.concatenate([gate[e * gsl:(e + 1) * gsl], up[e * gsl:(e + 1) * gsl],
+                                           down[e * dsl:(e + 1) * dsl]]) for e in range(n_exp)])
+    r = np.random.default_rng(24)
+    sel = np.stack([r.choice(n_exp, k, replace=False) for _ in range(B)]).astype(np.int32)
+    sel[1, 2:] = -1
+    sel[4, 3] = -1
+    x = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
+    got = run_moe(qtype, [pack], sel, x, k, B, k, n_exp, F, H, stride=stride, w_off=[0, gsl])
+    check_members(port, qtype, [gate, up], sel, x, k, got, F, H)
+    act = np.stack([synth.gaussian(r, F) for _ in range(B * k)]).reshape(-1)
+    got = run_moe(qtype, [pack], sel, act, 1, B, k, n_exp, H, F, stride=stride, w_off=[2 * gsl])
+    check_members(port, qtype, [down], sel, act, 1, got, H, F)
+
+
+@pytest.mark.parametrize("B", [1, 16])
+def test_moe_config_routed_on_device(port, B):
+    """The MoE configuration (128 experts, top-8, hidden 2048, expert ffn
+    768, Q4_K): router probabilities -> device top-k -> gate/up gather, the
+    selection feeding the GEMV without leaving the device; sampled members
+    against the oracle and their single GEMVs."""
+    qtype, n_exp, H, F, k = 12, 128, 2048, 768, 8
+    gate, up = experts(qtype, n_exp, F, H, 31), experts(qtype, n_exp, F, H, 32)
+    r = np.random.default_rng(33 + B)
+    probs = softmax_rows(r.standard_normal((B, n_exp)).astype(np.float32))
+    x = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
+    dp = dev(probs)
+    dsel = torch.empty(B * k, dtype=torch.int32, device="cuda")
+    dselw = torch.empty(B * k, dtype=torch.float32, device="cuda")
+    K.moe_topk_dev(dp.data_ptr(), B, n_exp, k, dsel.data_ptr(), dselw.data_ptr(), stream())
+    dg, du, dx = dev(gate), dev(up), dev(x)
+    ys = [torch.empty(B * k * F, dtype=torch.float32, device="cuda") for _ in range(2)]
+    op = K.moe_op(qtype, F, H, [dg.data_ptr(), du.data_ptr()],
+                  F * K.lib().kq_row_bytes(qtype, H), dx.data_ptr(), k, [y.data_ptr() for y in ys])
+    K.moe_gemv_dev(op, dsel.data_ptr(), B, k, n_exp, stream())
+    torch.cuda.synchronize()
+    sel = dsel.cpu().numpy().reshape(B, k)
+    for s in range(B):
+        assert list(sel[s]) == port.topk(probs[s], k)[0]
+    got = [y.cpu().numpy().reshape(B * k, F) for y in ys]
+    members = [0, B * k - 1] if B > 1 else [0, 7]
+    sl = F * K.lib().kq_row_bytes(qtype, H)
+    for t, w in enumerate([gate, up]):
+        for m in members:
+            e = sel.reshape(-1)[m]
+            xm = x[(m // k) * H:(m // k + 1) * H]
+            ws = w[e * sl:(e + 1) * sl]
+            assert same_values(got[t][m], single(qtype, ws, xm, F, H)), (t, m)
+            assert O.rel_err(got[t][m], port.gemv(qtype, ws, xm, F, H)).max() <= 1e-5
