@@ -816,6 +816,11 @@ constexpr int MAXG = 16;
 // The fields a segment needs first come first (one scalar load).
 struct Seg {
     const float* x;
+    // MoE gather (nullptr: unused): part p's weights are w[p] plus
+    // sel[p % ksel] expert strides, the expert index read on the device
+    // (clamped to [0, emax)).  Read with the leading fields: the part mode
+    // depends on it.
+    const int* sel;
     int type, K, N, nparts, x_stride;
     int pn;            // rows per part when every part has the same count, else 0
     uint32_t pn_m;     // magic multiplier for division by pn (0: pn <= 1)
@@ -826,19 +831,15 @@ struct Seg {
     float* y[MAXG];
     const float* add[MAXG];
     int start[MAXG];
-    // MoE gather (nullptr: unused): part p's weights are w[p] plus
-    // sel[p % ksel] expert strides, the expert index read on the device
-    // (clamped to [0, emax))
-    const int* sel;
-    long estride;
-    int ksel, emax;
+    long estride;      // MoE gather: bytes per expert,
+    int ksel, emax;    // the selection period and the expert count
 };
 
 // Issues the scalar loads of a segment's leading fields together and waits
 // for them once: used as they are needed, the fields would be fetched in
 // several dependent round trips to the kernel-argument memory.
 __device__ __forceinline__ void prefetch_seg(const Seg& S) {
-    asm volatile("" ::"s"(S.x), "s"(S.type), "s"(S.K), "s"(S.N), "s"(S.nparts),
+    asm volatile("" ::"s"(S.x), "s"(S.sel), "s"(S.type), "s"(S.K), "s"(S.N), "s"(S.nparts),
                  "s"(S.x_stride), "s"(S.pn), "s"(S.pn_m), "s"(S.pn_l), "s"(S.nc_m), "s"(S.nc_l),
                  "s"(S.w[0]), "s"(S.y[0]), "s"(S.add[0]));
 }
@@ -880,7 +881,9 @@ constexpr int SCR_BYTES = SCR_TABS + 3 * 8 * MAXG;
 // same-input group: the part of a row by comparing with the part starts,
 // its base by selection); or up to 16 equal parts (MoE experts: the part of
 // a row by division, its base from an LDS table).
-constexpr int PM_ONE = 0, PM_LIST = 1, PM_EQUAL = 2;
+// PM_SEL: PM_EQUAL whose part bases are moved by a device-side expert
+// selection (the MoE gather kernels only).
+constexpr int PM_ONE = 0, PM_LIST = 1, PM_EQUAL = 2, PM_SEL = 3;
 constexpr int LIST_MAX = 4;
 
 template <typename V>
@@ -896,7 +899,7 @@ __device__ __forceinline__ uint32_t part_of(const Seg& S, uint32_t r, uint32_t& 
         return 0;
     }
     uint32_t g;
-    if (PM == PM_EQUAL) {
+    if (PM >= PM_EQUAL) {
         g = div_magic(r, S.pn_m, S.pn_l);
         rg = r - g * (uint32_t)S.pn;
         return g;
@@ -998,7 +1001,7 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
     const float** atab = reinterpret_cast<const float**>(smem + A.scr_off + SCR_TABS + 16 * MAXG);
     const int ngx = (PM != PM_ONE && S.x_stride) ? S.nparts : 1;
 
-    if (PM == PM_EQUAL) {
+    if (PM >= PM_EQUAL) {
         // each wave writes the part tables itself (identical values), so its
         // own reads need no barrier
         const uint8_t* wv = S.w[0];
@@ -1011,7 +1014,7 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
             av = lane == g ? S.add[g] : av;
         }
         if (lane < S.nparts) {
-            if (S.sel) {                          // the expert chosen on the device
+            if (PM == PM_SEL) {                   // the expert chosen on the device
                 const int e = min(max(S.sel[lane % S.ksel], 0), S.emax - 1);
                 wv += (size_t)e * S.estride;
             }
@@ -1127,6 +1130,8 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
 // types present, so a single-type launch carries one type's code and the
 // register allocation is not constrained by the others.
 constexpr int TB_Q4K = 1, TB_Q6K = 2, TB_Q2K = 4, TB_NIB = 8, TB_ALL = 15;
+// TB_SEL: the MoE gather instantiations (every segment has a selection)
+constexpr int TB_SEL = 16;
 
 // MULTI = false: the launch has exactly one segment (no segment loop, so
 // no state flows between segments and the compiler's wait analysis stays
@@ -1145,20 +1150,22 @@ __global__ __launch_bounds__(1024) void kq_segs_kernel(SegsArg A) {
     Staged st = {nullptr, 0, -1, 0, 0, 0, false};
     // a single-type instantiation does not read the segment types (the host
     // launches it only for segment lists of that type)
-    constexpr bool SINGLE = TYPES == TB_Q4K || TYPES == TB_Q6K || TYPES == TB_Q2K || TYPES == TB_NIB;
+    constexpr bool SELK = (TYPES & TB_SEL) != 0;    // MoE gather: every segment has sel
+    constexpr int TYB = TYPES & TB_ALL;
+    constexpr bool SINGLE = TYB == TB_Q4K || TYB == TB_Q6K || TYB == TB_Q2K || TYB == TB_NIB;
     for (int i = 0; i < nseg; i++) {
         const Seg& S = A.s[i];
         if (i) prefetch_seg(S);
-        const int pm = S.sel ? PM_EQUAL
-                     : S.nparts == 1 ? PM_ONE : S.nparts <= LIST_MAX ? PM_LIST : PM_EQUAL;
+        const int pm = S.nparts == 1 ? PM_ONE : S.nparts <= LIST_MAX ? PM_LIST : PM_EQUAL;
         const bool last = i == nseg - 1;
 #define KQ_RUN(T_)                                                                   \
-        if (pm == PM_ONE) run_segment<T_, DEPTH, PM_ONE>(S, A, i, st, smem, last);   \
+        if (SELK) run_segment<T_, DEPTH, PM_SEL>(S, A, i, st, smem, last);           \
+        else if (pm == PM_ONE) run_segment<T_, DEPTH, PM_ONE>(S, A, i, st, smem, last); \
         else if (pm == PM_LIST) run_segment<T_, DEPTH, PM_LIST>(S, A, i, st, smem, last); \
         else run_segment<T_, DEPTH, PM_EQUAL>(S, A, i, st, smem, last);
         if (SINGLE) {
-            constexpr int TY = TYPES == TB_Q4K ? T_Q4K : TYPES == TB_Q6K ? T_Q6K
-                             : TYPES == TB_Q2K ? T_Q2K : T_NIB;
+            constexpr int TY = TYB == TB_Q4K ? T_Q4K : TYB == TB_Q6K ? T_Q6K
+                             : TYB == TB_Q2K ? T_Q2K : T_NIB;
             KQ_RUN(TY)
         } else {
             switch (S.type) {
@@ -1813,13 +1820,21 @@ typedef void (*segs_fn)(SegsArg);
 static const segs_fn k_segs[2][2][5] = {{KQ_SEGS_ROW(1, false), KQ_SEGS_ROW(2, false)},
                                         {KQ_SEGS_ROW(1, true), KQ_SEGS_ROW(2, true)}};
 #undef KQ_SEGS_ROW
+// the MoE gather (TB_SEL) instantiations, single type only
+#define KQ_SEL_ROW(D, M)                                                                  \
+    {&kq_segs_kernel<D, TB_Q4K | TB_SEL, M>, &kq_segs_kernel<D, TB_Q6K | TB_SEL, M>,       \
+     &kq_segs_kernel<D, TB_Q2K | TB_SEL, M>, &kq_segs_kernel<D, TB_NIB | TB_SEL, M>}
+static const segs_fn k_segs_sel[2][2][4] = {{KQ_SEL_ROW(1, false), KQ_SEL_ROW(2, false)},
+                                            {KQ_SEL_ROW(1, true), KQ_SEL_ROW(2, true)}};
+#undef KQ_SEL_ROW
 
 int kqk_set_max_lds(int bytes) {
     for (int m = 0; m < 2; m++)
         for (int d = 0; d < 2; d++)
-            for (int t = 0; t < 5; t++) {
+            for (int t = 0; t < 9; t++) {
+                const segs_fn f = t < 5 ? k_segs[m][d][t] : k_segs_sel[m][d][t - 5];
                 const hipError_t e =
-                    hipFuncSetAttribute(reinterpret_cast<const void*>(k_segs[m][d][t]),
+                    hipFuncSetAttribute(reinterpret_cast<const void*>(f),
                                         hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
                 if (e != hipSuccess) return (int)e;
             }
@@ -1872,8 +1887,11 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
     }
     const int t = set == TB_Q4K ? 0 : set == TB_Q6K ? 1 : set == TB_Q2K ? 2 : set == TB_NIB ? 3 : 4;
     if (t == 4) depth = 1;   // the all-types kernel fits 128 VGPRs at depth 1 only
-    hipLaunchKernelGGL(k_segs[nseg > 1][depth - 1][t], dim3(grid), dim3(threads),
-                       (size_t)lds_bytes, st, A);
+    int nsel = 0;
+    for (int i = 0; i < nseg; i++) nsel += segs[i].sel != nullptr;
+    if (nsel && (nsel != nseg || t == 4)) return (int)hipErrorInvalidValue;
+    const segs_fn f = nsel ? k_segs_sel[nseg > 1][depth - 1][t] : k_segs[nseg > 1][depth - 1][t];
+    hipLaunchKernelGGL(f, dim3(grid), dim3(threads), (size_t)lds_bytes, st, A);
     return (int)hipGetLastError();
 }
 

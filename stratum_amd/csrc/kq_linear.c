@@ -639,21 +639,27 @@ int kq_moe_gemv_dev(const kq_moe_op* op, const int* sel, int B, int k, int E, kq
          * sel[r] (read on the device) */
         kqk_seg h[2];
         memset(h, 0, sizeof h);
+        /* gate and up on one x: one row space of 2k parts (part p uses
+         * sel[p % k]); else one segment per tensor */
+        const int one = nt == 2 && op->x_div == k && 2 * k <= KQ_MAX_GROUPS;
+        const int nh = one ? 1 : nt;
         for (int t = 0; t < nt; t++) {
+            kqk_seg* g = &h[one ? 0 : t];
+            const int p0 = one ? t * k : 0;
             for (int r = 0; r < k; r++) {
-                h[t].w[r] = op->w[t];
-                h[t].y[r] = op->y[t] + (size_t)r * op->n_out;
-                h[t].rows[r] = op->n_out;
+                g->w[p0 + r] = op->w[t];
+                g->y[p0 + r] = op->y[t] + (size_t)r * op->n_out;
+                g->rows[p0 + r] = op->n_out;
             }
-            h[t].type = op->type; h[t].K = op->k_in; h[t].nparts = k;
-            h[t].x = op->x;
-            h[t].x_stride = op->x_div == 1 && k > 1 ? op->k_in : 0;
-            h[t].sel = sel;
-            h[t].estride = (long)op->expert_stride;
-            h[t].ksel = k;
-            h[t].emax = E;
+            g->type = op->type; g->K = op->k_in; g->nparts = p0 + k;
+            g->x = op->x;
+            g->x_stride = op->x_div == 1 && k > 1 ? op->k_in : 0;
+            g->sel = sel;
+            g->estride = (long)op->expert_stride;
+            g->ksel = k;
+            g->emax = E;
         }
-        return launch_segs(h, nt, st);
+        return launch_segs(h, nh, st);
     }
     /* several tokens: expert groups built on the device, then one weight
      * pass per selected expert for all of its tokens */
