@@ -121,6 +121,195 @@ def load_traffic() -> dict | None:
     return json.load(open(path)).get(DOMINANT)
 
 
+# ---------------------------------------------------------------- other configs
+# BASELINE.json's other configurations, timed in the same run (their lines
+# in DESIGN.md): weights rotated over enough device copies that each pass
+# reads HBM (>= 600 MB rotating set), HIP events on the launch stream.
+QWEN06B = [  # name, type, N, K, activation (hidden 1024, q 2048, ffn 3072)
+    ("attn_q", KQ.TYPE_Q4_K, 2048, 1024, "h"),
+    ("attn_k", KQ.TYPE_Q4_K, 1024, 1024, "h"),
+    ("attn_v", KQ.TYPE_Q4_K, 1024, 1024, "h"),
+    ("attn_output", KQ.TYPE_Q4_K, 1024, 2048, "attn"),
+    ("ffn_gate", KQ.TYPE_Q4_K, 3072, 1024, "h"),
+    ("ffn_up", KQ.TYPE_Q4_K, 3072, 1024, "h"),
+    ("ffn_down", KQ.TYPE_Q6_K, 1024, 3072, "ff"),
+]
+QWEN06B_GROUPS = [["attn_q", "attn_k", "attn_v"], ["attn_output"], ["ffn_gate", "ffn_up"],
+                  ["ffn_down"]]
+ROTATE_BYTES = 600 << 20
+
+
+def _events_us(torch, stream, fn, reps, warmup=3):
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for i in range(reps):
+        fn(i)
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / reps
+
+
+def _copies(torch, host: np.ndarray, min_copies: int = 3):
+    n = max(min_copies, -(-ROTATE_BYTES // max(1, host.size)))
+    d = torch.from_numpy(host).cuda()
+    return [d] + [d.clone() for _ in range(n - 1)]
+
+
+def _check(L, rc):
+    if rc != 0:
+        raise RuntimeError(L.kq_last_error().decode())
+
+
+def other_configs(L, torch, stream, host_w) -> dict:
+    sh = stream.cuda_stream
+    out = {}
+
+    # one Q4_K GEMV, W 1024 x 1024 (4096 blocks), batch 1
+    w = synth.tensor(KQ.TYPE_Q4_K, 1024, 1024, 3000)
+    cw = _copies(torch, w)
+    x = torch.from_numpy(synth.gaussian(synth.rng(3001), 1024)).cuda()
+    y = torch.empty(1024, dtype=torch.float32, device="cuda")
+    us = _events_us(torch, stream, lambda i: _check(L, L.kq_gemv_dev(
+        12, cw[i % len(cw)].data_ptr(), x.data_ptr(), None, y.data_ptr(), 1024, 1024, sh)), 200)
+    nb = algo_bytes(12, 1024, 1024)
+    out["cfg1_q4k_1024x1024"] = {"us_per_call": round(us, 2), "bytes": nb,
+                                 "GB/s": round(nb / us / 1e3, 1)}
+    del cw
+
+    # Qwen3-0.6B layer set (4 launches) and the LM head
+    spec = {n: (t, N, K, xn) for n, t, N, K, xn in QWEN06B}
+    xl = {"h": 1024, "attn": 2048, "ff": 3072}
+    hw = {n: synth.tensor(t, N, K, 3100 + i) for i, (n, t, N, K, _) in enumerate(QWEN06B)}
+    offs, tot = {}, 0
+    for n in hw:
+        offs[n] = tot
+        tot += (hw[n].size + 255) // 256 * 256
+    blob = np.zeros(tot, np.uint8)
+    for n in hw:
+        blob[offs[n]:offs[n] + hw[n].size] = hw[n]
+    cb = _copies(torch, blob)
+    xq = {k: torch.from_numpy(synth.gaussian(synth.rng(3200 + j), n)).cuda()
+          for j, (k, n) in enumerate(xl.items())}
+    yq = {n: torch.empty(N, dtype=torch.float32, device="cuda") for n, _, N, _, _ in QWEN06B}
+    arrs = []
+    for c in cb:
+        per = []
+        for members in QWEN06B_GROUPS:
+            segs = [KQ.segment(spec[m][0], spec[m][2], spec[m][1], [c.data_ptr() + offs[m]],
+                               xq[spec[m][3]].data_ptr(), yq[m].data_ptr()) for m in members]
+            per.append(((KQ.KqSegment * len(segs))(*segs), len(segs)))
+        arrs.append(per)
+
+    def qstep(i):
+        for arr, n in arrs[i % len(arrs)]:
+            _check(L, L.kq_gemv_segments_dev(arr, n, sh))
+    us = _events_us(torch, stream, qstep, 100)
+    nb = sum(algo_bytes(t, N, K) for _, t, N, K, _ in QWEN06B)
+    res = {"us_per_layer_set": round(us, 2), "bytes": nb, "GB/s": round(nb / us / 1e3, 1),
+           "launches": len(QWEN06B_GROUPS)}
+    del cb, arrs
+    lm = synth.tensor(KQ.TYPE_Q6_K, 151936, 1024, 3300)
+    cl = _copies(torch, lm)
+    ylm = torch.empty(151936, dtype=torch.float32, device="cuda")
+    us = _events_us(torch, stream, lambda i: _check(L, L.kq_gemv_dev(
+        14, cl[i % len(cl)].data_ptr(), xq["h"].data_ptr(), None, ylm.data_ptr(), 151936, 1024,
+        sh)), 50)
+    nb = algo_bytes(14, 151936, 1024)
+    res["lm_head_q6k"] = {"us_per_call": round(us, 2), "bytes": nb, "GB/s": round(nb / us / 1e3, 1)}
+    out["cfg2_qwen3_0.6b"] = res
+    del cl
+
+    # configs[2] extra: gate + up as Q2_K and as type 42 (one launch of two tensors)
+    res = {}
+    q2 = [synth.tensor(KQ.TYPE_Q2_K, 17408, 5120, 3400 + i) for i in range(2)]
+    for t, name in ((KQ.TYPE_Q2_K, "q2k"), (KQ.TYPE_Q2K_NIB, "type42")):
+        ws = q2 if t == KQ.TYPE_Q2_K else [
+            np.concatenate([synth.q2k_to_nib(q[j:j + 84 * 20000]) for j in range(0, q.size, 84 * 20000)])
+            for q in q2]
+        both = np.concatenate(ws)
+        cg = _copies(torch, both)
+        xg = torch.from_numpy(synth.gaussian(synth.rng(3500), 5120)).cuda()
+        yg = [torch.empty(17408, dtype=torch.float32, device="cuda") for _ in range(2)]
+        half = ws[0].size
+        arrs = []
+        for c in cg:
+            segs = [KQ.segment(t, 5120, 17408, [c.data_ptr() + j * half], xg.data_ptr(),
+                               yg[j].data_ptr()) for j in range(2)]
+            arrs.append((KQ.KqSegment * 2)(*segs))
+        us = _events_us(torch, stream, lambda i: _check(L, L.kq_gemv_segments_dev(
+            arrs[i % len(arrs)], 2, sh)), 50)
+        nb = 2 * algo_bytes(t, 17408, 5120)
+        res[name] = {"us_per_launch": round(us, 2), "bytes": nb, "GB/s": round(nb / us / 1e3, 1)}
+        del cg, arrs
+    out["cfg3_gate_up_q2k_type42"] = res
+
+    # MULTISEQ, B streams with one weight pass (27B gate / up / down)
+    res = {}
+    for name, t, N, K in (("ffn_gate", 12, 17408, 5120), ("ffn_up", 12, 17408, 5120),
+                          ("ffn_down", 14, 5120, 17408)):
+        cm = _copies(torch, host_w[name])
+        for B in (8, 16, 64):
+            xs = torch.from_numpy(np.stack([synth.gaussian(synth.rng(3600 + s), K)
+                                            for s in range(B)])).cuda()
+            ysb = torch.empty(B * N, dtype=torch.float32, device="cuda")
+            us = _events_us(torch, stream, lambda i: _check(L, L.kq_gemv_multix_dev(
+                t, cm[i % len(cm)].data_ptr(), xs.data_ptr(), ysb.data_ptr(), B, N, K, sh)),
+                10 if B == 64 else 20)
+            nb = algo_bytes(t, N, K, B)
+            res[f"{name}_B{B}"] = {"us_per_call": round(us, 2), "us_per_stream": round(us / B, 2),
+                                   "GB/s": round(nb / us / 1e3, 1),
+                                   "TFLOP/s": round(2.0 * N * K * B / us / 1e6, 2)}
+        del cm
+    out["cfg4_multiseq_exact"] = res
+
+    # MoE gather, 128 experts, top-8, hidden 2048, expert ffn 768, Q4_K
+    E, H, F, k = 128, 2048, 768, 8
+    rbg, rbd = L.kq_row_bytes(12, H), L.kq_row_bytes(12, F)
+    gsl, dsl = F * rbg, H * rbd
+    ex = [synth.tensor(12, E * F, H, 3700), synth.tensor(12, E * F, H, 3701),
+          synth.tensor(12, E * H, F, 3702)]
+    stacked = np.concatenate(ex)
+    cm = _copies(torch, stacked, 2)
+    res = {}
+    for B in (1, 16):
+        r = np.random.default_rng(3800 + B)
+        lg = r.standard_normal((B, E)).astype(np.float32)
+        p = np.exp(lg - lg.max(1, keepdims=True))
+        probs = torch.from_numpy((p / p.sum(1, keepdims=True)).astype(np.float32)).cuda()
+        xm = torch.from_numpy(np.stack([synth.gaussian(r, H) for _ in range(B)])).cuda()
+        act = torch.from_numpy(np.stack([synth.gaussian(r, F) for _ in range(B * k)])).cuda()
+        sel = torch.empty(B * k, dtype=torch.int32, device="cuda")
+        selw = torch.empty(B * k, dtype=torch.float32, device="cuda")
+        yg, yu = (torch.empty(B * k * F, device="cuda") for _ in range(2))
+        yd = torch.empty(B * k * H, device="cuda")
+        ops = []
+        for c in cm:
+            base = c.data_ptr()
+            ops.append((KQ.moe_op(12, F, H, [base, base + E * gsl], gsl, xm.data_ptr(), k,
+                                  [yg.data_ptr(), yu.data_ptr()]),
+                        KQ.moe_op(12, H, F, [base + 2 * E * gsl], dsl, act.data_ptr(), 1,
+                                  [yd.data_ptr()])))
+
+        def moe_step(i):
+            _check(L, L.kq_moe_topk_dev(probs.data_ptr(), B, E, k, sel.data_ptr(),
+                                        selw.data_ptr(), sh))
+            gu, dn = ops[i % len(ops)]
+            _check(L, L.kq_moe_gemv_dev(ctypes.byref(gu), sel.data_ptr(), B, k, E, sh))
+            _check(L, L.kq_moe_gemv_dev(ctypes.byref(dn), sel.data_ptr(), B, k, E, sh))
+        us = _events_us(torch, stream, moe_step, 50)
+        distinct = len(set(sel.cpu().numpy().tolist()))
+        nb = distinct * (2 * gsl + dsl) + 4 * (B * H + 2 * B * k * F + B * k * F + B * k * H)
+        res[f"B{B}"] = {"us_per_layer": round(us, 2), "distinct_experts": distinct,
+                        "bytes": nb, "GB/s": round(nb / us / 1e3, 1),
+                        "launches": 3}
+    out["cfg5_moe_128e_top8"] = res
+    del cm
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -131,6 +320,8 @@ def main() -> int:
     ap.add_argument("--skip-separate", action="store_true",
                     help="do not time the 7-launch form (profiling runs: then every "
                          "kq_segs_kernel<1, 1, false> dispatch is the dominant launch)")
+    ap.add_argument("--main-only", action="store_true",
+                    help="time only the 27B layer set (skip BASELINE's other configurations)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 5 copies of 64 MiB (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -276,6 +467,9 @@ def main() -> int:
         },
         "cpu_baseline": None,
     }
+    if not args.main_only:
+        del copies, seg_arrays
+        out["other_configs"] = other_configs(L, torch, stream, host_w)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(host_w, xs_host)
     print(json.dumps(out), flush=True)

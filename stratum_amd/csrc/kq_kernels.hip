@@ -1264,7 +1264,8 @@ template <int TYPE, int S, bool WHOLE, bool SC>
 __device__ __forceinline__ void mx_sweep(const MxArg& A, const MxTasks& tk, wptr gw,
                                          double (&part)[MX_TW][S], int MC, int mc0,
                                          const int* d_xi, const float* sums, float4* xb0,
-                                         float4* xb1, int TC, int ntile) {
+                                         float4* xb1, int TC, int ntile,
+                                         typename Chunk<TYPE>::Raw first) {
     using TI = TypeInfo<TYPE>;
     using C = Chunk<TYPE>;
     const int tid = threadIdx.x, T = A.threads, GP = tk.GP;
@@ -1314,7 +1315,7 @@ __device__ __forceinline__ void mx_sweep(const MxArg& A, const MxTasks& tk, wptr
         tile_store(xv, xb0);
         __syncthreads();
     }
-    typename C::Raw nxt = C::load(wrow(0) + (size_t)(min(p, NC - 1) >> 2) * TI::BB, u);
+    typename C::Raw nxt = first;                  // issued before the x staging
     for (int ti = 0; ti < ntile; ti++) {
         const float4* xcur = (ti & 1) ? xb1 : xb0;
         const bool more = !WHOLE && ti + 1 < ntile;
@@ -1420,6 +1421,30 @@ __global__ __launch_bounds__(1024) void kq_mx_kernel(MxArg A) {
             const int MC = min(A.mch, M - mc0);
             __syncthreads();                      // tables in; the previous chunk's LDS reads done
 
+            // this wave's tasks t = wave + k * W
+            const int nsg = (MC + S - 1) / S;
+            const int ntask = ((rows + RPT - 1) / RPT) * nsg;
+            MxTasks tk;
+            tk.ntw = wave < ntask ? min(MX_TW, (ntask - wave + W - 1) / W) : 0;
+            tk.r0 = r0;
+            tk.rows = rows;
+            tk.GP = GP;
+            tk.lgp = lgp;
+            tk.RPT = RPT;
+#pragma unroll
+            for (int k = 0; k < MX_TW; k++) {
+                const int t = wave + k * W;
+                tk.grp[k] = t / nsg;
+                tk.sg[k] = t - tk.grp[k] * nsg;
+            }
+            // the first weights go out now, so their latency overlaps the x
+            // staging
+            const typename Chunk<TYPE>::Raw first = Chunk<TYPE>::load(
+                to_global(gw) + (size_t)(r0 + min(RPT * tk.grp[0] + (lane >> lgp), rows - 1)) *
+                                    ((size_t)(K >> 8) * TI::BB) +
+                    (size_t)(min(lane & (GP - 1), NC - 1) >> 2) * TI::BB,
+                lane & 3);
+
             // prologue: sums, window vote, and x itself when staged whole
             uint32_t dist = 0;
             if (SUMS || WHOLE) {
@@ -1481,22 +1506,6 @@ __global__ __launch_bounds__(1024) void kq_mx_kernel(MxArg A) {
                 __syncthreads();
             }
 
-            // this wave's tasks t = wave + k * W
-            const int nsg = (MC + S - 1) / S;
-            const int ntask = ((rows + RPT - 1) / RPT) * nsg;
-            MxTasks tk;
-            tk.ntw = wave < ntask ? min(MX_TW, (ntask - wave + W - 1) / W) : 0;
-            tk.r0 = r0;
-            tk.rows = rows;
-            tk.GP = GP;
-            tk.lgp = lgp;
-            tk.RPT = RPT;
-#pragma unroll
-            for (int k = 0; k < MX_TW; k++) {
-                const int t = wave + k * W;
-                tk.grp[k] = t / nsg;
-                tk.sg[k] = t - tk.grp[k] * nsg;
-            }
             double part[MX_TW][S];
 #pragma unroll
             for (int k = 0; k < MX_TW; k++)
@@ -1505,10 +1514,10 @@ __global__ __launch_bounds__(1024) void kq_mx_kernel(MxArg A) {
 
             if (sc)
                 mx_sweep<TYPE, S, WHOLE, SCTYPE>(A, tk, to_global(gw), part, MC, mc0, d_xi, sums,
-                                                 xb0, xb1, TC, ntile);
+                                                 xb0, xb1, TC, ntile, first);
             else
                 mx_sweep<TYPE, S, WHOLE, false>(A, tk, to_global(gw), part, MC, mc0, d_xi, sums,
-                                                xb0, xb1, TC, ntile);
+                                                xb0, xb1, TC, ntile, first);
 
             // phase_tree per member (every lane of the wave takes part)
 #pragma unroll
@@ -1580,14 +1589,78 @@ __global__ __launch_bounds__(256) void kq_moe_topk_kernel(const float* probs, in
     }
 }
 
+// The same selection for E <= 256 by ranks: expert e's slot is the number
+// of eligible experts that beat it (a larger weight, or an equal weight and
+// a lower id); one pass over the weights (LDS broadcast) per expert a lane
+// holds, instead of k dependent wave reductions.
+template <int NI>   // experts per lane: E <= 64 * NI
+__global__ __launch_bounds__(256) void kq_moe_topk_rank_kernel(const float* probs, int B, int E,
+                                                              int k, int* sel, float* selw) {
+    __shared__ __align__(16) float wl[4][64 * NI];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int tok = blockIdx.x * 4 + wv;
+    if (tok >= B) return;                      // uniform over the wave
+    const float* w = probs + (size_t)tok * E;
+    float v[NI];
+    bool el[NI];
+    int nel = 0;
+#pragma unroll
+    for (int i = 0; i < NI; i++) v[i] = w[min(lane + 64 * i, E - 1)];   // all loads in flight
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int e = lane + 64 * i;
+        v[i] = e < E ? v[i] : -1.0f;
+        el[i] = v[i] > -1.0f;                  // NaN is not eligible either
+        wl[wv][e] = v[i];
+        nel += __popcll(__ballot(el[i]));
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    int rank[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) rank[i] = 0;
+    const int E4 = (E + 3) & ~3;
+    for (int q = 0; q < E4; q += 4) {
+        const float4 o = *reinterpret_cast<const float4*>(&wl[wv][q]);
+        const float ov[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int eo = q + j;
+            const float x = ov[j];                 // -1 past E (never eligible)
+            const int xel = x > -1.0f;
+#pragma unroll
+            for (int i = 0; i < NI; i++) {
+                // bitwise, not short-circuit: straight-line compares
+                const int beat = (x > v[i]) | ((x == v[i]) & (eo < lane + 64 * i));
+                rank[i] += xel & beat;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int e = lane + 64 * i;
+        if (el[i] && rank[i] < k) {
+            sel[(size_t)tok * k + rank[i]] = e;
+            selw[(size_t)tok * k + rank[i]] = v[i];
+        }
+    }
+    for (int r = nel + lane; r < k; r += 64) {   // slots without an expert
+        sel[(size_t)tok * k + r] = -1;
+        selw[(size_t)tok * k + r] = -1.0f;
+    }
+}
+
 // Expert groups of the selected (token, rank) members, in increasing expert
 // order (moe_forward_b's member lists, stratum_arch_moe.inc.c:1130-1140):
-// for each distinct expert e, one MxGroup per tensor t with the members m
-// (in increasing m) that chose e: weights w[t] + e * estride, x row
-// m / x_div, output row m of y[t].  One workgroup; *ng = nt * distinct.
+// for each distinct expert e, the members m (in increasing m) that chose e,
+// cut into runs of at most mch (the reference's chunked tickets, :1158-1170,
+// here so that every work item carries about the same load), and one
+// MxGroup per run and tensor t: weights w[t] + e * estride, x row m / x_div,
+// output row m of y[t].  One workgroup; *ng = nt * runs.
 struct MoeGroupArg {
     const int* sel;
-    int nm, E, nt, x_div;          // members (B * k), experts, tensors, x divisor
+    int nm, E, nt, x_div, mch;     // members (B * k), experts, tensors, x divisor, run
     const uint8_t* w[2];
     float* y[2];
     long estride;
@@ -1611,10 +1684,11 @@ __global__ __launch_bounds__(1024) void kq_moe_group_kernel(MoeGroupArg a) {
         if (ok) atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
-    // exclusive scan of (cnt[e] > 0) over e: each thread a run of experts
+    // exclusive scan of the run counts ceil(cnt[e] / mch) over e: each
+    // thread a range of experts
     const int run = (a.E + T - 1) / T, e0 = tid * run, e1 = min(a.E, e0 + run);
     int local = 0;
-    for (int e = e0; e < e1; e++) local += cnt[e] > 0;
+    for (int e = e0; e < e1; e++) local += (cnt[e] + a.mch - 1) / a.mch;
     int incl = local;
     for (int off = 1; off < 64; off <<= 1) {
         const int o = __shfl_up(incl, off);
@@ -1626,7 +1700,7 @@ __global__ __launch_bounds__(1024) void kq_moe_group_kernel(MoeGroupArg a) {
     for (int i = 0; i < wave; i++) before += wsum[i];
     for (int e = e0; e < e1; e++) {
         gid[e] = before;
-        before += cnt[e] > 0;
+        before += (cnt[e] + a.mch - 1) / a.mch;
     }
     int nd = 0;
     for (int i = 0; i < (T >> 6); i++) nd += wsum[i];
@@ -1636,20 +1710,21 @@ __global__ __launch_bounds__(1024) void kq_moe_group_kernel(MoeGroupArg a) {
     for (int e = tid; e < a.E; e += T) {
         const int c = cnt[e];
         if (c == 0) continue;
-        for (int t = 0; t < a.nt; t++) {
-            MxGroup* G = a.groups + (size_t)t * nd + gid[e];
-            G->w = a.w[t] + (size_t)e * a.estride;
-            G->y = a.y[t];
-            G->M = min(c, MX_MAXM);
-            G->pad_ = 0;
-        }
+        for (int r = 0; r * a.mch < c; r++)
+            for (int t = 0; t < a.nt; t++) {
+                MxGroup* G = a.groups + (size_t)t * nd + gid[e] + r;
+                G->w = a.w[t] + (size_t)e * a.estride;
+                G->y = a.y[t];
+                G->M = min(c - r * a.mch, a.mch);
+                G->pad_ = 0;
+            }
         int j = 0;
-        for (int m = 0; m < a.nm && j < MX_MAXM; m++) {
+        for (int m = 0; m < a.nm; m++) {
             if (ms[m] != e) continue;
             for (int t = 0; t < a.nt; t++) {
-                MxGroup* G = a.groups + (size_t)t * nd + gid[e];
-                G->xi[j] = m / a.x_div;
-                G->yi[j] = m;
+                MxGroup* G = a.groups + (size_t)t * nd + gid[e] + j / a.mch;
+                G->xi[j % a.mch] = m / a.x_div;
+                G->yi[j % a.mch] = m;
             }
             j++;
         }
@@ -1918,6 +1993,7 @@ long kqk_mx_plan(int type, int N, int K, int mmax, int ngmax, int grid, int lds_
     const int G4 = type == T_Q4K ? 8 : 4;
     const long per = K / (4 * G4);
     const long head = 8L * MX_MAXM + 64;
+    const long rbytes = (long)(K >> 8) * (type == T_Q4K ? 144 : type == T_Q6K ? 210 : type == T_Q2K ? 84 : 148);
     const double c0 = type == T_Q4K ? 45 : type == T_Q6K ? 170 : type == T_Q2K ? 30 : 35;
     const double c1 = type == T_Q6K ? 140 : 150;
     // per-pass and per-tile overheads, fitted to timings of the 27B gate
@@ -1962,8 +2038,13 @@ long kqk_mx_plan(int type, int N, int K, int mmax, int ngmax, int grid, int lds_
                 const long rounds = (items + grid - 1) / grid;
                 const int simd = (ntask + 3) / 4;
                 const double step = (simd < 3 ? 3 : simd) * (c0 + S * c1);
+                // weight streaming: a CU's share of HBM is ~33 B per issue;
+                // a pass needs about 32 tasks (two per wave) in flight to
+                // draw it, and later member chunks re-read from L2
+                const double stream = (double)RB * rbytes / 33.0 / (ntask < 32 ? ntask / 32.0 : 1.0);
                 const double cost =
-                    (double)rounds * nmc * (step * nstep + item_cost + (ntile - 1) * tile_cost);
+                    (double)rounds * ((step * nstep > stream ? step * nstep : stream) * nmc +
+                                      nmc * (item_cost + (ntile - 1) * tile_cost));
                 if (cost <= best) {             // ties: the later (more items, or fewer
                     best = cost;                // members per load) choice
                     best_lds = lds;
@@ -2024,19 +2105,28 @@ int kqk_launch_mx(int type, const int* plan, long lds, int grid, const void* w, 
 int kqk_launch_moe_topk(const float* probs, int B, int E, int k, int* sel, float* selw,
                         hipStream_t st) {
     if (B < 1 || E < 1 || E > 4096 || k < 1) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(kq_moe_topk_kernel, dim3((B + 3) / 4), dim3(256), 0, st, probs, B, E, k,
-                       sel, selw);
+    const dim3 g((B + 3) / 4), t(256);
+    if (E <= 64)
+        hipLaunchKernelGGL(kq_moe_topk_rank_kernel<1>, g, t, 0, st, probs, B, E, k, sel, selw);
+    else if (E <= 128)
+        hipLaunchKernelGGL(kq_moe_topk_rank_kernel<2>, g, t, 0, st, probs, B, E, k, sel, selw);
+    else if (E <= 256)
+        hipLaunchKernelGGL(kq_moe_topk_rank_kernel<4>, g, t, 0, st, probs, B, E, k, sel, selw);
+    else
+        hipLaunchKernelGGL(kq_moe_topk_kernel, dim3((B + 3) / 4), dim3(256), 0, st, probs, B, E,
+                           k, sel, selw);
     return (int)hipGetLastError();
 }
 
 long kqk_mx_group_bytes(void) { return (long)sizeof(MxGroup); }
 
-int kqk_launch_moe_group(const int* sel, int nm, int E, int nt, int x_div, const void* w0,
-                         const void* w1, float* y0, float* y1, long estride, void* groups,
-                         int* ng, hipStream_t st) {
-    if (nm < 1 || E < 1 || E > 4096 || nt < 1 || nt > 2 || x_div < 1) return (int)hipErrorInvalidValue;
+int kqk_launch_moe_group(const int* sel, int nm, int E, int nt, int x_div, int mch,
+                         const void* w0, const void* w1, float* y0, float* y1, long estride,
+                         void* groups, int* ng, hipStream_t st) {
+    if (nm < 1 || E < 1 || E > 4096 || nt < 1 || nt > 2 || x_div < 1 || mch < 1 || mch > MX_MAXM)
+        return (int)hipErrorInvalidValue;
     MoeGroupArg a;
-    a.sel = sel; a.nm = nm; a.E = E; a.nt = nt; a.x_div = x_div;
+    a.sel = sel; a.nm = nm; a.E = E; a.nt = nt; a.x_div = x_div; a.mch = mch;
     a.w[0] = static_cast<const uint8_t*>(w0);
     a.w[1] = static_cast<const uint8_t*>(nt > 1 ? w1 : w0);
     a.y[0] = y0;

@@ -16,6 +16,7 @@
 #include "../../include/kq_gemv.h"
 
 #include <hip/hip_runtime_api.h>
+#include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -56,9 +57,9 @@ int kqk_mx_set_max_lds(int bytes);
 int kqk_launch_moe_topk(const float* probs, int B, int E, int k, int* sel, float* selw,
                         hipStream_t st);
 long kqk_mx_group_bytes(void);
-int kqk_launch_moe_group(const int* sel, int nm, int E, int nt, int x_div, const void* w0,
-                         const void* w1, float* y0, float* y1, long estride, void* groups,
-                         int* ng, hipStream_t st);
+int kqk_launch_moe_group(const int* sel, int nm, int E, int nt, int x_div, int mch,
+                         const void* w0, const void* w1, float* y0, float* y1, long estride,
+                         void* groups, int* ng, hipStream_t st);
 
 #define KQ_MAX_REGIONS 16
 
@@ -662,19 +663,30 @@ int kq_moe_gemv_dev(const kq_moe_op* op, const int* sel, int B, int k, int E, kq
         return launch_segs(h, nh, st);
     }
     /* several tokens: expert groups built on the device, then one weight
-     * pass per selected expert for all of its tokens */
-    const int nm = B * k, ngmax = nt * (E < nm ? E : nm);
+     * pass per selected expert for all of its tokens.  The launch is
+     * planned for the typical group: under uniform routing the expected
+     * number of distinct experts is E (1 - (1 - k/E)^B), each with nm / that
+     * many members; the member lists are cut into runs of the planned size
+     * so that every work item carries about the same load. */
+    const int nm = B * k, dmax = E < nm ? E : nm;
+    double dexp = E * (1.0 - pow(1.0 - (double)k / E, B));
+    if (dexp < 1.0) dexp = 1.0;
+    int mplan = (int)ceil(nm / dexp);
+    mplan = mplan < 1 ? 1 : mplan > B ? B : mplan;
+    const int grid = plan_grid();
+    int plan[KQK_MX_PLAN];
+    const long lds = kqk_mx_plan(op->type, op->n_out, op->k_in, mplan, nt * (int)ceil(dexp), grid,
+                                 g_kq.lds_max, plan);
+    if (lds < 0) return kq_fail("kq_moe_gemv_dev: no launch plan for K=%d", op->k_in);
+    const int mch = plan[7];
+    const int ngmax = nt * (dmax + (nm + mch - 1) / mch);
     const size_t gbytes = (size_t)kqk_mx_group_bytes();
     if (grow(&g_kq.d_moe, &g_kq.cap_moe, (ngmax * gbytes + 64) / sizeof(float) + 1)) return -1;
     void* groups = g_kq.d_moe;
     int* ng = (int*)((uint8_t*)g_kq.d_moe + ngmax * gbytes);
-    int e = kqk_launch_moe_group(sel, nm, E, nt, op->x_div, op->w[0], op->w[nt - 1], op->y[0],
+    int e = kqk_launch_moe_group(sel, nm, E, nt, op->x_div, mch, op->w[0], op->w[nt - 1], op->y[0],
                                  op->y[nt - 1], (long)op->expert_stride, groups, ng, st);
     if (e) return kq_fail("moe group launch: %s", hipGetErrorString((hipError_t)e));
-    const int grid = plan_grid();
-    int plan[KQK_MX_PLAN];
-    const long lds = kqk_mx_plan(op->type, op->n_out, op->k_in, B, ngmax, grid, g_kq.lds_max, plan);
-    if (lds < 0) return kq_fail("kq_moe_gemv_dev: no launch plan for K=%d", op->k_in);
     e = kqk_launch_mx(op->type, plan, lds, grid, NULL, 0, groups, ng, op->x, op->k_in, NULL,
                       op->n_out, op->n_out, op->k_in, st);
     if (e) return kq_fail("moe gemv launch: %s", hipGetErrorString((hipError_t)e));
