@@ -119,6 +119,19 @@ int kq_gemv_dev(int type, const void* w, const float* x, const float* add, float
 int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,
                        int B, int N, int K, kq_stream stream);
 
+/* The same product on the matrix cores, for many streams (B >= 16 is where
+ * it pays): Q4_K and Q6_K only (-1 for other types).  Each sub-block's
+ * inner product sum_k q_k x_k runs as bf16 x bf16 -> fp32 MFMAs over an
+ * exact split of x into three bf16 planes; the scaling and the sums across
+ * sub-blocks follow the reference's formula in binary32.  The results are
+ * NOT bit-identical to kq_gemv_multix_dev: they differ by about one
+ * binary32 ulp of each sub-block's sum (the measured bound is reported with
+ * the MULTISEQ benchmark).  No counterpart in the reference, whose multix
+ * must equal the single-stream result (stratum_linear.h:963-966); this is
+ * the opt-in dense-contraction path for large B.  x must be finite. */
+int kq_gemv_multix_mfma_dev(int type, const void* w, const float* xs, float* ys,
+                            int B, int N, int K, kq_stream stream);
+
 /* One segment of a batched launch: ngroups * rows_per_group rows of one
  * type and row length K.  Rows [g*rows_per_group, (g+1)*rows_per_group)
  * start at device address w[g] (separate bases: e.g. the selected MoE

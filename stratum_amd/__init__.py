@@ -42,7 +42,7 @@ EXPORTS = (
     "kq_q4k_group", "kq_gemv_dev", "kq_gemv_multix_dev", "kq_gemv_segments_dev",
     "kq_dequant_dev", "kq_row_bytes", "kq_moe_slice_bytes", "kq_moe_bind_slice",
     "kq_moe_pack_open", "kq_moe_pack_which", "kq_moe_topk", "kq_moe_topk_dev",
-    "kq_moe_gemv_dev",
+    "kq_moe_gemv_dev", "kq_gemv_multix_mfma_dev",
 )
 
 MAX_SEGMENTS = 8
@@ -187,6 +187,7 @@ def lib() -> ctypes.CDLL:
     L.kq_q4k_group.argtypes = [F, I, TP, F, I, TP, F, I, TP, F, I]
     L.kq_gemv_dev.argtypes = [I, P, P, P, P, I, I, P]
     L.kq_gemv_multix_dev.argtypes = [I, P, P, P, I, I, I, P]
+    L.kq_gemv_multix_mfma_dev.argtypes = [I, P, P, P, I, I, I, P]
     L.kq_dequant_dev.argtypes = [I, P, P, ctypes.c_int64, P]
     L.kq_gemv_segments_dev.argtypes = [ctypes.POINTER(KqSegment), I, P]
     L.kq_row_bytes.argtypes = [I, I]
@@ -280,6 +281,13 @@ def gemv_multix_dev(qtype: int, w_ptr: int, xs_ptr: int, ys_ptr: int, B: int, N:
                     K: int, stream: int | None = None) -> None:
     _check(lib().kq_gemv_multix_dev(qtype, w_ptr, xs_ptr, ys_ptr, B, N, K, stream),
            "kq_gemv_multix_dev")
+
+
+def gemv_multix_mfma_dev(qtype: int, w_ptr: int, xs_ptr: int, ys_ptr: int, B: int, N: int,
+                         K: int, stream: int | None = None) -> None:
+    """Matrix-core multi-stream GEMV (tolerance path, Q4_K / Q6_K)."""
+    _check(lib().kq_gemv_multix_mfma_dev(qtype, w_ptr, xs_ptr, ys_ptr, B, N, K, stream),
+           "kq_gemv_multix_mfma_dev")
 
 
 def gemv_segments_dev(segs: list[KqSegment], stream: int | None = None) -> None:

@@ -45,6 +45,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "kq_launch.h"
+
 
 #pragma clang fp contract(off)
 
@@ -1731,6 +1733,378 @@ __global__ __launch_bounds__(1024) void kq_moe_group_kernel(MoeGroupArg a) {
     }
 }
 
+// ------------------------------------------------------- MFMA multi-x
+// Tolerance path for many streams (B >= 16): the inner products of each
+// sub-block, sum_k q_k x_k, run on the matrix cores as bf16 x bf16 -> fp32
+// MFMAs and are then scaled as the reference does (d*sc times the sum, minus
+// dmin*m times the sum of x).  x enters exactly as three bf16 planes
+// (x = h + m + l: 8 + 8 + 8 significand bits), and every product q * plane
+// is exact in fp32, so the only difference from the reference is the fp32
+// rounding order of the sums (the reference adds sequentially, the MFMA in
+// its own tree) plus fp32 accumulation across sub-blocks: results agree to
+// about one binary32 ulp of each sub-block's sum, not bit for bit.
+//
+// Operands: D[stream][row] = sum_k A[stream][k] B[k][row], A = an x plane,
+// B = the weights.  In the 16x16xK MFMAs lane l holds B[k][row = l % 16]
+// for k = KV*(l/16) + v and receives D[4*(l/16) + v][l % 16]: a lane's
+// weight row is its output row, so each lane decodes only its own row's
+// scales.  Within a sub-block any permutation of k is allowed as long as A
+// and B use the same one, which lets a Q6_K lane take 4 consecutive bytes.
+//  * kq_mfma_xsplit_kernel writes the planes in the A-operand order (64 lanes
+//    x KV bf16 per sub-block, stream group of 16 and plane) and the
+//    sequential binary32 sum of x per (stream, sub-block);
+//  * kq_mfma_mx_kernel: a work unit is 64 rows (4 waves, one 16-row tile
+//    each) x a K-part of MF_SBP super-blocks; the x planes of one
+//    super-block are staged in LDS (double-buffered, shared by the 4 waves)
+//    while the previous one is consumed.  Units of a row range with several
+//    K-parts write partial sums, which kq_mfma_reduce_kernel adds in part
+//    order (a fixed order: the result does not depend on timing).
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+constexpr int MF_SBP = 4;            // super-blocks per K-part
+
+template <int TYPE> struct MfInfo;
+template <> struct MfInfo<T_Q4K> { static constexpr int SUB = 32, KV = 8, NSUB = 8; };
+template <> struct MfInfo<T_Q6K> { static constexpr int SUB = 16, KV = 4, NSUB = 16; };
+
+// binary32 -> bf16, round to nearest even (finite inputs)
+__device__ __forceinline__ uint32_t bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+struct MfSplitArg {
+    const float* x;          // B x K
+    uint16_t* planes;        // (K/SUB) x NSG x 3 x 64 x KV
+    float* xs;               // (K/32) x (16 NSG): sums of 32 (Q4_K), or null
+    int B, K, NSG;
+};
+
+template <int TYPE>
+__global__ __launch_bounds__(256) void kq_mfma_xsplit_kernel(MfSplitArg a) {
+    using MI = MfInfo<TYPE>;
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    const int nsb = a.K / MI::SUB;
+    if (t >= nsb * a.NSG * 64) return;
+    const int l = t & 63, g = (t >> 6) % a.NSG, sb = (t >> 6) / a.NSG;
+    const int s = 16 * g + (l & 15);
+    const int k0 = MI::SUB * sb + MI::KV * (l >> 4);
+    uint32_t h[MI::KV], m[MI::KV], lo[MI::KV];
+#pragma unroll
+    for (int v = 0; v < MI::KV; v++) {
+        const float xv = s < a.B ? a.x[(size_t)s * a.K + k0 + v] : 0.0f;
+        h[v] = bf16_rne(xv);
+        const float r1 = xv - __uint_as_float(h[v] << 16);
+        m[v] = bf16_rne(r1);
+        const float r2 = r1 - __uint_as_float(m[v] << 16);
+        lo[v] = bf16_rne(r2);
+    }
+    uint16_t* base = a.planes + ((size_t)(sb * a.NSG + g) * 3 * 64 + l) * MI::KV;
+#pragma unroll
+    for (int v = 0; v < MI::KV; v++) {
+        base[v] = (uint16_t)h[v];
+        base[64 * MI::KV + v] = (uint16_t)m[v];
+        base[128 * MI::KV + v] = (uint16_t)lo[v];
+    }
+    // per (stream, 32-value sub-block) sums for the Q4_K min terms, in order
+    if (a.xs && MI::SUB == 32 && l < 16) {
+        float acc = 0.0f;
+        for (int k = 0; k < 32; k++)
+            acc = acc + (s < a.B ? a.x[(size_t)s * a.K + 32 * sb + k] : 0.0f);
+        a.xs[(size_t)sb * (16 * a.NSG) + s] = acc;
+    }
+}
+
+struct MfArg {
+    const uint8_t* w;
+    const uint16_t* planes;
+    const float* xs;
+    float* y;                // B x N
+    float* part;             // KP x (16 NSG) x N partial sums (KP > 1)
+    int B, N, K, NSG, KP, nunits, grid;
+};
+
+// bf16 of the 4 bytes of v (each an unsigned value < 256), k order = byte order
+__device__ __forceinline__ void bf16_bytes(uint32_t v, uint32_t& lo2, uint32_t& hi2) {
+    float f0, f1, f2, f3;
+    ubytes(v, f0, f1, f2, f3);                     // v_cvt_f32_ubyte{0..3}
+    lo2 = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+    hi2 = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
+}
+// bf16 of the 4 signed bytes of v
+__device__ __forceinline__ void bf16_sbytes(uint32_t v, uint32_t& lo2, uint32_t& hi2) {
+    const float f0 = (float)(int32_t)(int8_t)(v & 0xffu);
+    const float f1 = (float)(int32_t)(int8_t)((v >> 8) & 0xffu);
+    const float f2 = (float)(int32_t)(int8_t)((v >> 16) & 0xffu);
+    const float f3 = (float)(int32_t)(int8_t)(v >> 24);
+    lo2 = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+    hi2 = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
+}
+
+// One super-block of one row's weights as one lane needs them (k-group kg).
+struct MfRawQ4 { uint4 hd; uint2 q[4]; };
+struct MfRawQ6 { uint32_t p[12][2]; uint32_t s[5]; uint32_t d, sh; };
+template <int TYPE> struct MfRaw;
+template <> struct MfRaw<T_Q4K> { using T = MfRawQ4; };
+template <> struct MfRaw<T_Q6K> { using T = MfRawQ6; };
+
+__device__ __forceinline__ MfRawQ4 mf_load_q4k(wptr blk, int kg) {
+    MfRawQ4 r;
+    r.hd = ld16(blk);
+#pragma unroll
+    for (int c = 0; c < 4; c++) r.q[c] = ld8a4(blk + 16 + 32 * c + 8 * kg);
+    return r;
+}
+
+// Q6_K: sub-block s16 = 8h + 2t + is holds positions l' = 16 is .. +15 of
+// run (h, t); this lane takes l' = 16 is + 4 kg + v: one ql dword (nibble
+// t >> 1) and one qh dword (bits 2t).  Blocks are 2-byte aligned: each
+// dword is read as two aligned dwords and realigned; when the block is
+// aligned the second read repeats the first, so the last block of a tensor
+// is never read past its 210 bytes.
+__device__ __forceinline__ MfRawQ6 mf_load_q6k(wptr blk, int kg) {
+    MfRawQ6 r;
+    const uint32_t mis = (uint32_t)reinterpret_cast<uintptr_t>(blk) & 3u;
+    r.sh = mis * 8u;
+    const wptr b4 = blk - mis;
+    const int nx = mis ? 4 : 0;
+    int i = 0;
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int is = 0; is < 2; is++) {
+            const int o[3] = {64 * h + 16 * is + 4 * kg, 64 * h + 32 + 16 * is + 4 * kg,
+                              128 + 32 * h + 16 * is + 4 * kg};
+#pragma unroll
+            for (int f = 0; f < 3; f++, i++) {
+                r.p[i][0] = ld4(b4 + o[f]);
+                r.p[i][1] = ld4(b4 + o[f] + nx);
+            }
+        }
+    const uint4 sv = ld16a4(b4 + 192);
+    r.s[0] = sv.x; r.s[1] = sv.y; r.s[2] = sv.z; r.s[3] = sv.w;
+    r.s[4] = ld4(b4 + 192 + 12 + nx);
+    r.d = ld2(blk + 208);
+    return r;
+}
+
+template <int TYPE>
+__device__ __forceinline__ typename MfRaw<TYPE>::T mf_load(wptr blk, int kg) {
+    if constexpr (TYPE == T_Q4K) return mf_load_q4k(blk, kg);
+    else return mf_load_q6k(blk, kg);
+}
+
+__device__ __forceinline__ uint32_t byte_of(const uint4& v, int i) {
+    const uint32_t w = i < 4 ? v.x : i < 8 ? v.y : i < 12 ? v.z : v.w;
+    return (w >> (8 * (i & 3))) & 0xffu;
+}
+
+// one super-block of one 16-row tile for one stream group: acc[v] (streams
+// 4*(l/16)+v of the group, the lane's row) += the super-block's terms
+template <int TYPE>
+__device__ __forceinline__ void mf_superblock(const typename MfRaw<TYPE>::T& r, int kg,
+                                              const uint8_t* xl, const float* xsl, f32x4& acc) {
+    if constexpr (TYPE == T_Q4K) {
+        const float d = f16_bits_to_f32(r.hd.x & 0xffffu);
+        const float dmin = f16_bits_to_f32(r.hd.x >> 16);
+        // scales[12] are bytes 4..15 of the block: words y, z, w of hd
+        const uint4 sc = make_uint4(r.hd.y, r.hd.z, r.hd.w, 0u);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            // 6-bit scale / min of sub-block j (stratum_q4k.h:57-65)
+            uint32_t s_, m_;
+            if (j < 4) {
+                s_ = byte_of(sc, j) & 63u;
+                m_ = byte_of(sc, j + 4) & 63u;
+            } else {
+                s_ = (byte_of(sc, j + 4) & 15u) | ((byte_of(sc, j - 4) >> 6) << 4);
+                m_ = (byte_of(sc, j + 4) >> 4) | ((byte_of(sc, j) >> 6) << 4);
+            }
+            const float ds = d * (float)s_, dm = dmin * (float)m_;
+            const uint2 q = r.q[j >> 1];
+            const uint32_t w0 = (j & 1) ? (q.x >> 4) & 0x0f0f0f0fu : q.x & 0x0f0f0f0fu;
+            const uint32_t w1 = (j & 1) ? (q.y >> 4) & 0x0f0f0f0fu : q.y & 0x0f0f0f0fu;
+            uint32_t b[4];
+            bf16_bytes(w0, b[0], b[1]);
+            bf16_bytes(w1, b[2], b[3]);
+            const bf16x8 bw = __builtin_bit_cast(bf16x8, make_uint4(b[0], b[1], b[2], b[3]));
+            const uint4* ap = reinterpret_cast<const uint4*>(xl) + (size_t)j * 3 * 64 + (threadIdx.x & 63);
+            f32x4 C = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int p = 0; p < 3; p++)
+                C = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ap[p * 64]), bw,
+                                                            C, 0, 0, 0);
+            const float4 xsum = reinterpret_cast<const float4*>(xsl + j * 16)[kg];
+            acc.x = acc.x + (ds * C.x - dm * xsum.x);
+            acc.y = acc.y + (ds * C.y - dm * xsum.y);
+            acc.z = acc.z + (ds * C.z - dm * xsum.z);
+            acc.w = acc.w + (ds * C.w - dm * xsum.w);
+        }
+    } else {
+        const uint32_t sh = r.sh;
+        uint32_t ql[2][2][2], qh[2][2];
+        int i = 0;
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int is = 0; is < 2; is++) {
+                ql[h][0][is] = __builtin_amdgcn_alignbit(r.p[i][1], r.p[i][0], sh); i++;
+                ql[h][1][is] = __builtin_amdgcn_alignbit(r.p[i][1], r.p[i][0], sh); i++;
+                qh[h][is] = __builtin_amdgcn_alignbit(r.p[i][1], r.p[i][0], sh); i++;
+            }
+        uint32_t scw[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) scw[k] = __builtin_amdgcn_alignbit(r.s[k + 1], r.s[k], sh);
+        const float d4 = f16_bits_to_f32(r.d) * 0.25f;        // bytes hold 4 (q - 32)
+#pragma unroll
+        for (int s16 = 0; s16 < 16; s16++) {
+            const int h = s16 >> 3, t = (s16 >> 1) & 3, is = s16 & 1;
+            const uint32_t L = ql[h][t & 1][is], H = qh[h][is];
+            const uint32_t q = ((L >> (4 * (t >> 1))) & 0x0f0f0f0fu) | (((H >> (2 * t)) & 0x03030303u) << 4);
+            const uint32_t y = (q ^ 0x20202020u) << 2;             // int8 4 (q - 32) per byte
+            uint32_t b0, b1;
+            bf16_sbytes(y, b0, b1);
+            const s16x4 bw = __builtin_bit_cast(s16x4, make_uint2(b0, b1));
+            const float scv = (float)(int32_t)(int8_t)((scw[s16 >> 2] >> (8 * (s16 & 3))) & 0xffu);
+            const float ds = d4 * scv;
+            const uint2* ap = reinterpret_cast<const uint2*>(xl) + (size_t)s16 * 3 * 64 + (threadIdx.x & 63);
+            f32x4 C = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int p = 0; p < 3; p++)
+                C = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, ap[p * 64]), bw,
+                                                              C, 0, 0, 0);
+            acc.x = acc.x + ds * C.x;
+            acc.y = acc.y + ds * C.y;
+            acc.z = acc.z + ds * C.z;
+            acc.w = acc.w + ds * C.w;
+        }
+    }
+}
+
+template <int TYPE>
+__global__ __launch_bounds__(256) void kq_mfma_mx_kernel(MfArg A) {
+    using MI = MfInfo<TYPE>;
+    using TI = TypeInfo<TYPE>;
+    constexpr int OPB = 3 * 64 * MI::KV * 2;                 // plane bytes per sub-block and group
+    constexpr int XB = MI::NSUB * OPB;                       // per super-block and group
+    extern __shared__ __align__(16) uint8_t smem[];
+    // two buffers of planes, then two of sums
+    auto xb = [&](int buf) { return smem + buf * XB; };
+    auto xsb = [&](int buf) { return reinterpret_cast<float*>(smem + 2 * XB) + buf * 8 * 16; };
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, kg = lane >> 4;
+    const int NSB = A.K >> 8;
+    const size_t rbytes = (size_t)NSB * TI::BB;
+    for (int u = blockIdx.x; u < A.nunits; u += A.grid) {
+        const int rq = u / A.KP, kp = u - rq * A.KP;
+        const int sb0 = kp * MF_SBP, sb1 = min(NSB, sb0 + MF_SBP);
+        const int row = 64 * rq + 16 * wave + (lane & 15);
+        const wptr wr = to_global(A.w) + (size_t)min(row, A.N - 1) * rbytes;
+        for (int g = 0; g < A.NSG; g++) {
+            // one super-block's planes (and sums) of group g: XB / 16 uint4
+            // of planes, 6 per thread (XB = 24 KB), loaded a step ahead
+            constexpr int NV = XB / 16 / 256;
+            static_assert(NV * 256 * 16 == XB, "plane staging split");
+            const u32x4* src = reinterpret_cast<const u32x4*>(A.planes);   // native vectors: no memcpy
+            auto sload = [&](int sb, u32x4 (&v)[NV], float& xsv) {
+#pragma unroll
+                for (int k = 0; k < NV; k++) {
+                    const int i = tid + 256 * k;
+                    const int j = i / (OPB / 16), rr = i - j * (OPB / 16);
+                    v[k] = src[((size_t)(sb * MI::NSUB + j) * A.NSG + g) * (OPB / 16) + rr];
+                }
+                if (TYPE == T_Q4K && tid < 8 * 16)
+                    xsv = A.xs[(size_t)(sb * 8 + (tid >> 4)) * (16 * A.NSG) + 16 * g + (tid & 15)];
+            };
+            auto sstore = [&](int buf, const u32x4 (&v)[NV], float xsv) {
+#pragma unroll
+                for (int k = 0; k < NV; k++) reinterpret_cast<u32x4*>(xb(buf))[tid + 256 * k] = v[k];
+                if (TYPE == T_Q4K && tid < 8 * 16) xsb(buf)[tid] = xsv;
+            };
+            __syncthreads();                    // the previous group's LDS reads are done
+            {
+                u32x4 s0v[NV];
+                float x0 = 0.0f;
+                sload(sb0, s0v, x0);
+                sstore(0, s0v, x0);
+            }
+            u32x4 sv[NV];
+            float xsv = 0.0f;
+            typename MfRaw<TYPE>::T cur = mf_load<TYPE>(wr + (size_t)sb0 * TI::BB, kg);
+            __syncthreads();
+            f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int sb = sb0; sb < sb1; sb++) {
+                const int buf = (sb - sb0) & 1;
+                const bool more = sb + 1 < sb1;
+                // next weights and planes in flight while this super-block runs
+                const typename MfRaw<TYPE>::T nxt =
+                    mf_load<TYPE>(wr + (size_t)min(sb + 1, sb1 - 1) * TI::BB, kg);
+                sload(min(sb + 1, sb1 - 1), sv, xsv);   // unconditional: no join on sv
+                mf_superblock<TYPE>(cur, kg, xb(buf), xsb(buf), acc);
+                if (more) sstore(buf ^ 1, sv, xsv);
+                __syncthreads();
+                cur = nxt;
+            }
+            // the lane's 4 outputs: streams 16 g + 4 kg + v of its row
+            const int s0 = 16 * g + 4 * kg;
+            const float av[4] = {acc.x, acc.y, acc.z, acc.w};
+            if (A.KP == 1) {
+                if (row < A.N)
+#pragma unroll
+                    for (int v = 0; v < 4; v++)
+                        if (s0 + v < A.B) A.y[(size_t)(s0 + v) * A.N + row] = av[v];
+            } else if (row < A.N) {
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    A.part[((size_t)kp * 16 * A.NSG + s0 + v) * A.N + row] = av[v];
+            }
+        }
+    }
+}
+
+// y = the K-parts' partial sums added in part order (MFMA multi-x with
+// several K-parts; a separate launch, so no cross-workgroup ordering is
+// needed inside the sweep)
+__global__ __launch_bounds__(256) void kq_mfma_reduce_kernel(const float* part, float* y, int B,
+                                                            int N, int NSG, int KP) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (long)B * N) return;
+    const int s = (int)(i / N), r = (int)(i - (long)s * N);
+    float v = 0.0f;
+    for (int q = 0; q < KP; q++) v = v + part[((size_t)q * 16 * NSG + s) * N + r];
+    y[i] = v;
+}
+
+template <int TYPE>
+int launch_mfma_t(const float* x, const void* w, float* y, int B, int N, int K, void* planes,
+                  float* xs, float* part, int grid, hipStream_t st) {
+    using MI = MfInfo<TYPE>;
+    const int NSG = (B + 15) / 16;
+    MfSplitArg s;
+    s.x = x; s.planes = static_cast<uint16_t*>(planes); s.xs = TYPE == T_Q4K ? xs : nullptr;
+    s.B = B; s.K = K; s.NSG = NSG;
+    const long nt = (long)(K / MI::SUB) * NSG * 64;
+    hipLaunchKernelGGL(kq_mfma_xsplit_kernel<TYPE>, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0,
+                       st, s);
+    MfArg a;
+    a.w = static_cast<const uint8_t*>(w);
+    a.planes = static_cast<const uint16_t*>(planes);
+    a.xs = xs; a.y = y; a.part = part;
+    a.B = B; a.N = N; a.K = K; a.NSG = NSG;
+    a.KP = ((K >> 8) + MF_SBP - 1) / MF_SBP;
+    a.nunits = (N + 63) / 64 * a.KP;
+    a.grid = grid < a.nunits ? grid : a.nunits;
+    constexpr int XB = MI::NSUB * 3 * 64 * MI::KV * 2;
+    hipLaunchKernelGGL(kq_mfma_mx_kernel<TYPE>, dim3(a.grid), dim3(256), (size_t)(2 * XB + 2 * 8 * 16 * 4),
+                       st, a);
+    if (a.KP > 1) {
+        const long n = (long)B * N;
+        hipLaunchKernelGGL(kq_mfma_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                           (const float*)part, y, B, N, NSG, a.KP);
+    }
+    return (int)hipGetLastError();
+}
+
 // --------------------------------------------------------------- dequant
 // Bit-exact dequantization, one lane per 64-weight chunk (64 floats out).
 template <int TYPE>
@@ -1819,17 +2193,6 @@ extern "C" {
 // Host view of one segment (plain C layout, mirrored in kq_linear.c):
 // nparts parts, part p = rows [start[p], start[p] + rows[p]) at w[p],
 // writing y[p] (+ add[p]); x, or x + p * x_stride when x_stride != 0.
-struct kqk_seg {
-    const void* w[MAXG];
-    float* y[MAXG];
-    const float* add[MAXG];
-    int rows[MAXG];
-    const float* x;
-    int type, K, nparts, x_stride;
-    const int* sel;          // MoE gather (NULL: none), as in Seg
-    long estride;
-    int ksel, emax;
-};
 
 static long seg_rows(const kqk_seg& g) {
     long n = 0;
@@ -2137,6 +2500,27 @@ int kqk_launch_moe_group(const int* sel, int nm, int E, int nt, int x_div, int m
     const size_t lds = (size_t)(2 * E + nm) * sizeof(int);
     hipLaunchKernelGGL(kq_moe_group_kernel, dim3(1), dim3(1024), lds, st, a);
     return (int)hipGetLastError();
+}
+
+// MFMA multi-x (Q4_K, Q6_K): workspace sizes for B streams of N x K, and the
+// launch (x split into planes, the matrix-core sweep, and the sum of the
+// K-parts' partials).
+int kqk_mfma_workspace(int type, int B, int N, int K, long* planes, long* xs, long* part) {
+    if ((type != T_Q4K && type != T_Q6K) || B < 1 || N < 1 || K <= 0 || (K & 255)) return -1;
+    const long NSG = (B + 15) / 16, KP = ((K >> 8) + MF_SBP - 1) / MF_SBP;
+    *planes = (long)K * NSG * 16 * 3 * 2;
+    *xs = (long)(K / 32) * NSG * 16 * 4;
+    *part = KP > 1 ? KP * NSG * 16 * (long)N * 4 : 0;
+    return 0;
+}
+
+int kqk_launch_mfma(int type, const float* x, const void* w, float* y, int B, int N, int K,
+                    void* planes, float* xs, float* part, int grid, hipStream_t st) {
+    switch (type) {
+    case T_Q4K: return launch_mfma_t<T_Q4K>(x, w, y, B, N, K, planes, xs, part, grid, st);
+    case T_Q6K: return launch_mfma_t<T_Q6K>(x, w, y, B, N, K, planes, xs, part, grid, st);
+    default: return (int)hipErrorInvalidValue;
+    }
 }
 
 int kqk_launch_dequant(int type, const void* w, float* y, long nblocks, hipStream_t st) {

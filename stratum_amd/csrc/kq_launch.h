@@ -1,0 +1,63 @@
+/*
+ * kq_launch.h -- the launchers of kq_kernels.hip as the host layer
+ * (kq_linear.c) calls them.  Internal to the library (not installed);
+ * included by both sides so that the two agree on every signature.
+ */
+#ifndef KQ_LAUNCH_H
+#define KQ_LAUNCH_H
+
+#include <hip/hip_runtime_api.h>
+
+#include "../../include/kq_gemv.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* launchers (kq_kernels.hip).  A launcher segment has nparts parts; part p
+ * is rows[p] rows at w[p] writing y[p] (+ add[p]), reading x, or
+ * x + p * x_stride when x_stride != 0. */
+typedef struct {
+    const void* w[KQ_MAX_GROUPS];
+    float* y[KQ_MAX_GROUPS];
+    const float* add[KQ_MAX_GROUPS];
+    int rows[KQ_MAX_GROUPS];
+    const float* x;
+    int type, K, nparts, x_stride;
+    const int* sel;          /* MoE gather: part p uses expert sel[p % ksel] */
+    long estride;            /* bytes per expert */
+    int ksel, emax;
+} kqk_seg;
+#define KQK_LIST_MAX 4   /* parts of unequal sizes one launcher segment takes */
+long kqk_segs_lds(const kqk_seg* segs, int nseg, int grid, int* xs_off, int* terms_off,
+                  int* scr_off);
+int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int depth,
+                    long lds_bytes, int xs_off, int terms_off, int scr_off, hipStream_t st);
+int kqk_launch_dequant(int type, const void* w, float* y, long nblocks, hipStream_t st);
+int kqk_set_max_lds(int bytes);
+/* multi-x launcher: plan[] = threads, S, RB, nblk, TC, sums bytes, x buffer
+ * bytes, members staged together (kqk_mx_plan returns the LDS bytes, or
+ * -1); gdev == NULL launches one inline group of M members (x_j = X + j
+ * x_stride, y_j = Y + j y_stride) */
+#define KQK_MX_PLAN 8
+long kqk_mx_plan(int type, int N, int K, int mmax, int ngmax, int grid, int lds_max, int* plan);
+int kqk_launch_mx(int type, const int* plan, long lds, int grid, const void* w, int M,
+                  const void* gdev, const int* ngdev, const float* X, long x_stride, float* Y,
+                  long y_stride, int N, int K, hipStream_t st);
+int kqk_mx_set_max_lds(int bytes);
+/* MoE: top-k per token; the expert groups (MxGroup records) of a selection */
+int kqk_launch_moe_topk(const float* probs, int B, int E, int k, int* sel, float* selw,
+                        hipStream_t st);
+long kqk_mx_group_bytes(void);
+/* MFMA multi-x (Q4_K, Q6_K): workspace sizes, and the launch */
+int kqk_mfma_workspace(int type, int B, int N, int K, long* planes, long* xs, long* part);
+int kqk_launch_mfma(int type, const float* x, const void* w, float* y, int B, int N, int K,
+                    void* planes, float* xs, float* part, int grid, hipStream_t st);
+int kqk_launch_moe_group(const int* sel, int nm, int E, int nt, int x_div, int mch,
+                         const void* w0, const void* w1, float* y0, float* y1, long estride,
+                         void* groups, int* ng, hipStream_t st);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KQ_LAUNCH_H */

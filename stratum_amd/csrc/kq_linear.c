@@ -22,44 +22,7 @@
 #include <stdlib.h>
 #include <string.h>
 
-/* launchers (kq_kernels.hip).  A launcher segment has nparts parts; part p
- * is rows[p] rows at w[p] writing y[p] (+ add[p]), reading x, or
- * x + p * x_stride when x_stride != 0. */
-typedef struct {
-    const void* w[KQ_MAX_GROUPS];
-    float* y[KQ_MAX_GROUPS];
-    const float* add[KQ_MAX_GROUPS];
-    int rows[KQ_MAX_GROUPS];
-    const float* x;
-    int type, K, nparts, x_stride;
-    const int* sel;          /* MoE gather: part p uses expert sel[p % ksel] */
-    long estride;            /* bytes per expert */
-    int ksel, emax;
-} kqk_seg;
-#define KQK_LIST_MAX 4   /* parts of unequal sizes one launcher segment takes */
-long kqk_segs_lds(const kqk_seg* segs, int nseg, int grid, int* xs_off, int* terms_off,
-                  int* scr_off);
-int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int depth,
-                    long lds_bytes, int xs_off, int terms_off, int scr_off, hipStream_t st);
-int kqk_launch_dequant(int type, const void* w, float* y, long nblocks, hipStream_t st);
-int kqk_set_max_lds(int bytes);
-/* multi-x launcher: plan[] = threads, S, RB, nblk, TC, sums bytes, x buffer
- * bytes, members staged together (kqk_mx_plan returns the LDS bytes, or
- * -1); gdev == NULL launches one inline group of M members (x_j = X + j
- * x_stride, y_j = Y + j y_stride) */
-#define KQK_MX_PLAN 8
-long kqk_mx_plan(int type, int N, int K, int mmax, int ngmax, int grid, int lds_max, int* plan);
-int kqk_launch_mx(int type, const int* plan, long lds, int grid, const void* w, int M,
-                  const void* gdev, const int* ngdev, const float* X, long x_stride, float* Y,
-                  long y_stride, int N, int K, hipStream_t st);
-int kqk_mx_set_max_lds(int bytes);
-/* MoE: top-k per token; the expert groups (MxGroup records) of a selection */
-int kqk_launch_moe_topk(const float* probs, int B, int E, int k, int* sel, float* selw,
-                        hipStream_t st);
-long kqk_mx_group_bytes(void);
-int kqk_launch_moe_group(const int* sel, int nm, int E, int nt, int x_div, int mch,
-                         const void* w0, const void* w1, float* y0, float* y1, long estride,
-                         void* groups, int* ng, hipStream_t st);
+#include "kq_launch.h"
 
 #define KQ_MAX_REGIONS 16
 
@@ -83,6 +46,7 @@ typedef struct {
     float* d_y; size_t cap_y;
     float* d_a; size_t cap_a;
     float* d_moe; size_t cap_moe;   /* MoE expert groups + their count */
+    uint8_t* d_mf; size_t cap_mf;   /* MFMA multi-x: x planes, sums, partials */
     char err[512];
 } kq_state;
 
@@ -197,6 +161,7 @@ void kq_linear_shutdown(void) {
     if (g_kq.d_y) (void)hipFree(g_kq.d_y);
     if (g_kq.d_a) (void)hipFree(g_kq.d_a);
     if (g_kq.d_moe) (void)hipFree(g_kq.d_moe);
+    if (g_kq.d_mf) (void)hipFree(g_kq.d_mf);
     if (g_kq.ready && g_kq.stream) (void)hipStreamDestroy(g_kq.stream);
     memset(&g_kq, 0, sizeof g_kq);
 }
@@ -410,6 +375,38 @@ int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,
         }
         s0 += nb;
     }
+    return 0;
+}
+
+/* B streams on the matrix cores (Q4_K and Q6_K): the tolerance path.  Each
+ * sub-block's inner product runs as bf16 MFMAs over an exact three-plane
+ * split of x, so results differ from the single-stream ones by about one
+ * binary32 ulp of each sub-block sum (not bit for bit). */
+int kq_gemv_multix_mfma_dev(int type, const void* w, const float* xs, float* ys,
+                            int B, int N, int K, kq_stream stream) {
+    if (type != KQ_TYPE_Q4_K && type != KQ_TYPE_Q6_K)
+        return kq_fail("kq_gemv_multix_mfma_dev: type %d has no MFMA path", type);
+    if (B < 1) return kq_fail("kq_gemv_multix_mfma_dev: B=%d", B);
+    if (check_shape(type, N, K) || kq_ready()) return -1;
+    if (!w || !xs || !ys) return kq_fail("kq_gemv_multix_mfma_dev: NULL pointer");
+    long pl, xsb, pt;
+    if (kqk_mfma_workspace(type, B, N, K, &pl, &xsb, &pt))
+        return kq_fail("kq_gemv_multix_mfma_dev: bad shape");
+    const size_t a = 256;
+    const size_t o_xs = (pl + a - 1) / a * a, o_pt = o_xs + (xsb + a - 1) / a * a,
+                 need = o_pt + (size_t)pt;
+    if (g_kq.cap_mf < need) {
+        if (g_kq.d_mf) (void)hipFree(g_kq.d_mf);
+        g_kq.d_mf = NULL;
+        g_kq.cap_mf = 0;
+        if (hip_ok(hipMalloc((void**)&g_kq.d_mf, need), "hipMalloc(mfma workspace)")) return -1;
+        g_kq.cap_mf = need;
+    }
+    uint8_t* ws = g_kq.d_mf;
+    const int e = kqk_launch_mfma(type, xs, w, ys, B, N, K, ws, (float*)(ws + o_xs),
+                                  (float*)(ws + o_pt), 2 * g_kq.n_cu,
+                                  pick(stream));
+    if (e) return kq_fail("mfma multix launch: %s", hipGetErrorString((hipError_t)e));
     return 0;
 }
 
