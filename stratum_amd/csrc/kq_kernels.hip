@@ -2030,20 +2030,27 @@ __global__ __launch_bounds__(256) void kq_mfma_mx_kernel(MfArg A) {
             }
             u32x4 sv[NV];
             float xsv = 0.0f;
-            typename MfRaw<TYPE>::T cur = mf_load<TYPE>(wr + (size_t)sb0 * TI::BB, kg);
+            typename MfRaw<TYPE>::T ra = mf_load<TYPE>(wr + (size_t)sb0 * TI::BB, kg), rb;
             __syncthreads();
             f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-            for (int sb = sb0; sb < sb1; sb++) {
+            // one super-block: the next planes and weights go out first (the
+            // planes before the weights: loads complete in order, so storing
+            // the planes does not wait for the weights), then this one runs
+            auto step = [&](int sb, const typename MfRaw<TYPE>::T& cur,
+                            typename MfRaw<TYPE>::T& nxt) {
                 const int buf = (sb - sb0) & 1;
-                const bool more = sb + 1 < sb1;
-                // next weights and planes in flight while this super-block runs
-                const typename MfRaw<TYPE>::T nxt =
-                    mf_load<TYPE>(wr + (size_t)min(sb + 1, sb1 - 1) * TI::BB, kg);
                 sload(min(sb + 1, sb1 - 1), sv, xsv);   // unconditional: no join on sv
+                nxt = mf_load<TYPE>(wr + (size_t)min(sb + 1, sb1 - 1) * TI::BB, kg);
                 mf_superblock<TYPE>(cur, kg, xb(buf), xsb(buf), acc);
-                if (more) sstore(buf ^ 1, sv, xsv);
+                if (sb + 1 < sb1) sstore(buf ^ 1, sv, xsv);
                 __syncthreads();
-                cur = nxt;
+            };
+            // unrolled by two, the weights alternating between ra and rb: no
+            // register copy (which would wait for the loads in flight)
+            for (int sb = sb0; sb < sb1; sb += 2) {
+                step(sb, ra, rb);
+                if (sb + 1 >= sb1) break;
+                step(sb + 1, rb, ra);
             }
             // the lane's 4 outputs: streams 16 g + 4 kg + v of its row
             const int s0 = 16 * g + 4 * kg;
