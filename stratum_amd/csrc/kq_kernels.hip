@@ -324,23 +324,34 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u32x2a __attribute__((ext_vector_type(2), aligned(4)));
 
+// Weight loads use the default cache policy.  The nontemporal policy
+// (global_load ... nt) lifts a plain read stream on this GPU from about 6.4
+// to 7.1 TB/s, but here neighbouring lanes read one cache line through
+// different load instructions (a block's header and the two quant vectors
+// of a 64-weight chunk), and with nt each of them fetches the line again:
+// measured 2x slower for Q6_K, 1.2x for Q4_K.
+template <typename V>
+__device__ __forceinline__ V wload(wptr p) {
+    return *reinterpret_cast<const KQ_GLOBAL V*>(p);
+}
+
 __device__ __forceinline__ uint4 ld16(wptr p) {
-    const u32x4 v = *reinterpret_cast<const KQ_GLOBAL u32x4*>(p);
+    const u32x4 v = wload<u32x4>(p);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 __device__ __forceinline__ uint4 ld16a4(wptr p) {
-    const u32x4a v = *reinterpret_cast<const KQ_GLOBAL u32x4a*>(p);
+    const u32x4a v = wload<u32x4a>(p);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 __device__ __forceinline__ uint2 ld8a4(wptr p) {
-    const u32x2a v = *reinterpret_cast<const KQ_GLOBAL u32x2a*>(p);
+    const u32x2a v = wload<u32x2a>(p);
     return make_uint2(v.x, v.y);
 }
 __device__ __forceinline__ uint32_t ld4(wptr p) {
-    return *reinterpret_cast<const KQ_GLOBAL uint32_t*>(p);
+    return wload<uint32_t>(p);
 }
 __device__ __forceinline__ uint32_t ld2(wptr p) {
-    return *reinterpret_cast<const KQ_GLOBAL uint16_t*>(p);
+    return wload<uint16_t>(p);
 }
 
 struct RawQ4 { uint4 hd, qa, qb; };
@@ -1037,6 +1048,15 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
     const XStage<TYPE> xg = {S.x, S.x_stride, K / (4 * G4), ngx * (K / (4 * G4)), NC};
     f32x4 xv[G4];
     if (restage) xg.load(tid, xv);            // first round of x, ahead of the weights
+    // A second round (x longer than one round of the workgroup, e.g. Q6_K
+    // at K = 17408 with 1024 lanes) is loaded together with the first, so
+    // its latency is not paid after the first round's stores.  Types with
+    // 16-float groups only: their registers allow it (Q4_K needs a second
+    // round only beyond K = 32768).
+    constexpr bool PRE2 = G4 == 4;
+    const bool two = PRE2 && restage && xg.total > T;   // uniform
+    f32x4 xv2[PRE2 ? G4 : 1];
+    if (PRE2 && two) xg.load(tid + T, xv2);
 
     // first DEPTH batches: static (wave w takes chunks 64w .., then
     // 64(W + w) ..); their latency overlaps the staging
@@ -1050,7 +1070,12 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
 
     if (restage) {
         bool bad = xg.store(tid, xv, SCTYPE, true, xl, xs);
-        for (int gi = tid + T; gi < xg.total; gi += T) {
+        int gi0 = tid + T;
+        if (PRE2 && two) {
+            bad |= xg.store(gi0, xv2, SCTYPE, true, xl, xs);
+            gi0 += T;
+        }
+        for (int gi = gi0; gi < xg.total; gi += T) {
             xg.load(gi, xv);
             bad |= xg.store(gi, xv, SCTYPE, true, xl, xs);
         }

@@ -306,6 +306,26 @@ def test_gemv_x_all_below_window(port, qtype, scale):
     assert same_values(got, want), f"{K.TYPE_NAMES[qtype]} x ~ {scale:.1e} not bit-identical"
 
 
+@pytest.mark.parametrize("where", [None, 5000, 9000])
+@pytest.mark.parametrize("Kd", [6144, 12288])
+@pytest.mark.parametrize("qtype", [14, 10, 42])
+def test_gemv_x_staging_rounds(port, qtype, Kd, where, monkeypatch):
+    """x longer than one staging round of the workgroup (256 lanes: 4096
+    values per round for 16-value groups): two rounds (the second loaded
+    with the first) and three, with an out-of-window x value in the second
+    or third round (it must still switch every workgroup to the unscaled
+    path)."""
+    monkeypatch.setenv("KQ_WG_THREADS", "256")
+    N = 96
+    w = synth.tensor(qtype, N, Kd, 540 + qtype)
+    x = synth.gaussian(synth.rng(541), Kd)
+    if where is not None and where < Kd:
+        x[where] = 2.0 ** 60
+    print(f"staging rounds type={qtype} K={Kd} big x at {where}", flush=True)
+    check_close(gpu_gemv(qtype, w, x, N, Kd), port.gemv(qtype, w, x, N, Kd),
+                f"{K.TYPE_NAMES[qtype]} K={Kd} rounds, x[{where}] = 2^60")
+
+
 @pytest.mark.parametrize("wide", [False, True])
 def test_segments_shared_x_across_types(port, wide):
     """Segments that share one x in different ways: sums recomputed from a
