@@ -163,11 +163,61 @@ def _check(L, rc):
         raise RuntimeError(L.kq_last_error().decode())
 
 
-def other_configs(L, torch, stream, host_w) -> dict:
-    sh = stream.cuda_stream
-    out = {}
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 
-    # one Q4_K GEMV, W 1024 x 1024 (4096 blocks), batch 1
+
+def multiseq_mfma(L, torch, stream, host_w) -> dict:
+    """configs[3] on the matrix cores (kq_gemv_multix_mfma_dev, B >= 16).
+
+    Time per call with HIP events on the launch stream; TFLOP/s counts the
+    product's 2*N*K*B flops; mfma_util counts what the kernel issues (three
+    bf16 planes of x, streams padded to 16) against the dense bf16 peak.
+    Tolerance: every output against the exact multi-x path (bit-identical to
+    the reference's scalar routine in the GPU tests): max |a-b|/max(|b|,1e-6),
+    the fraction within 1e-5, and max |a-b| / sum_k |w_k x_k| (the error
+    relative to the magnitude of the terms, |W| from the device dequant)."""
+    sh = stream.cuda_stream
+    res = {}
+    for name, t, N, K in (("ffn_gate", 12, 17408, 5120), ("ffn_up", 12, 17408, 5120),
+                          ("ffn_down", 14, 5120, 17408)):
+        cm = _copies(torch, host_w[name])
+        wabs = torch.empty(N * K, dtype=torch.float32, device="cuda")
+        _check(L, L.kq_dequant_dev(t, cm[0].data_ptr(), wabs.data_ptr(), N * K // 256, sh))
+        wabs = wabs.view(N, K).abs_()
+        for B in (16, 32, 64):
+            xs = torch.from_numpy(np.stack([synth.gaussian(synth.rng(3900 + s), K)
+                                            for s in range(B)])).cuda()
+            ym = torch.empty(B * N, dtype=torch.float32, device="cuda")
+            ye = torch.empty(B * N, dtype=torch.float32, device="cuda")
+            us = _events_us(torch, stream, lambda i: _check(L, L.kq_gemv_multix_mfma_dev(
+                t, cm[i % len(cm)].data_ptr(), xs.data_ptr(), ym.data_ptr(), B, N, K, sh)),
+                20)
+            _check(L, L.kq_gemv_multix_mfma_dev(t, cm[0].data_ptr(), xs.data_ptr(),
+                                                ym.data_ptr(), B, N, K, sh))
+            _check(L, L.kq_gemv_multix_dev(t, cm[0].data_ptr(), xs.data_ptr(), ye.data_ptr(),
+                                           B, N, K, sh))
+            mag = torch.matmul(xs.abs(), wabs.t()).reshape(-1)
+            torch.cuda.synchronize()
+            d = (ym - ye).abs()
+            rel = d / ye.abs().clamp_min(1e-6)
+            nb = algo_bytes(t, N, K, B)
+            flops = 2.0 * N * K * B
+            issued = 3 * 2.0 * N * K * ((B + 15) // 16 * 16)
+            res[f"{name}_B{B}"] = {
+                "us_per_call": round(us, 2), "us_per_stream": round(us / B, 2),
+                "GB/s": round(nb / us / 1e3, 1), "TFLOP/s": round(flops / us / 1e6, 2),
+                "mfma_util": round(issued / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4),
+                "max_rel_err_vs_exact": float(f"{rel.max().item():.3e}"),
+                "frac_within_1e-5": round((rel <= 1e-5).float().mean().item(), 5),
+                "max_err_over_mag": float(f"{(d / mag.clamp_min(1e-30)).max().item():.3e}")}
+            del xs, ym, ye, mag, d, rel
+        del cm, wabs
+    return res
+
+
+def cfg1(L, torch, stream, host_w) -> dict:
+    """one Q4_K GEMV, W 1024 x 1024 (4096 blocks), batch 1."""
+    sh = stream.cuda_stream
     w = synth.tensor(KQ.TYPE_Q4_K, 1024, 1024, 3000)
     cw = _copies(torch, w)
     x = torch.from_numpy(synth.gaussian(synth.rng(3001), 1024)).cuda()
@@ -175,11 +225,12 @@ def other_configs(L, torch, stream, host_w) -> dict:
     us = _events_us(torch, stream, lambda i: _check(L, L.kq_gemv_dev(
         12, cw[i % len(cw)].data_ptr(), x.data_ptr(), None, y.data_ptr(), 1024, 1024, sh)), 200)
     nb = algo_bytes(12, 1024, 1024)
-    out["cfg1_q4k_1024x1024"] = {"us_per_call": round(us, 2), "bytes": nb,
-                                 "GB/s": round(nb / us / 1e3, 1)}
-    del cw
+    return {"us_per_call": round(us, 2), "bytes": nb, "GB/s": round(nb / us / 1e3, 1)}
 
-    # Qwen3-0.6B layer set (4 launches) and the LM head
+
+def cfg2(L, torch, stream, host_w) -> dict:
+    """Qwen3-0.6B layer set (4 launches) and the LM head."""
+    sh = stream.cuda_stream
     spec = {n: (t, N, K, xn) for n, t, N, K, xn in QWEN06B}
     xl = {"h": 1024, "attn": 2048, "ff": 3072}
     hw = {n: synth.tensor(t, N, K, 3100 + i) for i, (n, t, N, K, _) in enumerate(QWEN06B)}
@@ -219,10 +270,12 @@ def other_configs(L, torch, stream, host_w) -> dict:
         sh)), 50)
     nb = algo_bytes(14, 151936, 1024)
     res["lm_head_q6k"] = {"us_per_call": round(us, 2), "bytes": nb, "GB/s": round(nb / us / 1e3, 1)}
-    out["cfg2_qwen3_0.6b"] = res
-    del cl
+    return res
 
-    # configs[2] extra: gate + up as Q2_K and as type 42 (one launch of two tensors)
+
+def cfg3(L, torch, stream, host_w) -> dict:
+    """configs[2] extra: gate + up as Q2_K and as type 42 (one launch of two tensors)."""
+    sh = stream.cuda_stream
     res = {}
     q2 = [synth.tensor(KQ.TYPE_Q2_K, 17408, 5120, 3400 + i) for i in range(2)]
     for t, name in ((KQ.TYPE_Q2_K, "q2k"), (KQ.TYPE_Q2K_NIB, "type42")):
@@ -244,9 +297,13 @@ def other_configs(L, torch, stream, host_w) -> dict:
         nb = 2 * algo_bytes(t, 17408, 5120)
         res[name] = {"us_per_launch": round(us, 2), "bytes": nb, "GB/s": round(nb / us / 1e3, 1)}
         del cg, arrs
-    out["cfg3_gate_up_q2k_type42"] = res
+    return res
 
-    # MULTISEQ, B streams with one weight pass (27B gate / up / down)
+
+def cfg4(L, torch, stream, host_w) -> dict:
+    """MULTISEQ, B streams with one weight pass (27B gate / up /
+    down), exact path (each stream bit-identical to its single-stream result)."""
+    sh = stream.cuda_stream
     res = {}
     for name, t, N, K in (("ffn_gate", 12, 17408, 5120), ("ffn_up", 12, 17408, 5120),
                           ("ffn_down", 14, 5120, 17408)):
@@ -263,9 +320,13 @@ def other_configs(L, torch, stream, host_w) -> dict:
                                    "GB/s": round(nb / us / 1e3, 1),
                                    "TFLOP/s": round(2.0 * N * K * B / us / 1e6, 2)}
         del cm
-    out["cfg4_multiseq_exact"] = res
+    return res
 
-    # MoE gather, 128 experts, top-8, hidden 2048, expert ffn 768, Q4_K
+
+def cfg5(L, torch, stream, host_w) -> dict:
+    """MoE gather, 128 experts, top-8, hidden 2048, expert ffn
+    768, Q4_K; a step is top-k on the device, gate+up, down."""
+    sh = stream.cuda_stream
     E, H, F, k = 128, 2048, 768, 8
     rbg, rbd = L.kq_row_bytes(12, H), L.kq_row_bytes(12, F)
     gsl, dsl = F * rbg, H * rbd
@@ -305,8 +366,23 @@ def other_configs(L, torch, stream, host_w) -> dict:
         res[f"B{B}"] = {"us_per_layer": round(us, 2), "distinct_experts": distinct,
                         "bytes": nb, "GB/s": round(nb / us / 1e3, 1),
                         "launches": 3}
-    out["cfg5_moe_128e_top8"] = res
     del cm
+    return res
+
+
+# bench.py --only NAME runs one of these (the keys of other_configs' result)
+OTHER = {"cfg1_q4k_1024x1024": cfg1, "cfg2_qwen3_0.6b": cfg2, "cfg3_gate_up_q2k_type42": cfg3,
+         "cfg4_multiseq_exact": cfg4, "cfg4_multiseq_mfma": multiseq_mfma,
+         "cfg5_moe_128e_top8": cfg5}
+
+
+def other_configs(L, torch, stream, host_w, only=None) -> dict:
+    out = {}
+    for name, fn in OTHER.items():
+        if only is None or name == only:
+            out[name] = fn(L, torch, stream, host_w)
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
     return out
 
 
@@ -324,6 +400,9 @@ def main() -> int:
                     help="time only the 27B layer set (skip BASELINE's other configurations)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 5 copies of 64 MiB (counter calibration for rocprofv3 --pmc)")
+    ap.add_argument("--only", choices=sorted(OTHER),
+                    help="run only this one of BASELINE's other configurations and print its "
+                         "figures (profiling runs of one path)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -355,6 +434,12 @@ def main() -> int:
     ys = {name: torch.empty(N, dtype=torch.float32, device="cuda") for name, _, N, _, _ in LAYER_27B}
     stream = torch.cuda.current_stream()
     sh = stream.cuda_stream
+    if args.only:
+        del copies, dev0
+        res = other_configs(L, torch, stream, host_w, only=args.only)
+        print(json.dumps({"only": args.only, "data": "synthetic (seeded k-quant super-blocks, "
+                          "x ~ N(0,1))", "figures": res[args.only]}), flush=True)
+        return 0
 
     # segment arrays of every (copy, group), built once
     seg_arrays = []
