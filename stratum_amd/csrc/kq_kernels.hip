@@ -1699,13 +1699,16 @@ __global__ __launch_bounds__(1024) void kq_moe_group_kernel(MoeGroupArg a) {
     extern __shared__ __align__(16) int lds_i[];
     int* cnt = lds_i;                 // [E]
     int* gid = cnt + a.E;             // [E] group index of expert e
-    int* ms = gid + a.E;              // [nm] the members' experts
+    // [4 ceil(nm/4)] the members' experts (-1: none), 16-byte aligned, the
+    // tail past nm filled with -1 (it is read in whole int4s)
+    int* ms = lds_i + ((2 * a.E + 3) & ~3);
+    const int nm4 = (a.nm + 3) >> 2;
     __shared__ int wsum[16];
     const int tid = threadIdx.x, T = blockDim.x, lane = tid & 63, wave = tid >> 6;
     for (int e = tid; e < a.E; e += T) cnt[e] = 0;
     __syncthreads();
-    for (int m = tid; m < a.nm; m += T) {
-        const int e = a.sel[m];
+    for (int m = tid; m < 4 * nm4; m += T) {
+        const int e = m < a.nm ? a.sel[m] : -1;
         const int ok = e >= 0 && e < a.E;
         ms[m] = ok ? e : -1;
         if (ok) atomicAdd(&cnt[e], 1);
@@ -1733,27 +1736,37 @@ __global__ __launch_bounds__(1024) void kq_moe_group_kernel(MoeGroupArg a) {
     for (int i = 0; i < (T >> 6); i++) nd += wsum[i];
     __syncthreads();
     if (tid == 0) *a.ng = a.nt * nd;
-    // one thread per distinct expert collects its members in increasing m
-    for (int e = tid; e < a.E; e += T) {
-        const int c = cnt[e];
-        if (c == 0) continue;
-        for (int r = 0; r * a.mch < c; r++)
+    // One thread per member: its place j among the members of its expert
+    // (the members before it with the same expert, so places follow
+    // increasing m), then its slot j % mch of run j / mch; the first member
+    // of a run writes the run's header.  The scan reads ms[] at the same
+    // index in every lane (broadcast), four entries per LDS read.
+    for (int m0 = 0; m0 < a.nm; m0 += T) {
+        const int m = m0 + tid;
+        const int e = m < a.nm ? ms[m] : -1;
+        int j = 0;
+        const int lim = min(a.nm, m0 + T);               // uniform bound of the scan
+        for (int q = 0; q < min(nm4, (lim + 3) >> 2); q++) {
+            const int4 v = reinterpret_cast<const int4*>(ms)[q];
+            const int b = 4 * q;
+            j += (b + 0 < m) & (v.x == e);
+            j += (b + 1 < m) & (v.y == e);
+            j += (b + 2 < m) & (v.z == e);
+            j += (b + 3 < m) & (v.w == e);
+        }
+        if (e >= 0) {
+            const int r = j / a.mch, slot = j - r * a.mch;
             for (int t = 0; t < a.nt; t++) {
                 MxGroup* G = a.groups + (size_t)t * nd + gid[e] + r;
-                G->w = a.w[t] + (size_t)e * a.estride;
-                G->y = a.y[t];
-                G->M = min(c - r * a.mch, a.mch);
-                G->pad_ = 0;
+                G->xi[slot] = m / a.x_div;
+                G->yi[slot] = m;
+                if (slot == 0) {
+                    G->w = a.w[t] + (size_t)e * a.estride;
+                    G->y = a.y[t];
+                    G->M = min(cnt[e] - j, a.mch);
+                    G->pad_ = 0;
+                }
             }
-        int j = 0;
-        for (int m = 0; m < a.nm; m++) {
-            if (ms[m] != e) continue;
-            for (int t = 0; t < a.nt; t++) {
-                MxGroup* G = a.groups + (size_t)t * nd + gid[e] + j / a.mch;
-                G->xi[j % a.mch] = m / a.x_div;
-                G->yi[j % a.mch] = m;
-            }
-            j++;
         }
     }
 }
@@ -2529,7 +2542,7 @@ int kqk_launch_moe_group(const int* sel, int nm, int E, int nt, int x_div, int m
     a.estride = estride;
     a.groups = static_cast<MxGroup*>(groups);
     a.ng = ng;
-    const size_t lds = (size_t)(2 * E + nm) * sizeof(int);
+    const size_t lds = (size_t)(((2 * E + 3) & ~3) + 4 * ((nm + 3) / 4)) * sizeof(int);
     hipLaunchKernelGGL(kq_moe_group_kernel, dim3(1), dim3(1024), lds, st, a);
     return (int)hipGetLastError();
 }
