@@ -2382,7 +2382,10 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
 // and at most ngmax groups.  plan[]: 0 threads, 1 S (members per weight
 // load), 2 RB (rows per item), 3 nblk (items per group), 4 TC (chunks per x
 // tile), 5 sums bytes, 6 x buffer bytes, 7 mch (members staged together).
-// Returns the LDS bytes, or -1.
+// Returns the LDS bytes, or -1.  ngm (MoE batches, else null): ngm[m] is
+// the expected number of groups when member lists are cut into runs of at
+// most m members (m = 1..MX_MC); the item count then follows the chosen
+// run length, as the grouping kernel will cut them.
 //
 // The choice comes from a small cost model, in instruction issues of the
 // busiest SIMD: item rounds x member chunks x (steps x task-step cost +
@@ -2390,7 +2393,8 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
 // costs c0 (shared by the S members) + S c1 (per member) issues, per-type
 // counts from the generated code; a SIMD with fewer than 3 tasks is
 // latency-bound and taken as 3.
-long kqk_mx_plan(int type, int N, int K, int mmax, int ngmax, int grid, int lds_max, int* plan) {
+long kqk_mx_plan(int type, int N, int K, int mmax, int ngmax, int grid, int lds_max, int* plan,
+                 const float* ngm) {
     const int xpc = xs_per_chunk(type);
     if (xpc < 0 || mmax < 1 || mmax > MX_MAXM || ngmax < 1 || N < 1 || K <= 0 || (K & 255) ||
         grid < 1)
@@ -2430,7 +2434,9 @@ long kqk_mx_plan(int type, int N, int K, int mmax, int ngmax, int grid, int lds_
             lds = head + sums + 2 * xt;
         }
         const int ntile = (NC + TC - 1) / TC;
-        const int nmc = (mmax + mch - 1) / mch;
+        // MoE runs are cut at mch members: one member chunk each, and
+        // ngm[mch] groups expected
+        const int nmc = ngm ? 1 : (mmax + mch - 1) / mch;
         for (int S = 1; S <= 2; S++) {
             if (S > 1 && S > mch) break;
             const int nsg = (mch + S - 1) / S;
@@ -2442,7 +2448,7 @@ long kqk_mx_plan(int type, int N, int K, int mmax, int ngmax, int grid, int lds_
                 if (nblk > nblk0 && (N + RB - 1) / RB != nblk) continue;
                 const int ntask = ((RB + RPT - 1) / RPT) * nsg;
                 if (ntask > W * MX_TW) continue;
-                const long items = (long)ngmax * nblk;
+                const long items = ngm ? (long)ceil((double)ngm[mch] * nblk) : (long)ngmax * nblk;
                 const long rounds = (items + grid - 1) / grid;
                 const int simd = (ntask + 3) / 4;
                 const double step = (simd < 3 ? 3 : simd) * (c0 + S * c1);

@@ -40,7 +40,8 @@ int kqk_set_max_lds(int bytes);
  * -1); gdev == NULL launches one inline group of M members (x_j = X + j
  * x_stride, y_j = Y + j y_stride) */
 #define KQK_MX_PLAN 8
-long kqk_mx_plan(int type, int N, int K, int mmax, int ngmax, int grid, int lds_max, int* plan);
+long kqk_mx_plan(int type, int N, int K, int mmax, int ngmax, int grid, int lds_max, int* plan,
+                 const float* ngm);
 int kqk_launch_mx(int type, const int* plan, long lds, int grid, const void* w, int M,
                   const void* gdev, const int* ngdev, const float* X, long x_stride, float* Y,
                   long y_stride, int N, int K, hipStream_t st);

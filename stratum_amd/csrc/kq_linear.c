@@ -347,6 +347,66 @@ int kq_gemv_segments_dev(const kq_segment* segs, int nseg, kq_stream stream) {
     return launch_segs(h, nh, pick(stream));
 }
 
+/* Multi-x launch plans come from a cost model that scans every row-block
+ * count, which costs more host time than a small launch takes on the GPU;
+ * a decode loop asks for the same few shapes on every call, so the plans
+ * are kept in a small table (replaced round robin).  moe[] is (B, k, E,
+ * ntensors) for a MoE batch, zeros otherwise. */
+typedef struct {
+    int used, type, N, K, mmax, ngmax, grid, lds_max, moe[4];
+    long lds;
+    int plan[KQK_MX_PLAN];
+} mx_plan_entry;
+#define MX_PLAN_CACHE 32
+static mx_plan_entry g_plans[MX_PLAN_CACHE];
+static int g_plan_next;
+
+static long mx_plan(int type, int N, int K, int mmax, int ngmax, int grid, const int moe[4],
+                    int* plan) {
+    for (int i = 0; i < MX_PLAN_CACHE; i++) {
+        const mx_plan_entry* c = &g_plans[i];
+        if (c->used && c->type == type && c->N == N && c->K == K && c->mmax == mmax &&
+            c->ngmax == ngmax && c->grid == grid && c->lds_max == g_kq.lds_max &&
+            !memcmp(c->moe, moe, sizeof c->moe)) {
+            memcpy(plan, c->plan, sizeof c->plan);
+            return c->lds;
+        }
+    }
+    long lds;
+    if (moe[0] > 0) {
+        /* MoE batch of B = moe[0] tokens, k = moe[1] of E = moe[2] experts:
+         * under uniform routing an expert is chosen by a token with
+         * probability p = k/E, so its member count c is Binomial(B, p); with
+         * member lists cut into runs of at most m members the expected
+         * number of groups is nt * E * sum_c P(c) ceil(c/m) */
+        const int B = moe[0], k = moe[1], E = moe[2], nt = moe[3];
+        const double pe = (double)k / E;
+        double pc[KQ_MOE_MAX_TOKENS + 1];
+        float ngm[17];
+        pc[0] = pow(1.0 - pe, B);
+        for (int c = 1; c <= B; c++)          /* P(c) from P(c-1): binomial recurrence */
+            pc[c] = pe < 1.0 ? pc[c - 1] * (double)(B - c + 1) / c * pe / (1.0 - pe)
+                             : (c == B ? 1.0 : 0.0);
+        for (int m = 1; m <= 16; m++) {
+            double runs = 0.0;
+            for (int c = 1; c <= B; c++) runs += pc[c] * (double)((c + m - 1) / m);
+            ngm[m] = (float)(nt * E * runs);
+        }
+        ngm[0] = ngm[1];
+        lds = kqk_mx_plan(type, N, K, mmax, ngmax, grid, g_kq.lds_max, plan, ngm);
+    } else {
+        lds = kqk_mx_plan(type, N, K, mmax, ngmax, grid, g_kq.lds_max, plan, NULL);
+    }
+    mx_plan_entry* c = &g_plans[g_plan_next];
+    g_plan_next = (g_plan_next + 1) % MX_PLAN_CACHE;
+    c->used = 1; c->type = type; c->N = N; c->K = K; c->mmax = mmax; c->ngmax = ngmax;
+    c->grid = grid; c->lds_max = g_kq.lds_max;
+    memcpy(c->moe, moe, sizeof c->moe);
+    c->lds = lds;
+    memcpy(c->plan, plan, sizeof c->plan);
+    return lds;
+}
+
 /* B streams with one pass over the weights per group of up to 64 streams
  * (the multi-x kernel); each stream's y equals its single-stream result bit
  * for bit. */
@@ -361,7 +421,8 @@ int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,
     for (int s0 = 0; s0 < B; ) {
         const int nb = B - s0 < 64 ? B - s0 : 64;
         int plan[KQK_MX_PLAN];
-        const long lds = kqk_mx_plan(type, N, K, nb, 1, grid, g_kq.lds_max, plan);
+        static const int no_moe[4] = {0, 0, 0, 0};
+        const long lds = mx_plan(type, N, K, nb, 1, grid, no_moe, plan);
         if (lds < 0) {
             /* x too long to stage even in 8-chunk tiles: single-stream launches */
             for (int s = s0; s < s0 + nb; s++)
@@ -661,19 +722,15 @@ int kq_moe_gemv_dev(const kq_moe_op* op, const int* sel, int B, int k, int E, kq
     }
     /* several tokens: expert groups built on the device, then one weight
      * pass per selected expert for all of its tokens.  The launch is
-     * planned for the typical group: under uniform routing the expected
-     * number of distinct experts is E (1 - (1 - k/E)^B), each with nm / that
-     * many members; the member lists are cut into runs of the planned size
-     * so that every work item carries about the same load. */
+     * planned for uniform routing (mx_plan): the planner picks the run
+     * length, and with it the item count, and the grouping kernel cuts the
+     * member lists accordingly. */
     const int nm = B * k, dmax = E < nm ? E : nm;
-    double dexp = E * (1.0 - pow(1.0 - (double)k / E, B));
-    if (dexp < 1.0) dexp = 1.0;
-    int mplan = (int)ceil(nm / dexp);
-    mplan = mplan < 1 ? 1 : mplan > B ? B : mplan;
+    const int mmax = B < 16 ? B : 16;
     const int grid = plan_grid();
     int plan[KQK_MX_PLAN];
-    const long lds = kqk_mx_plan(op->type, op->n_out, op->k_in, mplan, nt * (int)ceil(dexp), grid,
-                                 g_kq.lds_max, plan);
+    const int moe[4] = {B, k, E, nt};
+    const long lds = mx_plan(op->type, op->n_out, op->k_in, mmax, nt * dmax, grid, moe, plan);
     if (lds < 0) return kq_fail("kq_moe_gemv_dev: no launch plan for K=%d", op->k_in);
     const int mch = plan[7];
     const int ngmax = nt * (dmax + (nm + mch - 1) / mch);
