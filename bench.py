@@ -18,7 +18,10 @@ layer's weights (860 MB) are rotated so no step finds its weights in the
 256 MB MALL or the L2s.
 
 value = algorithmic bytes of the layer set / measured time per step, with
-algorithmic bytes per matvec = N*(K/256)*block_bytes + 4K + 4N.
+algorithmic bytes per matvec = N*(K/256)*block_bytes + 4K + 4N.  Before the
+W warm-up steps the step runs untimed for 50 ms (clock_ramp_ms): an idle
+GPU needs ~20 ms of sustained work to reach its clocks, as a running decode
+loop has.
 roofline: the dominant launch ([gate, up], kernel kq_segs_kernel<1, 1, false>)
 timed per launch with HIP events on the stream it runs on; traffic from
 profiles/traffic.json (rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated).
@@ -139,7 +142,26 @@ QWEN06B_GROUPS = [["attn_q", "attn_k", "attn_v"], ["attn_output"], ["ffn_gate", 
 ROTATE_BYTES = 600 << 20
 
 
+RAMP_MS = 50.0   # untimed work before any timing: the GPU's clocks take ~20 ms to ramp up
+
+
+def ramp(torch, fn, ms=RAMP_MS):
+    """Runs fn untimed for `ms` of wall time.  After an idle period the GPU
+    needs about 20 ms of sustained work to reach its clocks (measured: the
+    27B layer set runs at ~69 us per step after 1.4 ms of warm-up and ~64 us
+    after 20 ms or more), and a decode loop runs continuously."""
+    t0, i = time.perf_counter(), 0
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        fn(i)
+        i += 1
+        if i % 32 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return i
+
+
 def _events_us(torch, stream, fn, reps, warmup=3):
+    ramp(torch, fn, 20.0)
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
@@ -468,6 +490,7 @@ def main() -> int:
                 raise RuntimeError(L.kq_last_error().decode())
 
     def timed(fn, steps, warmup):
+        ramp(torch, fn)
         for i in range(warmup):
             fn(i)
         torch.cuda.synchronize()
@@ -537,6 +560,7 @@ def main() -> int:
             "launches_per_step": len(GROUPS),
         },
         "us_per_layer_set": round(ms_per_step * 1e3, 2),
+        "clock_ramp_ms": RAMP_MS,
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "host_enqueue_us_per_step": round(enq_ms * 1e3, 1),
         "separate_launches": None if sep_ms is None else {
