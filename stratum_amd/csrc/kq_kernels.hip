@@ -1616,63 +1616,57 @@ __global__ __launch_bounds__(256) void kq_moe_topk_kernel(const float* probs, in
     }
 }
 
-// The same selection for E <= 256 by ranks: expert e's slot is the number
+// The same selection for E <= 1024 by ranks: expert e's slot is the number
 // of eligible experts that beat it (a larger weight, or an equal weight and
-// a lower id); one pass over the weights (LDS broadcast) per expert a lane
-// holds, instead of k dependent wave reductions.
-template <int NI>   // experts per lane: E <= 64 * NI
-__global__ __launch_bounds__(256) void kq_moe_topk_rank_kernel(const float* probs, int B, int E,
+// a lower id).  One 1024-lane workgroup per token: the weights go to LDS,
+// lane (p, e) counts the experts of part p (of P) that beat e, and the P
+// partial counts are added.  (One wave per token, scanning all E experts,
+// was a serial chain of ~E x 15 dependent instructions: 8 us at E = 128.)
+__global__ __launch_bounds__(1024) void kq_moe_topk_rank_kernel(const float* probs, int B, int E,
                                                               int k, int* sel, float* selw) {
-    __shared__ __align__(16) float wl[4][64 * NI];
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int tok = blockIdx.x * 4 + wv;
-    if (tok >= B) return;                      // uniform over the wave
+    __shared__ __align__(16) float wl[1024];
+    __shared__ int part[1024];
+    __shared__ int nel;
+    const int tid = threadIdx.x, tok = blockIdx.x;
+    const int E64 = (E + 63) & ~63;                  // experts, padded: <= 1024
+    // parts: a power of two P with P * E64 <= 1024 and E64 / P a multiple of 4
+    int P = 1;
+    while (2 * P * E64 <= 1024 && (E64 / (2 * P)) % 4 == 0) P *= 2;
+    const int L = E64 / P;                           // experts per part
     const float* w = probs + (size_t)tok * E;
-    float v[NI];
-    bool el[NI];
-    int nel = 0;
+    if (tid < E64) wl[tid] = tid < E ? w[tid] : -1.0f;   // -1: never eligible
+    if (tid == 0) nel = 0;
+    __syncthreads();
+    const int e = tid % E64, p = tid / E64;
+    if (p < P) {
+        const float v = wl[e];
+        int r = 0;
+        const int q0 = p * L;
+        for (int q = q0; q < q0 + L; q += 4) {
+            const float4 o = *reinterpret_cast<const float4*>(&wl[q]);
+            const float ov[4] = {o.x, o.y, o.z, o.w};
 #pragma unroll
-    for (int i = 0; i < NI; i++) v[i] = w[min(lane + 64 * i, E - 1)];   // all loads in flight
-#pragma unroll
-    for (int i = 0; i < NI; i++) {
-        const int e = lane + 64 * i;
-        v[i] = e < E ? v[i] : -1.0f;
-        el[i] = v[i] > -1.0f;                  // NaN is not eligible either
-        wl[wv][e] = v[i];
-        nel += __popcll(__ballot(el[i]));
-    }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    int rank[NI];
-#pragma unroll
-    for (int i = 0; i < NI; i++) rank[i] = 0;
-    const int E4 = (E + 3) & ~3;
-    for (int q = 0; q < E4; q += 4) {
-        const float4 o = *reinterpret_cast<const float4*>(&wl[wv][q]);
-        const float ov[4] = {o.x, o.y, o.z, o.w};
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int eo = q + j;
-            const float x = ov[j];                 // -1 past E (never eligible)
-            const int xel = x > -1.0f;
-#pragma unroll
-            for (int i = 0; i < NI; i++) {
+            for (int j = 0; j < 4; j++) {
+                const float x = ov[j];
                 // bitwise, not short-circuit: straight-line compares
-                const int beat = (x > v[i]) | ((x == v[i]) & (eo < lane + 64 * i));
-                rank[i] += xel & beat;
+                const int beat = (x > v) | ((x == v) & (q + j < e));
+                r += (x > -1.0f) & beat;             // NaN is not eligible either
             }
         }
+        part[tid] = r;
+        if (p == 0 && e < E && v > -1.0f) atomicAdd(&nel, 1);
     }
-#pragma unroll
-    for (int i = 0; i < NI; i++) {
-        const int e = lane + 64 * i;
-        if (el[i] && rank[i] < k) {
-            sel[(size_t)tok * k + rank[i]] = e;
-            selw[(size_t)tok * k + rank[i]] = v[i];
+    __syncthreads();
+    if (tid < E) {
+        int rank = 0;
+        for (int i = 0; i < P; i++) rank += part[i * E64 + tid];
+        const float v = wl[tid];
+        if (v > -1.0f && rank < k) {
+            sel[(size_t)tok * k + rank] = tid;
+            selw[(size_t)tok * k + rank] = v;
         }
     }
-    for (int r = nel + lane; r < k; r += 64) {   // slots without an expert
+    for (int r = nel + tid; r < k; r += 1024) {     // slots without an expert
         sel[(size_t)tok * k + r] = -1;
         selw[(size_t)tok * k + r] = -1.0f;
     }
@@ -2519,13 +2513,9 @@ int kqk_launch_mx(int type, const int* plan, long lds, int grid, const void* w, 
 int kqk_launch_moe_topk(const float* probs, int B, int E, int k, int* sel, float* selw,
                         hipStream_t st) {
     if (B < 1 || E < 1 || E > 4096 || k < 1) return (int)hipErrorInvalidValue;
-    const dim3 g((B + 3) / 4), t(256);
-    if (E <= 64)
-        hipLaunchKernelGGL(kq_moe_topk_rank_kernel<1>, g, t, 0, st, probs, B, E, k, sel, selw);
-    else if (E <= 128)
-        hipLaunchKernelGGL(kq_moe_topk_rank_kernel<2>, g, t, 0, st, probs, B, E, k, sel, selw);
-    else if (E <= 256)
-        hipLaunchKernelGGL(kq_moe_topk_rank_kernel<4>, g, t, 0, st, probs, B, E, k, sel, selw);
+    if (E <= 1024)
+        hipLaunchKernelGGL(kq_moe_topk_rank_kernel, dim3(B), dim3(1024), 0, st, probs, B, E, k, sel,
+                           selw);
     else
         hipLaunchKernelGGL(kq_moe_topk_kernel, dim3((B + 3) / 4), dim3(256), 0, st, probs, B, E,
                            k, sel, selw);

@@ -50,7 +50,8 @@ def gpu_topk(probs, k):
 
 
 @pytest.mark.parametrize("B,E,k", [(16, 128, 8), (1, 128, 8), (5, 100, 6), (3, 4096, 8),
-                                   (2, 5, 5), (4, 64, 1)])
+                                   (2, 5, 5), (4, 64, 1), (2, 1000, 8), (1, 1024, 16),
+                                   (3, 1025, 4), (2, 192, 7)])
 def test_topk_dev_matches_oracle(port, B, E, k):
     r = np.random.default_rng(B * 1000 + E + k)
     probs = softmax_rows(r.standard_normal((B, E)).astype(np.float32))
@@ -59,6 +60,24 @@ def test_topk_dev_matches_oracle(port, B, E, k):
         ws, ww = port.topk(probs[s], k)
         assert list(sel[s]) == ws, s
         assert same_values(selw[s], ww), s
+
+
+@pytest.mark.parametrize("E", [200, 1000])
+def test_topk_dev_ties_across_parts(port, E):
+    """Wide router rows, where several lanes share one expert's comparisons:
+    all-equal weights (the lowest ids win), repeated values spread over the
+    whole row, and ineligible weights in between."""
+    r = np.random.default_rng(E)
+    rows = [np.full(E, 0.5 / E, np.float32),
+            r.integers(0, 4, E).astype(np.float32) * 0.25,
+            np.where(r.random(E) < 0.5, -1.5, r.integers(0, 3, E) * 0.5).astype(np.float32)]
+    probs = np.stack(rows)
+    for k in (1, 8, 16):
+        sel, selw = gpu_topk(probs, k)
+        for s in range(len(rows)):
+            ws, ww = port.topk(probs[s], k)
+            assert list(sel[s]) == ws, (E, s, k)
+            assert same_values(selw[s], ww), (E, s, k)
 
 
 def test_topk_dev_ties_and_ineligible(port):
