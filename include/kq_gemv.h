@@ -109,7 +109,10 @@ int kq_q4k_group(const float* x, int K,
 /* ----------------------------------------- device-pointer entry points
  * For a device-resident decode loop: all pointers are device pointers,
  * the call only enqueues work on `stream` (asynchronous).  x and xs must
- * be 16-byte aligned. */
+ * be 16-byte aligned.  The MoE batch and matrix-core entries use scratch
+ * buffers owned by the library (one per kind, grown on demand): calls of
+ * the same kind on different streams that overlap in time race on it;
+ * calls on one stream are ordered. */
 
 /* y = W . x (+ add when add != NULL), W = N rows of K/256 blocks of `type`. */
 int kq_gemv_dev(int type, const void* w, const float* x, const float* add, float* y,
