@@ -187,6 +187,35 @@ def _check(L, rc):
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
+# the CPU baseline beside each other configuration (cleared by --no-cpu-baseline)
+CPU = {"on": True}
+
+
+def cpu_impl(qtype: int):
+    """The reference's scalar routines (oracle/_ref) for the types it runs on
+    x86 (its type-42 kernel is NEON only), else the repo's restatement."""
+    from oracle import oracle as O
+    r = O.ref()
+    if r is not None and qtype in (KQ.TYPE_Q2_K, KQ.TYPE_Q4_K, KQ.TYPE_Q6_K):
+        return r, "reference"
+    return O.port(), "port"
+
+
+def cpu_us(fn, min_s: float = 0.3, max_n: int = 50) -> float:
+    """Mean host time of fn over at least min_s (after one untimed call)."""
+    fn()
+    t0, n = time.perf_counter(), 0
+    while True:
+        fn()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_s or n >= max_n:
+            return dt / n * 1e6
+
+
+def cpu_entry(us: float, kind: str, what: str) -> dict:
+    return {"us": round(us, 1), "cores": host_cores(), "kind": kind, "sample": what}
+
 
 def multiseq_mfma(L, torch, stream, host_w) -> dict:
     """configs[3] on the matrix cores (kq_gemv_multix_mfma_dev, B >= 16).
@@ -242,12 +271,19 @@ def cfg1(L, torch, stream, host_w) -> dict:
     sh = stream.cuda_stream
     w = synth.tensor(KQ.TYPE_Q4_K, 1024, 1024, 3000)
     cw = _copies(torch, w)
-    x = torch.from_numpy(synth.gaussian(synth.rng(3001), 1024)).cuda()
+    xh = synth.gaussian(synth.rng(3001), 1024)
+    x = torch.from_numpy(xh).cuda()
     y = torch.empty(1024, dtype=torch.float32, device="cuda")
     us = _events_us(torch, stream, lambda i: _check(L, L.kq_gemv_dev(
         12, cw[i % len(cw)].data_ptr(), x.data_ptr(), None, y.data_ptr(), 1024, 1024, sh)), 200)
     nb = algo_bytes(12, 1024, 1024)
-    return {"us_per_call": round(us, 2), "bytes": nb, "GB/s": round(nb / us / 1e3, 1)}
+    res = {"us_per_call": round(us, 2), "bytes": nb, "GB/s": round(nb / us / 1e3, 1)}
+    if CPU["on"]:
+        impl, kind = cpu_impl(12)
+        res["cpu"] = cpu_entry(cpu_us(lambda: impl.gemv(12, w, xh, 1024, 1024,
+                                                        threads=host_cores())), kind,
+                               "one call of the same GEMV")
+    return res
 
 
 def cfg2(L, torch, stream, host_w) -> dict:
@@ -264,8 +300,8 @@ def cfg2(L, torch, stream, host_w) -> dict:
     for n in hw:
         blob[offs[n]:offs[n] + hw[n].size] = hw[n]
     cb = _copies(torch, blob)
-    xq = {k: torch.from_numpy(synth.gaussian(synth.rng(3200 + j), n)).cuda()
-          for j, (k, n) in enumerate(xl.items())}
+    xqh = {k: synth.gaussian(synth.rng(3200 + j), n) for j, (k, n) in enumerate(xl.items())}
+    xq = {k: torch.from_numpy(v).cuda() for k, v in xqh.items()}
     yq = {n: torch.empty(N, dtype=torch.float32, device="cuda") for n, _, N, _, _ in QWEN06B}
     arrs = []
     for c in cb:
@@ -292,6 +328,14 @@ def cfg2(L, torch, stream, host_w) -> dict:
         sh)), 50)
     nb = algo_bytes(14, 151936, 1024)
     res["lm_head_q6k"] = {"us_per_call": round(us, 2), "bytes": nb, "GB/s": round(nb / us / 1e3, 1)}
+    if CPU["on"]:
+        impl, kind = cpu_impl(12)
+        res["cpu"] = cpu_entry(cpu_us(lambda: [impl.gemv(t, hw[n], xqh[xn], N, K, threads=host_cores())
+                                               for n, t, N, K, xn in QWEN06B]), kind,
+                               "the 7 matvecs of the layer set")
+        res["lm_head_q6k"]["cpu"] = cpu_entry(
+            cpu_us(lambda: impl.gemv(14, lm, xqh["h"], 151936, 1024, threads=host_cores())), kind,
+            "one LM-head GEMV")
     return res
 
 
@@ -306,7 +350,8 @@ def cfg3(L, torch, stream, host_w) -> dict:
             for q in q2]
         both = np.concatenate(ws)
         cg = _copies(torch, both)
-        xg = torch.from_numpy(synth.gaussian(synth.rng(3500), 5120)).cuda()
+        xgh = synth.gaussian(synth.rng(3500), 5120)
+        xg = torch.from_numpy(xgh).cuda()
         yg = [torch.empty(17408, dtype=torch.float32, device="cuda") for _ in range(2)]
         half = ws[0].size
         arrs = []
@@ -318,6 +363,11 @@ def cfg3(L, torch, stream, host_w) -> dict:
             arrs[i % len(arrs)], 2, sh)), 50)
         nb = 2 * algo_bytes(t, 17408, 5120)
         res[name] = {"us_per_launch": round(us, 2), "bytes": nb, "GB/s": round(nb / us / 1e3, 1)}
+        if CPU["on"]:
+            impl, kind = cpu_impl(t)
+            res[name]["cpu"] = cpu_entry(
+                cpu_us(lambda: [impl.gemv(t, wj, xgh, 17408, 5120, threads=host_cores())
+                                for wj in ws]), kind, "gate and up (two GEMVs)")
         del cg, arrs
     return res
 
@@ -331,8 +381,8 @@ def cfg4(L, torch, stream, host_w) -> dict:
                           ("ffn_down", 14, 5120, 17408)):
         cm = _copies(torch, host_w[name])
         for B in (8, 16, 64):
-            xs = torch.from_numpy(np.stack([synth.gaussian(synth.rng(3600 + s), K)
-                                            for s in range(B)])).cuda()
+            xsh = np.stack([synth.gaussian(synth.rng(3600 + s), K) for s in range(B)])
+            xs = torch.from_numpy(xsh).cuda()
             ysb = torch.empty(B * N, dtype=torch.float32, device="cuda")
             us = _events_us(torch, stream, lambda i: _check(L, L.kq_gemv_multix_dev(
                 t, cm[i % len(cm)].data_ptr(), xs.data_ptr(), ysb.data_ptr(), B, N, K, sh)),
@@ -341,6 +391,12 @@ def cfg4(L, torch, stream, host_w) -> dict:
             res[f"{name}_B{B}"] = {"us_per_call": round(us, 2), "us_per_stream": round(us / B, 2),
                                    "GB/s": round(nb / us / 1e3, 1),
                                    "TFLOP/s": round(2.0 * N * K * B / us / 1e6, 2)}
+            if CPU["on"]:
+                impl, kind = cpu_impl(t)
+                res[f"{name}_B{B}"]["cpu"] = cpu_entry(
+                    cpu_us(lambda: impl.gemv_multix(t, host_w[name], xsh, N, K,
+                                                    threads=host_cores()), min_s=0.2, max_n=5),
+                    kind, f"one call of {B} streams (the scalar routine per stream)")
         del cm
     return res
 
@@ -362,8 +418,10 @@ def cfg5(L, torch, stream, host_w) -> dict:
         lg = r.standard_normal((B, E)).astype(np.float32)
         p = np.exp(lg - lg.max(1, keepdims=True))
         probs = torch.from_numpy((p / p.sum(1, keepdims=True)).astype(np.float32)).cuda()
-        xm = torch.from_numpy(np.stack([synth.gaussian(r, H) for _ in range(B)])).cuda()
-        act = torch.from_numpy(np.stack([synth.gaussian(r, F) for _ in range(B * k)])).cuda()
+        xmh = np.stack([synth.gaussian(r, H) for _ in range(B)])
+        acth = np.stack([synth.gaussian(r, F) for _ in range(B * k)])
+        xm = torch.from_numpy(xmh).cuda()
+        act = torch.from_numpy(acth).cuda()
         sel = torch.empty(B * k, dtype=torch.int32, device="cuda")
         selw = torch.empty(B * k, dtype=torch.float32, device="cuda")
         yg, yu = (torch.empty(B * k * F, device="cuda") for _ in range(2))
@@ -388,6 +446,27 @@ def cfg5(L, torch, stream, host_w) -> dict:
         res[f"B{B}"] = {"us_per_layer": round(us, 2), "distinct_experts": distinct,
                         "bytes": nb, "GB/s": round(nb / us / 1e3, 1),
                         "launches": 3}
+        if CPU["on"]:
+            from oracle import oracle as O
+            impl, kind = cpu_impl(12)
+            rb = (rbg, rbg, rbd)
+            sl = (gsl, gsl, dsl)
+            selh = sel.cpu().numpy()
+            pr = probs.cpu().numpy()
+
+            def cpu_layer():
+                for s in range(B):            # moe_topk per token, then the selected slices
+                    es, _ = O.port().topk(pr[s], k)
+                    for rr, e in enumerate(es):
+                        m = s * k + rr
+                        for ti, (nout, kin, xv) in enumerate(((F, H, xmh[s]), (F, H, xmh[s]),
+                                                              (H, F, acth[m]))):
+                            off = e * sl[ti]
+                            impl.gemv(12, ex[ti][off:off + nout * rb[ti]], xv, nout, kin,
+                                      threads=host_cores())
+            del selh
+            res[f"B{B}"]["cpu"] = cpu_entry(cpu_us(cpu_layer, min_s=0.2, max_n=10), kind,
+                                            "top-k and the selected gate, up and down slices")
     del cm
     return res
 
@@ -456,6 +535,7 @@ def main() -> int:
     ys = {name: torch.empty(N, dtype=torch.float32, device="cuda") for name, _, N, _, _ in LAYER_27B}
     stream = torch.cuda.current_stream()
     sh = stream.cuda_stream
+    CPU["on"] = not args.no_cpu_baseline
     if args.only:
         del copies, dev0
         res = other_configs(L, torch, stream, host_w, only=args.only)
