@@ -477,6 +477,15 @@ OTHER = {"cfg1_q4k_1024x1024": cfg1, "cfg2_qwen3_0.6b": cfg2, "cfg3_gate_up_q2k_
          "cfg5_moe_128e_top8": cfg5}
 
 
+def _hbm_frac(o) -> None:
+    """Adds hbm_frac = GB/s / 8000 next to every algorithmic-bytes rate."""
+    if isinstance(o, dict):
+        if "GB/s" in o:
+            o["hbm_frac"] = round(o["GB/s"] / PEAK_HBM_GBS, 4)
+        for v in o.values():
+            _hbm_frac(v)
+
+
 def other_configs(L, torch, stream, host_w, only=None) -> dict:
     out = {}
     for name, fn in OTHER.items():
@@ -484,6 +493,7 @@ def other_configs(L, torch, stream, host_w, only=None) -> dict:
             out[name] = fn(L, torch, stream, host_w)
             torch.cuda.synchronize()
             torch.cuda.empty_cache()
+    _hbm_frac(out)
     return out
 
 
