@@ -2038,15 +2038,23 @@ __global__ __launch_bounds__(256) void kq_mfma_mx_kernel(MfArg A) {
             constexpr int NV = XB / 16 / 256;
             static_assert(NV * 256 * 16 == XB, "plane staging split");
             const u32x4* src = reinterpret_cast<const u32x4*>(A.planes);   // native vectors: no memcpy
-            auto sload = [&](int sb, u32x4 (&v)[NV], float& xsv) {
+            // this thread's offsets within a super-block's planes (and sums),
+            // fixed for the group: a super-block only moves a uniform base
+            uint32_t off[NV];
 #pragma unroll
-                for (int k = 0; k < NV; k++) {
-                    const int i = tid + 256 * k;
-                    const int j = i / (OPB / 16), rr = i - j * (OPB / 16);
-                    v[k] = src[((size_t)(sb * MI::NSUB + j) * A.NSG + g) * (OPB / 16) + rr];
-                }
+            for (int k = 0; k < NV; k++) {
+                const int i = tid + 256 * k;
+                const int j = i / (OPB / 16), rr = i - j * (OPB / 16);
+                off[k] = (uint32_t)((j * A.NSG + g) * (OPB / 16) + rr);
+            }
+            const uint32_t xoff = (uint32_t)((tid >> 4) * (16 * A.NSG) + 16 * g + (tid & 15));
+            const size_t sb_stride = (size_t)MI::NSUB * A.NSG * (OPB / 16);
+            auto sload = [&](int sb, u32x4 (&v)[NV], float& xsv) {
+                const u32x4* sp = src + (size_t)sb * sb_stride;
+#pragma unroll
+                for (int k = 0; k < NV; k++) v[k] = sp[off[k]];
                 if (TYPE == T_Q4K && tid < 8 * 16)
-                    xsv = A.xs[(size_t)(sb * 8 + (tid >> 4)) * (16 * A.NSG) + 16 * g + (tid & 15)];
+                    xsv = A.xs[(size_t)sb * 8 * (16 * A.NSG) + xoff];
             };
             auto sstore = [&](int buf, const u32x4 (&v)[NV], float xsv) {
 #pragma unroll
