@@ -403,7 +403,8 @@ def cfg4(L, torch, stream, host_w) -> dict:
 
 def cfg5(L, torch, stream, host_w) -> dict:
     """MoE gather, 128 experts, top-8, hidden 2048, expert ffn
-    768, Q4_K; a step is top-k on the device, gate+up, down."""
+    768, Q4_K; a step is top-k on the device, gate+up, down (batch 1: the
+    top-k inside the gate+up launch, kq_moe_gemv_routed_dev)."""
     sh = stream.cuda_stream
     E, H, F, k = 128, 2048, 768, 8
     rbg, rbd = L.kq_row_bytes(12, H), L.kq_row_bytes(12, F)
@@ -435,17 +436,22 @@ def cfg5(L, torch, stream, host_w) -> dict:
                                   [yd.data_ptr()])))
 
         def moe_step(i):
-            _check(L, L.kq_moe_topk_dev(probs.data_ptr(), B, E, k, sel.data_ptr(),
-                                        selw.data_ptr(), sh))
             gu, dn = ops[i % len(ops)]
-            _check(L, L.kq_moe_gemv_dev(ctypes.byref(gu), sel.data_ptr(), B, k, E, sh))
+            if B == 1:      # routed inside the gate+up launch
+                _check(L, L.kq_moe_gemv_routed_dev(ctypes.byref(gu), probs.data_ptr(), k, E,
+                                                   sel.data_ptr(), selw.data_ptr(), sh))
+            else:
+                _check(L, L.kq_moe_topk_dev(probs.data_ptr(), B, E, k, sel.data_ptr(),
+                                            selw.data_ptr(), sh))
+                _check(L, L.kq_moe_gemv_dev(ctypes.byref(gu), sel.data_ptr(), B, k, E, sh))
             _check(L, L.kq_moe_gemv_dev(ctypes.byref(dn), sel.data_ptr(), B, k, E, sh))
         us = _events_us(torch, stream, moe_step, 50)
         distinct = len(set(sel.cpu().numpy().tolist()))
         nb = distinct * (2 * gsl + dsl) + 4 * (B * H + 2 * B * k * F + B * k * F + B * k * H)
         res[f"B{B}"] = {"us_per_layer": round(us, 2), "distinct_experts": distinct,
                         "bytes": nb, "GB/s": round(nb / us / 1e3, 1),
-                        "launches": 3}
+                        "launches": 2 if B == 1 else 3,
+                        "route": "in the gate+up launch" if B == 1 else "kq_moe_topk_dev"}
         if CPU["on"]:
             from oracle import oracle as O
             impl, kind = cpu_impl(12)

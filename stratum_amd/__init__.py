@@ -42,7 +42,7 @@ EXPORTS = (
     "kq_q4k_group", "kq_gemv_dev", "kq_gemv_multix_dev", "kq_gemv_segments_dev",
     "kq_dequant_dev", "kq_row_bytes", "kq_moe_slice_bytes", "kq_moe_bind_slice",
     "kq_moe_pack_open", "kq_moe_pack_which", "kq_moe_topk", "kq_moe_topk_dev",
-    "kq_moe_gemv_dev", "kq_gemv_multix_mfma_dev",
+    "kq_moe_gemv_dev", "kq_gemv_multix_mfma_dev", "kq_moe_gemv_routed_dev",
 )
 
 MAX_SEGMENTS = 8
@@ -204,6 +204,7 @@ def lib() -> ctypes.CDLL:
     L.kq_moe_topk.restype = None
     L.kq_moe_topk_dev.argtypes = [P, I, I, I, P, P, P]
     L.kq_moe_gemv_dev.argtypes = [ctypes.POINTER(KqMoeOp), P, I, I, I, P]
+    L.kq_moe_gemv_routed_dev.argtypes = [ctypes.POINTER(KqMoeOp), P, I, I, P, P, P]
     _LIB = L
     return L
 
@@ -343,3 +344,11 @@ def moe_topk_dev(probs_ptr: int, B: int, E: int, k: int, sel_ptr: int, selw_ptr:
 def moe_gemv_dev(op: KqMoeOp, sel_ptr: int, B: int, k: int, E: int,
                  stream: int | None = None) -> None:
     _check(lib().kq_moe_gemv_dev(ctypes.byref(op), sel_ptr, B, k, E, stream), "kq_moe_gemv_dev")
+
+
+def moe_gemv_routed_dev(op: KqMoeOp, probs_ptr: int, k: int, E: int, sel_ptr: int,
+                        selw_ptr: int, stream: int | None = None) -> None:
+    """One token: top-k of probs inside the launch that runs op (written to
+    sel / selw), then op on the selected experts (kq_moe_gemv_routed_dev)."""
+    _check(lib().kq_moe_gemv_routed_dev(ctypes.byref(op), probs_ptr, k, E, sel_ptr, selw_ptr,
+                                        stream), "kq_moe_gemv_routed_dev")

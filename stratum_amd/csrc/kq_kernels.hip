@@ -846,6 +846,12 @@ struct Seg {
     int start[MAXG];
     long estride;      // MoE gather: bytes per expert,
     int ksel, emax;    // the selection period and the expert count
+    // routed in the launch (nullptr: sel is an input): every workgroup
+    // takes the top-ksel of the emax router weights probs[] itself, and
+    // workgroup 0 writes them to sel_out / selw_out
+    const float* probs;
+    int* sel_out;
+    float* selw_out;
 };
 
 // Issues the scalar loads of a segment's leading fields together and waits
@@ -990,6 +996,66 @@ __device__ __forceinline__ void sweep(const Walk<TYPE, PM>& W, int nch, int u, i
     for (int k = 0; k < DEPTH; k++) C::drain(buf[k]);
 }
 
+// A workgroup barrier for LDS traffic only: waits for this wave's LDS
+// operations (lgkmcnt), not for its global loads (vmcnt), which
+// __syncthreads() would also wait for.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0); vmcnt, expcnt unconstrained
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Top-k of one token's router weights, E <= 1024, computed by the whole
+// workgroup (T lanes) with the rule of kq_moe_topk_rank_kernel: slot r of
+// rsel gets the expert with r eligible experts beating it (a larger weight,
+// or an equal weight and a lower id; weights <= -1 and NaN are not
+// eligible); slots without an expert stay -1.  Lane (p, e) counts the
+// experts of part p (of P) that beat e.  pv holds w[tid] (lanes tid < E64,
+// -1 past E), loaded by the caller ahead of its other loads; where E64 > T
+// the lanes load the rest here.  Scratch: ROUTE_BYTES of LDS.  Only LDS
+// barriers: global loads the caller issued stay in flight.
+constexpr int ROUTE_BYTES = 1024 * 4 + 1024 * 4 + MAXG * 8 + 16;
+__device__ void wg_topk(const float* w, float pv, int E, int k, int T, uint8_t* scratch) {
+    float* wl = reinterpret_cast<float*>(scratch);
+    int* part = reinterpret_cast<int*>(scratch + 4096);
+    int* rsel = reinterpret_cast<int*>(scratch + 8192);
+    float* rselw = reinterpret_cast<float*>(scratch + 8192 + MAXG * 4);
+    const int tid = threadIdx.x, E64 = (E + 63) & ~63;
+    int P = 1;
+    while (2 * P * E64 <= T && (E64 / (2 * P)) % 4 == 0) P *= 2;
+    const int L = E64 / P;
+    if (tid < E64) wl[tid] = pv;
+    if (E64 > T)                          // uniform: its wait covers every load in flight
+        for (int i = tid + T; i < E64; i += T) wl[i] = i < E ? w[i] : -1.0f;
+    if (tid < MAXG) { rsel[tid] = -1; rselw[tid] = -1.0f; }
+    lds_barrier();
+    for (int idx = tid; idx < P * E64; idx += T) {
+        const int e = idx % E64, p = idx / E64;
+        const float v = wl[e];
+        int r = 0;
+        for (int q = p * L; q < (p + 1) * L; q += 4) {
+            const float4 o = *reinterpret_cast<const float4*>(&wl[q]);
+            const float ov[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float x = ov[j];
+                const int beat = (x > v) | ((x == v) & (q + j < e));
+                r += (x > -1.0f) & beat;
+            }
+        }
+        part[idx] = r;
+    }
+    lds_barrier();
+    for (int e = tid; e < E; e += T) {
+        int rank = 0;
+        for (int i = 0; i < P; i++) rank += part[i * E64 + e];
+        const float v = wl[e];
+        if (v > -1.0f && rank < k) { rsel[rank] = e; rselw[rank] = v; }
+    }
+    lds_barrier();
+}
+
 template <int TYPE, int DEPTH, int PM>
 __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st, uint8_t* smem,
                             bool last_seg) {
@@ -1014,6 +1080,43 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
     const float** atab = reinterpret_cast<const float**>(smem + A.scr_off + SCR_TABS + 16 * MAXG);
     const int ngx = (PM != PM_ONE && S.x_stride) ? S.nparts : 1;
 
+    // x staging decision: SC types stage x scaled, Q6_K unscaled; a Q6_K
+    // segment can read a scaled x, an SC type restages an unscaled one
+    // unless the window already failed for it.
+    constexpr bool SCTYPE = TYPE != T_Q6K;
+    const bool same_x = st.x == S.x && st.K == K && st.layout == (int)TI::LINEAR && st.ngx == ngx;
+    const bool restage = !same_x || (SCTYPE && st.k == 0 && !st.bad);
+    constexpr int G4 = XGroup<TYPE>::G4;
+    const XStage<TYPE> xg = {S.x, S.x_stride, K / (4 * G4), ngx * (K / (4 * G4)), NC};
+    // routed in the launch: the router weights go out first, so the routing
+    // can wait for them while the x loads behind them are still in flight
+    const bool route = PM == PM_SEL && S.probs;   // uniform
+    float pv = -1.0f;
+    if (PM == PM_SEL && route && tid < S.emax) pv = S.probs[tid];
+    f32x4 xv[G4];
+    // first round of x, ahead of the weights (and of the routing, which
+    // does not depend on it)
+    if (restage) xg.load(tid, xv);
+    // A second round (x longer than one round of the workgroup, e.g. Q6_K
+    // at K = 17408 with 1024 lanes) is loaded together with the first, so
+    // its latency is not paid after the first round's stores.  Types with
+    // 16-float groups only: their registers allow it (Q4_K needs a second
+    // round only beyond K = 32768).
+    constexpr bool PRE2 = G4 == 4;
+    const bool two = PRE2 && restage && xg.total > T;   // uniform
+    f32x4 xv2[PRE2 ? G4 : 1];
+    if (PRE2 && two) xg.load(tid + T, xv2);
+
+    const int* rsel = nullptr;
+    if (PM == PM_SEL && route) {
+        uint8_t* scr = smem + A.terms_off;    // the terms are written only later
+        wg_topk(S.probs, pv, S.emax, S.ksel, T, scr);
+        rsel = reinterpret_cast<const int*>(scr + 8192);
+        if (b == 0 && tid < S.ksel) {
+            S.sel_out[tid] = rsel[tid];
+            S.selw_out[tid] = reinterpret_cast<const float*>(scr + 8192 + MAXG * 4)[tid];
+        }
+    }
     if (PM >= PM_EQUAL) {
         // each wave writes the part tables itself (identical values), so its
         // own reads need no barrier
@@ -1028,7 +1131,8 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
         }
         if (lane < S.nparts) {
             if (PM == PM_SEL) {                   // the expert chosen on the device
-                const int e = min(max(S.sel[lane % S.ksel], 0), S.emax - 1);
+                const int se = rsel ? rsel[lane % S.ksel] : S.sel[lane % S.ksel];
+                const int e = min(max(se, 0), S.emax - 1);
                 wv += (size_t)e * S.estride;
             }
             wtab[lane] = wv;
@@ -1038,25 +1142,6 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
     }
     const Walk<TYPE, PM> W = {&S, wtab, NC, b, G, lane, last, rbytes};
 
-    // x staging decision: SC types stage x scaled, Q6_K unscaled; a Q6_K
-    // segment can read a scaled x, an SC type restages an unscaled one
-    // unless the window already failed for it.
-    constexpr bool SCTYPE = TYPE != T_Q6K;
-    const bool same_x = st.x == S.x && st.K == K && st.layout == (int)TI::LINEAR && st.ngx == ngx;
-    const bool restage = !same_x || (SCTYPE && st.k == 0 && !st.bad);
-    constexpr int G4 = XGroup<TYPE>::G4;
-    const XStage<TYPE> xg = {S.x, S.x_stride, K / (4 * G4), ngx * (K / (4 * G4)), NC};
-    f32x4 xv[G4];
-    if (restage) xg.load(tid, xv);            // first round of x, ahead of the weights
-    // A second round (x longer than one round of the workgroup, e.g. Q6_K
-    // at K = 17408 with 1024 lanes) is loaded together with the first, so
-    // its latency is not paid after the first round's stores.  Types with
-    // 16-float groups only: their registers allow it (Q4_K needs a second
-    // round only beyond K = 32768).
-    constexpr bool PRE2 = G4 == 4;
-    const bool two = PRE2 && restage && xg.total > T;   // uniform
-    f32x4 xv2[PRE2 ? G4 : 1];
-    if (PRE2 && two) xg.load(tid + T, xv2);
 
     // first DEPTH batches: static (wave w takes chunks 64w .., then
     // 64(W + w) ..); their latency overlaps the staging
@@ -2288,6 +2373,10 @@ long kqk_segs_lds(const kqk_seg* segs, int nseg, int grid, int* xs_off, int* ter
         xsb = xsb > ngx * NC * xpc * 4 ? xsb : ngx * NC * xpc * 4;
         const long R = (N + grid - 1) / grid;
         tb = tb > R * NC * 8 ? tb : R * NC * 8;
+        if (g.probs) {                       // routing scratch (wg_topk) in the terms region
+            if (!g.sel_out || g.emax < 1 || g.emax > 1024 || g.ksel < 1 || g.ksel > MAXG) return -1;
+            tb = tb > ROUTE_BYTES ? tb : ROUTE_BYTES;
+        }
     }
     xsb = (xsb + 15) & ~15L;
     *xs_off = (int)xl;
@@ -2360,6 +2449,9 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
         }
         d.x = h.x;
         d.sel = h.sel;
+        d.probs = h.probs;
+        d.sel_out = h.sel_out;
+        d.selw_out = h.selw_out;
         d.estride = h.estride;
         d.ksel = h.ksel > 0 ? h.ksel : 1;
         d.emax = h.emax > 0 ? h.emax : 1;

@@ -27,6 +27,9 @@ typedef struct {
     const int* sel;          /* MoE gather: part p uses expert sel[p % ksel] */
     long estride;            /* bytes per expert */
     int ksel, emax;
+    const float* probs;      /* routed in the launch: top-ksel of probs[0..emax), */
+    int* sel_out;            /* written by workgroup 0 to sel_out / selw_out */
+    float* selw_out;
 } kqk_seg;
 #define KQK_LIST_MAX 4   /* parts of unequal sizes one launcher segment takes */
 long kqk_segs_lds(const kqk_seg* segs, int nseg, int grid, int* xs_off, int* terms_off,

@@ -676,50 +676,76 @@ int kq_moe_topk_dev(const float* probs, int B, int E, int k, int* sel, float* se
     return 0;
 }
 
-int kq_moe_gemv_dev(const kq_moe_op* op, const int* sel, int B, int k, int E, kq_stream stream) {
-    if (!op || !sel) return kq_fail("kq_moe_gemv_dev: NULL argument");
+/* One token: the single-stream kernel, part r of tensor t on expert sel[r]
+ * read on the device, or (probs != NULL) routed in the launch itself: every
+ * workgroup takes the top-k of probs and workgroup 0 writes it to sel and
+ * selw. */
+static int moe_one_token(const kq_moe_op* op, const int* sel, int k, int E, const float* probs,
+                         float* selw, hipStream_t st) {
+    const int nt = op->ntensors;
+    kqk_seg h[2];
+    memset(h, 0, sizeof h);
+    /* gate and up on one x: one row space of 2k parts (part p uses
+     * sel[p % k]); else one segment per tensor */
+    const int one = nt == 2 && op->x_div == k && 2 * k <= KQ_MAX_GROUPS;
+    const int nh = one ? 1 : nt;
+    for (int t = 0; t < nt; t++) {
+        kqk_seg* g = &h[one ? 0 : t];
+        const int p0 = one ? t * k : 0;
+        for (int r = 0; r < k; r++) {
+            g->w[p0 + r] = op->w[t];
+            g->y[p0 + r] = op->y[t] + (size_t)r * op->n_out;
+            g->rows[p0 + r] = op->n_out;
+        }
+        g->type = op->type; g->K = op->k_in; g->nparts = p0 + k;
+        g->x = op->x;
+        g->x_stride = op->x_div == 1 && k > 1 ? op->k_in : 0;
+        g->sel = sel;
+        g->estride = (long)op->expert_stride;
+        g->ksel = k;
+        g->emax = E;
+        if (probs) {
+            g->probs = probs;
+            g->sel_out = (int*)sel;
+            g->selw_out = selw;
+        }
+    }
+    return launch_segs(h, nh, st);
+}
+
+static int moe_check_op(const kq_moe_op* op, int k, int E, const char* who) {
     if (check_shape(op->type, op->n_out, op->k_in) || kq_ready()) return -1;
     const int nt = op->ntensors;
-    if (nt < 1 || nt > 2) return kq_fail("kq_moe_gemv_dev: ntensors=%d", nt);
+    if (nt < 1 || nt > 2) return kq_fail("%s: ntensors=%d", who, nt);
+    if (op->x_div != 1 && op->x_div != k) return kq_fail("%s: x_div must be 1 or k", who);
+    if (!op->x || ((uintptr_t)op->x & 15)) return kq_fail("%s: x NULL or unaligned", who);
+    const int64_t rb = kq_row_bytes(op->type, op->k_in);
+    if (op->expert_stride < rb * op->n_out)
+        return kq_fail("%s: expert_stride below the slice size", who);
+    for (int t = 0; t < nt; t++)
+        if (!op->w[t] || !op->y[t]) return kq_fail("%s: NULL w or y", who);
+    (void)E;
+    return 0;
+}
+
+int kq_moe_gemv_routed_dev(const kq_moe_op* op, const float* probs, int k, int E, int* sel,
+                           float* selw, kq_stream stream) {
+    if (!op || !probs || !sel || !selw) return kq_fail("kq_moe_gemv_routed_dev: NULL argument");
+    if (k < 1 || k > KQ_MAX_GROUPS || E < 1 || E > 1024)
+        return kq_fail("kq_moe_gemv_routed_dev: k=%d E=%d (E <= 1024)", k, E);
+    if (moe_check_op(op, k, E, "kq_moe_gemv_routed_dev")) return -1;
+    return moe_one_token(op, sel, k, E, probs, selw, pick(stream));
+}
+
+int kq_moe_gemv_dev(const kq_moe_op* op, const int* sel, int B, int k, int E, kq_stream stream) {
+    if (!op || !sel) return kq_fail("kq_moe_gemv_dev: NULL argument");
     if (B < 1 || B > KQ_MOE_MAX_TOKENS || k < 1 || k > KQ_MAX_GROUPS || E < 1 ||
         E > KQ_MOE_MAX_EXPERTS)
         return kq_fail("kq_moe_gemv_dev: B=%d k=%d E=%d", B, k, E);
-    if (op->x_div != 1 && op->x_div != k)
-        return kq_fail("kq_moe_gemv_dev: x_div must be 1 or k");
-    if (!op->x || ((uintptr_t)op->x & 15)) return kq_fail("kq_moe_gemv_dev: x NULL or unaligned");
-    const int64_t rb = kq_row_bytes(op->type, op->k_in);
-    if (op->expert_stride < rb * op->n_out)
-        return kq_fail("kq_moe_gemv_dev: expert_stride below the slice size");
-    for (int t = 0; t < nt; t++)
-        if (!op->w[t] || !op->y[t]) return kq_fail("kq_moe_gemv_dev: NULL w or y");
+    if (moe_check_op(op, k, E, "kq_moe_gemv_dev")) return -1;
+    const int nt = op->ntensors;
     hipStream_t st = pick(stream);
-    if (B == 1) {
-        /* one token: the single-stream kernel, part r of tensor t on expert
-         * sel[r] (read on the device) */
-        kqk_seg h[2];
-        memset(h, 0, sizeof h);
-        /* gate and up on one x: one row space of 2k parts (part p uses
-         * sel[p % k]); else one segment per tensor */
-        const int one = nt == 2 && op->x_div == k && 2 * k <= KQ_MAX_GROUPS;
-        const int nh = one ? 1 : nt;
-        for (int t = 0; t < nt; t++) {
-            kqk_seg* g = &h[one ? 0 : t];
-            const int p0 = one ? t * k : 0;
-            for (int r = 0; r < k; r++) {
-                g->w[p0 + r] = op->w[t];
-                g->y[p0 + r] = op->y[t] + (size_t)r * op->n_out;
-                g->rows[p0 + r] = op->n_out;
-            }
-            g->type = op->type; g->K = op->k_in; g->nparts = p0 + k;
-            g->x = op->x;
-            g->x_stride = op->x_div == 1 && k > 1 ? op->k_in : 0;
-            g->sel = sel;
-            g->estride = (long)op->expert_stride;
-            g->ksel = k;
-            g->emax = E;
-        }
-        return launch_segs(h, nh, st);
-    }
+    if (B == 1) return moe_one_token(op, sel, k, E, NULL, NULL, st);
     /* several tokens: expert groups built on the device, then one weight
      * pass per selected expert for all of its tokens.  The launch is
      * planned for uniform routing (mx_plan): the planner picks the run

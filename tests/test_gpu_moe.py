@@ -169,6 +169,57 @@ def test_moe_one_token_gate_up_and_down(port, qtype):
     check_members(port, qtype, [down], sel, act, 1, got, H, F)
 
 
+def run_routed(qtype, wts, probs, x, x_div, k, N_out, K_in):
+    """kq_moe_gemv_routed_dev: top-k of probs inside the launch; returns the
+    outputs and the sel / selw it wrote."""
+    dws = [dev(w) for w in wts]
+    stride = N_out * K.lib().kq_row_bytes(qtype, K_in)
+    dx, dp = dev(x), dev(probs)
+    ys = [torch.full((k * N_out,), float("nan"), dtype=torch.float32, device="cuda")
+          for _ in wts]
+    sel = torch.full((k,), -7, dtype=torch.int32, device="cuda")
+    selw = torch.full((k,), 7.0, dtype=torch.float32, device="cuda")
+    op = K.moe_op(qtype, N_out, K_in, [d.data_ptr() for d in dws], stride, dx.data_ptr(), x_div,
+                  [y.data_ptr() for y in ys])
+    K.moe_gemv_routed_dev(op, dp.data_ptr(), k, probs.size, sel.data_ptr(), selw.data_ptr(),
+                          stream())
+    torch.cuda.synchronize()
+    return ([y.cpu().numpy().reshape(k, N_out) for y in ys], sel.cpu().numpy(),
+            selw.cpu().numpy())
+
+
+@pytest.mark.parametrize("qtype", [12, 14])
+@pytest.mark.parametrize("E,k,case", [(32, 8, "random"), (128, 8, "random"), (1000, 4, "random"),
+                                      (64, 8, "ties"), (40, 16, "few-eligible")])
+def test_moe_routed_one_token(port, qtype, E, k, case):
+    """Routing inside the gate+up launch: sel / selw equal the device top-k
+    (and the oracle's moe_topk), and every output equals the unrouted
+    call's bit for bit; the down call then runs on the written sel."""
+    H, F = 512, 256
+    gate, up = experts(qtype, E, F, H, 11), experts(qtype, E, F, H, 12)
+    r = np.random.default_rng(E + k)
+    if case == "random":
+        probs = softmax_rows(r.standard_normal((1, E)).astype(np.float32))[0]
+    elif case == "ties":
+        probs = (r.integers(0, 3, E) * 0.25).astype(np.float32)
+    else:                                   # fewer eligible experts than k
+        probs = np.full(E, -2.0, np.float32)
+        probs[[3, 17, 30]] = [0.5, 0.25, 0.5]
+    x = synth.gaussian(r, H)
+    got, sel, selw = run_routed(qtype, [gate, up], probs, x, k, k, F, H)
+    ws, ww = port.topk(probs, k)
+    assert list(sel) == ws
+    assert same_values(selw, ww)
+    dsel, dselw = gpu_topk(probs[None, :], k)
+    assert list(dsel[0]) == list(sel) and same_values(dselw[0], selw)
+    want = run_moe(qtype, [gate, up], sel, x, k, 1, k, E, F, H)
+    for t in range(2):
+        for m in range(k):
+            if sel[m] >= 0:
+                assert same_values(got[t][m], want[t][m]), (t, m)
+    check_members(port, qtype, [gate, up], sel, x, k, got, F, H)
+
+
 @pytest.mark.parametrize("qtype", [12, 14, 10])
 @pytest.mark.parametrize("B,n_exp", [(16, 32), (16, 128), (3, 8), (64, 16)])
 def test_moe_batch_grouped(port, qtype, B, n_exp):
