@@ -920,7 +920,7 @@ __device__ __forceinline__ uint32_t part_of(const Seg& S, uint32_t r, uint32_t& 
     uint32_t g;
     if (PM >= PM_EQUAL) {
         g = div_magic(r, S.pn_m, S.pn_l);
-        rg = r - g * (uint32_t)S.pn;
+        rg = r - __umul24(g, (uint32_t)S.pn);   // g <= 16, rows < 2^24
         return g;
     }
     g = 0;
@@ -940,26 +940,45 @@ __device__ __forceinline__ const uint8_t* part_w(const Seg& S, uint32_t g,
 }
 
 // Where chunk f = base + lane of a workgroup's range lives: its staged-x
-// chunk cx and weight address (f clamped to the last chunk).  Branch-free,
+// chunk cx and weight address (past the last chunk, the row is clamped to
+// the last row: an in-bounds load whose term is never stored).  Branch-free,
 // so the loads that follow are unconditional and the compiler can count the
 // outstanding ones exactly.
+//
+// base is the same in every lane of a wave, so its row and column are
+// scalar work; a lane adds its fixed offset (lane / NC rows, lane % NC
+// columns, set once per segment) with one carry.  Rows, row bytes and
+// chunk counts stay below 2^24 (the host rejects larger segments), so every
+// product is a full-rate 24-bit multiply rather than a 32-bit one.
 template <int TYPE, int PM>
 struct Walk {
     const Seg* S;
     const uint8_t* const* wtab;
-    int NC, b, G, lane, last;
-    size_t rbytes;
+    int NC, b, G, lane;
+    uint32_t rbytes;
+    uint32_t lq, lr;      // lane / NC, lane % NC
+    uint32_t rho_max;     // the workgroup's last row (R - 1)
 
     __device__ __forceinline__ wptr locate(int base, int& cx) const {
-        const uint32_t f = (uint32_t)min(base + lane, last);
-        const uint32_t rho = div_magic(f, S->nc_m, S->nc_l);
-        const uint32_t c = f - rho * (uint32_t)NC;
-        const uint32_t r = (uint32_t)b + (uint32_t)G * rho;
+        const uint32_t ub = (uint32_t)__builtin_amdgcn_readfirstlane(base);
+        const uint32_t rho0 = div_magic(ub, S->nc_m, S->nc_l);
+        const uint32_t c0 = ub - rho0 * (uint32_t)NC;
+        uint32_t c = c0 + lr, rho = rho0 + lq;
+        if (c >= (uint32_t)NC) {
+            c -= (uint32_t)NC;
+            rho += 1u;
+        }
+        rho = min(rho, rho_max);
+        __builtin_assume(rho < (1u << 24));
+        const uint32_t r = (uint32_t)b + __umul24((uint32_t)G, rho);
         uint32_t rg;
         const uint32_t g = part_of<PM>(*S, r, rg);
-        cx = (PM != PM_ONE && S->x_stride ? (int)g * NC : 0) + (int)c;
-        return to_global(part_w<PM>(*S, g, wtab)) + (size_t)rg * rbytes +
-               (size_t)(c >> 2) * TypeInfo<TYPE>::BB;
+        __builtin_assume(rg < (1u << 24));
+        __builtin_assume(rbytes < (1u << 24));
+        __builtin_assume(c < (1u << 24));
+        cx = (PM != PM_ONE && S->x_stride ? (int)__umul24(g, (uint32_t)NC) : 0) + (int)c;
+        return to_global(part_w<PM>(*S, g, wtab)) + (uint64_t)rg * rbytes +
+               __umul24(c >> 2, (uint32_t)TypeInfo<TYPE>::BB);
     }
 };
 
@@ -980,6 +999,7 @@ __device__ __forceinline__ void sweep(const Walk<TYPE, PM>& W, int nch, int u, i
             if (W.lane == 0) nb = atomicAdd(next, 64);
             if (base[k] < nch) {                 // uniform over the wave
                 const int fi = base[k] + W.lane;
+                __builtin_assume(cx[k] >= 0 && cx[k] < (1 << 24));   // 24-bit multiply
                 const double t = C::template term<SC>(buf[k], u, xl + cx[k] * XPAD, xs, cx[k],
                                                       f, f6);
                 if (fi < nch) terms[fi] = t;
@@ -1067,9 +1087,8 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
     const int R = N > b ? (N - b + G - 1) / G : 0;
     if (R == 0) return;                       // uniform over the workgroup
     const int nch = R * NC;
-    const int last = nch - 1;
     const int u = tid & 3;
-    const size_t rbytes = (size_t)(K >> 8) * TI::BB;
+    const uint32_t rbytes = (uint32_t)(K >> 8) * TI::BB;
     float4* xl = reinterpret_cast<float4*>(smem);
     float* xs = reinterpret_cast<float*>(smem + A.xs_off);
     double* terms = reinterpret_cast<double*>(smem + A.terms_off);
@@ -1140,7 +1159,9 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
             atab[lane] = av;
         }
     }
-    const Walk<TYPE, PM> W = {&S, wtab, NC, b, G, lane, last, rbytes};
+    const uint32_t lq = (uint32_t)lane / (uint32_t)NC;
+    const Walk<TYPE, PM> W = {&S, wtab, NC, b, G, lane, rbytes,
+                              lq, (uint32_t)lane - lq * (uint32_t)NC, (uint32_t)(R - 1)};
 
 
     // first DEPTH batches: static (wave w takes chunks 64w .., then
@@ -2455,6 +2476,8 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
         d.estride = h.estride;
         d.ksel = h.ksel > 0 ? h.ksel : 1;
         d.emax = h.emax > 0 ? h.emax : 1;
+        if (start >= (1 << 24) || (long)(h.K >> 8) * 210 >= (1L << 24))   // 24-bit addressing
+            return (int)hipErrorInvalidValue;
         d.type = h.type; d.K = h.K; d.N = start; d.nparts = h.nparts;
         d.x_stride = h.nparts > 1 ? h.x_stride : 0;
         d.pn = equal ? h.rows[0] : 0;

@@ -230,6 +230,13 @@ static int plan_depth(int threads) {
 
 static int launch_segs(const kqk_seg* segs, int nseg, hipStream_t st) {
     const int grid = plan_grid(), threads = plan_threads(segs, nseg, grid);
+    for (int i = 0; i < nseg; i++) {   /* the kernel's row arithmetic is 24-bit */
+        long n = 0;
+        for (int p = 0; p < segs[i].nparts; p++) n += segs[i].rows[p];
+        if (n >= (1L << 24))
+            return kq_fail("segment %d has %ld rows (at most 2^24 - 1 per launch): split the rows",
+                           i, n);
+    }
     int xs_off = 0, terms_off = 0, scr_off = 0;
     long lds = kqk_segs_lds(segs, nseg, grid, &xs_off, &terms_off, &scr_off);
     if (lds < 0) return kq_fail("invalid segment list");

@@ -200,6 +200,25 @@ def test_host_abi_dispatch_multix_group(port):
 
 
 # ------------------------------------------------------- batched segments
+def test_segments_row_limit():
+    """A segment of 2^24 rows or more is refused with a message before any
+    launch (the kernel's row arithmetic is 24-bit); one row fewer is not
+    refused for that reason."""
+    import torch
+    w = torch.zeros(4096, dtype=torch.uint8, device="cuda")
+    x = torch.zeros(256, device="cuda")
+    y = torch.zeros(16, device="cuda")
+    L = K.lib()
+    seg = K.segment(12, 256, 1 << 24, [w.data_ptr()], x.data_ptr(), y.data_ptr())
+    assert L.kq_gemv_segments_dev((K.KqSegment * 1)(seg), 1, None) == -1
+    assert "2^24" in L.kq_last_error().decode()
+    seg = K.segment(12, 256, 16, [w.data_ptr()], x.data_ptr(), y.data_ptr())
+    sh = torch.cuda.current_stream().cuda_stream
+    assert L.kq_gemv_segments_dev((K.KqSegment * 1)(seg), 1, sh) == 0
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(y).item() == 0
+
+
 def test_segments_layer_set_matches_single_launches(port):
     """A layer's matvecs in ONE launch (kq_gemv_segments_dev): each output is
     bit-identical to its own kq_gemv_dev launch, and matches the oracle."""
