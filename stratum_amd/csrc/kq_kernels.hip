@@ -819,6 +819,7 @@ template <> struct Chunk<T_NIB> {
 // groups (QKV, gate+up).
 constexpr int MAXSEG = 8;
 constexpr int MAXG = 16;
+constexpr int LIST_MAX = 4;   // parts of a same-input group of any sizes
 
 // A segment: N rows of one type and row length K, made of nparts parts.
 // Part p holds rows [start[p], start[p+1]) at weight base w[p], writes
@@ -840,12 +841,14 @@ struct Seg {
     int pn_l;          // its shift
     uint32_t nc_m;     // the same for division by NC = K / 64
     int nc_l;
+    // the fields the first weight address needs sit ahead of the pointer
+    // tables, in the kernel's first round of scalar loads
+    int start[LIST_MAX];
+    long estride;      // MoE gather: bytes per expert,
+    int ksel, emax;    // the selection period and the expert count
     const uint8_t* w[MAXG];
     float* y[MAXG];
     const float* add[MAXG];
-    int start[MAXG];
-    long estride;      // MoE gather: bytes per expert,
-    int ksel, emax;    // the selection period and the expert count
     // routed in the launch (nullptr: sel is an input): every workgroup
     // takes the top-ksel of the emax router weights probs[] itself, and
     // workgroup 0 writes them to sel_out / selw_out
@@ -860,7 +863,8 @@ struct Seg {
 __device__ __forceinline__ void prefetch_seg(const Seg& S) {
     asm volatile("" ::"s"(S.x), "s"(S.sel), "s"(S.type), "s"(S.K), "s"(S.N), "s"(S.nparts),
                  "s"(S.x_stride), "s"(S.pn), "s"(S.pn_m), "s"(S.pn_l), "s"(S.nc_m), "s"(S.nc_l),
-                 "s"(S.w[0]), "s"(S.y[0]), "s"(S.add[0]));
+                 "s"(S.start[1]), "s"(S.start[2]), "s"(S.start[3]), "s"(S.w[0]), "s"(S.y[0]),
+                 "s"(S.add[0]));
 }
 
 struct SegsArg {
@@ -903,7 +907,6 @@ constexpr int SCR_BYTES = SCR_TABS + 3 * 8 * MAXG;
 // PM_SEL: PM_EQUAL whose part bases are moved by a device-side expert
 // selection (the MoE gather kernels only).
 constexpr int PM_ONE = 0, PM_LIST = 1, PM_EQUAL = 2, PM_SEL = 3;
-constexpr int LIST_MAX = 4;
 
 template <typename V>
 __device__ __forceinline__ V pick4(uint32_t g, V v0, V v1, V v2, V v3) {
@@ -1112,6 +1115,18 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
     const bool route = PM == PM_SEL && S.probs;   // uniform
     float pv = -1.0f;
     if (PM == PM_SEL && route && tid < S.emax) pv = S.probs[tid];
+    // equal parts: lane g reads part g's pointers itself (vector loads from
+    // the argument block, issued at once and ahead of x, rather than a
+    // second round of scalar loads of all 48 pointers)
+    const int gl = lane & (MAXG - 1);
+    const uint8_t* wv = nullptr;
+    float* yv = nullptr;
+    const float* av = nullptr;
+    if (PM >= PM_EQUAL) {
+        wv = S.w[gl];
+        yv = S.y[gl];
+        av = S.add[gl];
+    }
     f32x4 xv[G4];
     // first round of x, ahead of the weights (and of the routing, which
     // does not depend on it)
@@ -1139,15 +1154,6 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
     if (PM >= PM_EQUAL) {
         // each wave writes the part tables itself (identical values), so its
         // own reads need no barrier
-        const uint8_t* wv = S.w[0];
-        float* yv = S.y[0];
-        const float* av = S.add[0];
-#pragma unroll
-        for (int g = 1; g < MAXG; g++) {
-            wv = lane == g ? S.w[g] : wv;
-            yv = lane == g ? S.y[g] : yv;
-            av = lane == g ? S.add[g] : av;
-        }
         if (lane < S.nparts) {
             if (PM == PM_SEL) {                   // the expert chosen on the device
                 const int se = rsel ? rsel[lane % S.ksel] : S.sel[lane % S.ksel];
@@ -2462,7 +2468,7 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
             d.w[g] = static_cast<const uint8_t*>(h.w[q]);
             d.y[g] = h.y[q];
             d.add[g] = h.add[q];
-            d.start[g] = g < h.nparts ? start : 0;
+            if (g < LIST_MAX) d.start[g] = g < h.nparts ? start : 0;
             if (g < h.nparts) {
                 start += h.rows[g];
                 equal = equal && h.rows[g] == h.rows[0];
