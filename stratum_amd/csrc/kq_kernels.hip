@@ -872,6 +872,8 @@ struct SegsArg {
     int nseg;
     int threads;       // blockDim.x and gridDim.x, passed as plain arguments:
     int grid;          // the built-ins are read through a dependent load chain
+    uint32_t grid_m;   // magic multiplier and shift for division by grid
+    int grid_l;
     int xs_off;        // LDS byte offsets of the xs, terms and scratch regions
     int terms_off;
     int scr_off;
@@ -1087,7 +1089,7 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
     const int tid = threadIdx.x, T = A.threads, lane = tid & 63, wave = tid >> 6;
     const int b = blockIdx.x, G = A.grid;
     const int K = S.K, NC = K >> 6, N = S.N;
-    const int R = N > b ? (N - b + G - 1) / G : 0;
+    const int R = N > b ? (int)div_magic((uint32_t)(N - b + G - 1), A.grid_m, A.grid_l) : 0;
     if (R == 0) return;                       // uniform over the workgroup
     const int nch = R * NC;
     const int u = tid & 3;
@@ -1165,7 +1167,7 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
             atab[lane] = av;
         }
     }
-    const uint32_t lq = (uint32_t)lane / (uint32_t)NC;
+    const uint32_t lq = div_magic((uint32_t)lane, S.nc_m, S.nc_l);
     const Walk<TYPE, PM> W = {&S, wtab, NC, b, G, lane, rbytes,
                               lq, (uint32_t)lane - lq * (uint32_t)NC, (uint32_t)(R - 1)};
 
@@ -2457,6 +2459,7 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
     A.scr_off = scr_off;
     A.threads = threads;
     A.grid = grid;
+    magic_for((uint32_t)grid, A.grid_m, A.grid_l);
     int set = 0;
     for (int i = 0; i < nseg; i++) {
         Seg& d = A.s[i];
