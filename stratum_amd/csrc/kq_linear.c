@@ -199,11 +199,25 @@ static const void* tensor_dev(const kq_tensor* w, int N, int K) {
  * idle lanes on small tensors (KQ_WG_THREADS overrides: 256, 512 or
  * 1024).  Each wave keeps one batch of loads in flight, two when the
  * workgroup has fewer than 16 waves to hide the memory latency with
- * (KQ_DEPTH overrides: 1 or 2). */
+ * (KQ_DEPTH overrides: 1 or 2).  A share of 2048-4095 chunks (a 512-lane
+ * workgroup, e.g. a 27B Q/K/V group) is instead split over two workgroups
+ * per CU when their LDS fits: twice the waves per CU, and two prologues
+ * and tails that overlap (measured 9.7 -> 8.7 us for Q/K/V). */
 static int plan_grid(void) {
     const char* e = getenv("KQ_GRID");
     int g = e && atoi(e) > 0 ? atoi(e) : g_kq.n_cu;
     return g;
+}
+
+static long max_share(const kqk_seg* segs, int nseg, int grid) {
+    long chunks = 0;
+    for (int i = 0; i < nseg; i++) {
+        long n = 0;
+        for (int p = 0; p < segs[i].nparts; p++) n += segs[i].rows[p];
+        const long c = ((n + grid - 1) / grid) * (segs[i].K / 64);
+        if (c > chunks) chunks = c;
+    }
+    return chunks;
 }
 
 static int plan_threads(const kqk_seg* segs, int nseg, int grid) {
@@ -212,13 +226,7 @@ static int plan_threads(const kqk_seg* segs, int nseg, int grid) {
         const int t = atoi(e);
         if (t == 256 || t == 512 || t == 1024) return t;
     }
-    long chunks = 0;
-    for (int i = 0; i < nseg; i++) {
-        long n = 0;
-        for (int p = 0; p < segs[i].nparts; p++) n += segs[i].rows[p];
-        const long c = ((n + grid - 1) / grid) * (segs[i].K / 64);
-        if (c > chunks) chunks = c;
-    }
+    const long chunks = max_share(segs, nseg, grid);
     return chunks >= 4096 ? 1024 : chunks >= 1024 ? 512 : 256;
 }
 
@@ -229,7 +237,7 @@ static int plan_depth(int threads) {
 }
 
 static int launch_segs(const kqk_seg* segs, int nseg, hipStream_t st) {
-    const int grid = plan_grid(), threads = plan_threads(segs, nseg, grid);
+    int grid = plan_grid(), threads = plan_threads(segs, nseg, grid), depth = plan_depth(threads);
     for (int i = 0; i < nseg; i++) {   /* the kernel's row arithmetic is 24-bit */
         long n = 0;
         for (int p = 0; p < segs[i].nparts; p++) n += segs[i].rows[p];
@@ -237,14 +245,22 @@ static int launch_segs(const kqk_seg* segs, int nseg, hipStream_t st) {
             return kq_fail("segment %d has %ld rows (at most 2^24 - 1 per launch): split the rows",
                            i, n);
     }
+    if (!getenv("KQ_GRID") && !getenv("KQ_WG_THREADS") && !getenv("KQ_DEPTH") &&
+        max_share(segs, nseg, grid) >= 2048 && threads == 512) {
+        int a = 0, b = 0, c = 0;
+        const long lds2 = kqk_segs_lds(segs, nseg, 2 * grid, &a, &b, &c);
+        if (lds2 > 0 && 2 * lds2 <= g_kq.lds_max) {
+            grid *= 2;
+            depth = 1;
+        }
+    }
     int xs_off = 0, terms_off = 0, scr_off = 0;
     long lds = kqk_segs_lds(segs, nseg, grid, &xs_off, &terms_off, &scr_off);
     if (lds < 0) return kq_fail("invalid segment list");
     if (lds > g_kq.lds_max)
         return kq_fail("segments need %ld bytes of LDS (max %d): split the rows", lds,
                        g_kq.lds_max);
-    int e = kqk_launch_segs(segs, nseg, grid, threads, plan_depth(threads), lds, xs_off, terms_off,
-                            scr_off, st);
+    int e = kqk_launch_segs(segs, nseg, grid, threads, depth, lds, xs_off, terms_off, scr_off, st);
     if (e) return kq_fail("gemv launch: %s", hipGetErrorString((hipError_t)e));
     return 0;
 }
