@@ -1376,6 +1376,15 @@ struct MxArg {
     int TC;                   // chunks per x tile; >= K/64: x staged whole
     int sums_bytes;           // LDS bytes of the sums of mch members
     int xt_bytes;             // LDS bytes of one x buffer
+    // MoE batch grouped in the launch (sel != nullptr): every workgroup
+    // builds the expert runs of the selection itself (MoeRuns), in LDS at
+    // byte offset grp_off, instead of reading groups made by a separate
+    // launch.  Group g = t * nd + run, as kq_moe_group_kernel numbers them.
+    const int* sel;
+    int nm, E, nt, x_div, grp_off;
+    const uint8_t* wt[2];
+    float* yt[2];
+    long estride;
 };
 
 // LDS slot of the float4 at tile-relative x position pos (a multiple of 4;
@@ -1511,6 +1520,69 @@ __device__ __forceinline__ void mx_sweep(const MxArg& A, const MxTasks& tk, wptr
     C::drain(nxt);
 }
 
+// The expert runs of a MoE selection, built in LDS by one workgroup: the
+// same runs and member order as kq_moe_group_kernel writes to memory.
+//  cnt[e]  members of expert e;  gid[e]  its first run (exclusive scan of
+//  ceil(cnt / mch));  ms[m]  member m's expert (-1: none);  pl[m]  its place
+//  among its expert's members (increasing m);  rexp[run]  the run's expert.
+// Returns nd, the number of runs.  Every thread of the workgroup calls it.
+struct MoeRuns {
+    int* cnt;
+    int* gid;
+    int* ms;
+    int* pl;
+    int* rexp;
+
+    __device__ int build(const MxArg& A, int* wsum) {
+        const int tid = threadIdx.x, T = A.threads, lane = tid & 63, wave = tid >> 6;
+        const int nm4 = (A.nm + 3) >> 2;
+        for (int e = tid; e < A.E; e += T) cnt[e] = 0;
+        __syncthreads();
+        for (int m = tid; m < 4 * nm4; m += T) {
+            const int e = m < A.nm ? A.sel[m] : -1;
+            const int ok = e >= 0 && e < A.E;
+            ms[m] = ok ? e : -1;
+            if (ok) atomicAdd(&cnt[e], 1);
+        }
+        __syncthreads();
+        const int run = (A.E + T - 1) / T, e0 = tid * run, e1 = min(A.E, e0 + run);
+        int local = 0;
+        for (int e = e0; e < e1; e++) local += (cnt[e] + A.mch - 1) / A.mch;
+        int incl = local;
+        for (int off = 1; off < 64; off <<= 1) {
+            const int o = __shfl_up(incl, off);
+            if (lane >= off) incl += o;
+        }
+        if (lane == 63) wsum[wave] = incl;
+        __syncthreads();
+        int before = incl - local;
+        for (int i = 0; i < wave; i++) before += wsum[i];
+        for (int e = e0; e < e1; e++) {
+            const int nr = (cnt[e] + A.mch - 1) / A.mch;
+            gid[e] = before;
+            for (int r = 0; r < nr; r++) rexp[before + r] = e;
+            before += nr;
+        }
+        int nd = 0;
+        for (int i = 0; i < (T >> 6); i++) nd += wsum[i];
+        for (int m = tid; m < A.nm; m += T) {
+            const int e = ms[m];
+            int j = 0;
+            for (int q = 0; q < nm4; q++) {            // broadcast reads, 4 entries each
+                const int4 v = reinterpret_cast<const int4*>(ms)[q];
+                const int b = 4 * q;
+                j += (b + 0 < m) & (v.x == e);
+                j += (b + 1 < m) & (v.y == e);
+                j += (b + 2 < m) & (v.z == e);
+                j += (b + 3 < m) & (v.w == e);
+            }
+            pl[m] = j;
+        }
+        __syncthreads();
+        return nd;
+    }
+};
+
 template <int TYPE, int S, bool WHOLE>
 __global__ __launch_bounds__(1024) void kq_mx_kernel(MxArg A) {
     using TI = TypeInfo<TYPE>;
@@ -1537,7 +1609,18 @@ __global__ __launch_bounds__(1024) void kq_mx_kernel(MxArg A) {
     float4* xb0 = reinterpret_cast<float4*>(smem + 8 * MX_MAXM + 64 + A.sums_bytes);
     float4* xb1 = reinterpret_cast<float4*>(reinterpret_cast<uint8_t*>(xb0) + A.xt_bytes);
 
-    const int ng = A.gdev ? *A.ngdev : 1;
+    MoeRuns mr;
+    int nd = 1;
+    if (A.sel) {                                  // uniform: MoE runs built here
+        int* gi = reinterpret_cast<int*>(smem + A.grp_off);
+        mr.cnt = gi;
+        mr.gid = gi + A.E;
+        mr.ms = gi + ((2 * A.E + 3) & ~3);
+        mr.pl = mr.ms + 4 * ((A.nm + 3) >> 2);
+        mr.rexp = mr.pl + A.nm;
+        nd = mr.build(A, flags);
+    }
+    const int ng = A.sel ? A.nt * nd : A.gdev ? *A.ngdev : 1;
     const int nitems = ng * A.nblk;
     for (int item = blockIdx.x; item < nitems; item += A.grid) {
         const int g = item / A.nblk, blk = item - g * A.nblk;
@@ -1546,7 +1629,21 @@ __global__ __launch_bounds__(1024) void kq_mx_kernel(MxArg A) {
         float* Yb;
         int M;
         __syncthreads();                          // the previous item's table reads are done
-        if (A.gdev) {
+        if (A.sel) {
+            const int t = g >= nd ? 1 : 0, rn = g - t * nd;
+            const int e = mr.rexp[rn], r = rn - mr.gid[e];
+            gw = A.wt[t] + (size_t)e * A.estride;
+            Yb = A.yt[t];
+            M = min(mr.cnt[e] - r * A.mch, A.mch);
+            for (int m = tid; m < A.nm; m += T) {
+                const int j = mr.pl[m];
+                if (mr.ms[m] == e && j / A.mch == r) {
+                    const int slot = j - r * A.mch;
+                    d_xi[slot] = m / A.x_div;
+                    d_yi[slot] = m;
+                }
+            }
+        } else if (A.gdev) {
             const MxGroup* Gd = A.gdev + g;
             gw = Gd->w;
             Yb = Gd->y;
@@ -2631,6 +2728,11 @@ int kqk_launch_mx(int type, const int* plan, long lds, int grid, const void* w, 
     a.RB = plan[2]; a.nblk = plan[3];
     a.threads = plan[0]; a.grid = grid;
     a.TC = plan[4]; a.sums_bytes = plan[5]; a.xt_bytes = plan[6]; a.mch = plan[7];
+    a.sel = nullptr;
+    a.nm = a.E = a.nt = a.x_div = a.grp_off = 0;
+    a.wt[0] = a.wt[1] = nullptr;
+    a.yt[0] = a.yt[1] = nullptr;
+    a.estride = 0;
     const bool whole = a.TC >= (K >> 6);
     switch (type) {
     case T_Q4K: return launch_mx_t<T_Q4K>(a, plan[1], whole, lds, st);
@@ -2655,6 +2757,49 @@ int kqk_launch_moe_topk(const float* probs, int B, int E, int k, int* sel, float
 }
 
 long kqk_mx_group_bytes(void) { return (long)sizeof(MxGroup); }
+
+// LDS bytes of the in-launch MoE runs (MoeRuns) for nm members, E experts
+// and at most ndmax runs
+long kqk_moe_runs_lds(int nm, int E, int ndmax) {
+    return 4L * (((2L * E + 3) & ~3L) + 4L * ((nm + 3) / 4) + nm + ndmax);
+}
+
+// A MoE batch in one multi-x launch that groups the selection itself: the
+// groups kq_moe_group_kernel would write, built in every workgroup's LDS
+// at byte offset plan_lds (lds = plan_lds + kqk_moe_runs_lds(...)).
+int kqk_launch_mx_moe(int type, const int* plan, long plan_lds, long lds, int grid, const int* sel,
+                      int nm, int E, int nt, int x_div, const void* w0, const void* w1, float* y0,
+                      float* y1, long estride, const float* X, int N, int K, hipStream_t st) {
+    if (nm < 1 || E < 1 || E > 4096 || nt < 1 || nt > 2 || x_div < 1 || plan[7] < 1 ||
+        plan[7] > MX_MAXM || plan_lds < 0 || (plan_lds & 15))
+        return (int)hipErrorInvalidValue;
+    MxArg a;
+    a.w = nullptr;
+    a.M = 0;
+    a.N = N; a.K = K;
+    a.gdev = nullptr;
+    a.ngdev = nullptr;
+    a.X = X; a.Y = nullptr;
+    a.x_stride = K; a.y_stride = N;
+    a.RB = plan[2]; a.nblk = plan[3];
+    a.threads = plan[0]; a.grid = grid;
+    a.TC = plan[4]; a.sums_bytes = plan[5]; a.xt_bytes = plan[6]; a.mch = plan[7];
+    a.sel = sel;
+    a.nm = nm; a.E = E; a.nt = nt; a.x_div = x_div; a.grp_off = (int)plan_lds;
+    a.wt[0] = static_cast<const uint8_t*>(w0);
+    a.wt[1] = static_cast<const uint8_t*>(nt > 1 ? w1 : w0);
+    a.yt[0] = y0;
+    a.yt[1] = nt > 1 ? y1 : y0;
+    a.estride = estride;
+    const bool whole = a.TC >= (K >> 6);
+    switch (type) {
+    case T_Q4K: return launch_mx_t<T_Q4K>(a, plan[1], whole, lds, st);
+    case T_Q6K: return launch_mx_t<T_Q6K>(a, plan[1], whole, lds, st);
+    case T_Q2K: return launch_mx_t<T_Q2K>(a, plan[1], whole, lds, st);
+    case T_NIB: return launch_mx_t<T_NIB>(a, plan[1], whole, lds, st);
+    default: return (int)hipErrorInvalidValue;
+    }
+}
 
 int kqk_launch_moe_group(const int* sel, int nm, int E, int nt, int x_div, int mch,
                          const void* w0, const void* w1, float* y0, float* y1, long estride,

@@ -385,11 +385,11 @@ static mx_plan_entry g_plans[MX_PLAN_CACHE];
 static int g_plan_next;
 
 static long mx_plan(int type, int N, int K, int mmax, int ngmax, int grid, const int moe[4],
-                    int* plan) {
+                    int lds_max, int* plan) {
     for (int i = 0; i < MX_PLAN_CACHE; i++) {
         const mx_plan_entry* c = &g_plans[i];
         if (c->used && c->type == type && c->N == N && c->K == K && c->mmax == mmax &&
-            c->ngmax == ngmax && c->grid == grid && c->lds_max == g_kq.lds_max &&
+            c->ngmax == ngmax && c->grid == grid && c->lds_max == lds_max &&
             !memcmp(c->moe, moe, sizeof c->moe)) {
             memcpy(plan, c->plan, sizeof c->plan);
             return c->lds;
@@ -416,14 +416,14 @@ static long mx_plan(int type, int N, int K, int mmax, int ngmax, int grid, const
             ngm[m] = (float)(nt * E * runs);
         }
         ngm[0] = ngm[1];
-        lds = kqk_mx_plan(type, N, K, mmax, ngmax, grid, g_kq.lds_max, plan, ngm);
+        lds = kqk_mx_plan(type, N, K, mmax, ngmax, grid, lds_max, plan, ngm);
     } else {
-        lds = kqk_mx_plan(type, N, K, mmax, ngmax, grid, g_kq.lds_max, plan, NULL);
+        lds = kqk_mx_plan(type, N, K, mmax, ngmax, grid, lds_max, plan, NULL);
     }
     mx_plan_entry* c = &g_plans[g_plan_next];
     g_plan_next = (g_plan_next + 1) % MX_PLAN_CACHE;
     c->used = 1; c->type = type; c->N = N; c->K = K; c->mmax = mmax; c->ngmax = ngmax;
-    c->grid = grid; c->lds_max = g_kq.lds_max;
+    c->grid = grid; c->lds_max = lds_max;
     memcpy(c->moe, moe, sizeof c->moe);
     c->lds = lds;
     memcpy(c->plan, plan, sizeof c->plan);
@@ -445,7 +445,7 @@ int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,
         const int nb = B - s0 < 64 ? B - s0 : 64;
         int plan[KQK_MX_PLAN];
         static const int no_moe[4] = {0, 0, 0, 0};
-        const long lds = mx_plan(type, N, K, nb, 1, grid, no_moe, plan);
+        const long lds = mx_plan(type, N, K, nb, 1, grid, no_moe, g_kq.lds_max, plan);
         if (lds < 0) {
             /* x too long to stage even in 8-chunk tiles: single-stream launches */
             for (int s = s0; s < s0 + nb; s++)
@@ -779,7 +779,25 @@ int kq_moe_gemv_dev(const kq_moe_op* op, const int* sel, int B, int k, int E, kq
     const int grid = plan_grid();
     int plan[KQK_MX_PLAN];
     const int moe[4] = {B, k, E, nt};
-    const long lds = mx_plan(op->type, op->n_out, op->k_in, mmax, nt * dmax, grid, moe, plan);
+    /* The expert runs are built inside the multi-x launch when their LDS
+     * fits beside the plan's: one launch instead of two (the grouping
+     * launch is kept for the rest, and under KQ_MOE_GROUP_LAUNCH=1). */
+    const long rbytes = kqk_moe_runs_lds(nm, E, dmax + nm);
+    if (!getenv("KQ_MOE_GROUP_LAUNCH") && rbytes + 16 < g_kq.lds_max / 2) {
+        const long pl = mx_plan(op->type, op->n_out, op->k_in, mmax, nt * dmax, grid, moe,
+                                g_kq.lds_max - (int)rbytes - 16, plan);
+        if (pl >= 0) {
+            const long off = (pl + 15) & ~15L;
+            const int e = kqk_launch_mx_moe(op->type, plan, off, off + rbytes, grid, sel, nm, E,
+                                            nt, op->x_div, op->w[0], op->w[nt - 1], op->y[0],
+                                            op->y[nt - 1], (long)op->expert_stride, op->x,
+                                            op->n_out, op->k_in, st);
+            if (e) return kq_fail("moe gemv launch: %s", hipGetErrorString((hipError_t)e));
+            return 0;
+        }
+    }
+    const long lds = mx_plan(op->type, op->n_out, op->k_in, mmax, nt * dmax, grid, moe,
+                             g_kq.lds_max, plan);
     if (lds < 0) return kq_fail("kq_moe_gemv_dev: no launch plan for K=%d", op->k_in);
     const int mch = plan[7];
     const int ngmax = nt * (dmax + (nm + mch - 1) / mch);

@@ -220,11 +220,16 @@ def test_moe_routed_one_token(port, qtype, E, k, case):
     check_members(port, qtype, [gate, up], sel, x, k, got, F, H)
 
 
+@pytest.mark.parametrize("grouping", ["in_launch", "group_launch"])
 @pytest.mark.parametrize("qtype", [12, 14, 10])
 @pytest.mark.parametrize("B,n_exp", [(16, 32), (16, 128), (3, 8), (64, 16)])
-def test_moe_batch_grouped(port, qtype, B, n_exp):
+def test_moe_batch_grouped(port, qtype, B, n_exp, grouping, monkeypatch):
     """Batches whose tokens share experts: each selected slice is streamed
-    once for all its tokens; every member still equals its single GEMV."""
+    once for all its tokens; every member still equals its single GEMV.
+    The expert runs are built inside the multi-x launch, or (forced) by the
+    separate grouping launch."""
+    if grouping == "group_launch":
+        monkeypatch.setenv("KQ_MOE_GROUP_LAUNCH", "1")
     H, F, k = 512, 256, min(8, n_exp)
     gate, up = experts(qtype, n_exp, F, H, 11), experts(qtype, n_exp, F, H, 12)
     down = experts(qtype, n_exp, H, F, 13)
@@ -239,9 +244,12 @@ def test_moe_batch_grouped(port, qtype, B, n_exp):
     check_members(port, qtype, [down], sel, act, 1, got, H, F)
 
 
-def test_moe_pack_layout_and_unselected_slots(port):
+@pytest.mark.parametrize("grouping", ["in_launch", "group_launch"])
+def test_moe_pack_layout_and_unselected_slots(port, grouping, monkeypatch):
     """Expert slices in a pack (gate|up|down per expert, stride = their sum),
     with some ranks unselected (sel -1): the selected ranks are exact."""
+    if grouping == "group_launch":
+        monkeypatch.setenv("KQ_MOE_GROUP_LAUNCH", "1")
     qtype, n_exp, H, F, B, k = 12, 12, 512, 256, 6, 4
     rb_g = K.lib().kq_row_bytes(qtype, H)
     rb_d = K.lib().kq_row_bytes(qtype, F)
