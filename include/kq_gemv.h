@@ -266,15 +266,19 @@ typedef struct kq_moe_op {
 } kq_moe_op;
 int kq_moe_gemv_dev(const kq_moe_op* op, const int* sel, int B, int k, int E, kq_stream stream);
 
-/* One token, routed and gathered in one launch: the top-k of the router
- * weights probs[0..E) (E <= 1024; the rule of kq_moe_topk) is taken inside
- * the launch that runs op, written to sel[0..k) / selw[0..k) (device
- * memory) as kq_moe_topk_dev writes it, and used as kq_moe_gemv_dev(op,
- * sel, 1, k, E) uses it -- the same outputs bit for bit, one launch fewer.
- * The usual call is the gate+up op; the down op then takes sel.  No
- * counterpart in the reference, which routes on the host (moe_topk,
- * stratum_arch_moe.inc.c:368-385) before the per-slice dispatch. */
-int kq_moe_gemv_routed_dev(const kq_moe_op* op, const float* probs, int k, int E, int* sel,
+/* Routed and gathered in one launch: the top-k of each token's router
+ * weights probs[B][E] (E <= 1024; the rule of kq_moe_topk) is taken inside
+ * the launch that runs op, written to sel[B*k] / selw[B*k] (device memory)
+ * as kq_moe_topk_dev writes them, and used as kq_moe_gemv_dev(op, sel, B,
+ * k, E) uses them -- the same outputs bit for bit, one launch fewer.  A
+ * larger batch (B x E^2 above 2^16, E rounded up to 64: ranking in every
+ * workgroup would cost more than the launch it saves) or one whose router
+ * weights do not fit in the launch's LDS is routed by a separate top-k
+ * launch first, with the same results.  The usual call is the gate+up op; the down
+ * op then takes sel.  No counterpart in the reference, which routes on the
+ * host (moe_topk, stratum_arch_moe.inc.c:368-385) before the per-slice
+ * dispatch. */
+int kq_moe_gemv_routed_dev(const kq_moe_op* op, const float* probs, int B, int k, int E, int* sel,
                            float* selw, kq_stream stream);
 
 #ifdef __cplusplus

@@ -204,7 +204,7 @@ def lib() -> ctypes.CDLL:
     L.kq_moe_topk.restype = None
     L.kq_moe_topk_dev.argtypes = [P, I, I, I, P, P, P]
     L.kq_moe_gemv_dev.argtypes = [ctypes.POINTER(KqMoeOp), P, I, I, I, P]
-    L.kq_moe_gemv_routed_dev.argtypes = [ctypes.POINTER(KqMoeOp), P, I, I, P, P, P]
+    L.kq_moe_gemv_routed_dev.argtypes = [ctypes.POINTER(KqMoeOp), P, I, I, I, P, P, P]
     _LIB = L
     return L
 
@@ -346,9 +346,9 @@ def moe_gemv_dev(op: KqMoeOp, sel_ptr: int, B: int, k: int, E: int,
     _check(lib().kq_moe_gemv_dev(ctypes.byref(op), sel_ptr, B, k, E, stream), "kq_moe_gemv_dev")
 
 
-def moe_gemv_routed_dev(op: KqMoeOp, probs_ptr: int, k: int, E: int, sel_ptr: int,
+def moe_gemv_routed_dev(op: KqMoeOp, probs_ptr: int, B: int, k: int, E: int, sel_ptr: int,
                         selw_ptr: int, stream: int | None = None) -> None:
-    """One token: top-k of probs inside the launch that runs op (written to
-    sel / selw), then op on the selected experts (kq_moe_gemv_routed_dev)."""
-    _check(lib().kq_moe_gemv_routed_dev(ctypes.byref(op), probs_ptr, k, E, sel_ptr, selw_ptr,
+    """B tokens: top-k of probs[B][E] inside the launch that runs op (written
+    to sel / selw), then op on the selected experts (kq_moe_gemv_routed_dev)."""
+    _check(lib().kq_moe_gemv_routed_dev(ctypes.byref(op), probs_ptr, B, k, E, sel_ptr, selw_ptr,
                                         stream), "kq_moe_gemv_routed_dev")

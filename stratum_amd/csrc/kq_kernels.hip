@@ -1385,6 +1385,14 @@ struct MxArg {
     const uint8_t* wt[2];
     float* yt[2];
     long estride;
+    // routed in the launch (probs != nullptr, sel unused): every workgroup
+    // also takes the top-k of each token's router weights probs[B][E] (the
+    // rule of kq_moe_topk_rank_kernel), and workgroup 0 writes them to
+    // sel_out / selw_out
+    const float* probs;
+    int B, k;
+    int* sel_out;
+    float* selw_out;
 };
 
 // LDS slot of the float4 at tile-relative x position pos (a multiple of 4;
@@ -1533,16 +1541,66 @@ struct MoeRuns {
     int* pl;
     int* rexp;
 
-    __device__ int build(const MxArg& A, int* wsum) {
+    // LDS at base: [routed: B x E64 router weights, 4 ceil(nm/4) selected
+    // weights], cnt[E], gid[E] (16-byte padded), ms[4 ceil(nm/4)], pl[nm],
+    // rexp[runs]
+    __device__ int build(const MxArg& A, int* wsum, uint8_t* base) {
         const int tid = threadIdx.x, T = A.threads, lane = tid & 63, wave = tid >> 6;
-        const int nm4 = (A.nm + 3) >> 2;
+        const int nm4 = (A.nm + 3) >> 2, E64 = (A.E + 63) & ~63;
+        const bool routed = A.probs != nullptr;                 // uniform
+        float* pw = reinterpret_cast<float*>(base);
+        float* msw = pw + (routed ? A.B * E64 : 0);
+        cnt = reinterpret_cast<int*>(msw + (routed ? 4 * nm4 : 0));
+        gid = cnt + A.E;
+        ms = cnt + ((2 * A.E + 3) & ~3);
+        pl = ms + 4 * nm4;
+        rexp = pl + A.nm;
         for (int e = tid; e < A.E; e += T) cnt[e] = 0;
-        __syncthreads();
-        for (int m = tid; m < 4 * nm4; m += T) {
-            const int e = m < A.nm ? A.sel[m] : -1;
-            const int ok = e >= 0 && e < A.E;
-            ms[m] = ok ? e : -1;
-            if (ok) atomicAdd(&cnt[e], 1);
+        if (routed) {
+            for (int i = tid; i < A.B * E64; i += T) {
+                const int t = i / E64, e = i - t * E64;
+                pw[i] = e < A.E ? A.probs[(size_t)t * A.E + e] : -1.0f;   // -1: never eligible
+            }
+            for (int m = tid; m < 4 * nm4; m += T) ms[m] = -1;
+            __syncthreads();
+            // expert e of token t takes slot rank = the eligible experts that
+            // beat it (larger weight, or equal and lower id) when rank < k
+            for (int i = tid; i < A.B * E64; i += T) {
+                const int t = i / E64, e = i - t * E64;
+                const float* row = pw + t * E64;
+                const float v = row[e];
+                int r = 0;
+                for (int q = 0; q < E64; q += 4) {
+                    const float4 o = *reinterpret_cast<const float4*>(row + q);
+                    const float ov[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const float x = ov[j];
+                        const int beat = (x > v) | ((x == v) & (q + j < e));
+                        r += (x > -1.0f) & beat;
+                    }
+                }
+                if (v > -1.0f && r < A.k) {
+                    ms[t * A.k + r] = e;
+                    msw[t * A.k + r] = v;
+                }
+            }
+            __syncthreads();
+            if (blockIdx.x == 0)
+                for (int m = tid; m < A.nm; m += T) {
+                    A.sel_out[m] = ms[m];
+                    A.selw_out[m] = ms[m] >= 0 ? msw[m] : -1.0f;
+                }
+            for (int m = tid; m < A.nm; m += T)
+                if (ms[m] >= 0) atomicAdd(&cnt[ms[m]], 1);
+        } else {
+            __syncthreads();
+            for (int m = tid; m < 4 * nm4; m += T) {
+                const int e = m < A.nm ? A.sel[m] : -1;
+                const int ok = e >= 0 && e < A.E;
+                ms[m] = ok ? e : -1;
+                if (ok) atomicAdd(&cnt[e], 1);
+            }
         }
         __syncthreads();
         const int run = (A.E + T - 1) / T, e0 = tid * run, e1 = min(A.E, e0 + run);
@@ -1611,16 +1669,9 @@ __global__ __launch_bounds__(1024) void kq_mx_kernel(MxArg A) {
 
     MoeRuns mr;
     int nd = 1;
-    if (A.sel) {                                  // uniform: MoE runs built here
-        int* gi = reinterpret_cast<int*>(smem + A.grp_off);
-        mr.cnt = gi;
-        mr.gid = gi + A.E;
-        mr.ms = gi + ((2 * A.E + 3) & ~3);
-        mr.pl = mr.ms + 4 * ((A.nm + 3) >> 2);
-        mr.rexp = mr.pl + A.nm;
-        nd = mr.build(A, flags);
-    }
-    const int ng = A.sel ? A.nt * nd : A.gdev ? *A.ngdev : 1;
+    const bool moe = A.nm > 0;                    // uniform: MoE runs built here
+    if (moe) nd = mr.build(A, flags, smem + A.grp_off);
+    const int ng = moe ? A.nt * nd : A.gdev ? *A.ngdev : 1;
     const int nitems = ng * A.nblk;
     for (int item = blockIdx.x; item < nitems; item += A.grid) {
         const int g = item / A.nblk, blk = item - g * A.nblk;
@@ -1629,7 +1680,7 @@ __global__ __launch_bounds__(1024) void kq_mx_kernel(MxArg A) {
         float* Yb;
         int M;
         __syncthreads();                          // the previous item's table reads are done
-        if (A.sel) {
+        if (moe) {
             const int t = g >= nd ? 1 : 0, rn = g - t * nd;
             const int e = mr.rexp[rn], r = rn - mr.gid[e];
             gw = A.wt[t] + (size_t)e * A.estride;
@@ -2733,6 +2784,10 @@ int kqk_launch_mx(int type, const int* plan, long lds, int grid, const void* w, 
     a.wt[0] = a.wt[1] = nullptr;
     a.yt[0] = a.yt[1] = nullptr;
     a.estride = 0;
+    a.probs = nullptr;
+    a.B = a.k = 0;
+    a.sel_out = nullptr;
+    a.selw_out = nullptr;
     const bool whole = a.TC >= (K >> 6);
     switch (type) {
     case T_Q4K: return launch_mx_t<T_Q4K>(a, plan[1], whole, lds, st);
@@ -2759,9 +2814,10 @@ int kqk_launch_moe_topk(const float* probs, int B, int E, int k, int* sel, float
 long kqk_mx_group_bytes(void) { return (long)sizeof(MxGroup); }
 
 // LDS bytes of the in-launch MoE runs (MoeRuns) for nm members, E experts
-// and at most ndmax runs
-long kqk_moe_runs_lds(int nm, int E, int ndmax) {
-    return 4L * (((2L * E + 3) & ~3L) + 4L * ((nm + 3) / 4) + nm + ndmax);
+// and at most ndmax runs; B > 0: routed in the launch for B tokens
+long kqk_moe_runs_lds(int nm, int E, int ndmax, int B) {
+    const long E64 = (E + 63) & ~63L, nm4 = (nm + 3) / 4;
+    return 4L * ((B > 0 ? B * E64 + 4 * nm4 : 0) + ((2L * E + 3) & ~3L) + 4 * nm4 + nm + ndmax);
 }
 
 // A MoE batch in one multi-x launch that groups the selection itself: the
@@ -2769,9 +2825,11 @@ long kqk_moe_runs_lds(int nm, int E, int ndmax) {
 // at byte offset plan_lds (lds = plan_lds + kqk_moe_runs_lds(...)).
 int kqk_launch_mx_moe(int type, const int* plan, long plan_lds, long lds, int grid, const int* sel,
                       int nm, int E, int nt, int x_div, const void* w0, const void* w1, float* y0,
-                      float* y1, long estride, const float* X, int N, int K, hipStream_t st) {
+                      float* y1, long estride, const float* X, int N, int K, const float* probs,
+                      int B, int k, int* sel_out, float* selw_out, hipStream_t st) {
     if (nm < 1 || E < 1 || E > 4096 || nt < 1 || nt > 2 || x_div < 1 || plan[7] < 1 ||
-        plan[7] > MX_MAXM || plan_lds < 0 || (plan_lds & 15))
+        plan[7] > MX_MAXM || plan_lds < 0 || (plan_lds & 15) ||
+        (probs && (B < 1 || k < 1 || B * k != nm || !sel_out || !selw_out)) || (!probs && !sel))
         return (int)hipErrorInvalidValue;
     MxArg a;
     a.w = nullptr;
@@ -2791,6 +2849,11 @@ int kqk_launch_mx_moe(int type, const int* plan, long plan_lds, long lds, int gr
     a.yt[0] = y0;
     a.yt[1] = nt > 1 ? y1 : y0;
     a.estride = estride;
+    a.probs = probs;
+    a.B = probs ? B : 0;
+    a.k = probs ? k : 0;
+    a.sel_out = sel_out;
+    a.selw_out = selw_out;
     const bool whole = a.TC >= (K >> 6);
     switch (type) {
     case T_Q4K: return launch_mx_t<T_Q4K>(a, plan[1], whole, lds, st);

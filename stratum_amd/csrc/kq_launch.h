@@ -53,10 +53,11 @@ int kqk_mx_set_max_lds(int bytes);
 int kqk_launch_moe_topk(const float* probs, int B, int E, int k, int* sel, float* selw,
                         hipStream_t st);
 long kqk_mx_group_bytes(void);
-long kqk_moe_runs_lds(int nm, int E, int ndmax);
+long kqk_moe_runs_lds(int nm, int E, int ndmax, int B);
 int kqk_launch_mx_moe(int type, const int* plan, long plan_lds, long lds, int grid, const int* sel,
                       int nm, int E, int nt, int x_div, const void* w0, const void* w1, float* y0,
-                      float* y1, long estride, const float* X, int N, int K, hipStream_t st);
+                      float* y1, long estride, const float* X, int N, int K, const float* probs,
+                      int B, int k, int* sel_out, float* selw_out, hipStream_t st);
 /* MFMA multi-x (Q4_K, Q6_K): workspace sizes, and the launch */
 int kqk_mfma_workspace(int type, int B, int N, int K, long* planes, long* xs, long* part);
 int kqk_launch_mfma(int type, const float* x, const void* w, float* y, int B, int N, int K,

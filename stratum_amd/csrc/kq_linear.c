@@ -751,38 +751,30 @@ static int moe_check_op(const kq_moe_op* op, int k, int E, const char* who) {
     return 0;
 }
 
-int kq_moe_gemv_routed_dev(const kq_moe_op* op, const float* probs, int k, int E, int* sel,
-                           float* selw, kq_stream stream) {
-    if (!op || !probs || !sel || !selw) return kq_fail("kq_moe_gemv_routed_dev: NULL argument");
-    if (k < 1 || k > KQ_MAX_GROUPS || E < 1 || E > 1024)
-        return kq_fail("kq_moe_gemv_routed_dev: k=%d E=%d (E <= 1024)", k, E);
-    if (moe_check_op(op, k, E, "kq_moe_gemv_routed_dev")) return -1;
-    return moe_one_token(op, sel, k, E, probs, selw, pick(stream));
-}
-
-int kq_moe_gemv_dev(const kq_moe_op* op, const int* sel, int B, int k, int E, kq_stream stream) {
-    if (!op || !sel) return kq_fail("kq_moe_gemv_dev: NULL argument");
-    if (B < 1 || B > KQ_MOE_MAX_TOKENS || k < 1 || k > KQ_MAX_GROUPS || E < 1 ||
-        E > KQ_MOE_MAX_EXPERTS)
-        return kq_fail("kq_moe_gemv_dev: B=%d k=%d E=%d", B, k, E);
-    if (moe_check_op(op, k, E, "kq_moe_gemv_dev")) return -1;
+/* Several tokens: expert groups built on the device, then one weight pass
+ * per selected expert for all of its tokens.  The launch is planned for
+ * uniform routing (mx_plan): the planner picks the run length, and with it
+ * the item count, and the runs are cut accordingly.  The runs are built
+ * inside the multi-x launch when their LDS fits beside the plan's (one
+ * launch instead of two; the grouping launch is kept for the rest, and
+ * under KQ_MOE_GROUP_LAUNCH=1).  probs != NULL: the top-k is taken in that
+ * launch too, written to sel / selw; returns 1 (nothing launched) when it
+ * does not fit or does not pay, for the caller to route separately.  Every
+ * workgroup ranks all B x E weights itself, about B E^2 compares: at
+ * B = 16, E = 128 that took longer (114 us per layer) than the separate
+ * top-k launch (104 us), so the in-launch ranking is kept to B E^2 <= 2^16
+ * (E padded to 64). */
+static int moe_batch(const kq_moe_op* op, int* sel, const float* probs, float* selw, int B, int k,
+                     int E, hipStream_t st) {
+    const long E64 = (E + 63) & ~63L;
+    if (probs && (long)B * E64 * E64 > (1L << 16)) return 1;
     const int nt = op->ntensors;
-    hipStream_t st = pick(stream);
-    if (B == 1) return moe_one_token(op, sel, k, E, NULL, NULL, st);
-    /* several tokens: expert groups built on the device, then one weight
-     * pass per selected expert for all of its tokens.  The launch is
-     * planned for uniform routing (mx_plan): the planner picks the run
-     * length, and with it the item count, and the grouping kernel cuts the
-     * member lists accordingly. */
     const int nm = B * k, dmax = E < nm ? E : nm;
     const int mmax = B < 16 ? B : 16;
     const int grid = plan_grid();
     int plan[KQK_MX_PLAN];
     const int moe[4] = {B, k, E, nt};
-    /* The expert runs are built inside the multi-x launch when their LDS
-     * fits beside the plan's: one launch instead of two (the grouping
-     * launch is kept for the rest, and under KQ_MOE_GROUP_LAUNCH=1). */
-    const long rbytes = kqk_moe_runs_lds(nm, E, dmax + nm);
+    const long rbytes = kqk_moe_runs_lds(nm, E, dmax + nm, probs ? B : 0);
     if (!getenv("KQ_MOE_GROUP_LAUNCH") && rbytes + 16 < g_kq.lds_max / 2) {
         const long pl = mx_plan(op->type, op->n_out, op->k_in, mmax, nt * dmax, grid, moe,
                                 g_kq.lds_max - (int)rbytes - 16, plan);
@@ -791,11 +783,12 @@ int kq_moe_gemv_dev(const kq_moe_op* op, const int* sel, int B, int k, int E, kq
             const int e = kqk_launch_mx_moe(op->type, plan, off, off + rbytes, grid, sel, nm, E,
                                             nt, op->x_div, op->w[0], op->w[nt - 1], op->y[0],
                                             op->y[nt - 1], (long)op->expert_stride, op->x,
-                                            op->n_out, op->k_in, st);
+                                            op->n_out, op->k_in, probs, B, k, sel, selw, st);
             if (e) return kq_fail("moe gemv launch: %s", hipGetErrorString((hipError_t)e));
             return 0;
         }
     }
+    if (probs) return 1;
     const long lds = mx_plan(op->type, op->n_out, op->k_in, mmax, nt * dmax, grid, moe,
                              g_kq.lds_max, plan);
     if (lds < 0) return kq_fail("kq_moe_gemv_dev: no launch plan for K=%d", op->k_in);
@@ -812,4 +805,31 @@ int kq_moe_gemv_dev(const kq_moe_op* op, const int* sel, int B, int k, int E, kq
                       op->n_out, op->n_out, op->k_in, st);
     if (e) return kq_fail("moe gemv launch: %s", hipGetErrorString((hipError_t)e));
     return 0;
+}
+
+int kq_moe_gemv_routed_dev(const kq_moe_op* op, const float* probs, int B, int k, int E, int* sel,
+                           float* selw, kq_stream stream) {
+    if (!op || !probs || !sel || !selw) return kq_fail("kq_moe_gemv_routed_dev: NULL argument");
+    if (B < 1 || B > KQ_MOE_MAX_TOKENS || k < 1 || k > KQ_MAX_GROUPS || E < 1 || E > 1024)
+        return kq_fail("kq_moe_gemv_routed_dev: B=%d k=%d E=%d (E <= 1024)", B, k, E);
+    if (moe_check_op(op, k, E, "kq_moe_gemv_routed_dev")) return -1;
+    hipStream_t st = pick(stream);
+    if (B == 1) return moe_one_token(op, sel, k, E, probs, selw, st);
+    const int r = moe_batch(op, sel, probs, selw, B, k, E, st);
+    if (r <= 0) return r;
+    /* the router weights do not fit beside the plan: route separately */
+    const int e = kqk_launch_moe_topk(probs, B, E, k, sel, selw, st);
+    if (e) return kq_fail("moe topk launch: %s", hipGetErrorString((hipError_t)e));
+    return moe_batch(op, sel, NULL, NULL, B, k, E, st);
+}
+
+int kq_moe_gemv_dev(const kq_moe_op* op, const int* sel, int B, int k, int E, kq_stream stream) {
+    if (!op || !sel) return kq_fail("kq_moe_gemv_dev: NULL argument");
+    if (B < 1 || B > KQ_MOE_MAX_TOKENS || k < 1 || k > KQ_MAX_GROUPS || E < 1 ||
+        E > KQ_MOE_MAX_EXPERTS)
+        return kq_fail("kq_moe_gemv_dev: B=%d k=%d E=%d", B, k, E);
+    if (moe_check_op(op, k, E, "kq_moe_gemv_dev")) return -1;
+    hipStream_t st = pick(stream);
+    if (B == 1) return moe_one_token(op, sel, k, E, NULL, NULL, st);
+    return moe_batch(op, (int*)sel, NULL, NULL, B, k, E, st);
 }

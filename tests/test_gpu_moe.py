@@ -170,21 +170,22 @@ def test_moe_one_token_gate_up_and_down(port, qtype):
 
 
 def run_routed(qtype, wts, probs, x, x_div, k, N_out, K_in):
-    """kq_moe_gemv_routed_dev: top-k of probs inside the launch; returns the
-    outputs and the sel / selw it wrote."""
+    """kq_moe_gemv_routed_dev: top-k of probs ([E] or [B, E]) inside the
+    launch; returns the outputs and the sel / selw it wrote."""
+    probs2 = probs.reshape(-1, probs.shape[-1])
+    B, E = probs2.shape
     dws = [dev(w) for w in wts]
     stride = N_out * K.lib().kq_row_bytes(qtype, K_in)
-    dx, dp = dev(x), dev(probs)
-    ys = [torch.full((k * N_out,), float("nan"), dtype=torch.float32, device="cuda")
+    dx, dp = dev(x), dev(np.ascontiguousarray(probs2).reshape(-1))
+    ys = [torch.full((B * k * N_out,), float("nan"), dtype=torch.float32, device="cuda")
           for _ in wts]
-    sel = torch.full((k,), -7, dtype=torch.int32, device="cuda")
-    selw = torch.full((k,), 7.0, dtype=torch.float32, device="cuda")
+    sel = torch.full((B * k,), -7, dtype=torch.int32, device="cuda")
+    selw = torch.full((B * k,), 7.0, dtype=torch.float32, device="cuda")
     op = K.moe_op(qtype, N_out, K_in, [d.data_ptr() for d in dws], stride, dx.data_ptr(), x_div,
                   [y.data_ptr() for y in ys])
-    K.moe_gemv_routed_dev(op, dp.data_ptr(), k, probs.size, sel.data_ptr(), selw.data_ptr(),
-                          stream())
+    K.moe_gemv_routed_dev(op, dp.data_ptr(), B, k, E, sel.data_ptr(), selw.data_ptr(), stream())
     torch.cuda.synchronize()
-    return ([y.cpu().numpy().reshape(k, N_out) for y in ys], sel.cpu().numpy(),
+    return ([y.cpu().numpy().reshape(B * k, N_out) for y in ys], sel.cpu().numpy(),
             selw.cpu().numpy())
 
 
@@ -218,6 +219,43 @@ def test_moe_routed_one_token(port, qtype, E, k, case):
             if sel[m] >= 0:
                 assert same_values(got[t][m], want[t][m]), (t, m)
     check_members(port, qtype, [gate, up], sel, x, k, got, F, H)
+
+
+@pytest.mark.parametrize("qtype", [12, 14])
+@pytest.mark.parametrize("B,E,k,case", [(16, 128, 8, "random"), (3, 32, 4, "ties"),
+                                        (8, 40, 16, "few-eligible"), (64, 16, 2, "random")])
+def test_moe_routed_batch(port, qtype, B, E, k, case):
+    """Batches routed inside the gate+up launch: sel / selw equal the device
+    top-k of every token, and every output equals the unrouted batch call's
+    bit for bit; the down call then runs on the written sel."""
+    H, F = 512, 256
+    gate, up = experts(qtype, E, F, H, 31), experts(qtype, E, F, H, 32)
+    r = np.random.default_rng(B * E + k)
+    if case == "random":
+        probs = softmax_rows(r.standard_normal((B, E)).astype(np.float32))
+    elif case == "ties":
+        probs = (r.integers(0, 3, (B, E)) * 0.25).astype(np.float32)
+    else:                                   # fewer eligible experts than k in some tokens
+        probs = softmax_rows(r.standard_normal((B, E)).astype(np.float32))
+        probs[1] = -2.0
+        probs[1, [3, 17, 30]] = [0.5, 0.25, 0.5]
+        probs[5, :] = np.nan
+    x = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
+    got, sel, selw = run_routed(qtype, [gate, up], probs, x, k, k, F, H)
+    dsel, dselw = gpu_topk(probs, k)
+    assert np.array_equal(dsel.reshape(-1), sel) and same_values(dselw.reshape(-1), selw)
+    for s_ in range(min(B, 4)):
+        ws, ww = port.topk(probs[s_], k)
+        assert list(sel[s_ * k:(s_ + 1) * k]) == ws
+    want = run_moe(qtype, [gate, up], sel.reshape(B, k), x, k, B, k, E, F, H)
+    for t in range(2):
+        for m in range(B * k):
+            if sel[m] >= 0:
+                assert same_values(got[t][m], want[t][m]), (t, m)
+    act = np.stack([synth.gaussian(r, F) for _ in range(B * k)]).reshape(-1)
+    down = experts(qtype, E, H, F, 33)
+    dn = run_moe(qtype, [down], sel.reshape(B, k), act, 1, B, k, E, H, F)
+    check_members(port, qtype, [down], sel.reshape(B, k), act, 1, dn, H, F)
 
 
 @pytest.mark.parametrize("grouping", ["in_launch", "group_launch"])
