@@ -859,7 +859,8 @@ struct Seg {
 
 // Issues the scalar loads of a segment's leading fields together and waits
 // for them once: used as they are needed, the fields would be fetched in
-// several dependent round trips to the kernel-argument memory.
+// several dependent round trips to the kernel-argument memory.  (The
+// launch-wide fields are loaded in the same round by the kernel's entry.)
 __device__ __forceinline__ void prefetch_seg(const Seg& S) {
     asm volatile("" ::"s"(S.x), "s"(S.sel), "s"(S.type), "s"(S.K), "s"(S.N), "s"(S.nparts),
                  "s"(S.x_stride), "s"(S.pn), "s"(S.pn_m), "s"(S.pn_l), "s"(S.nc_m), "s"(S.nc_l),
@@ -1280,9 +1281,17 @@ constexpr int TB_SEL = 16;
 template <int DEPTH, int TYPES, bool MULTI>
 __global__ __launch_bounds__(1024) void kq_segs_kernel(SegsArg A) {
     extern __shared__ __align__(16) uint8_t smem[];
-    asm volatile("" ::"s"(A.nseg), "s"(A.threads), "s"(A.grid), "s"(A.xs_off),
-                 "s"(A.terms_off), "s"(A.scr_off));
-    prefetch_seg(A.s[0]);
+    // one round of scalar loads for the launch-wide and first-segment fields
+    // (two asm statements would wait between them)
+    {
+        const Seg& S = A.s[0];
+        asm volatile("" ::"s"(A.nseg), "s"(A.threads), "s"(A.grid), "s"(A.grid_m),
+                     "s"(A.grid_l), "s"(A.xs_off), "s"(A.terms_off), "s"(A.scr_off), "s"(S.x),
+                     "s"(S.sel), "s"(S.type), "s"(S.K), "s"(S.N), "s"(S.nparts), "s"(S.x_stride),
+                     "s"(S.pn), "s"(S.pn_m), "s"(S.pn_l), "s"(S.nc_m), "s"(S.nc_l),
+                     "s"(S.start[1]), "s"(S.start[2]), "s"(S.start[3]), "s"(S.w[0]),
+                     "s"(S.y[0]), "s"(S.add[0]));
+    }
     const int nseg = MULTI ? A.nseg : 1;
     // batch counters of every segment (the first segment that runs stages
     // x, and its barrier orders these writes before any batch is taken)
