@@ -1133,7 +1133,11 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
     f32x4 xv[G4];
     // first round of x, ahead of the weights (and of the routing, which
     // does not depend on it)
-    if (restage) xg.load(tid, xv);
+    // (only the lanes that own a group: the clamped loads of the others
+    // would queue ahead of the weights in the address units, e.g. 864 of
+    // 1024 lanes at Q4_K, K = 5120; measured over lane- and wave-granular
+    // guards, the lane form gave the best layer set: 63.2 -> 62.1 us)
+    if (restage && tid < xg.total) xg.load(tid, xv);
     // A second round (x longer than one round of the workgroup, e.g. Q6_K
     // at K = 17408 with 1024 lanes) is loaded together with the first, so
     // its latency is not paid after the first round's stores.  Types with
@@ -1142,7 +1146,7 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
     constexpr bool PRE2 = G4 == 4;
     const bool two = PRE2 && restage && xg.total > T;   // uniform
     f32x4 xv2[PRE2 ? G4 : 1];
-    if (PRE2 && two) xg.load(tid + T, xv2);
+    if (PRE2 && two && tid + T < xg.total) xg.load(tid + T, xv2);
 
     const int* rsel = nullptr;
     if (PM == PM_SEL && route) {
