@@ -125,9 +125,9 @@ def load_traffic() -> dict | None:
 
 
 # ---------------------------------------------------------------- other configs
-# BASELINE.json's other configurations, timed in the same run (their lines
-# in DESIGN.md): weights rotated over enough device copies that each pass
-# reads HBM (>= 600 MB rotating set), HIP events on the launch stream.
+# The other benchmark configurations, timed in the same run: weights rotated
+# over enough device copies that each pass reads HBM (>= 600 MB rotating
+# set), HIP events on the launch stream.
 QWEN06B = [  # name, type, N, K, activation (hidden 1024, q 2048, ffn 3072)
     ("attn_q", KQ.TYPE_Q4_K, 2048, 1024, "h"),
     ("attn_k", KQ.TYPE_Q4_K, 1024, 1024, "h"),
@@ -519,8 +519,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
-              f"(--gpus {args.gpus} was asked for); the row split across GPUs is "
-              f"described in DESIGN.md.", file=sys.stderr)
+              f"(--gpus {args.gpus} was asked for): every box here has one GPU, and the "
+              f"row split across GPUs is a design, not code.", file=sys.stderr)
         return 2
 
     import torch
