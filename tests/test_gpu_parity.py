@@ -147,11 +147,13 @@ def test_gemv_add_epilogue(port, qtype):
 
 
 @pytest.mark.parametrize("qtype,N,Kd", [(12, 17408, 5120), (14, 5120, 17408), (12, 6144, 5120),
-                                        (12, 8192, 5120), (42, 17408, 5120), (10, 17408, 5120)])
+                                        (12, 8192, 5120), (14, 8191, 5120), (42, 17408, 5120),
+                                        (10, 17408, 5120)])
 def test_gemv_27b_shape_sampled(port, qtype, N, Kd, monkeypatch):
     """27B-class shapes: 384 sampled rows against the oracle, bit-identical
     reruns, and the same bits under a different row decomposition.  8192 x
-    5120 (the merged Q/K/V row count) runs two workgroups per CU."""
+    5120 (the merged Q/K/V row count) and 8191 x 5120 (ragged: workgroups
+    with 15 and 16 rows) run two workgroups per CU."""
     w = synth.tensor(qtype, N, Kd, 31)
     x = synth.gaussian(synth.rng(32), Kd)
     print(f"27b shape type={qtype} N={N} K={Kd}", flush=True)
