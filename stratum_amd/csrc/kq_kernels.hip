@@ -1088,7 +1088,12 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
     using TI = TypeInfo<TYPE>;
     using C = Chunk<TYPE>;
     const int tid = threadIdx.x, T = A.threads, lane = tid & 63, wave = tid >> 6;
-    const int b = blockIdx.x, G = A.grid;
+    const int G = A.grid;
+    // logical workgroup index, XCD-major (dispatch is round robin over the 8
+    // XCDs, each with its own L2): neighbouring rows, which share the cache
+    // line at their boundary, are then read on one XCD
+    const int b = (G & 7) ? (int)blockIdx.x
+                          : (int)(blockIdx.x & 7) * (G >> 3) + (int)(blockIdx.x >> 3);
     const int K = S.K, NC = K >> 6, N = S.N;
     const int R = N > b ? (int)div_magic((uint32_t)(N - b + G - 1), A.grid_m, A.grid_l) : 0;
     if (R == 0) return;                       // uniform over the workgroup
@@ -1686,7 +1691,14 @@ __global__ __launch_bounds__(1024) void kq_mx_kernel(MxArg A) {
     if (moe) nd = mr.build(A, flags, smem + A.grp_off);
     const int ng = moe ? A.nt * nd : A.gdev ? *A.ngdev : 1;
     const int nitems = ng * A.nblk;
-    for (int item = blockIdx.x; item < nitems; item += A.grid) {
+    // Workgroups are dispatched round robin over the 8 XCDs (each with its
+    // own L2): workgroup b takes the item sequence of logical index
+    // (b % 8) * (grid / 8) + b / 8, so neighbouring items -- the runs of
+    // one expert, which stream the same slice -- run on one XCD and share
+    // its L2.  (grid a multiple of 8; otherwise the plain order.)
+    const int lb = (A.grid & 7) ? (int)blockIdx.x
+                                : (int)(blockIdx.x & 7) * (A.grid >> 3) + (int)(blockIdx.x >> 3);
+    for (int item = lb; item < nitems; item += A.grid) {
         const int g = item / A.nblk, blk = item - g * A.nblk;
         const int r0 = blk * A.RB, rows = min(A.RB, N - r0);
         const uint8_t* gw;
