@@ -78,6 +78,15 @@ void kq_linear_shutdown(void);
 /* Message of the last failure (never NULL). */
 const char* kq_last_error(void);
 
+/* Launch-shape overrides for tuning runs and tests: KQ_GRID (workgroups),
+ * KQ_WG_THREADS (256, 512 or 1024 lanes), KQ_DEPTH (1 or 2 batches in
+ * flight) and KQ_MOE_GROUP_LAUNCH (MoE batches grouped by a separate
+ * launch).  The environment is read once, at the first call that touches
+ * the device; this re-reads it.  Results never depend on these (the
+ * reduction order is fixed by the row length), only the launch shape.  No
+ * counterpart in the reference.  Returns 0. */
+int kq_tuning_reload(void);
+
 /* ------------------------------------------- host-pointer entry points
  * x/y/add are host buffers, exactly as in the reference; each call copies
  * the activations in, runs the kernel and copies y back (synchronous). */

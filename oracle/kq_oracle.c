@@ -69,6 +69,20 @@ void ko_q4k_scale_min(int j, const uint8_t* s, uint8_t* sc, uint8_t* m) {
     }
 }
 
+/* Test sweep (no reference counterpart): ko_q4k_scale_min for sub-block j
+ * on every value of the nidx bytes idx[] of the 12 scale bytes (the others
+ * fixed to bg[]), combination c = sum_i byte_i << (8 i); out[2c] = sc,
+ * out[2c + 1] = m.  2^(8 nidx) combinations, nidx <= 3. */
+void ko_q4k_scale_min_sweep(int j, const int* idx, int nidx, const uint8_t* bg, uint8_t* out) {
+    uint8_t s[12];
+    memcpy(s, bg, 12);
+    const uint32_t n = 1u << (8 * nidx);
+    for (uint32_t c = 0; c < n; c++) {
+        for (int i = 0; i < nidx; i++) s[idx[i]] = (uint8_t)(c >> (8 * i));
+        ko_q4k_scale_min(j, s, &out[2 * (size_t)c], &out[2 * (size_t)c + 1]);
+    }
+}
+
 /* ---------------------------------------------------------------- Q4_K */
 /* block_q4_K (stratum_q4k.h:16-22): d@0, dmin@2, scales[12]@4, qs[128]@16.
  * Sub-block s (32 weights, positions 32s..32s+31) reads qs bytes

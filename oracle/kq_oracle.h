@@ -54,6 +54,10 @@ int ko_block_bytes(int type);
 
 float ko_fp16_to_fp32(uint16_t h);
 void ko_q4k_scale_min(int j, const uint8_t* scales, uint8_t* sc, uint8_t* m);
+/* ko_q4k_scale_min over every value of the bytes idx[0..nidx) (nidx <= 3),
+ * the other scale bytes fixed to bg[12]: out[2c], out[2c+1] = sc, m of
+ * combination c = sum_i byte_i << 8i (an exhaustive-test helper) */
+void ko_q4k_scale_min_sweep(int j, const int* idx, int nidx, const uint8_t* bg, uint8_t* out);
 
 /* one row of K weights (K % 256 == 0) */
 void ko_dequant_row(int type, const uint8_t* row, int K, float* y);

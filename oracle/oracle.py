@@ -54,6 +54,8 @@ class Port:
         L.ko_fp16_to_fp32.argtypes = [ctypes.c_uint16]
         L.ko_fp16_to_fp32.restype = ctypes.c_float
         L.ko_q4k_scale_min.argtypes = [I, _U8, _U8, _U8]
+        L.ko_q4k_scale_min_sweep.argtypes = [I, ctypes.POINTER(I), I, _U8, _U8]
+        L.ko_q4k_scale_min_sweep.restype = None
         L.ko_dequant_row.argtypes = [I, _U8, I, _F]
         L.ko_dot_row.argtypes = [I, _U8, I, _F]
         L.ko_dot_row.restype = ctypes.c_float
@@ -120,6 +122,17 @@ class Port:
         return list(sel), selw
 
 
+def scale_min_sweep(fn, j: int, idx, bg: np.ndarray) -> np.ndarray:
+    """(sc, m) of sub-block j for every value of the scale bytes idx (the
+    rest fixed to bg), through fn = ko_q4k_scale_min_sweep or its reference
+    twin: array [256^len(idx), 2]."""
+    n = 1 << (8 * len(idx))
+    out = np.empty(2 * n, np.uint8)
+    ia = (ctypes.c_int * len(idx))(*idx)
+    fn(j, ia, len(idx), _u8(np.ascontiguousarray(bg, np.uint8)), _u8(out))
+    return out.reshape(n, 2)
+
+
 class Ref:
     """The reference's own scalar routines (oracle/_ref/libkqref.so)."""
 
@@ -129,6 +142,8 @@ class Ref:
         L.kqref_fp16_to_fp32.argtypes = [ctypes.c_uint16]
         L.kqref_fp16_to_fp32.restype = ctypes.c_float
         L.kqref_scale_min.argtypes = [I, _U8, _U8, _U8]
+        L.kqref_scale_min_sweep.argtypes = [I, ctypes.POINTER(I), I, _U8, _U8]
+        L.kqref_scale_min_sweep.restype = None
         L.kqref_dequant_row.argtypes = [I, _U8, I, _F]
         L.kqref_dot_row.argtypes = [I, _U8, I, _F]
         L.kqref_dot_row.restype = ctypes.c_float

@@ -32,6 +32,19 @@ void kqref_scale_min(int j, const uint8_t* s, uint8_t* sc, uint8_t* m) {
     q4k_get_scale_min(j, s, sc, m);
 }
 
+/* q4k_get_scale_min for sub-block j over every value of the bytes idx[]
+ * (the same enumeration as ko_q4k_scale_min_sweep, for an exhaustive
+ * comparison) */
+void kqref_scale_min_sweep(int j, const int* idx, int nidx, const uint8_t* bg, uint8_t* out) {
+    uint8_t s[12];
+    memcpy(s, bg, 12);
+    const uint32_t n = 1u << (8 * nidx);
+    for (uint32_t c = 0; c < n; c++) {
+        for (int i = 0; i < nidx; i++) s[idx[i]] = (uint8_t)(c >> (8 * i));
+        q4k_get_scale_min(j, s, &out[2 * (size_t)c], &out[2 * (size_t)c + 1]);
+    }
+}
+
 int kqref_block_bytes(int type) {
     return type == 12 ? (int)sizeof(block_q4_K)
          : type == 14 ? (int)sizeof(block_q6_K)

@@ -43,6 +43,7 @@ EXPORTS = (
     "kq_dequant_dev", "kq_row_bytes", "kq_moe_slice_bytes", "kq_moe_bind_slice",
     "kq_moe_pack_open", "kq_moe_pack_which", "kq_moe_topk", "kq_moe_topk_dev",
     "kq_moe_gemv_dev", "kq_gemv_multix_mfma_dev", "kq_moe_gemv_routed_dev",
+    "kq_tuning_reload",
 )
 
 MAX_SEGMENTS = 8
@@ -181,6 +182,7 @@ def lib() -> ctypes.CDLL:
     L.kq_linear_shutdown.argtypes = []
     L.kq_linear_shutdown.restype = None
     L.kq_last_error.restype = ctypes.c_char_p
+    L.kq_tuning_reload.argtypes = []
     L.kq_linear_dispatch.argtypes = [TP, F, F, I, I]
     L.kq_linear_dispatch_add.argtypes = [TP, F, F, F, I, I]
     L.kq_linear_multix.argtypes = [TP, FPP, FPP, I, I, I]
@@ -207,6 +209,11 @@ def lib() -> ctypes.CDLL:
     L.kq_moe_gemv_routed_dev.argtypes = [ctypes.POINTER(KqMoeOp), P, I, I, I, P, P, P]
     _LIB = L
     return L
+
+
+def reload_tuning() -> None:
+    """Re-read the KQ_* launch-shape overrides (kq_tuning_reload)."""
+    lib().kq_tuning_reload()
 
 
 def _fptr(a: np.ndarray):

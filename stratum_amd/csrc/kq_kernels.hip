@@ -888,20 +888,26 @@ __device__ __forceinline__ uint32_t div_magic(uint32_t n, uint32_t m, int l) {
     return (t + ((n - t) >> 1)) >> (l - 1);
 }
 
-// What the LDS x region currently holds: x (pointer, K, groups, layout),
+// What the LDS x region currently holds: x (pointer, K, groups, the
+// stride between the groups' x, layout),
 // which type's per-group sums are in the xs region (0: none), the scale
 // exponent of the staged values (0 or KSC) and whether some x fell outside
 // the scaled-mode window.
 struct Staged {
     const float* x;
-    int K, layout, ngx, sums, k;
+    int K, layout, ngx, xst, sums, k;
     bool bad;
 };
 
-// LDS scratch: per-segment batch counters, per-wave flags, part tables
+// LDS scratch: per-segment batch counters, per-wave flags, part tables,
+// and the experts chosen when a segment is routed in the launch (kept here
+// rather than beside the routing's work arrays in the terms region: the
+// part tables read them after the routing's last barrier, and a segment
+// that reuses the staged x has no barrier before its sweep writes terms)
 constexpr int SCR_FLAGS = 4 * MAXSEG;
 constexpr int SCR_TABS = SCR_FLAGS + 4 * 16;
-constexpr int SCR_BYTES = SCR_TABS + 3 * 8 * MAXG;
+constexpr int SCR_RSEL = SCR_TABS + 3 * 8 * MAXG;
+constexpr int SCR_BYTES = SCR_RSEL + 8 * MAXG;
 
 // Part layout of a segment: one part; up to 4 parts of any sizes (a merged
 // same-input group: the part of a row by comparing with the part starts,
@@ -1039,14 +1045,15 @@ __device__ __forceinline__ void lds_barrier() {
 // eligible); slots without an expert stay -1.  Lane (p, e) counts the
 // experts of part p (of P) that beat e.  pv holds w[tid] (lanes tid < E64,
 // -1 past E), loaded by the caller ahead of its other loads; where E64 > T
-// the lanes load the rest here.  Scratch: ROUTE_BYTES of LDS.  Only LDS
-// barriers: global loads the caller issued stay in flight.
-constexpr int ROUTE_BYTES = 1024 * 4 + 1024 * 4 + MAXG * 8 + 16;
-__device__ void wg_topk(const float* w, float pv, int E, int k, int T, uint8_t* scratch) {
+// the lanes load the rest here.  Work arrays: ROUTE_BYTES of LDS at
+// scratch, free again on return; the result goes to rsel / rselw (MAXG
+// entries each, elsewhere in LDS).  Only LDS barriers: global loads the
+// caller issued stay in flight.
+constexpr int ROUTE_BYTES = 1024 * 4 + 1024 * 4;
+__device__ void wg_topk(const float* w, float pv, int E, int k, int T, uint8_t* scratch,
+                        int* rsel, float* rselw) {
     float* wl = reinterpret_cast<float*>(scratch);
     int* part = reinterpret_cast<int*>(scratch + 4096);
-    int* rsel = reinterpret_cast<int*>(scratch + 8192);
-    float* rselw = reinterpret_cast<float*>(scratch + 8192 + MAXG * 4);
     const int tid = threadIdx.x, E64 = (E + 63) & ~63;
     int P = 1;
     while (2 * P * E64 <= T && (E64 / (2 * P)) % 4 == 0) P *= 2;
@@ -1114,7 +1121,9 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
     // segment can read a scaled x, an SC type restages an unscaled one
     // unless the window already failed for it.
     constexpr bool SCTYPE = TYPE != T_Q6K;
-    const bool same_x = st.x == S.x && st.K == K && st.layout == (int)TI::LINEAR && st.ngx == ngx;
+    const int xst = ngx > 1 ? S.x_stride : 0;
+    const bool same_x = st.x == S.x && st.K == K && st.layout == (int)TI::LINEAR && st.ngx == ngx &&
+                        st.xst == xst;
     const bool restage = !same_x || (SCTYPE && st.k == 0 && !st.bad);
     constexpr int G4 = XGroup<TYPE>::G4;
     const XStage<TYPE> xg = {S.x, S.x_stride, K / (4 * G4), ngx * (K / (4 * G4)), NC};
@@ -1155,12 +1164,15 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
 
     const int* rsel = nullptr;
     if (PM == PM_SEL && route) {
-        uint8_t* scr = smem + A.terms_off;    // the terms are written only later
-        wg_topk(S.probs, pv, S.emax, S.ksel, T, scr);
-        rsel = reinterpret_cast<const int*>(scr + 8192);
+        // work arrays in the terms region (written only by the sweep, after
+        // the routing's last barrier); the result in the scratch region
+        int* rs = reinterpret_cast<int*>(smem + A.scr_off + SCR_RSEL);
+        float* rw = reinterpret_cast<float*>(rs + MAXG);
+        wg_topk(S.probs, pv, S.emax, S.ksel, T, smem + A.terms_off, rs, rw);
+        rsel = rs;
         if (b == 0 && tid < S.ksel) {
-            S.sel_out[tid] = rsel[tid];
-            S.selw_out[tid] = reinterpret_cast<const float*>(scr + 8192 + MAXG * 4)[tid];
+            S.sel_out[tid] = rs[tid];
+            S.selw_out[tid] = rw[tid];
         }
     }
     if (PM >= PM_EQUAL) {
@@ -1208,7 +1220,7 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
         __syncthreads();
         int any = 0;
         for (int i = 0; i < (T >> 6); i++) any |= flags[i];
-        st.x = S.x; st.K = K; st.layout = (int)TI::LINEAR; st.ngx = ngx;
+        st.x = S.x; st.K = K; st.layout = (int)TI::LINEAR; st.ngx = ngx; st.xst = xst;
         st.sums = TI::XS_PER_CHUNK ? TYPE : 0;
         st.k = SCTYPE ? KSC : 0;
         st.bad = SCTYPE && any;
@@ -1306,7 +1318,7 @@ __global__ __launch_bounds__(1024) void kq_segs_kernel(SegsArg A) {
     // x, and its barrier orders these writes before any batch is taken)
     if (threadIdx.x < (unsigned)nseg)
         reinterpret_cast<int*>(smem + A.scr_off)[threadIdx.x] = 64 * DEPTH * (A.threads >> 6);
-    Staged st = {nullptr, 0, -1, 0, 0, 0, false};
+    Staged st = {nullptr, 0, -1, 0, 0, 0, 0, false};
     // a single-type instantiation does not read the segment types (the host
     // launches it only for segment lists of that type)
     constexpr bool SELK = (TYPES & TB_SEL) != 0;    // MoE gather: every segment has sel

@@ -47,6 +47,9 @@ typedef struct {
     float* d_a; size_t cap_a;
     float* d_moe; size_t cap_moe;   /* MoE expert groups + their count */
     uint8_t* d_mf; size_t cap_mf;   /* MFMA multi-x: x planes, sums, partials */
+    /* launch overrides from the environment (0: unset), read by kq_ready
+     * and again only by kq_tuning_reload: the planner runs on every call */
+    int env_grid, env_threads, env_depth, env_moe_group_launch;
     char err[512];
 } kq_state;
 
@@ -84,8 +87,23 @@ static int hip_ok(hipError_t e, const char* what) {
     return kq_fail("%s: %s", what, hipGetErrorString(e));
 }
 
+static int env_int(const char* name) {
+    const char* e = getenv(name);
+    return e ? atoi(e) : 0;
+}
+
+int kq_tuning_reload(void) {
+    const int t = env_int("KQ_WG_THREADS"), d = env_int("KQ_DEPTH");
+    g_kq.env_grid = env_int("KQ_GRID") > 0 ? env_int("KQ_GRID") : 0;
+    g_kq.env_threads = t == 256 || t == 512 || t == 1024 ? t : 0;
+    g_kq.env_depth = getenv("KQ_DEPTH") ? (d == 2 ? 2 : 1) : 0;
+    g_kq.env_moe_group_launch = getenv("KQ_MOE_GROUP_LAUNCH") != NULL;
+    return 0;
+}
+
 static int kq_ready(void) {
     if (g_kq.ready) return 0;
+    kq_tuning_reload();
     int dev = 0, n = 0;
     if (hip_ok(hipGetDeviceCount(&n), "hipGetDeviceCount")) return -1;
     if (n < 1) return kq_fail("no HIP device");
@@ -204,9 +222,7 @@ static const void* tensor_dev(const kq_tensor* w, int N, int K) {
  * per CU when their LDS fits: twice the waves per CU, and two prologues
  * and tails that overlap (measured 9.7 -> 8.7 us for Q/K/V). */
 static int plan_grid(void) {
-    const char* e = getenv("KQ_GRID");
-    int g = e && atoi(e) > 0 ? atoi(e) : g_kq.n_cu;
-    return g;
+    return g_kq.env_grid > 0 ? g_kq.env_grid : g_kq.n_cu;
 }
 
 static long max_share(const kqk_seg* segs, int nseg, int grid) {
@@ -221,18 +237,13 @@ static long max_share(const kqk_seg* segs, int nseg, int grid) {
 }
 
 static int plan_threads(const kqk_seg* segs, int nseg, int grid) {
-    const char* e = getenv("KQ_WG_THREADS");
-    if (e) {
-        const int t = atoi(e);
-        if (t == 256 || t == 512 || t == 1024) return t;
-    }
+    if (g_kq.env_threads) return g_kq.env_threads;
     const long chunks = max_share(segs, nseg, grid);
     return chunks >= 4096 ? 1024 : chunks >= 1024 ? 512 : 256;
 }
 
 static int plan_depth(int threads) {
-    const char* e = getenv("KQ_DEPTH");
-    if (e) return atoi(e) == 2 ? 2 : 1;
+    if (g_kq.env_depth) return g_kq.env_depth;
     return threads < 1024 ? 2 : 1;
 }
 
@@ -245,7 +256,7 @@ static int launch_segs(const kqk_seg* segs, int nseg, hipStream_t st) {
             return kq_fail("segment %d has %ld rows (at most 2^24 - 1 per launch): split the rows",
                            i, n);
     }
-    if (!getenv("KQ_GRID") && !getenv("KQ_WG_THREADS") && !getenv("KQ_DEPTH") &&
+    if (!g_kq.env_grid && !g_kq.env_threads && !g_kq.env_depth &&
         max_share(segs, nseg, grid) >= 2048 && threads == 512) {
         int a = 0, b = 0, c = 0;
         const long lds2 = kqk_segs_lds(segs, nseg, 2 * grid, &a, &b, &c);
@@ -775,7 +786,7 @@ static int moe_batch(const kq_moe_op* op, int* sel, const float* probs, float* s
     int plan[KQK_MX_PLAN];
     const int moe[4] = {B, k, E, nt};
     const long rbytes = kqk_moe_runs_lds(nm, E, dmax + nm, probs ? B : 0);
-    if (!getenv("KQ_MOE_GROUP_LAUNCH") && rbytes + 16 < g_kq.lds_max / 2) {
+    if (!g_kq.env_moe_group_launch && rbytes + 16 < g_kq.lds_max / 2) {
         const long pl = mx_plan(op->type, op->n_out, op->k_in, mmax, nt * dmax, grid, moe,
                                 g_kq.lds_max - (int)rbytes - 16, plan);
         if (pl >= 0) {

@@ -15,6 +15,22 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs through the C ABI on the GPU)")
 
 
+@pytest.fixture
+def kq_env(monkeypatch):
+    """Sets KQ_* launch-shape overrides for one test: the library reads them
+    once, so each change is followed by kq_tuning_reload, and the previous
+    environment is restored and re-read when the test ends."""
+    import stratum_amd as K
+
+    def set_env(**kv):
+        for k, v in kv.items():
+            monkeypatch.setenv(k, str(v))
+        K.reload_tuning()
+    yield set_env
+    monkeypatch.undo()
+    K.reload_tuning()
+
+
 @pytest.fixture(scope="session")
 def port():
     from oracle import oracle as O

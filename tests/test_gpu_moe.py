@@ -261,13 +261,13 @@ def test_moe_routed_batch(port, qtype, B, E, k, case):
 @pytest.mark.parametrize("grouping", ["in_launch", "group_launch"])
 @pytest.mark.parametrize("qtype", [12, 14, 10])
 @pytest.mark.parametrize("B,n_exp", [(16, 32), (16, 128), (3, 8), (64, 16)])
-def test_moe_batch_grouped(port, qtype, B, n_exp, grouping, monkeypatch):
+def test_moe_batch_grouped(port, qtype, B, n_exp, grouping, kq_env):
     """Batches whose tokens share experts: each selected slice is streamed
     once for all its tokens; every member still equals its single GEMV.
     The expert runs are built inside the multi-x launch, or (forced) by the
     separate grouping launch."""
     if grouping == "group_launch":
-        monkeypatch.setenv("KQ_MOE_GROUP_LAUNCH", "1")
+        kq_env(KQ_MOE_GROUP_LAUNCH=1)
     H, F, k = 512, 256, min(8, n_exp)
     gate, up = experts(qtype, n_exp, F, H, 11), experts(qtype, n_exp, F, H, 12)
     down = experts(qtype, n_exp, H, F, 13)
@@ -283,11 +283,11 @@ def test_moe_batch_grouped(port, qtype, B, n_exp, grouping, monkeypatch):
 
 
 @pytest.mark.parametrize("grouping", ["in_launch", "group_launch"])
-def test_moe_pack_layout_and_unselected_slots(port, grouping, monkeypatch):
+def test_moe_pack_layout_and_unselected_slots(port, grouping, kq_env):
     """Expert slices in a pack (gate|up|down per expert, stride = their sum),
     with some ranks unselected (sel -1): the selected ranks are exact."""
     if grouping == "group_launch":
-        monkeypatch.setenv("KQ_MOE_GROUP_LAUNCH", "1")
+        kq_env(KQ_MOE_GROUP_LAUNCH=1)
     qtype, n_exp, H, F, B, k = 12, 12, 512, 256, 6, 4
     rb_g = K.lib().kq_row_bytes(qtype, H)
     rb_d = K.lib().kq_row_bytes(qtype, F)
@@ -343,3 +343,29 @@ def test_moe_config_routed_on_device(port, B):
             ws = w[e * sl:(e + 1) * sl]
             assert same_values(got[t][m], single(qtype, ws, xm, F, H)), (t, m)
             assert O.rel_err(got[t][m], port.gemv(qtype, ws, xm, F, H)).max() <= 1e-5
+
+
+@pytest.mark.parametrize("B", [1, 16])
+def test_moe_config_full_layer_routed(port, B):
+    """The MoE configuration as bench.py runs it: kq_moe_gemv_routed_dev for
+    gate+up (top-k of the router weights inside the launch for B = 1, a
+    top-k launch first for B = 16), then the down op (2048 x 768 per slice)
+    through kq_moe_gemv_dev on the sel it wrote.  Every member of gate, up
+    and down equals its own single-slice GEMV bit for bit; at least 4
+    members per tensor are checked against the oracle; sel equals the
+    oracle's moe_topk."""
+    qtype, n_exp, H, F, k = 12, 128, 2048, 768, 8
+    gate, up = experts(qtype, n_exp, F, H, 41), experts(qtype, n_exp, F, H, 42)
+    down = experts(qtype, n_exp, H, F, 43)
+    r = np.random.default_rng(44 + B)
+    probs = softmax_rows(r.standard_normal((B, n_exp)).astype(np.float32))
+    x = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
+    got, sel, selw = run_routed(qtype, [gate, up], probs, x, k, k, F, H)
+    for s_ in range(B):
+        ws, ww = port.topk(probs[s_], k)
+        assert list(sel[s_ * k:(s_ + 1) * k]) == ws, s_
+        assert same_values(selw[s_ * k:(s_ + 1) * k], ww), s_
+    check_members(port, qtype, [gate, up], sel, x, k, got, F, H, n_oracle=8)
+    act = np.stack([synth.gaussian(r, F) for _ in range(B * k)]).reshape(-1)
+    dn = run_moe(qtype, [down], sel.reshape(B, k), act, 1, B, k, n_exp, H, F)
+    check_members(port, qtype, [down], sel, act, 1, dn, H, F, n_oracle=4)

@@ -142,18 +142,26 @@ def test_gemv_add_epilogue(port, qtype):
     w = synth.tensor(qtype, N, Kd, 5)
     x = synth.gaussian(synth.rng(6), Kd)
     add = synth.gaussian(synth.rng(7), N)
-    check_close(gpu_gemv(qtype, w, x, N, Kd, add=add),
-                port.gemv(qtype, w, x, N, Kd, add=add), f"add {qtype}")
+    got = gpu_gemv(qtype, w, x, N, Kd, add=add)
+    check_close(got, port.gemv(qtype, w, x, N, Kd, add=add), f"add {qtype}")
+    # the add is one binary32 addition to the row's rounded result
+    # (y[r] = add[r] + dot, stratum_linear.h:566-600)
+    assert same_values(got, add + gpu_gemv(qtype, w, x, N, Kd))
 
 
 @pytest.mark.parametrize("qtype,N,Kd", [(12, 17408, 5120), (14, 5120, 17408), (12, 6144, 5120),
                                         (12, 8192, 5120), (14, 8191, 5120), (42, 17408, 5120),
-                                        (10, 17408, 5120)])
-def test_gemv_27b_shape_sampled(port, qtype, N, Kd, monkeypatch):
-    """27B-class shapes: 384 sampled rows against the oracle, bit-identical
-    reruns, and the same bits under a different row decomposition.  8192 x
-    5120 (the merged Q/K/V row count) and 8191 x 5120 (ragged: workgroups
-    with 15 and 16 rows) run two workgroups per CU."""
+                                        (10, 17408, 5120), (14, 151936, 1024), (12, 5120, 6144),
+                                        (12, 1024, 5120)])
+def test_gemv_27b_shape_sampled(port, qtype, N, Kd, kq_env):
+    """Full-size config shapes: 384 sampled rows against the oracle,
+    bit-identical reruns, and the same bits under a different row
+    decomposition (37 workgroups of 256 lanes).  27B-class: gate/up, down,
+    Q, the merged Q/K/V row count 8192 and a ragged 8191 (two workgroups per
+    CU), type 42 and Q2_K gate, O (5120 x 6144) and K/V (1024 x 5120) alone;
+    Qwen3-0.6B: the Q6_K LM head 151936 x 1024 (594 rows per workgroup, and
+    several launches under the 37-workgroup decomposition, whose terms would
+    not fit one launch's LDS)."""
     w = synth.tensor(qtype, N, Kd, 31)
     x = synth.gaussian(synth.rng(32), Kd)
     print(f"27b shape type={qtype} N={N} K={Kd}", flush=True)
@@ -162,8 +170,7 @@ def test_gemv_27b_shape_sampled(port, qtype, N, Kd, monkeypatch):
                                      [0, 1, N - 2, N - 1]]))
     check_close(y[rows], port.gemv_rows(qtype, w, x, rows, Kd), f"27b {qtype} {N}x{Kd}")
     assert same_values(gpu_gemv(qtype, w, x, N, Kd), y)
-    monkeypatch.setenv("KQ_GRID", "37")
-    monkeypatch.setenv("KQ_WG_THREADS", "256")
+    kq_env(KQ_GRID=37, KQ_WG_THREADS=256)
     assert same_values(gpu_gemv(qtype, w, x, N, Kd), y)
 
 
@@ -277,6 +284,29 @@ def test_segments_groups_expert_slices(port):
                     f"down e{e}")
 
 
+def test_segments_same_x_other_stride(port):
+    """Two multi-group segments on the same x pointer, K and group count but
+    different x strides: the second must restage its own x rows, not reuse
+    the first segment's (each output equals its own launch)."""
+    H, F, G = 512, 256, 3
+    xs = np.stack([synth.gaussian(synth.rng(640 + g), 2 * H) for g in range(G)]).reshape(-1)
+    dx = dev(xs)
+    ws = [[synth.tensor(12, F, H, 650 + 10 * i + g) for g in range(G)] for i in range(2)]
+    dws = [[dev(w) for w in row] for row in ws]
+    ys = [torch.empty(G * F, dtype=torch.float32, device="cuda") for _ in range(2)]
+    strides = [H, 2 * H]                  # rows g*H (overlapping) and g*2H of the same buffer
+    segs = [K.segment(12, H, F, [d.data_ptr() for d in dws[i]], dx.data_ptr(), ys[i].data_ptr(),
+                      x_stride=strides[i]) for i in range(2)]
+    K.gemv_segments_dev(segs, stream=stream())
+    torch.cuda.synchronize()
+    for i in range(2):
+        got = ys[i].cpu().numpy().reshape(G, F)
+        for g in range(G):
+            xg = xs[g * strides[i]:g * strides[i] + H]
+            assert same_values(got[g], gpu_gemv(12, ws[i][g], xg, F, H)), (i, g)
+            check_close(got[g], port.gemv(12, ws[i][g], xg, F, H), f"stride {strides[i]} g{g}")
+
+
 def test_segments_rejects_bad_input():
     bad = K.segment(12, 1000, 16, [0], 0, 0)
     with pytest.raises(RuntimeError):
@@ -331,13 +361,13 @@ def test_gemv_x_all_below_window(port, qtype, scale):
 @pytest.mark.parametrize("where", [None, 5000, 9000])
 @pytest.mark.parametrize("Kd", [6144, 12288])
 @pytest.mark.parametrize("qtype", [14, 10, 42])
-def test_gemv_x_staging_rounds(port, qtype, Kd, where, monkeypatch):
+def test_gemv_x_staging_rounds(port, qtype, Kd, where, kq_env):
     """x longer than one staging round of the workgroup (256 lanes: 4096
     values per round for 16-value groups): two rounds (the second loaded
     with the first) and three, with an out-of-window x value in the second
     or third round (it must still switch every workgroup to the unscaled
     path)."""
-    monkeypatch.setenv("KQ_WG_THREADS", "256")
+    kq_env(KQ_WG_THREADS=256)
     N = 96
     w = synth.tensor(qtype, N, Kd, 540 + qtype)
     x = synth.gaussian(synth.rng(541), Kd)

@@ -57,26 +57,45 @@ def test_q4k_scale_pack_roundtrip_exhaustive(port):
                 sc[:, k] = (7 * k + 3) % 64
                 m[:, k] = (11 * k + 5) % 64
         packed = synth.pack_q4k_scales(sc, m)
-        for i in range(0, sc_all.size, 97):
+        for i in range(sc_all.size):
             row = np.ascontiguousarray(packed[i])
             port.L.ko_q4k_scale_min(j, O._u8(row), ctypes.byref(out_sc), ctypes.byref(out_m))
             assert (out_sc.value, out_m.value) == (sc[i, j], m[i, j])
 
 
-def test_q4k_scale_decode_matches_reference_exhaustive(port, ref):
-    """All 2^24 values of the three bytes a high sub-block reads, and all
-    2^16 of the two bytes a low sub-block reads, for every j."""
-    import ctypes
-    a, b = ctypes.c_uint8(), ctypes.c_uint8()
-    c, d = ctypes.c_uint8(), ctypes.c_uint8()
-    rng = np.random.default_rng(1)
-    s = np.zeros(12, np.uint8)
-    for j in range(8):
-        for trial in range(4000):
-            s[:] = rng.integers(0, 256, 12, dtype=np.uint8)
-            port.L.ko_q4k_scale_min(j, O._u8(s), ctypes.byref(a), ctypes.byref(b))
-            ref.L.kqref_scale_min(j, O._u8(s), ctypes.byref(c), ctypes.byref(d))
-            assert (a.value, b.value) == (c.value, d.value)
+def scale_bytes_read(j):
+    """The scale bytes q4k_get_scale_min reads for sub-block j
+    (stratum_q4k.h:57-65): j < 4 reads bytes j and j + 4; j >= 4 reads
+    j + 4, j - 4 and j."""
+    return [j, j + 4] if j < 4 else [j + 4, j - 4, j]
+
+
+@pytest.mark.parametrize("j", range(8))
+def test_q4k_scale_decode_matches_reference_exhaustive(port, ref, j):
+    """Every value of the bytes sub-block j reads (2^16 for j < 4, 2^24 for
+    j >= 4), with the other nine or ten bytes fixed to zeros, to ones, and
+    to a random pattern: the oracle equals the reference's own decode on
+    all of them, and the result does not depend on the other bytes."""
+    idx = scale_bytes_read(j)
+    first = None
+    for bg in (np.zeros(12, np.uint8), np.full(12, 0xff, np.uint8),
+               np.random.default_rng(j).integers(0, 256, 12).astype(np.uint8)):
+        got = O.scale_min_sweep(port.L.ko_q4k_scale_min_sweep, j, idx, bg)
+        want = O.scale_min_sweep(ref.L.kqref_scale_min_sweep, j, idx, bg)
+        assert np.array_equal(got, want), j
+        if first is None:
+            first = got
+        assert np.array_equal(got, first), j
+    # closed form of the decode on the first byte combinations: the 6-bit
+    # fields, and for j >= 4 the nibble plus the top bits of bytes j-4 / j
+    c = np.arange(first.shape[0], dtype=np.int64)
+    b = [(c >> (8 * i)) & 0xff for i in range(len(idx))]
+    if j < 4:
+        sc, m = b[0] & 63, b[1] & 63
+    else:
+        sc = (b[0] & 15) | ((b[1] >> 6) << 4)
+        m = (b[0] >> 4) | ((b[2] >> 6) << 4)
+    assert np.array_equal(first[:, 0], sc) and np.array_equal(first[:, 1], m), j
 
 
 # ------------------------------------------------------- golden fixtures
@@ -99,6 +118,30 @@ def test_oracle_matches_reference_random(port, ref, qtype, K):
         x = synth.gaussian(synth.rng(100 + seed), K)
         assert same_values(port.dequant(qtype, w, N, K), ref.dequant(qtype, w, N, K))
         assert same_values(port.gemv(qtype, w, x, N, K), ref.gemv(qtype, w, x, N, K))
+
+
+@pytest.mark.parametrize("qtype", [12, 14, 10])
+def test_oracle_add_is_one_binary32_add_after_the_row(port, ref, qtype):
+    """st_linear_dispatch_add computes y[r] = add[r] + dot, the row's
+    result rounded to binary32 first and then one binary32 addition
+    (stratum_linear.h:566-600).  The oracle's add path must equal the
+    reference's plain GEMV plus a numpy float32 add bit for bit; adding
+    before the final rounding (in binary64) would differ on these inputs."""
+    N, K = 257, 1024
+    w = synth.tensor(qtype, N, K, 61)
+    x = synth.gaussian(synth.rng(62), K)
+    r = np.random.default_rng(63)
+    # adds of every magnitude relative to the row results, so that the
+    # rounding of the sum differs between the two orders on many rows
+    add = (synth.gaussian(r, N) * np.float32(2.0) ** r.integers(-30, 30, N)).astype(np.float32)
+    got = port.gemv(qtype, w, x, N, K, add=add)
+    want = add + ref.gemv(qtype, w, x, N, K)
+    assert same_values(got, want)
+    # the other order (binary64 sum, rounded once) gives different bits
+    fused = np.array([np.float32(np.float64(a) + port.L.ko_dot_row_f64(
+        qtype, O._u8(np.ascontiguousarray(w[i * (w.size // N):(i + 1) * (w.size // N)])), K,
+        O._f(x))) for i, a in enumerate(add)], np.float32)
+    assert not same_values(fused, want)
 
 
 def test_oracle_threads_do_not_change_results(port):
