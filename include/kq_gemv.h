@@ -144,6 +144,21 @@ int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,
 int kq_gemv_multix_mfma_dev(int type, const void* w, const float* xs, float* ys,
                             int B, int N, int K, kq_stream stream);
 
+/* kq_gemv_multix_mfma_dev without any allocation: the same kernels and the
+ * same results bit for bit, with the workspace (x planes, x sums, K-part
+ * partial sums) in a static device array of KQ_NOALLOC_SCRATCH_BYTES that
+ * each GPU holds for the life of the process.  No counterpart in the
+ * reference; it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, allocation-free serving loops).  Calls no
+ * hipMalloc/hipFree and creates no stream; returns -1 with a message when
+ * the workspace of (type, B, N, K) exceeds the array (the 27B MULTISEQ
+ * shapes up to B = 64 fit).  Every call on one GPU shares that GPU's array:
+ * calls that overlap in time on one GPU race (calls on one stream are
+ * ordered). */
+#define KQ_NOALLOC_SCRATCH_BYTES (32L << 20)
+int kq_gemv_multix_mfma_noalloc_dev(int type, const void* w, const float* xs, float* ys,
+                                    int B, int N, int K, kq_stream stream);
+
 /* One segment of a batched launch: ngroups * rows_per_group rows of one
  * type and row length K.  Rows [g*rows_per_group, (g+1)*rows_per_group)
  * start at device address w[g] (separate bases: e.g. the selected MoE

@@ -43,8 +43,10 @@ EXPORTS = (
     "kq_dequant_dev", "kq_row_bytes", "kq_moe_slice_bytes", "kq_moe_bind_slice",
     "kq_moe_pack_open", "kq_moe_pack_which", "kq_moe_topk", "kq_moe_topk_dev",
     "kq_moe_gemv_dev", "kq_gemv_multix_mfma_dev", "kq_moe_gemv_routed_dev",
-    "kq_tuning_reload",
+    "kq_tuning_reload", "kq_gemv_multix_mfma_noalloc_dev",
 )
+
+NOALLOC_SCRATCH_BYTES = 32 << 20   # KQ_NOALLOC_SCRATCH_BYTES
 
 MAX_SEGMENTS = 8
 MAX_GROUPS = 16
@@ -190,6 +192,7 @@ def lib() -> ctypes.CDLL:
     L.kq_gemv_dev.argtypes = [I, P, P, P, P, I, I, P]
     L.kq_gemv_multix_dev.argtypes = [I, P, P, P, I, I, I, P]
     L.kq_gemv_multix_mfma_dev.argtypes = [I, P, P, P, I, I, I, P]
+    L.kq_gemv_multix_mfma_noalloc_dev.argtypes = [I, P, P, P, I, I, I, P]
     L.kq_dequant_dev.argtypes = [I, P, P, ctypes.c_int64, P]
     L.kq_gemv_segments_dev.argtypes = [ctypes.POINTER(KqSegment), I, P]
     L.kq_row_bytes.argtypes = [I, I]

@@ -1046,14 +1046,14 @@ __device__ __forceinline__ void lds_barrier() {
 // experts of part p (of P) that beat e.  pv holds w[tid] (lanes tid < E64,
 // -1 past E), loaded by the caller ahead of its other loads; where E64 > T
 // the lanes load the rest here.  Work arrays: ROUTE_BYTES of LDS at
-// scratch, free again on return; the result goes to rsel / rselw (MAXG
+// work, free again on return; the result goes to rsel / rselw (MAXG
 // entries each, elsewhere in LDS).  Only LDS barriers: global loads the
 // caller issued stay in flight.
 constexpr int ROUTE_BYTES = 1024 * 4 + 1024 * 4;
-__device__ void wg_topk(const float* w, float pv, int E, int k, int T, uint8_t* scratch,
+__device__ void wg_topk(const float* w, float pv, int E, int k, int T, uint8_t* work,
                         int* rsel, float* rselw) {
-    float* wl = reinterpret_cast<float*>(scratch);
-    int* part = reinterpret_cast<int*>(scratch + 4096);
+    float* wl = reinterpret_cast<float*>(work);
+    int* part = reinterpret_cast<int*>(work + 4096);
     const int tid = threadIdx.x, E64 = (E + 63) & ~63;
     int P = 1;
     while (2 * P * E64 <= T && (E64 / (2 * P)) % 4 == 0) P *= 2;
@@ -2533,8 +2533,43 @@ int launch_dequant(const uint8_t* w, float* y, long nblocks, hipStream_t st) {
 
 }  // namespace
 
+// ------------------------------------------------------ static scratch
+// Device memory for the entry point that allocates nothing
+// (kq_gemv_multix_mfma_noalloc_dev): its workspace -- x planes, x sums and
+// K-part partials -- lives in this array instead of a library allocation.
+// Every GPU the library runs on holds its own copy, at its own address,
+// until the process ends.  Host code never passes `scratch` itself (in host
+// code the name is a host-side stand-in, not a device address): it uses the
+// address hipGetSymbolAddress returns for the current device, looked up
+// once per device and kept in scratch_dev[].  Calls that overlap on one GPU
+// share the array and race; every byte a launch reads is written by that
+// launch first, so nothing needs clearing between calls.
+static __device__ __align__(256) uint8_t scratch[KQK_NOALLOC_BYTES];
+
+namespace {
+constexpr int SCRATCH_MAX_DEVICES = 64;
+void* scratch_dev[SCRATCH_MAX_DEVICES];
+}  // namespace
+
 // ------------------------------------------------------------ C launchers
 extern "C" {
+
+int kqk_noalloc_scratch(void** ptr, long* bytes) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= SCRATCH_MAX_DEVICES) return (int)hipErrorInvalidDevice;
+    if (!scratch_dev[dev]) {                  // first use on this device (it is current)
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        if (!p) return (int)hipErrorInvalidSymbol;
+        scratch_dev[dev] = p;
+    }
+    *ptr = scratch_dev[dev];
+    *bytes = (long)KQK_NOALLOC_BYTES;
+    return 0;
+}
 
 // Host view of one segment (plain C layout, mirrored in kq_linear.c):
 // nparts parts, part p = rows [start[p], start[p] + rows[p]) at w[p],

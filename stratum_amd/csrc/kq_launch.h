@@ -60,6 +60,11 @@ int kqk_launch_mx_moe(int type, const int* plan, long plan_lds, long lds, int gr
                       int B, int k, int* sel_out, float* selw_out, hipStream_t st);
 /* MFMA multi-x (Q4_K, Q6_K): workspace sizes, and the launch */
 int kqk_mfma_workspace(int type, int B, int N, int K, long* planes, long* xs, long* part);
+/* Bytes of the library's static device scratch (the public limit). */
+#define KQK_NOALLOC_BYTES KQ_NOALLOC_SCRATCH_BYTES
+/* Device address (on the current device) and size of the library's static
+ * scratch array; the address is looked up once per device and cached. */
+int kqk_noalloc_scratch(void** ptr, long* bytes);
 int kqk_launch_mfma(int type, const float* x, const void* w, float* y, int B, int N, int K,
                     void* planes, float* xs, float* part, int grid, hipStream_t st);
 int kqk_launch_moe_group(const int* sel, int nm, int E, int nt, int x_div, int mch,

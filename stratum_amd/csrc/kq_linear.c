@@ -37,7 +37,9 @@ typedef struct {
     int device;
     int n_cu;
     int lds_max;           /* bytes of LDS one workgroup may use */
-    hipStream_t stream;    /* library stream (default priority) */
+    hipStream_t stream;    /* library stream of the host-pointer ABI (default
+                            * priority), created at its first use */
+    int stream_ready;
     kq_region reg[KQ_MAX_REGIONS];
     int nreg;
     const uint8_t* base;   /* kq_linear_init base: offsets resolve here */
@@ -113,14 +115,29 @@ static int kq_ready(void) {
                "hipDeviceGetAttribute(CU count)")) return -1;
     if (hip_ok(hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev),
                "hipDeviceGetAttribute(LDS)")) return -1;
-    /* blocking stream, default priority: orders with the null stream */
-    if (hip_ok(hipStreamCreate(&g_kq.stream), "hipStreamCreate")) return -1;
     g_kq.device = dev;
     g_kq.n_cu = ncu > 0 ? ncu : 1;
     g_kq.lds_max = lds > 0 ? lds : 65536;
     if (kqk_set_max_lds(g_kq.lds_max) != 0 || kqk_mx_set_max_lds(g_kq.lds_max) != 0)
         return kq_fail("cannot raise the LDS limit");
+    /* the static scratch of the no-allocation entry point: its address on
+     * this device, looked up once now (other devices at their first call) */
+    void* scr = NULL;
+    long scr_bytes = 0;
+    const int e = kqk_noalloc_scratch(&scr, &scr_bytes);
+    if (e) return kq_fail("static scratch: %s", hipGetErrorString((hipError_t)e));
     g_kq.ready = 1;
+    return 0;
+}
+
+/* The library's own stream, used only by the host-pointer entry points
+ * (created at their first call: the device-pointer entry points create
+ * nothing).  A blocking stream at the default priority, so it orders with
+ * the null stream. */
+static int host_stream(void) {
+    if (g_kq.stream_ready) return 0;
+    if (hip_ok(hipStreamCreate(&g_kq.stream), "hipStreamCreate")) return -1;
+    g_kq.stream_ready = 1;
     return 0;
 }
 
@@ -180,7 +197,7 @@ void kq_linear_shutdown(void) {
     if (g_kq.d_a) (void)hipFree(g_kq.d_a);
     if (g_kq.d_moe) (void)hipFree(g_kq.d_moe);
     if (g_kq.d_mf) (void)hipFree(g_kq.d_mf);
-    if (g_kq.ready && g_kq.stream) (void)hipStreamDestroy(g_kq.stream);
+    if (g_kq.stream_ready) (void)hipStreamDestroy(g_kq.stream);
     memset(&g_kq, 0, sizeof g_kq);
 }
 
@@ -477,19 +494,44 @@ int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,
  * sub-block's inner product runs as bf16 MFMAs over an exact three-plane
  * split of x, so results differ from the single-stream ones by about one
  * binary32 ulp of each sub-block sum (not bit for bit). */
+/* Checks an MFMA multi-x call and lays out its workspace (x planes, x
+ * sums, K-part partials, each 256-byte aligned): *o_xs, *o_pt are the
+ * offsets of the second and third parts, the return value the bytes
+ * needed, or 0 after a failure (message set). */
+static size_t mfma_prepare(const char* who, int type, const void* w, const float* xs, float* ys,
+                           int B, int N, int K, size_t* o_xs, size_t* o_pt) {
+    if (type != KQ_TYPE_Q4_K && type != KQ_TYPE_Q6_K) {
+        kq_fail("%s: type %d has no MFMA path", who, type);
+        return 0;
+    }
+    if (B < 1) { kq_fail("%s: B=%d", who, B); return 0; }
+    if (check_shape(type, N, K) || kq_ready()) return 0;
+    if (!w || !xs || !ys) { kq_fail("%s: NULL pointer", who); return 0; }
+    long pl, xsb, pt;
+    if (kqk_mfma_workspace(type, B, N, K, &pl, &xsb, &pt)) {
+        kq_fail("%s: bad shape", who);
+        return 0;
+    }
+    const size_t a = 256;
+    *o_xs = (pl + a - 1) / a * a;
+    *o_pt = *o_xs + (xsb + a - 1) / a * a;
+    return *o_pt + (size_t)pt;
+}
+
+static int mfma_launch(int type, const void* w, const float* xs, float* ys, int B, int N, int K,
+                       uint8_t* ws, size_t o_xs, size_t o_pt, kq_stream stream) {
+    const int e = kqk_launch_mfma(type, xs, w, ys, B, N, K, ws, (float*)(ws + o_xs),
+                                  (float*)(ws + o_pt), 2 * g_kq.n_cu, pick(stream));
+    if (e) return kq_fail("mfma multix launch: %s", hipGetErrorString((hipError_t)e));
+    return 0;
+}
+
 int kq_gemv_multix_mfma_dev(int type, const void* w, const float* xs, float* ys,
                             int B, int N, int K, kq_stream stream) {
-    if (type != KQ_TYPE_Q4_K && type != KQ_TYPE_Q6_K)
-        return kq_fail("kq_gemv_multix_mfma_dev: type %d has no MFMA path", type);
-    if (B < 1) return kq_fail("kq_gemv_multix_mfma_dev: B=%d", B);
-    if (check_shape(type, N, K) || kq_ready()) return -1;
-    if (!w || !xs || !ys) return kq_fail("kq_gemv_multix_mfma_dev: NULL pointer");
-    long pl, xsb, pt;
-    if (kqk_mfma_workspace(type, B, N, K, &pl, &xsb, &pt))
-        return kq_fail("kq_gemv_multix_mfma_dev: bad shape");
-    const size_t a = 256;
-    const size_t o_xs = (pl + a - 1) / a * a, o_pt = o_xs + (xsb + a - 1) / a * a,
-                 need = o_pt + (size_t)pt;
+    size_t o_xs, o_pt;
+    const size_t need = mfma_prepare("kq_gemv_multix_mfma_dev", type, w, xs, ys, B, N, K,
+                                     &o_xs, &o_pt);
+    if (!need) return -1;
     if (g_kq.cap_mf < need) {
         if (g_kq.d_mf) (void)hipFree(g_kq.d_mf);
         g_kq.d_mf = NULL;
@@ -497,12 +539,27 @@ int kq_gemv_multix_mfma_dev(int type, const void* w, const float* xs, float* ys,
         if (hip_ok(hipMalloc((void**)&g_kq.d_mf, need), "hipMalloc(mfma workspace)")) return -1;
         g_kq.cap_mf = need;
     }
-    uint8_t* ws = g_kq.d_mf;
-    const int e = kqk_launch_mfma(type, xs, w, ys, B, N, K, ws, (float*)(ws + o_xs),
-                                  (float*)(ws + o_pt), 2 * g_kq.n_cu,
-                                  pick(stream));
-    if (e) return kq_fail("mfma multix launch: %s", hipGetErrorString((hipError_t)e));
-    return 0;
+    return mfma_launch(type, w, xs, ys, B, N, K, g_kq.d_mf, o_xs, o_pt, stream);
+}
+
+/* The same launch with its workspace in the library's static device
+ * scratch (kqk_noalloc_scratch): no allocation at all, for callers that
+ * cannot allocate (graph capture, allocation-free serving loops). */
+int kq_gemv_multix_mfma_noalloc_dev(int type, const void* w, const float* xs, float* ys,
+                                    int B, int N, int K, kq_stream stream) {
+    size_t o_xs, o_pt;
+    const size_t need = mfma_prepare("kq_gemv_multix_mfma_noalloc_dev", type, w, xs, ys, B, N, K,
+                                     &o_xs, &o_pt);
+    if (!need) return -1;
+    void* scr = NULL;
+    long cap = 0;
+    const int e = kqk_noalloc_scratch(&scr, &cap);
+    if (e) return kq_fail("static scratch: %s", hipGetErrorString((hipError_t)e));
+    if (need > (size_t)cap)
+        return kq_fail("kq_gemv_multix_mfma_noalloc_dev: B=%d N=%d K=%d needs %zu bytes of "
+                       "scratch, more than the static %ld (KQ_NOALLOC_SCRATCH_BYTES)",
+                       B, N, K, need, cap);
+    return mfma_launch(type, w, xs, ys, B, N, K, (uint8_t*)scr, o_xs, o_pt, stream);
 }
 
 int kq_dequant_dev(int type, const void* w, float* y, int64_t nblocks, kq_stream stream) {
@@ -530,7 +587,7 @@ static int finish_y(float* y, const float* d_y, size_t n) {
 int kq_linear_dispatch_add(const kq_tensor* w, const float* x, const float* add,
                            float* y, int N, int K) {
     if (!w) return kq_fail("NULL tensor");
-    if (check_shape((int)w->type, N, K) || kq_ready()) return -1;
+    if (check_shape((int)w->type, N, K) || kq_ready() || host_stream()) return -1;
     const void* dw = tensor_dev(w, N, K);
     if (!dw) return -1;
     if (grow(&g_kq.d_x, &g_kq.cap_x, (size_t)K) || grow(&g_kq.d_y, &g_kq.cap_y, (size_t)N))
@@ -553,7 +610,7 @@ int kq_linear_multix(const kq_tensor* w, const float* const* xs, float* const* y
                      int B, int N, int K) {
     if (!w) return kq_fail("NULL tensor");
     if (B < 1) return kq_fail("kq_linear_multix: B=%d", B);
-    if (check_shape((int)w->type, N, K) || kq_ready()) return -1;
+    if (check_shape((int)w->type, N, K) || kq_ready() || host_stream()) return -1;
     const void* dw = tensor_dev(w, N, K);
     if (!dw) return -1;
     if (grow(&g_kq.d_x, &g_kq.cap_x, (size_t)B * K) ||
@@ -576,7 +633,7 @@ int kq_q4k_group(const float* x, int K,
     float* ys[3] = {y0, y1, y2};
     const int Ns[3] = {N0, N1, N2};
     const int nw = w2 ? 3 : 2;
-    if (kq_ready()) return -1;
+    if (kq_ready() || host_stream()) return -1;
     size_t ytot = 0;
     kq_segment sg[3];
     memset(sg, 0, sizeof sg);
