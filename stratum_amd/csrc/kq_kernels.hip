@@ -1256,8 +1256,18 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
     for (int task = tid; task < R * GP; task += T) {
         const int rho = task >> lgp, p = task & (GP - 1);
         const double* tr = terms + rho * NC;
+        // four terms are read ahead of their additions (one LDS round trip
+        // per four adds, not per add); the adds stay in order
         double s = 0.0;
-        for (int i = p; i < NC; i += GP) s = s + tr[i];
+        int i = p;
+        for (; i + 3 * GP < NC; i += 4 * GP) {
+            const double t0 = tr[i], t1 = tr[i + GP], t2 = tr[i + 2 * GP], t3 = tr[i + 3 * GP];
+            s = s + t0;
+            s = s + t1;
+            s = s + t2;
+            s = s + t3;
+        }
+        for (; i < NC; i += GP) s = s + tr[i];
         s = phase_tree(s, GP);
         if (p == 0) {
             uint32_t rg;
