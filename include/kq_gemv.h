@@ -11,10 +11,14 @@
  *
  * Numerics: every GEMV entry point computes, per row, the reference scalar
  * routine's binary32 sub-block arithmetic (stratum_q4k.h:95-131,
- * stratum_q6k.h:38-73, stratum_q2k.h:44-89) with the sub-block terms summed
+ * stratum_q6k.h:38-73, stratum_q2k.h:44-89, stratum_q5k.h:44-82,
+ * stratum_q3k.h:58-99, stratum_q8_0.h:19-33) with the sub-block terms summed
  * in binary64; outputs match the scalar routine bit for bit except where a
  * binary64 re-association crosses a binary32 rounding boundary (at most
- * one ulp).  Dequantization is bit-exact.
+ * one ulp).  F16 and F32 rows are the binary64 sum of exact products,
+ * rounded once (st_linear_f16 sums in element order; F32 goes to
+ * cblas_sgemv in the reference, stratum_linear.h:491-512).  Dequantization
+ * is bit-exact.
  *
  * Threading: like the reference (single caller, non-reentrant global
  * state, stratum_linear.h:239-242), one host thread drives the library.
@@ -29,11 +33,19 @@
 extern "C" {
 #endif
 
-/* GGML type ids the GEMV accepts (stratum_gguf.h:20-49).  Any other type
- * makes the dispatch return -1, as st_linear_dispatch does for types it
- * has no kernel for (stratum_linear.h:553-556). */
+/* GGML type ids the GEMV accepts (stratum_gguf.h:20-49): every type of
+ * st_linear_dispatch's switch (stratum_linear.h:533-541) except the Apple
+ * W16 repacks (43, 44), plus type 42.  Any other type makes the dispatch
+ * return -1, as st_linear_dispatch does for types it has no kernel for
+ * (stratum_linear.h:553-556).  K must be a multiple of 256 for every type
+ * (Q8_0 rows then hold K/32 blocks of 34 bytes). */
+#define KQ_TYPE_F32     0
+#define KQ_TYPE_F16     1
+#define KQ_TYPE_Q8_0    8
 #define KQ_TYPE_Q2_K    10
+#define KQ_TYPE_Q3_K    11
 #define KQ_TYPE_Q4_K    12
+#define KQ_TYPE_Q5_K    13
 #define KQ_TYPE_Q6_K    14
 #define KQ_TYPE_Q2K_NIB 42
 

@@ -19,10 +19,15 @@
 #include <string.h>
 
 int ko_block_bytes(int type) {
-    switch (type) {   /* stratum_gguf.h:57-79 */
+    switch (type) {   /* stratum_gguf.h:57-79, per 256 weights */
     case KO_Q2_K: return 84;
+    case KO_Q3_K: return 110;
     case KO_Q4_K: return 144;
+    case KO_Q5_K: return 176;
     case KO_Q6_K: return 210;
+    case KO_Q8_0: return 8 * 34;     /* eight 32-weight blocks */
+    case KO_F16: return 512;
+    case KO_F32: return 1024;
     case KO_Q2K_NIB: return 148;
     default: return 0;
     }
@@ -240,6 +245,168 @@ static double q2_dot(const uint8_t* row, int K, const float* x, int nib) {
     return dot;
 }
 
+/* ---------------------------------------------------------------- Q5_K */
+/* block_q5_K (stratum_q5k.h:9-16): d@0, dmin@2, scales[12]@4 (Q4_K's
+ * 6-bit packing), qh[32]@16, qs[128]@48.  Chunk j (64 weights at 64j):
+ * sub-block 2j takes the low nibbles of qs[32j + l] plus 16 when bit 2j of
+ * qh[l] is set; sub-block 2j+1 the high nibbles plus bit 2j+1. */
+static inline int q5k_q(const uint8_t* blk, int s, int l) {
+    const int j = s >> 1;
+    const uint8_t b = blk[48 + 32 * j + l];
+    const int lo = (s & 1) ? (b >> 4) : (b & 0x0f);
+    return lo + ((blk[16 + l] >> s) & 1) * 16;
+}
+
+static void q5k_dequant_block(const uint8_t* blk, float* y) {
+    /* stratum_q5k.h:18-42: y = fl(fl(d*sc)*q) - fl(dmin*m) */
+    const float d = ko_fp16_to_fp32(rd16(blk));
+    const float dmin = ko_fp16_to_fp32(rd16(blk + 2));
+    for (int s = 0; s < 8; s++) {
+        uint8_t sc, m;
+        ko_q4k_scale_min(s, blk + 4, &sc, &m);
+        const float ds = d * (float)sc;
+        const float dm = dmin * (float)m;
+        for (int l = 0; l < 32; l++) y[32 * s + l] = ds * (float)q5k_q(blk, s, l) - dm;
+    }
+}
+
+static double q5k_dot(const uint8_t* row, int K, const float* x) {
+    /* stratum_q5k.h:44-82: per 64-weight chunk, one binary32 expression
+     * ((d1*qx1 - m1*sx1) + d2*qx2) - m2*sx2, then widened and added */
+    double dot = 0.0;
+    for (int b = 0; b < K / 256; b++) {
+        const uint8_t* blk = row + (size_t)b * 176;
+        const float* xb = x + (size_t)b * 256;
+        const float d = ko_fp16_to_fp32(rd16(blk));
+        const float dmin = ko_fp16_to_fp32(rd16(blk + 2));
+        for (int j = 0; j < 4; j++) {
+            uint8_t sc1, mn1, sc2, mn2;
+            ko_q4k_scale_min(2 * j, blk + 4, &sc1, &mn1);
+            ko_q4k_scale_min(2 * j + 1, blk + 4, &sc2, &mn2);
+            const float d1 = d * (float)sc1, m1 = dmin * (float)mn1;
+            const float d2 = d * (float)sc2, m2 = dmin * (float)mn2;
+            float qx1 = 0.0f, sx1 = 0.0f, qx2 = 0.0f, sx2 = 0.0f;
+            for (int l = 0; l < 32; l++) {
+                qx1 += (float)q5k_q(blk, 2 * j, l) * xb[64 * j + l];
+                sx1 += xb[64 * j + l];
+            }
+            for (int l = 0; l < 32; l++) {
+                qx2 += (float)q5k_q(blk, 2 * j + 1, l) * xb[64 * j + 32 + l];
+                sx2 += xb[64 * j + 32 + l];
+            }
+            dot += (double)(d1 * qx1 - m1 * sx1 + d2 * qx2 - m2 * sx2);
+        }
+    }
+    return dot;
+}
+
+/* ---------------------------------------------------------------- Q3_K */
+/* block_q3_K (stratum_q3k.h:8-14): hmask[32]@0, qs[64]@32, scales[12]@96,
+ * d@108.  Group g = 8s + 2j + h (16 weights at 128s + 32j + 16h + l):
+ * low two bits (qs[32s + 16h + l] >> 2j) & 3, minus 4 unless bit 4s + j
+ * of hmask[16h + l] is set.  Scale g is 6 bits: the low nibble from byte
+ * g%4 (g < 4, 8 <= g < 12: low nibble; otherwise high nibble) of bytes
+ * 0..7, the top two bits from byte 8 + g%4 (stratum_q3k.h:17-28). */
+static inline int q3k_scale(const uint8_t* sc12, int g) {
+    const int w = g >> 2, bi = g & 3;
+    const uint8_t lo = w == 0 ? (sc12[bi] & 0x0f) : w == 1 ? (sc12[4 + bi] & 0x0f)
+                     : w == 2 ? (sc12[bi] >> 4) : (sc12[4 + bi] >> 4);
+    const uint8_t hi = (sc12[8 + bi] >> (2 * w)) & 3;
+    return (int)(lo | (hi << 4));
+}
+
+/* Test sweep (no reference counterpart): q3k_scale for group g on every
+ * value of the nidx bytes idx[] of the 12 scale bytes (the others fixed to
+ * bg[]); out[c] = the 6-bit scale of combination c = sum_i byte_i << 8i. */
+void ko_q3k_scale_sweep(int g, const int* idx, int nidx, const uint8_t* bg, uint8_t* out) {
+    uint8_t s[12];
+    memcpy(s, bg, 12);
+    const uint32_t n = 1u << (8 * nidx);
+    for (uint32_t c = 0; c < n; c++) {
+        for (int i = 0; i < nidx; i++) s[idx[i]] = (uint8_t)(c >> (8 * i));
+        out[c] = (uint8_t)q3k_scale(s, g);
+    }
+}
+
+static inline int q3k_q(const uint8_t* blk, int g, int l) {
+    const int s = g >> 3, j = (g >> 1) & 3, h = g & 1;
+    const int lo = (blk[32 + 32 * s + 16 * h + l] >> (2 * j)) & 3;
+    const int hb = (blk[16 * h + l] >> (4 * s + j)) & 1;
+    return lo - (hb ? 0 : 4);
+}
+
+static void q3k_dequant_block(const uint8_t* blk, float* y) {
+    /* stratum_q3k.h:30-56: y = fl(fl(d*(sc-32))*q) */
+    const float d = ko_fp16_to_fp32(rd16(blk + 108));
+    for (int g = 0; g < 16; g++) {
+        const float dl = d * (float)(q3k_scale(blk + 96, g) - 32);
+        for (int l = 0; l < 16; l++) y[q2_pos(g, l)] = dl * (float)q3k_q(blk, g, l);
+    }
+}
+
+static double q3k_dot(const uint8_t* row, int K, const float* x) {
+    /* stratum_q3k.h:58-99, groups in (s, j, h) order:
+     * dot += (double)fl(dl * acc), acc the binary32 sum of 16 products */
+    double dot = 0.0;
+    for (int b = 0; b < K / 256; b++) {
+        const uint8_t* blk = row + (size_t)b * 110;
+        const float* xb = x + (size_t)b * 256;
+        const float d = ko_fp16_to_fp32(rd16(blk + 108));
+        for (int g = 0; g < 16; g++) {
+            const float dl = d * (float)(q3k_scale(blk + 96, g) - 32);
+            float acc = 0.0f;
+            for (int l = 0; l < 16; l++) acc += (float)q3k_q(blk, g, l) * xb[q2_pos(g, l)];
+            dot += (double)(dl * acc);
+        }
+    }
+    return dot;
+}
+
+/* ---------------------------------------------------------------- Q8_0 */
+/* block_q8_0 (stratum_q8_0.h:8-12): d@0, int8 qs[32]@2, 34 bytes per 32
+ * weights. */
+static void q8_0_dequant_block(const uint8_t* blk, float* y) {
+    /* stratum_q8_0.h:14-17 */
+    const float d = ko_fp16_to_fp32(rd16(blk));
+    for (int k = 0; k < 32; k++) y[k] = d * (float)(int8_t)blk[2 + k];
+}
+
+static double q8_0_dot(const uint8_t* row, int K, const float* x) {
+    /* stratum_q8_0.h:19-33: dot += (double)fl(d * acc) per 32 weights */
+    double dot = 0.0;
+    for (int b = 0; b < K / 32; b++) {
+        const uint8_t* blk = row + (size_t)b * 34;
+        const float d = ko_fp16_to_fp32(rd16(blk));
+        float acc = 0.0f;
+        for (int k = 0; k < 32; k++) acc += (float)(int8_t)blk[2 + k] * x[32 * b + k];
+        dot += (double)(d * acc);
+    }
+    return dot;
+}
+
+/* ----------------------------------------------------------- F16 / F32 */
+static double f16_dot(const uint8_t* row, int K, const float* x) {
+    /* stratum_linear.h:491-505 (st_linear_f16): every product exact in
+     * binary64, summed in binary64 in element order */
+    double acc = 0.0;
+    for (int c = 0; c < K; c++) acc += (double)ko_fp16_to_fp32(rd16(row + 2 * c)) * (double)x[c];
+    return acc;
+}
+
+static double f32_dot(const uint8_t* row, int K, const float* x) {
+    /* stratum_linear.h:508-512 hands F32 to cblas_sgemv, whose summation
+     * order is the BLAS library's.  Restated as the binary64 sum of the
+     * exact products in element order: the value every ordering
+     * approximates, within K binary32 roundings of sum |w x|. */
+    double acc = 0.0;
+    for (int c = 0; c < K; c++) {
+        float w;
+        memcpy(&w, row + 4 * (size_t)c, 4);
+        acc += (double)w * (double)x[c];
+    }
+    return acc;
+}
+
 /* ------------------------------------------------------------ dispatch */
 void ko_dequant_row(int type, const uint8_t* row, int K, float* y) {
     const int bb = ko_block_bytes(type);
@@ -251,6 +418,15 @@ void ko_dequant_row(int type, const uint8_t* row, int K, float* y) {
         case KO_Q6_K: q6k_dequant_block(blk, yb); break;
         case KO_Q2_K: q2_dequant_block(blk, 0, yb); break;
         case KO_Q2K_NIB: q2_dequant_block(blk, 1, yb); break;
+        case KO_Q5_K: q5k_dequant_block(blk, yb); break;
+        case KO_Q3_K: q3k_dequant_block(blk, yb); break;
+        case KO_Q8_0:
+            for (int q = 0; q < 8; q++) q8_0_dequant_block(blk + 34 * q, yb + 32 * q);
+            break;
+        case KO_F16:
+            for (int k = 0; k < 256; k++) yb[k] = ko_fp16_to_fp32(rd16(blk + 2 * k));
+            break;
+        case KO_F32: memcpy(yb, blk, 1024); break;
         default: return;
         }
     }
@@ -262,6 +438,11 @@ double ko_dot_row_f64(int type, const uint8_t* row, int K, const float* x) {
     case KO_Q6_K: return q6k_dot(row, K, x);
     case KO_Q2_K: return q2_dot(row, K, x, 0);
     case KO_Q2K_NIB: return q2_dot(row, K, x, 1);
+    case KO_Q5_K: return q5k_dot(row, K, x);
+    case KO_Q3_K: return q3k_dot(row, K, x);
+    case KO_Q8_0: return q8_0_dot(row, K, x);
+    case KO_F16: return f16_dot(row, K, x);
+    case KO_F32: return f32_dot(row, K, x);
     default: return 0.0;
     }
 }

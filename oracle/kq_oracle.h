@@ -18,6 +18,13 @@
  *   stratum_q6k.h:38-73   q6k_dot_row_scalar      -> ko_dot_row (Q6_K)
  *   stratum_q2k.h:16-42   q2k_dequant_block_scalar-> ko_dequant_row (Q2_K)
  *   stratum_q2k.h:44-89   q2k_dot_row_scalar      -> ko_dot_row (Q2_K)
+ *   stratum_q5k.h:18-82   q5k_dequant/dot_row_scalar -> ko_dequant_row / ko_dot_row (Q5_K)
+ *   stratum_q3k.h:17-99   q3k_unpack_scales, dequant/dot_row_scalar -> (Q3_K)
+ *   stratum_q8_0.h:14-33  q8_0_dequant/dot_row_scalar -> (Q8_0, eight blocks per 256)
+ *   stratum_linear.h:491-505 st_linear_f16 (binary64 element-order sum) -> (F16)
+ *   stratum_linear.h:508-512 st_linear_f32 (cblas_sgemv; restated as the
+ *                          binary64 sum of exact products: parity pinned
+ *                          by closed forms only, not against the BLAS bits)
  *   tools_gguf_nib_convert.c:99-120  Q2_K -> type 42 byte permutation
  *                                     -> ko_q2k_to_nib / ko_nib_to_q2k
  *   stratum_linear.h:201-228 ST_PAR_ROWS 64-row tickets -> ko_gemv threads
@@ -43,8 +50,13 @@ extern "C" {
 
 /* GGML type ids (stratum_gguf.h:20-49). */
 enum {
+    KO_F32 = 0,
+    KO_F16 = 1,
+    KO_Q8_0 = 8,
     KO_Q2_K = 10,
+    KO_Q3_K = 11,
     KO_Q4_K = 12,
+    KO_Q5_K = 13,
     KO_Q6_K = 14,
     KO_Q2K_NIB = 42,
 };
@@ -58,6 +70,10 @@ void ko_q4k_scale_min(int j, const uint8_t* scales, uint8_t* sc, uint8_t* m);
  * the other scale bytes fixed to bg[12]: out[2c], out[2c+1] = sc, m of
  * combination c = sum_i byte_i << 8i (an exhaustive-test helper) */
 void ko_q4k_scale_min_sweep(int j, const int* idx, int nidx, const uint8_t* bg, uint8_t* out);
+
+/* the Q3_K 6-bit scale of group g over every value of the bytes idx[]
+ * (nidx <= 3), others fixed to bg[12] (an exhaustive-test helper) */
+void ko_q3k_scale_sweep(int g, const int* idx, int nidx, const uint8_t* bg, uint8_t* out);
 
 /* one row of K weights (K % 256 == 0) */
 void ko_dequant_row(int type, const uint8_t* row, int K, float* y);

@@ -56,6 +56,8 @@ class Port:
         L.ko_q4k_scale_min.argtypes = [I, _U8, _U8, _U8]
         L.ko_q4k_scale_min_sweep.argtypes = [I, ctypes.POINTER(I), I, _U8, _U8]
         L.ko_q4k_scale_min_sweep.restype = None
+        L.ko_q3k_scale_sweep.argtypes = [I, ctypes.POINTER(I), I, _U8, _U8]
+        L.ko_q3k_scale_sweep.restype = None
         L.ko_dequant_row.argtypes = [I, _U8, I, _F]
         L.ko_dot_row.argtypes = [I, _U8, I, _F]
         L.ko_dot_row.restype = ctypes.c_float
@@ -89,7 +91,7 @@ class Port:
 
     def gemv_rows(self, qtype: int, w: np.ndarray, x: np.ndarray, rows, K: int) -> np.ndarray:
         """Oracle result for a subset of rows (large tensors)."""
-        rb = (K // 256) * {10: 84, 12: 144, 14: 210, 42: 148}[qtype]
+        rb = (K // 256) * BLOCK_BYTES[qtype]
         out = np.empty(len(rows), np.float32)
         for i, r in enumerate(rows):
             seg = w[r * rb:(r + 1) * rb]
@@ -133,6 +135,16 @@ def scale_min_sweep(fn, j: int, idx, bg: np.ndarray) -> np.ndarray:
     return out.reshape(n, 2)
 
 
+def q3k_scale_sweep(fn, g: int, idx, bg: np.ndarray) -> np.ndarray:
+    """The Q3_K scale of group g for every value of the scale bytes idx,
+    through fn = ko_q3k_scale_sweep or its reference twin."""
+    n = 1 << (8 * len(idx))
+    out = np.empty(n, np.uint8)
+    ia = (ctypes.c_int * len(idx))(*idx)
+    fn(g, ia, len(idx), _u8(np.ascontiguousarray(bg, np.uint8)), _u8(out))
+    return out
+
+
 class Ref:
     """The reference's own scalar routines (oracle/_ref/libkqref.so)."""
 
@@ -144,6 +156,8 @@ class Ref:
         L.kqref_scale_min.argtypes = [I, _U8, _U8, _U8]
         L.kqref_scale_min_sweep.argtypes = [I, ctypes.POINTER(I), I, _U8, _U8]
         L.kqref_scale_min_sweep.restype = None
+        L.kqref_q3k_scale_sweep.argtypes = [I, ctypes.POINTER(I), I, _U8, _U8]
+        L.kqref_q3k_scale_sweep.restype = None
         L.kqref_dequant_row.argtypes = [I, _U8, I, _F]
         L.kqref_dot_row.argtypes = [I, _U8, I, _F]
         L.kqref_dot_row.restype = ctypes.c_float
@@ -195,7 +209,8 @@ def ref() -> Ref | None:
 # Integer restatements of the expert-slice and pack addressing (pure
 # arithmetic, so plain Python).
 
-BLOCK_BYTES = {10: 84, 12: 144, 14: 210, 42: 148}
+# bytes per 256 weights (stratum_gguf.h:57-79)
+BLOCK_BYTES = {0: 1024, 1: 512, 8: 272, 10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 42: 148}
 
 
 def moe_slice_bytes(qtype: int, nelem: int, nbytes: int, K_in: int, N_out: int) -> int:

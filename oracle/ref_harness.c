@@ -13,6 +13,8 @@
  *   q4k_fp16_to_fp32, q4k_get_scale_min          (stratum_q4k.h:24-65)
  *   q{4,6,2}k_dequant_block_scalar               (stratum_q4k.h:67, q6k.h:17, q2k.h:16)
  *   q{4,6,2}k_dot_row_scalar                     (stratum_q4k.h:95, q6k.h:38, q2k.h:44)
+ *   q{3,5}k_dequant_block_scalar / _dot_row_scalar (stratum_q3k.h:30, 58; q5k.h:18, 44)
+ *   q8_0_dequant_block_scalar / _dot_row_scalar  (stratum_q8_0.h:14, 19)
  * plus a pthread row split with 64-row tickets, as ST_PAR_ROWS does
  * (stratum_linear.h:201-228) on a machine without NEON (stratum_linear.h:446-451).
  */
@@ -20,6 +22,9 @@
 #include "stratum_q4k.h"
 #include "stratum_q6k.h"
 #include "stratum_q2k.h"
+#include "stratum_q3k.h"
+#include "stratum_q5k.h"
+#include "stratum_q8_0.h"
 
 #include <pthread.h>
 #include <stdatomic.h>
@@ -45,10 +50,30 @@ void kqref_scale_min_sweep(int j, const int* idx, int nidx, const uint8_t* bg, u
     }
 }
 
+/* bytes per 256 weights (Q8_0: eight of its 32-weight blocks) */
+/* q3k_unpack_scales (stratum_q3k.h:17-28) group g over every value of the
+ * bytes idx[] (the same enumeration as ko_q3k_scale_sweep); the unpacked
+ * int8 is stored as its byte */
+void kqref_q3k_scale_sweep(int g, const int* idx, int nidx, const uint8_t* bg, uint8_t* out) {
+    uint8_t s[12];
+    memcpy(s, bg, 12);
+    const uint32_t n = 1u << (8 * nidx);
+    for (uint32_t c = 0; c < n; c++) {
+        for (int i = 0; i < nidx; i++) s[idx[i]] = (uint8_t)(c >> (8 * i));
+        int8_t sc[16];
+        q3k_unpack_scales(s, sc);
+        out[c] = (uint8_t)sc[g];
+    }
+}
+
+/* bytes per 256 weights (Q8_0: eight of its 32-weight blocks) */
 int kqref_block_bytes(int type) {
     return type == 12 ? (int)sizeof(block_q4_K)
          : type == 14 ? (int)sizeof(block_q6_K)
-         : type == 10 ? (int)sizeof(block_q2_K) : 0;
+         : type == 10 ? (int)sizeof(block_q2_K)
+         : type == 11 ? (int)sizeof(block_q3_K)
+         : type == 13 ? (int)sizeof(block_q5_K)
+         : type == 8 ? 8 * (int)sizeof(block_q8_0) : 0;
 }
 
 int kqref_dequant_row(int type, const uint8_t* row, int K, float* y) {
@@ -57,6 +82,12 @@ int kqref_dequant_row(int type, const uint8_t* row, int K, float* y) {
         case 12: q4k_dequant_block_scalar((const block_q4_K*)row + b, y + 256 * b); break;
         case 14: q6k_dequant_block_scalar((const block_q6_K*)row + b, y + 256 * b); break;
         case 10: q2k_dequant_block_scalar((const block_q2_K*)row + b, y + 256 * b); break;
+        case 11: q3k_dequant_block_scalar((const block_q3_K*)row + b, y + 256 * b); break;
+        case 13: q5k_dequant_block_scalar((const block_q5_K*)row + b, y + 256 * b); break;
+        case 8:
+            for (int q = 0; q < 8; q++)
+                q8_0_dequant_block_scalar((const block_q8_0*)row + 8 * b + q, y + 256 * b + 32 * q);
+            break;
         default: return -1;
         }
     }
@@ -68,6 +99,9 @@ float kqref_dot_row(int type, const uint8_t* row, int K, const float* x) {
     case 12: return q4k_dot_row_scalar((const block_q4_K*)row, K, x);
     case 14: return q6k_dot_row_scalar((const block_q6_K*)row, K, x);
     case 10: return q2k_dot_row_scalar((const block_q2_K*)row, K, x);
+    case 11: return q3k_dot_row_scalar((const block_q3_K*)row, K, x);
+    case 13: return q5k_dot_row_scalar((const block_q5_K*)row, K, x);
+    case 8: return q8_0_dot_row_scalar((const block_q8_0*)row, K, x);
     default: return 0.0f;
     }
 }

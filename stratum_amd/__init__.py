@@ -24,13 +24,22 @@ import os
 
 import numpy as np
 
+TYPE_F32 = 0
+TYPE_F16 = 1
+TYPE_Q8_0 = 8
 TYPE_Q2_K = 10
+TYPE_Q3_K = 11
 TYPE_Q4_K = 12
+TYPE_Q5_K = 13
 TYPE_Q6_K = 14
 TYPE_Q2K_NIB = 42
 
-BLOCK_BYTES = {TYPE_Q2_K: 84, TYPE_Q4_K: 144, TYPE_Q6_K: 210, TYPE_Q2K_NIB: 148}
-TYPE_NAMES = {TYPE_Q2_K: "Q2_K", TYPE_Q4_K: "Q4_K", TYPE_Q6_K: "Q6_K", TYPE_Q2K_NIB: "Q2K_NIB"}
+# bytes per 256 weights (stratum_gguf.h:57-79; Q8_0: eight 34-byte blocks)
+BLOCK_BYTES = {TYPE_F32: 1024, TYPE_F16: 512, TYPE_Q8_0: 272, TYPE_Q2_K: 84, TYPE_Q3_K: 110,
+               TYPE_Q4_K: 144, TYPE_Q5_K: 176, TYPE_Q6_K: 210, TYPE_Q2K_NIB: 148}
+TYPE_NAMES = {TYPE_F32: "F32", TYPE_F16: "F16", TYPE_Q8_0: "Q8_0", TYPE_Q2_K: "Q2_K",
+              TYPE_Q3_K: "Q3_K", TYPE_Q4_K: "Q4_K", TYPE_Q5_K: "Q5_K", TYPE_Q6_K: "Q6_K",
+              TYPE_Q2K_NIB: "Q2K_NIB"}
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libkqgemv.so")

@@ -52,8 +52,11 @@
 
 namespace {
 
+constexpr int T_Q80 = 8;
 constexpr int T_Q2K = 10;
+constexpr int T_Q3K = 11;
 constexpr int T_Q4K = 12;
+constexpr int T_Q5K = 13;
 constexpr int T_Q6K = 14;
 constexpr int T_NIB = 42;
 
@@ -61,11 +64,19 @@ constexpr int XPAD = 17;  // float4 slots per 64-weight chunk in LDS (16 + 1 pad
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// BB: bytes per 256 weights; LINEAR: a chunk is 64 consecutive x values
+// (else 4 runs of 16, spaced 32 apart); XS_PER_CHUNK: x sums per chunk for
+// min terms; SCALED: products by the byte-select multiply on x staged as
+// x * 2^KSC (the other types read x as staged and fold the factor into
+// their scale).
 template <int TYPE> struct TypeInfo;
-template <> struct TypeInfo<T_Q4K> { static constexpr int BB = 144; static constexpr bool LINEAR = true;  static constexpr int XS_PER_CHUNK = 2; };
-template <> struct TypeInfo<T_Q6K> { static constexpr int BB = 210; static constexpr bool LINEAR = false; static constexpr int XS_PER_CHUNK = 0; };
-template <> struct TypeInfo<T_Q2K> { static constexpr int BB = 84;  static constexpr bool LINEAR = false; static constexpr int XS_PER_CHUNK = 4; };
-template <> struct TypeInfo<T_NIB> { static constexpr int BB = 148; static constexpr bool LINEAR = true;  static constexpr int XS_PER_CHUNK = 4; };
+template <> struct TypeInfo<T_Q4K> { static constexpr int BB = 144; static constexpr bool LINEAR = true;  static constexpr int XS_PER_CHUNK = 2; static constexpr bool SCALED = true; };
+template <> struct TypeInfo<T_Q6K> { static constexpr int BB = 210; static constexpr bool LINEAR = false; static constexpr int XS_PER_CHUNK = 0; static constexpr bool SCALED = false; };
+template <> struct TypeInfo<T_Q2K> { static constexpr int BB = 84;  static constexpr bool LINEAR = false; static constexpr int XS_PER_CHUNK = 4; static constexpr bool SCALED = true; };
+template <> struct TypeInfo<T_NIB> { static constexpr int BB = 148; static constexpr bool LINEAR = true;  static constexpr int XS_PER_CHUNK = 4; static constexpr bool SCALED = true; };
+template <> struct TypeInfo<T_Q5K> { static constexpr int BB = 176; static constexpr bool LINEAR = true;  static constexpr int XS_PER_CHUNK = 2; static constexpr bool SCALED = true; };
+template <> struct TypeInfo<T_Q3K> { static constexpr int BB = 110; static constexpr bool LINEAR = false; static constexpr int XS_PER_CHUNK = 0; static constexpr bool SCALED = false; };
+template <> struct TypeInfo<T_Q80> { static constexpr int BB = 272; static constexpr bool LINEAR = true;  static constexpr int XS_PER_CHUNK = 0; static constexpr bool SCALED = false; };
 
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
@@ -205,7 +216,8 @@ constexpr int KSC_ELO = 24 - KSC;
 constexpr uint32_t KSC_SPAN = 117 - 24;
 
 template <int TYPE> struct XGroup {
-    static constexpr int G4 = TYPE == T_Q4K ? 8 : 4;            // float4 per group
+    // float4 per group: 32 values for the types with 32-weight sub-blocks
+    static constexpr int G4 = (TYPE == T_Q4K || TYPE == T_Q5K || TYPE == T_Q80) ? 8 : 4;
     static constexpr bool SUMS = TypeInfo<TYPE>::XS_PER_CHUNK != 0;
 };
 
@@ -220,7 +232,7 @@ __device__ __forceinline__ uint32_t window_dist(float v) {
 // one x) of the group's sum.
 template <int TYPE>
 __device__ __forceinline__ void group_place(int gi, int& slot0, int& xsi) {
-    if (TYPE == T_Q4K) {               // sub-block gi: chunk gi/2, slots 8*(gi&1)..
+    if (XGroup<TYPE>::G4 == 8) {       // 32 values gi: chunk gi/2, slots 8*(gi&1)..
         slot0 = (gi >> 1) * XPAD + 8 * (gi & 1);
         xsi = gi;
     } else if (TYPE == T_NIB) {        // 16-group gi: chunk gi/4, slots 4*(gi&3)..
@@ -358,6 +370,9 @@ struct RawQ4 { uint4 hd, qa, qb; };
 struct RawQ6 { uint32_t l[5], h[5], q[5], s[3], d; uint32_t sh; };
 struct RawQ2 { uint4 q; uint2 s; uint32_t dd; };
 struct RawNB { uint4 qa, qb; uint32_t s, dd; };
+struct RawQ5 { uint4 hd, h0, h1, qa, qb; };
+struct RawQ3 { uint32_t q[5], m[5], s[4]; uint32_t d, sh; };
+struct RawQ8 { uint32_t w[17]; };
 
 __device__ __forceinline__ RawQ4 load_q4k(wptr blk, int j) {
     RawQ4 r;
@@ -400,6 +415,51 @@ __device__ __forceinline__ RawQ2 load_q2k(wptr blk, int u) {
     r.q = ld16a4(blk + 16 + 32 * s + 16 * h);
     r.s = ld8a4(blk + 8 * s);
     r.dd = ld4(blk + 80);
+    return r;
+}
+
+// Q5_K (176 B, 16-byte aligned): header (d, dmin, scales), all of qh, and
+// the 32 qs bytes of chunk j
+__device__ __forceinline__ RawQ5 load_q5k(wptr blk, int j) {
+    RawQ5 r;
+    r.hd = ld16(blk);
+    r.h0 = ld16(blk + 16);
+    r.h1 = ld16(blk + 32);
+    r.qa = ld16(blk + 48 + 32 * j);
+    r.qb = ld16(blk + 64 + 32 * j);
+    return r;
+}
+
+// Q3_K (110 B, blocks 2-byte aligned): chunk u = (s, h) reads 16 qs bytes
+// at 32 + 32s + 16h, 16 hmask bytes at 16h, the 12 scale bytes at 96 and d
+// at 108.  Dword-aligned loads realigned by v_alignbit; the fourth scale
+// dword is needed only when the block is 2 bytes off (else dword 2 is read
+// again), so the last block of a tensor is never read past its end.
+__device__ __forceinline__ RawQ3 load_q3k(wptr blk, int u) {
+    RawQ3 r;
+    const int s = u >> 1, h = u & 1;
+    const uint32_t mis = (uint32_t)reinterpret_cast<uintptr_t>(blk) & 3u;
+    r.sh = mis * 8u;
+    const wptr b4 = blk - mis;
+    load5(b4 + 32 + 32 * s + 16 * h, r.q);
+    load5(b4 + 16 * h, r.m);
+    r.s[0] = ld4(b4 + 96); r.s[1] = ld4(b4 + 100); r.s[2] = ld4(b4 + 104);
+    r.s[3] = ld4(b4 + (mis ? 108 : 104));
+    r.d = ld2(blk + 108);
+    return r;
+}
+
+// Q8_0: a 256-weight unit is eight 34-byte blocks (272 B, 16-byte aligned);
+// chunk u is blocks 2u, 2u+1: 68 bytes from the dword-aligned offset 68u
+__device__ __forceinline__ RawQ8 load_q80(wptr blk, int u) {
+    RawQ8 r;
+    const wptr p = blk + 68 * u;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint4 v = ld16a4(p + 16 * k);
+        r.w[4 * k] = v.x; r.w[4 * k + 1] = v.y; r.w[4 * k + 2] = v.z; r.w[4 * k + 3] = v.w;
+    }
+    r.w[16] = ld4(p + 64);
     return r;
 }
 
@@ -744,6 +804,137 @@ __device__ __forceinline__ double term_nib(const RawNB& r, const float4* xc, con
     return acc;
 }
 
+// Q4_K / Q5_K 6-bit scale and min of sub-blocks 2j, 2j+1 from the 12
+// scale bytes in words s0..s2 (stratum_q4k.h:57-65)
+__device__ __forceinline__ void scale_min_pair(uint32_t s0, uint32_t s1, uint32_t s2, int j,
+                                               uint32_t& sc1, uint32_t& m1, uint32_t& sc2,
+                                               uint32_t& m2) {
+    const bool lo = j < 2;
+    const uint32_t ob = (uint32_t)((2 * j) & 3) * 8u;
+    const uint32_t a_sc = lo ? s0 : s2;
+    const uint32_t a_m = lo ? s1 : s2;
+    const uint32_t w6 = lo ? 6u : 4u;
+    const uint32_t om = lo ? 0u : 4u;
+    const uint32_t wh = lo ? 0u : 2u;
+    sc1 = bfe(a_sc, ob, w6) | (bfe(s0, ob + 6, wh) << 4);
+    m1 = bfe(a_m, ob + om, w6) | (bfe(s1, ob + 6, wh) << 4);
+    sc2 = bfe(a_sc, ob + 8, w6) | (bfe(s0, ob + 14, wh) << 4);
+    m2 = bfe(a_m, ob + 8 + om, w6) | (bfe(s1, ob + 14, wh) << 4);
+}
+
+// Q5_K chunk j (stratum_q5k.h:44-82): sub-blocks 2j and 2j+1 with the
+// fifth bit from qh bits 2j / 2j+1; the chunk's term is ONE binary32
+// expression ((d1*qx1 - m1*sx1) + d2*qx2) - m2*sx2.  Bytes hold q (0..31),
+// so the scaled byte-select products apply as for Q4_K.
+template <bool SC>
+__device__ __forceinline__ double term_q5k(const RawQ5& r, int j, const float4* xc, float xs1,
+                                           float xs2, float f) {
+    const float d = f16_bits_to_f32(r.hd.x & 0xffffu);
+    const float dmin = f16_bits_to_f32(r.hd.x >> 16);
+    uint32_t sc1, mn1, sc2, mn2;
+    scale_min_pair(r.hd.y, r.hd.z, r.hd.w, j, sc1, mn1, sc2, mn2);
+    const float d1 = d * (float)sc1, m1 = dmin * (float)mn1;
+    const float d2 = d * (float)sc2, m2 = dmin * (float)mn2;
+    const uint32_t b1 = 2u * (uint32_t)j;
+    float a1 = 0.0f, a2 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const uint32_t v = k < 4 ? dw_of(r.qa, k) : dw_of(r.qb, k - 4);
+        const uint32_t h = k < 4 ? dw_of(r.h0, k) : dw_of(r.h1, k - 4);
+        const uint32_t vl = (v & 0x0f0f0f0fu) | (((h >> b1) & 0x01010101u) << 4);
+        const uint32_t vh = ((v >> 4) & 0x0f0f0f0fu) | (((h >> (b1 + 1)) & 0x01010101u) << 4);
+        float l0, l1, l2, l3, h0, h1, h2, h3;
+        bmul4<SC>(vl, xc + k, l0, l1, l2, l3);
+        bmul4<SC>(vh, xc + 8 + k, h0, h1, h2, h3);
+        a1 = a1 + l0; a2 = a2 + h0;
+        a1 = a1 + l1; a2 = a2 + h1;
+        a1 = a1 + l2; a2 = a2 + h2;
+        a1 = a1 + l3; a2 = a2 + h3;
+        // fence every two steps: without it the x reads of all eight are
+        // hoisted and, with qh held too, the kernel spills at 128 VGPRs
+        if (k & 1) {
+            asm volatile("" : "+v"(a1), "+v"(a2));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    const float d1s = SC ? d1 * f : d1;
+    const float d2s = SC ? d2 * f : d2;
+    const float t = ((d1s * a1 - m1 * xs1) + d2s * a2) - m2 * xs2;
+    return (double)t;
+}
+
+// Q3_K chunk u = (s, h): groups j = 0..3 of 16 weights at 128s + 32j + 16h
+// (stratum_q3k.h:58-99).  q3 = ((qs >> 2j) & 3) - 4 unless bit 4s + j of
+// hmask is set; each byte is built as the int8 32*q3 (the three bits of the
+// two's-complement q3 in bits 5..7) and converted exactly, so every partial
+// sum is 32x the reference's; that factor and the staging scale 2^k are
+// folded into the group's scale (fk = 2^-k).
+__device__ __forceinline__ double term_q3k(const RawQ3& r, int u, const float4* xc, double fk) {
+    const int s = u >> 1, h = u & 1;
+    const uint32_t sh = r.sh;
+    const float d = f16_bits_to_f32(r.d);
+    const float fs = (float)(fk * 0.03125);
+    const uint32_t S0 = __builtin_amdgcn_alignbit(r.s[1], r.s[0], sh);
+    const uint32_t S1 = __builtin_amdgcn_alignbit(r.s[2], r.s[1], sh);
+    const uint32_t S2 = __builtin_amdgcn_alignbit(r.s[3], r.s[2], sh);
+    uint32_t Q[4], M[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        Q[k] = __builtin_amdgcn_alignbit(r.q[k + 1], r.q[k], sh);
+        M[k] = __builtin_amdgcn_alignbit(r.m[k + 1], r.m[k], sh);
+    }
+    double acc = 0.0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        // 6-bit scale of group g = 8s + 2j + h: word 2s + (j >> 1), byte
+        // bi = 2(j & 1) + h (stratum_q3k.h:17-28)
+        const uint32_t bi = 8u * (uint32_t)(2 * (j & 1) + h);
+        const uint32_t w = (uint32_t)(2 * s + (j >> 1));
+        const uint32_t nib = bfe((w & 1u) ? S1 : S0, bi + ((w & 2u) ? 4u : 0u), 4);
+        const uint32_t hi2 = bfe(S2, bi + 2u * w, 2);
+        const float dl = d * (float)((int)(nib | (hi2 << 4)) - 32);
+        float a = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t lo2 = (Q[k] >> (2 * j)) & 0x03030303u;
+            const uint32_t neg = ((~M[k] >> (4 * s + j)) & 0x01010101u) << 2;
+            const uint32_t y = (lo2 | neg) << 5;              // int8 32 * q3 per byte
+            const float4 xv = xc[4 * j + k];
+            a = a + i8f(y, 0) * xv.x;
+            a = a + i8f(y, 1) * xv.y;
+            a = a + i8f(y, 2) * xv.z;
+            a = a + i8f(y, 3) * xv.w;
+        }
+        acc = acc + (double)((dl * fs) * a);
+    }
+    return acc;
+}
+
+// Q8_0 chunk u: blocks 2u and 2u+1 (stratum_q8_0.h:19-33): per block the
+// binary32 sum of 32 products int8 q * x, then fl(d * acc); fk = 2^-k for
+// x staged as x * 2^k.
+__device__ __forceinline__ double term_q80(const RawQ8& r, const float4* xc, double fk) {
+    const float f = (float)fk;
+    double acc = 0.0;
+#pragma unroll
+    for (int half = 0; half < 2; half++) {
+        const float d = f16_bits_to_f32(half ? (r.w[8] >> 16) : (r.w[0] & 0xffffu));
+        float a = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            // block 0's quants start 2 bytes into dword 0; block 1's at dword 9
+            const uint32_t v = half ? r.w[9 + k] : __builtin_amdgcn_alignbit(r.w[k + 1], r.w[k], 16);
+            const float4 xv = xc[8 * half + k];
+            a = a + i8f(v, 0) * xv.x;
+            a = a + i8f(v, 1) * xv.y;
+            a = a + i8f(v, 2) * xv.z;
+            a = a + i8f(v, 3) * xv.w;
+        }
+        acc = acc + (double)((d * f) * a);
+    }
+    return acc;
+}
+
 // ------------------------------------------------------ per-type dispatch
 template <int TYPE> struct Chunk;
 
@@ -783,6 +974,44 @@ template <> struct Chunk<T_Q2K> {
     static __device__ __forceinline__ double term(const Raw& r, int u, const float4* xc,
                                                   const float* xs, int c, float f, double) {
         return term_q2k<SC, LOWREG>(r, u, xc, reinterpret_cast<const float4*>(xs)[c], f);
+    }
+};
+template <> struct Chunk<T_Q5K> {
+    using Raw = RawQ5;
+    static __device__ __forceinline__ Raw load(wptr blk, int u) { return load_q5k(blk, u); }
+    static __device__ __forceinline__ void drain(const Raw& r) {
+        asm volatile("" ::"v"(r.hd.x), "v"(r.h0.x), "v"(r.h1.x), "v"(r.qa.x), "v"(r.qb.x));
+    }
+    template <bool SC, bool LOWREG = false>
+    static __device__ __forceinline__ double term(const Raw& r, int u, const float4* xc,
+                                                  const float* xs, int c, float f, double) {
+        const float2 sx = reinterpret_cast<const float2*>(xs)[c];
+        return term_q5k<SC>(r, u, xc, sx.x, sx.y, f);
+    }
+};
+template <> struct Chunk<T_Q3K> {
+    using Raw = RawQ3;
+    static __device__ __forceinline__ Raw load(wptr blk, int u) { return load_q3k(blk, u); }
+    static __device__ __forceinline__ void drain(const Raw& r) {
+        asm volatile("" ::"v"(r.q[0]), "v"(r.q[4]), "v"(r.m[0]), "v"(r.m[4]), "v"(r.s[0]),
+                     "v"(r.s[3]), "v"(r.d));
+    }
+    template <bool SC, bool LOWREG = false>
+    static __device__ __forceinline__ double term(const Raw& r, int u, const float4* xc,
+                                                  const float*, int, float, double f6) {
+        return term_q3k(r, u, xc, 4.0 * f6);
+    }
+};
+template <> struct Chunk<T_Q80> {
+    using Raw = RawQ8;
+    static __device__ __forceinline__ Raw load(wptr blk, int u) { return load_q80(blk, u); }
+    static __device__ __forceinline__ void drain(const Raw& r) {
+        asm volatile("" ::"v"(r.w[0]), "v"(r.w[12]), "v"(r.w[16]));
+    }
+    template <bool SC, bool LOWREG = false>
+    static __device__ __forceinline__ double term(const Raw& r, int, const float4* xc,
+                                                  const float*, int, float, double f6) {
+        return term_q80(r, xc, 4.0 * f6);
     }
 };
 template <> struct Chunk<T_NIB> {
@@ -1120,7 +1349,7 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
     // x staging decision: SC types stage x scaled, Q6_K unscaled; a Q6_K
     // segment can read a scaled x, an SC type restages an unscaled one
     // unless the window already failed for it.
-    constexpr bool SCTYPE = TYPE != T_Q6K;
+    constexpr bool SCTYPE = TI::SCALED;
     const int xst = ngx > 1 ? S.x_stride : 0;
     const bool same_x = st.x == S.x && st.K == K && st.layout == (int)TI::LINEAR && st.ngx == ngx &&
                         st.xst == xst;
@@ -1299,10 +1528,13 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
 }
 
 // TYPES is a bit set of the types the launch contains (bit 0 Q4_K, 1 Q6_K,
-// 2 Q2_K, 3 type 42): the host launches the instantiation with only the
-// types present, so a single-type launch carries one type's code and the
-// register allocation is not constrained by the others.
+// 2 Q2_K, 3 type 42, 5 Q5_K, 6 Q3_K, 7 Q8_0): the host launches the
+// instantiation with only the types present, so a single-type launch
+// carries one type's code and the register allocation is not constrained
+// by the others.  Launches that mix types run the TB_ALL kernel (the first
+// four types); the host gives each of the other types launches of its own.
 constexpr int TB_Q4K = 1, TB_Q6K = 2, TB_Q2K = 4, TB_NIB = 8, TB_ALL = 15;
+constexpr int TB_Q5K = 32, TB_Q3K = 64, TB_Q80 = 128;
 // TB_SEL: the MoE gather instantiations (every segment has a selection)
 constexpr int TB_SEL = 16;
 
@@ -1332,8 +1564,9 @@ __global__ __launch_bounds__(1024) void kq_segs_kernel(SegsArg A) {
     // a single-type instantiation does not read the segment types (the host
     // launches it only for segment lists of that type)
     constexpr bool SELK = (TYPES & TB_SEL) != 0;    // MoE gather: every segment has sel
-    constexpr int TYB = TYPES & TB_ALL;
-    constexpr bool SINGLE = TYB == TB_Q4K || TYB == TB_Q6K || TYB == TB_Q2K || TYB == TB_NIB;
+    constexpr int TYB = TYPES & ~TB_SEL;
+    constexpr bool SINGLE = TYB == TB_Q4K || TYB == TB_Q6K || TYB == TB_Q2K || TYB == TB_NIB ||
+                            TYB == TB_Q5K || TYB == TB_Q3K || TYB == TB_Q80;
     for (int i = 0; i < nseg; i++) {
         const Seg& S = A.s[i];
         if (i) prefetch_seg(S);
@@ -1346,7 +1579,8 @@ __global__ __launch_bounds__(1024) void kq_segs_kernel(SegsArg A) {
         else run_segment<T_, DEPTH, PM_EQUAL>(S, A, i, st, smem, last);
         if (SINGLE) {
             constexpr int TY = TYB == TB_Q4K ? T_Q4K : TYB == TB_Q6K ? T_Q6K
-                             : TYB == TB_Q2K ? T_Q2K : T_NIB;
+                             : TYB == TB_Q2K ? T_Q2K : TYB == TB_NIB ? T_NIB
+                             : TYB == TB_Q5K ? T_Q5K : TYB == TB_Q3K ? T_Q3K : T_Q80;
             KQ_RUN(TY)
         } else {
             switch (S.type) {
@@ -2504,6 +2738,49 @@ __global__ __launch_bounds__(256) void kq_dequant_kernel(const uint8_t* __restri
                 yb[128 * h + 32 * t + l] = ds * (float)q;
             }
         }
+    } else if (TYPE == T_Q5K) {
+        // stratum_q5k.h:18-42: y = fl(fl(d*sc)*q) - fl(dmin*m), q 5 bits
+        const float d = f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+        const float dmin = f16_bits_to_f32((uint32_t)blk[2] | ((uint32_t)blk[3] << 8));
+        const wptr s = blk + 4;
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+            const int sb = 2 * u + half;
+            uint32_t sc, m;
+            if (sb < 4) { sc = s[sb] & 63u; m = s[sb + 4] & 63u; }
+            else { sc = (s[sb + 4] & 15u) | ((uint32_t)(s[sb - 4] >> 6) << 4);
+                   m = ((uint32_t)s[sb + 4] >> 4) | ((uint32_t)(s[sb] >> 6) << 4); }
+            const float ds = d * (float)sc, dm = dmin * (float)m;
+            for (int l = 0; l < 32; l++) {
+                const uint32_t v = blk[48 + 32 * u + l];
+                const uint32_t q = (half ? (v >> 4) : (v & 15u)) + (((uint32_t)blk[16 + l] >> sb) & 1u) * 16u;
+                yb[32 * sb + l] = ds * (float)q - dm;
+            }
+        }
+    } else if (TYPE == T_Q3K) {
+        // stratum_q3k.h:30-56: y = fl(fl(d*(sc-32))*q3), chunk u = (s, h)
+        const float d = f16_bits_to_f32((uint32_t)blk[108] | ((uint32_t)blk[109] << 8));
+        const int s = u >> 1, h = u & 1;
+        for (int j = 0; j < 4; j++) {
+            const int g = 8 * s + 2 * j + h, w = g >> 2, bi = g & 3;
+            const uint32_t lo = (w & 1) ? blk[100 + bi] : blk[96 + bi];
+            const uint32_t nib = (w & 2) ? (lo >> 4) : (lo & 15u);
+            const uint32_t hi2 = ((uint32_t)blk[104 + bi] >> (2 * w)) & 3u;
+            const float dl = d * (float)((int)(nib | (hi2 << 4)) - 32);
+            for (int l = 0; l < 16; l++) {
+                const int q = (int)(((uint32_t)blk[32 + 32 * s + 16 * h + l] >> (2 * j)) & 3u) -
+                              ((((uint32_t)blk[16 * h + l] >> (4 * s + j)) & 1u) ? 0 : 4);
+                yb[128 * s + 32 * j + 16 * h + l] = dl * (float)q;
+            }
+        }
+    } else if (TYPE == T_Q80) {
+        // stratum_q8_0.h:14-17, blocks 2u and 2u+1 of the 256-weight unit
+        for (int half = 0; half < 2; half++) {
+            const wptr bp = blk + 68 * u + 34 * half;
+            const float d = f16_bits_to_f32((uint32_t)bp[0] | ((uint32_t)bp[1] << 8));
+            for (int k = 0; k < 32; k++)
+                yb[64 * u + 32 * half + k] = d * (float)(int8_t)bp[2 + k];
+        }
     } else {
         const bool nib = TYPE == T_NIB;
         const int doff = nib ? 144 : 80;
@@ -2530,6 +2807,105 @@ __global__ __launch_bounds__(256) void kq_dequant_kernel(const uint8_t* __restri
                 yb[p] = dl * (float)q - ml;
             }
         }
+    }
+}
+
+// --------------------------------------------------------- dense rows
+// F16 and F32 tensors (st_linear_f16 / st_linear_f32, stratum_linear.h:
+// 491-512).  Every product w * x is exact in binary64 (11 or 24 bits times
+// 24), so y is the binary64 sum of exact products rounded once; the
+// reference sums F16 rows in element order (a different binary64 grouping,
+// at most one binary32 ulp apart after the final rounding) and hands F32
+// to cblas_sgemv.  A wave takes a row; lane i takes elements
+// [E i + 64 E m, +E) of step m (E = 4 for F32, 8 for F16: one 16-byte load,
+// a wave reads 1 KB of the row per step), summed in increasing m, and the
+// 64 lane sums are combined by a fixed butterfly: the order depends on K
+// only.  Rows go to waves w, w + 4G, ... of G workgroups of 256 lanes.
+constexpr int T_F32 = 0, T_F16 = 1;
+constexpr int DENSE_XLDS_MAX = 16384;   // x staged in LDS up to this K
+
+struct DenseArg {
+    const uint8_t* w;
+    const float* x;
+    const float* add;
+    float* y;
+    long row_bytes;
+    int N, K;
+};
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int lo = __shfl_xor(__double2loint(v), off);
+        const int hi = __shfl_xor(__double2hiint(v), off);
+        v = v + __hiloint2double(hi, lo);
+    }
+    return v;
+}
+
+template <int TYPE, bool XLDS>
+__global__ __launch_bounds__(256) void kq_dense_kernel(DenseArg a) {
+    extern __shared__ __align__(16) float xl[];
+    constexpr int E = TYPE == T_F32 ? 4 : 8;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int K = a.K;
+    if (XLDS) {
+        for (int i = 4 * tid; i < K; i += 1024)
+            *reinterpret_cast<float4*>(xl + i) = *reinterpret_cast<const float4*>(a.x + i);
+        __syncthreads();
+    }
+    const float* xs = XLDS ? xl : a.x;
+    for (int r = blockIdx.x * 4 + wave; r < a.N; r += gridDim.x * 4) {
+        const wptr row = to_global(a.w) + (size_t)r * a.row_bytes;
+        double acc = 0.0;
+        for (int m = 0; m < K; m += 64 * E) {
+            const int e0 = m + E * lane;
+            if (e0 < K) {                       // F16 rows of K % 512 == 256 end half-way
+                const uint4 v = ld16(row + (size_t)e0 * (TYPE == T_F32 ? 4 : 2));
+                const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int q = 0; q < E / 4; q++) {
+                    const float4 xv = *reinterpret_cast<const float4*>(xs + e0 + 4 * q);
+                    float wf[4];
+                    if (TYPE == T_F32) {
+                        wf[0] = __uint_as_float(wv[0]); wf[1] = __uint_as_float(wv[1]);
+                        wf[2] = __uint_as_float(wv[2]); wf[3] = __uint_as_float(wv[3]);
+                    } else {
+                        wf[0] = f16_bits_to_f32(wv[2 * q] & 0xffffu);
+                        wf[1] = f16_bits_to_f32(wv[2 * q] >> 16);
+                        wf[2] = f16_bits_to_f32(wv[2 * q + 1] & 0xffffu);
+                        wf[3] = f16_bits_to_f32(wv[2 * q + 1] >> 16);
+                    }
+                    acc = fma((double)wf[0], (double)xv.x, acc);   // exact product, one rounding
+                    acc = fma((double)wf[1], (double)xv.y, acc);
+                    acc = fma((double)wf[2], (double)xv.z, acc);
+                    acc = fma((double)wf[3], (double)xv.w, acc);
+                }
+            }
+        }
+        acc = wave_sum_f64(acc);
+        if (lane == 0) {
+            float v = (float)acc;
+            if (a.add) v = a.add[r] + v;
+            a.y[r] = v;
+        }
+    }
+}
+
+// dense dequant: F16 widened, F32 copied (4 values per lane)
+__global__ __launch_bounds__(256) void kq_dense_dequant_kernel(const uint8_t* w, float* y, long n,
+                                                               int type) {
+    const long i = 4 * ((long)blockIdx.x * 256 + threadIdx.x);
+    if (i >= n) return;
+    const wptr p = to_global(w);
+    if (type == T_F32) {
+        const uint4 v = ld16(p + 4 * i);
+        y[i] = __uint_as_float(v.x); y[i + 1] = __uint_as_float(v.y);
+        y[i + 2] = __uint_as_float(v.z); y[i + 3] = __uint_as_float(v.w);
+    } else {
+        const uint2 v = ld8a4(p + 2 * i);
+        y[i] = f16_bits_to_f32(v.x & 0xffffu); y[i + 1] = f16_bits_to_f32(v.x >> 16);
+        y[i + 2] = f16_bits_to_f32(v.y & 0xffffu); y[i + 3] = f16_bits_to_f32(v.y >> 16);
     }
 }
 
@@ -2597,6 +2973,36 @@ static int xs_per_chunk(int type) {
     case T_Q6K: return TypeInfo<T_Q6K>::XS_PER_CHUNK;
     case T_Q2K: return TypeInfo<T_Q2K>::XS_PER_CHUNK;
     case T_NIB: return TypeInfo<T_NIB>::XS_PER_CHUNK;
+    case T_Q5K: return TypeInfo<T_Q5K>::XS_PER_CHUNK;
+    case T_Q3K: return TypeInfo<T_Q3K>::XS_PER_CHUNK;
+    case T_Q80: return TypeInfo<T_Q80>::XS_PER_CHUNK;
+    default: return -1;
+    }
+}
+
+static int block_bytes_of(int type) {
+    switch (type) {
+    case T_Q4K: return TypeInfo<T_Q4K>::BB;
+    case T_Q6K: return TypeInfo<T_Q6K>::BB;
+    case T_Q2K: return TypeInfo<T_Q2K>::BB;
+    case T_NIB: return TypeInfo<T_NIB>::BB;
+    case T_Q5K: return TypeInfo<T_Q5K>::BB;
+    case T_Q3K: return TypeInfo<T_Q3K>::BB;
+    case T_Q80: return TypeInfo<T_Q80>::BB;
+    default: return 0;
+    }
+}
+
+// index of a type's single-type instantiations (k_segs, k_segs_sel), or -1
+static int type_slot(int type) {
+    switch (type) {
+    case T_Q4K: return 0;
+    case T_Q6K: return 1;
+    case T_Q2K: return 2;
+    case T_NIB: return 3;
+    case T_Q5K: return 5;
+    case T_Q3K: return 6;
+    case T_Q80: return 7;
     default: return -1;
     }
 }
@@ -2644,28 +3050,32 @@ long kqk_segs_lds(const kqk_seg* segs, int nseg, int grid, int* xs_off, int* ter
     return xl + xsb + tb + SCR_BYTES;
 }
 
-// Every instantiation, indexed by [multi][depth - 1][type set].
+// Every instantiation, indexed by [multi][depth - 1][slot]: slots 0..3 and
+// 5..7 single types (type_slot), 4 the mixed-type kernel.
 #define KQ_SEGS_ROW(D, M)                                                       \
     {&kq_segs_kernel<D, TB_Q4K, M>, &kq_segs_kernel<D, TB_Q6K, M>,              \
      &kq_segs_kernel<D, TB_Q2K, M>, &kq_segs_kernel<D, TB_NIB, M>,              \
-     &kq_segs_kernel<D, TB_ALL, M>}
+     &kq_segs_kernel<D, TB_ALL, M>, &kq_segs_kernel<D, TB_Q5K, M>,              \
+     &kq_segs_kernel<D, TB_Q3K, M>, &kq_segs_kernel<D, TB_Q80, M>}
 typedef void (*segs_fn)(SegsArg);
-static const segs_fn k_segs[2][2][5] = {{KQ_SEGS_ROW(1, false), KQ_SEGS_ROW(2, false)},
+static const segs_fn k_segs[2][2][8] = {{KQ_SEGS_ROW(1, false), KQ_SEGS_ROW(2, false)},
                                         {KQ_SEGS_ROW(1, true), KQ_SEGS_ROW(2, true)}};
 #undef KQ_SEGS_ROW
-// the MoE gather (TB_SEL) instantiations, single type only
+// the MoE gather (TB_SEL) instantiations, single type only (slot 4 unused)
 #define KQ_SEL_ROW(D, M)                                                                  \
     {&kq_segs_kernel<D, TB_Q4K | TB_SEL, M>, &kq_segs_kernel<D, TB_Q6K | TB_SEL, M>,       \
-     &kq_segs_kernel<D, TB_Q2K | TB_SEL, M>, &kq_segs_kernel<D, TB_NIB | TB_SEL, M>}
-static const segs_fn k_segs_sel[2][2][4] = {{KQ_SEL_ROW(1, false), KQ_SEL_ROW(2, false)},
+     &kq_segs_kernel<D, TB_Q2K | TB_SEL, M>, &kq_segs_kernel<D, TB_NIB | TB_SEL, M>,       \
+     &kq_segs_kernel<D, TB_Q4K | TB_SEL, M>, &kq_segs_kernel<D, TB_Q5K | TB_SEL, M>,       \
+     &kq_segs_kernel<D, TB_Q3K | TB_SEL, M>, &kq_segs_kernel<D, TB_Q80 | TB_SEL, M>}
+static const segs_fn k_segs_sel[2][2][8] = {{KQ_SEL_ROW(1, false), KQ_SEL_ROW(2, false)},
                                             {KQ_SEL_ROW(1, true), KQ_SEL_ROW(2, true)}};
 #undef KQ_SEL_ROW
 
 int kqk_set_max_lds(int bytes) {
     for (int m = 0; m < 2; m++)
         for (int d = 0; d < 2; d++)
-            for (int t = 0; t < 9; t++) {
-                const segs_fn f = t < 5 ? k_segs[m][d][t] : k_segs_sel[m][d][t - 5];
+            for (int t = 0; t < 16; t++) {
+                const segs_fn f = t < 8 ? k_segs[m][d][t] : k_segs_sel[m][d][t - 8];
                 const hipError_t e =
                     hipFuncSetAttribute(reinterpret_cast<const void*>(f),
                                         hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
@@ -2715,16 +3125,22 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
         d.estride = h.estride;
         d.ksel = h.ksel > 0 ? h.ksel : 1;
         d.emax = h.emax > 0 ? h.emax : 1;
-        if (start >= (1 << 24) || (long)(h.K >> 8) * 210 >= (1L << 24))   // 24-bit addressing
+        if (start >= (1 << 24) || (long)(h.K >> 8) * block_bytes_of(h.type) >= (1L << 24) ||
+            type_slot(h.type) < 0)                                    // 24-bit addressing
             return (int)hipErrorInvalidValue;
         d.type = h.type; d.K = h.K; d.N = start; d.nparts = h.nparts;
         d.x_stride = h.nparts > 1 ? h.x_stride : 0;
         d.pn = equal ? h.rows[0] : 0;
         magic_for((uint32_t)(equal ? h.rows[0] : 1), d.pn_m, d.pn_l);
         magic_for((uint32_t)(h.K >> 6), d.nc_m, d.nc_l);
-        set |= h.type == T_Q4K ? TB_Q4K : h.type == T_Q6K ? TB_Q6K : h.type == T_Q2K ? TB_Q2K : TB_NIB;
+        set |= h.type == T_Q4K ? TB_Q4K : h.type == T_Q6K ? TB_Q6K : h.type == T_Q2K ? TB_Q2K
+             : h.type == T_NIB ? TB_NIB : h.type == T_Q5K ? TB_Q5K : h.type == T_Q3K ? TB_Q3K
+             : TB_Q80;
     }
-    const int t = set == TB_Q4K ? 0 : set == TB_Q6K ? 1 : set == TB_Q2K ? 2 : set == TB_NIB ? 3 : 4;
+    const int t = set == TB_Q4K ? 0 : set == TB_Q6K ? 1 : set == TB_Q2K ? 2 : set == TB_NIB ? 3
+                : set == TB_Q5K ? 5 : set == TB_Q3K ? 6 : set == TB_Q80 ? 7
+                : (set & ~TB_ALL) ? -1 : 4;
+    if (t < 0) return (int)hipErrorInvalidValue;   // other types are never mixed in a launch
     if (t == 4) depth = 1;   // the all-types kernel fits 128 VGPRs at depth 1 only
     int nsel = 0;
     for (int i = 0; i < nseg; i++) nsel += segs[i].sel != nullptr;
@@ -2993,8 +3409,48 @@ int kqk_launch_dequant(int type, const void* w, float* y, long nblocks, hipStrea
     case T_Q6K: return launch_dequant<T_Q6K>(wb, y, nblocks, st);
     case T_Q2K: return launch_dequant<T_Q2K>(wb, y, nblocks, st);
     case T_NIB: return launch_dequant<T_NIB>(wb, y, nblocks, st);
+    case T_Q5K: return launch_dequant<T_Q5K>(wb, y, nblocks, st);
+    case T_Q3K: return launch_dequant<T_Q3K>(wb, y, nblocks, st);
+    case T_Q80: return launch_dequant<T_Q80>(wb, y, nblocks, st);
+    case T_F16: case T_F32: {
+        const long n = nblocks * 256;
+        hipLaunchKernelGGL(kq_dense_dequant_kernel, dim3((unsigned)((n / 4 + 255) / 256)), dim3(256),
+                           0, st, wb, y, n, type);
+        return (int)hipGetLastError();
+    }
     default: return -1;
     }
+}
+
+// Dense rows (F16, F32): x staged in LDS when K <= DENSE_XLDS_MAX
+int kqk_launch_dense(int type, const void* w, const float* x, const float* add, float* y, int N,
+                     int K, int grid, hipStream_t st) {
+    if ((type != T_F16 && type != T_F32) || N < 1 || K < 256 || (K & 255) || grid < 1)
+        return (int)hipErrorInvalidValue;
+    DenseArg a;
+    a.w = static_cast<const uint8_t*>(w);
+    a.x = x; a.add = add; a.y = y; a.N = N; a.K = K;
+    a.row_bytes = (long)K * (type == T_F32 ? 4 : 2);
+    const bool lds = K <= DENSE_XLDS_MAX;
+    const size_t shm = lds ? (size_t)K * 4 : 0;
+#define KQ_DENSE_GO(T_, L_) hipLaunchKernelGGL((kq_dense_kernel<T_, L_>), dim3(grid), dim3(256), shm, st, a)
+    if (type == T_F32) { if (lds) KQ_DENSE_GO(T_F32, true); else KQ_DENSE_GO(T_F32, false); }
+    else { if (lds) KQ_DENSE_GO(T_F16, true); else KQ_DENSE_GO(T_F16, false); }
+#undef KQ_DENSE_GO
+    return (int)hipGetLastError();
+}
+
+int kqk_dense_set_max_lds(int bytes) {
+    const void* fns[4] = {reinterpret_cast<const void*>(&kq_dense_kernel<T_F32, true>),
+                          reinterpret_cast<const void*>(&kq_dense_kernel<T_F16, true>),
+                          reinterpret_cast<const void*>(&kq_dense_kernel<T_F32, false>),
+                          reinterpret_cast<const void*>(&kq_dense_kernel<T_F16, false>)};
+    for (int i = 0; i < 4; i++) {
+        const hipError_t e = hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 bytes < DENSE_XLDS_MAX * 4 ? bytes : DENSE_XLDS_MAX * 4);
+        if (e != hipSuccess) return (int)e;
+    }
+    return 0;
 }
 
 }  // extern "C"

@@ -37,6 +37,10 @@ long kqk_segs_lds(const kqk_seg* segs, int nseg, int grid, int* xs_off, int* ter
 int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int depth,
                     long lds_bytes, int xs_off, int terms_off, int scr_off, hipStream_t st);
 int kqk_launch_dequant(int type, const void* w, float* y, long nblocks, hipStream_t st);
+/* dense F16 / F32 rows (types 1 / 0): y = W x (+ add) on `grid` workgroups */
+int kqk_launch_dense(int type, const void* w, const float* x, const float* add, float* y, int N,
+                     int K, int grid, hipStream_t st);
+int kqk_dense_set_max_lds(int bytes);
 int kqk_set_max_lds(int bytes);
 /* multi-x launcher: plan[] = threads, S, RB, nblk, TC, sums bytes, x buffer
  * bytes, members staged together (kqk_mx_plan returns the LDS bytes, or

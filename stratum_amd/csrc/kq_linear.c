@@ -68,14 +68,31 @@ static int kq_fail(const char* fmt, ...) {
 
 const char* kq_last_error(void) { return g_kq.err; }
 
+/* bytes per 256 weights (stratum_gguf.h:57-79; Q8_0: eight 34-byte blocks) */
 static int block_bytes(int type) {
-    switch (type) {   /* stratum_gguf.h:57-79 */
+    switch (type) {
+    case KQ_TYPE_F32: return 1024;
+    case KQ_TYPE_F16: return 512;
+    case KQ_TYPE_Q8_0: return 272;
     case KQ_TYPE_Q2_K: return 84;
+    case KQ_TYPE_Q3_K: return 110;
     case KQ_TYPE_Q4_K: return 144;
+    case KQ_TYPE_Q5_K: return 176;
     case KQ_TYPE_Q6_K: return 210;
     case KQ_TYPE_Q2K_NIB: return 148;
     default: return 0;
     }
+}
+
+/* dense rows (their own kernel) */
+static int is_dense(int type) { return type == KQ_TYPE_F16 || type == KQ_TYPE_F32; }
+
+/* the types the multi-x (MULTISEQ, MoE batch) kernel and the mixed-type
+ * segment kernel cover; the other block types run single-type launches and
+ * per-stream calls */
+static int is_core(int type) {
+    return type == KQ_TYPE_Q2_K || type == KQ_TYPE_Q4_K || type == KQ_TYPE_Q6_K ||
+           type == KQ_TYPE_Q2K_NIB;
 }
 
 int64_t kq_row_bytes(int type, int K) {
@@ -118,7 +135,8 @@ static int kq_ready(void) {
     g_kq.device = dev;
     g_kq.n_cu = ncu > 0 ? ncu : 1;
     g_kq.lds_max = lds > 0 ? lds : 65536;
-    if (kqk_set_max_lds(g_kq.lds_max) != 0 || kqk_mx_set_max_lds(g_kq.lds_max) != 0)
+    if (kqk_set_max_lds(g_kq.lds_max) != 0 || kqk_mx_set_max_lds(g_kq.lds_max) != 0 ||
+        kqk_dense_set_max_lds(g_kq.lds_max) != 0)
         return kq_fail("cannot raise the LDS limit");
     /* the static scratch of the no-allocation entry point: its address on
      * this device, looked up once now (other devices at their first call) */
@@ -264,7 +282,25 @@ static int plan_depth(int threads) {
     return threads < 1024 ? 2 : 1;
 }
 
+static int launch_segs_one(const kqk_seg* segs, int nseg, hipStream_t st);
+
+/* One launch per run of consecutive segments that one kernel instantiation
+ * takes: any mix of the core types, or one other block type.  The
+ * segments are independent, so splitting changes no result. */
 static int launch_segs(const kqk_seg* segs, int nseg, hipStream_t st) {
+    int i = 0;
+    while (i < nseg) {
+        int j = i + 1;
+        while (j < nseg && (is_core(segs[i].type) ? is_core(segs[j].type)
+                                                   : segs[j].type == segs[i].type))
+            j++;
+        if (launch_segs_one(segs + i, j - i, st)) return -1;
+        i = j;
+    }
+    return 0;
+}
+
+static int launch_segs_one(const kqk_seg* segs, int nseg, hipStream_t st) {
     int grid = plan_grid(), threads = plan_threads(segs, nseg, grid), depth = plan_depth(threads);
     for (int i = 0; i < nseg; i++) {   /* the kernel's row arithmetic is 24-bit */
         long n = 0;
@@ -320,11 +356,23 @@ static int check_shape(int type, int N, int K) {
 
 /* ------------------------------------------------- device-pointer ABI */
 
+/* Dense F16 / F32 rows: their own kernel, one wave per row at a time. */
+static int dense_gemv(int type, const void* w, const float* x, const float* add, float* y, int N,
+                      int K, hipStream_t st) {
+    if ((uintptr_t)w & 15) return kq_fail("dense GEMV: weights must be 16-byte aligned");
+    long g = ((long)N + 3) / 4;
+    if (g > 8L * g_kq.n_cu) g = 8L * g_kq.n_cu;
+    const int e = kqk_launch_dense(type, w, x, add, y, N, K, (int)g, st);
+    if (e) return kq_fail("dense gemv launch: %s", hipGetErrorString((hipError_t)e));
+    return 0;
+}
+
 int kq_gemv_dev(int type, const void* w, const float* x, const float* add, float* y,
                 int N, int K, kq_stream stream) {
     if (check_shape(type, N, K) || kq_ready()) return -1;
     if (!w || !x || !y) return kq_fail("kq_gemv_dev: NULL pointer");
     if ((uintptr_t)x & 15) return kq_fail("kq_gemv_dev: x must be 16-byte aligned");
+    if (is_dense(type)) return dense_gemv(type, w, x, add, y, N, K, pick(stream));
     kqk_seg sg;
     memset(&sg, 0, sizeof sg);
     sg.type = type; sg.K = K; sg.nparts = 1; sg.x = x;
@@ -384,6 +432,16 @@ int kq_gemv_segments_dev(const kq_segment* segs, int nseg, kq_stream stream) {
             return kq_fail("segment %d: too many rows", i);
         for (int g = 0; g < s->ngroups; g++)
             if (!s->w[g]) return kq_fail("segment %d: NULL weights for group %d", i, g);
+        if (is_dense(s->type)) {               /* dense rows: one launch per group */
+            for (int g = 0; g < s->ngroups; g++) {
+                const float* xg = s->x + (s->ngroups > 1 ? (size_t)g * s->x_stride : 0);
+                const size_t o = (size_t)g * s->rows_per_group;
+                if (dense_gemv(s->type, s->w[g], xg, s->add ? s->add + o : NULL, s->y + o,
+                               s->rows_per_group, s->K, pick(stream)))
+                    return -1;
+            }
+            continue;
+        }
         if (nh > 0 && try_merge(h, nh, s, grid)) continue;
         kqk_seg* t = &h[nh++];
         for (int g = 0; g < s->ngroups; g++) {
@@ -395,7 +453,7 @@ int kq_gemv_segments_dev(const kq_segment* segs, int nseg, kq_stream stream) {
         t->type = s->type; t->K = s->K; t->nparts = s->ngroups;
         t->x = s->x; t->x_stride = s->ngroups > 1 ? s->x_stride : 0;
     }
-    return launch_segs(h, nh, pick(stream));
+    return nh ? launch_segs(h, nh, pick(stream)) : 0;
 }
 
 /* Multi-x launch plans come from a cost model that scans every row-block
@@ -467,7 +525,12 @@ int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,
     if (check_shape(type, N, K) || kq_ready()) return -1;
     if (!w || !xs || !ys) return kq_fail("kq_gemv_multix_dev: NULL pointer");
     if ((uintptr_t)xs & 15) return kq_fail("kq_gemv_multix_dev: xs must be 16-byte aligned");
-    if (B == 1) return kq_gemv_dev(type, w, xs, NULL, ys, N, K, stream);
+    if (B == 1 || !is_core(type)) {   /* per-stream launches: the same bits as single calls */
+        for (int s = 0; s < B; s++)
+            if (kq_gemv_dev(type, w, xs + (size_t)s * K, NULL, ys + (size_t)s * N, N, K, stream))
+                return -1;
+        return 0;
+    }
     const int grid = plan_grid();
     for (int s0 = 0; s0 < B; ) {
         const int nb = B - s0 < 64 ? B - s0 : 64;
@@ -806,6 +869,7 @@ static int moe_one_token(const kq_moe_op* op, const int* sel, int k, int E, cons
 
 static int moe_check_op(const kq_moe_op* op, int k, int E, const char* who) {
     if (check_shape(op->type, op->n_out, op->k_in) || kq_ready()) return -1;
+    if (is_dense(op->type)) return kq_fail("%s: dense (F16/F32) experts are not supported", who);
     const int nt = op->ntensors;
     if (nt < 1 || nt > 2) return kq_fail("%s: ntensors=%d", who, nt);
     if (op->x_div != 1 && op->x_div != k) return kq_fail("%s: x_div must be 1 or k", who);
@@ -875,6 +939,18 @@ static int moe_batch(const kq_moe_op* op, int* sel, const float* probs, float* s
     return 0;
 }
 
+/* B tokens of a type the multi-x kernel does not cover: one launch per
+ * token, each with its k selections (the same bits as the batched path). */
+static int moe_per_token(const kq_moe_op* op, const int* sel, int B, int k, int E, hipStream_t st) {
+    for (int s = 0; s < B; s++) {
+        kq_moe_op o = *op;
+        o.x = op->x + (size_t)s * (op->x_div == k ? 1 : k) * op->k_in;
+        for (int t = 0; t < op->ntensors; t++) o.y[t] = op->y[t] + (size_t)s * k * op->n_out;
+        if (moe_one_token(&o, sel + (size_t)s * k, k, E, NULL, NULL, st)) return -1;
+    }
+    return 0;
+}
+
 int kq_moe_gemv_routed_dev(const kq_moe_op* op, const float* probs, int B, int k, int E, int* sel,
                            float* selw, kq_stream stream) {
     if (!op || !probs || !sel || !selw) return kq_fail("kq_moe_gemv_routed_dev: NULL argument");
@@ -883,6 +959,11 @@ int kq_moe_gemv_routed_dev(const kq_moe_op* op, const float* probs, int B, int k
     if (moe_check_op(op, k, E, "kq_moe_gemv_routed_dev")) return -1;
     hipStream_t st = pick(stream);
     if (B == 1) return moe_one_token(op, sel, k, E, probs, selw, st);
+    if (!is_core(op->type)) {
+        const int e = kqk_launch_moe_topk(probs, B, E, k, sel, selw, st);
+        if (e) return kq_fail("moe topk launch: %s", hipGetErrorString((hipError_t)e));
+        return moe_per_token(op, sel, B, k, E, st);
+    }
     const int r = moe_batch(op, sel, probs, selw, B, k, E, st);
     if (r <= 0) return r;
     /* the router weights do not fit beside the plan: route separately */
@@ -899,5 +980,6 @@ int kq_moe_gemv_dev(const kq_moe_op* op, const int* sel, int B, int k, int E, kq
     if (moe_check_op(op, k, E, "kq_moe_gemv_dev")) return -1;
     hipStream_t st = pick(stream);
     if (B == 1) return moe_one_token(op, sel, k, E, NULL, NULL, st);
+    if (!is_core(op->type)) return moe_per_token(op, sel, B, k, E, st);
     return moe_batch(op, (int*)sel, NULL, NULL, B, k, E, st);
 }

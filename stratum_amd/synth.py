@@ -13,6 +13,10 @@ see identical inputs.
         d = fp16(|N(0,1)| * 0.01).
   Q2_K  scale bytes uniform 0..255; qs uniform; d, dmin as Q4_K.
   type 42  the Q2_K blocks above re-laid by the converter.
+  Q5_K  d, dmin and scales as Q4_K; qh and qs uniform bytes.
+  Q3_K  hmask, qs and the 12 packed scale bytes uniform; d as Q4_K.
+  Q8_0  per 32 weights d = fp16(|N(0,1)| * 0.01), int8 quants uniform.
+  F16   weights fp16(N(0,1) * 0.05).   F32  weights N(0,1) * 0.05.
 
 fp16 fields use numpy's round-to-nearest-even binary32 -> binary16.
 """
@@ -20,7 +24,8 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import BLOCK_BYTES, TYPE_Q2_K, TYPE_Q2K_NIB, TYPE_Q4_K, TYPE_Q6_K
+from . import (BLOCK_BYTES, TYPE_F16, TYPE_F32, TYPE_Q2_K, TYPE_Q2K_NIB, TYPE_Q3_K, TYPE_Q4_K,
+               TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0)
 
 
 def rng(seed: int) -> np.random.Generator:
@@ -73,6 +78,43 @@ def q2k_blocks(r: np.random.Generator, nblocks: int) -> np.ndarray:
     return b.reshape(-1)
 
 
+def q5k_blocks(r: np.random.Generator, nblocks: int) -> np.ndarray:
+    b = np.empty((nblocks, 176), np.uint8)
+    b[:, 0:2] = _fp16_scale(r, nblocks).view(np.uint8).reshape(nblocks, 2)
+    b[:, 2:4] = _fp16_scale(r, nblocks).view(np.uint8).reshape(nblocks, 2)
+    sc = r.integers(0, 64, (nblocks, 8), dtype=np.uint8)
+    m = r.integers(0, 64, (nblocks, 8), dtype=np.uint8)
+    b[:, 4:16] = pack_q4k_scales(sc, m)
+    b[:, 16:176] = r.integers(0, 256, (nblocks, 160), dtype=np.uint8)   # qh, qs
+    return b.reshape(-1)
+
+
+def q3k_blocks(r: np.random.Generator, nblocks: int) -> np.ndarray:
+    b = np.empty((nblocks, 110), np.uint8)
+    b[:, 0:108] = r.integers(0, 256, (nblocks, 108), dtype=np.uint8)  # hmask, qs, scales
+    b[:, 108:110] = _fp16_scale(r, nblocks).view(np.uint8).reshape(nblocks, 2)
+    return b.reshape(-1)
+
+
+def q8_0_blocks(r: np.random.Generator, nblocks: int) -> np.ndarray:
+    """nblocks super-blocks of 256 weights: eight 34-byte Q8_0 blocks each."""
+    n = 8 * nblocks
+    b = np.empty((n, 34), np.uint8)
+    b[:, 0:2] = _fp16_scale(r, n).view(np.uint8).reshape(n, 2)
+    b[:, 2:34] = r.integers(0, 256, (n, 32), dtype=np.uint8)
+    return b.reshape(-1)
+
+
+def f16_blocks(r: np.random.Generator, nblocks: int) -> np.ndarray:
+    v = r.standard_normal(256 * nblocks, dtype=np.float32) * np.float32(0.05)
+    return v.astype(np.float16).view(np.uint8).copy()
+
+
+def f32_blocks(r: np.random.Generator, nblocks: int) -> np.ndarray:
+    v = r.standard_normal(256 * nblocks, dtype=np.float32) * np.float32(0.05)
+    return v.view(np.uint8).copy()
+
+
 def q2k_to_nib(q2k: np.ndarray) -> np.ndarray:
     """Type-42 layout of Q2_K blocks (tools_gguf_nib_convert.c:99-120).
 
@@ -104,6 +146,16 @@ def blocks(qtype: int, r: np.random.Generator, nblocks: int) -> np.ndarray:
         return q2k_blocks(r, nblocks)
     if qtype == TYPE_Q2K_NIB:
         return q2k_to_nib(q2k_blocks(r, nblocks))
+    if qtype == TYPE_Q5_K:
+        return q5k_blocks(r, nblocks)
+    if qtype == TYPE_Q3_K:
+        return q3k_blocks(r, nblocks)
+    if qtype == TYPE_Q8_0:
+        return q8_0_blocks(r, nblocks)
+    if qtype == TYPE_F16:
+        return f16_blocks(r, nblocks)
+    if qtype == TYPE_F32:
+        return f32_blocks(r, nblocks)
     raise ValueError(f"type {qtype}")
 
 

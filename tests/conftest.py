@@ -56,7 +56,7 @@ def load_golden(name: str):
     return cases
 
 
-GOLDEN_FILES = {12: "q4k", 14: "q6k", 10: "q2k", 42: "q2k_nib"}
+GOLDEN_FILES = {12: "q4k", 14: "q6k", 10: "q2k", 42: "q2k_nib", 13: "q5k", 11: "q3k", 8: "q8_0"}
 
 
 def same_values(a: np.ndarray, b: np.ndarray) -> bool:

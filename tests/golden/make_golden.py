@@ -7,8 +7,10 @@ committed; the GPU box never runs this):
 
 Expected values come ONLY from the reference's own code, compiled from its
 sources where they lie by oracle/Makefile:
-  * oracle/_ref/libkqref.so -- q{4,6,2}k_dequant_block_scalar and
-    q{4,6,2}k_dot_row_scalar (stratum_q4k.h, stratum_q6k.h, stratum_q2k.h);
+  * oracle/_ref/libkqref.so -- q{4,6,2,5,3}k_dequant_block_scalar,
+    q{4,6,2,5,3}k_dot_row_scalar and q8_0_dequant_block_scalar /
+    q8_0_dot_row_scalar (stratum_q4k.h, stratum_q6k.h, stratum_q2k.h,
+    stratum_q5k.h, stratum_q3k.h, stratum_q8_0.h);
   * oracle/_ref/nib_convert -- tools_gguf_nib_convert.c, run on a small GGUF
     v3 file written here, for the type-42 bytes.
 Inputs are seeded numpy draws plus hand-built edge blocks.  Nothing from
@@ -37,7 +39,11 @@ sys.path.insert(0, ROOT)
 from oracle import oracle as O  # noqa: E402
 
 Q2, Q4, Q6, NIB = 10, 12, 14, 42
-BB = {Q2: 84, Q4: 144, Q6: 210, NIB: 148}
+Q5, Q3, Q80 = 13, 11, 8
+BB = {Q2: 84, Q4: 144, Q6: 210, NIB: 148, Q5: 176, Q3: 110, Q80: 272}   # per 256 weights
+# byte offsets of the fp16 d (and dmin) fields in a 256-weight unit
+D_AT = {Q4: [0], Q5: [0], Q6: [208], Q2: [80], Q3: [108], Q80: [34 * q for q in range(8)]}
+DMIN_AT = {Q4: 2, Q5: 2, Q2: 82}
 
 
 def f16(v) -> np.ndarray:
@@ -56,6 +62,9 @@ def rand_blocks(t: int, r: np.random.Generator, n: int) -> np.ndarray:
     elif t == Q2:
         b[:, 80:82] = f16(np.abs(r.standard_normal(n)) * 0.01).view(np.uint8).reshape(n, 2)
         b[:, 82:84] = f16(np.abs(r.standard_normal(n)) * 0.01).view(np.uint8).reshape(n, 2)
+    elif t in (Q5, Q3, Q80):
+        for o in D_AT[t] + ([DMIN_AT[t]] if t in DMIN_AT else []):
+            b[:, o:o + 2] = f16(np.abs(r.standard_normal(n)) * 0.01).view(np.uint8).reshape(n, 2)
     return b
 
 
@@ -74,6 +83,8 @@ def edge_blocks(t: int, r: np.random.Generator) -> np.ndarray:
             b[i, 2:4] = np.frombuffer(struct.pack("<H", mv), np.uint8)
         elif t == Q6:
             b[i, 208:210] = np.frombuffer(struct.pack("<H", dv), np.uint8)
+        elif t in (Q5, Q3, Q80):
+            pass                 # set with the payloads below
         else:
             b[i, 80:82] = np.frombuffer(struct.pack("<H", dv), np.uint8)
             b[i, 82:84] = np.frombuffer(struct.pack("<H", mv), np.uint8)
@@ -86,6 +97,19 @@ def edge_blocks(t: int, r: np.random.Generator) -> np.ndarray:
         b[1, 192:208] = 0x80     # scales -128
         b[2, 192:208] = 0x7F     # scales 127
         b[9, 0:208] = 0x00       # q = 0 -> -32, scales 0
+    elif t in (Q5, Q3, Q80):
+        for i, dv in enumerate(EDGE_D):
+            for o in D_AT[t]:
+                b[i, o:o + 2] = np.frombuffer(struct.pack("<H", dv), np.uint8)
+            if t in DMIN_AT:
+                b[i, DMIN_AT[t]:DMIN_AT[t] + 2] = np.frombuffer(
+                    struct.pack("<H", EDGE_D[(i + 3) % n]), np.uint8)
+        payload = [k for k in range(BB[t])
+                   if all(not (o <= k < o + 2) for o in D_AT[t]) and
+                   not (t in DMIN_AT and DMIN_AT[t] <= k < DMIN_AT[t] + 2)]
+        b[0, payload] = 0xFF     # Q5_K: q 31, scales 63; Q3_K: q 3, scale 31; Q8_0: -1
+        b[1, payload] = 0x80 if t == Q80 else 0x55
+        b[9, payload] = 0x00     # Q3_K: q -4, scale -32
     else:
         b[0, 0:80] = 0xFF
         b[9, 0:80] = 0x00
@@ -156,7 +180,8 @@ def main() -> None:
     if ref is None or not os.path.exists(O.NIBCONV_PATH):
         sys.exit("oracle/_ref is not built: /root/reference is required to write fixtures")
     manifest = []
-    for t, fname in [(Q4, "q4k"), (Q6, "q6k"), (Q2, "q2k"), (NIB, "q2k_nib")]:
+    for t, fname in [(Q4, "q4k"), (Q6, "q6k"), (Q2, "q2k"), (NIB, "q2k_nib"), (Q5, "q5k"),
+                     (Q3, "q3k"), (Q80, "q8_0")]:
         cases = make_cases(t, ref)
         arrays = {f"{c}_{k}": v for c, d in cases.items() for k, v in d.items()}
         path = os.path.join(HERE, f"{fname}.npz")

@@ -69,7 +69,15 @@ def test_row_bytes_and_type_table():
     assert L.kq_row_bytes(14, 17408) == 68 * 210
     assert L.kq_row_bytes(10, 5120) == 20 * 84
     assert L.kq_row_bytes(42, 5120) == 20 * 148
-    assert L.kq_row_bytes(8, 1024) == -1      # Q8_0: no kernel -> -1
+    # every type of st_linear_dispatch's switch (stratum_linear.h:533-541):
+    # GGUF row bytes (stratum_gguf.h:57-79)
+    assert L.kq_row_bytes(8, 1024) == 32 * 34       # Q8_0
+    assert L.kq_row_bytes(11, 5120) == 20 * 110     # Q3_K
+    assert L.kq_row_bytes(13, 5120) == 20 * 176     # Q5_K
+    assert L.kq_row_bytes(1, 2048) == 2048 * 2      # F16
+    assert L.kq_row_bytes(0, 2048) == 2048 * 4      # F32
+    for t in (2, 3, 6, 7, 9, 15, 16, 43, 44):        # no kernel -> -1
+        assert L.kq_row_bytes(t, 1024) == -1, t
     assert L.kq_row_bytes(12, 1000) == -1     # K % 256 != 0
 
 
@@ -80,7 +88,7 @@ def test_errors_return_minus_one_with_message():
     x = np.zeros(1024, np.float32)
     y = np.zeros(16, np.float32)
     t = K.make_tensor(12, 16, 1024, 0)
-    t.type = 8
+    t.type = 7        # Q5_1: in GGUF's table, no kernel here or in the reference switch
     rc = L.kq_linear_dispatch(ctypes.byref(t), K._fptr(x), K._fptr(y), 16, 1024)
     assert rc == -1
     assert b"type" in L.kq_last_error()

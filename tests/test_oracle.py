@@ -18,7 +18,8 @@ from conftest import GOLDEN_FILES, load_golden, same_values
 from oracle import oracle as O
 from stratum_amd import synth
 
-TYPES = [12, 14, 10, 42]
+TYPES = [12, 14, 10, 42, 13, 11, 8]
+REF_TYPES = [12, 14, 10, 13, 11, 8]    # the types whose scalar routines _ref builds
 
 
 # ------------------------------------------------------------ fp16 widening
@@ -98,6 +99,35 @@ def test_q4k_scale_decode_matches_reference_exhaustive(port, ref, j):
     assert np.array_equal(first[:, 0], sc) and np.array_equal(first[:, 1], m), j
 
 
+def q3k_scale_bytes_read(g):
+    """Bytes q3k_unpack_scales reads for scale g (stratum_q3k.h:17-28): the
+    nibble from byte g%4 (+4 for words 1 and 3), the top two bits from
+    byte 8 + g%4."""
+    w, bi = g // 4, g % 4
+    return [(4 if w & 1 else 0) + bi, 8 + bi]
+
+
+@pytest.mark.parametrize("g", range(16))
+def test_q3k_scale_decode_matches_reference_exhaustive(port, ref, g):
+    """Every value of the two bytes Q3_K scale g reads, with the other ten
+    fixed to zeros, ones and a random pattern: the oracle's decode equals
+    the reference's q3k_unpack_scales and ignores the other bytes."""
+    idx = q3k_scale_bytes_read(g)
+    first = None
+    for bg in (np.zeros(12, np.uint8), np.full(12, 0xff, np.uint8),
+               np.random.default_rng(100 + g).integers(0, 256, 12).astype(np.uint8)):
+        got = O.q3k_scale_sweep(port.L.ko_q3k_scale_sweep, g, idx, bg)
+        want = O.q3k_scale_sweep(ref.L.kqref_q3k_scale_sweep, g, idx, bg)
+        assert np.array_equal(got, want), g
+        first = got if first is None else first
+        assert np.array_equal(got, first), g
+    c = np.arange(first.size)
+    lo, hi = c & 0xff, c >> 8
+    w = g // 4
+    nib = (lo >> 4) if w & 2 else (lo & 15)
+    assert np.array_equal(first, nib | (((hi >> (2 * w)) & 3) << 4)), g
+
+
 # ------------------------------------------------------- golden fixtures
 @pytest.mark.parametrize("qtype", TYPES)
 def test_oracle_matches_golden(port, qtype):
@@ -109,7 +139,7 @@ def test_oracle_matches_golden(port, qtype):
         assert same_values(y, d["y"]), (qtype, case, "dot")
 
 
-@pytest.mark.parametrize("qtype", [12, 14, 10])
+@pytest.mark.parametrize("qtype", REF_TYPES)
 @pytest.mark.parametrize("K", [256, 768, 2048])
 def test_oracle_matches_reference_random(port, ref, qtype, K):
     for seed in range(3):
@@ -303,3 +333,52 @@ def test_topk_matches_sort(port):
         order = sorted(range(128), key=lambda e: (-w[e], e))[:8]
         assert sel == order
         assert np.array_equal(selw, w[order])
+
+
+# ------------------------------------------------------------ F16 / F32
+# st_linear_f16 (stratum_linear.h:491-505) sums exact binary64 products in
+# element order; F32 goes to cblas_sgemv (:508-512), restated as the same
+# binary64 sum of exact products.  Neither builds here (the file needs
+# Accelerate), so these pin the restatement by closed forms.
+def _dense(qtype, vals):
+    v = np.asarray(vals, np.float32)
+    return (v.astype(np.float16).view(np.uint8) if qtype == 1 else v.view(np.uint8)).copy()
+
+
+@pytest.mark.parametrize("qtype", [1, 0])
+def test_dense_unit_vectors_and_integers(port, qtype):
+    K = 512
+    r = np.random.default_rng(7 + qtype)
+    w = r.integers(-8, 8, (3, K)).astype(np.float32)
+    w[1] *= np.float32(0.125)                 # exact in fp16 as well
+    wb = _dense(qtype, w.reshape(-1))
+    for i in (0, 1, 255, 256, K - 1):
+        x = np.zeros(K, np.float32)
+        x[i] = 1.0
+        assert np.array_equal(port.gemv(qtype, wb, x, 3, K), w[:, i])
+    x = r.integers(-100, 100, K).astype(np.float32)
+    assert np.array_equal(port.gemv(qtype, wb, x, 3, K), (w.astype(np.float64) @ x).astype(np.float32))
+
+
+@pytest.mark.parametrize("qtype", [1, 0])
+def test_dense_sum_is_elementwise_binary64(port, qtype):
+    """Random rows: the oracle equals a Python loop of exact binary64
+    products added in element order, and differs from the correctly rounded
+    sum (math.fsum) by less than one binary32 ulp; the fp16 decode is
+    numpy's."""
+    import math
+    K = 1024
+    r = np.random.default_rng(11 + qtype)
+    w = (r.standard_normal((4, K)) * 0.05).astype(np.float32)
+    wb = _dense(qtype, w.reshape(-1))
+    wv = (wb.view(np.float16).astype(np.float64) if qtype == 1 else wb.view(np.float32).astype(np.float64))
+    wv = wv.reshape(4, K)
+    x = r.standard_normal(K).astype(np.float32)
+    got = port.gemv(qtype, wb, x, 4, K)
+    for rr in range(4):
+        acc = 0.0
+        for c in range(K):
+            acc += float(wv[rr, c]) * float(x[c])
+        assert got[rr] == np.float32(acc)
+        exact = math.fsum(float(wv[rr, c]) * float(x[c]) for c in range(K))
+        assert abs(float(got[rr]) - exact) <= np.spacing(np.float32(abs(exact)))
