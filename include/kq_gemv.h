@@ -49,6 +49,23 @@ extern "C" {
 #define KQ_TYPE_Q6_K    14
 #define KQ_TYPE_Q2K_NIB 42
 
+/* Int8-activation mode of Q4_K and Q6_K: `type | KQ_INT8_ACT` on
+ * kq_gemv_dev, kq_gemv_multix_dev and kq_gemv_segments_dev computes the
+ * reference's SDOT path (g_st.use_sdot, stratum_linear.h:376-404,
+ * 581-603, 643-690): x quantized to int8 per 32 (Q4_K,
+ * q4k_quantize_x_q8, stratum_q4k_neon.h:229-275) or per 16 (Q6_K,
+ * q6k_quantize_x_q8_g16, stratum_q6k_neon.h:117-133), exact integer dot
+ * products per sub-block, and the terms of q4k_dot_row_sdot_f /
+ * q6k_dot_row_sdot_f (stratum_q4k_neon.h:365-407, q6k_neon.h:265-317):
+ * coefficient fl(fl(d*sc)*xscale) times the integer sum.  The quantized x,
+ * the integer parts and the coefficients are bit-identical to the
+ * reference's; the terms are summed in binary64 instead of the reference's
+ * four binary32 FMA lanes, so y differs from q*_dot_row_sdot_f by at most
+ * 2^-22 * sum|term| (the lanes' own rounding) and is independent of the
+ * launch shape.  The weights are unchanged: kq_row_bytes is the base
+ * type's.  No MoE or matrix-core form. */
+#define KQ_INT8_ACT     0x100
+
 /* Layout-compatible with GgufTensor (stratum_gguf.h:129-137): a caller may
  * pass its GgufTensor* cast to kq_tensor*.  `offset` is in bytes from the
  * weight base registered with kq_linear_init (the reference's
@@ -99,6 +116,14 @@ const char* kq_last_error(void);
  * counterpart in the reference.  Returns 0. */
 int kq_tuning_reload(void);
 
+/* g_st.use_sdot for the host-pointer entry points (kq_linear_dispatch*,
+ * kq_linear_multix, kq_q4k_group): on != 0 routes Q4_K and Q6_K through
+ * the int8-activation mode (KQ_INT8_ACT), as st_linear_q4k / _q6k do when
+ * use_sdot is set (stratum_linear.h:376-404).  Off at start-up: the
+ * reference turns it on by default only where its NEON kernels exist
+ * (stratum_linear.h:133-137).  Returns the previous setting. */
+int kq_linear_set_sdot(int on);
+
 /* ------------------------------------------- host-pointer entry points
  * x/y/add are host buffers, exactly as in the reference; each call copies
  * the activations in, runs the kernel and copies y back (synchronous). */
@@ -134,6 +159,14 @@ int kq_q4k_group(const float* x, int K,
  * buffers owned by the library (one per kind, grown on demand): calls of
  * the same kind on different streams that overlap in time race on it;
  * calls on one stream are ordered. */
+
+/* The int8 quantizer of the int8-activation mode on its own: group 32 is
+ * q4k_quantize_x_q8 (+ q4k_sum_i8_32 sums, stratum_q4k_neon.h:229-275,
+ * 414-420), group 16 is q6k_quantize_x_q8_g16 (+ q6k_xsum16_i8,
+ * stratum_q6k_neon.h:117-133, 261-264).  xq gets K bytes, xscale and xsum
+ * (may be NULL) K/group entries.  Bit-identical to the reference. */
+int kq_quantize_x_q8_dev(const float* x, int K, int group, int8_t* xq, float* xscale,
+                         int32_t* xsum, kq_stream stream);
 
 /* y = W . x (+ add when add != NULL), W = N rows of K/256 blocks of `type`. */
 int kq_gemv_dev(int type, const void* w, const float* x, const float* add, float* y,

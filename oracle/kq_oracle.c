@@ -13,6 +13,7 @@
 #define _GNU_SOURCE
 #include "kq_oracle.h"
 
+#include <math.h>
 #include <pthread.h>
 #include <stdatomic.h>
 #include <stdlib.h>
@@ -405,6 +406,196 @@ static double f32_dot(const uint8_t* row, int K, const float* x) {
         acc += (double)w * (double)x[c];
     }
     return acc;
+}
+
+/* -------------------------------------------------- int8 activations */
+/* q4k_quantize_x_q8 (stratum_q4k_neon.h:230-277; its portable form
+ * :261-276) with G = 32, and q6k_quantize_x_q8_g16 (stratum_q6k_neon.h:
+ * 117-133) with G = 16: per group amax = max |x|, scale = fl(amax / 127),
+ * inv = scale > 0 ? fl(1 / scale) : 0, q = clamp(rne(fl(x * inv)),
+ * -128, 127) (lrintf in the default rounding mode; vcvtnq_s32_f32 on NEON
+ * also rounds to nearest, ties to even). */
+void ko_quantize_x_q8(const float* x, int K, int G, int8_t* xq, float* xscale) {
+    for (int g = 0; g < K / G; g++) {
+        const float* xp = x + (size_t)g * G;
+        float amax = 0.0f;
+        for (int i = 0; i < G; i++) {
+            const float a = fabsf(xp[i]);
+            if (a > amax) amax = a;
+        }
+        const float scale = amax / 127.0f;
+        const float inv = (scale > 0.0f) ? (1.0f / scale) : 0.0f;
+        xscale[g] = scale;
+        for (int i = 0; i < G; i++) {
+            int v = (int)lrintf(xp[i] * inv);
+            if (v > 127) v = 127;
+            if (v < -128) v = -128;
+            xq[(size_t)g * G + i] = (int8_t)v;
+        }
+    }
+}
+
+/* integer sums of each group of G quantized values (q4k_sum_i8_32,
+ * stratum_q4k_neon.h:414-420; q6k_xsum16_i8, stratum_q6k_neon.h:261-264) */
+static void xsums(const int8_t* xq, int K, int G, int32_t* out) {
+    for (int g = 0; g < K / G; g++) {
+        int32_t t = 0;
+        for (int i = 0; i < G; i++) t += xq[(size_t)g * G + i];
+        out[g] = t;
+    }
+}
+
+/* Q4_K with int8 activations in the reference's order, q4k_dot_row_sdot_f
+ * (stratum_q4k_neon.h:365-407): per 64-weight chunk the exact integer dots
+ * L, H of the two sub-blocks, coefficients fl(fl(d*sc)*xs) and
+ * fl(fl(-dmin*m)*xs), four binary32 lanes each a fused multiply-add chain
+ * over the chunks ([L, xsum_lo, H, xsum_hi] times the coefficients), then
+ * (f0 + f1) + (f2 + f3) (vaddvq_f32's pairwise reduction).  *mag gets the
+ * sum of |term| (for error bounds). */
+static float q4k_sdot_f(const uint8_t* row, int K, const int8_t* xq, const float* xs,
+                        const int32_t* xsum, double* mag) {
+    float f[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    double m_ = 0.0;
+    for (int b = 0; b < K / 256; b++) {
+        const uint8_t* blk = row + (size_t)b * 144;
+        const float d = ko_fp16_to_fp32(rd16(blk)), dmin = ko_fp16_to_fp32(rd16(blk + 2));
+        for (int j = 0; j < 4; j++) {
+            const int g0 = 8 * b + 2 * j, g1 = g0 + 1;
+            uint8_t sc1, mn1, sc2, mn2;
+            ko_q4k_scale_min(2 * j, blk + 4, &sc1, &mn1);
+            ko_q4k_scale_min(2 * j + 1, blk + 4, &sc2, &mn2);
+            int32_t L = 0, H = 0;
+            for (int l = 0; l < 32; l++) {
+                L += (int32_t)(blk[16 + 32 * j + l] & 15) * xq[32 * g0 + l];
+                H += (int32_t)(blk[16 + 32 * j + l] >> 4) * xq[32 * g1 + l];
+            }
+            const float c[4] = {d * (float)sc1 * xs[g0], -dmin * (float)mn1 * xs[g0],
+                                d * (float)sc2 * xs[g1], -dmin * (float)mn2 * xs[g1]};
+            const int32_t t[4] = {L, xsum[g0], H, xsum[g1]};
+            for (int k = 0; k < 4; k++) {
+                f[k] = fmaf((float)t[k], c[k], f[k]);
+                m_ += fabs((double)t[k] * (double)c[k]);
+            }
+        }
+    }
+    if (mag) *mag = m_;
+    return (f[0] + f[1]) + (f[2] + f[3]);
+}
+
+/* Q6_K with int8 activations per 16, q6k_dot_row_sdot_f
+ * (stratum_q6k_neon.h:265-317): per (half, is) the four runs t hold the
+ * unsigned 6-bit values (0..63); g4[t] = their exact dot with the run's 16
+ * quantized values minus 32 * that group's x sum; coefficient
+ * fl(fl(d * sc[g]) * xs[g]) for group g = 8 half + is + 2t; lane t of a
+ * binary32 fused multiply-add chain; then (f0 + f1) + (f2 + f3). */
+static float q6k_sdot_f(const uint8_t* row, int K, const int8_t* xq, const float* xs,
+                        const int32_t* xsum, double* mag) {
+    float f[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    double m_ = 0.0;
+    for (int b = 0; b < K / 256; b++) {
+        const uint8_t* blk = row + (size_t)b * 210;
+        const float d = ko_fp16_to_fp32(rd16(blk + 208));
+        const int8_t* sc = (const int8_t*)(blk + 192);
+        for (int h = 0; h < 2; h++)
+            for (int is = 0; is < 2; is++) {
+                for (int t = 0; t < 4; t++) {
+                    const int g = 16 * b + 8 * h + is + 2 * t;
+                    int32_t acc = 0;
+                    for (int l = 0; l < 16; l++)
+                        acc += (int32_t)(q6k_q(blk, h, t, 16 * is + l) + 32) * xq[16 * g + l];
+                    acc -= 32 * xsum[g];
+                    const float c = d * (float)sc[8 * h + is + 2 * t] * xs[g];
+                    f[t] = fmaf((float)acc, c, f[t]);
+                    m_ += fabs((double)acc * (double)c);
+                }
+            }
+    }
+    if (mag) *mag = m_;
+    return (f[0] + f[1]) + (f[2] + f[3]);
+}
+
+/* The int8-activation GEMV as the GPU computes it: the same quantized x,
+ * exact integer dots and coefficients as above, each sub-block term
+ * (Q4_K: c1*L + c2*xsum; Q6_K: c*g4) formed exactly in binary64 and the
+ * terms summed in binary64 (here in element order; the GPU's grouping of
+ * that binary64 sum is its own, as for the exact path). */
+static double q4k_i8_dot(const uint8_t* row, int K, const int8_t* xq, const float* xs,
+                         const int32_t* xsum) {
+    double dot = 0.0;
+    for (int b = 0; b < K / 256; b++) {
+        const uint8_t* blk = row + (size_t)b * 144;
+        const float d = ko_fp16_to_fp32(rd16(blk)), dmin = ko_fp16_to_fp32(rd16(blk + 2));
+        for (int s = 0; s < 8; s++) {
+            const int g = 8 * b + s;
+            uint8_t sc, mn;
+            ko_q4k_scale_min(s, blk + 4, &sc, &mn);
+            int32_t L = 0;
+            for (int l = 0; l < 32; l++) L += (int32_t)q4k_q(blk, s, l) * xq[32 * g + l];
+            const float c1 = d * (float)sc * xs[g], c2 = -dmin * (float)mn * xs[g];
+            dot += fma((double)c1, (double)L, (double)c2 * (double)xsum[g]);
+        }
+    }
+    return dot;
+}
+
+static double q6k_i8_dot(const uint8_t* row, int K, const int8_t* xq, const float* xs,
+                         const int32_t* xsum) {
+    double dot = 0.0;
+    for (int b = 0; b < K / 256; b++) {
+        const uint8_t* blk = row + (size_t)b * 210;
+        const float d = ko_fp16_to_fp32(rd16(blk + 208));
+        const int8_t* sc = (const int8_t*)(blk + 192);
+        for (int h = 0; h < 2; h++)
+            for (int is = 0; is < 2; is++)
+                for (int t = 0; t < 4; t++) {
+                    const int g = 16 * b + 8 * h + is + 2 * t;
+                    int32_t acc = 0;
+                    for (int l = 0; l < 16; l++)
+                        acc += (int32_t)(q6k_q(blk, h, t, 16 * is + l) + 32) * xq[16 * g + l];
+                    acc -= 32 * xsum[g];
+                    const float c = d * (float)sc[8 * h + is + 2 * t] * xs[g];
+                    dot += (double)c * (double)acc;
+                }
+    }
+    return dot;
+}
+
+/* y[r] (+ add[r]) for the int8-activation mode: x quantized once per call
+ * (per 32 for Q4_K, per 16 for Q6_K), then each row in the reference's
+ * order (sdot_f != 0) or the GPU's (binary64 terms).  mag (optional)
+ * receives each row's sum of |term|. */
+int ko_gemv_i8(int type, const uint8_t* w, const float* x, const float* add, float* y,
+               double* mag, int N, int K, int sdot_f) {
+    if ((type != KO_Q4_K && type != KO_Q6_K) || K % 256) return -1;
+    const int G = type == KO_Q4_K ? 32 : 16;
+    int8_t* xq = malloc((size_t)K);
+    float* xs = malloc((size_t)(K / G) * sizeof(float));
+    int32_t* xsum = malloc((size_t)(K / G) * sizeof(int32_t));
+    if (!xq || !xs || !xsum) { free(xq); free(xs); free(xsum); return -1; }
+    ko_quantize_x_q8(x, K, G, xq, xs);
+    xsums(xq, K, G, xsum);
+    const size_t rb = (size_t)(K / 256) * (size_t)ko_block_bytes(type);
+    for (int r = 0; r < N; r++) {
+        const uint8_t* row = w + (size_t)r * rb;
+        double m_ = 0.0;
+        float v;
+        if (sdot_f)
+            v = type == KO_Q4_K ? q4k_sdot_f(row, K, xq, xs, xsum, &m_)
+                                : q6k_sdot_f(row, K, xq, xs, xsum, &m_);
+        else
+            v = (float)(type == KO_Q4_K ? q4k_i8_dot(row, K, xq, xs, xsum)
+                                        : q6k_i8_dot(row, K, xq, xs, xsum));
+        if (add) v = add[r] + v;
+        y[r] = v;
+        if (mag) {
+            if (!sdot_f)
+                (void)(type == KO_Q4_K ? q4k_sdot_f(row, K, xq, xs, xsum, &m_)
+                                       : q6k_sdot_f(row, K, xq, xs, xsum, &m_));
+            mag[r] = m_;
+        }
+    }
+    free(xq); free(xs); free(xsum);
+    return 0;
 }
 
 /* ------------------------------------------------------------ dispatch */

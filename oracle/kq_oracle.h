@@ -25,6 +25,10 @@
  *   stratum_linear.h:508-512 st_linear_f32 (cblas_sgemv; restated as the
  *                          binary64 sum of exact products: parity pinned
  *                          by closed forms only, not against the BLAS bits)
+ *   stratum_q4k_neon.h:261-276 / stratum_q6k_neon.h:117-133 the int8
+ *                          activation quantizers -> ko_quantize_x_q8
+ *   stratum_q4k_neon.h:365-407 / stratum_q6k_neon.h:265-317 the int8 GEMV
+ *                          (sdot_f) -> ko_gemv_i8(..., sdot_f = 1)
  *   tools_gguf_nib_convert.c:99-120  Q2_K -> type 42 byte permutation
  *                                     -> ko_q2k_to_nib / ko_nib_to_q2k
  *   stratum_linear.h:201-228 ST_PAR_ROWS 64-row tickets -> ko_gemv threads
@@ -90,6 +94,14 @@ int ko_gemv(int type, const uint8_t* w, const float* x, const float* add,
 /* B streams over one weight: ys[s*N + r] = dot(row r, xs[s*K ...]) */
 int ko_gemv_multix(int type, const uint8_t* w, const float* xs, float* ys,
                    int B, int N, int K, int nthreads);
+
+/* int8 activations: q4k_quantize_x_q8 (G = 32) / q6k_quantize_x_q8_g16
+ * (G = 16), and the GEMV of the int8 mode for Q4_K / Q6_K: sdot_f != 0 in
+ * the reference's order (q4k_dot_row_sdot_f, q6k_dot_row_sdot_f), else the
+ * GPU's (binary64 terms); mag, if not NULL, gets each row's sum |term| */
+void ko_quantize_x_q8(const float* x, int K, int G, int8_t* xq, float* xscale);
+int ko_gemv_i8(int type, const uint8_t* w, const float* x, const float* add, float* y,
+               double* mag, int N, int K, int sdot_f);
 
 /* type-42 permutation (148-byte blocks) and its inverse */
 void ko_q2k_to_nib(const uint8_t* q2k, uint8_t* nib, int64_t nblocks);

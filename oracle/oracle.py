@@ -68,6 +68,9 @@ class Port:
         L.ko_q2k_to_nib.argtypes = [_U8, _U8, ctypes.c_int64]
         L.ko_nib_to_q2k.argtypes = [_U8, _U8, ctypes.c_int64]
         L.ko_moe_topk.argtypes = [_F, I, I, ctypes.POINTER(ctypes.c_int), _F]
+        L.ko_quantize_x_q8.argtypes = [_F, I, I, ctypes.POINTER(ctypes.c_int8), _F]
+        L.ko_quantize_x_q8.restype = None
+        L.ko_gemv_i8.argtypes = [I, _U8, _F, _F, _F, ctypes.POINTER(ctypes.c_double), I, I, I]
         self.L = L
 
     def fp16_to_fp32(self, h: int) -> float:
@@ -116,6 +119,24 @@ class Port:
         out = np.empty(n * 84, np.uint8)
         self.L.ko_nib_to_q2k(_u8(nib), _u8(out), n)
         return out
+
+    def quantize_q8(self, x: np.ndarray, G: int):
+        """(xq int8 [K], xscale float32 [K/G])"""
+        xq = np.empty(x.size, np.int8)
+        xs = np.empty(x.size // G, np.float32)
+        self.L.ko_quantize_x_q8(_f(x), x.size, G, xq.ctypes.data_as(ctypes.POINTER(ctypes.c_int8)),
+                                _f(xs))
+        return xq, xs
+
+    def gemv_i8(self, qtype, w, x, N, K, add=None, sdot_f=False, with_mag=False):
+        """int8-activation GEMV: the GPU's order, or (sdot_f) the reference's"""
+        y = np.empty(N, np.float32)
+        mag = np.empty(N, np.float64) if with_mag else None
+        rc = self.L.ko_gemv_i8(qtype, _u8(w), _f(x), _f(add) if add is not None else None, _f(y),
+                               mag.ctypes.data_as(ctypes.POINTER(ctypes.c_double))
+                               if with_mag else None, N, K, int(sdot_f))
+        assert rc == 0
+        return (y, mag) if with_mag else y
 
     def topk(self, w: np.ndarray, k: int):
         sel = (ctypes.c_int * k)()

@@ -33,6 +33,8 @@ TYPE_Q4_K = 12
 TYPE_Q5_K = 13
 TYPE_Q6_K = 14
 TYPE_Q2K_NIB = 42
+# int8-activation mode flag (KQ_INT8_ACT): TYPE_Q4_K | INT8_ACT, TYPE_Q6_K | INT8_ACT
+INT8_ACT = 0x100
 
 # bytes per 256 weights (stratum_gguf.h:57-79; Q8_0: eight 34-byte blocks)
 BLOCK_BYTES = {TYPE_F32: 1024, TYPE_F16: 512, TYPE_Q8_0: 272, TYPE_Q2_K: 84, TYPE_Q3_K: 110,
@@ -52,7 +54,8 @@ EXPORTS = (
     "kq_dequant_dev", "kq_row_bytes", "kq_moe_slice_bytes", "kq_moe_bind_slice",
     "kq_moe_pack_open", "kq_moe_pack_which", "kq_moe_topk", "kq_moe_topk_dev",
     "kq_moe_gemv_dev", "kq_gemv_multix_mfma_dev", "kq_moe_gemv_routed_dev",
-    "kq_tuning_reload", "kq_gemv_multix_mfma_noalloc_dev",
+    "kq_tuning_reload", "kq_gemv_multix_mfma_noalloc_dev", "kq_linear_set_sdot",
+    "kq_quantize_x_q8_dev",
 )
 
 NOALLOC_SCRATCH_BYTES = 32 << 20   # KQ_NOALLOC_SCRATCH_BYTES
@@ -203,6 +206,8 @@ def lib() -> ctypes.CDLL:
     L.kq_gemv_multix_mfma_dev.argtypes = [I, P, P, P, I, I, I, P]
     L.kq_gemv_multix_mfma_noalloc_dev.argtypes = [I, P, P, P, I, I, I, P]
     L.kq_dequant_dev.argtypes = [I, P, P, ctypes.c_int64, P]
+    L.kq_linear_set_sdot.argtypes = [I]
+    L.kq_quantize_x_q8_dev.argtypes = [P, I, I, P, P, P, P]
     L.kq_gemv_segments_dev.argtypes = [ctypes.POINTER(KqSegment), I, P]
     L.kq_row_bytes.argtypes = [I, I]
     L.kq_row_bytes.restype = ctypes.c_int64
@@ -295,6 +300,18 @@ def gemv_dev(qtype: int, w_ptr: int, x_ptr: int, y_ptr: int, N: int, K: int,
     """Device-pointer GEMV (raw addresses, e.g. torch tensor .data_ptr())."""
     _check(lib().kq_gemv_dev(qtype, w_ptr, x_ptr, add_ptr, y_ptr, N, K, stream),
            "kq_gemv_dev")
+
+
+def quantize_x_q8_dev(x_ptr: int, K: int, group: int, xq_ptr: int, xscale_ptr: int,
+                      xsum_ptr: int | None = None, stream: int | None = None) -> None:
+    """int8 quantizer of the int8-activation mode (kq_quantize_x_q8_dev)."""
+    _check(lib().kq_quantize_x_q8_dev(x_ptr, K, group, xq_ptr, xscale_ptr, xsum_ptr, stream),
+           "kq_quantize_x_q8_dev")
+
+
+def set_sdot(on: bool) -> bool:
+    """use_sdot for the host-pointer entry points; returns the previous setting."""
+    return bool(lib().kq_linear_set_sdot(int(on)))
 
 
 def gemv_multix_dev(qtype: int, w_ptr: int, xs_ptr: int, ys_ptr: int, B: int, N: int,

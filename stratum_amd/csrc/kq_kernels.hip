@@ -59,6 +59,15 @@ constexpr int T_Q4K = 12;
 constexpr int T_Q5K = 13;
 constexpr int T_Q6K = 14;
 constexpr int T_NIB = 42;
+// the int8-activation mode of Q4_K / Q6_K (the reference's SDOT path):
+// the type id with this bit set
+constexpr int T_I8 = 0x100;
+constexpr int T_Q4K_I8 = T_I8 | T_Q4K;
+constexpr int T_Q6K_I8 = T_I8 | T_Q6K;
+// float4 slots per chunk in the int8 x layout: 64 bytes padded to 80
+// (chunk c at byte 80c; 16-byte reads by consecutive chunks hit distinct
+// banks)
+constexpr int XPAD_I8 = 5;
 
 constexpr int XPAD = 17;  // float4 slots per 64-weight chunk in LDS (16 + 1 pad)
 
@@ -69,8 +78,13 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // min terms; SCALED: products by the byte-select multiply on x staged as
 // x * 2^KSC (the other types read x as staged and fold the factor into
 // their scale).
+// I8: the int8-activation mode (x quantized per group, XSTRIDE float4
+// slots per chunk of int8 x; XS_PER_CHUNK floats hold each group's scale
+// and integer sum).
 template <int TYPE> struct TypeInfo;
 template <> struct TypeInfo<T_Q4K> { static constexpr int BB = 144; static constexpr bool LINEAR = true;  static constexpr int XS_PER_CHUNK = 2; static constexpr bool SCALED = true; };
+template <> struct TypeInfo<T_Q4K_I8> { static constexpr int BB = 144; static constexpr bool LINEAR = true;  static constexpr int XS_PER_CHUNK = 4; static constexpr bool SCALED = false; };
+template <> struct TypeInfo<T_Q6K_I8> { static constexpr int BB = 210; static constexpr bool LINEAR = false; static constexpr int XS_PER_CHUNK = 8; static constexpr bool SCALED = false; };
 template <> struct TypeInfo<T_Q6K> { static constexpr int BB = 210; static constexpr bool LINEAR = false; static constexpr int XS_PER_CHUNK = 0; static constexpr bool SCALED = false; };
 template <> struct TypeInfo<T_Q2K> { static constexpr int BB = 84;  static constexpr bool LINEAR = false; static constexpr int XS_PER_CHUNK = 4; static constexpr bool SCALED = true; };
 template <> struct TypeInfo<T_NIB> { static constexpr int BB = 148; static constexpr bool LINEAR = true;  static constexpr int XS_PER_CHUNK = 4; static constexpr bool SCALED = true; };
@@ -217,8 +231,12 @@ constexpr uint32_t KSC_SPAN = 117 - 24;
 
 template <int TYPE> struct XGroup {
     // float4 per group: 32 values for the types with 32-weight sub-blocks
-    static constexpr int G4 = (TYPE == T_Q4K || TYPE == T_Q5K || TYPE == T_Q80) ? 8 : 4;
+    // (and the int8 mode's per-32 quantization), else 16
+    static constexpr int G4 =
+        (TYPE == T_Q4K || TYPE == T_Q5K || TYPE == T_Q80 || TYPE == T_Q4K_I8) ? 8 : 4;
     static constexpr bool SUMS = TypeInfo<TYPE>::XS_PER_CHUNK != 0;
+    static constexpr bool I8 = (TYPE & T_I8) != 0;
+    static constexpr int XSTRIDE = I8 ? XPAD_I8 : XPAD;   // float4 slots per chunk
 };
 
 // (e - KSC_ELO) as unsigned: >= KSC_SPAN when v is finite, nonzero and
@@ -316,6 +334,55 @@ __device__ __forceinline__ void resum(int K, int ngx, int tid, int T, const floa
         }
         xs[gx * per + xsi] = ks ? ldexpf(acc, -ks) : acc;
     }
+}
+
+// int8 staging (q4k_quantize_x_q8, stratum_q4k_neon.h:230-277, per 32;
+// q6k_quantize_x_q8_g16, stratum_q6k_neon.h:117-133, per 16): a lane
+// quantizes the group it loaded -- amax = max |x|, scale = fl(amax / 127),
+// inv = scale > 0 ? fl(1 / scale) : 0, q = clamp(rne(fl(x * inv)), -128,
+// 127) -- and writes the int8 values to the chunk's slot (Q4_K: sub-block
+// gi at byte 80(gi/2) + 32(gi&1); Q6_K: the 16-group at positions 16gi, run
+// t of chunk (block, half, is), at byte 80c + 16t) and {scale, sum} to the
+// group's two floats (Q4_K: 4 per chunk; Q6_K: 8).  x must be finite.
+template <int TYPE>
+__device__ __forceinline__ void store_i8(int gidx, int per, int NC, const f32x4* v, uint8_t* xq,
+                                         float* xs) {
+    constexpr int G4 = XGroup<TYPE>::G4;
+    const int gx = gidx / per, gi = gidx - gx * per;
+    float amax = 0.0f;
+#pragma unroll
+    for (int q = 0; q < G4; q++)
+        amax = fmaxf(fmaxf(fmaxf(amax, fabsf(v[q].x)), fmaxf(fabsf(v[q].y), fabsf(v[q].z))),
+                     fabsf(v[q].w));
+    const float scale = __fdiv_rn(amax, 127.0f);
+    const float inv = scale > 0.0f ? __fdiv_rn(1.0f, scale) : 0.0f;
+    int sum = 0;
+    uint32_t packed[G4];
+#pragma unroll
+    for (int q = 0; q < G4; q++) {
+        const float e[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+        uint32_t w = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int iv = min(127, max(-128, __float2int_rn(e[i] * inv)));
+            sum += iv;
+            w |= ((uint32_t)iv & 0xffu) << (8 * i);
+        }
+        packed[q] = w;
+    }
+    int c, off, slot;
+    if (TYPE == T_Q4K_I8) {
+        c = gi >> 1; off = 32 * (gi & 1); slot = 2 * gi;
+    } else {
+        const int p = 16 * gi, bi = p >> 8, h = (p >> 7) & 1, t = (p >> 5) & 3, is = (p >> 4) & 1;
+        c = 4 * bi + 2 * h + is; off = 16 * t; slot = 8 * c + 2 * t;
+    }
+    uint4* dst = reinterpret_cast<uint4*>(xq + (size_t)(gx * NC + c) * 80 + off);
+#pragma unroll
+    for (int q = 0; q < G4; q += 4)
+        dst[q / 4] = make_uint4(packed[q], packed[q + 1], packed[q + 2], packed[q + 3]);
+    float2* xs2 = reinterpret_cast<float2*>(xs + (size_t)gx * NC * TypeInfo<TYPE>::XS_PER_CHUNK + slot);
+    *xs2 = make_float2(scale, (float)sum);
 }
 
 // ------------------------------------------------------------ raw loads
@@ -935,8 +1002,103 @@ __device__ __forceinline__ double term_q80(const RawQ8& r, const float4* xc, dou
     return acc;
 }
 
+// Q4_K chunk j with int8 activations: exact integer dots L, H of the two
+// sub-blocks (v_dot4), coefficients as q4k_dot_row_sdot_f forms them
+// (stratum_q4k_neon.h:389-392: fl(fl(d*sc)*xs), fl(fl(-dmin*m)*xs)), and
+// each sub-block's term c1*L + c2*xsum formed exactly in binary64 (the
+// products are exact; one rounding).  xq: the chunk's 16 dwords; xs4 =
+// {scale, sum} of the two sub-blocks.
+__device__ __forceinline__ double term_q4k_i8(const RawQ4& r, int j, const uint32_t* xq,
+                                              float4 xs4) {
+    const float d = f16_bits_to_f32(r.hd.x & 0xffffu);
+    const float dmin = f16_bits_to_f32(r.hd.x >> 16);
+    uint32_t sc1, mn1, sc2, mn2;
+    scale_min_pair(r.hd.y, r.hd.z, r.hd.w, j, sc1, mn1, sc2, mn2);
+    const uint4 xa = reinterpret_cast<const uint4*>(xq)[0], xb = reinterpret_cast<const uint4*>(xq)[1];
+    const uint4 xc = reinterpret_cast<const uint4*>(xq)[2], xd = reinterpret_cast<const uint4*>(xq)[3];
+    const uint32_t lo_x[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+    const uint32_t hi_x[8] = {xc.x, xc.y, xc.z, xc.w, xd.x, xd.y, xd.z, xd.w};
+    int L = 0, H = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const uint32_t v = k < 4 ? dw_of(r.qa, k) : dw_of(r.qb, k - 4);
+        L = __builtin_amdgcn_sdot4((int)(v & 0x0f0f0f0fu), (int)lo_x[k], L, false);
+        H = __builtin_amdgcn_sdot4((int)((v >> 4) & 0x0f0f0f0fu), (int)hi_x[k], H, false);
+    }
+    const float c1 = d * (float)sc1 * xs4.x, c2 = -dmin * (float)mn1 * xs4.x;
+    const float c3 = d * (float)sc2 * xs4.z, c4 = -dmin * (float)mn2 * xs4.z;
+    const double t1 = fma((double)c1, (double)L, (double)c2 * (double)xs4.y);
+    const double t2 = fma((double)c3, (double)H, (double)c4 * (double)xs4.w);
+    return t1 + t2;
+}
+
+// Q6_K chunk (half h, sub is) with int8 activations per 16
+// (q6k_dot_row_sdot_f, stratum_q6k_neon.h:265-317): run t holds the
+// unsigned 6-bit values; g4 = their exact dot with the run's 16 quantized
+// values minus 32 * the group's x sum; the coefficient fl(fl(d*sc)*xs);
+// term c * g4 exact in binary64, summed over t in order.  xs8 = {scale,
+// sum} of the four groups.
+__device__ __forceinline__ double term_q6k_i8(const RawQ6& r, int u, const uint32_t* xq,
+                                              const float* xs8) {
+    int acc[4] = {0, 0, 0, 0};
+    const uint32_t sh = r.sh;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint32_t L = __builtin_amdgcn_alignbit(r.l[k + 1], r.l[k], sh);
+        const uint32_t H = __builtin_amdgcn_alignbit(r.h[k + 1], r.h[k], sh);
+        const uint32_t Q = __builtin_amdgcn_alignbit(r.q[k + 1], r.q[k], sh);
+        const uint32_t y[4] = {(L & 0x0f0f0f0fu) | ((Q & 0x03030303u) << 4),
+                               (H & 0x0f0f0f0fu) | (((Q >> 2) & 0x03030303u) << 4),
+                               ((L >> 4) & 0x0f0f0f0fu) | (((Q >> 4) & 0x03030303u) << 4),
+                               ((H >> 4) & 0x0f0f0f0fu) | (((Q >> 6) & 0x03030303u) << 4)};
+#pragma unroll
+        for (int t = 0; t < 4; t++) acc[t] = __builtin_amdgcn_sdot4((int)y[t], (int)xq[4 * t + k], acc[t], false);
+    }
+    const int is = u & 1;
+    const uint32_t S0 = __builtin_amdgcn_alignbit(r.s[1], r.s[0], sh);
+    const uint32_t S1 = __builtin_amdgcn_alignbit(r.s[2], r.s[1], sh);
+    const uint32_t Sa = is ? (S0 >> 8) : S0, Sb = is ? (S1 >> 8) : S1;
+    const int scv[4] = {(int8_t)(uint8_t)Sa, (int8_t)(uint8_t)(Sa >> 16), (int8_t)(uint8_t)Sb,
+                        (int8_t)(uint8_t)(Sb >> 16)};
+    const float d = f16_bits_to_f32(r.d);
+    double t = 0.0;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const float c = d * (float)scv[q] * xs8[2 * q];
+        const int g4 = acc[q] - 32 * (int)xs8[2 * q + 1];
+        t = t + (double)c * (double)g4;
+    }
+    return t;
+}
+
 // ------------------------------------------------------ per-type dispatch
 template <int TYPE> struct Chunk;
+template <> struct Chunk<T_Q4K_I8> {
+    using Raw = RawQ4;
+    static __device__ __forceinline__ Raw load(wptr blk, int u) { return load_q4k(blk, u); }
+    static __device__ __forceinline__ void drain(const Raw& r) {
+        asm volatile("" ::"v"(r.hd.x), "v"(r.qa.x), "v"(r.qb.x));
+    }
+    template <bool SC, bool LOWREG = false>
+    static __device__ __forceinline__ double term(const Raw& r, int u, const float4* xc,
+                                                  const float* xs, int c, float, double) {
+        return term_q4k_i8(r, u, reinterpret_cast<const uint32_t*>(xc),
+                           reinterpret_cast<const float4*>(xs)[c]);
+    }
+};
+template <> struct Chunk<T_Q6K_I8> {
+    using Raw = RawQ6;
+    static __device__ __forceinline__ Raw load(wptr blk, int u) { return load_q6k(blk, u); }
+    static __device__ __forceinline__ void drain(const Raw& r) {
+        asm volatile("" ::"v"(r.l[0]), "v"(r.l[4]), "v"(r.h[0]), "v"(r.h[4]), "v"(r.q[0]),
+                     "v"(r.q[4]), "v"(r.s[0]), "v"(r.s[1]), "v"(r.s[2]), "v"(r.d));
+    }
+    template <bool SC, bool LOWREG = false>
+    static __device__ __forceinline__ double term(const Raw& r, int u, const float4* xc,
+                                                  const float* xs, int c, float, double) {
+        return term_q6k_i8(r, u, reinterpret_cast<const uint32_t*>(xc), xs + 8 * c);
+    }
+};
 
 template <> struct Chunk<T_Q4K> {
     using Raw = RawQ4;
@@ -1241,8 +1403,9 @@ __device__ __forceinline__ void sweep(const Walk<TYPE, PM>& W, int nch, int u, i
             if (base[k] < nch) {                 // uniform over the wave
                 const int fi = base[k] + W.lane;
                 __builtin_assume(cx[k] >= 0 && cx[k] < (1 << 24));   // 24-bit multiply
-                const double t = C::template term<SC>(buf[k], u, xl + cx[k] * XPAD, xs, cx[k],
-                                                      f, f6);
+                const double t = C::template term<SC>(buf[k], u,
+                                                      xl + cx[k] * XGroup<TYPE>::XSTRIDE, xs,
+                                                      cx[k], f, f6);
                 if (fi < nch) terms[fi] = t;
             }
             base[k] = __builtin_amdgcn_readfirstlane(nb);
@@ -1351,7 +1514,9 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
     // unless the window already failed for it.
     constexpr bool SCTYPE = TI::SCALED;
     const int xst = ngx > 1 ? S.x_stride : 0;
-    const bool same_x = st.x == S.x && st.K == K && st.layout == (int)TI::LINEAR && st.ngx == ngx &&
+    // x layouts: 0 strided fp32, 1 linear fp32, 2 / 3 int8 per 32 / per 16
+    constexpr int LAYOUT = XGroup<TYPE>::I8 ? (TYPE == T_Q4K_I8 ? 2 : 3) : (int)TI::LINEAR;
+    const bool same_x = st.x == S.x && st.K == K && st.layout == LAYOUT && st.ngx == ngx &&
                         st.xst == xst;
     const bool restage = !same_x || (SCTYPE && st.k == 0 && !st.bad);
     constexpr int G4 = XGroup<TYPE>::G4;
@@ -1433,7 +1598,25 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
         buf[k] = C::load(W.locate(base[k], cx[k]), u);
     }
 
-    if (restage) {
+    if (XGroup<TYPE>::I8 && restage) {
+        uint8_t* xq = reinterpret_cast<uint8_t*>(xl);
+        const int per = xg.per;
+        if (tid < xg.total) store_i8<TYPE>(tid, per, NC, xv, xq, xs);
+        int gi0 = tid + T;
+        if (PRE2 && two) {
+            if (gi0 < xg.total) store_i8<TYPE>(gi0, per, NC, xv2, xq, xs);
+            gi0 += T;
+        }
+        for (int gi = gi0; gi < xg.total; gi += T) {
+            xg.load(gi, xv);
+            store_i8<TYPE>(gi, per, NC, xv, xq, xs);
+        }
+        __syncthreads();
+        st.x = S.x; st.K = K; st.layout = LAYOUT; st.ngx = ngx; st.xst = xst;
+        st.sums = TYPE;
+        st.k = 0;
+        st.bad = false;
+    } else if (restage) {
         bool bad = xg.store(tid, xv, SCTYPE, true, xl, xs);
         int gi0 = tid + T;
         if (PRE2 && two) {
@@ -1449,7 +1632,7 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
         __syncthreads();
         int any = 0;
         for (int i = 0; i < (T >> 6); i++) any |= flags[i];
-        st.x = S.x; st.K = K; st.layout = (int)TI::LINEAR; st.ngx = ngx; st.xst = xst;
+        st.x = S.x; st.K = K; st.layout = LAYOUT; st.ngx = ngx; st.xst = xst;
         st.sums = TI::XS_PER_CHUNK ? TYPE : 0;
         st.k = SCTYPE ? KSC : 0;
         st.bad = SCTYPE && any;
@@ -1461,7 +1644,7 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
             __syncthreads();
             st.k = 0;
         }
-    } else if (TI::XS_PER_CHUNK && st.sums != TYPE) {   // sums are laid out per type
+    } else if (!XGroup<TYPE>::I8 && TI::XS_PER_CHUNK && st.sums != TYPE) {   // sums per type
         resum<TYPE>(K, ngx, tid, T, xl, xs, st.k);
         __syncthreads();
         st.sums = TYPE;
@@ -1534,7 +1717,7 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
 // by the others.  Launches that mix types run the TB_ALL kernel (the first
 // four types); the host gives each of the other types launches of its own.
 constexpr int TB_Q4K = 1, TB_Q6K = 2, TB_Q2K = 4, TB_NIB = 8, TB_ALL = 15;
-constexpr int TB_Q5K = 32, TB_Q3K = 64, TB_Q80 = 128;
+constexpr int TB_Q5K = 32, TB_Q3K = 64, TB_Q80 = 128, TB_Q4K_I8 = 256, TB_Q6K_I8 = 512;
 // TB_SEL: the MoE gather instantiations (every segment has a selection)
 constexpr int TB_SEL = 16;
 
@@ -1566,7 +1749,8 @@ __global__ __launch_bounds__(1024) void kq_segs_kernel(SegsArg A) {
     constexpr bool SELK = (TYPES & TB_SEL) != 0;    // MoE gather: every segment has sel
     constexpr int TYB = TYPES & ~TB_SEL;
     constexpr bool SINGLE = TYB == TB_Q4K || TYB == TB_Q6K || TYB == TB_Q2K || TYB == TB_NIB ||
-                            TYB == TB_Q5K || TYB == TB_Q3K || TYB == TB_Q80;
+                            TYB == TB_Q5K || TYB == TB_Q3K || TYB == TB_Q80 ||
+                            TYB == TB_Q4K_I8 || TYB == TB_Q6K_I8;
     for (int i = 0; i < nseg; i++) {
         const Seg& S = A.s[i];
         if (i) prefetch_seg(S);
@@ -1580,7 +1764,8 @@ __global__ __launch_bounds__(1024) void kq_segs_kernel(SegsArg A) {
         if (SINGLE) {
             constexpr int TY = TYB == TB_Q4K ? T_Q4K : TYB == TB_Q6K ? T_Q6K
                              : TYB == TB_Q2K ? T_Q2K : TYB == TB_NIB ? T_NIB
-                             : TYB == TB_Q5K ? T_Q5K : TYB == TB_Q3K ? T_Q3K : T_Q80;
+                             : TYB == TB_Q5K ? T_Q5K : TYB == TB_Q3K ? T_Q3K
+                             : TYB == TB_Q80 ? T_Q80 : TYB == TB_Q4K_I8 ? T_Q4K_I8 : T_Q6K_I8;
             KQ_RUN(TY)
         } else {
             switch (S.type) {
@@ -2909,6 +3094,43 @@ __global__ __launch_bounds__(256) void kq_dense_dequant_kernel(const uint8_t* w,
     }
 }
 
+// x -> int8 per group of G (32: q4k_quantize_x_q8 + q4k_sum_i8_32; 16:
+// q6k_quantize_x_q8_g16 + q6k_xsum16_i8), the arithmetic of store_i8: one
+// lane per group.
+template <int G>
+__global__ __launch_bounds__(256) void kq_quantize_kernel(const float* x, int ngroups, int8_t* xq,
+                                                          float* xscale, int* xsum) {
+    const int g = blockIdx.x * 256 + threadIdx.x;
+    if (g >= ngroups) return;
+    const f32x4* src = reinterpret_cast<const f32x4*>(x) + (size_t)g * (G / 4);
+    f32x4 v[G / 4];
+#pragma unroll
+    for (int q = 0; q < G / 4; q++) v[q] = src[q];
+    float amax = 0.0f;
+#pragma unroll
+    for (int q = 0; q < G / 4; q++)
+        amax = fmaxf(fmaxf(fmaxf(amax, fabsf(v[q].x)), fmaxf(fabsf(v[q].y), fabsf(v[q].z))),
+                     fabsf(v[q].w));
+    const float scale = __fdiv_rn(amax, 127.0f);
+    const float inv = scale > 0.0f ? __fdiv_rn(1.0f, scale) : 0.0f;
+    int sum = 0;
+    uint32_t* dst = reinterpret_cast<uint32_t*>(xq + (size_t)g * G);
+#pragma unroll
+    for (int q = 0; q < G / 4; q++) {
+        const float e[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+        uint32_t w = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int iv = min(127, max(-128, __float2int_rn(e[i] * inv)));
+            sum += iv;
+            w |= ((uint32_t)iv & 0xffu) << (8 * i);
+        }
+        dst[q] = w;
+    }
+    xscale[g] = scale;
+    if (xsum) xsum[g] = sum;
+}
+
 template <int TYPE>
 int launch_dequant(const uint8_t* w, float* y, long nblocks, hipStream_t st) {
     const long nch = nblocks * 4;
@@ -2976,6 +3198,8 @@ static int xs_per_chunk(int type) {
     case T_Q5K: return TypeInfo<T_Q5K>::XS_PER_CHUNK;
     case T_Q3K: return TypeInfo<T_Q3K>::XS_PER_CHUNK;
     case T_Q80: return TypeInfo<T_Q80>::XS_PER_CHUNK;
+    case T_Q4K_I8: return TypeInfo<T_Q4K_I8>::XS_PER_CHUNK;
+    case T_Q6K_I8: return TypeInfo<T_Q6K_I8>::XS_PER_CHUNK;
     default: return -1;
     }
 }
@@ -2989,6 +3213,8 @@ static int block_bytes_of(int type) {
     case T_Q5K: return TypeInfo<T_Q5K>::BB;
     case T_Q3K: return TypeInfo<T_Q3K>::BB;
     case T_Q80: return TypeInfo<T_Q80>::BB;
+    case T_Q4K_I8: return TypeInfo<T_Q4K_I8>::BB;
+    case T_Q6K_I8: return TypeInfo<T_Q6K_I8>::BB;
     default: return 0;
     }
 }
@@ -3003,6 +3229,8 @@ static int type_slot(int type) {
     case T_Q5K: return 5;
     case T_Q3K: return 6;
     case T_Q80: return 7;
+    case T_Q4K_I8: return 8;
+    case T_Q6K_I8: return 9;
     default: return -1;
     }
 }
@@ -3034,7 +3262,8 @@ long kqk_segs_lds(const kqk_seg* segs, int nseg, int grid, int* xs_off, int* ter
         if (N > 0x7fffffffL) return -1;
         const long NC = g.K >> 6;
         const long ngx = g.x_stride && g.nparts > 1 ? g.nparts : 1;
-        xl = xl > ngx * NC * XPAD * 16 ? xl : ngx * NC * XPAD * 16;
+        const long xb = ngx * NC * ((g.type & T_I8) ? XPAD_I8 : XPAD) * 16;   // int8: 80 B/chunk
+        xl = xl > xb ? xl : xb;
         xsb = xsb > ngx * NC * xpc * 4 ? xsb : ngx * NC * xpc * 4;
         const long R = (N + grid - 1) / grid;
         tb = tb > R * NC * 8 ? tb : R * NC * 8;
@@ -3056,26 +3285,29 @@ long kqk_segs_lds(const kqk_seg* segs, int nseg, int grid, int* xs_off, int* ter
     {&kq_segs_kernel<D, TB_Q4K, M>, &kq_segs_kernel<D, TB_Q6K, M>,              \
      &kq_segs_kernel<D, TB_Q2K, M>, &kq_segs_kernel<D, TB_NIB, M>,              \
      &kq_segs_kernel<D, TB_ALL, M>, &kq_segs_kernel<D, TB_Q5K, M>,              \
-     &kq_segs_kernel<D, TB_Q3K, M>, &kq_segs_kernel<D, TB_Q80, M>}
+     &kq_segs_kernel<D, TB_Q3K, M>, &kq_segs_kernel<D, TB_Q80, M>,              \
+     &kq_segs_kernel<D, TB_Q4K_I8, M>, &kq_segs_kernel<D, TB_Q6K_I8, M>}
 typedef void (*segs_fn)(SegsArg);
-static const segs_fn k_segs[2][2][8] = {{KQ_SEGS_ROW(1, false), KQ_SEGS_ROW(2, false)},
+static const segs_fn k_segs[2][2][10] = {{KQ_SEGS_ROW(1, false), KQ_SEGS_ROW(2, false)},
                                         {KQ_SEGS_ROW(1, true), KQ_SEGS_ROW(2, true)}};
 #undef KQ_SEGS_ROW
-// the MoE gather (TB_SEL) instantiations, single type only (slot 4 unused)
+// the MoE gather (TB_SEL) instantiations, single type only (slots 4, 8
+// and 9 unused: the mixed kernel and the int8 mode have no gather form)
 #define KQ_SEL_ROW(D, M)                                                                  \
     {&kq_segs_kernel<D, TB_Q4K | TB_SEL, M>, &kq_segs_kernel<D, TB_Q6K | TB_SEL, M>,       \
      &kq_segs_kernel<D, TB_Q2K | TB_SEL, M>, &kq_segs_kernel<D, TB_NIB | TB_SEL, M>,       \
      &kq_segs_kernel<D, TB_Q4K | TB_SEL, M>, &kq_segs_kernel<D, TB_Q5K | TB_SEL, M>,       \
-     &kq_segs_kernel<D, TB_Q3K | TB_SEL, M>, &kq_segs_kernel<D, TB_Q80 | TB_SEL, M>}
-static const segs_fn k_segs_sel[2][2][8] = {{KQ_SEL_ROW(1, false), KQ_SEL_ROW(2, false)},
+     &kq_segs_kernel<D, TB_Q3K | TB_SEL, M>, &kq_segs_kernel<D, TB_Q80 | TB_SEL, M>,       \
+     &kq_segs_kernel<D, TB_Q4K | TB_SEL, M>, &kq_segs_kernel<D, TB_Q4K | TB_SEL, M>}
+static const segs_fn k_segs_sel[2][2][10] = {{KQ_SEL_ROW(1, false), KQ_SEL_ROW(2, false)},
                                             {KQ_SEL_ROW(1, true), KQ_SEL_ROW(2, true)}};
 #undef KQ_SEL_ROW
 
 int kqk_set_max_lds(int bytes) {
     for (int m = 0; m < 2; m++)
         for (int d = 0; d < 2; d++)
-            for (int t = 0; t < 16; t++) {
-                const segs_fn f = t < 8 ? k_segs[m][d][t] : k_segs_sel[m][d][t - 8];
+            for (int t = 0; t < 20; t++) {
+                const segs_fn f = t < 10 ? k_segs[m][d][t] : k_segs_sel[m][d][t - 10];
                 const hipError_t e =
                     hipFuncSetAttribute(reinterpret_cast<const void*>(f),
                                         hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
@@ -3135,16 +3367,17 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
         magic_for((uint32_t)(h.K >> 6), d.nc_m, d.nc_l);
         set |= h.type == T_Q4K ? TB_Q4K : h.type == T_Q6K ? TB_Q6K : h.type == T_Q2K ? TB_Q2K
              : h.type == T_NIB ? TB_NIB : h.type == T_Q5K ? TB_Q5K : h.type == T_Q3K ? TB_Q3K
-             : TB_Q80;
+             : h.type == T_Q80 ? TB_Q80 : h.type == T_Q4K_I8 ? TB_Q4K_I8 : TB_Q6K_I8;
     }
     const int t = set == TB_Q4K ? 0 : set == TB_Q6K ? 1 : set == TB_Q2K ? 2 : set == TB_NIB ? 3
                 : set == TB_Q5K ? 5 : set == TB_Q3K ? 6 : set == TB_Q80 ? 7
+                : set == TB_Q4K_I8 ? 8 : set == TB_Q6K_I8 ? 9
                 : (set & ~TB_ALL) ? -1 : 4;
     if (t < 0) return (int)hipErrorInvalidValue;   // other types are never mixed in a launch
     if (t == 4) depth = 1;   // the all-types kernel fits 128 VGPRs at depth 1 only
     int nsel = 0;
     for (int i = 0; i < nseg; i++) nsel += segs[i].sel != nullptr;
-    if (nsel && (nsel != nseg || t == 4)) return (int)hipErrorInvalidValue;
+    if (nsel && (nsel != nseg || t == 4 || t >= 8)) return (int)hipErrorInvalidValue;
     const segs_fn f = nsel ? k_segs_sel[nseg > 1][depth - 1][t] : k_segs[nseg > 1][depth - 1][t];
     hipLaunchKernelGGL(f, dim3(grid), dim3(threads), (size_t)lds_bytes, st, A);
     return (int)hipGetLastError();
@@ -3420,6 +3653,19 @@ int kqk_launch_dequant(int type, const void* w, float* y, long nblocks, hipStrea
     }
     default: return -1;
     }
+}
+
+int kqk_launch_quantize_q8(const float* x, int K, int group, int8_t* xq, float* xscale, int* xsum,
+                           hipStream_t st) {
+    if ((group != 32 && group != 16) || K < group || K % group) return (int)hipErrorInvalidValue;
+    const int ng = K / group;
+    if (group == 32)
+        hipLaunchKernelGGL(kq_quantize_kernel<32>, dim3((ng + 255) / 256), dim3(256), 0, st, x, ng, xq,
+                           xscale, xsum);
+    else
+        hipLaunchKernelGGL(kq_quantize_kernel<16>, dim3((ng + 255) / 256), dim3(256), 0, st, x, ng, xq,
+                           xscale, xsum);
+    return (int)hipGetLastError();
 }
 
 // Dense rows (F16, F32): x staged in LDS when K <= DENSE_XLDS_MAX

@@ -41,6 +41,9 @@ int kqk_launch_dequant(int type, const void* w, float* y, long nblocks, hipStrea
 int kqk_launch_dense(int type, const void* w, const float* x, const float* add, float* y, int N,
                      int K, int grid, hipStream_t st);
 int kqk_dense_set_max_lds(int bytes);
+/* x -> int8 per group (32 or 16), scales, integer sums (xsum may be NULL) */
+int kqk_launch_quantize_q8(const float* x, int K, int group, int8_t* xq, float* xscale, int* xsum,
+                           hipStream_t st);
 int kqk_set_max_lds(int bytes);
 /* multi-x launcher: plan[] = threads, S, RB, nblk, TC, sums bytes, x buffer
  * bytes, members staged together (kqk_mx_plan returns the LDS bytes, or

@@ -52,6 +52,7 @@ typedef struct {
     /* launch overrides from the environment (0: unset), read by kq_ready
      * and again only by kq_tuning_reload: the planner runs on every call */
     int env_grid, env_threads, env_depth, env_moe_group_launch;
+    int use_sdot;          /* host-pointer ABI: Q4_K / Q6_K in the int8 mode */
     char err[512];
 } kq_state;
 
@@ -68,8 +69,11 @@ static int kq_fail(const char* fmt, ...) {
 
 const char* kq_last_error(void) { return g_kq.err; }
 
-/* bytes per 256 weights (stratum_gguf.h:57-79; Q8_0: eight 34-byte blocks) */
+/* bytes per 256 weights (stratum_gguf.h:57-79; Q8_0: eight 34-byte blocks);
+ * the int8-activation mode of Q4_K / Q6_K (KQ_INT8_ACT) keeps the blocks */
 static int block_bytes(int type) {
+    if (type == (KQ_INT8_ACT | KQ_TYPE_Q4_K)) return 144;
+    if (type == (KQ_INT8_ACT | KQ_TYPE_Q6_K)) return 210;
     switch (type) {
     case KQ_TYPE_F32: return 1024;
     case KQ_TYPE_F16: return 512;
@@ -636,6 +640,32 @@ int kq_dequant_dev(int type, const void* w, float* y, int64_t nblocks, kq_stream
 
 /* --------------------------------------------------- host-pointer ABI */
 
+/* st_linear_q4k / st_linear_q6k take the SDOT (int8-activation) path when
+ * g_st.use_sdot is set (stratum_linear.h:369-409): the same switch for the
+ * host-pointer entry points */
+static int sdot_type(int type) {
+    return g_kq.use_sdot && (type == KQ_TYPE_Q4_K || type == KQ_TYPE_Q6_K) ? type | KQ_INT8_ACT
+                                                                          : type;
+}
+
+int kq_linear_set_sdot(int on) {
+    const int prev = g_kq.use_sdot;
+    g_kq.use_sdot = on != 0;
+    return prev;
+}
+
+int kq_quantize_x_q8_dev(const float* x, int K, int group, int8_t* xq, float* xscale,
+                         int32_t* xsum, kq_stream stream) {
+    if (kq_ready()) return -1;
+    if (!x || !xq || !xscale) return kq_fail("kq_quantize_x_q8_dev: NULL pointer");
+    if ((group != 32 && group != 16) || K <= 0 || K % group)
+        return kq_fail("kq_quantize_x_q8_dev: group %d, K %d", group, K);
+    if ((uintptr_t)x & 15) return kq_fail("kq_quantize_x_q8_dev: x must be 16-byte aligned");
+    const int e = kqk_launch_quantize_q8(x, K, group, xq, xscale, (int*)xsum, pick(stream));
+    if (e) return kq_fail("quantize launch: %s", hipGetErrorString((hipError_t)e));
+    return 0;
+}
+
 static int h2d(float* d, const float* h, size_t n) {
     return hip_ok(hipMemcpyAsync(d, h, n * sizeof(float), hipMemcpyHostToDevice, g_kq.stream),
                   "copy x in");
@@ -661,7 +691,8 @@ int kq_linear_dispatch_add(const kq_tensor* w, const float* x, const float* add,
         if (grow(&g_kq.d_a, &g_kq.cap_a, (size_t)N) || h2d(g_kq.d_a, add, (size_t)N)) return -1;
         d_add = g_kq.d_a;
     }
-    if (kq_gemv_dev((int)w->type, dw, g_kq.d_x, d_add, g_kq.d_y, N, K, g_kq.stream)) return -1;
+    if (kq_gemv_dev(sdot_type((int)w->type), dw, g_kq.d_x, d_add, g_kq.d_y, N, K, g_kq.stream))
+        return -1;
     return finish_y(y, g_kq.d_y, (size_t)N);
 }
 
@@ -680,7 +711,8 @@ int kq_linear_multix(const kq_tensor* w, const float* const* xs, float* const* y
         grow(&g_kq.d_y, &g_kq.cap_y, (size_t)B * N)) return -1;
     for (int s = 0; s < B; s++)
         if (h2d(g_kq.d_x + (size_t)s * K, xs[s], (size_t)K)) return -1;
-    if (kq_gemv_multix_dev((int)w->type, dw, g_kq.d_x, g_kq.d_y, B, N, K, g_kq.stream)) return -1;
+    if (kq_gemv_multix_dev(sdot_type((int)w->type), dw, g_kq.d_x, g_kq.d_y, B, N, K, g_kq.stream))
+        return -1;
     for (int s = 0; s < B; s++)
         if (hip_ok(hipMemcpyAsync(ys[s], g_kq.d_y + (size_t)s * N, (size_t)N * sizeof(float),
                                   hipMemcpyDeviceToHost, g_kq.stream), "copy y out"))
@@ -705,7 +737,7 @@ int kq_q4k_group(const float* x, int K,
         if (check_shape((int)ws[i]->type, Ns[i], K)) return -1;
         const void* dw = tensor_dev(ws[i], Ns[i], K);
         if (!dw) return -1;
-        sg[i].type = (int)ws[i]->type; sg[i].K = K; sg[i].rows_per_group = Ns[i];
+        sg[i].type = sdot_type((int)ws[i]->type); sg[i].K = K; sg[i].rows_per_group = Ns[i];
         sg[i].ngroups = 1; sg[i].w[0] = dw;
         ytot += (size_t)Ns[i];
     }
@@ -870,6 +902,7 @@ static int moe_one_token(const kq_moe_op* op, const int* sel, int k, int E, cons
 static int moe_check_op(const kq_moe_op* op, int k, int E, const char* who) {
     if (check_shape(op->type, op->n_out, op->k_in) || kq_ready()) return -1;
     if (is_dense(op->type)) return kq_fail("%s: dense (F16/F32) experts are not supported", who);
+    if (op->type & KQ_INT8_ACT) return kq_fail("%s: the int8-activation mode has no MoE form", who);
     const int nt = op->ntensors;
     if (nt < 1 || nt > 2) return kq_fail("%s: ntensors=%d", who, nt);
     if (op->x_div != 1 && op->x_div != k) return kq_fail("%s: x_div must be 1 or k", who);

@@ -1,0 +1,165 @@
+"""The int8-activation restatement in oracle/kq_oracle.c, pinned on the CPU.
+
+The reference's SDOT kernels (stratum_q4k_neon.h, stratum_q6k_neon.h) need
+NEON and do not build here, so oracle/_ref cannot check this part.  What
+pins it instead:
+
+  * the quantizer against closed forms: groups whose largest |x| is
+    127 * 2^e quantize exactly (scale 2^e, q = x / 2^e), halfway values
+    round to even, zero groups give scale 0 and q 0, and for any x the
+    rounding error is at most half a step;
+  * the integer dots, group indexing and coefficients against the pinned
+    dequantization: with power-of-two d / dmin and exactly quantizable x,
+    every step is exact and the int8 GEMV must equal the binary64 sum of
+    dequant(w) * x (a wrong group, scale or sign breaks this);
+  * the reference's own test of the mode (quant_test.c:95-122): on its
+    data (d = 0.01, dmin = 0.001, x uniform in [-0.5, 0.5)) the result is
+    within 5e-2 relative of the exact dot;
+  * the two summation orders (binary32 FMA lanes of q*_dot_row_sdot_f vs
+    binary64 terms) within the lanes' rounding bound.
+"""
+import numpy as np
+import pytest
+
+from stratum_amd import TYPE_Q4_K, TYPE_Q6_K, synth
+
+I8_TYPES = [TYPE_Q4_K, TYPE_Q6_K]
+GROUP = {TYPE_Q4_K: 32, TYPE_Q6_K: 16}
+
+
+def exact_x(r, K, G, e):
+    """x whose every group has max |x| = 127 * 2^e and values k * 2^e"""
+    k = r.integers(-127, 128, K).astype(np.int32)
+    k.reshape(-1, G)[:, r.integers(0, G)] = np.where(r.integers(0, 2, K // G) > 0, 127, -127)
+    return (k.astype(np.float32) * np.float32(2.0 ** e)), k
+
+
+@pytest.mark.parametrize("G", [32, 16])
+def test_quantize_exact_groups(port, G):
+    r = synth.rng(7100 + G)
+    K = 1024
+    x, k = exact_x(r, K, G, -7)
+    xq, xs = port.quantize_q8(x, G)
+    assert np.array_equal(xq.astype(np.int32), k)
+    assert np.all(xs == np.float32(2.0 ** -7))
+
+
+@pytest.mark.parametrize("G", [32, 16])
+def test_quantize_halfway_zero_sign(port, G):
+    K = 4 * G
+    x = np.zeros(K, np.float32)
+    g0 = x[0:G]
+    g0[0] = 127.0
+    g0[1:9] = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -126.5]   # ties to even
+    x[G] = -127.0 * 4                                              # negative amax
+    x[G + 1] = 3.0 * 4
+    # group 2 stays zero; group 3: a denormal-free tiny group
+    x[3 * G:4 * G] = np.float32(1e-30)
+    xq, xs = port.quantize_q8(x, G)
+    assert list(xq[0:9]) == [127, 0, 2, 2, 0, -2, -2, 126, -126]
+    assert xs[0] == 1.0 and xs[1] == 4.0
+    assert xq[G] == -127 and xq[G + 1] == 3
+    assert xs[2] == 0.0 and not np.any(xq[2 * G:3 * G])
+    assert np.all(xq[3 * G:4 * G] == 127)
+
+
+@pytest.mark.parametrize("G", [32, 16])
+def test_quantize_error_bound(port, G):
+    r = synth.rng(7200 + G)
+    K = 8192
+    x = synth.gaussian(r, K) * np.float32(3.0)
+    xq, xs = port.quantize_q8(x, G)
+    amax = np.abs(x.reshape(-1, G)).max(axis=1)
+    assert np.all(xs == amax / np.float32(127.0))
+    step = np.repeat(xs.astype(np.float64), G)
+    err = np.abs(xq.astype(np.float64) * step - x.astype(np.float64))
+    assert np.all(err <= 0.5 * step * (1 + 2.0 ** -20))
+    assert np.all(np.abs(xq.astype(np.int32)) <= 127)
+    # the largest |x| of each group maps to +-127
+    imax = np.abs(x.reshape(-1, G)).argmax(axis=1)
+    top = xq.reshape(-1, G)[np.arange(K // G), imax].astype(np.int32)
+    assert np.all(np.abs(top) == 127)
+
+
+def pow2_blocks(qtype, r, nblocks, small=False):
+    """random blocks with d = 2^-10 (and dmin = 2^-12), so every product is
+    exact; small: scales (and mins) limited to 3 bits, so that the
+    reference's binary32 lanes stay exact too over one block"""
+    b = synth.blocks(qtype, r, nblocks).reshape(nblocks, -1)
+    if qtype == TYPE_Q4_K:
+        b[:, 0:2] = np.array([2.0 ** -10], np.float16).view(np.uint8)
+        b[:, 2:4] = np.array([2.0 ** -12], np.float16).view(np.uint8)
+        if small:
+            b[:, 4:16] = synth.pack_q4k_scales(r.integers(0, 8, (nblocks, 8)),
+                                               r.integers(0, 8, (nblocks, 8)))
+    else:
+        b[:, 208:210] = np.array([2.0 ** -10], np.float16).view(np.uint8)
+        if small:
+            b[:, 192:208] = r.integers(-4, 4, (nblocks, 16)).astype(np.int8).view(np.uint8)
+    return b.reshape(-1)
+
+
+@pytest.mark.parametrize("qtype", I8_TYPES)
+@pytest.mark.parametrize("case", ["wide", "small-f32-lanes", "small"])
+def test_i8_exact_against_dequant(port, qtype, case):
+    """exactly quantizable x and exact products: y == fl(sum dequant(w) * x).
+    'wide' (random scales, two blocks) holds for the binary64 order only;
+    'small' also for the reference's binary32 lanes (sdot_f)."""
+    r = synth.rng(7300 + qtype + (0 if case == "wide" else 50))
+    small = case != "wide"
+    N, K = 24, 256 if small else 512
+    w = pow2_blocks(qtype, r, N * K // 256, small)
+    x, _ = exact_x(r, K, GROUP[qtype], -7)
+    deq = port.dequant(qtype, w, N, K).reshape(N, K).astype(np.float64)
+    want = (deq * x.astype(np.float64)).sum(axis=1)          # exact in binary64
+    y = port.gemv_i8(qtype, w, x, N, K, sdot_f=case == "small-f32-lanes")
+    assert np.array_equal(y, want.astype(np.float32))
+
+
+@pytest.mark.parametrize("qtype", I8_TYPES)
+def test_i8_reference_quant_test_case(port, qtype):
+    """quant_test.c:95-122 (Q4_K) / :196-237 (Q6_K) data, rel err <= 5e-2"""
+    r = synth.rng(7400 + qtype)
+    N, K = 8, 1024
+    b = r.integers(0, 256, (N * K // 256, 144 if qtype == TYPE_Q4_K else 210), dtype=np.uint8)
+    if qtype == TYPE_Q4_K:
+        b[:, 0:2] = np.array([0.01], np.float16).view(np.uint8)
+        b[:, 2:4] = np.array([0.001], np.float16).view(np.uint8)
+    else:
+        b[:, 208:210] = np.array([0.01], np.float16).view(np.uint8)
+    w = b.reshape(-1)
+    x = (r.integers(0, 0x10000, K) / 32768.0 - 0.5).astype(np.float32)
+    deq = port.dequant(qtype, w, N, K).reshape(N, K).astype(np.float64)
+    ref = (deq * x.astype(np.float64)).sum(axis=1).astype(np.float32)
+    for sdot_f in (True, False):
+        y = port.gemv_i8(qtype, w, x, N, K, sdot_f=sdot_f)
+        rel = np.abs(y - ref) / np.maximum(np.abs(ref), 1e-6)
+        assert rel.max() <= 5e-2, (sdot_f, rel.max())
+
+
+@pytest.mark.parametrize("qtype", I8_TYPES)
+def test_i8_orders_within_lane_bound(port, qtype):
+    r = synth.rng(7500 + qtype)
+    N, K = 64, 4096
+    w = synth.blocks(qtype, r, N * K // 256)
+    x = synth.gaussian(r, K)
+    yg = port.gemv_i8(qtype, w, x, N, K)
+    yf, mag = port.gemv_i8(qtype, w, x, N, K, sdot_f=True, with_mag=True)
+    d = np.abs(yg.astype(np.float64) - yf.astype(np.float64))
+    bound = (K / 64 + 3) * 2.0 ** -24 * mag + 2.0 ** -24 * np.abs(yg.astype(np.float64))
+    assert np.all(d <= bound)
+    # int8 quantization error stays small against the exact fp32 path
+    y32 = port.gemv(qtype, w, x, N, K)
+    assert np.max(np.abs(yg - y32)) <= 5e-2 * np.max(np.abs(y32))
+
+
+@pytest.mark.parametrize("qtype", I8_TYPES)
+def test_i8_add(port, qtype):
+    r = synth.rng(7600 + qtype)
+    N, K = 16, 768
+    w = synth.blocks(qtype, r, N * K // 256)
+    x = synth.gaussian(r, K)
+    add = synth.gaussian(r, N)
+    y = port.gemv_i8(qtype, w, x, N, K)
+    ya = port.gemv_i8(qtype, w, x, N, K, add=add)
+    assert np.array_equal(ya, add + y)
