@@ -512,9 +512,68 @@ def cfg5(L, torch, stream, host_w) -> dict:
 
 
 # bench.py --only NAME runs one of these (the keys of other_configs' result)
+def cfg_int8(L, torch, stream, host_w) -> dict:
+    """configs[2] in the int8-activation mode (type | KQ_INT8_ACT, the
+    reference's SDOT path): the same four launches of the 27B layer set,
+    weights rotated over device copies.  Tolerance: within one binary32 ulp
+    of the binary64-term order, and within the binary32 lanes' rounding
+    bound of q*_dot_row_sdot_f (tests/test_gpu_int8.py)."""
+    sh = stream.cuda_stream
+    spec = {name: (t, N, K, xn) for name, t, N, K, xn in LAYER_27B}
+    xs_host = {k: synth.gaussian(synth.rng(2000 + j), n) for j, (k, n) in enumerate(X_LEN.items())}
+    xs = {k: torch.from_numpy(v).cuda() for k, v in xs_host.items()}
+    ys = {name: torch.empty(N, dtype=torch.float32, device="cuda") for name, _, N, _, _ in LAYER_27B}
+    offs, total = {}, 0
+    for name, *_ in LAYER_27B:
+        offs[name] = total
+        total += (host_w[name].size + 255) // 256 * 256
+    blob = np.zeros(total, np.uint8)
+    for name, *_ in LAYER_27B:
+        blob[offs[name]:offs[name] + host_w[name].size] = host_w[name]
+    copies = _copies(torch, blob, COPIES)
+    arrs = {}
+    for flag in (KQ.INT8_ACT, 0):
+        arrs[flag] = []
+        for c in copies:
+            per_group = []
+            for gname, members in GROUPS:
+                segs = [KQ.segment(spec[m][0] | flag, spec[m][2], spec[m][1],
+                                   [c.data_ptr() + offs[m]], xs[spec[m][3]].data_ptr(),
+                                   ys[m].data_ptr()) for m in members]
+                per_group.append(((KQ.KqSegment * len(segs))(*segs), len(segs)))
+            arrs[flag].append(per_group)
+
+    def launch(ci, g, flag=KQ.INT8_ACT):
+        arr, n = arrs[flag][ci % len(arrs[flag])][g]
+        _check(L, L.kq_gemv_segments_dev(arr, n, sh))
+
+    res = {}
+    set_bytes = sum(algo_bytes(t, N, K) for _, t, N, K, _ in LAYER_27B)
+    for flag, key in ((KQ.INT8_ACT, "layer_set"), (0, "layer_set_exact_same_process")):
+        us = _events_us(torch, stream,
+                        lambda i: [launch(i, g, flag) for g in range(len(GROUPS))], 100)
+        res[key] = {"us_per_layer_set": round(us, 2), "bytes": set_bytes,
+                    "GB/s": round(set_bytes / us / 1e3, 1)}
+    for g, (gname, members) in enumerate(GROUPS):
+        gus = _events_us(torch, stream, lambda i: launch(i, g), 100)
+        nb = sum(algo_bytes(spec[m][0], spec[m][1], spec[m][2]) for m in members)
+        res[gname] = {"us": round(gus, 2), "bytes": nb, "GB/s": round(nb / gus / 1e3, 1)}
+    if CPU["on"]:
+        from oracle import oracle as O
+        port = O.port()
+        res["layer_set"]["cpu"] = cpu_entry(
+            cpu_us(lambda: [port.gemv_i8(spec[m][0], host_w[m], xs_host[spec[m][3]], spec[m][1],
+                                         spec[m][2], sdot_f=True) for m, *_ in LAYER_27B],
+                   min_s=0.5, max_n=3),
+            "port", "the seven matvecs in q*_dot_row_sdot_f's order, one thread")
+        res["layer_set"]["cpu"]["cores"] = 1
+    del copies, arrs
+    return res
+
+
 OTHER = {"cfg1_q4k_1024x1024": cfg1, "cfg2_qwen3_0.6b": cfg2, "cfg3_gate_up_q2k_type42": cfg3,
          "cfg4_multiseq_exact": cfg4, "cfg4_multiseq_mfma": multiseq_mfma,
-         "cfg5_moe_128e_top8": cfg5}
+         "cfg5_moe_128e_top8": cfg5, "cfg3_int8_activations": cfg_int8}
 
 
 def _hbm_frac(o) -> None:

@@ -350,6 +350,64 @@ int kq_moe_gemv_dev(const kq_moe_op* op, const int* sel, int B, int k, int E, kq
 int kq_moe_gemv_routed_dev(const kq_moe_op* op, const float* probs, int B, int k, int E, int* sel,
                            float* selw, kq_stream stream);
 
+/* ---------------------------------------------------- MoE FFN step
+ * The pieces around the gather that make it the whole expert FFN step of
+ * the reference's MoE decode (stratum_arch_moe.inc.c:689-743 for one token,
+ * 1107-1226 for a batch).  Device pointers, enqueue only. */
+
+/* Softmax of B rows of E values in place: stratum_softmax_inplace
+ * (stratum_engine.h:395-423, its scalar path): max by the sequential scan,
+ * expf(x - max), the binary64 sum in index order, inv = (float)(1.0 / sum),
+ * x * inv.  expf is the device's (within one ulp of correctly rounded
+ * exp; the reference calls the host libm's), so probabilities agree with
+ * the reference's to a few binary32 ulps, not bit for bit.  E <=
+ * KQ_MOE_MAX_EXPERTS. */
+int kq_softmax_dev(float* x, int B, int E, kq_stream stream);
+
+/* SwiGLU y = (g / (1 + expf(-g))) * u over n values: stratum_swiglu
+ * (stratum_engine.h:373-392, its scalar loop), binary32 with the device
+ * expf (same caveat).  g, u, y 16-byte aligned. */
+int kq_swiglu_dev(const float* g, const float* u, float* y, int64_t n, kq_stream stream);
+
+/* Rank-ordered weighted accumulate plus the residual
+ * (stratum_arch_moe.inc.c:728-743; batches :1213-1226): for token s < B,
+ * x[s][i] = resid[s][i] + (((0 + selw[s][0] o[s*k][i]) + selw[s][1]
+ * o[s*k+1][i]) + ...), ranks with sel < 0 skipped, every product and sum
+ * rounded in binary32 -- bit-identical to the reference's loop.  o holds
+ * B*k rows of H (member m = s*k + r), x may equal resid.  H % 4 == 0. */
+int kq_moe_combine_dev(const float* o, const int* sel, const float* selw, const float* resid,
+                       float* x, int B, int k, int H, kq_stream stream);
+
+/* One MoE layer's expert tensors: the router (ffn_gate_inp, n_experts rows
+ * of n_embed, any GEMV type; F32 in the usual GGUF) and expert 0's slice
+ * of each stacked expert tensor with the byte stride between experts
+ * (kq_moe_slice_bytes, or the pack stride). */
+typedef struct kq_moe_ffn {
+    int n_embed, n_ff, n_experts, k;
+    int router_type;
+    const void* router;
+    int gate_type, up_type, down_type;
+    const void* gate;
+    const void* up;
+    const void* down;
+    int64_t gate_stride, up_stride, down_stride;
+} kq_moe_ffn;
+
+/* Bytes of device workspace kq_moe_ffn_dev needs for B tokens, or -1. */
+int64_t kq_moe_ffn_workspace_bytes(const kq_moe_ffn* f, int B);
+
+/* The expert FFN step for B tokens: router logits of xn (B x n_embed, the
+ * normed hidden state), softmax, top-k (sel, selw: B x k, written), gate
+ * and up of each selected slice, SwiGLU, down, and x = x + the rank-ordered
+ * weighted sum (x: B x n_embed, the residual stream, updated in place).
+ * The GEMVs follow the per-slice contract of kq_moe_gemv_dev; expf-based
+ * steps as above.  No allocation: work is caller-provided device memory of
+ * kq_moe_ffn_workspace_bytes.  B <= KQ_MOE_MAX_TOKENS, k <= KQ_MAX_GROUPS,
+ * n_embed and n_ff multiples of 256.  Replaces the FFN half of
+ * moe_forward_one_token / moe_forward_b after moe_rmsnorm. */
+int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* sel, float* selw,
+                   void* work, int64_t work_bytes, kq_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -760,3 +760,95 @@ void ko_moe_topk(const float* w, int E, int K, int* sel, float* selw) {
         selw[pos] = w[e];
     }
 }
+
+/* ------------------------------------------------------ MoE FFN step */
+
+/* stratum_softmax_inplace (stratum_engine.h:395-423) as its scalar path
+ * runs it: the max by a sequential strictly-greater scan from x[0], libm
+ * expf of each x - max, the binary64 sum in index order, one binary32
+ * reciprocal of that sum, then a binary32 product per value. */
+void ko_softmax(float* x, int N) {
+    if (N <= 0) return;
+    float top = x[0];
+    for (int i = 1; i < N; i++)
+        if (x[i] > top) top = x[i];
+    double total = 0.0;
+    for (int i = 0; i < N; i++) {
+        x[i] = expf(x[i] - top);
+    }
+    for (int i = 0; i < N; i++) total += (double)x[i];
+    const float r = (float)(1.0 / total);
+    for (int i = 0; i < N; i++) x[i] = x[i] * r;
+}
+
+/* stratum_swiglu's scalar loop (stratum_engine.h:386-391) */
+void ko_swiglu(const float* g, const float* u, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) {
+        const float gate = g[i];
+        const float sig = gate / (1.0f + expf(-gate));
+        y[i] = sig * u[i];
+    }
+}
+
+/* Rank-ordered weighted accumulate and residual
+ * (stratum_arch_moe.inc.c:728-743 and 1213-1226): o has B*k rows of H */
+void ko_moe_combine(const float* o, const int* sel, const float* selw, const float* resid,
+                    float* x, int B, int k, int H) {
+    for (int s = 0; s < B; s++)
+        for (int i = 0; i < H; i++) {
+            float acc = 0.0f;
+            for (int r = 0; r < k; r++) {
+                if (sel[s * k + r] < 0) continue;
+                const float t = selw[s * k + r] * o[((size_t)s * k + r) * H + i];
+                acc = acc + t;
+            }
+            x[(size_t)s * H + i] = resid[(size_t)s * H + i] + acc;
+        }
+}
+
+/* The whole expert FFN step for B tokens (stratum_arch_moe.inc.c:689-743):
+ * router GEMV on each token's xn, softmax, top-k, then per selected rank
+ * the gate, up (slices at e * stride), SwiGLU and down, and the combine.
+ * The intermediate buffers are returned when their pointers are not NULL:
+ * probs B x E, g / u / act B*k x F, ffo B*k x H. */
+int ko_moe_ffn(const ko_moe_ffn_desc* f, const float* xn, float* x, int B, int* sel,
+               float* selw, float* probs, float* g, float* u, float* act, float* ffo) {
+    const int H = f->n_embed, F = f->n_ff, E = f->n_experts, k = f->k;
+    const size_t bk = (size_t)B * k;
+    float* P = malloc((size_t)B * E * sizeof(float));
+    float* G = malloc(bk * F * sizeof(float));
+    float* U = malloc(bk * F * sizeof(float));
+    float* A = malloc(bk * F * sizeof(float));
+    float* O = malloc(bk * H * sizeof(float));
+    int rc = (P && G && U && A && O) ? 0 : -1;
+    for (int s = 0; s < B && !rc; s++) {
+        float* ps = P + (size_t)s * E;
+        rc = ko_gemv(f->router_type, f->router, xn + (size_t)s * H, NULL, ps, E, H, 1);
+        if (rc) break;
+        ko_softmax(ps, E);
+        ko_moe_topk(ps, E, k, sel + (size_t)s * k, selw + (size_t)s * k);
+        for (int r = 0; r < k && !rc; r++) {
+            const size_t m = (size_t)s * k + r;
+            const int e = sel[m];
+            if (e < 0) continue;
+            rc = ko_gemv(f->gate_type, f->gate + (size_t)e * f->gate_stride, xn + (size_t)s * H,
+                         NULL, G + m * F, F, H, 1) ||
+                 ko_gemv(f->up_type, f->up + (size_t)e * f->up_stride, xn + (size_t)s * H, NULL,
+                         U + m * F, F, H, 1);
+            if (rc) break;
+            ko_swiglu(G + m * F, U + m * F, A + m * F, F);
+            rc = ko_gemv(f->down_type, f->down + (size_t)e * f->down_stride, A + m * F, NULL,
+                         O + m * H, H, F, 1);
+        }
+    }
+    if (!rc) {
+        ko_moe_combine(O, sel, selw, x, x, B, k, H);
+        if (probs) memcpy(probs, P, (size_t)B * E * sizeof(float));
+        if (g) memcpy(g, G, bk * F * sizeof(float));
+        if (u) memcpy(u, U, bk * F * sizeof(float));
+        if (act) memcpy(act, A, bk * F * sizeof(float));
+        if (ffo) memcpy(ffo, O, bk * H * sizeof(float));
+    }
+    free(P); free(G); free(U); free(A); free(O);
+    return rc;
+}

@@ -33,6 +33,12 @@
  *                                     -> ko_q2k_to_nib / ko_nib_to_q2k
  *   stratum_linear.h:201-228 ST_PAR_ROWS 64-row tickets -> ko_gemv threads
  *   stratum_arch_moe.inc.c:368-385 moe_topk        -> ko_moe_topk
+ *   stratum_engine.h:395-423 stratum_softmax_inplace -> ko_softmax
+ *   stratum_engine.h:373-392 stratum_swiglu          -> ko_swiglu
+ *   stratum_arch_moe.inc.c:689-743, 1213-1226 the FFN step's router,
+ *                          accumulate and residual -> ko_moe_ffn, ko_moe_combine
+ *                          (stratum_engine.h needs macOS headers and does not
+ *                          build here: pinned by closed forms only)
  *
  * Pinning (what checks each function, see tests/test_oracle_*.py):
  *   - golden vectors in tests/golden/ written by the reference's own scalar
@@ -109,6 +115,25 @@ void ko_nib_to_q2k(const uint8_t* nib, uint8_t* q2k, int64_t nblocks);
 
 /* top-k with strict '>' replacement: ties keep the lower expert id */
 void ko_moe_topk(const float* w, int E, int K, int* sel, float* selw);
+
+/* MoE FFN step pieces: softmax in place (libm expf, binary64 sum in
+ * order), SwiGLU, rank-ordered combine + residual, and the whole step */
+void ko_softmax(float* x, int N);
+void ko_swiglu(const float* g, const float* u, float* y, int64_t n);
+void ko_moe_combine(const float* o, const int* sel, const float* selw, const float* resid,
+                    float* x, int B, int k, int H);
+typedef struct ko_moe_ffn_desc {
+    int n_embed, n_ff, n_experts, k;
+    int router_type;
+    const uint8_t* router;
+    int gate_type, up_type, down_type;
+    const uint8_t* gate;
+    const uint8_t* up;
+    const uint8_t* down;
+    int64_t gate_stride, up_stride, down_stride;
+} ko_moe_ffn_desc;
+int ko_moe_ffn(const ko_moe_ffn_desc* f, const float* xn, float* x, int B, int* sel,
+               float* selw, float* probs, float* g, float* u, float* act, float* ffo);
 
 #ifdef __cplusplus
 }

@@ -43,6 +43,16 @@ def _f(a: np.ndarray):
     return a.ctypes.data_as(_F)
 
 
+class MoeFfnDesc(ctypes.Structure):
+    """ko_moe_ffn_desc (oracle/kq_oracle.h)"""
+    _fields_ = [("n_embed", ctypes.c_int), ("n_ff", ctypes.c_int), ("n_experts", ctypes.c_int),
+                ("k", ctypes.c_int), ("router_type", ctypes.c_int), ("router", ctypes.c_void_p),
+                ("gate_type", ctypes.c_int), ("up_type", ctypes.c_int),
+                ("down_type", ctypes.c_int), ("gate", ctypes.c_void_p), ("up", ctypes.c_void_p),
+                ("down", ctypes.c_void_p), ("gate_stride", ctypes.c_int64),
+                ("up_stride", ctypes.c_int64), ("down_stride", ctypes.c_int64)]
+
+
 class Port:
     """The restatement in oracle/kq_oracle.c."""
 
@@ -71,6 +81,15 @@ class Port:
         L.ko_quantize_x_q8.argtypes = [_F, I, I, ctypes.POINTER(ctypes.c_int8), _F]
         L.ko_quantize_x_q8.restype = None
         L.ko_gemv_i8.argtypes = [I, _U8, _F, _F, _F, ctypes.POINTER(ctypes.c_double), I, I, I]
+        L.ko_softmax.argtypes = [_F, I]
+        L.ko_softmax.restype = None
+        L.ko_swiglu.argtypes = [_F, _F, _F, ctypes.c_int64]
+        L.ko_swiglu.restype = None
+        _I = ctypes.POINTER(ctypes.c_int)
+        L.ko_moe_combine.argtypes = [_F, _I, _F, _F, _F, I, I, I]
+        L.ko_moe_combine.restype = None
+        L.ko_moe_ffn.argtypes = [ctypes.POINTER(MoeFfnDesc), _F, _F, I, _I, _F, _F, _F, _F, _F,
+                                 _F]
         self.L = L
 
     def fp16_to_fp32(self, h: int) -> float:
@@ -137,6 +156,53 @@ class Port:
                                if with_mag else None, N, K, int(sdot_f))
         assert rc == 0
         return (y, mag) if with_mag else y
+
+    def softmax(self, x: np.ndarray) -> np.ndarray:
+        """softmax of each row of x (copied)"""
+        out = np.array(x, np.float32, copy=True, order="C")
+        rows = out.reshape(-1, out.shape[-1])
+        for r in rows:
+            self.L.ko_softmax(_f(r), r.size)
+        return out
+
+    def swiglu(self, g: np.ndarray, u: np.ndarray) -> np.ndarray:
+        y = np.empty_like(g)
+        self.L.ko_swiglu(_f(g), _f(u), _f(y), g.size)
+        return y
+
+    def moe_combine(self, o, sel, selw, resid, B, k, H):
+        x = np.empty(B * H, np.float32)
+        s = np.ascontiguousarray(sel, np.int32)
+        self.L.ko_moe_combine(_f(o), s.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), _f(selw),
+                              _f(resid), _f(x), B, k, H)
+        return x
+
+    def moe_ffn(self, d: dict, xn: np.ndarray, x: np.ndarray, B: int) -> dict:
+        """the whole expert FFN step; d holds n_embed, n_ff, n_experts, k,
+        router_type / router, gate_type / gate, up_type / up, down_type /
+        down (uint8 arrays of all experts' slices) and the strides"""
+        H, F, E, k = d["n_embed"], d["n_ff"], d["n_experts"], d["k"]
+        desc = MoeFfnDesc()
+        keep = []
+        for name in ("router", "gate", "up", "down"):
+            a = np.ascontiguousarray(d[name], np.uint8)
+            keep.append(a)
+            setattr(desc, name, a.ctypes.data)
+            setattr(desc, name + "_type", d[name + "_type"])
+        desc.n_embed, desc.n_ff, desc.n_experts, desc.k = H, F, E, k
+        desc.gate_stride, desc.up_stride, desc.down_stride = (
+            d["gate_stride"], d["up_stride"], d["down_stride"])
+        out = {"x": np.array(x, np.float32, copy=True),
+               "sel": np.empty(B * k, np.int32), "selw": np.empty(B * k, np.float32),
+               "probs": np.empty(B * E, np.float32), "g": np.empty(B * k * F, np.float32),
+               "u": np.empty(B * k * F, np.float32), "act": np.empty(B * k * F, np.float32),
+               "ffo": np.empty(B * k * H, np.float32)}
+        rc = self.L.ko_moe_ffn(ctypes.byref(desc), _f(xn), _f(out["x"]), B,
+                               out["sel"].ctypes.data_as(ctypes.POINTER(ctypes.c_int)),
+                               _f(out["selw"]), _f(out["probs"]), _f(out["g"]), _f(out["u"]),
+                               _f(out["act"]), _f(out["ffo"]))
+        assert rc == 0
+        return out
 
     def topk(self, w: np.ndarray, k: int):
         sel = (ctypes.c_int * k)()

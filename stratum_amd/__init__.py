@@ -55,7 +55,8 @@ EXPORTS = (
     "kq_moe_pack_open", "kq_moe_pack_which", "kq_moe_topk", "kq_moe_topk_dev",
     "kq_moe_gemv_dev", "kq_gemv_multix_mfma_dev", "kq_moe_gemv_routed_dev",
     "kq_tuning_reload", "kq_gemv_multix_mfma_noalloc_dev", "kq_linear_set_sdot",
-    "kq_quantize_x_q8_dev",
+    "kq_quantize_x_q8_dev", "kq_softmax_dev", "kq_swiglu_dev", "kq_moe_combine_dev",
+    "kq_moe_ffn_workspace_bytes", "kq_moe_ffn_dev",
 )
 
 NOALLOC_SCRATCH_BYTES = 32 << 20   # KQ_NOALLOC_SCRATCH_BYTES
@@ -160,6 +161,19 @@ class KqMoeOp(ctypes.Structure):
     ]
 
 
+class KqMoeFfn(ctypes.Structure):
+    """kq_moe_ffn: one MoE layer's router and stacked expert tensors."""
+
+    _fields_ = [
+        ("n_embed", ctypes.c_int), ("n_ff", ctypes.c_int), ("n_experts", ctypes.c_int),
+        ("k", ctypes.c_int), ("router_type", ctypes.c_int), ("router", ctypes.c_void_p),
+        ("gate_type", ctypes.c_int), ("up_type", ctypes.c_int), ("down_type", ctypes.c_int),
+        ("gate", ctypes.c_void_p), ("up", ctypes.c_void_p), ("down", ctypes.c_void_p),
+        ("gate_stride", ctypes.c_int64), ("up_stride", ctypes.c_int64),
+        ("down_stride", ctypes.c_int64),
+    ]
+
+
 def moe_op(qtype: int, n_out: int, k_in: int, w_ptrs, expert_stride: int, x_ptr: int,
            x_div: int, y_ptrs) -> KqMoeOp:
     op = KqMoeOp()
@@ -207,6 +221,12 @@ def lib() -> ctypes.CDLL:
     L.kq_gemv_multix_mfma_noalloc_dev.argtypes = [I, P, P, P, I, I, I, P]
     L.kq_dequant_dev.argtypes = [I, P, P, ctypes.c_int64, P]
     L.kq_linear_set_sdot.argtypes = [I]
+    L.kq_softmax_dev.argtypes = [P, I, I, P]
+    L.kq_swiglu_dev.argtypes = [P, P, P, ctypes.c_int64, P]
+    L.kq_moe_combine_dev.argtypes = [P, P, P, P, P, I, I, I, P]
+    L.kq_moe_ffn_workspace_bytes.argtypes = [ctypes.POINTER(KqMoeFfn), I]
+    L.kq_moe_ffn_workspace_bytes.restype = ctypes.c_int64
+    L.kq_moe_ffn_dev.argtypes = [ctypes.POINTER(KqMoeFfn), P, P, I, P, P, P, ctypes.c_int64, P]
     L.kq_quantize_x_q8_dev.argtypes = [P, I, I, P, P, P, P]
     L.kq_gemv_segments_dev.argtypes = [ctypes.POINTER(KqSegment), I, P]
     L.kq_row_bytes.argtypes = [I, I]
@@ -388,3 +408,43 @@ def moe_gemv_routed_dev(op: KqMoeOp, probs_ptr: int, B: int, k: int, E: int, sel
     to sel / selw), then op on the selected experts (kq_moe_gemv_routed_dev)."""
     _check(lib().kq_moe_gemv_routed_dev(ctypes.byref(op), probs_ptr, B, k, E, sel_ptr, selw_ptr,
                                         stream), "kq_moe_gemv_routed_dev")
+
+
+def softmax_dev(x_ptr: int, B: int, E: int, stream: int | None = None) -> None:
+    _check(lib().kq_softmax_dev(x_ptr, B, E, stream), "kq_softmax_dev")
+
+
+def swiglu_dev(g_ptr: int, u_ptr: int, y_ptr: int, n: int, stream: int | None = None) -> None:
+    _check(lib().kq_swiglu_dev(g_ptr, u_ptr, y_ptr, n, stream), "kq_swiglu_dev")
+
+
+def moe_combine_dev(o_ptr: int, sel_ptr: int, selw_ptr: int, resid_ptr: int, x_ptr: int, B: int,
+                    k: int, H: int, stream: int | None = None) -> None:
+    _check(lib().kq_moe_combine_dev(o_ptr, sel_ptr, selw_ptr, resid_ptr, x_ptr, B, k, H, stream),
+           "kq_moe_combine_dev")
+
+
+def moe_ffn_workspace_bytes(f: KqMoeFfn, B: int) -> int:
+    n = lib().kq_moe_ffn_workspace_bytes(ctypes.byref(f), B)
+    if n < 0:
+        raise RuntimeError(f"kq_moe_ffn_workspace_bytes failed: {lib().kq_last_error().decode()}")
+    return n
+
+
+def moe_ffn_workspace_offsets(f: KqMoeFfn, B: int) -> dict:
+    """Offsets of probs, g, u, act and ffo in the step's workspace (the
+    layout kq_moe_ffn_dev uses: in that order, each 256-byte aligned)."""
+    bk = B * f.k
+    sizes = [("probs", B * f.n_experts * 4), ("g", bk * f.n_ff * 4), ("u", bk * f.n_ff * 4),
+             ("act", bk * f.n_ff * 4), ("ffo", bk * f.n_embed * 4)]
+    out, t = {}, 0
+    for name, n in sizes:
+        out[name] = t
+        t += (n + 255) // 256 * 256
+    return out
+
+
+def moe_ffn_dev(f: KqMoeFfn, xn_ptr: int, x_ptr: int, B: int, sel_ptr: int, selw_ptr: int,
+                work_ptr: int, work_bytes: int, stream: int | None = None) -> None:
+    _check(lib().kq_moe_ffn_dev(ctypes.byref(f), xn_ptr, x_ptr, B, sel_ptr, selw_ptr, work_ptr,
+                                work_bytes, stream), "kq_moe_ffn_dev")

@@ -3016,7 +3016,11 @@ struct DenseArg {
     float* y;
     long row_bytes;
     int N, K;
+    int B;               // streams: x is B x K, y is B x N (add only for B == 1)
 };
+
+// streams per workgroup pass of the dense multi-stream kernel
+constexpr int DENSE_SB = 8;
 
 __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll
@@ -3028,21 +3032,30 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     return v;
 }
 
-template <int TYPE, bool XLDS>
+// One wave per row; lane l takes elements E*l + 64*E*i in order, the 64
+// partial sums meet in a fixed butterfly, so the result does not depend on
+// the grid.  SB streams (blockIdx.y selects the group of SB) share each
+// weight load; every stream's sum runs in the single-stream order.
+template <int TYPE, bool XLDS, int SB>
 __global__ __launch_bounds__(256) void kq_dense_kernel(DenseArg a) {
     extern __shared__ __align__(16) float xl[];
     constexpr int E = TYPE == T_F32 ? 4 : 8;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int K = a.K;
+    const int s0 = blockIdx.y * SB;
+    const int nb = min(SB, a.B - s0);
+    const float* xg = a.x + (size_t)s0 * K;
     if (XLDS) {
-        for (int i = 4 * tid; i < K; i += 1024)
-            *reinterpret_cast<float4*>(xl + i) = *reinterpret_cast<const float4*>(a.x + i);
+        for (int i = 4 * tid; i < nb * K; i += 1024)
+            *reinterpret_cast<float4*>(xl + i) = *reinterpret_cast<const float4*>(xg + i);
         __syncthreads();
     }
-    const float* xs = XLDS ? xl : a.x;
+    const float* xs = XLDS ? xl : xg;
     for (int r = blockIdx.x * 4 + wave; r < a.N; r += gridDim.x * 4) {
         const wptr row = to_global(a.w) + (size_t)r * a.row_bytes;
-        double acc = 0.0;
+        double acc[SB];
+#pragma unroll
+        for (int s = 0; s < SB; s++) acc[s] = 0.0;
         for (int m = 0; m < K; m += 64 * E) {
             const int e0 = m + E * lane;
             if (e0 < K) {                       // F16 rows of K % 512 == 256 end half-way
@@ -3050,7 +3063,6 @@ __global__ __launch_bounds__(256) void kq_dense_kernel(DenseArg a) {
                 const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                 for (int q = 0; q < E / 4; q++) {
-                    const float4 xv = *reinterpret_cast<const float4*>(xs + e0 + 4 * q);
                     float wf[4];
                     if (TYPE == T_F32) {
                         wf[0] = __uint_as_float(wv[0]); wf[1] = __uint_as_float(wv[1]);
@@ -3061,18 +3073,30 @@ __global__ __launch_bounds__(256) void kq_dense_kernel(DenseArg a) {
                         wf[2] = f16_bits_to_f32(wv[2 * q + 1] & 0xffffu);
                         wf[3] = f16_bits_to_f32(wv[2 * q + 1] >> 16);
                     }
-                    acc = fma((double)wf[0], (double)xv.x, acc);   // exact product, one rounding
-                    acc = fma((double)wf[1], (double)xv.y, acc);
-                    acc = fma((double)wf[2], (double)xv.z, acc);
-                    acc = fma((double)wf[3], (double)xv.w, acc);
+#pragma unroll
+                    for (int s = 0; s < SB; s++) {
+                        if (s < nb) {
+                            const float4 xv =
+                                *reinterpret_cast<const float4*>(xs + (size_t)s * K + e0 + 4 * q);
+                            acc[s] = fma((double)wf[0], (double)xv.x, acc[s]);   // exact product
+                            acc[s] = fma((double)wf[1], (double)xv.y, acc[s]);
+                            acc[s] = fma((double)wf[2], (double)xv.z, acc[s]);
+                            acc[s] = fma((double)wf[3], (double)xv.w, acc[s]);
+                        }
+                    }
                 }
             }
         }
-        acc = wave_sum_f64(acc);
-        if (lane == 0) {
-            float v = (float)acc;
-            if (a.add) v = a.add[r] + v;
-            a.y[r] = v;
+#pragma unroll
+        for (int s = 0; s < SB; s++) {
+            if (s < nb) {
+                const double t = wave_sum_f64(acc[s]);
+                if (lane == 0) {
+                    float v = (float)t;
+                    if (SB == 1 && a.add) v = a.add[r] + v;
+                    a.y[(size_t)(s0 + s) * a.N + r] = v;
+                }
+            }
         }
     }
 }
@@ -3092,6 +3116,93 @@ __global__ __launch_bounds__(256) void kq_dense_dequant_kernel(const uint8_t* w,
         y[i] = f16_bits_to_f32(v.x & 0xffffu); y[i + 1] = f16_bits_to_f32(v.x >> 16);
         y[i + 2] = f16_bits_to_f32(v.y & 0xffffu); y[i + 3] = f16_bits_to_f32(v.y >> 16);
     }
+}
+
+// ------------------------------------------------------ MoE FFN step
+// Softmax of one row of E values per workgroup (stratum_softmax_inplace,
+// stratum_engine.h:395-423): max as the sequential scan takes it (a NaN
+// first value stays the max; later NaNs never replace it), e = expf(x -
+// max) per value, the binary64 sum in index order by one lane (the
+// reference's order), inv = (float)(1.0 / sum), x = e * inv.  expf is the
+// device's (within 1 ulp of a correctly rounded exp).
+__global__ __launch_bounds__(256) void kq_softmax_kernel(float* x, int E) {
+    extern __shared__ __align__(16) float sm[];          // E values + 64 for the max
+    float* row = x + (size_t)blockIdx.x * E;
+    const int tid = threadIdx.x;
+    float m = -INFINITY;
+    for (int i = tid; i < E; i += 256) {
+        const float v = row[i];
+        sm[i] = v;
+        m = fmaxf(m, v);                                 // NaN-ignoring
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+    float* wm = sm + ((E + 3) & ~3);
+    if ((tid & 63) == 0) wm[tid >> 6] = m;
+    __syncthreads();
+    float maxv = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+    if (isnan(sm[0])) maxv = sm[0];
+    __syncthreads();
+    for (int i = tid; i < E; i += 256) sm[i] = expf(sm[i] - maxv);
+    __syncthreads();
+    if (tid == 0) {
+        double sum = 0.0;
+        int i = 0;
+        for (; i + 4 <= E; i += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(sm + i);
+            sum = sum + (double)v.x; sum = sum + (double)v.y;
+            sum = sum + (double)v.z; sum = sum + (double)v.w;
+        }
+        for (; i < E; i++) sum = sum + (double)sm[i];
+        wm[0] = (float)(1.0 / sum);
+    }
+    __syncthreads();
+    const float inv = wm[0];
+    for (int i = tid; i < E; i += 256) row[i] = sm[i] * inv;
+}
+
+// SwiGLU (stratum_swiglu, stratum_engine.h:373-392, the scalar loop):
+// y = (g / (1 + expf(-g))) * u, binary32 throughout, 4 values per lane.
+__global__ __launch_bounds__(256) void kq_swiglu_kernel(const float* g, const float* u, float* y,
+                                                        long n) {
+    const long i = 4 * ((long)blockIdx.x * 256 + threadIdx.x);
+    if (i + 4 <= n) {
+        const float4 gv = *reinterpret_cast<const float4*>(g + i);
+        const float4 uv = *reinterpret_cast<const float4*>(u + i);
+        float4 o;
+        o.x = (gv.x / (1.0f + expf(-gv.x))) * uv.x;
+        o.y = (gv.y / (1.0f + expf(-gv.y))) * uv.y;
+        o.z = (gv.z / (1.0f + expf(-gv.z))) * uv.z;
+        o.w = (gv.w / (1.0f + expf(-gv.w))) * uv.w;
+        *reinterpret_cast<float4*>(y + i) = o;
+    } else {
+        for (long j = i; j < n; j++) y[j] = (g[j] / (1.0f + expf(-g[j]))) * u[j];
+    }
+}
+
+// Weighted accumulate in rank order plus the residual (batch 1:
+// stratum_arch_moe.inc.c:728-743; batches: :1213-1226): for token s and
+// element i, acc = 0; for r < k with sel >= 0: acc = acc + selw[r] * o[r][i]
+// (product and sum rounded separately); x = resid + acc.  o is the down
+// output of member s*k + r (B*k rows of H).
+__global__ __launch_bounds__(256) void kq_moe_combine_kernel(const float* o, const int* sel,
+                                                             const float* selw,
+                                                             const float* resid, float* x, int k,
+                                                             int H) {
+    const int s = blockIdx.y;
+    const int i = 4 * (blockIdx.x * 256 + threadIdx.x);
+    if (i >= H) return;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int r = 0; r < k; r++) {
+        if (sel[s * k + r] < 0) continue;
+        const float w = selw[s * k + r];
+        const float4 v = *reinterpret_cast<const float4*>(o + ((size_t)s * k + r) * H + i);
+        acc.x = acc.x + w * v.x; acc.y = acc.y + w * v.y;
+        acc.z = acc.z + w * v.z; acc.w = acc.w + w * v.w;
+    }
+    const float4 rv = *reinterpret_cast<const float4*>(resid + (size_t)s * H + i);
+    *reinterpret_cast<float4*>(x + (size_t)s * H + i) =
+        make_float4(rv.x + acc.x, rv.y + acc.y, rv.z + acc.z, rv.w + acc.w);
 }
 
 // x -> int8 per group of G (32: q4k_quantize_x_q8 + q4k_sum_i8_32; 16:
@@ -3655,6 +3766,29 @@ int kqk_launch_dequant(int type, const void* w, float* y, long nblocks, hipStrea
     }
 }
 
+int kqk_launch_softmax(float* x, int B, int E, hipStream_t st) {
+    if (B < 1 || E < 1 || E > KQ_MOE_MAX_EXPERTS) return (int)hipErrorInvalidValue;
+    const size_t shm = (size_t)(((E + 3) & ~3) + 64) * sizeof(float);
+    hipLaunchKernelGGL(kq_softmax_kernel, dim3(B), dim3(256), shm, st, x, E);
+    return (int)hipGetLastError();
+}
+
+int kqk_launch_swiglu(const float* g, const float* u, float* y, long n, hipStream_t st) {
+    if (n < 1) return (int)hipErrorInvalidValue;
+    const long lanes = (n + 3) / 4;
+    hipLaunchKernelGGL(kq_swiglu_kernel, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0, st, g,
+                       u, y, n);
+    return (int)hipGetLastError();
+}
+
+int kqk_launch_moe_combine(const float* o, const int* sel, const float* selw, const float* resid,
+                           float* x, int B, int k, int H, hipStream_t st) {
+    if (B < 1 || k < 1 || H < 4 || (H & 3)) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(kq_moe_combine_kernel, dim3((H / 4 + 255) / 256, B), dim3(256), 0, st, o, sel,
+                       selw, resid, x, k, H);
+    return (int)hipGetLastError();
+}
+
 int kqk_launch_quantize_q8(const float* x, int K, int group, int8_t* xq, float* xscale, int* xsum,
                            hipStream_t st) {
     if ((group != 32 && group != 16) || K < group || K % group) return (int)hipErrorInvalidValue;
@@ -3670,27 +3804,33 @@ int kqk_launch_quantize_q8(const float* x, int K, int group, int8_t* xq, float* 
 
 // Dense rows (F16, F32): x staged in LDS when K <= DENSE_XLDS_MAX
 int kqk_launch_dense(int type, const void* w, const float* x, const float* add, float* y, int N,
-                     int K, int grid, hipStream_t st) {
-    if ((type != T_F16 && type != T_F32) || N < 1 || K < 256 || (K & 255) || grid < 1)
+                     int K, int B, int grid, hipStream_t st) {
+    if ((type != T_F16 && type != T_F32) || N < 1 || K < 256 || (K & 255) || grid < 1 || B < 1 ||
+        (B > 1 && add))
         return (int)hipErrorInvalidValue;
     DenseArg a;
     a.w = static_cast<const uint8_t*>(w);
-    a.x = x; a.add = add; a.y = y; a.N = N; a.K = K;
+    a.x = x; a.add = add; a.y = y; a.N = N; a.K = K; a.B = B;
     a.row_bytes = (long)K * (type == T_F32 ? 4 : 2);
-    const bool lds = K <= DENSE_XLDS_MAX;
-    const size_t shm = lds ? (size_t)K * 4 : 0;
-#define KQ_DENSE_GO(T_, L_) hipLaunchKernelGGL((kq_dense_kernel<T_, L_>), dim3(grid), dim3(256), shm, st, a)
-    if (type == T_F32) { if (lds) KQ_DENSE_GO(T_F32, true); else KQ_DENSE_GO(T_F32, false); }
-    else { if (lds) KQ_DENSE_GO(T_F16, true); else KQ_DENSE_GO(T_F16, false); }
+    const int sb = B == 1 ? 1 : DENSE_SB;
+    const bool lds = (long)sb * K <= DENSE_XLDS_MAX;
+    const size_t shm = lds ? (size_t)sb * K * 4 : 0;
+    const dim3 g(grid, (B + sb - 1) / sb);
+#define KQ_DENSE_GO(T_, L_, S_) hipLaunchKernelGGL((kq_dense_kernel<T_, L_, S_>), g, dim3(256), shm, st, a)
+#define KQ_DENSE_SB(S_)                                                              \
+    if (type == T_F32) { if (lds) KQ_DENSE_GO(T_F32, true, S_); else KQ_DENSE_GO(T_F32, false, S_); } \
+    else { if (lds) KQ_DENSE_GO(T_F16, true, S_); else KQ_DENSE_GO(T_F16, false, S_); }
+    if (sb == 1) { KQ_DENSE_SB(1) } else { KQ_DENSE_SB(DENSE_SB) }
+#undef KQ_DENSE_SB
 #undef KQ_DENSE_GO
     return (int)hipGetLastError();
 }
 
 int kqk_dense_set_max_lds(int bytes) {
-    const void* fns[4] = {reinterpret_cast<const void*>(&kq_dense_kernel<T_F32, true>),
-                          reinterpret_cast<const void*>(&kq_dense_kernel<T_F16, true>),
-                          reinterpret_cast<const void*>(&kq_dense_kernel<T_F32, false>),
-                          reinterpret_cast<const void*>(&kq_dense_kernel<T_F16, false>)};
+    const void* fns[4] = {reinterpret_cast<const void*>(&kq_dense_kernel<T_F32, true, 1>),
+                          reinterpret_cast<const void*>(&kq_dense_kernel<T_F16, true, 1>),
+                          reinterpret_cast<const void*>(&kq_dense_kernel<T_F32, true, DENSE_SB>),
+                          reinterpret_cast<const void*>(&kq_dense_kernel<T_F16, true, DENSE_SB>)};
     for (int i = 0; i < 4; i++) {
         const hipError_t e = hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  bytes < DENSE_XLDS_MAX * 4 ? bytes : DENSE_XLDS_MAX * 4);

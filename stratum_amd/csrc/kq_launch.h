@@ -39,7 +39,12 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
 int kqk_launch_dequant(int type, const void* w, float* y, long nblocks, hipStream_t st);
 /* dense F16 / F32 rows (types 1 / 0): y = W x (+ add) on `grid` workgroups */
 int kqk_launch_dense(int type, const void* w, const float* x, const float* add, float* y, int N,
-                     int K, int grid, hipStream_t st);
+                     int K, int B, int grid, hipStream_t st);
+/* MoE FFN step pieces */
+int kqk_launch_softmax(float* x, int B, int E, hipStream_t st);
+int kqk_launch_swiglu(const float* g, const float* u, float* y, long n, hipStream_t st);
+int kqk_launch_moe_combine(const float* o, const int* sel, const float* selw, const float* resid,
+                           float* x, int B, int k, int H, hipStream_t st);
 int kqk_dense_set_max_lds(int bytes);
 /* x -> int8 per group (32 or 16), scales, integer sums (xsum may be NULL) */
 int kqk_launch_quantize_q8(const float* x, int K, int group, int8_t* xq, float* xscale, int* xsum,

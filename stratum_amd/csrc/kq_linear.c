@@ -360,13 +360,15 @@ static int check_shape(int type, int N, int K) {
 
 /* ------------------------------------------------- device-pointer ABI */
 
-/* Dense F16 / F32 rows: their own kernel, one wave per row at a time. */
+/* Dense F16 / F32 rows: their own kernel, one wave per row at a time; B
+ * streams share each weight load (each stream's sum in the single-stream
+ * order, so ys[s] equals the single call bit for bit). */
 static int dense_gemv(int type, const void* w, const float* x, const float* add, float* y, int N,
-                      int K, hipStream_t st) {
+                      int K, int B, hipStream_t st) {
     if ((uintptr_t)w & 15) return kq_fail("dense GEMV: weights must be 16-byte aligned");
     long g = ((long)N + 3) / 4;
     if (g > 8L * g_kq.n_cu) g = 8L * g_kq.n_cu;
-    const int e = kqk_launch_dense(type, w, x, add, y, N, K, (int)g, st);
+    const int e = kqk_launch_dense(type, w, x, add, y, N, K, B, (int)g, st);
     if (e) return kq_fail("dense gemv launch: %s", hipGetErrorString((hipError_t)e));
     return 0;
 }
@@ -376,7 +378,7 @@ int kq_gemv_dev(int type, const void* w, const float* x, const float* add, float
     if (check_shape(type, N, K) || kq_ready()) return -1;
     if (!w || !x || !y) return kq_fail("kq_gemv_dev: NULL pointer");
     if ((uintptr_t)x & 15) return kq_fail("kq_gemv_dev: x must be 16-byte aligned");
-    if (is_dense(type)) return dense_gemv(type, w, x, add, y, N, K, pick(stream));
+    if (is_dense(type)) return dense_gemv(type, w, x, add, y, N, K, 1, pick(stream));
     kqk_seg sg;
     memset(&sg, 0, sizeof sg);
     sg.type = type; sg.K = K; sg.nparts = 1; sg.x = x;
@@ -441,7 +443,7 @@ int kq_gemv_segments_dev(const kq_segment* segs, int nseg, kq_stream stream) {
                 const float* xg = s->x + (s->ngroups > 1 ? (size_t)g * s->x_stride : 0);
                 const size_t o = (size_t)g * s->rows_per_group;
                 if (dense_gemv(s->type, s->w[g], xg, s->add ? s->add + o : NULL, s->y + o,
-                               s->rows_per_group, s->K, pick(stream)))
+                               s->rows_per_group, s->K, 1, pick(stream)))
                     return -1;
             }
             continue;
@@ -529,6 +531,7 @@ int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,
     if (check_shape(type, N, K) || kq_ready()) return -1;
     if (!w || !xs || !ys) return kq_fail("kq_gemv_multix_dev: NULL pointer");
     if ((uintptr_t)xs & 15) return kq_fail("kq_gemv_multix_dev: xs must be 16-byte aligned");
+    if (is_dense(type) && B > 1) return dense_gemv(type, w, xs, NULL, ys, N, K, B, pick(stream));
     if (B == 1 || !is_core(type)) {   /* per-stream launches: the same bits as single calls */
         for (int s = 0; s < B; s++)
             if (kq_gemv_dev(type, w, xs + (size_t)s * K, NULL, ys + (size_t)s * N, N, K, stream))
@@ -1015,4 +1018,138 @@ int kq_moe_gemv_dev(const kq_moe_op* op, const int* sel, int B, int k, int E, kq
     if (B == 1) return moe_one_token(op, sel, k, E, NULL, NULL, st);
     if (!is_core(op->type)) return moe_per_token(op, sel, B, k, E, st);
     return moe_batch(op, (int*)sel, NULL, NULL, B, k, E, st);
+}
+
+/* ------------------------------------------------------ MoE FFN step */
+
+int kq_softmax_dev(float* x, int B, int E, kq_stream stream) {
+    if (kq_ready()) return -1;
+    if (!x) return kq_fail("kq_softmax_dev: NULL pointer");
+    if (B < 1 || E < 1 || E > KQ_MOE_MAX_EXPERTS)
+        return kq_fail("kq_softmax_dev: B=%d E=%d (E <= %d)", B, E, KQ_MOE_MAX_EXPERTS);
+    const int e = kqk_launch_softmax(x, B, E, pick(stream));
+    if (e) return kq_fail("softmax launch: %s", hipGetErrorString((hipError_t)e));
+    return 0;
+}
+
+int kq_swiglu_dev(const float* g, const float* u, float* y, int64_t n, kq_stream stream) {
+    if (kq_ready()) return -1;
+    if (!g || !u || !y) return kq_fail("kq_swiglu_dev: NULL pointer");
+    if (((uintptr_t)g | (uintptr_t)u | (uintptr_t)y) & 15)
+        return kq_fail("kq_swiglu_dev: g, u and y must be 16-byte aligned");
+    if (n < 1) return kq_fail("kq_swiglu_dev: n=%lld", (long long)n);
+    const int e = kqk_launch_swiglu(g, u, y, (long)n, pick(stream));
+    if (e) return kq_fail("swiglu launch: %s", hipGetErrorString((hipError_t)e));
+    return 0;
+}
+
+int kq_moe_combine_dev(const float* o, const int* sel, const float* selw, const float* resid,
+                       float* x, int B, int k, int H, kq_stream stream) {
+    if (kq_ready()) return -1;
+    if (!o || !sel || !selw || !resid || !x) return kq_fail("kq_moe_combine_dev: NULL pointer");
+    if (((uintptr_t)o | (uintptr_t)resid | (uintptr_t)x) & 15)
+        return kq_fail("kq_moe_combine_dev: o, resid and x must be 16-byte aligned");
+    if (B < 1 || k < 1 || H < 4 || H % 4)
+        return kq_fail("kq_moe_combine_dev: B=%d k=%d H=%d (H %% 4 must be 0)", B, k, H);
+    const int e = kqk_launch_moe_combine(o, sel, selw, resid, x, B, k, H, pick(stream));
+    if (e) return kq_fail("combine launch: %s", hipGetErrorString((hipError_t)e));
+    return 0;
+}
+
+/* workspace of one step: probs B x E, g / u / act B*k x F, down outputs
+ * B*k x H, each 256-byte aligned */
+static int64_t ffn_layout(const kq_moe_ffn* f, int B, int64_t off[5]) {
+    const int64_t bk = (int64_t)B * f->k;
+    const int64_t sz[5] = {(int64_t)B * f->n_experts * 4, bk * f->n_ff * 4, bk * f->n_ff * 4,
+                           bk * f->n_ff * 4, bk * f->n_embed * 4};
+    int64_t t = 0;
+    for (int i = 0; i < 5; i++) {
+        off[i] = t;
+        t += (sz[i] + 255) & ~(int64_t)255;
+    }
+    return t;
+}
+
+static int ffn_check(const kq_moe_ffn* f, int B, const char* who) {
+    if (!f) return kq_fail("%s: NULL descriptor", who);
+    if (B < 1 || B > KQ_MOE_MAX_TOKENS) return kq_fail("%s: B=%d", who, B);
+    if (f->k < 1 || f->k > KQ_MAX_GROUPS || f->n_experts < f->k ||
+        f->n_experts > KQ_MOE_MAX_EXPERTS)
+        return kq_fail("%s: k=%d E=%d", who, f->k, f->n_experts);
+    if (f->n_embed <= 0 || f->n_embed % 256 || f->n_ff <= 0 || f->n_ff % 256)
+        return kq_fail("%s: n_embed=%d n_ff=%d (multiples of 256)", who, f->n_embed, f->n_ff);
+    if (!f->router || !f->gate || !f->up || !f->down) return kq_fail("%s: NULL tensor", who);
+    return 0;
+}
+
+int64_t kq_moe_ffn_workspace_bytes(const kq_moe_ffn* f, int B) {
+    if (ffn_check(f, B, "kq_moe_ffn_workspace_bytes")) return -1;
+    int64_t off[5];
+    return ffn_layout(f, B, off);
+}
+
+/* The expert FFN step of moe_forward_one_token / moe_forward_b
+ * (stratum_arch_moe.inc.c:689-743, 1107-1226) after the norm: router GEMV,
+ * softmax, top-k, gate and up of the selected slices, SwiGLU, down, and
+ * the rank-ordered weighted accumulate plus the residual -- six launches
+ * on one stream, no allocation. */
+int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* sel, float* selw,
+                   void* work, int64_t work_bytes, kq_stream stream) {
+    static const char who[] = "kq_moe_ffn_dev";
+    if (ffn_check(f, B, who) || kq_ready()) return -1;
+    if (!xn || !x || !sel || !selw || !work) return kq_fail("%s: NULL pointer", who);
+    if (((uintptr_t)xn | (uintptr_t)x | (uintptr_t)work) & 15)
+        return kq_fail("%s: xn, x and work must be 16-byte aligned", who);
+    int64_t off[5];
+    const int64_t need = ffn_layout(f, B, off);
+    if (work_bytes < need)
+        return kq_fail("%s: workspace of %lld bytes, %lld needed", who, (long long)work_bytes,
+                       (long long)need);
+    uint8_t* w8 = (uint8_t*)work;
+    float* probs = (float*)(w8 + off[0]);
+    float* g = (float*)(w8 + off[1]);
+    float* u = (float*)(w8 + off[2]);
+    float* act = (float*)(w8 + off[3]);
+    float* ffo = (float*)(w8 + off[4]);
+    const int H = f->n_embed, F = f->n_ff, E = f->n_experts, k = f->k;
+
+    /* router logits, softmax (stratum_arch_moe.inc.c:689-691, 1107-1121) */
+    if (B == 1 ? kq_gemv_dev(f->router_type, f->router, xn, NULL, probs, E, H, stream)
+               : kq_gemv_multix_dev(f->router_type, f->router, xn, probs, B, E, H, stream))
+        return -1;
+    if (kq_softmax_dev(probs, B, E, stream)) return -1;
+
+    /* gate and up of the selected slices, routed in the launch when one op
+     * holds both */
+    kq_moe_op gu;
+    memset(&gu, 0, sizeof gu);
+    gu.type = f->gate_type; gu.n_out = F; gu.k_in = H; gu.x = xn; gu.x_div = k;
+    const int pair = f->gate_type == f->up_type && f->gate_stride == f->up_stride;
+    gu.ntensors = pair ? 2 : 1;
+    gu.w[0] = f->gate; gu.y[0] = g;
+    gu.w[1] = pair ? f->up : NULL; gu.y[1] = pair ? u : NULL;
+    gu.expert_stride = f->gate_stride;
+    if (E <= 1024) {
+        if (kq_moe_gemv_routed_dev(&gu, probs, B, k, E, sel, selw, stream)) return -1;
+    } else {
+        if (kq_moe_topk_dev(probs, B, E, k, sel, selw, stream) ||
+            kq_moe_gemv_dev(&gu, sel, B, k, E, stream))
+            return -1;
+    }
+    if (!pair) {
+        kq_moe_op up;
+        memset(&up, 0, sizeof up);
+        up.type = f->up_type; up.n_out = F; up.k_in = H; up.x = xn; up.x_div = k;
+        up.ntensors = 1; up.w[0] = f->up; up.y[0] = u; up.expert_stride = f->up_stride;
+        if (kq_moe_gemv_dev(&up, sel, B, k, E, stream)) return -1;
+    }
+
+    /* SwiGLU, down, weighted accumulate + residual */
+    if (kq_swiglu_dev(g, u, act, (int64_t)B * k * F, stream)) return -1;
+    kq_moe_op dn;
+    memset(&dn, 0, sizeof dn);
+    dn.type = f->down_type; dn.n_out = H; dn.k_in = F; dn.x = act; dn.x_div = 1;
+    dn.ntensors = 1; dn.w[0] = f->down; dn.y[0] = ffo; dn.expert_stride = f->down_stride;
+    if (kq_moe_gemv_dev(&dn, sel, B, k, E, stream)) return -1;
+    return kq_moe_combine_dev(ffo, sel, selw, x, x, B, k, H, stream);
 }

@@ -1,0 +1,290 @@
+"""GPU parity of the MoE FFN step around the gather (kq_softmax_dev,
+kq_swiglu_dev, kq_moe_combine_dev, the dense multi-stream router GEMV and
+kq_moe_ffn_dev) against the CPU oracle (oracle/kq_oracle.c ko_softmax,
+ko_swiglu, ko_moe_combine, ko_moe_ffn, pinned by
+tests/test_oracle_moe_ffn.py).
+
+Bars:
+  * softmax and SwiGLU use the device expf (within one ulp of exp) where
+    the reference calls libm's: every output within 4 binary32 ulps of the
+    oracle's; exactly representable cases (equal logits, -inf, NaN, g = 0,
+    large |g|) bit for bit;
+  * combine: bit for bit (binary32 in rank order);
+  * router GEMV (F32 / F16 rows): within one ulp of the oracle's binary64
+    element-order sum; every stream of the multi-stream form bit-identical
+    to its single-stream launch;
+  * the whole step: each stage checked against the oracle applied to the
+    device's own previous stage (GEMVs at their 1e-5 contract, bit-identical
+    counts printed; combine bit for bit), sel identical to the oracle's
+    top-k of the device's probabilities, and the final x within 1e-4 of
+    the all-oracle chain relative to the largest FFN contribution.
+"""
+import numpy as np
+import pytest
+
+import stratum_amd as K
+from conftest import same_values
+from oracle import oracle as O
+from stratum_amd import TYPE_F16, TYPE_F32, TYPE_Q4_K, synth
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    K.lib()
+    yield
+    torch.cuda.synchronize()
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def ulps(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    sp = np.spacing(np.abs(b).astype(np.float32)).astype(np.float64)
+    d = np.abs(a - b)
+    d[np.isnan(a) & np.isnan(b)] = 0.0
+    return d / sp
+
+
+def gpu_softmax(x2d):
+    d = dev(x2d.reshape(-1))
+    K.softmax_dev(d.data_ptr(), x2d.shape[0], x2d.shape[1], stream())
+    torch.cuda.synchronize()
+    return d.cpu().numpy().reshape(x2d.shape)
+
+
+def gpu_swiglu(g, u):
+    dg, du = dev(g), dev(u)
+    dy = torch.full(g.shape, float("nan"), dtype=torch.float32, device="cuda")
+    K.swiglu_dev(dg.data_ptr(), du.data_ptr(), dy.data_ptr(), g.size, stream())
+    torch.cuda.synchronize()
+    return dy.cpu().numpy()
+
+
+# ---------------------------------------------------------------- softmax
+@pytest.mark.parametrize("B,E", [(1, 1), (1, 128), (16, 128), (4, 1000), (2, 4096)])
+def test_softmax_within_ulps(port, B, E):
+    r = synth.rng(9100 + E + B)
+    x = (r.standard_normal((B, E)) * 4).astype(np.float32)
+    print(f"softmax B={B} E={E}", flush=True)
+    got, want = gpu_softmax(x), port.softmax(x)
+    u = ulps(got, want)
+    print(f"  max ulps {u.max():.1f}, bit-identical {int(np.sum(got == want))}/{got.size}",
+          flush=True)
+    assert u.max() <= 4.0
+
+
+def test_softmax_exact_cases(port):
+    ar = np.arange(128, dtype=np.float32)
+    x = np.stack([np.full(128, 0.375, np.float32),
+                  np.array([0.0, -np.inf] * 64, np.float32),
+                  np.where(ar == 0, np.float32(np.nan), ar - 1),
+                  np.where(ar == 127, np.float32(np.nan), ar)]).astype(np.float32)
+    got = gpu_softmax(x)
+    assert same_values(got, port.softmax(x))
+    assert np.all(got[0] == np.float32(1 / 128))
+    assert np.all(np.isnan(got[2])) and np.all(np.isnan(got[3]))
+
+
+# ----------------------------------------------------------------- SwiGLU
+@pytest.mark.parametrize("n", [1, 5, 768, 98304 + 3])
+def test_swiglu_within_ulps(port, n):
+    r = synth.rng(9200 + n)
+    g = (r.standard_normal(n) * 4).astype(np.float32)
+    u = r.standard_normal(n).astype(np.float32)
+    got, want = gpu_swiglu(g, u), port.swiglu(g, u)
+    uu = ulps(got, want)
+    print(f"swiglu n={n}: max ulps {uu.max():.1f}, bit-identical "
+          f"{int(np.sum(got == want))}/{n}", flush=True)
+    assert uu.max() <= 4.0
+
+
+def test_swiglu_exact_cases(port):
+    g = np.array([0.0, 0.0, 100.0, 100.0, -100.0, 2.0, -0.0, 90.0], np.float32)
+    u = np.array([5.0, -3.0, 0.25, -1.5, 3.0, 0.0, 1.0, 2.0], np.float32)
+    assert same_values(gpu_swiglu(g, u), port.swiglu(g, u))
+
+
+# ---------------------------------------------------------------- combine
+@pytest.mark.parametrize("B,k,H", [(1, 8, 2048), (16, 8, 2048), (3, 2, 4)])
+def test_combine_bit_exact(port, B, k, H):
+    r = synth.rng(9300 + B)
+    o = (r.standard_normal(B * k * H) * 3).astype(np.float32)
+    sel = r.integers(0, 128, B * k).astype(np.int32)
+    sel[::5] = -1
+    selw = r.random(B * k).astype(np.float32)
+    resid = r.standard_normal(B * H).astype(np.float32)
+    do, ds, dw, dr = dev(o), dev(sel), dev(selw), dev(resid)
+    dx = torch.full((B * H,), float("nan"), dtype=torch.float32, device="cuda")
+    K.moe_combine_dev(do.data_ptr(), ds.data_ptr(), dw.data_ptr(), dr.data_ptr(), dx.data_ptr(),
+                      B, k, H, stream())
+    torch.cuda.synchronize()
+    assert same_values(dx.cpu().numpy(), port.moe_combine(o, sel, selw, resid, B, k, H))
+    # in place (x == resid)
+    K.moe_combine_dev(do.data_ptr(), ds.data_ptr(), dw.data_ptr(), dr.data_ptr(), dr.data_ptr(),
+                      B, k, H, stream())
+    torch.cuda.synchronize()
+    assert same_values(dr.cpu().numpy(), port.moe_combine(o, sel, selw, resid, B, k, H))
+
+
+# ------------------------------------------------------------ dense router
+@pytest.mark.parametrize("qtype", [TYPE_F32, TYPE_F16])
+@pytest.mark.parametrize("B,N,Kd", [(16, 128, 2048), (9, 300, 1024), (3, 64, 5120)])
+def test_dense_multix_equals_single(port, qtype, B, N, Kd):
+    w = synth.tensor(qtype, N, Kd, 9400 + N)
+    xs = np.stack([synth.gaussian(synth.rng(9401 + s), Kd) for s in range(B)])
+    dw, dx = dev(w), dev(xs.reshape(-1))
+    dy = torch.full((B * N,), float("nan"), dtype=torch.float32, device="cuda")
+    K.gemv_multix_dev(qtype, dw.data_ptr(), dx.data_ptr(), dy.data_ptr(), B, N, Kd, stream())
+    torch.cuda.synchronize()
+    ys = dy.cpu().numpy().reshape(B, N)
+    for s in range(B):
+        d1 = torch.full((N,), float("nan"), dtype=torch.float32, device="cuda")
+        K.gemv_dev(qtype, dw.data_ptr(), dx.data_ptr() + 4 * s * Kd, d1.data_ptr(), N, Kd,
+                   stream=stream())
+        torch.cuda.synchronize()
+        assert same_values(ys[s], d1.cpu().numpy()), s
+    assert ulps(ys[0], port.gemv(qtype, w, xs[0], N, Kd)).max() <= 1.0
+
+
+# --------------------------------------------------------- the whole step
+def make_layer(H, F, E, k, seed, qtype=TYPE_Q4_K, router_type=TYPE_F32):
+    rb_in = synth.row_bytes(qtype, H)
+    rb_ff = synth.row_bytes(qtype, F)
+    router = synth.tensor(router_type, E, H, seed)
+    return {"n_embed": H, "n_ff": F, "n_experts": E, "k": k,
+            "router_type": router_type, "router": router,
+            "gate_type": qtype, "gate": synth.tensor(qtype, E * F, H, seed + 1),
+            "up_type": qtype, "up": synth.tensor(qtype, E * F, H, seed + 2),
+            "down_type": qtype, "down": synth.tensor(qtype, E * H, F, seed + 3),
+            "gate_stride": F * rb_in, "up_stride": F * rb_in, "down_stride": H * rb_ff}
+
+
+def run_step(d, xn, x0, B):
+    H, F, E, k = d["n_embed"], d["n_ff"], d["n_experts"], d["k"]
+    bufs = {n: dev(d[n]) for n in ("router", "gate", "up", "down")}
+    f = K.KqMoeFfn()
+    f.n_embed, f.n_ff, f.n_experts, f.k = H, F, E, k
+    for n in ("router", "gate", "up", "down"):
+        setattr(f, n, bufs[n].data_ptr())
+        setattr(f, n + "_type", d[n + "_type"])
+    f.gate_stride, f.up_stride, f.down_stride = d["gate_stride"], d["up_stride"], d["down_stride"]
+    nbytes = K.moe_ffn_workspace_bytes(f, B)
+    work = torch.full((nbytes // 4,), float("nan"), dtype=torch.float32, device="cuda")
+    dxn, dx = dev(xn), dev(x0)
+    sel = torch.full((B * k,), -7, dtype=torch.int32, device="cuda")
+    selw = torch.full((B * k,), 7.0, dtype=torch.float32, device="cuda")
+    K.moe_ffn_dev(f, dxn.data_ptr(), dx.data_ptr(), B, sel.data_ptr(), selw.data_ptr(),
+                  work.data_ptr(), nbytes, stream())
+    torch.cuda.synchronize()
+    off = K.moe_ffn_workspace_offsets(f, B)
+    wk = work.cpu().numpy()
+    sizes = {"probs": B * E, "g": B * k * F, "u": B * k * F, "act": B * k * F, "ffo": B * k * H}
+    out = {n: wk[off[n] // 4:off[n] // 4 + sizes[n]] for n in sizes}
+    out.update(x=dx.cpu().numpy(), sel=sel.cpu().numpy(), selw=selw.cpu().numpy())
+    return out
+
+
+@pytest.mark.parametrize("B", [1, 16])
+def test_moe_ffn_step_config(port, B):
+    """128 experts, top-8, hidden 2048, expert ffn 768, Q4_K
+    experts, F32 router."""
+    H, F, E, k = 2048, 768, 128, 8
+    d = make_layer(H, F, E, k, 9500)
+    r = synth.rng(9501 + B)
+    xn = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
+    x0 = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
+    print(f"moe ffn step B={B}", flush=True)
+    got = run_step(d, xn, x0, B)
+    rb_in, rb_ff = synth.row_bytes(TYPE_Q4_K, H), synth.row_bytes(TYPE_Q4_K, F)
+    # the router logits as the step computes them (the same dense kernel)
+    dr, dxn = dev(d["router"]), dev(xn)
+    dl = torch.empty(B * E, dtype=torch.float32, device="cuda")
+    K.gemv_multix_dev(TYPE_F32, dr.data_ptr(), dxn.data_ptr(), dl.data_ptr(), B, E, H, stream())
+    torch.cuda.synchronize()
+    glog = dl.cpu().numpy()
+    n_or = 0
+    for s in range(B):
+        xs = xn[s * H:(s + 1) * H]
+        lg = glog[s * E:(s + 1) * E]
+        assert ulps(lg, port.gemv(TYPE_F32, d["router"], xs, E, H)).max() <= 1.0, s
+        p = got["probs"][s * E:(s + 1) * E]
+        assert ulps(p, port.softmax(lg)).max() <= 4.0, s
+        sel, selw = port.topk(p, k)
+        assert list(got["sel"][s * k:(s + 1) * k]) == sel, s
+        assert same_values(got["selw"][s * k:(s + 1) * k], selw), s
+        for r_, e in enumerate(sel):
+            m = s * k + r_
+            g, u = got["g"][m * F:(m + 1) * F], got["u"][m * F:(m + 1) * F]
+            a = got["act"][m * F:(m + 1) * F]
+            assert ulps(a, port.swiglu(g, u)).max() <= 4.0, m
+            if n_or < 6:      # the GEMV members against the oracle (1e-5 contract)
+                gw = port.gemv(TYPE_Q4_K, d["gate"][e * F * rb_in:(e + 1) * F * rb_in], xs, F, H)
+                uw = port.gemv(TYPE_Q4_K, d["up"][e * F * rb_in:(e + 1) * F * rb_in], xs, F, H)
+                ow = port.gemv(TYPE_Q4_K, d["down"][e * H * rb_ff:(e + 1) * H * rb_ff], a, H, F)
+                o = got["ffo"][m * H:(m + 1) * H]
+                for name, gv, wv in (("gate", g, gw), ("up", u, uw), ("down", o, ow)):
+                    rel = O.rel_err(gv, wv).max()
+                    print(f"  member {m} {name}: max rel {rel:.2e}, bit-identical "
+                          f"{int(np.sum(gv == wv))}/{wv.size}", flush=True)
+                    assert rel <= 1e-5, (m, name)
+                n_or += 1
+    want_x = port.moe_combine(got["ffo"], got["sel"], got["selw"], x0, B, k, H)
+    assert same_values(got["x"], want_x)
+    full = port.moe_ffn(d, xn, x0, B)
+    assert np.array_equal(full["sel"], got["sel"])
+    contrib = np.abs(full["x"] - x0).max()
+    err = np.abs(got["x"] - full["x"]).max()
+    print(f"  end to end: max |x - x_oracle| {err:.3e} (largest FFN contribution {contrib:.3e})",
+          flush=True)
+    assert err <= 1e-4 * contrib
+
+
+def test_moe_ffn_step_f16_router_mixed_types(port):
+    """An F16 router and gate/up/down of different types (Q4_K gate/up,
+    Q6_K down): gate and up still share one routed launch, down has its
+    own type."""
+    H, F, E, k, B = 1024, 512, 32, 4, 3
+    d = make_layer(H, F, E, k, 9600, router_type=TYPE_F16)
+    d["down_type"] = 14
+    d["down"] = synth.tensor(14, E * H, F, 9604)
+    d["down_stride"] = H * synth.row_bytes(14, F)
+    r = synth.rng(9601)
+    xn = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
+    x0 = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
+    got = run_step(d, xn, x0, B)
+    full = port.moe_ffn(d, xn, x0, B)
+    assert np.array_equal(full["sel"], got["sel"])
+    assert same_values(got["x"], port.moe_combine(got["ffo"], got["sel"], got["selw"], x0, B, k,
+                                                  H))
+    contrib = np.abs(full["x"] - x0).max()
+    assert np.abs(got["x"] - full["x"]).max() <= 1e-4 * contrib
+
+
+def test_moe_ffn_refuses_short_workspace():
+    H, F, E, k, B = 512, 256, 16, 4, 2
+    f = K.KqMoeFfn()
+    f.n_embed, f.n_ff, f.n_experts, f.k = H, F, E, k
+    f.router_type = f.gate_type = f.up_type = f.down_type = TYPE_Q4_K
+    buf = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    for n in ("router", "gate", "up", "down"):
+        setattr(f, n, buf.data_ptr())
+    f.gate_stride = f.up_stride = f.down_stride = 1 << 16
+    need = K.moe_ffn_workspace_bytes(f, B)
+    x = torch.zeros(B * H, dtype=torch.float32, device="cuda")
+    sel = torch.zeros(B * k, dtype=torch.int32, device="cuda")
+    rc = K.lib().kq_moe_ffn_dev(K.ctypes.byref(f), x.data_ptr(), x.data_ptr(), B, sel.data_ptr(),
+                                sel.data_ptr(), buf.data_ptr(), need - 256, None)
+    assert rc == -1 and b"workspace" in K.lib().kq_last_error()
