@@ -249,7 +249,37 @@ class Ref:
         L.kqref_dot_row.argtypes = [I, _U8, I, _F]
         L.kqref_dot_row.restype = ctypes.c_float
         L.kqref_gemv.argtypes = [I, _U8, _F, _F, I, I, I, I]
+        self.has_gguf = hasattr(L, "kqref_gguf_open")
+        if self.has_gguf:
+            P = ctypes.c_void_p
+            L.kqref_gguf_open.argtypes = [ctypes.c_char_p, P, I, P, P, P, P, P, P, P]
         self.L = L
+
+    def gguf_open(self, path: str, cap: int = 64):
+        """gguf_open on the file: None if refused, else (n_tensors, n_kv,
+        body_offset, alignment) and per-tensor dicts (the first cap)."""
+        counts = np.zeros(4, np.uint64)
+        types = np.zeros(cap, np.uint32)
+        ndims = np.zeros(cap, np.uint32)
+        dims = np.zeros(8 * cap, np.uint64)
+        offs = np.zeros(cap, np.uint64)
+        nelem = np.zeros(cap, np.int64)
+        nbytes = np.zeros(cap, np.int64)
+        names = np.zeros(64 * cap, np.uint8)
+        rc = self.L.kqref_gguf_open(path.encode(), counts.ctypes.data, cap, types.ctypes.data,
+                                    ndims.ctypes.data, dims.ctypes.data, offs.ctypes.data,
+                                    nelem.ctypes.data, nbytes.ctypes.data, names.ctypes.data)
+        if rc != 0:
+            return None
+        n = int(counts[0])
+        ts = []
+        for i in range(min(n, cap)):
+            nm = bytes(names[64 * i:64 * i + 64]).split(b"\0")[0]
+            ts.append({"name": nm, "type": int(types[i]), "n_dims": int(ndims[i]),
+                       "dims": [int(v) for v in dims[8 * i:8 * i + int(ndims[i])]],
+                       "offset": int(offs[i]), "nelem": int(nelem[i]),
+                       "nbytes": int(nbytes[i])})
+        return tuple(int(c) for c in counts), ts
 
     def dequant(self, qtype: int, w: np.ndarray, nrows: int, K: int) -> np.ndarray:
         y = np.empty(nrows * K, np.float32)

@@ -15,6 +15,7 @@
  *   q{4,6,2}k_dot_row_scalar                     (stratum_q4k.h:95, q6k.h:38, q2k.h:44)
  *   q{3,5}k_dequant_block_scalar / _dot_row_scalar (stratum_q3k.h:30, 58; q5k.h:18, 44)
  *   q8_0_dequant_block_scalar / _dot_row_scalar  (stratum_q8_0.h:14, 19)
+ *   gguf_open / gguf_close                        (stratum_gguf.h:226-463)
  * plus a pthread row split with 64-row tickets, as ST_PAR_ROWS does
  * (stratum_linear.h:201-228) on a machine without NEON (stratum_linear.h:446-451).
  */
@@ -25,6 +26,7 @@
 #include "stratum_q3k.h"
 #include "stratum_q5k.h"
 #include "stratum_q8_0.h"
+#include "stratum_gguf.h"
 
 #include <pthread.h>
 #include <stdatomic.h>
@@ -149,5 +151,27 @@ int kqref_gemv(int type, const uint8_t* w, const float* xs, float* ys,
     }
     kqref_worker(&j);
     for (int t = 0; t < started; t++) pthread_join(th[t], NULL);
+    return 0;
+}
+
+/* gguf_open on a file, its index copied out: 0 (opened) or -1 (refused).
+ * Per tensor i < min(n_tensors, cap): type, n_dims, dims[8 i ..], offset
+ * (absolute, as gguf_open leaves it), nelem, nbytes and the first 63
+ * bytes of the name at names + 64 i. */
+int kqref_gguf_open(const char* path, uint64_t* counts /* n_tensors, n_kv, body, align */,
+                    int cap, uint32_t* types, uint32_t* ndims, uint64_t* dims, uint64_t* offsets,
+                    int64_t* nelem, int64_t* nbytes, char* names) {
+    Gguf g;
+    if (gguf_open(path, &g) != 0) return -1;
+    counts[0] = g.n_tensors; counts[1] = g.n_kv; counts[2] = g.body_offset; counts[3] = g.alignment;
+    for (uint64_t i = 0; i < g.n_tensors && i < (uint64_t)cap; i++) {
+        const GgufTensor* t = &g.tensors[i];
+        types[i] = t->type; ndims[i] = t->n_dims;
+        for (int d = 0; d < 8; d++) dims[8 * i + d] = t->dims[d];
+        offsets[i] = t->offset; nelem[i] = t->nelem; nbytes[i] = t->nbytes;
+        strncpy(names + 64 * i, t->name, 63);
+        names[64 * i + 63] = 0;
+    }
+    gguf_close(&g);
     return 0;
 }

@@ -58,6 +58,12 @@ EXPORTS = (
     "kq_quantize_x_q8_dev", "kq_softmax_dev", "kq_swiglu_dev", "kq_moe_combine_dev",
     "kq_moe_ffn_workspace_bytes", "kq_moe_ffn_dev",
 )
+# include/kq_gguf.h (bound in stratum_amd/gguf.py)
+GGUF_EXPORTS = (
+    "kq_gguf_open", "kq_gguf_close", "kq_gguf_find_tensor", "kq_gguf_find_kv",
+    "kq_gguf_get_u32", "kq_gguf_get_u64", "kq_gguf_get_f32", "kq_gguf_get_string_dup",
+    "kq_gguf_type_size", "kq_gguf_nib_convert", "kq_q2k_to_nib_dev", "kq_moe_pack_check",
+)
 
 NOALLOC_SCRATCH_BYTES = 32 << 20   # KQ_NOALLOC_SCRATCH_BYTES
 
@@ -260,7 +266,8 @@ def _fptr(a: np.ndarray):
 
 def _check(rc: int, what: str) -> None:
     if rc != 0:
-        raise RuntimeError(f"{what} failed: {lib().kq_last_error().decode()}")
+        msg = lib().kq_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed: {msg}")
 
 
 class WeightRegion:
@@ -427,7 +434,8 @@ def moe_combine_dev(o_ptr: int, sel_ptr: int, selw_ptr: int, resid_ptr: int, x_p
 def moe_ffn_workspace_bytes(f: KqMoeFfn, B: int) -> int:
     n = lib().kq_moe_ffn_workspace_bytes(ctypes.byref(f), B)
     if n < 0:
-        raise RuntimeError(f"kq_moe_ffn_workspace_bytes failed: {lib().kq_last_error().decode()}")
+        msg = lib().kq_last_error().decode(errors="replace")
+        raise RuntimeError(f"kq_moe_ffn_workspace_bytes failed: {msg}")
     return n
 
 

@@ -3205,6 +3205,32 @@ __global__ __launch_bounds__(256) void kq_moe_combine_kernel(const float* o, con
         make_float4(rv.x + acc.x, rv.y + acc.y, rv.z + acc.z, rv.w + acc.w);
 }
 
+// Q2_K (84 B) -> type 42 (148 B), one lane per output dword: dwords 0-3
+// the scales, 4-35 the nibbles (weight p of the block, the 2-bit field
+// (p % 128) / 32 of qs byte 32 (p / 128) + p % 32, goes to byte
+// 16 + 16 (p / 32) + p % 16, low nibble for p % 32 < 16), 36 d and dmin
+// (tools_gguf_nib_convert.c:99-120).
+__global__ __launch_bounds__(256) void kq_q2k_to_nib_kernel(const uint32_t* q, uint32_t* o,
+                                                            long nblocks) {
+    const long t = (long)blockIdx.x * 256 + threadIdx.x;
+    if (t >= nblocks * 37) return;
+    const long b = t / 37;
+    const int w = (int)(t - b * 37);
+    const uint32_t* src = q + b * 21;
+    uint32_t v;
+    if (w < 4) {
+        v = src[w];
+    } else if (w == 36) {
+        v = src[20];
+    } else {
+        const int grp = (w - 4) >> 2, l0 = 4 * ((w - 4) & 3), sh = 2 * (grp & 3);
+        const uint32_t lo = src[4 + 8 * (grp >> 2) + (l0 >> 2)];       // qs bytes l0 .. l0+3
+        const uint32_t hi = src[4 + 8 * (grp >> 2) + 4 + (l0 >> 2)];   // qs bytes l0+16 ..
+        v = ((lo >> sh) & 0x03030303u) | (((hi >> sh) & 0x03030303u) << 4);
+    }
+    o[b * 37 + w] = v;
+}
+
 // x -> int8 per group of G (32: q4k_quantize_x_q8 + q4k_sum_i8_32; 16:
 // q6k_quantize_x_q8_g16 + q6k_xsum16_i8), the arithmetic of store_i8: one
 // lane per group.
@@ -3764,6 +3790,14 @@ int kqk_launch_dequant(int type, const void* w, float* y, long nblocks, hipStrea
     }
     default: return -1;
     }
+}
+
+int kqk_launch_q2k_to_nib(const void* q2k, void* nib, long nblocks, hipStream_t st) {
+    if (nblocks < 1) return (int)hipErrorInvalidValue;
+    const long n = nblocks * 37;
+    hipLaunchKernelGGL(kq_q2k_to_nib_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                       static_cast<const uint32_t*>(q2k), static_cast<uint32_t*>(nib), nblocks);
+    return (int)hipGetLastError();
 }
 
 int kqk_launch_softmax(float* x, int B, int E, hipStream_t st) {

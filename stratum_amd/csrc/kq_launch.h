@@ -40,6 +40,8 @@ int kqk_launch_dequant(int type, const void* w, float* y, long nblocks, hipStrea
 /* dense F16 / F32 rows (types 1 / 0): y = W x (+ add) on `grid` workgroups */
 int kqk_launch_dense(int type, const void* w, const float* x, const float* add, float* y, int N,
                      int K, int B, int grid, hipStream_t st);
+/* Q2_K -> type-42 block permutation */
+int kqk_launch_q2k_to_nib(const void* q2k, void* nib, long nblocks, hipStream_t st);
 /* MoE FFN step pieces */
 int kqk_launch_softmax(float* x, int B, int E, hipStream_t st);
 int kqk_launch_swiglu(const float* g, const float* u, float* y, long n, hipStream_t st);

@@ -14,6 +14,7 @@
  */
 #define _GNU_SOURCE
 #include "../../include/kq_gemv.h"
+#include "../../include/kq_gguf.h"
 
 #include <hip/hip_runtime_api.h>
 #include <math.h>
@@ -58,7 +59,8 @@ typedef struct {
 
 static kq_state g_kq;
 
-static int kq_fail(const char* fmt, ...) {
+/* shared with kq_gguf.c; not exported */
+__attribute__((visibility("hidden"))) int kq_fail(const char* fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
     vsnprintf(g_kq.err, sizeof g_kq.err, fmt, ap);
@@ -1152,4 +1154,16 @@ int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* s
     dn.ntensors = 1; dn.w[0] = f->down; dn.y[0] = ffo; dn.expert_stride = f->down_stride;
     if (kq_moe_gemv_dev(&dn, sel, B, k, E, stream)) return -1;
     return kq_moe_combine_dev(ffo, sel, selw, x, x, B, k, H, stream);
+}
+
+/* --------------------------------------------- type-42 on the device */
+int kq_q2k_to_nib_dev(const void* q2k, void* nib, int64_t nblocks, kq_stream stream) {
+    if (kq_ready()) return -1;
+    if (!q2k || !nib) return kq_fail("kq_q2k_to_nib_dev: NULL pointer");
+    if (((uintptr_t)q2k | (uintptr_t)nib) & 3)
+        return kq_fail("kq_q2k_to_nib_dev: buffers must be 4-byte aligned");
+    if (nblocks < 1 || nblocks > ((int64_t)1 << 40)) return kq_fail("kq_q2k_to_nib_dev: nblocks");
+    const int e = kqk_launch_q2k_to_nib(q2k, nib, (long)nblocks, pick(stream));
+    if (e) return kq_fail("q2k_to_nib launch: %s", hipGetErrorString((hipError_t)e));
+    return 0;
 }

@@ -12,7 +12,9 @@ sources where they lie by oracle/Makefile:
     q8_0_dot_row_scalar (stratum_q4k.h, stratum_q6k.h, stratum_q2k.h,
     stratum_q5k.h, stratum_q3k.h, stratum_q8_0.h);
   * oracle/_ref/nib_convert -- tools_gguf_nib_convert.c, run on a small GGUF
-    v3 file written here, for the type-42 bytes.
+    v3 file written here, for the type-42 bytes;
+  * gguf_open (stratum_gguf.h:226-444, through ref_harness.c) on the GGUF
+    corpus of gguf.npz: its verdict and index for every file.
 Inputs are seeded numpy draws plus hand-built edge blocks.  Nothing from
 the repo's own oracle (oracle/kq_oracle.c) is used, so the fixtures pin it.
 
@@ -20,6 +22,10 @@ Each fixture file <type>.npz holds, per case c:
   c_w (uint8 blocks), c_x (float32 [K]), c_shape ([N, K]),
   c_deq (float32 [N*K]), c_y (float32 [N]);
 and for type 42 also c_src, the Q2_K bytes given to the converter.
+gguf.npz holds the corpus files back to back (blob, lens), the reference's
+accept flag, (n_tensors, n_kv, body_offset, alignment) and the first 8
+tensors' type / offset / nelem / nbytes per file, and a small model before
+(nib_in) and after (nib_out) the reference's type-42 converter.
 """
 from __future__ import annotations
 
@@ -174,6 +180,84 @@ def make_cases(t: int, ref: O.Ref):
     return cases
 
 
+def gguf_corpus():
+    """The GGUF files of the parser fixture: the hostile cases of
+    gguf_bounds_test.c and input_guards_test.c, a well-formed model and
+    seeded corruptions of it."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import gguf_build as G
+    six = b"\xab" * 16
+    files = [
+        G.bounds_case([4], 0, 0, six), G.bounds_case([1 << 62, 8], 0, 0, b""),
+        G.bounds_case([(2 ** 63 - 1) // 4 + 1], 0, 0, b""), G.bounds_case([100], 12, 0, b""),
+        G.bounds_case([2 ** 64 - 1], 0, 0, b""), G.bounds_case([4], 99, 0, b""),
+        G.bounds_case([4], 0, 0, six, nest_depth=2), G.bounds_case([4], 0, 0, six, nest_depth=64),
+        G.bounds_case([4], 0, 0, b""),
+        G.guards_case(1, 1, 0, 0, 512), G.guards_case(1, 1, 0, 2 ** 64 - 9, 512),
+        G.guards_case(1, 1, 100, 1 << 40, 512), G.guards_case(1, 1, 100, 0, 512),
+        G.guards_case(1, 1, 100, 512, 512), G.guards_case(1 << 40, 1, 0, 0, 512),
+        G.guards_case(1, 1 << 40, 0, 0, 512),
+    ]
+    r = np.random.Generator(np.random.PCG64(0x66))
+    base = gguf_model(r)
+    files.append(base.tobytes())
+    files += [m.tobytes() for m in G.mutations(base, 400, 0x67)]
+    return files
+
+
+def gguf_model(r):
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import gguf_build as G
+    ts = [("blk.0.attn_q.weight", [512, 4], Q4, rand_blocks(Q4, r, 8).tobytes()),
+          ("blk.0.ffn_down.weight", [256, 2], Q6, rand_blocks(Q6, r, 2).tobytes()),
+          ("blk.0.ffn_gate.weight", [256, 3], Q2, rand_blocks(Q2, r, 3).tobytes()),
+          ("output_norm.weight", [40], 0, r.standard_normal(40).astype(np.float32).tobytes()),
+          ("blk.0.ffn_up.weight", [256, 2], Q2, rand_blocks(Q2, r, 2).tobytes()),
+          ("token_embd.weight", [16, 2], 1, r.standard_normal(32).astype(np.float16).tobytes())]
+    kvs = [G.kv_str("general.architecture", "llama"), G.kv_u32("llama.block_count", 1),
+           G.kv_u64("llama.context_length", 4096), G.kv_f32("llama.rope.freq_base", 1e6),
+           G.kv_array_u32("tokenizer.ggml.token_type", [1, 2, 3]),
+           G.kv_array_str("tokenizer.ggml.tokens", ["a", "bc", ""])]
+    return G.model(ts, kvs, align=64)
+
+
+def make_gguf_fixture(ref: O.Ref):
+    """gguf.npz: every corpus file with the reference gguf_open's verdict and
+    index (up to 8 tensors), and a model converted by the reference tool."""
+    files = gguf_corpus()
+    cap = 8
+    n = len(files)
+    accept = np.zeros(n, np.int8)
+    counts = np.zeros((n, 4), np.uint64)
+    types = np.zeros((n, cap), np.uint32)
+    offs = np.zeros((n, cap), np.uint64)
+    nelem = np.zeros((n, cap), np.int64)
+    nbytes = np.zeros((n, cap), np.int64)
+    with tempfile.TemporaryDirectory() as td:
+        path = os.path.join(td, "f.gguf")
+        for i, fb in enumerate(files):
+            with open(path, "wb") as f:
+                f.write(fb)
+            got = ref.gguf_open(path, cap)
+            if got is None:
+                continue
+            accept[i] = 1
+            counts[i] = got[0]
+            for j, t in enumerate(got[1]):
+                types[i, j], offs[i, j], nelem[i, j], nbytes[i, j] = (
+                    t["type"], t["offset"], t["nelem"], t["nbytes"])
+        r = np.random.Generator(np.random.PCG64(0x68))
+        model = gguf_model(r)
+        src, dst = os.path.join(td, "in.gguf"), os.path.join(td, "out.gguf")
+        model.tofile(src)
+        subprocess.run([O.NIBCONV_PATH, src, dst], check=True, capture_output=True)
+        conv = np.fromfile(dst, np.uint8)
+    lens = np.array([len(f) for f in files], np.int64)
+    blob = np.frombuffer(b"".join(files), np.uint8)
+    return dict(blob=blob, lens=lens, accept=accept, counts=counts, types=types, offsets=offs,
+                nelem=nelem, nbytes=nbytes, nib_in=model, nib_out=conv)
+
+
 def main() -> None:
     O.build()
     ref = O.ref()
@@ -188,6 +272,10 @@ def main() -> None:
         np.savez_compressed(path, **arrays)
         h = hashlib.sha256(open(path, "rb").read()).hexdigest()
         manifest.append(f"{fname}.npz {h} {os.path.getsize(path)}")
+    path = os.path.join(HERE, "gguf.npz")
+    np.savez_compressed(path, **make_gguf_fixture(ref))
+    h = hashlib.sha256(open(path, "rb").read()).hexdigest()
+    manifest.append(f"gguf.npz {h} {os.path.getsize(path)}")
     with open(os.path.join(HERE, "MANIFEST"), "w") as f:
         f.write("# sha256 and size of each fixture written by make_golden.py\n")
         f.write("\n".join(manifest) + "\n")

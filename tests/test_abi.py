@@ -13,16 +13,22 @@ import stratum_amd as K
 
 ROOT = os.path.abspath(os.path.join(os.path.dirname(__file__), ".."))
 HEADER = os.path.join(ROOT, "include", "kq_gemv.h")
+GGUF_HEADER = os.path.join(ROOT, "include", "kq_gguf.h")
 
 
-def declared_functions():
-    text = open(HEADER).read()
+def declared_in(path):
+    text = open(path).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(kq_[a-z0-9_]+)\s*\(", text)))
 
 
+def declared_functions():
+    return sorted(set(declared_in(HEADER)) | set(declared_in(GGUF_HEADER)))
+
+
 def test_header_and_python_export_list_agree():
-    assert declared_functions() == sorted(K.EXPORTS)
+    assert declared_in(HEADER) == sorted(K.EXPORTS)
+    assert declared_in(GGUF_HEADER) == sorted(K.GGUF_EXPORTS)
 
 
 def test_library_exports_every_declared_symbol():
