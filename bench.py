@@ -486,6 +486,32 @@ def cfg5(L, torch, stream, host_w) -> dict:
                         "bytes": nb, "GB/s": round(nb / us / 1e3, 1),
                         "launches": 2 if B * ((E + 63) // 64 * 64) ** 2 <= 1 << 16 else 3,
                         "route": "kq_moe_gemv_routed_dev"}
+        # the whole expert FFN step (kq_moe_ffn_dev): F32 router GEMV, softmax,
+        # routed gate+up, SwiGLU, down, rank-ordered combine + residual
+        router = torch.from_numpy(synth.tensor(KQ.TYPE_F32, E, H, 3703)).cuda()
+        ffns = []
+        for c in cm:
+            f = KQ.KqMoeFfn()
+            f.n_embed, f.n_ff, f.n_experts, f.k = H, F, E, k
+            f.router_type, f.router = KQ.TYPE_F32, router.data_ptr()
+            f.gate_type = f.up_type = f.down_type = 12
+            f.gate, f.up, f.down = c.data_ptr(), c.data_ptr() + E * gsl, c.data_ptr() + 2 * E * gsl
+            f.gate_stride, f.up_stride, f.down_stride = gsl, gsl, dsl
+            ffns.append(f)
+        wbytes = KQ.moe_ffn_workspace_bytes(ffns[0], B)
+        work = torch.empty(wbytes, dtype=torch.uint8, device="cuda")
+        xres = torch.from_numpy(np.stack([synth.gaussian(r, H) for _ in range(B)])).cuda()
+
+        def ffn_step(i):
+            _check(L, L.kq_moe_ffn_dev(ctypes.byref(ffns[i % len(ffns)]), xm.data_ptr(),
+                                       xres.data_ptr(), B, sel.data_ptr(), selw.data_ptr(),
+                                       work.data_ptr(), wbytes, sh))
+        fus = _events_us(torch, stream, ffn_step, 50)
+        res[f"B{B}"]["ffn_step"] = {
+            "us_per_layer": round(fus, 2),
+            "what": "router GEMV (F32 128x2048), softmax, routed gate+up, SwiGLU, down, "
+                    "combine + residual"}
+        del work, router
         if CPU["on"]:
             from oracle import oracle as O
             impl, kind = cpu_impl(12)
@@ -554,10 +580,34 @@ def cfg_int8(L, torch, stream, host_w) -> dict:
                         lambda i: [launch(i, g, flag) for g in range(len(GROUPS))], 100)
         res[key] = {"us_per_layer_set": round(us, 2), "bytes": set_bytes,
                     "GB/s": round(set_bytes / us / 1e3, 1)}
-    for g, (gname, members) in enumerate(GROUPS):
-        gus = _events_us(torch, stream, lambda i: launch(i, g), 100)
+    del arrs
+    # per launch: each group's weights rotated over >= ROTATE_BYTES of copies
+    # (so every launch reads HBM, not the MALL), both modes in one process
+    for gname, members in GROUPS:
+        goff, gtot = {}, 0
+        for m in members:
+            goff[m] = gtot
+            gtot += (host_w[m].size + 255) // 256 * 256
+        gblob = np.zeros(gtot, np.uint8)
+        for m in members:
+            gblob[goff[m]:goff[m] + host_w[m].size] = host_w[m]
+        gc = _copies(torch, gblob, COPIES)
         nb = sum(algo_bytes(spec[m][0], spec[m][1], spec[m][2]) for m in members)
-        res[gname] = {"us": round(gus, 2), "bytes": nb, "GB/s": round(nb / gus / 1e3, 1)}
+        res[gname] = {"bytes": nb, "copies_rotated": len(gc)}
+        for flag, key in ((KQ.INT8_ACT, "int8"), (0, "exact")):
+            garr = []
+            for c in gc:
+                segs = [KQ.segment(spec[m][0] | flag, spec[m][2], spec[m][1],
+                                   [c.data_ptr() + goff[m]], xs[spec[m][3]].data_ptr(),
+                                   ys[m].data_ptr()) for m in members]
+                garr.append(((KQ.KqSegment * len(segs))(*segs), len(segs)))
+
+            def go(i):
+                arr, n = garr[i % len(garr)]
+                _check(L, L.kq_gemv_segments_dev(arr, n, sh))
+            gus = _events_us(torch, stream, go, 100)
+            res[gname][key] = {"us": round(gus, 2), "GB/s": round(nb / gus / 1e3, 1)}
+        del gc
     if CPU["on"]:
         from oracle import oracle as O
         port = O.port()
@@ -567,7 +617,7 @@ def cfg_int8(L, torch, stream, host_w) -> dict:
                    min_s=0.5, max_n=3),
             "port", "the seven matvecs in q*_dot_row_sdot_f's order, one thread")
         res["layer_set"]["cpu"]["cores"] = 1
-    del copies, arrs
+    del copies
     return res
 
 
