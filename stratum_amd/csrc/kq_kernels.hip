@@ -2494,121 +2494,139 @@ __global__ __launch_bounds__(1024) void kq_moe_group_kernel(MoeGroupArg a) {
 }
 
 // ------------------------------------------------------- MFMA multi-x
-// Tolerance path for many streams (B >= 16): the inner products of each
-// sub-block, sum_k q_k x_k, run on the matrix cores as bf16 x bf16 -> fp32
-// MFMAs and are then scaled as the reference does (d*sc times the sum, minus
-// dmin*m times the sum of x).  x enters exactly as three bf16 planes
-// (x = h + m + l: 8 + 8 + 8 significand bits), and every product q * plane
-// is exact in fp32, so the only difference from the reference is the fp32
-// rounding order of the sums (the reference adds sequentially, the MFMA in
-// its own tree) plus fp32 accumulation across sub-blocks: results agree to
-// about one binary32 ulp of each sub-block's sum, not bit for bit.
+// Tolerance path for many streams (B >= 16), Q4_K and Q6_K, on the matrix
+// cores.  The weights enter with their sub-block scales folded in, as exact
+// fp16 integers: Q4_K w = sc*q (sc <= 63, q <= 15: at most 945), Q6_K
+// w = sc*(q - 32) (|w| <= 4096) split exactly into hi = w - (w & 7) and
+// lo = w & 7.  x enters exactly as three fp16 planes of x*2^(15-E), E the
+// binary exponent of the largest |x| of the (stream, super-block), so the
+// planes cannot overflow and every product w*plane is exact in fp32.  A
+// whole super-block (256 weights) accumulates in one MFMA accumulator
+// (mfma_f32_16x16x32_f16); per super-block and output the kernel then adds
+// 2^(E-15)*d*acc minus, for Q4_K, sum_j dmin*m_j*xsum_j (x sums of each
+// 32-value sub-block).  Differences from the reference: the fp32 order of
+// the sums inside a super-block and across super-blocks, and the scale
+// applied to the super-block sum instead of each sub-block's.  The weights
+// of a super-block are decoded once per lane and used for every 16-stream
+// group.
 //
 // Operands: D[stream][row] = sum_k A[stream][k] B[k][row], A = an x plane,
-// B = the weights.  In the 16x16xK MFMAs lane l holds B[k][row = l % 16]
-// for k = KV*(l/16) + v and receives D[4*(l/16) + v][l % 16]: a lane's
-// weight row is its output row, so each lane decodes only its own row's
-// scales.  Within a sub-block any permutation of k is allowed as long as A
-// and B use the same one, which lets a Q6_K lane take 4 consecutive bytes.
-//  * kq_mfma_xsplit_kernel writes the planes in the A-operand order (64 lanes
-//    x KV bf16 per sub-block, stream group of 16 and plane) and the
-//    sequential binary32 sum of x per (stream, sub-block);
-//  * kq_mfma_mx_kernel: a work unit is 64 rows (4 waves, one 16-row tile
-//    each) x a K-part of MF_SBP super-blocks; the x planes of one
-//    super-block are staged in LDS (double-buffered, shared by the 4 waves)
-//    while the previous one is consumed.  Units of a row range with several
-//    K-parts write partial sums, which kq_mfma_reduce_kernel adds in part
-//    order (a fixed order: the result does not depend on timing).
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-constexpr int MF_SBP = 4;            // super-blocks per K-part
-
-template <int TYPE> struct MfInfo;
-template <> struct MfInfo<T_Q4K> { static constexpr int SUB = 32, KV = 8, NSUB = 8; };
-template <> struct MfInfo<T_Q6K> { static constexpr int SUB = 16, KV = 4, NSUB = 16; };
-
-// binary32 -> bf16, round to nearest even (finite inputs)
-__device__ __forceinline__ uint32_t bf16_rne(float f) {
-    uint32_t u = __float_as_uint(f);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
-}
+// B = the weights.  In the 16x16x32 MFMAs lane l holds B[k][row = l % 16]
+// for k = 8*(l/16) + v and receives D[4*(l/16) + v][l % 16]: a lane's
+// weight row is its output row, so each lane decodes only its own row.
+//  * kq_mf_split_kernel: one workgroup per (super-block, 16-stream group)
+//    writes the three planes in A-operand order, E per stream, and (Q4_K)
+//    the sequential binary32 sum of each 32 x;
+//  * kq_mf_kernel: a work unit is 64 rows (4 waves x 16 rows) x a K-part of
+//    MF_SBP super-blocks; the planes of each (super-block, group) pair are
+//    staged in LDS (double-buffered, shared by the 4 waves) while the
+//    previous pair is consumed.  Units with several K-parts write partial
+//    sums, which kq_mfma_reduce_kernel adds in part order (a fixed order:
+//    the result does not depend on timing).
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+constexpr int MF_SBP = 4;                        // super-blocks per K-part
+constexpr int MF_PAIR_PLANES = 8 * 3 * 64;       // uint4 of planes per (super-block, group)
+constexpr int MF_PAIR_BYTES = MF_PAIR_PLANES * 16 + 8 * 16 * 4 + 16 * 4;   // + x sums + E
 
 struct MfSplitArg {
     const float* x;          // B x K
-    uint16_t* planes;        // (K/SUB) x NSG x 3 x 64 x KV
-    float* xs;               // (K/32) x (16 NSG): sums of 32 (Q4_K), or null
+    uint4* planes;           // NSB x NSG x 8 steps x 3 planes x 64 lanes (8 fp16 each)
+    float* xs;               // NSB x 8 x 16 NSG: sums of 32 (Q4_K), or null
+    int* ex;                 // NSB x 16 NSG: E of each (super-block, stream)
     int B, K, NSG;
 };
 
-template <int TYPE>
-__global__ __launch_bounds__(256) void kq_mfma_xsplit_kernel(MfSplitArg a) {
-    using MI = MfInfo<TYPE>;
-    const int t = blockIdx.x * 256 + threadIdx.x;
-    const int nsb = a.K / MI::SUB;
-    if (t >= nsb * a.NSG * 64) return;
-    const int l = t & 63, g = (t >> 6) % a.NSG, sb = (t >> 6) / a.NSG;
-    const int s = 16 * g + (l & 15);
-    const int k0 = MI::SUB * sb + MI::KV * (l >> 4);
-    uint32_t h[MI::KV], m[MI::KV], lo[MI::KV];
+__device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+__global__ __launch_bounds__(256) void kq_mf_split_kernel(MfSplitArg a) {
+    const int sb = blockIdx.x / a.NSG, g = blockIdx.x - sb * a.NSG;
+    const int t = threadIdx.x, si = t >> 4, p = t & 15;
+    const int s = 16 * g + si;
+    const bool live = s < a.B;
+    float v[16];
+    const float4* src = reinterpret_cast<const float4*>(a.x + (size_t)(live ? s : 0) * a.K + 256 * sb + 16 * p);
 #pragma unroll
-    for (int v = 0; v < MI::KV; v++) {
-        const float xv = s < a.B ? a.x[(size_t)s * a.K + k0 + v] : 0.0f;
-        h[v] = bf16_rne(xv);
-        const float r1 = xv - __uint_as_float(h[v] << 16);
-        m[v] = bf16_rne(r1);
-        const float r2 = r1 - __uint_as_float(m[v] << 16);
-        lo[v] = bf16_rne(r2);
+    for (int q = 0; q < 4; q++) {
+        const float4 f = live ? src[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
     }
-    uint16_t* base = a.planes + ((size_t)(sb * a.NSG + g) * 3 * 64 + l) * MI::KV;
+    float mx = 0.0f;
 #pragma unroll
-    for (int v = 0; v < MI::KV; v++) {
-        base[v] = (uint16_t)h[v];
-        base[64 * MI::KV + v] = (uint16_t)m[v];
-        base[128 * MI::KV + v] = (uint16_t)lo[v];
+    for (int i = 0; i < 16; i++) mx = fmaxf(mx, fabsf(v[i]));
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));   // the stream's 16 lanes
+    const int E = __builtin_amdgcn_frexp_expf(mx);        // mx = m 2^E, m in [0.5, 1); 0 for 0
+    // planes: step j = p / 2, lane slots kg = 2 (p & 1) and 2 (p & 1) + 1
+    uint32_t hw[8], mw[8], lw[8];
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) {
+        _Float16 h2[2], m2[2], l2[2];
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const float xv = ldexpf(v[i + e], 15 - E);
+            const _Float16 h = (_Float16)xv;
+            const float r1 = xv - (float)h;
+            const _Float16 m = (_Float16)r1;
+            h2[e] = h; m2[e] = m; l2[e] = (_Float16)(r1 - (float)m);
+        }
+        hw[i / 2] = pack_h2(h2[0], h2[1]);
+        mw[i / 2] = pack_h2(m2[0], m2[1]);
+        lw[i / 2] = pack_h2(l2[0], l2[1]);
     }
-    // per (stream, 32-value sub-block) sums for the Q4_K min terms, in order
-    if (a.xs && MI::SUB == 32 && l < 16) {
+    uint4* dst = a.planes + ((size_t)(sb * a.NSG + g) * 8 + (p >> 1)) * 3 * 64;
+    const int l0 = 16 * (2 * (p & 1)) + si;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        dst[l0 + 16 * h] = make_uint4(hw[4 * h], hw[4 * h + 1], hw[4 * h + 2], hw[4 * h + 3]);
+        dst[64 + l0 + 16 * h] = make_uint4(mw[4 * h], mw[4 * h + 1], mw[4 * h + 2], mw[4 * h + 3]);
+        dst[128 + l0 + 16 * h] = make_uint4(lw[4 * h], lw[4 * h + 1], lw[4 * h + 2], lw[4 * h + 3]);
+    }
+    if (p == 0) a.ex[(size_t)sb * 16 * a.NSG + s] = E;
+    if (a.xs) {
+        // sequential binary32 sum of the 32 values of sub-block p / 2: the
+        // even lane sums its 16, the odd lane continues from it
         float acc = 0.0f;
-        for (int k = 0; k < 32; k++)
-            acc = acc + (s < a.B ? a.x[(size_t)s * a.K + 32 * sb + k] : 0.0f);
-        a.xs[(size_t)sb * (16 * a.NSG) + s] = acc;
+        if (!(p & 1)) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc = acc + v[i];
+        }
+        const float first = __shfl(acc, (t & 63) - (p & 1));
+        if (p & 1) {
+            acc = first;
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc = acc + v[i];
+            a.xs[((size_t)sb * 8 + (p >> 1)) * 16 * a.NSG + s] = acc;
+        }
     }
 }
 
 struct MfArg {
     const uint8_t* w;
-    const uint16_t* planes;
+    const uint4* planes;
     const float* xs;
+    const int* ex;
     float* y;                // B x N
     float* part;             // KP x (16 NSG) x N partial sums (KP > 1)
     int B, N, K, NSG, KP, nunits, grid;
 };
 
-// bf16 of the 4 bytes of v (each an unsigned value < 256), k order = byte order
-__device__ __forceinline__ void bf16_bytes(uint32_t v, uint32_t& lo2, uint32_t& hi2) {
-    float f0, f1, f2, f3;
-    ubytes(v, f0, f1, f2, f3);                     // v_cvt_f32_ubyte{0..3}
-    lo2 = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
-    hi2 = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
-}
-// bf16 of the 4 signed bytes of v
-__device__ __forceinline__ void bf16_sbytes(uint32_t v, uint32_t& lo2, uint32_t& hi2) {
-    const float f0 = (float)(int32_t)(int8_t)(v & 0xffu);
-    const float f1 = (float)(int32_t)(int8_t)((v >> 8) & 0xffu);
-    const float f2 = (float)(int32_t)(int8_t)((v >> 16) & 0xffu);
-    const float f3 = (float)(int32_t)(int8_t)(v >> 24);
-    lo2 = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
-    hi2 = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
+__device__ __forceinline__ uint32_t byte_of(const uint4& v, int i) {
+    const uint32_t w = i < 4 ? v.x : i < 8 ? v.y : i < 12 ? v.z : v.w;
+    return (w >> (8 * (i & 3))) & 0xffu;
 }
 
-// One super-block of one row's weights as one lane needs them (k-group kg).
+// One super-block of one row as one lane needs it (k-group kg).
 struct MfRawQ4 { uint4 hd; uint2 q[4]; };
-struct MfRawQ6 { uint32_t p[12][2]; uint32_t s[5]; uint32_t d, sh; };
+struct MfRawQ6 { uint32_t ql[4][3], qh[2][3], sc[5]; uint32_t d, sh; };
 template <int TYPE> struct MfRaw;
 template <> struct MfRaw<T_Q4K> { using T = MfRawQ4; };
 template <> struct MfRaw<T_Q6K> { using T = MfRawQ6; };
 
+// Q4_K: chunk c's 8 bytes for this lane: low nibbles are sub-block 2c at
+// positions 64c + 8kg + v, high nibbles sub-block 2c + 1 at 64c + 32 + 8kg + v
 __device__ __forceinline__ MfRawQ4 mf_load_q4k(wptr blk, int kg) {
     MfRawQ4 r;
     r.hd = ld16(blk);
@@ -2617,34 +2635,37 @@ __device__ __forceinline__ MfRawQ4 mf_load_q4k(wptr blk, int kg) {
     return r;
 }
 
-// Q6_K: sub-block s16 = 8h + 2t + is holds positions l' = 16 is .. +15 of
-// run (h, t); this lane takes l' = 16 is + 4 kg + v: one ql dword (nibble
-// t >> 1) and one qh dword (bits 2t).  Blocks are 2-byte aligned: each
-// dword is read as two aligned dwords and realigned; when the block is
-// aligned the second read repeats the first, so the last block of a tensor
-// is never read past its 210 bytes.
+// Q6_K: positions 32 st + 8 kg + v (step st = 4h + t) are bytes
+// 64h + 32(t&1) + 16(kg>>1) + 8(kg&1) + v of ql (nibble t >> 1) and
+// 128 + 32h + 16(kg>>1) + 8(kg&1) + v of qh (bits 2t): four ql fields and
+// two qh fields of 8 bytes, each read as three dwords of the 4-aligned
+// block and realigned (the third repeats the second when the block is
+// aligned, so no read passes the block's 210 bytes); the lane's sub-block
+// scales are bytes 192 + 2 st + (kg >> 1).
 __device__ __forceinline__ MfRawQ6 mf_load_q6k(wptr blk, int kg) {
     MfRawQ6 r;
     const uint32_t mis = (uint32_t)reinterpret_cast<uintptr_t>(blk) & 3u;
     r.sh = mis * 8u;
     const wptr b4 = blk - mis;
     const int nx = mis ? 4 : 0;
-    int i = 0;
+    const int o = 16 * (kg >> 1) + 8 * (kg & 1);
 #pragma unroll
-    for (int h = 0; h < 2; h++)
+    for (int f = 0; f < 4; f++) {
+        const int off = 64 * (f >> 1) + 32 * (f & 1) + o;
+        r.ql[f][0] = ld4(b4 + off);
+        r.ql[f][1] = ld4(b4 + off + 4);
+        r.ql[f][2] = ld4(b4 + off + 4 + nx);
+    }
 #pragma unroll
-        for (int is = 0; is < 2; is++) {
-            const int o[3] = {64 * h + 16 * is + 4 * kg, 64 * h + 32 + 16 * is + 4 * kg,
-                              128 + 32 * h + 16 * is + 4 * kg};
-#pragma unroll
-            for (int f = 0; f < 3; f++, i++) {
-                r.p[i][0] = ld4(b4 + o[f]);
-                r.p[i][1] = ld4(b4 + o[f] + nx);
-            }
-        }
+    for (int h = 0; h < 2; h++) {
+        const int off = 128 + 32 * h + o;
+        r.qh[h][0] = ld4(b4 + off);
+        r.qh[h][1] = ld4(b4 + off + 4);
+        r.qh[h][2] = ld4(b4 + off + 4 + nx);
+    }
     const uint4 sv = ld16a4(b4 + 192);
-    r.s[0] = sv.x; r.s[1] = sv.y; r.s[2] = sv.z; r.s[3] = sv.w;
-    r.s[4] = ld4(b4 + 192 + 12 + nx);
+    r.sc[0] = sv.x; r.sc[1] = sv.y; r.sc[2] = sv.z; r.sc[3] = sv.w;
+    r.sc[4] = ld4(b4 + 192 + 12 + nx);
     r.d = ld2(blk + 208);
     return r;
 }
@@ -2655,174 +2676,224 @@ __device__ __forceinline__ typename MfRaw<TYPE>::T mf_load(wptr blk, int kg) {
     else return mf_load_q6k(blk, kg);
 }
 
-__device__ __forceinline__ uint32_t byte_of(const uint4& v, int i) {
-    const uint32_t w = i < 4 ? v.x : i < 8 ? v.y : i < 12 ? v.z : v.w;
-    return (w >> (8 * (i & 3))) & 0xffu;
+// fp16 of sc * q for the 4 nibble bytes of nib (each < 16), sc <= 63: the
+// bytes become 1024 + q (fp16 0x6400 | q), and fma((1024 + q), sc,
+// -1024 sc) = sc q exactly (every value is an integer below 2048)
+__device__ __forceinline__ void q4_scaled(uint32_t nib, half2v sc2, half2v off2, uint32_t& w01,
+                                          uint32_t& w23) {
+    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, nib, 0x05010400u);   // q0, q1
+    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, nib, 0x05030402u);   // q2, q3
+    w01 = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(half2v, a), sc2, off2));
+    w23 = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(half2v, b), sc2, off2));
 }
 
-// one super-block of one 16-row tile for one stream group: acc[v] (streams
-// 4*(l/16)+v of the group, the lane's row) += the super-block's terms
-template <int TYPE>
-__device__ __forceinline__ void mf_superblock(const typename MfRaw<TYPE>::T& r, int kg,
-                                              const uint8_t* xl, const float* xsl, f32x4& acc) {
-    if constexpr (TYPE == T_Q4K) {
-        const float d = f16_bits_to_f32(r.hd.x & 0xffffu);
-        const float dmin = f16_bits_to_f32(r.hd.x >> 16);
-        // scales[12] are bytes 4..15 of the block: words y, z, w of hd
-        const uint4 sc = make_uint4(r.hd.y, r.hd.z, r.hd.w, 0u);
+// fp16 hi / lo of w = sc * (q - 32) for two u16 lanes of q (0..63):
+// w in [-4064, 4096] (q - 32 in [-32, 31], sc in [-128, 127]); lo = w & 7
+// (fp16 of 1024 + lo minus 1024), hi = w - lo = 8 t with t = w >> 3 in
+// [-508, 512]: fp16 of 1532 + t is 0x6400 | (t + 508), and
+// fma(1532 + t, 8, -12256) = 8 t exactly
+__device__ __forceinline__ void q6_scaled(uint32_t q2, uint32_t scw, uint32_t& hi, uint32_t& lo) {
+    typedef short s16x2 __attribute__((ext_vector_type(2)));
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    const s16x2 q = __builtin_bit_cast(s16x2, q2);
+    const s16x2 sc = __builtin_bit_cast(s16x2, scw);
+    const s16x2 w = (q - (s16x2){32, 32}) * sc;                            // low 16 bits exact
+    const uint32_t wl = __builtin_bit_cast(uint32_t, w);
+    const uint32_t l = (wl & 0x00070007u) | 0x64006400u;
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, l) + (half2v){(_Float16)-1024.0f, (_Float16)-1024.0f});
+    const s16x2 tt = (w >> (s16x2){3, 3}) + (s16x2){508, 508};            // in [0, 1020]
+    const uint32_t hb = __builtin_bit_cast(uint32_t, tt) | 0x64006400u;
+    hi = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(
+             __builtin_bit_cast(half2v, hb), (half2v){(_Float16)8.0f, (_Float16)8.0f},
+             (half2v){(_Float16)-12256.0f, (_Float16)-12256.0f}));
+}
+
+// A super-block decoded for one lane: the B operand of each step (Q4_K: one
+// plane; Q6_K: hi and lo) and the per-row scale factors.
+template <int TYPE> struct MfDec;
+template <> struct MfDec<T_Q4K> { half8 w[8]; float d, dm[8]; };
+template <> struct MfDec<T_Q6K> { half8 wh[8], wl[8]; float d; };
+
+__device__ __forceinline__ void mf_decode(const MfRawQ4& r, MfDec<T_Q4K>& o) {
+    o.d = f16_bits_to_f32(r.hd.x & 0xffffu);
+    const float dmin = f16_bits_to_f32(r.hd.x >> 16);
+    const uint4 sc = make_uint4(r.hd.y, r.hd.z, r.hd.w, 0u);
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            // 6-bit scale / min of sub-block j (stratum_q4k.h:57-65)
-            uint32_t s_, m_;
-            if (j < 4) {
-                s_ = byte_of(sc, j) & 63u;
-                m_ = byte_of(sc, j + 4) & 63u;
-            } else {
-                s_ = (byte_of(sc, j + 4) & 15u) | ((byte_of(sc, j - 4) >> 6) << 4);
-                m_ = (byte_of(sc, j + 4) >> 4) | ((byte_of(sc, j) >> 6) << 4);
-            }
-            const float ds = d * (float)s_, dm = dmin * (float)m_;
-            const uint2 q = r.q[j >> 1];
-            const uint32_t w0 = (j & 1) ? (q.x >> 4) & 0x0f0f0f0fu : q.x & 0x0f0f0f0fu;
-            const uint32_t w1 = (j & 1) ? (q.y >> 4) & 0x0f0f0f0fu : q.y & 0x0f0f0f0fu;
-            uint32_t b[4];
-            bf16_bytes(w0, b[0], b[1]);
-            bf16_bytes(w1, b[2], b[3]);
-            const bf16x8 bw = __builtin_bit_cast(bf16x8, make_uint4(b[0], b[1], b[2], b[3]));
-            const uint4* ap = reinterpret_cast<const uint4*>(xl) + (size_t)j * 3 * 64 + (threadIdx.x & 63);
-            f32x4 C = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int p = 0; p < 3; p++)
-                C = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ap[p * 64]), bw,
-                                                            C, 0, 0, 0);
-            const float4 xsum = reinterpret_cast<const float4*>(xsl + j * 16)[kg];
-            acc.x = acc.x + (ds * C.x - dm * xsum.x);
-            acc.y = acc.y + (ds * C.y - dm * xsum.y);
-            acc.z = acc.z + (ds * C.z - dm * xsum.z);
-            acc.w = acc.w + (ds * C.w - dm * xsum.w);
+    for (int j = 0; j < 8; j++) {
+        // 6-bit scale / min of sub-block j (stratum_q4k.h:57-65)
+        uint32_t s_, m_;
+        if (j < 4) {
+            s_ = byte_of(sc, j) & 63u;
+            m_ = byte_of(sc, j + 4) & 63u;
+        } else {
+            s_ = (byte_of(sc, j + 4) & 15u) | ((byte_of(sc, j - 4) >> 6) << 4);
+            m_ = (byte_of(sc, j + 4) >> 4) | ((byte_of(sc, j) >> 6) << 4);
         }
-    } else {
-        const uint32_t sh = r.sh;
-        uint32_t ql[2][2][2], qh[2][2];
-        int i = 0;
+        o.dm[j] = dmin * (float)m_;
+        const _Float16 sh = (_Float16)(float)s_;
+        const half2v sc2 = {sh, sh};
+        const half2v off2 = {(_Float16)(-1024.0f * (float)s_), (_Float16)(-1024.0f * (float)s_)};
+        const uint2 q = r.q[j >> 1];
+        const uint32_t n0 = (j & 1) ? (q.x >> 4) & 0x0f0f0f0fu : q.x & 0x0f0f0f0fu;
+        const uint32_t n1 = (j & 1) ? (q.y >> 4) & 0x0f0f0f0fu : q.y & 0x0f0f0f0fu;
+        uint32_t w0, w1, w2, w3;
+        q4_scaled(n0, sc2, off2, w0, w1);
+        q4_scaled(n1, sc2, off2, w2, w3);
+        o.w[j] = __builtin_bit_cast(half8, make_uint4(w0, w1, w2, w3));
+    }
+}
+
+__device__ __forceinline__ void mf_decode(const MfRawQ6& r, int kg, MfDec<T_Q6K>& o) {
+    o.d = f16_bits_to_f32(r.d);
+    const uint32_t sh = r.sh;
+    uint32_t scw[4];
 #pragma unroll
-        for (int h = 0; h < 2; h++)
+    for (int k = 0; k < 4; k++) scw[k] = __builtin_amdgcn_alignbit(r.sc[k + 1], r.sc[k], sh);
 #pragma unroll
-            for (int is = 0; is < 2; is++) {
-                ql[h][0][is] = __builtin_amdgcn_alignbit(r.p[i][1], r.p[i][0], sh); i++;
-                ql[h][1][is] = __builtin_amdgcn_alignbit(r.p[i][1], r.p[i][0], sh); i++;
-                qh[h][is] = __builtin_amdgcn_alignbit(r.p[i][1], r.p[i][0], sh); i++;
-            }
-        uint32_t scw[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) scw[k] = __builtin_amdgcn_alignbit(r.s[k + 1], r.s[k], sh);
-        const float d4 = f16_bits_to_f32(r.d) * 0.25f;        // bytes hold 4 (q - 32)
-#pragma unroll
-        for (int s16 = 0; s16 < 16; s16++) {
-            const int h = s16 >> 3, t = (s16 >> 1) & 3, is = s16 & 1;
-            const uint32_t L = ql[h][t & 1][is], H = qh[h][is];
-            const uint32_t q = ((L >> (4 * (t >> 1))) & 0x0f0f0f0fu) | (((H >> (2 * t)) & 0x03030303u) << 4);
-            const uint32_t y = (q ^ 0x20202020u) << 2;             // int8 4 (q - 32) per byte
-            uint32_t b0, b1;
-            bf16_sbytes(y, b0, b1);
-            const s16x4 bw = __builtin_bit_cast(s16x4, make_uint2(b0, b1));
-            const float scv = (float)(int32_t)(int8_t)((scw[s16 >> 2] >> (8 * (s16 & 3))) & 0xffu);
-            const float ds = d4 * scv;
-            const uint2* ap = reinterpret_cast<const uint2*>(xl) + (size_t)s16 * 3 * 64 + (threadIdx.x & 63);
-            f32x4 C = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int p = 0; p < 3; p++)
-                C = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, ap[p * 64]), bw,
-                                                              C, 0, 0, 0);
-            acc.x = acc.x + ds * C.x;
-            acc.y = acc.y + ds * C.y;
-            acc.z = acc.z + ds * C.z;
-            acc.w = acc.w + ds * C.w;
-        }
+    for (int st = 0; st < 8; st++) {
+        const int h = st >> 2, t = st & 3;
+        const int f = 2 * h + (t & 1);
+        const uint32_t L0 = __builtin_amdgcn_alignbit(r.ql[f][1], r.ql[f][0], sh);
+        const uint32_t L1 = __builtin_amdgcn_alignbit(r.ql[f][2], r.ql[f][1], sh);
+        const uint32_t H0 = __builtin_amdgcn_alignbit(r.qh[h][1], r.qh[h][0], sh);
+        const uint32_t H1 = __builtin_amdgcn_alignbit(r.qh[h][2], r.qh[h][1], sh);
+        const uint32_t q0 = ((L0 >> (4 * (t >> 1))) & 0x0f0f0f0fu) | (((H0 >> (2 * t)) & 0x03030303u) << 4);
+        const uint32_t q1 = ((L1 >> (4 * (t >> 1))) & 0x0f0f0f0fu) | (((H1 >> (2 * t)) & 0x03030303u) << 4);
+        // the lane's scale: byte 2 st + (kg >> 1), sign-extended to both u16 lanes
+        const int b = 2 * st + (kg >> 1);
+        const uint32_t s8 = (scw[b >> 2] >> (8 * (b & 3))) & 0xffu;
+        const uint32_t s16 = (uint32_t)(int32_t)(int8_t)s8 & 0xffffu;
+        const uint32_t scw2 = s16 | (s16 << 16);
+        uint32_t h4[4], l4[4];
+        q6_scaled(__builtin_amdgcn_perm(0u, q0, 0x0c010c00u), scw2, h4[0], l4[0]);
+        q6_scaled(__builtin_amdgcn_perm(0u, q0, 0x0c030c02u), scw2, h4[1], l4[1]);
+        q6_scaled(__builtin_amdgcn_perm(0u, q1, 0x0c010c00u), scw2, h4[2], l4[2]);
+        q6_scaled(__builtin_amdgcn_perm(0u, q1, 0x0c030c02u), scw2, h4[3], l4[3]);
+        o.wh[st] = __builtin_bit_cast(half8, make_uint4(h4[0], h4[1], h4[2], h4[3]));
+        o.wl[st] = __builtin_bit_cast(half8, make_uint4(l4[0], l4[1], l4[2], l4[3]));
     }
 }
 
 template <int TYPE>
-__global__ __launch_bounds__(256) void kq_mfma_mx_kernel(MfArg A) {
-    using MI = MfInfo<TYPE>;
+__global__ __launch_bounds__(256) void kq_mf_kernel(MfArg A) {
     using TI = TypeInfo<TYPE>;
-    constexpr int OPB = 3 * 64 * MI::KV * 2;                 // plane bytes per sub-block and group
-    constexpr int XB = MI::NSUB * OPB;                       // per super-block and group
     extern __shared__ __align__(16) uint8_t smem[];
-    // two buffers of planes, then two of sums
-    auto xb = [&](int buf) { return smem + buf * XB; };
-    auto xsb = [&](int buf) { return reinterpret_cast<float*>(smem + 2 * XB) + buf * 8 * 16; };
+    auto planes_of = [&](int buf) { return reinterpret_cast<const uint4*>(smem + buf * MF_PAIR_BYTES); };
+    auto xs_of = [&](int buf) {
+        return reinterpret_cast<const float*>(smem + buf * MF_PAIR_BYTES + MF_PAIR_PLANES * 16);
+    };
+    auto ex_of = [&](int buf) {
+        return reinterpret_cast<const int*>(smem + buf * MF_PAIR_BYTES + MF_PAIR_PLANES * 16 + 8 * 16 * 4);
+    };
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, kg = lane >> 4;
-    const int NSB = A.K >> 8;
+    const int NSB = A.K >> 8, NSG = A.NSG;
     const size_t rbytes = (size_t)NSB * TI::BB;
+    constexpr int NV = MF_PAIR_PLANES / 256;                 // uint4 of planes per thread
+    static_assert(NV * 256 == MF_PAIR_PLANES, "plane staging split");
     for (int u = blockIdx.x; u < A.nunits; u += A.grid) {
         const int rq = u / A.KP, kp = u - rq * A.KP;
         const int sb0 = kp * MF_SBP, sb1 = min(NSB, sb0 + MF_SBP);
+        const int npairs = (sb1 - sb0) * NSG;
         const int row = 64 * rq + 16 * wave + (lane & 15);
         const wptr wr = to_global(A.w) + (size_t)min(row, A.N - 1) * rbytes;
-        for (int g = 0; g < A.NSG; g++) {
-            // one super-block's planes (and sums) of group g: XB / 16 uint4
-            // of planes, 6 per thread (XB = 24 KB), loaded a step ahead
-            constexpr int NV = XB / 16 / 256;
-            static_assert(NV * 256 * 16 == XB, "plane staging split");
-            const u32x4* src = reinterpret_cast<const u32x4*>(A.planes);   // native vectors: no memcpy
-            // this thread's offsets within a super-block's planes (and sums),
-            // fixed for the group: a super-block only moves a uniform base
-            uint32_t off[NV];
+        // staging of pair i = (super-block sb0 + i / NSG, group i % NSG)
+        u32x4 sv[NV];
+        float xsv = 0.0f;
+        int exv = 0;
+        auto sload = [&](int i, u32x4 (&v)[NV], float& xv, int& ev) {
+            const int sb = sb0 + i / NSG, g = i - (i / NSG) * NSG;
+            const u32x4* sp = reinterpret_cast<const u32x4*>(A.planes) +
+                              (size_t)(sb * NSG + g) * MF_PAIR_PLANES;
 #pragma unroll
-            for (int k = 0; k < NV; k++) {
-                const int i = tid + 256 * k;
-                const int j = i / (OPB / 16), rr = i - j * (OPB / 16);
-                off[k] = (uint32_t)((j * A.NSG + g) * (OPB / 16) + rr);
-            }
-            const uint32_t xoff = (uint32_t)((tid >> 4) * (16 * A.NSG) + 16 * g + (tid & 15));
-            const size_t sb_stride = (size_t)MI::NSUB * A.NSG * (OPB / 16);
-            auto sload = [&](int sb, u32x4 (&v)[NV], float& xsv) {
-                const u32x4* sp = src + (size_t)sb * sb_stride;
+            for (int k = 0; k < NV; k++) v[k] = sp[tid + 256 * k];
+            if (TYPE == T_Q4K && tid < 8 * 16)
+                xv = A.xs[((size_t)sb * 8 + (tid >> 4)) * 16 * NSG + 16 * g + (tid & 15)];
+            if (tid < 16) ev = A.ex[(size_t)sb * 16 * NSG + 16 * g + tid];
+        };
+        auto sstore = [&](int buf, const u32x4 (&v)[NV], float xv, int ev) {
+            u32x4* pd = reinterpret_cast<u32x4*>(smem + buf * MF_PAIR_BYTES);
 #pragma unroll
-                for (int k = 0; k < NV; k++) v[k] = sp[off[k]];
-                if (TYPE == T_Q4K && tid < 8 * 16)
-                    xsv = A.xs[(size_t)sb * 8 * (16 * A.NSG) + xoff];
-            };
-            auto sstore = [&](int buf, const u32x4 (&v)[NV], float xsv) {
+            for (int k = 0; k < NV; k++) pd[tid + 256 * k] = v[k];
+            if (TYPE == T_Q4K && tid < 8 * 16)
+                reinterpret_cast<float*>(smem + buf * MF_PAIR_BYTES + MF_PAIR_PLANES * 16)[tid] = xv;
+            if (tid < 16)
+                reinterpret_cast<int*>(smem + buf * MF_PAIR_BYTES + MF_PAIR_PLANES * 16 + 8 * 16 * 4)[tid] = ev;
+        };
+        __syncthreads();                    // the previous unit's LDS reads are done
+        sload(0, sv, xsv, exv);
+        sstore(0, sv, xsv, exv);
+        typename MfRaw<TYPE>::T raw = mf_load<TYPE>(wr + (size_t)sb0 * TI::BB, kg);
+        __syncthreads();
+        f32x4 acc[4];
 #pragma unroll
-                for (int k = 0; k < NV; k++) reinterpret_cast<u32x4*>(xb(buf))[tid + 256 * k] = v[k];
-                if (TYPE == T_Q4K && tid < 8 * 16) xsb(buf)[tid] = xsv;
-            };
-            __syncthreads();                    // the previous group's LDS reads are done
-            {
-                u32x4 s0v[NV];
-                float x0 = 0.0f;
-                sload(sb0, s0v, x0);
-                sstore(0, s0v, x0);
-            }
-            u32x4 sv[NV];
-            float xsv = 0.0f;
-            typename MfRaw<TYPE>::T ra = mf_load<TYPE>(wr + (size_t)sb0 * TI::BB, kg), rb;
-            __syncthreads();
-            f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-            // one super-block: the next planes and weights go out first (the
-            // planes before the weights: loads complete in order, so storing
-            // the planes does not wait for the weights), then this one runs
-            auto step = [&](int sb, const typename MfRaw<TYPE>::T& cur,
-                            typename MfRaw<TYPE>::T& nxt) {
-                const int buf = (sb - sb0) & 1;
-                sload(min(sb + 1, sb1 - 1), sv, xsv);   // unconditional: no join on sv
-                nxt = mf_load<TYPE>(wr + (size_t)min(sb + 1, sb1 - 1) * TI::BB, kg);
-                mf_superblock<TYPE>(cur, kg, xb(buf), xsb(buf), acc);
-                if (sb + 1 < sb1) sstore(buf ^ 1, sv, xsv);
+        for (int g = 0; g < 4; g++) acc[g] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        for (int sb = sb0; sb < sb1; sb++) {
+            MfDec<TYPE> dec;
+            if constexpr (TYPE == T_Q4K) mf_decode(raw, dec);
+            else mf_decode(raw, kg, dec);
+            raw = mf_load<TYPE>(wr + (size_t)min(sb + 1, sb1 - 1) * TI::BB, kg);   // next super-block
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                if (g < NSG) {
+                const int i = (sb - sb0) * NSG + g, buf = i & 1;
+                const bool more = i + 1 < npairs;
+                if (more) sload(i + 1, sv, xsv, exv);
+                const uint4* ap = planes_of(buf) + lane;
+                f32x4 C = {0.0f, 0.0f, 0.0f, 0.0f};
+                // the three planes of step j + 1 are read while step j's MFMAs
+                // run; the barriers keep the compiler from hoisting all 24
+                // reads (which costs the registers of a second wave)
+                uint4 xa[3], xb[3];
+#pragma unroll
+                for (int p = 0; p < 3; p++) xa[p] = ap[p * 64];
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    if (j < 7) {
+#pragma unroll
+                        for (int p = 0; p < 3; p++) xb[p] = ap[((j + 1) * 3 + p) * 64];
+                    }
+#pragma unroll
+                    for (int p = 0; p < 3; p++) {
+                        const half8 x8 = __builtin_bit_cast(half8, xa[p]);
+                        if constexpr (TYPE == T_Q4K) {
+                            C = __builtin_amdgcn_mfma_f32_16x16x32_f16(x8, dec.w[j], C, 0, 0, 0);
+                        } else {
+                            C = __builtin_amdgcn_mfma_f32_16x16x32_f16(x8, dec.wh[j], C, 0, 0, 0);
+                            C = __builtin_amdgcn_mfma_f32_16x16x32_f16(x8, dec.wl[j], C, 0, 0, 0);
+                        }
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int p = 0; p < 3; p++) xa[p] = xb[p];
+                }
+                // the lane's outputs: streams 4 kg + v of group g, its row
+                const int4 e4 = reinterpret_cast<const int4*>(ex_of(buf))[kg];
+                f32x4 add = {ldexpf(dec.d * C.x, e4.x - 15), ldexpf(dec.d * C.y, e4.y - 15),
+                             ldexpf(dec.d * C.z, e4.z - 15), ldexpf(dec.d * C.w, e4.w - 15)};
+                if constexpr (TYPE == T_Q4K) {
+                    // minus sum_j dmin m_j xsum_j (fused: this is the tolerance path)
+                    const float4* xsl = reinterpret_cast<const float4*>(xs_of(buf)) + kg;
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        const float4 xv = xsl[4 * j];
+                        add.x = fmaf(-dec.dm[j], xv.x, add.x);
+                        add.y = fmaf(-dec.dm[j], xv.y, add.y);
+                        add.z = fmaf(-dec.dm[j], xv.z, add.z);
+                        add.w = fmaf(-dec.dm[j], xv.w, add.w);
+                    }
+                }
+                acc[g] = acc[g] + add;
+                if (more) sstore(buf ^ 1, sv, xsv, exv);
                 __syncthreads();
-            };
-            // unrolled by two, the weights alternating between ra and rb: no
-            // register copy (which would wait for the loads in flight)
-            for (int sb = sb0; sb < sb1; sb += 2) {
-                step(sb, ra, rb);
-                if (sb + 1 >= sb1) break;
-                step(sb + 1, rb, ra);
+                }
             }
-            // the lane's 4 outputs: streams 16 g + 4 kg + v of its row
+        }
+        // the lane's 4 outputs per group: streams 16 g + 4 kg + v of its row
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            if (g >= NSG) continue;
             const int s0 = 16 * g + 4 * kg;
-            const float av[4] = {acc.x, acc.y, acc.z, acc.w};
+            const float av[4] = {acc[g].x, acc[g].y, acc[g].z, acc[g].w};
             if (A.KP == 1) {
                 if (row < A.N)
 #pragma unroll
@@ -2831,7 +2902,7 @@ __global__ __launch_bounds__(256) void kq_mfma_mx_kernel(MfArg A) {
             } else if (row < A.N) {
 #pragma unroll
                 for (int v = 0; v < 4; v++)
-                    A.part[((size_t)kp * 16 * A.NSG + s0 + v) * A.N + row] = av[v];
+                    A.part[((size_t)kp * 16 * NSG + s0 + v) * A.N + row] = av[v];
             }
         }
     }
@@ -2853,25 +2924,23 @@ __global__ __launch_bounds__(256) void kq_mfma_reduce_kernel(const float* part, 
 template <int TYPE>
 int launch_mfma_t(const float* x, const void* w, float* y, int B, int N, int K, void* planes,
                   float* xs, float* part, int grid, hipStream_t st) {
-    using MI = MfInfo<TYPE>;
-    const int NSG = (B + 15) / 16;
+    const int NSG = (B + 15) / 16, NSB = K >> 8;
+    if (NSG > 4) return (int)hipErrorInvalidValue;
     MfSplitArg s;
-    s.x = x; s.planes = static_cast<uint16_t*>(planes); s.xs = TYPE == T_Q4K ? xs : nullptr;
+    s.x = x; s.planes = static_cast<uint4*>(planes);
+    s.xs = TYPE == T_Q4K ? xs : nullptr;
+    s.ex = reinterpret_cast<int*>(xs + (size_t)(K / 32) * 16 * NSG);
     s.B = B; s.K = K; s.NSG = NSG;
-    const long nt = (long)(K / MI::SUB) * NSG * 64;
-    hipLaunchKernelGGL(kq_mfma_xsplit_kernel<TYPE>, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0,
-                       st, s);
+    hipLaunchKernelGGL(kq_mf_split_kernel, dim3((unsigned)(NSB * NSG)), dim3(256), 0, st, s);
     MfArg a;
     a.w = static_cast<const uint8_t*>(w);
-    a.planes = static_cast<const uint16_t*>(planes);
-    a.xs = xs; a.y = y; a.part = part;
+    a.planes = static_cast<const uint4*>(planes);
+    a.xs = xs; a.ex = s.ex; a.y = y; a.part = part;
     a.B = B; a.N = N; a.K = K; a.NSG = NSG;
-    a.KP = ((K >> 8) + MF_SBP - 1) / MF_SBP;
+    a.KP = (NSB + MF_SBP - 1) / MF_SBP;
     a.nunits = (N + 63) / 64 * a.KP;
     a.grid = grid < a.nunits ? grid : a.nunits;
-    constexpr int XB = MI::NSUB * 3 * 64 * MI::KV * 2;
-    hipLaunchKernelGGL(kq_mfma_mx_kernel<TYPE>, dim3(a.grid), dim3(256), (size_t)(2 * XB + 2 * 8 * 16 * 4),
-                       st, a);
+    hipLaunchKernelGGL(kq_mf_kernel<TYPE>, dim3(a.grid), dim3(256), (size_t)(2 * MF_PAIR_BYTES), st, a);
     if (a.KP > 1) {
         const long n = (long)B * N;
         hipLaunchKernelGGL(kq_mfma_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
@@ -3754,22 +3823,32 @@ int kqk_launch_moe_group(const int* sel, int nm, int E, int nt, int x_div, int m
 // MFMA multi-x (Q4_K, Q6_K): workspace sizes for B streams of N x K, and the
 // launch (x split into planes, the matrix-core sweep, and the sum of the
 // K-parts' partials).
+// Workspace of one launch of up to 64 streams (larger B runs in chunks of
+// 64 on the same workspace): the planes, then the x sums and the exponents
+// (one region), then the K-part partial sums.
 int kqk_mfma_workspace(int type, int B, int N, int K, long* planes, long* xs, long* part) {
     if ((type != T_Q4K && type != T_Q6K) || B < 1 || N < 1 || K <= 0 || (K & 255)) return -1;
-    const long NSG = (B + 15) / 16, KP = ((K >> 8) + MF_SBP - 1) / MF_SBP;
-    *planes = (long)K * NSG * 16 * 3 * 2;
-    *xs = (long)(K / 32) * NSG * 16 * 4;
+    const long NSG = B >= 64 ? 4 : (B + 15) / 16, NSB = K >> 8;
+    const long KP = (NSB + MF_SBP - 1) / MF_SBP;
+    *planes = NSB * NSG * MF_PAIR_PLANES * 16;
+    *xs = (long)(K / 32) * NSG * 16 * 4 + NSB * NSG * 16 * 4;
     *part = KP > 1 ? KP * NSG * 16 * (long)N * 4 : 0;
     return 0;
 }
 
 int kqk_launch_mfma(int type, const float* x, const void* w, float* y, int B, int N, int K,
                     void* planes, float* xs, float* part, int grid, hipStream_t st) {
-    switch (type) {
-    case T_Q4K: return launch_mfma_t<T_Q4K>(x, w, y, B, N, K, planes, xs, part, grid, st);
-    case T_Q6K: return launch_mfma_t<T_Q6K>(x, w, y, B, N, K, planes, xs, part, grid, st);
-    default: return (int)hipErrorInvalidValue;
+    if (type != T_Q4K && type != T_Q6K) return (int)hipErrorInvalidValue;
+    for (int s0 = 0; s0 < B; s0 += 64) {
+        const int nb = B - s0 < 64 ? B - s0 : 64;
+        const float* xc = x + (size_t)s0 * K;
+        float* yc = y + (size_t)s0 * N;
+        const int e = type == T_Q4K
+                          ? launch_mfma_t<T_Q4K>(xc, w, yc, nb, N, K, planes, xs, part, grid, st)
+                          : launch_mfma_t<T_Q6K>(xc, w, yc, nb, N, K, planes, xs, part, grid, st);
+        if (e) return e;
     }
+    return 0;
 }
 
 int kqk_launch_dequant(int type, const void* w, float* y, long nblocks, hipStream_t st) {
