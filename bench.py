@@ -223,7 +223,7 @@ def _check(L, rc):
         raise RuntimeError(L.kq_last_error().decode())
 
 
-MFMA_BF16_PEAK_TFLOPS = 2500.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
 
 # the CPU baseline beside each other configuration (cleared by --no-cpu-baseline)
 CPU = {"on": True}
@@ -259,8 +259,9 @@ def multiseq_mfma(L, torch, stream, host_w) -> dict:
     """configs[3] on the matrix cores (kq_gemv_multix_mfma_dev, B >= 16).
 
     Time per call with HIP events on the launch stream; TFLOP/s counts the
-    product's 2*N*K*B flops; mfma_util counts what the kernel issues (three
-    bf16 planes of x, streams padded to 16) against the dense bf16 peak.
+    product's 2*N*K*B flops; mfma_util counts the fp16 MFMA flops the kernel
+    issues (two planes of x, times hi and lo of the weights for Q6_K, streams
+    padded to 16) against the dense fp16 peak.
     Tolerance: every output against the exact multi-x path (bit-identical to
     the reference's scalar routine in the GPU tests): max |a-b|/max(|b|,1e-6),
     the fraction within 1e-5, and max |a-b| / sum_k |w_k x_k| (the error
@@ -291,11 +292,11 @@ def multiseq_mfma(L, torch, stream, host_w) -> dict:
             rel = d / ye.abs().clamp_min(1e-6)
             nb = algo_bytes(t, N, K, B)
             flops = 2.0 * N * K * B
-            issued = 3 * 2.0 * N * K * ((B + 15) // 16 * 16)
+            issued = (2 if t == 12 else 4) * 2.0 * N * K * ((B + 15) // 16 * 16)
             res[f"{name}_B{B}"] = {
                 "us_per_call": round(us, 2), "us_per_stream": round(us / B, 2),
                 "GB/s": round(nb / us / 1e3, 1), "TFLOP/s": round(flops / us / 1e6, 2),
-                "mfma_util": round(issued / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4),
+                "mfma_util": round(issued / us / 1e6 / MFMA_F16_PEAK_TFLOPS, 4),
                 "max_rel_err_vs_exact": float(f"{rel.max().item():.3e}"),
                 "frac_within_1e-5": round((rel <= 1e-5).float().mean().item(), 5),
                 "max_err_over_mag": float(f"{(d / mag.clamp_min(1e-30)).max().item():.3e}")}

@@ -2498,42 +2498,80 @@ __global__ __launch_bounds__(1024) void kq_moe_group_kernel(MoeGroupArg a) {
 // cores.  The weights enter with their sub-block scales folded in, as exact
 // fp16 integers: Q4_K w = sc*q (sc <= 63, q <= 15: at most 945), Q6_K
 // w = sc*(q - 32) (|w| <= 4096) split exactly into hi = w - (w & 7) and
-// lo = w & 7.  x enters exactly as three fp16 planes of x*2^(15-E), E the
-// binary exponent of the largest |x| of the (stream, super-block), so the
-// planes cannot overflow and every product w*plane is exact in fp32.  A
-// whole super-block (256 weights) accumulates in one MFMA accumulator
-// (mfma_f32_16x16x32_f16); per super-block and output the kernel then adds
-// 2^(E-15)*d*acc minus, for Q4_K, sum_j dmin*m_j*xsum_j (x sums of each
-// 32-value sub-block).  Differences from the reference: the fp32 order of
-// the sums inside a super-block and across super-blocks, and the scale
-// applied to the super-block sum instead of each sub-block's.  The weights
-// of a super-block are decoded once per lane and used for every 16-stream
-// group.
+// lo = w & 7.  x enters as two fp16 planes, hi = fp16(x') and
+// mid = fp16(x' - hi), of x' = x*2^(15-E), E the binary exponent of the
+// largest |x| of the (stream, super-block): the planes cannot overflow, each
+// x keeps 22 significant bits (|x - (hi + mid) 2^(E-15)| <= 2^-21 |x| +
+// 2^-39 max|x|), and every product w*plane is exact in fp32.  A super-block
+// (256 weights) accumulates in one MFMA accumulator
+// (mfma_f32_16x16x32_f16) and joins the row's running sum as
+// fma(d*2^(E-15), acc, sum); the Q4_K min term -sum_j dmin*m_j*xsum_j
+// (xsum_j the sequential binary32 sum of sub-block j's 32 x) runs on the
+// fp32 matrix cores (mfma_f32_16x16x4_f32) into the same sum.  Differences
+// from the reference: x rounded to 22 bits, the fp32 order of the sums, and
+// the block scale applied to the super-block sum instead of each
+// sub-block's.
 //
 // Operands: D[stream][row] = sum_k A[stream][k] B[k][row], A = an x plane,
 // B = the weights.  In the 16x16x32 MFMAs lane l holds B[k][row = l % 16]
-// for k = 8*(l/16) + v and receives D[4*(l/16) + v][l % 16]: a lane's
-// weight row is its output row, so each lane decodes only its own row.
+// for k = 8*(l/16) + v and receives D[4*(l/16) + v][l % 16]; in the
+// 16x16x4 fp32 MFMA lane l holds A[l % 16][l / 16] and B[l / 16][l % 16].
+// A lane's weight row is its output row, so each lane decodes only its own
+// row.
 //  * kq_mf_split_kernel: one workgroup per (super-block, 16-stream group)
-//    writes the three planes in A-operand order, E per stream, and (Q4_K)
-//    the sequential binary32 sum of each 32 x;
-//  * kq_mf_kernel: a work unit is 64 rows (4 waves x 16 rows) x a K-part of
-//    MF_SBP super-blocks; the planes of each (super-block, group) pair are
-//    staged in LDS (double-buffered, shared by the 4 waves) while the
-//    previous pair is consumed.  Units with several K-parts write partial
-//    sums, which kq_mfma_reduce_kernel adds in part order (a fixed order:
-//    the result does not depend on timing).
+//    writes the two planes in A-operand order, the x sums and E;
+//  * kq_mf_kernel: 8 waves; a wave owns MfShape::TILES 16-row tiles (Q4_K 2,
+//    Q6_K 1: Q6_K's hi and lo already use each A operand twice), so a
+//    workgroup sweeps a block of 256 (Q4_K) or 128 (Q6_K) rows.  The
+//    (row block, super-block) iterations are split into one contiguous range
+//    per workgroup (whole row blocks when there are at least two per
+//    workgroup); a super-block's planes for all stream groups are staged in
+//    LDS (double-buffered) while the previous super-block is consumed, and
+//    each weight step is decoded once for every stream group;
+//  * kq_mf_reduce_kernel adds, in workgroup order, the partial sums of the
+//    row blocks that several workgroups share (a fixed order: the result
+//    does not depend on timing).
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-constexpr int MF_SBP = 4;                        // super-blocks per K-part
-constexpr int MF_PAIR_PLANES = 8 * 3 * 64;       // uint4 of planes per (super-block, group)
-constexpr int MF_PAIR_BYTES = MF_PAIR_PLANES * 16 + 8 * 16 * 4 + 16 * 4;   // + x sums + E
+constexpr int MF_NW = 8;                         // waves per workgroup
+constexpr int MF_GROUP_U4 = 8 * 2 * 64;          // uint4 of planes per (super-block, group)
+constexpr int MF_SIDE_U4 = (8 * 16 + 16) / 4;    // x sums (8 x 16 floats), then E (16 ints)
+
+template <int TYPE> struct MfShape {
+    static constexpr int TILES = TYPE == T_Q4K ? 2 : 1;
+    static constexpr int ROWS = 16 * TILES * MF_NW;                    // rows per row block
+};
+
+// uint4 of one super-block's LDS stage for nsg stream groups
+__host__ __device__ constexpr int mf_stage_u4(int nsg) { return nsg * (MF_GROUP_U4 + MF_SIDE_U4); }
+
+// How the (row block, super-block) iterations go to the workgroups: whole
+// row blocks per workgroup when there are at least two per workgroup, else
+// an even split of all nrb * NSB iterations (G <= T).
+struct MfPlan {
+    int rows, nrb, G, whole;
+    long T;
+    long part_floats;        // partial sums (0 when every row block has one owner)
+};
+
+__host__ __device__ inline MfPlan mf_plan(int type, int NSG, int N, int K, int grid) {
+    MfPlan p;
+    p.rows = type == T_Q4K ? MfShape<T_Q4K>::ROWS : MfShape<T_Q6K>::ROWS;
+    p.nrb = (N + p.rows - 1) / p.rows;
+    p.T = (long)p.nrb * (K >> 8);
+    p.whole = p.nrb >= 2 * grid;
+    p.G = p.whole ? grid : (int)(p.T < grid ? p.T : grid);
+    p.part_floats = p.whole ? 0 : (long)(p.G + p.nrb) * 16 * NSG * p.rows;
+    return p;
+}
+
+// the workgroup whose range holds iteration a (uneven split of T over G)
+__device__ __forceinline__ long mf_owner(long a, long T, int G) { return ((a + 1) * G - 1) / T; }
 
 struct MfSplitArg {
     const float* x;          // B x K
-    uint4* planes;           // NSB x NSG x 8 steps x 3 planes x 64 lanes (8 fp16 each)
-    float* xs;               // NSB x 8 x 16 NSG: sums of 32 (Q4_K), or null
-    int* ex;                 // NSB x 16 NSG: E of each (super-block, stream)
+    uint4* planes;           // NSB x NSG x 8 steps x 2 planes x 64 lanes (8 fp16 each)
+    uint4* side;             // NSB x NSG x (8 x 16 sums of 32, 16 E)
     int B, K, NSG;
 };
 
@@ -2541,6 +2579,10 @@ __device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
     return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
+// One workgroup per (super-block, 16-stream group): thread t = 16 si + p
+// takes stream si's 16 x at 16 p (sub-block p / 2, k-groups 2 (p & 1) and
+// 2 (p & 1) + 1 of step p / 2); E is the exponent of the stream's largest
+// |x| in the super-block (a 16-lane max).  Padding streams write zeros.
 __global__ __launch_bounds__(256) void kq_mf_split_kernel(MfSplitArg a) {
     const int sb = blockIdx.x / a.NSG, g = blockIdx.x - sb * a.NSG;
     const int t = threadIdx.x, si = t >> 4, p = t & 15;
@@ -2559,58 +2601,50 @@ __global__ __launch_bounds__(256) void kq_mf_split_kernel(MfSplitArg a) {
 #pragma unroll
     for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));   // the stream's 16 lanes
     const int E = __builtin_amdgcn_frexp_expf(mx);        // mx = m 2^E, m in [0.5, 1); 0 for 0
-    // planes: step j = p / 2, lane slots kg = 2 (p & 1) and 2 (p & 1) + 1
-    uint32_t hw[8], mw[8], lw[8];
+    uint32_t hw[8], mw[8];
 #pragma unroll
-    for (int i = 0; i < 16; i += 2) {
-        _Float16 h2[2], m2[2], l2[2];
+    for (int e = 0; e < 8; e++) {
+        _Float16 h2[2], m2[2];
 #pragma unroll
-        for (int e = 0; e < 2; e++) {
-            const float xv = ldexpf(v[i + e], 15 - E);
-            const _Float16 h = (_Float16)xv;
-            const float r1 = xv - (float)h;
-            const _Float16 m = (_Float16)r1;
-            h2[e] = h; m2[e] = m; l2[e] = (_Float16)(r1 - (float)m);
+        for (int i = 0; i < 2; i++) {
+            const float xv = ldexpf(v[2 * e + i], 15 - E);
+            h2[i] = (_Float16)xv;
+            m2[i] = (_Float16)(xv - (float)h2[i]);
         }
-        hw[i / 2] = pack_h2(h2[0], h2[1]);
-        mw[i / 2] = pack_h2(m2[0], m2[1]);
-        lw[i / 2] = pack_h2(l2[0], l2[1]);
+        hw[e] = pack_h2(h2[0], h2[1]);
+        mw[e] = pack_h2(m2[0], m2[1]);
     }
-    uint4* dst = a.planes + ((size_t)(sb * a.NSG + g) * 8 + (p >> 1)) * 3 * 64;
-    const int l0 = 16 * (2 * (p & 1)) + si;
+    const size_t pair = (size_t)sb * a.NSG + g;
+    uint4* dst = a.planes + (pair * 8 + (p >> 1)) * 128 + 16 * (2 * (p & 1)) + si;
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-        dst[l0 + 16 * h] = make_uint4(hw[4 * h], hw[4 * h + 1], hw[4 * h + 2], hw[4 * h + 3]);
-        dst[64 + l0 + 16 * h] = make_uint4(mw[4 * h], mw[4 * h + 1], mw[4 * h + 2], mw[4 * h + 3]);
-        dst[128 + l0 + 16 * h] = make_uint4(lw[4 * h], lw[4 * h + 1], lw[4 * h + 2], lw[4 * h + 3]);
+        dst[16 * h] = make_uint4(hw[4 * h], hw[4 * h + 1], hw[4 * h + 2], hw[4 * h + 3]);
+        dst[64 + 16 * h] = make_uint4(mw[4 * h], mw[4 * h + 1], mw[4 * h + 2], mw[4 * h + 3]);
     }
-    if (p == 0) a.ex[(size_t)sb * 16 * a.NSG + s] = E;
-    if (a.xs) {
-        // sequential binary32 sum of the 32 values of sub-block p / 2: the
-        // even lane sums its 16, the odd lane continues from it
-        float acc = 0.0f;
-        if (!(p & 1)) {
+    float* side = reinterpret_cast<float*>(a.side + pair * MF_SIDE_U4);
+    if (p == 0) reinterpret_cast<int*>(side)[128 + si] = E;
+    // sequential binary32 sum of the 32 values of sub-block p / 2: the even
+    // lane sums its 16, the odd lane continues from it
+    float acc = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 16; i++) acc = acc + v[i];
-        }
-        const float first = __shfl(acc, (t & 63) - (p & 1));
-        if (p & 1) {
-            acc = first;
+    for (int i = 0; i < 16; i++) acc = acc + v[i];
+    const float first = __shfl(acc, (t & 63) - (p & 1));
+    if (p & 1) {
+        acc = first;
 #pragma unroll
-            for (int i = 0; i < 16; i++) acc = acc + v[i];
-            a.xs[((size_t)sb * 8 + (p >> 1)) * 16 * a.NSG + s] = acc;
-        }
+        for (int i = 0; i < 16; i++) acc = acc + v[i];
+        side[(p >> 1) * 16 + si] = acc;
     }
 }
 
 struct MfArg {
     const uint8_t* w;
     const uint4* planes;
-    const float* xs;
-    const int* ex;
+    const uint4* side;
     float* y;                // B x N
-    float* part;             // KP x (16 NSG) x N partial sums (KP > 1)
-    int B, N, K, NSG, KP, nunits, grid;
+    float* part;             // (G + nrb) slots x 16 NSG x rows: partial sums
+    int B, N, K, NSG, nrb, G, whole;
+    long T;
 };
 
 __device__ __forceinline__ uint32_t byte_of(const uint4& v, int i) {
@@ -2694,7 +2728,6 @@ __device__ __forceinline__ void q4_scaled(uint32_t nib, half2v sc2, half2v off2,
 // fma(1532 + t, 8, -12256) = 8 t exactly
 __device__ __forceinline__ void q6_scaled(uint32_t q2, uint32_t scw, uint32_t& hi, uint32_t& lo) {
     typedef short s16x2 __attribute__((ext_vector_type(2)));
-    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
     const s16x2 q = __builtin_bit_cast(s16x2, q2);
     const s16x2 sc = __builtin_bit_cast(s16x2, scw);
     const s16x2 w = (q - (s16x2){32, 32}) * sc;                            // low 16 bits exact
@@ -2708,244 +2741,314 @@ __device__ __forceinline__ void q6_scaled(uint32_t q2, uint32_t scw, uint32_t& h
              (half2v){(_Float16)-12256.0f, (_Float16)-12256.0f}));
 }
 
-// A super-block decoded for one lane: the B operand of each step (Q4_K: one
-// plane; Q6_K: hi and lo) and the per-row scale factors.
-template <int TYPE> struct MfDec;
-template <> struct MfDec<T_Q4K> { half8 w[8]; float d, dm[8]; };
-template <> struct MfDec<T_Q6K> { half8 wh[8], wl[8]; float d; };
+// Per-super-block constants of one lane's row.  Q4_K: d, and the B operands
+// of the min term, -dmin*m_kg and -dmin*m_(4+kg) (6-bit mins,
+// stratum_q4k.h:57-65).  Q6_K: d, and the lane's scale bytes realigned.
+template <int TYPE> struct MfSb;
+template <> struct MfSb<T_Q4K> { float d, nm0, nm1; };
+template <> struct MfSb<T_Q6K> { float d; uint32_t scw[4]; };
 
-__device__ __forceinline__ void mf_decode(const MfRawQ4& r, MfDec<T_Q4K>& o) {
-    o.d = f16_bits_to_f32(r.hd.x & 0xffffu);
+__device__ __forceinline__ MfSb<T_Q4K> mf_sb(const MfRawQ4& r, int kg) {
+    MfSb<T_Q4K> c;
+    c.d = f16_bits_to_f32(r.hd.x & 0xffffu);
     const float dmin = f16_bits_to_f32(r.hd.x >> 16);
+    const uint32_t sh = 8u * (uint32_t)kg;
+    const uint32_t b4 = (r.hd.z >> sh) & 0xffu;           // scale byte 4 + kg
+    const uint32_t b8 = (r.hd.w >> sh) & 0xffu;           // scale byte 8 + kg
+    c.nm0 = -(dmin * (float)(b4 & 63u));
+    c.nm1 = -(dmin * (float)((b8 >> 4) | ((b4 >> 6) << 4)));
+    return c;
+}
+
+__device__ __forceinline__ MfSb<T_Q6K> mf_sb(const MfRawQ6& r, int) {
+    MfSb<T_Q6K> c;
+    c.d = f16_bits_to_f32(r.d);
+#pragma unroll
+    for (int k = 0; k < 4; k++) c.scw[k] = __builtin_amdgcn_alignbit(r.sc[k + 1], r.sc[k], r.sh);
+    return c;
+}
+
+// Q4_K step j (sub-block j): the lane's 8 weights sc_j * q
+__device__ __forceinline__ half8 mf_step_q4k(const MfRawQ4& r, int j) {
     const uint4 sc = make_uint4(r.hd.y, r.hd.z, r.hd.w, 0u);
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        // 6-bit scale / min of sub-block j (stratum_q4k.h:57-65)
-        uint32_t s_, m_;
-        if (j < 4) {
-            s_ = byte_of(sc, j) & 63u;
-            m_ = byte_of(sc, j + 4) & 63u;
-        } else {
-            s_ = (byte_of(sc, j + 4) & 15u) | ((byte_of(sc, j - 4) >> 6) << 4);
-            m_ = (byte_of(sc, j + 4) >> 4) | ((byte_of(sc, j) >> 6) << 4);
-        }
-        o.dm[j] = dmin * (float)m_;
-        const _Float16 sh = (_Float16)(float)s_;
-        const half2v sc2 = {sh, sh};
-        const half2v off2 = {(_Float16)(-1024.0f * (float)s_), (_Float16)(-1024.0f * (float)s_)};
-        const uint2 q = r.q[j >> 1];
-        const uint32_t n0 = (j & 1) ? (q.x >> 4) & 0x0f0f0f0fu : q.x & 0x0f0f0f0fu;
-        const uint32_t n1 = (j & 1) ? (q.y >> 4) & 0x0f0f0f0fu : q.y & 0x0f0f0f0fu;
-        uint32_t w0, w1, w2, w3;
-        q4_scaled(n0, sc2, off2, w0, w1);
-        q4_scaled(n1, sc2, off2, w2, w3);
-        o.w[j] = __builtin_bit_cast(half8, make_uint4(w0, w1, w2, w3));
-    }
+    const uint32_t s_ = j < 4 ? byte_of(sc, j) & 63u
+                              : (byte_of(sc, j + 4) & 15u) | ((byte_of(sc, j - 4) >> 6) << 4);
+    const _Float16 sh = (_Float16)(float)s_;
+    const half2v sc2 = {sh, sh};
+    const _Float16 of = (_Float16)(-1024.0f * (float)s_);
+    const half2v off2 = {of, of};
+    const uint2 q = r.q[j >> 1];
+    const uint32_t n0 = (j & 1) ? (q.x >> 4) & 0x0f0f0f0fu : q.x & 0x0f0f0f0fu;
+    const uint32_t n1 = (j & 1) ? (q.y >> 4) & 0x0f0f0f0fu : q.y & 0x0f0f0f0fu;
+    uint32_t w0, w1, w2, w3;
+    q4_scaled(n0, sc2, off2, w0, w1);
+    q4_scaled(n1, sc2, off2, w2, w3);
+    return __builtin_bit_cast(half8, make_uint4(w0, w1, w2, w3));
 }
 
-__device__ __forceinline__ void mf_decode(const MfRawQ6& r, int kg, MfDec<T_Q6K>& o) {
-    o.d = f16_bits_to_f32(r.d);
+// Q6_K step st: the lane's 8 weights sc * (q - 32) as hi and lo
+__device__ __forceinline__ void mf_step_q6k(const MfRawQ6& r, const MfSb<T_Q6K>& c, int kg, int st,
+                                            half8& wh, half8& wl) {
     const uint32_t sh = r.sh;
-    uint32_t scw[4];
-#pragma unroll
-    for (int k = 0; k < 4; k++) scw[k] = __builtin_amdgcn_alignbit(r.sc[k + 1], r.sc[k], sh);
-#pragma unroll
-    for (int st = 0; st < 8; st++) {
-        const int h = st >> 2, t = st & 3;
-        const int f = 2 * h + (t & 1);
-        const uint32_t L0 = __builtin_amdgcn_alignbit(r.ql[f][1], r.ql[f][0], sh);
-        const uint32_t L1 = __builtin_amdgcn_alignbit(r.ql[f][2], r.ql[f][1], sh);
-        const uint32_t H0 = __builtin_amdgcn_alignbit(r.qh[h][1], r.qh[h][0], sh);
-        const uint32_t H1 = __builtin_amdgcn_alignbit(r.qh[h][2], r.qh[h][1], sh);
-        const uint32_t q0 = ((L0 >> (4 * (t >> 1))) & 0x0f0f0f0fu) | (((H0 >> (2 * t)) & 0x03030303u) << 4);
-        const uint32_t q1 = ((L1 >> (4 * (t >> 1))) & 0x0f0f0f0fu) | (((H1 >> (2 * t)) & 0x03030303u) << 4);
-        // the lane's scale: byte 2 st + (kg >> 1), sign-extended to both u16 lanes
-        const int b = 2 * st + (kg >> 1);
-        const uint32_t s8 = (scw[b >> 2] >> (8 * (b & 3))) & 0xffu;
-        const uint32_t s16 = (uint32_t)(int32_t)(int8_t)s8 & 0xffffu;
-        const uint32_t scw2 = s16 | (s16 << 16);
-        uint32_t h4[4], l4[4];
-        q6_scaled(__builtin_amdgcn_perm(0u, q0, 0x0c010c00u), scw2, h4[0], l4[0]);
-        q6_scaled(__builtin_amdgcn_perm(0u, q0, 0x0c030c02u), scw2, h4[1], l4[1]);
-        q6_scaled(__builtin_amdgcn_perm(0u, q1, 0x0c010c00u), scw2, h4[2], l4[2]);
-        q6_scaled(__builtin_amdgcn_perm(0u, q1, 0x0c030c02u), scw2, h4[3], l4[3]);
-        o.wh[st] = __builtin_bit_cast(half8, make_uint4(h4[0], h4[1], h4[2], h4[3]));
-        o.wl[st] = __builtin_bit_cast(half8, make_uint4(l4[0], l4[1], l4[2], l4[3]));
-    }
+    const int h = st >> 2, t = st & 3;
+    const int f = 2 * h + (t & 1);
+    const uint32_t L0 = __builtin_amdgcn_alignbit(r.ql[f][1], r.ql[f][0], sh);
+    const uint32_t L1 = __builtin_amdgcn_alignbit(r.ql[f][2], r.ql[f][1], sh);
+    const uint32_t H0 = __builtin_amdgcn_alignbit(r.qh[h][1], r.qh[h][0], sh);
+    const uint32_t H1 = __builtin_amdgcn_alignbit(r.qh[h][2], r.qh[h][1], sh);
+    const uint32_t q0 = ((L0 >> (4 * (t >> 1))) & 0x0f0f0f0fu) | (((H0 >> (2 * t)) & 0x03030303u) << 4);
+    const uint32_t q1 = ((L1 >> (4 * (t >> 1))) & 0x0f0f0f0fu) | (((H1 >> (2 * t)) & 0x03030303u) << 4);
+    // the lane's scale: byte 2 st + (kg >> 1), sign-extended to both u16 lanes
+    const int b = 2 * st + (kg >> 1);
+    const uint32_t s8 = (c.scw[b >> 2] >> (8 * (b & 3))) & 0xffu;
+    const uint32_t s16 = (uint32_t)(int32_t)(int8_t)s8 & 0xffffu;
+    const uint32_t scw2 = s16 | (s16 << 16);
+    uint32_t h4[4], l4[4];
+    q6_scaled(__builtin_amdgcn_perm(0u, q0, 0x0c010c00u), scw2, h4[0], l4[0]);
+    q6_scaled(__builtin_amdgcn_perm(0u, q0, 0x0c030c02u), scw2, h4[1], l4[1]);
+    q6_scaled(__builtin_amdgcn_perm(0u, q1, 0x0c010c00u), scw2, h4[2], l4[2]);
+    q6_scaled(__builtin_amdgcn_perm(0u, q1, 0x0c030c02u), scw2, h4[3], l4[3]);
+    wh = __builtin_bit_cast(half8, make_uint4(h4[0], h4[1], h4[2], h4[3]));
+    wl = __builtin_bit_cast(half8, make_uint4(l4[0], l4[1], l4[2], l4[3]));
 }
 
-template <int TYPE>
-__global__ __launch_bounds__(256) void kq_mf_kernel(MfArg A) {
+template <int TYPE, int NSG>
+__global__ __launch_bounds__(64 * MF_NW) void kq_mf_kernel(MfArg A) {
     using TI = TypeInfo<TYPE>;
+    using SH = MfShape<TYPE>;
+    constexpr int TL = SH::TILES, R = SH::ROWS, NT = 64 * MF_NW;
+    constexpr int PU = NSG * MF_GROUP_U4, NX = NSG * MF_SIDE_U4, SU = PU + NX;   // uint4 per stage
+    constexpr int NP = PU / NT;                                        // plane uint4 per thread
+    constexpr int NH = NP / 2 + 1;                                     // per staging half
+    static_assert(NP * NT == PU && NP % 2 == 0 && NX <= NT, "stage split");
     extern __shared__ __align__(16) uint8_t smem[];
-    auto planes_of = [&](int buf) { return reinterpret_cast<const uint4*>(smem + buf * MF_PAIR_BYTES); };
-    auto xs_of = [&](int buf) {
-        return reinterpret_cast<const float*>(smem + buf * MF_PAIR_BYTES + MF_PAIR_PLANES * 16);
-    };
-    auto ex_of = [&](int buf) {
-        return reinterpret_cast<const int*>(smem + buf * MF_PAIR_BYTES + MF_PAIR_PLANES * 16 + 8 * 16 * 4);
-    };
+    u32x4* lds = reinterpret_cast<u32x4*>(smem);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, kg = lane >> 4;
-    const int NSB = A.K >> 8, NSG = A.NSG;
+    const int NSB = A.K >> 8;
     const size_t rbytes = (size_t)NSB * TI::BB;
-    constexpr int NV = MF_PAIR_PLANES / 256;                 // uint4 of planes per thread
-    static_assert(NV * 256 == MF_PAIR_PLANES, "plane staging split");
-    for (int u = blockIdx.x; u < A.nunits; u += A.grid) {
-        const int rq = u / A.KP, kp = u - rq * A.KP;
-        const int sb0 = kp * MF_SBP, sb1 = min(NSB, sb0 + MF_SBP);
-        const int npairs = (sb1 - sb0) * NSG;
-        const int row = 64 * rq + 16 * wave + (lane & 15);
-        const wptr wr = to_global(A.w) + (size_t)min(row, A.N - 1) * rbytes;
-        // staging of pair i = (super-block sb0 + i / NSG, group i % NSG)
-        u32x4 sv[NV];
-        float xsv = 0.0f;
-        int exv = 0;
-        auto sload = [&](int i, u32x4 (&v)[NV], float& xv, int& ev) {
-            const int sb = sb0 + i / NSG, g = i - (i / NSG) * NSG;
-            const u32x4* sp = reinterpret_cast<const u32x4*>(A.planes) +
-                              (size_t)(sb * NSG + g) * MF_PAIR_PLANES;
+    const int wg = blockIdx.x;
+    int it0, it1;
+    if (A.whole) {
+        it0 = (int)((long)wg * A.nrb / A.G) * NSB;
+        it1 = (int)((long)(wg + 1) * A.nrb / A.G) * NSB;
+    } else {
+        it0 = (int)((long)wg * A.T / A.G);
+        it1 = (int)((long)(wg + 1) * A.T / A.G);
+    }
+    if (it0 >= it1) return;                 // the whole workgroup: no barrier is left waiting
+    auto wrow = [&](int rb, int t) {
+        const int row = rb * R + 16 * (TL * wave + t) + (lane & 15);
+        return to_global(A.w) + (size_t)min(row, A.N - 1) * rbytes;
+    };
+    // staging of super-block sb in two halves (the planes' first half; the
+    // second half, the x sums and E); the loads are branch-free (clamped), so
+    // the compiler counts outstanding loads exactly
+    auto sload = [&](int h, int sb, u32x4 (&v)[NH]) {
+        const u32x4* pp = reinterpret_cast<const u32x4*>(A.planes) + (size_t)sb * PU + tid + NT * (NP / 2) * h;
 #pragma unroll
-            for (int k = 0; k < NV; k++) v[k] = sp[tid + 256 * k];
-            if (TYPE == T_Q4K && tid < 8 * 16)
-                xv = A.xs[((size_t)sb * 8 + (tid >> 4)) * 16 * NSG + 16 * g + (tid & 15)];
-            if (tid < 16) ev = A.ex[(size_t)sb * 16 * NSG + 16 * g + tid];
+        for (int k = 0; k < NP / 2; k++) v[k] = pp[NT * k];
+        if (h) v[NP / 2] = reinterpret_cast<const u32x4*>(A.side)[(size_t)sb * NX + min(tid, NX - 1)];
+    };
+    auto sstore = [&](int h, int buf, const u32x4 (&v)[NH]) {
+#pragma unroll
+        for (int k = 0; k < NP / 2; k++) lds[buf * SU + tid + NT * (k + (NP / 2) * h)] = v[k];
+        if (h && tid < NX) lds[buf * SU + PU + tid] = v[NP / 2];
+    };
+    int rb = it0 / NSB, sb = it0 - rb * NSB;
+    typename MfRaw<TYPE>::T raw[TL];
+    {
+        u32x4 v0[NH], v1[NH];
+        sload(0, sb, v0);
+        sload(1, sb, v1);
+#pragma unroll
+        for (int t = 0; t < TL; t++) raw[t] = mf_load<TYPE>(wrow(rb, t) + (size_t)sb * TI::BB, kg);
+        sstore(0, 0, v0);
+        sstore(1, 0, v1);
+    }
+    __syncthreads();
+    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 acc[TL][NSG];
+#pragma unroll
+    for (int t = 0; t < TL; t++)
+#pragma unroll
+        for (int g = 0; g < NSG; g++) acc[t][g] = zero;
+    for (int it = it0; it < it1; it++) {
+        const int buf = (it - it0) & 1;
+        const bool more = it + 1 < it1;
+        const int sbn = sb + 1 == NSB ? 0 : sb + 1, rbn = sb + 1 == NSB ? rb + 1 : rb;
+        const int sbl = more ? sbn : sb, rbl = more ? rbn : rb;   // the last iteration reloads its own
+        typename MfRaw<TYPE>::T rc[TL];
+        MfSb<TYPE> cs[TL];
+#pragma unroll
+        for (int t = 0; t < TL; t++) {
+            rc[t] = raw[t];
+            cs[t] = mf_sb(rc[t], kg);
+        }
+        u32x4 sv[NH];
+        sload(0, sbl, sv);                  // the next stage's first half, then the next weights
+#pragma unroll
+        for (int t = 0; t < TL; t++) raw[t] = mf_load<TYPE>(wrow(rbl, t) + (size_t)sbl * TI::BB, kg);
+        f32x4 C[TL][NSG], D[TL][NSG];       // D: Q6_K lo weights
+#pragma unroll
+        for (int t = 0; t < TL; t++)
+#pragma unroll
+            for (int g = 0; g < NSG; g++) C[t][g] = D[t][g] = zero;
+        const u32x4* sp = lds + buf * SU + lane;
+        // step j + 1's plane reads and weight decode are issued while step
+        // j's MFMAs run
+        half8 x0[2][NSG], x1[2][NSG], wa[2][TL], wb[2][TL];
+        auto fetch = [&](int j, int c) {
+#pragma unroll
+            for (int g = 0; g < NSG; g++) {
+                x0[c][g] = __builtin_bit_cast(half8, sp[(g * 8 + j) * 128]);
+                x1[c][g] = __builtin_bit_cast(half8, sp[(g * 8 + j) * 128 + 64]);
+            }
+#pragma unroll
+            for (int t = 0; t < TL; t++) {
+                if constexpr (TYPE == T_Q4K) wa[c][t] = mf_step_q4k(rc[t], j);
+                else mf_step_q6k(rc[t], cs[t], kg, j, wa[c][t], wb[c][t]);
+            }
         };
-        auto sstore = [&](int buf, const u32x4 (&v)[NV], float xv, int ev) {
-            u32x4* pd = reinterpret_cast<u32x4*>(smem + buf * MF_PAIR_BYTES);
+        fetch(0, 0);
 #pragma unroll
-            for (int k = 0; k < NV; k++) pd[tid + 256 * k] = v[k];
-            if (TYPE == T_Q4K && tid < 8 * 16)
-                reinterpret_cast<float*>(smem + buf * MF_PAIR_BYTES + MF_PAIR_PLANES * 16)[tid] = xv;
-            if (tid < 16)
-                reinterpret_cast<int*>(smem + buf * MF_PAIR_BYTES + MF_PAIR_PLANES * 16 + 8 * 16 * 4)[tid] = ev;
-        };
-        __syncthreads();                    // the previous unit's LDS reads are done
-        sload(0, sv, xsv, exv);
-        sstore(0, sv, xsv, exv);
-        typename MfRaw<TYPE>::T raw = mf_load<TYPE>(wr + (size_t)sb0 * TI::BB, kg);
-        __syncthreads();
-        f32x4 acc[4];
+        for (int j = 0; j < 8; j++) {
+            const int c = j & 1;
+            if (j < 7) fetch(j + 1, c ^ 1);
+            // every accumulator once per pass, so dependent MFMAs are
+            // TL * NSG instructions apart
 #pragma unroll
-        for (int g = 0; g < 4; g++) acc[g] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-        for (int sb = sb0; sb < sb1; sb++) {
-            MfDec<TYPE> dec;
-            if constexpr (TYPE == T_Q4K) mf_decode(raw, dec);
-            else mf_decode(raw, kg, dec);
-            raw = mf_load<TYPE>(wr + (size_t)min(sb + 1, sb1 - 1) * TI::BB, kg);   // next super-block
+            for (int pass = 0; pass < 2; pass++) {
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
-                if (g < NSG) {
-                const int i = (sb - sb0) * NSG + g, buf = i & 1;
-                const bool more = i + 1 < npairs;
-                if (more) sload(i + 1, sv, xsv, exv);
-                const uint4* ap = planes_of(buf) + lane;
-                f32x4 C = {0.0f, 0.0f, 0.0f, 0.0f};
-                // the three planes of step j + 1 are read while step j's MFMAs
-                // run; the barriers keep the compiler from hoisting all 24
-                // reads (which costs the registers of a second wave)
-                uint4 xa[3], xb[3];
+                for (int g = 0; g < NSG; g++)
 #pragma unroll
-                for (int p = 0; p < 3; p++) xa[p] = ap[p * 64];
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    if (j < 7) {
-#pragma unroll
-                        for (int p = 0; p < 3; p++) xb[p] = ap[((j + 1) * 3 + p) * 64];
+                    for (int t = 0; t < TL; t++) {
+                        const half8 xa = pass ? x1[c][g] : x0[c][g];
+                        C[t][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, wa[c][t], C[t][g], 0, 0, 0);
+                        if constexpr (TYPE == T_Q6K)
+                            D[t][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, wb[c][t], D[t][g], 0, 0, 0);
                     }
+            }
+            if (j == 3) {                   // the first half is in: store it, fetch the second
+                sstore(0, buf ^ 1, sv);
+                sload(1, sbl, sv);
+            }
+            // keeps the compiler from hoisting later steps' reads (registers)
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // the running sums: sum = fma(d 2^(E-15), C, sum), then (Q4_K) the
+        // min term
 #pragma unroll
-                    for (int p = 0; p < 3; p++) {
-                        const half8 x8 = __builtin_bit_cast(half8, xa[p]);
-                        if constexpr (TYPE == T_Q4K) {
-                            C = __builtin_amdgcn_mfma_f32_16x16x32_f16(x8, dec.w[j], C, 0, 0, 0);
-                        } else {
-                            C = __builtin_amdgcn_mfma_f32_16x16x32_f16(x8, dec.wh[j], C, 0, 0, 0);
-                            C = __builtin_amdgcn_mfma_f32_16x16x32_f16(x8, dec.wl[j], C, 0, 0, 0);
+        for (int g = 0; g < NSG; g++) {
+            const u32x4* sd = lds + buf * SU + PU + MF_SIDE_U4 * g;
+            const float a0 = reinterpret_cast<const float*>(sd)[lane];
+            const float a1 = reinterpret_cast<const float*>(sd)[64 + lane];
+            const u32x4 e4 = sd[32 + kg];         // E of streams 4 kg + v
+#pragma unroll
+            for (int t = 0; t < TL; t++) {
+                const float f0 = ldexpf(cs[t].d, (int)e4.x - 15), f1 = ldexpf(cs[t].d, (int)e4.y - 15);
+                const float f2 = ldexpf(cs[t].d, (int)e4.z - 15), f3 = ldexpf(cs[t].d, (int)e4.w - 15);
+                f32x4 s = acc[t][g];
+                s.x = fmaf(f0, C[t][g].x, s.x);
+                s.y = fmaf(f1, C[t][g].y, s.y);
+                s.z = fmaf(f2, C[t][g].z, s.z);
+                s.w = fmaf(f3, C[t][g].w, s.w);
+                if constexpr (TYPE == T_Q6K) {
+                    s.x = fmaf(f0, D[t][g].x, s.x);
+                    s.y = fmaf(f1, D[t][g].y, s.y);
+                    s.z = fmaf(f2, D[t][g].z, s.z);
+                    s.w = fmaf(f3, D[t][g].w, s.w);
+                } else {
+                    s = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, cs[t].nm0, s, 0, 0, 0);
+                    s = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, cs[t].nm1, s, 0, 0, 0);
+                }
+                acc[t][g] = s;
+            }
+        }
+        sstore(1, buf ^ 1, sv);             // unused after the last iteration
+        if (sb == NSB - 1 || !more) {       // the row block's sums: y, or a partial
+            const long a0 = (long)rb * NSB;
+            const bool own = A.whole || mf_owner(a0, A.T, A.G) == mf_owner(a0 + NSB - 1, A.T, A.G);
+#pragma unroll
+            for (int g = 0; g < NSG; g++) {
+                const int s0 = 16 * g + 4 * kg;
+#pragma unroll
+                for (int t = 0; t < TL; t++) {
+                    const int rr = 16 * (TL * wave + t) + (lane & 15);
+                    const int row = rb * R + rr;
+                    const float v4[4] = {acc[t][g].x, acc[t][g].y, acc[t][g].z, acc[t][g].w};
+                    if (row < A.N) {
+#pragma unroll
+                        for (int v = 0; v < 4; v++) {
+                            if (s0 + v >= A.B) continue;
+                            if (own) A.y[(size_t)(s0 + v) * A.N + row] = v4[v];
+                            else A.part[((size_t)(wg + rb) * 16 * NSG + s0 + v) * R + rr] = v4[v];
                         }
                     }
-                    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                    for (int p = 0; p < 3; p++) xa[p] = xb[p];
-                }
-                // the lane's outputs: streams 4 kg + v of group g, its row
-                const int4 e4 = reinterpret_cast<const int4*>(ex_of(buf))[kg];
-                f32x4 add = {ldexpf(dec.d * C.x, e4.x - 15), ldexpf(dec.d * C.y, e4.y - 15),
-                             ldexpf(dec.d * C.z, e4.z - 15), ldexpf(dec.d * C.w, e4.w - 15)};
-                if constexpr (TYPE == T_Q4K) {
-                    // minus sum_j dmin m_j xsum_j (fused: this is the tolerance path)
-                    const float4* xsl = reinterpret_cast<const float4*>(xs_of(buf)) + kg;
-#pragma unroll
-                    for (int j = 0; j < 8; j++) {
-                        const float4 xv = xsl[4 * j];
-                        add.x = fmaf(-dec.dm[j], xv.x, add.x);
-                        add.y = fmaf(-dec.dm[j], xv.y, add.y);
-                        add.z = fmaf(-dec.dm[j], xv.z, add.z);
-                        add.w = fmaf(-dec.dm[j], xv.w, add.w);
-                    }
-                }
-                acc[g] = acc[g] + add;
-                if (more) sstore(buf ^ 1, sv, xsv, exv);
-                __syncthreads();
+                    acc[t][g] = zero;
                 }
             }
         }
-        // the lane's 4 outputs per group: streams 16 g + 4 kg + v of its row
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            if (g >= NSG) continue;
-            const int s0 = 16 * g + 4 * kg;
-            const float av[4] = {acc[g].x, acc[g].y, acc[g].z, acc[g].w};
-            if (A.KP == 1) {
-                if (row < A.N)
-#pragma unroll
-                    for (int v = 0; v < 4; v++)
-                        if (s0 + v < A.B) A.y[(size_t)(s0 + v) * A.N + row] = av[v];
-            } else if (row < A.N) {
-#pragma unroll
-                for (int v = 0; v < 4; v++)
-                    A.part[((size_t)kp * 16 * NSG + s0 + v) * A.N + row] = av[v];
-            }
-        }
+        rb = rbn;
+        sb = sbn;
+        __syncthreads();
     }
 }
 
-// y = the K-parts' partial sums added in part order (MFMA multi-x with
-// several K-parts; a separate launch, so no cross-workgroup ordering is
-// needed inside the sweep)
-__global__ __launch_bounds__(256) void kq_mfma_reduce_kernel(const float* part, float* y, int B,
-                                                            int N, int NSG, int KP) {
-    const long i = (long)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (long)B * N) return;
-    const int s = (int)(i / N), r = (int)(i - (long)s * N);
-    float v = 0.0f;
-    for (int q = 0; q < KP; q++) v = v + part[((size_t)q * 16 * NSG + s) * N + r];
-    y[i] = v;
+// y of the row blocks that several workgroups share: their partial sums
+// added in workgroup order (slot wg + rb, written by kq_mf_kernel).  One
+// workgroup per (row block, 4 streams); a lane takes 4 consecutive rows and
+// loads up to 8 partials at a time.
+__global__ __launch_bounds__(256) void kq_mf_reduce_kernel(const float* part, float* y, int B, int N,
+                                                          int NSG, int R, int NSB, long T, int G) {
+    const int rb = blockIdx.x, s = 4 * blockIdx.y + (threadIdx.x >> 6), r = 4 * (threadIdx.x & 63);
+    const long w0 = mf_owner((long)rb * NSB, T, G), w1 = mf_owner((long)rb * NSB + NSB - 1, T, G);
+    if (w0 == w1 || s >= B || r >= R) return;
+    const size_t stride = (size_t)16 * NSG * R;           // floats between slots
+    const float4* p = reinterpret_cast<const float4*>(part + ((size_t)(w0 + rb) * 16 * NSG + s) * R + r);
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (long w = w0; w <= w1; w += 8) {
+        float4 q[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            q[i] = w + i <= w1 ? p[(size_t)(w - w0 + i) * (stride / 4)] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (w + i <= w1) {
+                v.x = v.x + q[i].x; v.y = v.y + q[i].y; v.z = v.z + q[i].z; v.w = v.w + q[i].w;
+            }
+    }
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+    const int row = rb * R + r;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        if (row + i < N) y[(size_t)s * N + row + i] = vv[i];
 }
 
 template <int TYPE>
 int launch_mfma_t(const float* x, const void* w, float* y, int B, int N, int K, void* planes,
                   float* xs, float* part, int grid, hipStream_t st) {
     const int NSG = (B + 15) / 16, NSB = K >> 8;
-    if (NSG > 4) return (int)hipErrorInvalidValue;
+    if (NSG > 4 || grid < 1) return (int)hipErrorInvalidValue;
     MfSplitArg s;
     s.x = x; s.planes = static_cast<uint4*>(planes);
-    s.xs = TYPE == T_Q4K ? xs : nullptr;
-    s.ex = reinterpret_cast<int*>(xs + (size_t)(K / 32) * 16 * NSG);
+    s.side = reinterpret_cast<uint4*>(xs);
     s.B = B; s.K = K; s.NSG = NSG;
     hipLaunchKernelGGL(kq_mf_split_kernel, dim3((unsigned)(NSB * NSG)), dim3(256), 0, st, s);
+    const MfPlan p = mf_plan(TYPE, NSG, N, K, grid);
     MfArg a;
     a.w = static_cast<const uint8_t*>(w);
     a.planes = static_cast<const uint4*>(planes);
-    a.xs = xs; a.ex = s.ex; a.y = y; a.part = part;
+    a.side = s.side; a.y = y; a.part = part;
     a.B = B; a.N = N; a.K = K; a.NSG = NSG;
-    a.KP = (NSB + MF_SBP - 1) / MF_SBP;
-    a.nunits = (N + 63) / 64 * a.KP;
-    a.grid = grid < a.nunits ? grid : a.nunits;
-    hipLaunchKernelGGL(kq_mf_kernel<TYPE>, dim3(a.grid), dim3(256), (size_t)(2 * MF_PAIR_BYTES), st, a);
-    if (a.KP > 1) {
-        const long n = (long)B * N;
-        hipLaunchKernelGGL(kq_mfma_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                           (const float*)part, y, B, N, NSG, a.KP);
-    }
+    a.nrb = p.nrb; a.G = p.G; a.whole = p.whole; a.T = p.T;
+    const size_t lds = (size_t)2 * mf_stage_u4(NSG) * 16;
+    typedef void (*mf_fn)(MfArg);
+    const mf_fn fn[4] = {&kq_mf_kernel<TYPE, 1>, &kq_mf_kernel<TYPE, 2>, &kq_mf_kernel<TYPE, 3>,
+                         &kq_mf_kernel<TYPE, 4>};
+    hipLaunchKernelGGL(fn[NSG - 1], dim3((unsigned)p.G), dim3(64 * MF_NW), lds, st, a);
+    if (!p.whole)
+        hipLaunchKernelGGL(kq_mf_reduce_kernel, dim3((unsigned)p.nrb, (unsigned)((B + 3) / 4)), dim3(256), 0,
+                           st, (const float*)part, y, B, N, NSG, p.rows, NSB, p.T, p.G);
     return (int)hipGetLastError();
 }
 
@@ -3696,6 +3799,16 @@ int kqk_mx_set_max_lds(int bytes) {
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
             if (e != hipSuccess) return (int)e;
         }
+    // the matrix-core sweep stages up to 2 x 66 KB
+    typedef void (*mf_fn)(MfArg);
+    const mf_fn mfs[8] = {&kq_mf_kernel<T_Q4K, 1>, &kq_mf_kernel<T_Q4K, 2>, &kq_mf_kernel<T_Q4K, 3>,
+                          &kq_mf_kernel<T_Q4K, 4>, &kq_mf_kernel<T_Q6K, 1>, &kq_mf_kernel<T_Q6K, 2>,
+                          &kq_mf_kernel<T_Q6K, 3>, &kq_mf_kernel<T_Q6K, 4>};
+    for (int i = 0; i < 8; i++) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(mfs[i]),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+        if (e != hipSuccess) return (int)e;
+    }
     return 0;
 }
 
@@ -3821,18 +3934,19 @@ int kqk_launch_moe_group(const int* sel, int nm, int E, int nt, int x_div, int m
 }
 
 // MFMA multi-x (Q4_K, Q6_K): workspace sizes for B streams of N x K, and the
-// launch (x split into planes, the matrix-core sweep, and the sum of the
-// K-parts' partials).
+// launch (x split into planes, the matrix-core sweep over `grid`
+// workgroups, and the sum of shared row blocks' partials).
 // Workspace of one launch of up to 64 streams (larger B runs in chunks of
 // 64 on the same workspace): the planes, then the x sums and the exponents
-// (one region), then the K-part partial sums.
-int kqk_mfma_workspace(int type, int B, int N, int K, long* planes, long* xs, long* part) {
-    if ((type != T_Q4K && type != T_Q6K) || B < 1 || N < 1 || K <= 0 || (K & 255)) return -1;
-    const long NSG = B >= 64 ? 4 : (B + 15) / 16, NSB = K >> 8;
-    const long KP = (NSB + MF_SBP - 1) / MF_SBP;
-    *planes = NSB * NSG * MF_PAIR_PLANES * 16;
-    *xs = (long)(K / 32) * NSG * 16 * 4 + NSB * NSG * 16 * 4;
-    *part = KP > 1 ? KP * NSG * 16 * (long)N * 4 : 0;
+// (one region), then the partial sums.
+int kqk_mfma_workspace(int type, int B, int N, int K, int grid, long* planes, long* xs, long* part) {
+    if ((type != T_Q4K && type != T_Q6K) || B < 1 || N < 1 || K <= 0 || (K & 255) || grid < 1)
+        return -1;
+    const int NSG = B >= 64 ? 4 : (B + 15) / 16;
+    const long NSB = K >> 8;
+    *planes = NSB * NSG * MF_GROUP_U4 * 16;
+    *xs = NSB * NSG * MF_SIDE_U4 * 16;
+    *part = mf_plan(type, NSG, N, K, grid).part_floats * 4;
     return 0;
 }
 

@@ -72,8 +72,9 @@ int kqk_launch_mx_moe(int type, const int* plan, long plan_lds, long lds, int gr
                       int nm, int E, int nt, int x_div, const void* w0, const void* w1, float* y0,
                       float* y1, long estride, const float* X, int N, int K, const float* probs,
                       int B, int k, int* sel_out, float* selw_out, hipStream_t st);
-/* MFMA multi-x (Q4_K, Q6_K): workspace sizes, and the launch */
-int kqk_mfma_workspace(int type, int B, int N, int K, long* planes, long* xs, long* part);
+/* MFMA multi-x (Q4_K, Q6_K): workspace sizes for a launch over `grid`
+ * workgroups, and the launch (the same grid) */
+int kqk_mfma_workspace(int type, int B, int N, int K, int grid, long* planes, long* xs, long* part);
 /* Bytes of the library's static device scratch (the public limit). */
 #define KQK_NOALLOC_BYTES KQ_NOALLOC_SCRATCH_BYTES
 /* Device address (on the current device) and size of the library's static

@@ -563,9 +563,10 @@ int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,
 }
 
 /* B streams on the matrix cores (Q4_K and Q6_K): the tolerance path.  Each
- * sub-block's inner product runs as bf16 MFMAs over an exact three-plane
- * split of x, so results differ from the single-stream ones by about one
- * binary32 ulp of each sub-block sum (not bit for bit). */
+ * super-block's inner product runs as fp16 MFMAs over the weights with
+ * their sub-block scales folded in and a two-plane (22-bit) split of x, so
+ * results differ from the single-stream ones by a few binary32 ulps of the
+ * terms' magnitude (not bit for bit). */
 /* Checks an MFMA multi-x call and lays out its workspace (x planes, x
  * sums, K-part partials, each 256-byte aligned): *o_xs, *o_pt are the
  * offsets of the second and third parts, the return value the bytes
@@ -580,7 +581,7 @@ static size_t mfma_prepare(const char* who, int type, const void* w, const float
     if (check_shape(type, N, K) || kq_ready()) return 0;
     if (!w || !xs || !ys) { kq_fail("%s: NULL pointer", who); return 0; }
     long pl, xsb, pt;
-    if (kqk_mfma_workspace(type, B, N, K, &pl, &xsb, &pt)) {
+    if (kqk_mfma_workspace(type, B, N, K, g_kq.n_cu, &pl, &xsb, &pt)) {
         kq_fail("%s: bad shape", who);
         return 0;
     }
@@ -593,7 +594,7 @@ static size_t mfma_prepare(const char* who, int type, const void* w, const float
 static int mfma_launch(int type, const void* w, const float* xs, float* ys, int B, int N, int K,
                        uint8_t* ws, size_t o_xs, size_t o_pt, kq_stream stream) {
     const int e = kqk_launch_mfma(type, xs, w, ys, B, N, K, ws, (float*)(ws + o_xs),
-                                  (float*)(ws + o_pt), 2 * g_kq.n_cu, pick(stream));
+                                  (float*)(ws + o_pt), g_kq.n_cu, pick(stream));
     if (e) return kq_fail("mfma multix launch: %s", hipGetErrorString((hipError_t)e));
     return 0;
 }

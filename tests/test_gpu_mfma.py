@@ -3,8 +3,9 @@ path, checked against the exact multi-stream GEMV (which equals the
 single-stream and oracle arithmetic).  Bound, per output:
     |y_mfma - y_exact| <= 2e-6 * sum_l |w_l| |x_l|
 (the row's dequantized weights times |x|: an upper bound on the sizes of the
-terms whose binary32 rounding order differs), i.e. a few binary32 ulps of
-the terms; the test also prints the max relative error against the oracle
+terms whose binary32 rounding order differs, and on the 2^-21 relative
+rounding of x to its two fp16 planes), i.e. a few binary32 ulps of the
+terms; the test also prints the max relative error against the oracle
 and the share of outputs within the GEMV bound of 1e-5."""
 import numpy as np
 import pytest
@@ -87,6 +88,69 @@ def test_mfma_27b_sampled(port, qtype, N, Kd):
     print(f"27B {K.TYPE_NAMES[qtype]}: max rel err vs oracle {rel.max():.2e}, "
           f"within 1e-5: {np.mean(O.rel_err(got, exact) <= 1e-5) * 100:.2f}%")
     assert np.all(np.isfinite(got))
+
+
+@pytest.mark.parametrize("qtype,N,Kd", [(12, 131100, 256), (14, 65600, 512)])
+def test_mfma_whole_row_blocks(port, qtype, N, Kd):
+    """Enough row blocks (256 rows for Q4_K, 128 for Q6_K) for at least two
+    per workgroup: whole row blocks per workgroup, no partial sums; the last
+    block is ragged."""
+    B = 16
+    w = synth.tensor(qtype, N, Kd, 1000 + qtype)
+    xs = np.stack([synth.gaussian(synth.rng(1010 + s), Kd) for s in range(B)])
+    dw = torch.from_numpy(w).cuda()
+    got = run(K.gemv_multix_mfma_dev, qtype, dw, xs, B, N, Kd)
+    exact = run(K.gemv_multix_dev, qtype, dw, xs, B, N, Kd)
+    rows = np.concatenate([np.random.default_rng(6).choice(N, 250, replace=False),
+                           np.arange(N - 6, N)])
+    mag = magnitude(port, qtype, w, xs, rows, Kd)
+    err = np.abs(got[:, rows].astype(np.float64) - exact[:, rows].astype(np.float64))
+    print(f"{K.TYPE_NAMES[qtype]} N={N}: max err/mag {(err / mag).max():.2e}")
+    assert np.all(np.isfinite(got))
+    assert (err / mag).max() <= TOL
+
+
+@pytest.mark.parametrize("qtype", [12, 14])
+def test_mfma_more_than_64_streams(port, qtype):
+    """B = 100 runs as chunks of 64 and 36 streams on one workspace."""
+    B, N, Kd = 100, 96, 1024
+    w = synth.tensor(qtype, N, Kd, 1020 + qtype)
+    xs = np.stack([synth.gaussian(synth.rng(1030 + s), Kd) for s in range(B)])
+    dw = torch.from_numpy(w).cuda()
+    got = run(K.gemv_multix_mfma_dev, qtype, dw, xs, B, N, Kd)
+    exact = run(K.gemv_multix_dev, qtype, dw, xs, B, N, Kd)
+    mag = magnitude(port, qtype, w, xs, range(N), Kd)
+    err = np.abs(got.astype(np.float64) - exact.astype(np.float64))
+    assert (err / mag).max() <= TOL
+
+
+@pytest.mark.parametrize("qtype", [12, 14])
+def test_mfma_wide_dynamic_range(port, qtype):
+    """x scaled per stream to the binary exponent of its largest |x|: streams
+    with outliers 1e4 above the rest, a tiny stream (1e-30), an all-zero
+    stream, subnormal values and a huge stream (1e30) keep the bound."""
+    B, N, Kd = 16, 80, 2048
+    w = synth.tensor(qtype, N, Kd, 1040 + qtype)
+    r = synth.rng(1041)
+    xs = np.stack([synth.gaussian(synth.rng(1050 + s), Kd) for s in range(B)])
+    for s in range(0, 6):                       # outliers
+        idx = r.choice(Kd, 5, replace=False)
+        xs[s, idx] *= np.float32(1e4)
+    xs[6] *= np.float32(1e-30)
+    xs[7] = 0.0
+    xs[8, ::3] = np.float32(1e-40)              # subnormal
+    xs[9] *= np.float32(1e30)
+    xs = xs.astype(np.float32)
+    dw = torch.from_numpy(w).cuda()
+    got = run(K.gemv_multix_mfma_dev, qtype, dw, xs, B, N, Kd)
+    exact = run(K.gemv_multix_dev, qtype, dw, xs, B, N, Kd)
+    mag = magnitude(port, qtype, w, xs, range(N), Kd)
+    err = np.abs(got.astype(np.float64) - exact.astype(np.float64))
+    assert np.all(got[7] == 0.0)
+    live = mag > 0
+    print(f"{K.TYPE_NAMES[qtype]}: max err/mag {(err[live] / mag[live]).max():.2e}")
+    assert np.all(np.isfinite(got))
+    assert (err[live] / mag[live]).max() <= TOL
 
 
 def test_mfma_repeatable_and_other_types_refused():

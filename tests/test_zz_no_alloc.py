@@ -54,10 +54,10 @@ def test_noalloc_matches_allocating_entry(qtype):
 
 def test_noalloc_refuses_sizes_beyond_the_array():
     L = K.lib()
-    # B = 64 over a 17408 x 17408 Q6_K matrix needs ~80 MB of partial sums;
-    # the buffers are real (and large enough), so nothing could be read out
-    # of bounds even if the refusal were missing
-    B, N, Kd = 64, 17408, 17408
+    # B = 64 streams of K = 131072 need 32 MiB of x planes alone, plus the
+    # x sums; the buffers are real (and large enough), so nothing could be
+    # read out of bounds even if the refusal were missing
+    B, N, Kd = 64, 16, 131072
     w = torch.zeros(N * L.kq_row_bytes(14, Kd), dtype=torch.uint8, device="cuda")
     x = torch.zeros(B * Kd, dtype=torch.float32, device="cuda")
     y = torch.zeros(B * N, dtype=torch.float32, device="cuda")
