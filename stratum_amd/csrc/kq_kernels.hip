@@ -2497,8 +2497,8 @@ __global__ __launch_bounds__(1024) void kq_moe_group_kernel(MoeGroupArg a) {
 // Tolerance path for many streams (B >= 16), Q4_K and Q6_K, on the matrix
 // cores.  The weights enter with their sub-block scales folded in, as exact
 // fp16 integers: Q4_K w = sc*q (sc <= 63, q <= 15: at most 945), Q6_K
-// w = sc*(q - 32) (|w| <= 4096) split exactly into hi = w - (w & 7) and
-// lo = w & 7.  x enters as two fp16 planes, hi = fp16(x') and
+// w = sc*(q - 32) (|w| <= 4096) split exactly into 16*sh*(q - 32) and
+// sl*(q - 32), sc = 16 sh + sl.  x enters as two fp16 planes, hi = fp16(x') and
 // mid = fp16(x' - hi), of x' = x*2^(15-E), E the binary exponent of the
 // largest |x| of the (stream, super-block): the planes cannot overflow, each
 // x keeps 22 significant bits (|x - (hi + mid) 2^(E-15)| <= 2^-21 |x| +
@@ -2521,7 +2521,7 @@ __global__ __launch_bounds__(1024) void kq_moe_group_kernel(MoeGroupArg a) {
 //  * kq_mf_split_kernel: one workgroup per (super-block, 16-stream group)
 //    writes the two planes in A-operand order, the x sums and E;
 //  * kq_mf_kernel: 8 waves; a wave owns MfShape::TILES 16-row tiles (Q4_K 2,
-//    Q6_K 1: Q6_K's hi and lo already use each A operand twice), so a
+//    Q6_K 1: Q6_K's two weight parts already use each A operand twice), so a
 //    workgroup sweeps a block of 256 (Q4_K) or 128 (Q6_K) rows.  The
 //    (row block, super-block) iterations are split into one contiguous range
 //    per workgroup (whole row blocks when there are at least two per
@@ -2721,24 +2721,23 @@ __device__ __forceinline__ void q4_scaled(uint32_t nib, half2v sc2, half2v off2,
     w23 = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(half2v, b), sc2, off2));
 }
 
-// fp16 hi / lo of w = sc * (q - 32) for two u16 lanes of q (0..63):
-// w in [-4064, 4096] (q - 32 in [-32, 31], sc in [-128, 127]); lo = w & 7
-// (fp16 of 1024 + lo minus 1024), hi = w - lo = 8 t with t = w >> 3 in
-// [-508, 512]: fp16 of 1532 + t is 0x6400 | (t + 508), and
-// fma(1532 + t, 8, -12256) = 8 t exactly
-__device__ __forceinline__ void q6_scaled(uint32_t q2, uint32_t scw, uint32_t& hi, uint32_t& lo) {
-    typedef short s16x2 __attribute__((ext_vector_type(2)));
-    const s16x2 q = __builtin_bit_cast(s16x2, q2);
-    const s16x2 sc = __builtin_bit_cast(s16x2, scw);
-    const s16x2 w = (q - (s16x2){32, 32}) * sc;                            // low 16 bits exact
-    const uint32_t wl = __builtin_bit_cast(uint32_t, w);
-    const uint32_t l = (wl & 0x00070007u) | 0x64006400u;
-    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, l) + (half2v){(_Float16)-1024.0f, (_Float16)-1024.0f});
-    const s16x2 tt = (w >> (s16x2){3, 3}) + (s16x2){508, 508};            // in [0, 1020]
-    const uint32_t hb = __builtin_bit_cast(uint32_t, tt) | 0x64006400u;
-    hi = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(
-             __builtin_bit_cast(half2v, hb), (half2v){(_Float16)8.0f, (_Float16)8.0f},
-             (half2v){(_Float16)-12256.0f, (_Float16)-12256.0f}));
+// fp16 of the two parts of w = sc * (q - 32) for the four q bytes of q4
+// (each < 64), sc = 16 sh + sl: the bytes 4 q become halves 0x6C00 | 4q =
+// 4096 + 16 q, and fma(4096 + 16 q, sh, -4608 sh) = 16 sh (q - 32),
+// fma(4096 + 16 q, sl / 16, -288 sl) = sl (q - 32): exact integers (every
+// intermediate below 65504, the results of at most 9 significant bits), and
+// their sum is w.  m1, a1, m2, a2 = sh, -4608 sh, sl / 16, -288 sl.
+__device__ __forceinline__ void q6_split(uint32_t q4, _Float16 m1, _Float16 a1, _Float16 m2,
+                                         _Float16 a2, uint32_t& h01, uint32_t& h23, uint32_t& l01,
+                                         uint32_t& l23) {
+    const uint32_t s4 = q4 << 2;                                               // 4 q per byte
+    const half2v p01 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x6c6c6c6cu, s4, 0x05010400u));
+    const half2v p23 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x6c6c6c6cu, s4, 0x05030402u));
+    const half2v M1 = {m1, m1}, A1 = {a1, a1}, M2 = {m2, m2}, A2 = {a2, a2};
+    h01 = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(p01, M1, A1));
+    h23 = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(p23, M1, A1));
+    l01 = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(p01, M2, A2));
+    l23 = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(p23, M2, A2));
 }
 
 // Per-super-block constants of one lane's row.  Q4_K: d, and the B operands
@@ -2786,7 +2785,7 @@ __device__ __forceinline__ half8 mf_step_q4k(const MfRawQ4& r, int j) {
     return __builtin_bit_cast(half8, make_uint4(w0, w1, w2, w3));
 }
 
-// Q6_K step st: the lane's 8 weights sc * (q - 32) as hi and lo
+// Q6_K step st: the lane's 8 weights sc * (q - 32) as its two parts 16 sh (q - 32) and sl (q - 32)
 __device__ __forceinline__ void mf_step_q6k(const MfRawQ6& r, const MfSb<T_Q6K>& c, int kg, int st,
                                             half8& wh, half8& wl) {
     const uint32_t sh = r.sh;
@@ -2798,16 +2797,16 @@ __device__ __forceinline__ void mf_step_q6k(const MfRawQ6& r, const MfSb<T_Q6K>&
     const uint32_t H1 = __builtin_amdgcn_alignbit(r.qh[h][2], r.qh[h][1], sh);
     const uint32_t q0 = ((L0 >> (4 * (t >> 1))) & 0x0f0f0f0fu) | (((H0 >> (2 * t)) & 0x03030303u) << 4);
     const uint32_t q1 = ((L1 >> (4 * (t >> 1))) & 0x0f0f0f0fu) | (((H1 >> (2 * t)) & 0x03030303u) << 4);
-    // the lane's scale: byte 2 st + (kg >> 1), sign-extended to both u16 lanes
+    // the lane's scale: byte 2 st + (kg >> 1), split as sc = 16 sh + sl
+    // (sh = sc >> 4 in [-8, 7], sl = sc & 15)
     const int b = 2 * st + (kg >> 1);
-    const uint32_t s8 = (c.scw[b >> 2] >> (8 * (b & 3))) & 0xffu;
-    const uint32_t s16 = (uint32_t)(int32_t)(int8_t)s8 & 0xffffu;
-    const uint32_t scw2 = s16 | (s16 << 16);
+    const int sc = (int)(int8_t)(uint8_t)(c.scw[b >> 2] >> (8 * (b & 3)));
+    const int shi = sc >> 4, slo = sc & 15;
+    const _Float16 m1 = (_Float16)(short)shi, a1 = (_Float16)(float)(-4608 * shi);   // |a1| <= 36864
+    const _Float16 m2 = (_Float16)(short)slo * (_Float16)0.0625f, a2 = (_Float16)(short)(-288 * slo);
     uint32_t h4[4], l4[4];
-    q6_scaled(__builtin_amdgcn_perm(0u, q0, 0x0c010c00u), scw2, h4[0], l4[0]);
-    q6_scaled(__builtin_amdgcn_perm(0u, q0, 0x0c030c02u), scw2, h4[1], l4[1]);
-    q6_scaled(__builtin_amdgcn_perm(0u, q1, 0x0c010c00u), scw2, h4[2], l4[2]);
-    q6_scaled(__builtin_amdgcn_perm(0u, q1, 0x0c030c02u), scw2, h4[3], l4[3]);
+    q6_split(q0, m1, a1, m2, a2, h4[0], h4[1], l4[0], l4[1]);
+    q6_split(q1, m1, a1, m2, a2, h4[2], h4[3], l4[2], l4[3]);
     wh = __builtin_bit_cast(half8, make_uint4(h4[0], h4[1], h4[2], h4[3]));
     wl = __builtin_bit_cast(half8, make_uint4(l4[0], l4[1], l4[2], l4[3]));
 }
@@ -2888,7 +2887,7 @@ __global__ __launch_bounds__(64 * MF_NW) void kq_mf_kernel(MfArg A) {
         sload(0, sbl, sv);                  // the next stage's first half, then the next weights
 #pragma unroll
         for (int t = 0; t < TL; t++) raw[t] = mf_load<TYPE>(wrow(rbl, t) + (size_t)sbl * TI::BB, kg);
-        f32x4 C[TL][NSG], D[TL][NSG];       // D: Q6_K lo weights
+        f32x4 C[TL][NSG], D[TL][NSG];       // D: the Q6_K sl parts
 #pragma unroll
         for (int t = 0; t < TL; t++)
 #pragma unroll
