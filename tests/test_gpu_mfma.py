@@ -67,11 +67,11 @@ def test_mfma_against_exact(port, qtype, B, N, Kd):
     assert worst <= TOL
 
 
+@pytest.mark.parametrize("B", [16, 64])
 @pytest.mark.parametrize("qtype,N,Kd", [(12, 17408, 5120), (14, 5120, 17408)])
-def test_mfma_27b_sampled(port, qtype, N, Kd):
-    """27B gate / down with 16 streams: every output against the exact path,
-    sampled rows against the oracle."""
-    B = 16
+def test_mfma_27b_sampled(port, qtype, N, Kd, B):
+    """27B gate / down with 16 and 64 streams: every output against the exact
+    path, sampled rows against the oracle."""
     w = synth.tensor(qtype, N, Kd, 970 + qtype)
     xs = np.stack([synth.gaussian(synth.rng(980 + s), Kd) for s in range(B)])
     dw = torch.from_numpy(w).cuda()
