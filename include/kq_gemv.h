@@ -177,21 +177,25 @@ int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,
                        int B, int N, int K, kq_stream stream);
 
 /* The same product on the matrix cores, for many streams (B >= 16 is where
- * it pays): Q4_K and Q6_K only (-1 for other types).  Each sub-block's
- * inner product sum_k q_k x_k runs as bf16 x bf16 -> fp32 MFMAs over an
- * exact split of x into three bf16 planes; the scaling and the sums across
- * sub-blocks follow the reference's formula in binary32.  The results are
- * NOT bit-identical to kq_gemv_multix_dev: they differ by about one
- * binary32 ulp of each sub-block's sum (the measured bound is reported with
- * the MULTISEQ benchmark).  No counterpart in the reference, whose multix
- * must equal the single-stream result (stratum_linear.h:963-966); this is
- * the opt-in dense-contraction path for large B.  x must be finite. */
+ * it pays): Q4_K and Q6_K only (-1 for other types).  Each super-block runs
+ * as fp16 x fp16 -> fp32 MFMAs: the weights with their sub-block scales
+ * folded in (exact fp16 integers), x as two fp16 planes (22 significant
+ * bits, scaled per stream and super-block); the block scale, the Q4_K min
+ * term and the sums across super-blocks are fp32.  The results are NOT
+ * bit-identical to kq_gemv_multix_dev: every output is within
+ * 2e-6 * sum_k |w_k x_k| of it (measured at most 6.6e-8 at the 27B shapes).
+ * No counterpart in the reference, whose multix must equal the
+ * single-stream result (stratum_linear.h:963-966); this is the opt-in
+ * dense-contraction path for large B.  x must be finite.  The workspace is
+ * the library's, grown on the first call of a larger shape (hipMalloc /
+ * hipFree, which synchronise the device): callers that cannot allocate use
+ * kq_gemv_multix_mfma_noalloc_dev. */
 int kq_gemv_multix_mfma_dev(int type, const void* w, const float* xs, float* ys,
                             int B, int N, int K, kq_stream stream);
 
 /* kq_gemv_multix_mfma_dev without any allocation: the same kernels and the
- * same results bit for bit, with the workspace (x planes, x sums, K-part
- * partial sums) in a static device array of KQ_NOALLOC_SCRATCH_BYTES that
+ * same results bit for bit, with the workspace (x planes, x sums and
+ * exponents, partial sums of shared row blocks) in a static device array of KQ_NOALLOC_SCRATCH_BYTES that
  * each GPU holds for the life of the process.  No counterpart in the
  * reference; it is for callers that cannot allocate device memory (code
  * under HIP graph capture, allocation-free serving loops).  Calls no
