@@ -11,6 +11,7 @@
 #include "../../include/kq_gguf.h"
 
 #include <stdarg.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
