@@ -252,16 +252,16 @@ static const void* tensor_dev(const kq_tensor* w, int N, int K) {
 }
 
 /* ----------------------------------------------------------- planning */
-/* One persistent workgroup per CU (KQ_GRID overrides).  The workgroup
- * size follows the largest per-workgroup share of 64-weight chunks over the
- * segments: enough waves to keep each CU's memory pipe busy without many
- * idle lanes on small tensors (KQ_WG_THREADS overrides: 256, 512 or
- * 1024).  Each wave keeps one batch of loads in flight, two when the
- * workgroup has fewer than 16 waves to hide the memory latency with
- * (KQ_DEPTH overrides: 1 or 2).  A share of 2048-4095 chunks (a 512-lane
- * workgroup, e.g. a 27B Q/K/V group) is instead split over two workgroups
- * per CU when their LDS fits: twice the waves per CU, and two prologues
- * and tails that overlap (measured 9.7 -> 8.7 us for Q/K/V). */
+/* One persistent workgroup per CU (KQ_GRID overrides), one batch of loads
+ * in flight per wave (KQ_DEPTH=2 overrides, for workgroups of at most 512
+ * lanes).  The workgroup size follows the largest per-workgroup share of
+ * 64-weight chunks over the segments: 1024 lanes above 512 chunks, else
+ * 512 (KQ_WG_THREADS overrides: 256, 512 or 1024).  Measured in one
+ * process over shares of 128-4096 chunks (K = 1024, 2048, 5120) against
+ * 256 or 512 lanes with two batches in flight and two 512-lane workgroups
+ * per CU: this rule was the fastest at every share measured, e.g. the
+ * 27B Q/K/V group (2560 chunks) 10.1 -> 9.3 us, 1600 chunks 7.3 -> 6.7
+ * us, 800 chunks 6.6 -> 5.6 us. */
 static int plan_grid(void) {
     return g_kq.env_grid > 0 ? g_kq.env_grid : g_kq.n_cu;
 }
@@ -279,13 +279,11 @@ static long max_share(const kqk_seg* segs, int nseg, int grid) {
 
 static int plan_threads(const kqk_seg* segs, int nseg, int grid) {
     if (g_kq.env_threads) return g_kq.env_threads;
-    const long chunks = max_share(segs, nseg, grid);
-    return chunks >= 4096 ? 1024 : chunks >= 1024 ? 512 : 256;
+    return max_share(segs, nseg, grid) > 512 ? 1024 : 512;
 }
 
-static int plan_depth(int threads) {
-    if (g_kq.env_depth) return g_kq.env_depth;
-    return threads < 1024 ? 2 : 1;
+static int plan_depth(void) {
+    return g_kq.env_depth ? g_kq.env_depth : 1;
 }
 
 static int launch_segs_one(const kqk_seg* segs, int nseg, hipStream_t st);
@@ -307,22 +305,13 @@ static int launch_segs(const kqk_seg* segs, int nseg, hipStream_t st) {
 }
 
 static int launch_segs_one(const kqk_seg* segs, int nseg, hipStream_t st) {
-    int grid = plan_grid(), threads = plan_threads(segs, nseg, grid), depth = plan_depth(threads);
+    const int grid = plan_grid(), threads = plan_threads(segs, nseg, grid), depth = plan_depth();
     for (int i = 0; i < nseg; i++) {   /* the kernel's row arithmetic is 24-bit */
         long n = 0;
         for (int p = 0; p < segs[i].nparts; p++) n += segs[i].rows[p];
         if (n >= (1L << 24))
             return kq_fail("segment %d has %ld rows (at most 2^24 - 1 per launch): split the rows",
                            i, n);
-    }
-    if (!g_kq.env_grid && !g_kq.env_threads && !g_kq.env_depth &&
-        max_share(segs, nseg, grid) >= 2048 && threads == 512) {
-        int a = 0, b = 0, c = 0;
-        const long lds2 = kqk_segs_lds(segs, nseg, 2 * grid, &a, &b, &c);
-        if (lds2 > 0 && 2 * lds2 <= g_kq.lds_max) {
-            grid *= 2;
-            depth = 1;
-        }
     }
     int xs_off = 0, terms_off = 0, scr_off = 0;
     long lds = kqk_segs_lds(segs, nseg, grid, &xs_off, &terms_off, &scr_off);

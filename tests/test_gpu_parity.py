@@ -155,10 +155,10 @@ def test_gemv_add_epilogue(port, qtype):
                                         (12, 1024, 5120)])
 def test_gemv_27b_shape_sampled(port, qtype, N, Kd, kq_env):
     """Full-size config shapes: 384 sampled rows against the oracle,
-    bit-identical reruns, and the same bits under a different row
-    decomposition (37 workgroups of 256 lanes).  27B-class: gate/up, down,
-    Q, the merged Q/K/V row count 8192 and a ragged 8191 (two workgroups per
-    CU), type 42 and Q2_K gate, O (5120 x 6144) and K/V (1024 x 5120) alone;
+    bit-identical reruns, and the same bits under two other launch shapes
+    (37 workgroups of 256 lanes; 512 lanes with two batches in flight per
+    wave).  27B-class: gate/up, down, Q, the merged Q/K/V row count 8192 and
+    a ragged 8191, type 42 and Q2_K gate, O (5120 x 6144) and K/V (1024 x 5120) alone;
     Qwen3-0.6B: the Q6_K LM head 151936 x 1024 (594 rows per workgroup, and
     several launches under the 37-workgroup decomposition, whose terms would
     not fit one launch's LDS)."""
@@ -171,6 +171,8 @@ def test_gemv_27b_shape_sampled(port, qtype, N, Kd, kq_env):
     check_close(y[rows], port.gemv_rows(qtype, w, x, rows, Kd), f"27b {qtype} {N}x{Kd}")
     assert same_values(gpu_gemv(qtype, w, x, N, Kd), y)
     kq_env(KQ_GRID=37, KQ_WG_THREADS=256)
+    assert same_values(gpu_gemv(qtype, w, x, N, Kd), y)
+    kq_env(KQ_GRID=0, KQ_WG_THREADS=512, KQ_DEPTH=2)
     assert same_values(gpu_gemv(qtype, w, x, N, Kd), y)
 
 
