@@ -265,6 +265,11 @@ __device__ __forceinline__ void group_place(int gi, int& slot0, int& xsi) {
     }
 }
 
+// SwiGLU (stratum_swiglu, stratum_engine.h:373-392): g / (1 + expf(-g)) * u,
+// binary32 -- kq_swiglu_kernel's expression, so the gather launch's fused
+// SwiGLU writes the activations that kernel writes.
+__device__ __forceinline__ float swiglu1(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+
 template <int TYPE>
 struct XStage {
     static constexpr int G4 = XGroup<TYPE>::G4;
@@ -1269,6 +1274,13 @@ struct SegsArg {
     int xs_off;        // LDS byte offsets of the xs, terms and scratch regions
     int terms_off;
     int scr_off;
+    // MoE FFN step pieces folded into a one-segment MoE gather launch
+    // (segment 0, selection kernels only; null / 0: unused), each instead
+    // of writing y (see run_segment's epilogue):
+    float* act;        // parts k gate then k up slices: act = SwiGLU(gate, up)
+    float* cx;         // parts = ranks: cx += the rank-ordered weighted sum,
+    const float* cw;   //   weights cw[part]
+    int logits;        // the routing input holds router logits: softmax first
 };
 
 // n / d for the divisor encoded by (m, l): the invariant-integer division
@@ -1298,7 +1310,8 @@ struct Staged {
 constexpr int SCR_FLAGS = 4 * MAXSEG;
 constexpr int SCR_TABS = SCR_FLAGS + 4 * 16;
 constexpr int SCR_RSEL = SCR_TABS + 3 * 8 * MAXG;
-constexpr int SCR_BYTES = SCR_RSEL + 8 * MAXG;
+constexpr int SCR_CMB = SCR_RSEL + 8 * MAXG;     // combine: weight per part (<0 skip flag)
+constexpr int SCR_BYTES = SCR_CMB + 8 * MAXG;
 
 // Part layout of a segment: one part; up to 4 parts of any sizes (a merged
 // same-input group: the part of a row by comparing with the part starts,
@@ -1481,6 +1494,50 @@ __device__ void wg_topk(const float* w, float pv, int E, int k, int T, uint8_t* 
     lds_barrier();
 }
 
+// Softmax of one token's E <= T router logits, computed by the whole
+// workgroup with kq_softmax_kernel's arithmetic (stratum_engine.h:395-423):
+// the NaN-ignoring maximum (NaN when logit 0 is NaN), expf(v - max), their
+// binary64 sum in index order by one lane, inv = (float)(1 / sum), p = e *
+// inv.  v: lane tid's logit (tid < E); returns its probability, -1 past E.
+// Work: E + 17 floats of LDS at sm, free again on return.
+__device__ float wg_softmax(float v, int E, int T, float* sm) {
+    const int tid = threadIdx.x;
+    float* wm = sm + 1024;                     // per-wave maxima, then inv
+    float m = tid < E ? v : -INFINITY;
+    if (tid < E) sm[tid] = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((tid & 63) == 0) wm[tid >> 6] = m;
+    lds_barrier();
+    float maxv = wm[0];
+    for (int w = 1; w < (T >> 6); w++) maxv = fmaxf(maxv, wm[w]);
+    if (isnan(sm[0])) maxv = sm[0];
+    lds_barrier();
+    const float e = tid < E ? expf(v - maxv) : 0.0f;
+    if (tid < E) sm[tid] = e;
+    lds_barrier();
+    if (tid == 0) {                            // 16 values per LDS round trip
+        double sum = 0.0;
+        int i = 0;
+        for (; i + 16 <= E; i += 16) {
+            float4 q[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) q[j] = *reinterpret_cast<const float4*>(sm + i + 4 * j);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                sum = sum + (double)q[j].x; sum = sum + (double)q[j].y;
+                sum = sum + (double)q[j].z; sum = sum + (double)q[j].w;
+            }
+        }
+        for (; i < E; i++) sum = sum + (double)sm[i];
+        wm[16] = (float)(1.0 / sum);
+    }
+    lds_barrier();
+    const float pr = e * wm[16];
+    lds_barrier();                             // sm is the caller's again
+    return tid < E ? pr : -1.0f;
+}
+
 template <int TYPE, int DEPTH, int PM>
 __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st, uint8_t* smem,
                             bool last_seg) {
@@ -1516,6 +1573,9 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
     const int xst = ngx > 1 ? S.x_stride : 0;
     // x layouts: 0 strided fp32, 1 linear fp32, 2 / 3 int8 per 32 / per 16
     constexpr int LAYOUT = XGroup<TYPE>::I8 ? (TYPE == T_Q4K_I8 ? 2 : 3) : (int)TI::LINEAR;
+    // the MoE FFN step pieces of a one-segment gather launch (segment 0)
+    const bool cmb = PM == PM_SEL && seg == 0 && A.cx != nullptr;   // uniform
+    const bool swe = PM == PM_SEL && seg == 0 && A.act != nullptr;  // uniform
     const bool same_x = st.x == S.x && st.K == K && st.layout == LAYOUT && st.ngx == ngx &&
                         st.xst == xst;
     const bool restage = !same_x || (SCTYPE && st.k == 0 && !st.bad);
@@ -1537,6 +1597,13 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
         wv = S.w[gl];
         yv = S.y[gl];
         av = S.add[gl];
+    }
+    // combine: part lane's weight, and the residual of output row b + tid G
+    // for the first pn / G lanes, loaded now so the epilogue waits for none
+    float cwl = 0.0f, cres = 0.0f;
+    if (PM == PM_SEL && cmb) {
+        if (lane < S.nparts) cwl = A.cw[lane];
+        if (tid < S.pn / G) cres = A.cx[b + tid * G];
     }
     f32x4 xv[G4];
     // first round of x, ahead of the weights (and of the routing, which
@@ -1562,6 +1629,9 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
         // the routing's last barrier); the result in the scratch region
         int* rs = reinterpret_cast<int*>(smem + A.scr_off + SCR_RSEL);
         float* rw = reinterpret_cast<float*>(rs + MAXG);
+        // router logits: their softmax first (the host allows it for emax <= 256,
+        // so wg_topk reads no weight beyond its lanes' pv)
+        if (A.logits) pv = wg_softmax(pv, S.emax, T, reinterpret_cast<float*>(smem + A.terms_off));
         wg_topk(S.probs, pv, S.emax, S.ksel, T, smem + A.terms_off, rs, rw);
         rsel = rs;
         if (b == 0 && tid < S.ksel) {
@@ -1573,14 +1643,19 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
         // each wave writes the part tables itself (identical values), so its
         // own reads need no barrier
         if (lane < S.nparts) {
+            int se = 0;
             if (PM == PM_SEL) {                   // the expert chosen on the device
-                const int se = rsel ? rsel[lane % S.ksel] : S.sel[lane % S.ksel];
+                se = rsel ? rsel[lane % S.ksel] : S.sel[lane % S.ksel];
                 const int e = min(max(se, 0), S.emax - 1);
                 wv += (size_t)e * S.estride;
             }
             wtab[lane] = wv;
             ytab[lane] = yv;
             atab[lane] = av;
+            if (PM == PM_SEL && cmb) {       // the combine's weight and skip flag (empty slot)
+                reinterpret_cast<float*>(smem + A.scr_off + SCR_CMB)[lane] = cwl;
+                reinterpret_cast<int*>(smem + A.scr_off + SCR_CMB + 4 * MAXG)[lane] = se < 0;
+            }
         }
     }
     const uint32_t lq = div_magic((uint32_t)lane, S.nc_m, S.nc_l);
@@ -1698,7 +1773,44 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
             }
             float v = (float)s;
             if (add) v = add[rg] + v;
-            y[rg] = v;
+            if (PM == PM_SEL && (cmb || swe))
+                reinterpret_cast<float*>(smem)[rho] = v;   // the x region is free now
+            else
+                y[rg] = v;
+        }
+    }
+    if (PM == PM_SEL && swe) {
+        // SwiGLU of one token's selections (stratum_engine.h:373-392, as
+        // kq_swiglu_kernel): parts 0..k-1 are the k ranks' gate slices,
+        // k..2k-1 their up slices; with the rows per part a multiple of G
+        // (the host checks) the workgroup holds rank r's gate and up row
+        // i = b + jG as its rows r * m + j and (k + r) * m + j.
+        __syncthreads();
+        const float* ov = reinterpret_cast<const float*>(smem);
+        const int m = S.pn / G, kr = S.nparts >> 1;
+        for (int t = tid; t < kr * m; t += T) {
+            const int r = t / m, j = t - r * m;
+            A.act[(size_t)r * S.pn + b + j * G] = swiglu1(ov[r * m + j], ov[(kr + r) * m + j]);
+        }
+    }
+    if (PM == PM_SEL && cmb) {
+        // The weighted accumulate in rank order plus the residual
+        // (stratum_arch_moe.inc.c:728-743; kq_moe_combine_kernel's
+        // arithmetic): part r is rank r of one token, and with the rows per
+        // part a multiple of G (the host checks) the workgroup holds every
+        // part's row i = b + jG as its row r * (pn / G) + j.
+        __syncthreads();
+        const float* ov = reinterpret_cast<const float*>(smem);
+        const float* cwt = reinterpret_cast<const float*>(smem + A.scr_off + SCR_CMB);
+        const int* skip = reinterpret_cast<const int*>(smem + A.scr_off + SCR_CMB + 4 * MAXG);
+        const int m = S.pn / G;                  // <= T (the host checks)
+        if (tid < m) {
+            float acc = 0.0f;
+            for (int r = 0; r < S.nparts; r++) {
+                if (skip[r]) continue;
+                acc = acc + cwt[r] * ov[r * m + tid];
+            }
+            A.cx[b + tid * G] = cres + acc;
         }
     }
     if (last_seg) return;
@@ -3634,6 +3746,10 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
         return (int)hipErrorInvalidValue;
     SegsArg A;
     A.nseg = nseg;
+    A.act = segs[0].act;
+    A.cx = segs[0].cx;
+    A.cw = segs[0].cw;
+    A.logits = segs[0].logits;
     A.xs_off = xs_off;
     A.terms_off = terms_off;
     A.scr_off = scr_off;
@@ -3686,6 +3802,24 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
     int nsel = 0;
     for (int i = 0; i < nseg; i++) nsel += segs[i].sel != nullptr;
     if (nsel && (nsel != nseg || t == 4 || t >= 8)) return (int)hipErrorInvalidValue;
+    // the MoE FFN step pieces: one selection segment; the combine needs
+    // equal parts whose rows are a multiple of the grid and its outputs in
+    // the x region; in-launch softmax needs every logit in a lane
+    const kqk_seg& h0 = segs[0];
+    if (h0.act || h0.cx || h0.logits) {
+        if (nseg != 1 || !h0.sel || t == 4 || t >= 8 || (h0.act && h0.cx))
+            return (int)hipErrorInvalidValue;
+        if (h0.act || h0.cx) {   // equal parts, rows a multiple of the grid, outputs in the x region
+            const int pn = h0.rows[0];
+            bool ok = pn % grid == 0 && (long)h0.nparts * (pn / grid) * 4 <= xs_off;
+            for (int p = 1; p < h0.nparts; p++) ok = ok && h0.rows[p] == pn;
+            if (h0.cx) ok = ok && h0.cw && pn / grid <= threads;
+            if (h0.act) ok = ok && !(h0.nparts & 1);
+            if (!ok) return (int)hipErrorInvalidValue;
+        }
+        if (h0.logits && (!h0.probs || ((h0.emax + 63) & ~63) > threads))
+            return (int)hipErrorInvalidValue;
+    }
     const segs_fn f = nsel ? k_segs_sel[nseg > 1][depth - 1][t] : k_segs[nseg > 1][depth - 1][t];
     hipLaunchKernelGGL(f, dim3(grid), dim3(threads), (size_t)lds_bytes, st, A);
     return (int)hipGetLastError();

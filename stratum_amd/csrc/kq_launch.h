@@ -30,6 +30,14 @@ typedef struct {
     const float* probs;      /* routed in the launch: top-ksel of probs[0..emax), */
     int* sel_out;            /* written by workgroup 0 to sel_out / selw_out */
     float* selw_out;
+    /* MoE FFN step pieces (first segment of a one-segment selection launch;
+     * zero: unused) */
+    int logits;              /* probs holds router logits: their softmax first */
+    float* act;              /* parts = k gate then k up slices of one token:
+                              * act[r][i] = SwiGLU(gate_r[i], up_r[i]) (no y written) */
+    float* cx;               /* parts = one token's ranks: cx[i] += the sum over parts r
+                              * with sel[r] >= 0, in order, of cw[r] * row i of part r */
+    const float* cw;         /*   (no y written) */
 } kqk_seg;
 #define KQK_LIST_MAX 4   /* parts of unequal sizes one launcher segment takes */
 long kqk_segs_lds(const kqk_seg* segs, int nseg, int grid, int* xs_off, int* terms_off,

@@ -52,7 +52,7 @@ typedef struct {
     uint8_t* d_mf; size_t cap_mf;   /* MFMA multi-x: x planes, sums, partials */
     /* launch overrides from the environment (0: unset), read by kq_ready
      * and again only by kq_tuning_reload: the planner runs on every call */
-    int env_grid, env_threads, env_depth, env_moe_group_launch;
+    int env_grid, env_threads, env_depth, env_moe_group_launch, env_ffn_split;
     int use_sdot;          /* host-pointer ABI: Q4_K / Q6_K in the int8 mode */
     char err[512];
 } kq_state;
@@ -123,6 +123,7 @@ int kq_tuning_reload(void) {
     g_kq.env_threads = t == 256 || t == 512 || t == 1024 ? t : 0;
     g_kq.env_depth = getenv("KQ_DEPTH") ? (d == 2 ? 2 : 1) : 0;
     g_kq.env_moe_group_launch = getenv("KQ_MOE_GROUP_LAUNCH") != NULL;
+    g_kq.env_ffn_split = getenv("KQ_MOE_FFN_SPLIT") != NULL;
     return 0;
 }
 
@@ -861,8 +862,14 @@ int kq_moe_topk_dev(const float* probs, int B, int E, int k, int* sel, float* se
  * read on the device, or (probs != NULL) routed in the launch itself: every
  * workgroup takes the top-k of probs and workgroup 0 writes it to sel and
  * selw. */
-static int moe_one_token(const kq_moe_op* op, const int* sel, int k, int E, const float* probs,
-                         float* selw, hipStream_t st) {
+/* One token: its k selections as the parts of one launch.  The FFN step's
+ * pieces (kq_moe_ffn_dev, batch 1), each instead of writing y: logits (probs
+ * holds router logits, their softmax taken in the launch), act (gate and
+ * up in one segment: act = SwiGLU(gate, up)), cx / cw (the ranks' outputs
+ * combined into cx). */
+static int moe_one_token_ffn(const kq_moe_op* op, const int* sel, int k, int E,
+                             const float* probs, float* selw, int logits, float* act, float* cx,
+                             const float* cw, hipStream_t st) {
     const int nt = op->ntensors;
     kqk_seg h[2];
     memset(h, 0, sizeof h);
@@ -889,9 +896,18 @@ static int moe_one_token(const kq_moe_op* op, const int* sel, int k, int E, cons
             g->probs = probs;
             g->sel_out = (int*)sel;
             g->selw_out = selw;
+            g->logits = logits;
         }
+        g->act = act;
+        g->cx = cx;
+        g->cw = cw;
     }
     return launch_segs(h, nh, st);
+}
+
+static int moe_one_token(const kq_moe_op* op, const int* sel, int k, int E, const float* probs,
+                         float* selw, hipStream_t st) {
+    return moe_one_token_ffn(op, sel, k, E, probs, selw, 0, NULL, NULL, NULL, st);
 }
 
 static int moe_check_op(const kq_moe_op* op, int k, int E, const char* who) {
@@ -1104,6 +1120,37 @@ int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* s
     float* act = (float*)(w8 + off[3]);
     float* ffo = (float*)(w8 + off[4]);
     const int H = f->n_embed, F = f->n_ff, E = f->n_experts, k = f->k;
+    const int pair = f->gate_type == f->up_type && f->gate_stride == f->up_stride;
+
+    /* One token in three launches: router logits; gate and up of the
+     * selected slices with the softmax and top-k taken in that launch and
+     * SwiGLU in its epilogue; down with the rank-ordered combine plus
+     * residual in its epilogue.  The same arithmetic as the six-launch form
+     * below (the tests hold the two bit-identical; KQ_MOE_FFN_SPLIT=1 forces
+     * that form).  Needs one gate+up segment (2k <= KQ_MAX_GROUPS), E <= 256
+     * (every logit in a lane), a core down type, and n_ff and n_embed
+     * multiples of the grid (a workgroup then holds a rank's gate and up
+     * row, and all k ranks' down rows, of the same index). */
+    if (B == 1 && pair && 2 * k <= KQ_MAX_GROUPS && E <= 256 && is_core(f->down_type) &&
+        F % plan_grid() == 0 && H % plan_grid() == 0 && !g_kq.env_ffn_split) {
+        if (kq_gemv_dev(f->router_type, f->router, xn, NULL, probs, E, H, stream)) return -1;
+        kq_moe_op gu;
+        memset(&gu, 0, sizeof gu);
+        gu.type = f->gate_type; gu.n_out = F; gu.k_in = H; gu.x = xn; gu.x_div = k;
+        gu.ntensors = 2;
+        gu.w[0] = f->gate; gu.y[0] = g;
+        gu.w[1] = f->up; gu.y[1] = u;
+        gu.expert_stride = f->gate_stride;
+        if (moe_check_op(&gu, k, E, who)) return -1;
+        hipStream_t st = pick(stream);
+        if (moe_one_token_ffn(&gu, sel, k, E, probs, selw, 1, act, NULL, NULL, st)) return -1;
+        kq_moe_op dn;
+        memset(&dn, 0, sizeof dn);
+        dn.type = f->down_type; dn.n_out = H; dn.k_in = F; dn.x = act; dn.x_div = 1;
+        dn.ntensors = 1; dn.w[0] = f->down; dn.y[0] = ffo; dn.expert_stride = f->down_stride;
+        if (moe_check_op(&dn, k, E, who)) return -1;
+        return moe_one_token_ffn(&dn, sel, k, E, NULL, NULL, 0, NULL, x, selw, st);
+    }
 
     /* router logits, softmax (stratum_arch_moe.inc.c:689-691, 1107-1121) */
     if (B == 1 ? kq_gemv_dev(f->router_type, f->router, xn, NULL, probs, E, H, stream)
@@ -1116,7 +1163,6 @@ int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* s
     kq_moe_op gu;
     memset(&gu, 0, sizeof gu);
     gu.type = f->gate_type; gu.n_out = F; gu.k_in = H; gu.x = xn; gu.x_div = k;
-    const int pair = f->gate_type == f->up_type && f->gate_stride == f->up_stride;
     gu.ntensors = pair ? 2 : 1;
     gu.w[0] = f->gate; gu.y[0] = g;
     gu.w[1] = pair ? f->up : NULL; gu.y[1] = pair ? u : NULL;

@@ -198,15 +198,19 @@ def run_step(d, xn, x0, B):
 
 
 @pytest.mark.parametrize("B", [1, 16])
-def test_moe_ffn_step_config(port, B):
+def test_moe_ffn_step_config(port, B, kq_env):
     """128 experts, top-8, hidden 2048, expert ffn 768, Q4_K
-    experts, F32 router."""
+    experts, F32 router.  Every stage's output is checked, so batch 1 runs
+    the six-launch form (KQ_MOE_FFN_SPLIT), whose intermediates the
+    three-launch form does not write; test_moe_ffn_fused_matches_split holds
+    the two bit-identical."""
     H, F, E, k = 2048, 768, 128, 8
     d = make_layer(H, F, E, k, 9500)
     r = synth.rng(9501 + B)
     xn = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
     x0 = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
     print(f"moe ffn step B={B}", flush=True)
+    kq_env(KQ_MOE_FFN_SPLIT=1)
     got = run_step(d, xn, x0, B)
     rb_in, rb_ff = synth.row_bytes(TYPE_Q4_K, H), synth.row_bytes(TYPE_Q4_K, F)
     # the router logits as the step computes them (the same dense kernel)
@@ -250,6 +254,39 @@ def test_moe_ffn_step_config(port, B):
     print(f"  end to end: max |x - x_oracle| {err:.3e} (largest FFN contribution {contrib:.3e})",
           flush=True)
     assert err <= 1e-4 * contrib
+
+
+@pytest.mark.parametrize("case", ["config", "q6k_down", "parts16", "grid37", "e512"])
+def test_moe_ffn_fused_matches_split(port, case, kq_env):
+    """Batch 1 in three launches (softmax and top-k inside the gate+up
+    launch and SwiGLU in its epilogue; the rank-ordered combine plus residual
+    in the down launch's epilogue) against the six-launch form: x, sel, selw
+    and the activations bit-identical, and x against the oracle.  grid37 (37
+    workgroups: the rows per part are not a multiple) and e512 (512 experts:
+    more than 256 logits) take the six-launch form inside kq_moe_ffn_dev and
+    must give the same bits too."""
+    H, F, E, k = {"config": (2048, 768, 128, 8), "q6k_down": (1024, 512, 64, 4),
+                  "parts16": (1024, 256, 32, 8), "grid37": (2048, 768, 128, 8),
+                  "e512": (1024, 256, 512, 4)}[case]
+    d = make_layer(H, F, E, k, 9700)
+    if case == "q6k_down":
+        d["down_type"] = 14
+        d["down"] = synth.tensor(14, E * H, F, 9704)
+        d["down_stride"] = H * synth.row_bytes(14, F)
+    r = synth.rng(9701)
+    xn, x0 = synth.gaussian(r, H), synth.gaussian(r, H)
+    if case == "grid37":
+        kq_env(KQ_GRID=37)
+    print(f"moe ffn fused vs split: {case}", flush=True)
+    fused = run_step(d, xn, x0, 1)
+    kq_env(KQ_MOE_FFN_SPLIT=1)
+    split = run_step(d, xn, x0, 1)
+    for n in ("sel", "selw", "act", "x"):
+        assert same_values(fused[n], split[n]), n
+    full = port.moe_ffn(d, xn, x0, 1)
+    assert np.array_equal(full["sel"], fused["sel"])
+    contrib = np.abs(full["x"] - x0).max()
+    assert np.abs(fused["x"] - full["x"]).max() <= 1e-4 * contrib
 
 
 def test_moe_ffn_step_f16_router_mixed_types(port):
