@@ -408,7 +408,11 @@ int64_t kq_moe_ffn_workspace_bytes(const kq_moe_ffn* f, int B);
  * steps as above.  No allocation: work is caller-provided device memory of
  * kq_moe_ffn_workspace_bytes.  B <= KQ_MOE_MAX_TOKENS, k <= KQ_MAX_GROUPS,
  * n_embed and n_ff multiples of 256.  Replaces the FFN half of
- * moe_forward_one_token / moe_forward_b after moe_rmsnorm. */
+ * moe_forward_one_token / moe_forward_b after moe_rmsnorm.  At B = 1 (gate
+ * and up of one type and stride, 2k <= KQ_MAX_GROUPS, n_experts <= 256,
+ * n_embed and n_ff multiples of the CU count) the step runs in three
+ * launches with the same results; the workspace then holds the
+ * activations but not the probabilities or the gate, up and down outputs. */
 int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* sel, float* selw,
                    void* work, int64_t work_bytes, kq_stream stream);
 
