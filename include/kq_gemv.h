@@ -109,11 +109,12 @@ const char* kq_last_error(void);
 
 /* Launch-shape overrides for tuning runs and tests: KQ_GRID (workgroups),
  * KQ_WG_THREADS (256, 512 or 1024 lanes), KQ_DEPTH (1 or 2 batches in
- * flight) and KQ_MOE_GROUP_LAUNCH (MoE batches grouped by a separate
- * launch).  The environment is read once, at the first call that touches
- * the device; this re-reads it.  Results never depend on these (the
- * reduction order is fixed by the row length), only the launch shape.  No
- * counterpart in the reference.  Returns 0. */
+ * flight; 2 only with at most 512 lanes), KQ_MOE_GROUP_LAUNCH (MoE batches
+ * grouped by a separate launch) and KQ_MOE_FFN_SPLIT (kq_moe_ffn_dev in its
+ * six-launch form at batch 1).  The environment is read once, at the first
+ * call that touches the device; this re-reads it.  Results never depend on
+ * these (the reduction order is fixed by the row length), only the launch
+ * shape.  No counterpart in the reference.  Returns 0. */
 int kq_tuning_reload(void);
 
 /* g_st.use_sdot for the host-pointer entry points (kq_linear_dispatch*,
