@@ -189,10 +189,29 @@ int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,
  * single-stream result (stratum_linear.h:963-966); this is the opt-in
  * dense-contraction path for large B.  x must be finite.  The workspace is
  * the library's, grown on the first call of a larger shape (hipMalloc /
- * hipFree, which synchronise the device): callers that cannot allocate use
+ * hipFree, which synchronise the device) unless reserved beforehand
+ * (kq_reserve_mfma_workspace); callers that cannot allocate at all use
  * kq_gemv_multix_mfma_noalloc_dev. */
 int kq_gemv_multix_mfma_dev(int type, const void* w, const float* xs, float* ys,
                             int B, int N, int K, kq_stream stream);
+
+/* Bytes of the library workspace kq_gemv_multix_mfma_dev uses for (type, B,
+ * N, K), or -1.  No counterpart in the reference. */
+int64_t kq_gemv_multix_mfma_workspace_bytes(int type, int B, int N, int K);
+
+/* Grows the library's matrix-core workspace to at least `bytes` now (one
+ * hipMalloc, which synchronises the device), so that later calls whose
+ * workspace fits allocate nothing: for callers that set up once and then
+ * enqueue only (graph capture of the calls, serving loops).  The workspace
+ * is never shrunk before kq_linear_shutdown.  No counterpart in the
+ * reference.  Returns 0, or -1 with a message. */
+int kq_reserve_mfma_workspace(int64_t bytes);
+
+/* Bytes of device scratch the library holds: the matrix-core workspace, the
+ * MoE grouping records and the host-pointer entry points' staging buffers
+ * (the uploads of kq_linear_init not included).  No counterpart in the
+ * reference. */
+int64_t kq_scratch_bytes(void);
 
 /* kq_gemv_multix_mfma_dev without any allocation: the same kernels and the
  * same results bit for bit, with the workspace (x planes, x sums and

@@ -56,7 +56,8 @@ EXPORTS = (
     "kq_moe_gemv_dev", "kq_gemv_multix_mfma_dev", "kq_moe_gemv_routed_dev",
     "kq_tuning_reload", "kq_gemv_multix_mfma_noalloc_dev", "kq_linear_set_sdot",
     "kq_quantize_x_q8_dev", "kq_softmax_dev", "kq_swiglu_dev", "kq_moe_combine_dev",
-    "kq_moe_ffn_workspace_bytes", "kq_moe_ffn_dev",
+    "kq_moe_ffn_workspace_bytes", "kq_moe_ffn_dev", "kq_gemv_multix_mfma_workspace_bytes",
+    "kq_reserve_mfma_workspace", "kq_scratch_bytes",
 )
 # include/kq_gguf.h (bound in stratum_amd/gguf.py)
 GGUF_EXPORTS = (
@@ -225,6 +226,11 @@ def lib() -> ctypes.CDLL:
     L.kq_gemv_multix_dev.argtypes = [I, P, P, P, I, I, I, P]
     L.kq_gemv_multix_mfma_dev.argtypes = [I, P, P, P, I, I, I, P]
     L.kq_gemv_multix_mfma_noalloc_dev.argtypes = [I, P, P, P, I, I, I, P]
+    L.kq_gemv_multix_mfma_workspace_bytes.argtypes = [I, I, I, I]
+    L.kq_gemv_multix_mfma_workspace_bytes.restype = ctypes.c_int64
+    L.kq_reserve_mfma_workspace.argtypes = [ctypes.c_int64]
+    L.kq_scratch_bytes.argtypes = []
+    L.kq_scratch_bytes.restype = ctypes.c_int64
     L.kq_dequant_dev.argtypes = [I, P, P, ctypes.c_int64, P]
     L.kq_linear_set_sdot.argtypes = [I]
     L.kq_softmax_dev.argtypes = [P, I, I, P]

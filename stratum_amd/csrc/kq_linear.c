@@ -589,20 +589,43 @@ static int mfma_launch(int type, const void* w, const float* xs, float* ys, int 
     return 0;
 }
 
+/* Grows the library's matrix-core workspace to at least `need` bytes. */
+static int mfma_reserve(size_t need) {
+    if (g_kq.cap_mf >= need) return 0;
+    if (g_kq.d_mf) (void)hipFree(g_kq.d_mf);
+    g_kq.d_mf = NULL;
+    g_kq.cap_mf = 0;
+    if (hip_ok(hipMalloc((void**)&g_kq.d_mf, need), "hipMalloc(mfma workspace)")) return -1;
+    g_kq.cap_mf = need;
+    return 0;
+}
+
 int kq_gemv_multix_mfma_dev(int type, const void* w, const float* xs, float* ys,
                             int B, int N, int K, kq_stream stream) {
     size_t o_xs, o_pt;
     const size_t need = mfma_prepare("kq_gemv_multix_mfma_dev", type, w, xs, ys, B, N, K,
                                      &o_xs, &o_pt);
-    if (!need) return -1;
-    if (g_kq.cap_mf < need) {
-        if (g_kq.d_mf) (void)hipFree(g_kq.d_mf);
-        g_kq.d_mf = NULL;
-        g_kq.cap_mf = 0;
-        if (hip_ok(hipMalloc((void**)&g_kq.d_mf, need), "hipMalloc(mfma workspace)")) return -1;
-        g_kq.cap_mf = need;
-    }
+    if (!need || mfma_reserve(need)) return -1;
     return mfma_launch(type, w, xs, ys, B, N, K, g_kq.d_mf, o_xs, o_pt, stream);
+}
+
+int64_t kq_gemv_multix_mfma_workspace_bytes(int type, int B, int N, int K) {
+    static const float dummy[4];
+    size_t o_xs, o_pt;
+    const size_t need = mfma_prepare("kq_gemv_multix_mfma_workspace_bytes", type, dummy,
+                                     dummy, (float*)dummy, B, N, K, &o_xs, &o_pt);
+    return need ? (int64_t)need : -1;
+}
+
+int kq_reserve_mfma_workspace(int64_t bytes) {
+    if (bytes < 0) return kq_fail("kq_reserve_mfma_workspace: bytes=%lld", (long long)bytes);
+    if (kq_ready()) return -1;
+    return mfma_reserve((size_t)bytes);
+}
+
+int64_t kq_scratch_bytes(void) {
+    return (int64_t)(g_kq.cap_mf + (g_kq.cap_moe + g_kq.cap_x + g_kq.cap_y + g_kq.cap_a) *
+                                       sizeof(float));
 }
 
 /* The same launch with its workspace in the library's static device

@@ -165,3 +165,26 @@ def test_mfma_repeatable_and_other_types_refused():
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     with pytest.raises(RuntimeError, match="no MFMA path"):
         run(K.gemv_multix_mfma_dev, 10, dw, xs, B, N, Kd)
+
+
+def test_mfma_reserved_workspace_allocates_nothing():
+    """kq_reserve_mfma_workspace grows the workspace once; calls whose
+    workspace fits (kq_gemv_multix_mfma_workspace_bytes) then leave the
+    library's scratch unchanged, with the same results as before."""
+    L = K.lib()
+    qtype, N, Kd = 12, 1000, 4096
+    need = {B: L.kq_gemv_multix_mfma_workspace_bytes(qtype, B, N, Kd) for B in (16, 40, 64)}
+    assert all(v > 0 for v in need.values()), need
+    assert L.kq_gemv_multix_mfma_workspace_bytes(10, 16, N, Kd) == -1
+    assert L.kq_reserve_mfma_workspace(max(need.values())) == 0
+    held = L.kq_scratch_bytes()
+    assert held >= max(need.values())
+    w = synth.tensor(qtype, N, Kd, 995)
+    dw = torch.from_numpy(w).cuda()
+    for B in (64, 16, 40):
+        xs = np.stack([synth.gaussian(synth.rng(996 + s), Kd) for s in range(B)])
+        a = run(K.gemv_multix_mfma_dev, qtype, dw, xs, B, N, Kd)
+        assert L.kq_scratch_bytes() == held, B
+        assert np.array_equal(a.view(np.uint32),
+                              run(K.gemv_multix_mfma_dev, qtype, dw, xs, B, N, Kd).view(np.uint32))
+    assert L.kq_reserve_mfma_workspace(-1) == -1
