@@ -3288,7 +3288,8 @@ __global__ __launch_bounds__(256) void kq_dequant_kernel(const uint8_t* __restri
 // [E i + 64 E m, +E) of step m (E = 4 for F32, 8 for F16: one 16-byte load,
 // a wave reads 1 KB of the row per step), summed in increasing m, and the
 // 64 lane sums are combined by a fixed butterfly: the order depends on K
-// only.  Rows go to waves w, w + 4G, ... of G workgroups of 256 lanes.
+// only.  Rows go to waves w, w + 4G, ... of G workgroups of 256 lanes
+// (G at most N / 4, rounded up).
 constexpr int T_F32 = 0, T_F16 = 1;
 constexpr int DENSE_XLDS_MAX = 16384;   // x staged in LDS up to this K
 
@@ -3329,8 +3330,19 @@ __global__ __launch_bounds__(256) void kq_dense_kernel(DenseArg a) {
     const int nb = min(SB, a.B - s0);
     const float* xg = a.x + (size_t)s0 * K;
     if (XLDS) {
-        for (int i = 4 * tid; i < nb * K; i += 1024)
-            *reinterpret_cast<float4*>(xl + i) = *reinterpret_cast<const float4*>(xg + i);
+        // eight loads in flight per lane before their stores; the index is
+        // clamped so the loads need no branch
+        const int n4 = nb * K / 4;
+        const float4* xg4 = reinterpret_cast<const float4*>(xg);
+        float4* xl4 = reinterpret_cast<float4*>(xl);
+        for (int i0 = tid; i0 < n4; i0 += 256 * 8) {
+            float4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = xg4[min(i0 + 256 * j, n4 - 1)];
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (i0 + 256 * j < n4) xl4[i0 + 256 * j] = v[j];
+        }
         __syncthreads();
     }
     const float* xs = XLDS ? xl : xg;
@@ -4172,10 +4184,16 @@ int kqk_launch_dense(int type, const void* w, const float* x, const float* add, 
     a.w = static_cast<const uint8_t*>(w);
     a.x = x; a.add = add; a.y = y; a.N = N; a.K = K; a.B = B;
     a.row_bytes = (long)K * (type == T_F32 ? 4 : 2);
-    const int sb = B == 1 ? 1 : DENSE_SB;
+    // DENSE_SB streams per wave share its weight loads, unless that leaves
+    // fewer than 8 waves per CU (a 128-row MoE router at B = 16: 256 waves
+    // of long serial chains); then one stream per wave
+    const long w8 = (long)N * ((B + DENSE_SB - 1) / DENSE_SB);
+    const int sb = B == 1 || w8 < 8L * 256 ? 1 : DENSE_SB;
     const bool lds = (long)sb * K <= DENSE_XLDS_MAX;
     const size_t shm = lds ? (size_t)sb * K * 4 : 0;
-    const dim3 g(grid, (B + sb - 1) / sb);
+    // a wave per row: no more workgroups than rows / 4 (each would stage x
+    // for nothing)
+    const dim3 g(grid < (N + 3) / 4 ? grid : (N + 3) / 4, (B + sb - 1) / sb);
 #define KQ_DENSE_GO(T_, L_, S_) hipLaunchKernelGGL((kq_dense_kernel<T_, L_, S_>), g, dim3(256), shm, st, a)
 #define KQ_DENSE_SB(S_)                                                              \
     if (type == T_F32) { if (lds) KQ_DENSE_GO(T_F32, true, S_); else KQ_DENSE_GO(T_F32, false, S_); } \

@@ -196,8 +196,11 @@ def test_segments_mixed_types_split(port):
 
 
 @pytest.mark.parametrize("qtype", NEW + DENSE)
-def test_multix_equals_single_stream(qtype):
-    N, Kd, B = 100, 1024, 5
+@pytest.mark.parametrize("N,Kd,B", [(100, 1024, 5), (2100, 512, 9)])
+def test_multix_equals_single_stream(qtype, N, Kd, B):
+    """Every stream bit-identical to its single-stream launch.  Dense rows:
+    the small shape runs one stream per wave, the large one eight streams
+    per wave sharing each weight load (the second group partial)."""
     w = synth.tensor(qtype, N, Kd, 700 + qtype)
     xs = np.stack([synth.gaussian(synth.rng(710 + s), Kd) for s in range(B)])
     dw, dx = dev(w), dev(xs.reshape(-1))
