@@ -432,7 +432,10 @@ int64_t kq_moe_ffn_workspace_bytes(const kq_moe_ffn* f, int B);
  * and up of one type and stride, 2k <= KQ_MAX_GROUPS, n_experts <= 256,
  * n_embed and n_ff multiples of the CU count) the step runs in three
  * launches with the same results; the workspace then holds the
- * activations but not the probabilities or the gate, up and down outputs. */
+ * activations but not the probabilities or the gate, up and down outputs.
+ * At B > 1 (core gate, up and down types) the grouped gate+up launch stores
+ * its expert-run tables in the workspace and the down launch loads them
+ * instead of grouping the selection again, with the same results. */
 int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* sel, float* selw,
                    void* work, int64_t work_bytes, kq_stream stream);
 

@@ -1964,6 +1964,12 @@ struct MxArg {
     int B, k;
     int* sel_out;
     float* selw_out;
+    // the runs as built (cnt, gid, ms, pl, rexp; [0] the run count):
+    // runs_out != nullptr: workgroup 0 stores them; runs_in != nullptr:
+    // every workgroup loads them instead of building (a later launch of the
+    // same selection, E, nm and run length)
+    int* runs_out;
+    const int* runs_in;
 };
 
 // LDS slot of the float4 at tile-relative x position pos (a multiple of 4;
@@ -2210,6 +2216,31 @@ struct MoeRuns {
         __syncthreads();
         return nd;
     }
+
+    // ints of the tables from cnt on, for nd runs
+    __device__ static int words(const MxArg& A, int nd) {
+        return ((2 * A.E + 3) & ~3) + 4 * ((A.nm + 3) >> 2) + A.nm + nd;
+    }
+    // workgroup 0, after build: the tables to runs_out (after their count)
+    __device__ void store(const MxArg& A, int nd) const {
+        const int n = words(A, nd);
+        for (int i = threadIdx.x; i < n; i += A.threads) A.runs_out[1 + i] = cnt[i];
+        if (threadIdx.x == 0) A.runs_out[0] = nd;
+    }
+    // instead of build: the tables a previous launch stored (no probs here)
+    __device__ int load(const MxArg& A, uint8_t* base) {
+        const int nm4 = (A.nm + 3) >> 2;
+        cnt = reinterpret_cast<int*>(base);
+        gid = cnt + A.E;
+        ms = cnt + ((2 * A.E + 3) & ~3);
+        pl = ms + 4 * nm4;
+        rexp = pl + A.nm;
+        const int nd = A.runs_in[0];
+        const int n = words(A, nd);
+        for (int i = threadIdx.x; i < n; i += A.threads) cnt[i] = A.runs_in[1 + i];
+        __syncthreads();
+        return nd;
+    }
 };
 
 template <int TYPE, int S, bool WHOLE>
@@ -2241,7 +2272,12 @@ __global__ __launch_bounds__(1024) void kq_mx_kernel(MxArg A) {
     MoeRuns mr;
     int nd = 1;
     const bool moe = A.nm > 0;                    // uniform: MoE runs built here
-    if (moe) nd = mr.build(A, flags, smem + A.grp_off);
+    if (moe && A.runs_in) {
+        nd = mr.load(A, smem + A.grp_off);
+    } else if (moe) {
+        nd = mr.build(A, flags, smem + A.grp_off);
+        if (A.runs_out && blockIdx.x == 0) mr.store(A, nd);
+    }
     const int ng = moe ? A.nt * nd : A.gdev ? *A.ngdev : 1;
     const int nitems = ng * A.nblk;
     // Workgroups are dispatched round robin over the 8 XCDs (each with its
@@ -3970,6 +4006,7 @@ int kqk_launch_mx(int type, const int* plan, long lds, int grid, const void* w, 
     a.gdev = static_cast<const MxGroup*>(gdev);
     a.ngdev = ngdev;
     a.X = X; a.Y = Y;
+    a.runs_out = nullptr; a.runs_in = nullptr;
     a.x_stride = x_stride; a.y_stride = y_stride;
     a.RB = plan[2]; a.nblk = plan[3];
     a.threads = plan[0]; a.grid = grid;
@@ -4010,6 +4047,10 @@ long kqk_mx_group_bytes(void) { return (long)sizeof(MxGroup); }
 
 // LDS bytes of the in-launch MoE runs (MoeRuns) for nm members, E experts
 // and at most ndmax runs; B > 0: routed in the launch for B tokens
+long kqk_moe_runs_words(int nm, int E, int ndmax) {
+    return 1 + ((2L * E + 3) & ~3L) + 4L * ((nm + 3) / 4) + nm + ndmax;
+}
+
 long kqk_moe_runs_lds(int nm, int E, int ndmax, int B) {
     const long E64 = (E + 63) & ~63L, nm4 = (nm + 3) / 4;
     return 4L * ((B > 0 ? B * E64 + 4 * nm4 : 0) + ((2L * E + 3) & ~3L) + 4 * nm4 + nm + ndmax);
@@ -4021,9 +4062,10 @@ long kqk_moe_runs_lds(int nm, int E, int ndmax, int B) {
 int kqk_launch_mx_moe(int type, const int* plan, long plan_lds, long lds, int grid, const int* sel,
                       int nm, int E, int nt, int x_div, const void* w0, const void* w1, float* y0,
                       float* y1, long estride, const float* X, int N, int K, const float* probs,
-                      int B, int k, int* sel_out, float* selw_out, hipStream_t st) {
+                      int B, int k, int* sel_out, float* selw_out, int* runs_out,
+                      const int* runs_in, hipStream_t st) {
     if (nm < 1 || E < 1 || E > 4096 || nt < 1 || nt > 2 || x_div < 1 || plan[7] < 1 ||
-        plan[7] > MX_MAXM || plan_lds < 0 || (plan_lds & 15) ||
+        plan[7] > MX_MAXM || plan_lds < 0 || (plan_lds & 15) || (runs_in && probs) ||
         (probs && (B < 1 || k < 1 || B * k != nm || !sel_out || !selw_out)) || (!probs && !sel))
         return (int)hipErrorInvalidValue;
     MxArg a;
@@ -4033,6 +4075,7 @@ int kqk_launch_mx_moe(int type, const int* plan, long plan_lds, long lds, int gr
     a.gdev = nullptr;
     a.ngdev = nullptr;
     a.X = X; a.Y = nullptr;
+    a.runs_out = runs_out; a.runs_in = runs_in;
     a.x_stride = K; a.y_stride = N;
     a.RB = plan[2]; a.nblk = plan[3];
     a.threads = plan[0]; a.grid = grid;

@@ -79,7 +79,11 @@ long kqk_moe_runs_lds(int nm, int E, int ndmax, int B);
 int kqk_launch_mx_moe(int type, const int* plan, long plan_lds, long lds, int grid, const int* sel,
                       int nm, int E, int nt, int x_div, const void* w0, const void* w1, float* y0,
                       float* y1, long estride, const float* X, int N, int K, const float* probs,
-                      int B, int k, int* sel_out, float* selw_out, hipStream_t st);
+                      int B, int k, int* sel_out, float* selw_out, int* runs_out,
+                      const int* runs_in, hipStream_t st);
+/* ints of a stored run table (count first) for nm members, E experts and
+ * at most ndmax runs */
+long kqk_moe_runs_words(int nm, int E, int ndmax);
 /* MFMA multi-x (Q4_K, Q6_K): workspace sizes for a launch over `grid`
  * workgroups, and the launch (the same grid) */
 int kqk_mfma_workspace(int type, int B, int N, int K, int grid, long* planes, long* xs, long* part);

@@ -963,8 +963,18 @@ static int moe_check_op(const kq_moe_op* op, int k, int E, const char* who) {
  * B = 16, E = 128 that took longer (114 us per layer) than the separate
  * top-k launch (104 us), so the in-launch ranking is kept to B E^2 <= 2^16
  * (E padded to 64). */
+/* Run tables of one selection shared by two grouped launches: out != NULL
+ * has the launch store the runs it builds (stored = 1, mch = its run
+ * length); in != NULL has a launch of the same run length load them
+ * instead of building. */
+typedef struct {
+    int* out;
+    const int* in;
+    int mch, stored;
+} moe_runs_io;
+
 static int moe_batch(const kq_moe_op* op, int* sel, const float* probs, float* selw, int B, int k,
-                     int E, hipStream_t st) {
+                     int E, moe_runs_io* io, hipStream_t st) {
     const long E64 = (E + 63) & ~63L;
     if (probs && (long)B * E64 * E64 > (1L << 16)) return 1;
     const int nt = op->ntensors;
@@ -979,11 +989,18 @@ static int moe_batch(const kq_moe_op* op, int* sel, const float* probs, float* s
                                 g_kq.lds_max - (int)rbytes - 16, plan);
         if (pl >= 0) {
             const long off = (pl + 15) & ~15L;
+            const int* rin = io && io->in && !probs && io->mch == plan[7] ? io->in : NULL;
+            int* rout = io && io->out && !rin ? io->out : NULL;
             const int e = kqk_launch_mx_moe(op->type, plan, off, off + rbytes, grid, sel, nm, E,
                                             nt, op->x_div, op->w[0], op->w[nt - 1], op->y[0],
                                             op->y[nt - 1], (long)op->expert_stride, op->x,
-                                            op->n_out, op->k_in, probs, B, k, sel, selw, st);
+                                            op->n_out, op->k_in, probs, B, k, sel, selw, rout,
+                                            rin, st);
             if (e) return kq_fail("moe gemv launch: %s", hipGetErrorString((hipError_t)e));
+            if (rout) {
+                io->stored = 1;
+                io->mch = plan[7];
+            }
             return 0;
         }
     }
@@ -1031,12 +1048,12 @@ int kq_moe_gemv_routed_dev(const kq_moe_op* op, const float* probs, int B, int k
         if (e) return kq_fail("moe topk launch: %s", hipGetErrorString((hipError_t)e));
         return moe_per_token(op, sel, B, k, E, st);
     }
-    const int r = moe_batch(op, sel, probs, selw, B, k, E, st);
+    const int r = moe_batch(op, sel, probs, selw, B, k, E, NULL, st);
     if (r <= 0) return r;
     /* the router weights do not fit beside the plan: route separately */
     const int e = kqk_launch_moe_topk(probs, B, E, k, sel, selw, st);
     if (e) return kq_fail("moe topk launch: %s", hipGetErrorString((hipError_t)e));
-    return moe_batch(op, sel, NULL, NULL, B, k, E, st);
+    return moe_batch(op, sel, NULL, NULL, B, k, E, NULL, st);
 }
 
 int kq_moe_gemv_dev(const kq_moe_op* op, const int* sel, int B, int k, int E, kq_stream stream) {
@@ -1048,7 +1065,7 @@ int kq_moe_gemv_dev(const kq_moe_op* op, const int* sel, int B, int k, int E, kq
     hipStream_t st = pick(stream);
     if (B == 1) return moe_one_token(op, sel, k, E, NULL, NULL, st);
     if (!is_core(op->type)) return moe_per_token(op, sel, B, k, E, st);
-    return moe_batch(op, (int*)sel, NULL, NULL, B, k, E, st);
+    return moe_batch(op, (int*)sel, NULL, NULL, B, k, E, NULL, st);
 }
 
 /* ------------------------------------------------------ MoE FFN step */
@@ -1088,13 +1105,15 @@ int kq_moe_combine_dev(const float* o, const int* sel, const float* selw, const 
 }
 
 /* workspace of one step: probs B x E, g / u / act B*k x F, down outputs
- * B*k x H, each 256-byte aligned */
-static int64_t ffn_layout(const kq_moe_ffn* f, int B, int64_t off[5]) {
+ * B*k x H, the run tables of the batch launches, each 256-byte aligned */
+static int64_t ffn_layout(const kq_moe_ffn* f, int B, int64_t off[6]) {
     const int64_t bk = (int64_t)B * f->k;
-    const int64_t sz[5] = {(int64_t)B * f->n_experts * 4, bk * f->n_ff * 4, bk * f->n_ff * 4,
-                           bk * f->n_ff * 4, bk * f->n_embed * 4};
+    const int dmax = f->n_experts < bk ? f->n_experts : (int)bk;
+    const int64_t sz[6] = {(int64_t)B * f->n_experts * 4, bk * f->n_ff * 4, bk * f->n_ff * 4,
+                           bk * f->n_ff * 4, bk * f->n_embed * 4,
+                           4 * kqk_moe_runs_words((int)bk, f->n_experts, dmax + (int)bk)};
     int64_t t = 0;
-    for (int i = 0; i < 5; i++) {
+    for (int i = 0; i < 6; i++) {
         off[i] = t;
         t += (sz[i] + 255) & ~(int64_t)255;
     }
@@ -1115,7 +1134,7 @@ static int ffn_check(const kq_moe_ffn* f, int B, const char* who) {
 
 int64_t kq_moe_ffn_workspace_bytes(const kq_moe_ffn* f, int B) {
     if (ffn_check(f, B, "kq_moe_ffn_workspace_bytes")) return -1;
-    int64_t off[5];
+    int64_t off[6];
     return ffn_layout(f, B, off);
 }
 
@@ -1131,7 +1150,7 @@ int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* s
     if (!xn || !x || !sel || !selw || !work) return kq_fail("%s: NULL pointer", who);
     if (((uintptr_t)xn | (uintptr_t)x | (uintptr_t)work) & 15)
         return kq_fail("%s: xn, x and work must be 16-byte aligned", who);
-    int64_t off[5];
+    int64_t off[6];
     const int64_t need = ffn_layout(f, B, off);
     if (work_bytes < need)
         return kq_fail("%s: workspace of %lld bytes, %lld needed", who, (long long)work_bytes,
@@ -1142,6 +1161,7 @@ int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* s
     float* u = (float*)(w8 + off[2]);
     float* act = (float*)(w8 + off[3]);
     float* ffo = (float*)(w8 + off[4]);
+    moe_runs_io rio = {(int*)(w8 + off[5]), NULL, 0, 0};
     const int H = f->n_embed, F = f->n_ff, E = f->n_experts, k = f->k;
     const int pair = f->gate_type == f->up_type && f->gate_stride == f->up_stride;
 
@@ -1190,7 +1210,23 @@ int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* s
     gu.w[0] = f->gate; gu.y[0] = g;
     gu.w[1] = pair ? f->up : NULL; gu.y[1] = pair ? u : NULL;
     gu.expert_stride = f->gate_stride;
-    if (E <= 1024) {
+    const int share = B > 1 && is_core(f->gate_type) && is_core(f->down_type) && E <= 1024 &&
+                      !g_kq.env_ffn_split;
+    if (share) {
+        /* a batch: the grouped gate+up launch stores its run tables for the
+         * down launch (routed inside it when that fits, else after a top-k
+         * launch) */
+        hipStream_t st = pick(stream);
+        if (moe_check_op(&gu, k, E, who)) return -1;
+        int r = moe_batch(&gu, sel, probs, selw, B, k, E, &rio, st);
+        if (r == 1) {
+            const int e = kqk_launch_moe_topk(probs, B, E, k, sel, selw, st);
+            if (e) return kq_fail("moe topk launch: %s", hipGetErrorString((hipError_t)e));
+            r = moe_batch(&gu, sel, NULL, NULL, B, k, E, &rio, st);
+        }
+        if (r < 0) return -1;
+        if (r > 0 && kq_moe_gemv_dev(&gu, sel, B, k, E, stream)) return -1;
+    } else if (E <= 1024) {
         if (kq_moe_gemv_routed_dev(&gu, probs, B, k, E, sel, selw, stream)) return -1;
     } else {
         if (kq_moe_topk_dev(probs, B, E, k, sel, selw, stream) ||
@@ -1211,7 +1247,17 @@ int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* s
     memset(&dn, 0, sizeof dn);
     dn.type = f->down_type; dn.n_out = H; dn.k_in = F; dn.x = act; dn.x_div = 1;
     dn.ntensors = 1; dn.w[0] = f->down; dn.y[0] = ffo; dn.expert_stride = f->down_stride;
-    if (kq_moe_gemv_dev(&dn, sel, B, k, E, stream)) return -1;
+    if (share && rio.stored) {
+        /* the gate+up launch's run tables, when the down plan cuts runs alike */
+        rio.in = rio.out;
+        rio.out = NULL;
+        if (moe_check_op(&dn, k, E, who)) return -1;
+        const int r = moe_batch(&dn, sel, NULL, NULL, B, k, E, &rio, pick(stream));
+        if (r < 0) return -1;
+        if (r > 0 && kq_moe_gemv_dev(&dn, sel, B, k, E, stream)) return -1;
+    } else if (kq_moe_gemv_dev(&dn, sel, B, k, E, stream)) {
+        return -1;
+    }
     return kq_moe_combine_dev(ffo, sel, selw, x, x, B, k, H, stream);
 }
 

@@ -289,6 +289,33 @@ def test_moe_ffn_fused_matches_split(port, case, kq_env):
     assert np.abs(fused["x"] - full["x"]).max() <= 1e-4 * contrib
 
 
+@pytest.mark.parametrize("case", ["config_b16", "routed_b4"])
+def test_moe_ffn_batch_shared_runs_match_split(port, case, kq_env):
+    """B > 1: the grouped gate+up launch stores its expert-run tables and
+    the down launch loads them instead of grouping the selection again.
+    config_b16 routes in a top-k launch first; routed_b4 (B E^2 <= 2^16)
+    inside the gate+up launch.  Every output (gate, up, activations, down
+    outputs, x, sel, selw) is bit-identical to the split form's
+    (KQ_MOE_FFN_SPLIT, where each launch groups for itself), and x agrees
+    with the oracle."""
+    B, H, F, E, k = {"config_b16": (16, 2048, 768, 128, 8),
+                     "routed_b4": (4, 1024, 512, 64, 4)}[case]
+    d = make_layer(H, F, E, k, 9800)
+    r = synth.rng(9801)
+    xn = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
+    x0 = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
+    print(f"moe ffn batch shared run tables vs split: {case}", flush=True)
+    fused = run_step(d, xn, x0, B)
+    kq_env(KQ_MOE_FFN_SPLIT=1)
+    split = run_step(d, xn, x0, B)
+    for n in ("sel", "selw", "g", "u", "act", "ffo", "x"):
+        assert same_values(fused[n], split[n]), n
+    full = port.moe_ffn(d, xn, x0, B)
+    assert np.array_equal(full["sel"], fused["sel"])
+    contrib = np.abs(full["x"] - x0).max()
+    assert np.abs(fused["x"] - full["x"]).max() <= 1e-4 * contrib
+
+
 def test_moe_ffn_step_f16_router_mixed_types(port):
     """An F16 router and gate/up/down of different types (Q4_K gate/up,
     Q6_K down): gate and up still share one routed launch, down has its
