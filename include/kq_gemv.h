@@ -111,7 +111,7 @@ const char* kq_last_error(void);
  * KQ_WG_THREADS (256, 512 or 1024 lanes), KQ_DEPTH (1 or 2 batches in
  * flight; 2 only with at most 512 lanes), KQ_MOE_GROUP_LAUNCH (MoE batches
  * grouped by a separate launch) and KQ_MOE_FFN_SPLIT (kq_moe_ffn_dev in its
- * six-launch form at batch 1).  The environment is read once, at the first
+ * six-launch form at batch 1, and without shared run tables at B > 1).  The environment is read once, at the first
  * call that touches the device; this re-reads it.  Results never depend on
  * these (the reduction order is fixed by the row length), only the launch
  * shape.  No counterpart in the reference.  Returns 0. */
