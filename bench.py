@@ -443,50 +443,76 @@ def cfg4(L, torch, stream, host_w) -> dict:
 def cfg5(L, torch, stream, host_w) -> dict:
     """MoE gather, 128 experts, top-8, hidden 2048, expert ffn
     768, Q4_K; a step is top-k on the device, gate+up, down (batch 1: the
-    top-k inside the gate+up launch, kq_moe_gemv_routed_dev)."""
+    top-k inside the gate+up launch, kq_moe_gemv_routed_dev).
+
+    Past the MALL: the selected slices change from step to step.  Step i
+    takes routing set i % MOE_SETS on weight copy (i // MOE_SETS) % 3: at
+    batch 1 the sets select disjoint experts (set j: experts 8j .. 8j+7,
+    by logits raised by 10), at batch 16 they are independent N(0,1)
+    logits.  One rotation then reads 48 x 21 MB = 1 GB (batch 1) or about
+    3 x 16 x 215 MB (batch 16) of distinct slices, 4x the 256 MB MALL.  The
+    FFN step routes from its own router GEMV, so it cycles MOE_SETS
+    different normed inputs the same way."""
     sh = stream.cuda_stream
     E, H, F, k = 128, 2048, 768, 8
+    MOE_SETS, NCOPY = 16, 3
     rbg, rbd = L.kq_row_bytes(12, H), L.kq_row_bytes(12, F)
     gsl, dsl = F * rbg, H * rbd
     ex = [synth.tensor(12, E * F, H, 3700), synth.tensor(12, E * F, H, 3701),
           synth.tensor(12, E * H, F, 3702)]
     stacked = np.concatenate(ex)
-    cm = _copies(torch, stacked, 2)
+    cm = _copies(torch, stacked, NCOPY)[:NCOPY]
+    from oracle import oracle as O
+    port = O.port()
     res = {}
     for B in (1, 16):
         r = np.random.default_rng(3800 + B)
-        lg = r.standard_normal((B, E)).astype(np.float32)
-        p = np.exp(lg - lg.max(1, keepdims=True))
-        probs = torch.from_numpy((p / p.sum(1, keepdims=True)).astype(np.float32)).cuda()
-        xmh = np.stack([synth.gaussian(r, H) for _ in range(B)])
+        lg = r.standard_normal((MOE_SETS, B, E)).astype(np.float32)
+        if B == 1:
+            for j in range(MOE_SETS):
+                lg[j, 0, 8 * j:8 * j + 8] += 10.0
+        p = np.exp(lg - lg.max(2, keepdims=True))
+        ph = (p / p.sum(2, keepdims=True)).astype(np.float32)
+        probs = torch.from_numpy(ph.reshape(-1)).cuda()
+        xmh = np.stack([synth.gaussian(r, H) for _ in range(MOE_SETS * B)])
         acth = np.stack([synth.gaussian(r, F) for _ in range(B * k)])
-        xm = torch.from_numpy(xmh).cuda()
+        xm = torch.from_numpy(xmh.reshape(-1)).cuda()
         act = torch.from_numpy(acth).cuda()
         sel = torch.empty(B * k, dtype=torch.int32, device="cuda")
         selw = torch.empty(B * k, dtype=torch.float32, device="cuda")
         yg, yu = (torch.empty(B * k * F, device="cuda") for _ in range(2))
         yd = torch.empty(B * k * H, device="cuda")
+        # the experts each routing set selects (moe_topk per token)
+        sets = [sorted({e for s in range(B) for e in port.topk(ph[j, s], k)[0]})
+                for j in range(MOE_SETS)]
+        distinct = float(np.mean([len(t) for t in sets]))
         ops = []
         for c in cm:
             base = c.data_ptr()
-            ops.append((KQ.moe_op(12, F, H, [base, base + E * gsl], gsl, xm.data_ptr(), k,
-                                  [yg.data_ptr(), yu.data_ptr()]),
-                        KQ.moe_op(12, H, F, [base + 2 * E * gsl], dsl, act.data_ptr(), 1,
-                                  [yd.data_ptr()])))
+            ops.append([(KQ.moe_op(12, F, H, [base, base + E * gsl], gsl,
+                                   xm.data_ptr() + 4 * j * B * H, k,
+                                   [yg.data_ptr(), yu.data_ptr()]),
+                         KQ.moe_op(12, H, F, [base + 2 * E * gsl], dsl, act.data_ptr(), 1,
+                                   [yd.data_ptr()]))
+                        for j in range(MOE_SETS)])
 
         def moe_step(i):
-            gu, dn = ops[i % len(ops)]
+            j = i % MOE_SETS
+            gu, dn = ops[(i // MOE_SETS) % NCOPY][j]
             # routed inside the gate+up launch
-            _check(L, L.kq_moe_gemv_routed_dev(ctypes.byref(gu), probs.data_ptr(), B, k, E,
-                                               sel.data_ptr(), selw.data_ptr(), sh))
+            _check(L, L.kq_moe_gemv_routed_dev(ctypes.byref(gu), probs.data_ptr() + 4 * j * B * E,
+                                               B, k, E, sel.data_ptr(), selw.data_ptr(), sh))
             _check(L, L.kq_moe_gemv_dev(ctypes.byref(dn), sel.data_ptr(), B, k, E, sh))
-        us = _events_us(torch, stream, moe_step, 50)
-        distinct = len(set(sel.cpu().numpy().tolist()))
+        us = _events_us(torch, stream, moe_step, 2 * MOE_SETS * NCOPY)
         nb = distinct * (2 * gsl + dsl) + 4 * (B * H + 2 * B * k * F + B * k * F + B * k * H)
-        res[f"B{B}"] = {"us_per_layer": round(us, 2), "distinct_experts": distinct,
-                        "bytes": nb, "GB/s": round(nb / us / 1e3, 1),
+        per_rot = sum(len(t) for t in sets) * NCOPY * (2 * gsl + dsl)
+        res[f"B{B}"] = {"us_per_layer": round(us, 2), "distinct_experts": round(distinct, 2),
+                        "bytes": int(nb), "GB/s": round(nb / us / 1e3, 1),
                         "launches": 2 if B * ((E + 63) // 64 * 64) ** 2 <= 1 << 16 else 3,
-                        "route": "kq_moe_gemv_routed_dev"}
+                        "route": "kq_moe_gemv_routed_dev",
+                        "rotation": f"{MOE_SETS} routing sets x {NCOPY} weight copies: "
+                                    f"{per_rot / 2 ** 20:.0f} MiB of selected slices per "
+                                    "rotation"}
         # the whole expert FFN step (kq_moe_ffn_dev): F32 router GEMV, softmax,
         # routed gate+up, SwiGLU, down, rank-ordered combine + residual
         router = torch.from_numpy(synth.tensor(KQ.TYPE_F32, E, H, 3703)).cuda()
@@ -504,26 +530,26 @@ def cfg5(L, torch, stream, host_w) -> dict:
         xres = torch.from_numpy(np.stack([synth.gaussian(r, H) for _ in range(B)])).cuda()
 
         def ffn_step(i):
-            _check(L, L.kq_moe_ffn_dev(ctypes.byref(ffns[i % len(ffns)]), xm.data_ptr(),
-                                       xres.data_ptr(), B, sel.data_ptr(), selw.data_ptr(),
-                                       work.data_ptr(), wbytes, sh))
-        fus = _events_us(torch, stream, ffn_step, 50)
+            j = i % MOE_SETS
+            _check(L, L.kq_moe_ffn_dev(ctypes.byref(ffns[(i // MOE_SETS) % NCOPY]),
+                                       xm.data_ptr() + 4 * j * B * H, xres.data_ptr(), B,
+                                       sel.data_ptr(), selw.data_ptr(), work.data_ptr(), wbytes,
+                                       sh))
+        fus = _events_us(torch, stream, ffn_step, 2 * MOE_SETS * NCOPY)
         res[f"B{B}"]["ffn_step"] = {
             "us_per_layer": round(fus, 2),
             "what": "router GEMV (F32 128x2048), softmax, routed gate+up, SwiGLU, down, "
-                    "combine + residual"}
+                    f"combine + residual; {MOE_SETS} normed inputs x {NCOPY} weight copies"}
         del work, router
         if CPU["on"]:
-            from oracle import oracle as O
             impl, kind = cpu_impl(12)
             rb = (rbg, rbg, rbd)
             sl = (gsl, gsl, dsl)
-            selh = sel.cpu().numpy()
-            pr = probs.cpu().numpy()
+            pr = ph[0]
 
             def cpu_layer():
                 for s in range(B):            # moe_topk per token, then the selected slices
-                    es, _ = O.port().topk(pr[s], k)
+                    es, _ = port.topk(pr[s], k)
                     for rr, e in enumerate(es):
                         m = s * k + rr
                         for ti, (nout, kin, xv) in enumerate(((F, H, xmh[s]), (F, H, xmh[s]),
@@ -531,7 +557,6 @@ def cfg5(L, torch, stream, host_w) -> dict:
                             off = e * sl[ti]
                             impl.gemv(12, ex[ti][off:off + nout * rb[ti]], xv, nout, kin,
                                       threads=host_cores())
-            del selh
             res[f"B{B}"]["cpu"] = cpu_entry(cpu_us(cpu_layer, min_s=0.2, max_n=10), kind,
                                             "top-k and the selected gate, up and down slices")
     del cm

@@ -435,9 +435,24 @@ int64_t kq_moe_ffn_workspace_bytes(const kq_moe_ffn* f, int B);
  * activations but not the probabilities or the gate, up and down outputs.
  * At B > 1 (core gate, up and down types) the grouped gate+up launch stores
  * its expert-run tables in the workspace and the down launch loads them
- * instead of grouping the selection again, with the same results. */
+ * instead of grouping the selection again, with the same results.  Where
+ * a launch groups the selection in a launch of its own (run tables too
+ * large for LDS, or KQ_MOE_GROUP_LAUNCH), the group records also go to the
+ * workspace: the step never touches the library's scratch. */
 int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* sel, float* selw,
                    void* work, int64_t work_bytes, kq_stream stream);
+
+/* What the last kq_moe_ffn_dev call ran, as bits (0 after a failure):
+ * KQ_FFN_FUSED_B1 the three-launch batch-1 form; KQ_FFN_RUNS_STORED the
+ * gate+up launch stored its run tables; KQ_FFN_RUNS_LOADED a later launch
+ * loaded them; KQ_FFN_GROUP_LAUNCH a separate grouping launch wrote its
+ * records to the workspace.  No counterpart in the reference: for callers
+ * and tests that check which form a layer shape takes. */
+#define KQ_FFN_FUSED_B1 1
+#define KQ_FFN_RUNS_STORED 2
+#define KQ_FFN_RUNS_LOADED 4
+#define KQ_FFN_GROUP_LAUNCH 8
+int kq_moe_ffn_last_path(void);
 
 #ifdef __cplusplus
 }

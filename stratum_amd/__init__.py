@@ -57,7 +57,7 @@ EXPORTS = (
     "kq_tuning_reload", "kq_gemv_multix_mfma_noalloc_dev", "kq_linear_set_sdot",
     "kq_quantize_x_q8_dev", "kq_softmax_dev", "kq_swiglu_dev", "kq_moe_combine_dev",
     "kq_moe_ffn_workspace_bytes", "kq_moe_ffn_dev", "kq_gemv_multix_mfma_workspace_bytes",
-    "kq_reserve_mfma_workspace", "kq_scratch_bytes",
+    "kq_reserve_mfma_workspace", "kq_scratch_bytes", "kq_moe_ffn_last_path",
 )
 # include/kq_gguf.h (bound in stratum_amd/gguf.py)
 GGUF_EXPORTS = (
@@ -239,6 +239,7 @@ def lib() -> ctypes.CDLL:
     L.kq_moe_ffn_workspace_bytes.argtypes = [ctypes.POINTER(KqMoeFfn), I]
     L.kq_moe_ffn_workspace_bytes.restype = ctypes.c_int64
     L.kq_moe_ffn_dev.argtypes = [ctypes.POINTER(KqMoeFfn), P, P, I, P, P, P, ctypes.c_int64, P]
+    L.kq_moe_ffn_last_path.argtypes = []
     L.kq_quantize_x_q8_dev.argtypes = [P, I, I, P, P, P, P]
     L.kq_gemv_segments_dev.argtypes = [ctypes.POINTER(KqSegment), I, P]
     L.kq_row_bytes.argtypes = [I, I]
@@ -445,9 +446,14 @@ def moe_ffn_workspace_bytes(f: KqMoeFfn, B: int) -> int:
     return n
 
 
+# kq_moe_ffn_last_path bits (include/kq_gemv.h)
+FFN_FUSED_B1, FFN_RUNS_STORED, FFN_RUNS_LOADED, FFN_GROUP_LAUNCH = 1, 2, 4, 8
+
+
 def moe_ffn_workspace_offsets(f: KqMoeFfn, B: int) -> dict:
-    """Offsets of probs, g, u, act and ffo in the step's workspace (the
-    layout kq_moe_ffn_dev uses: in that order, each 256-byte aligned)."""
+    """Offsets of probs, g, u, act, ffo and the run tables ("runs") in the
+    step's workspace (the layout kq_moe_ffn_dev uses: in that order, each
+    256-byte aligned; the grouping records follow the run tables)."""
     bk = B * f.k
     sizes = [("probs", B * f.n_experts * 4), ("g", bk * f.n_ff * 4), ("u", bk * f.n_ff * 4),
              ("act", bk * f.n_ff * 4), ("ffo", bk * f.n_embed * 4)]
@@ -455,7 +461,13 @@ def moe_ffn_workspace_offsets(f: KqMoeFfn, B: int) -> dict:
     for name, n in sizes:
         out[name] = t
         t += (n + 255) // 256 * 256
+    out["runs"] = t
     return out
+
+
+def moe_ffn_last_path() -> int:
+    """What the last kq_moe_ffn_dev call ran (FFN_* bits)."""
+    return int(lib().kq_moe_ffn_last_path())
 
 
 def moe_ffn_dev(f: KqMoeFfn, xn_ptr: int, x_ptr: int, B: int, sel_ptr: int, selw_ptr: int,

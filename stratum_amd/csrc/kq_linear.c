@@ -344,6 +344,13 @@ static int max_rows_per_launch(const kqk_seg* proto) {
 
 static hipStream_t pick(kq_stream s) { return (hipStream_t)s; }
 
+/* whether one segment fits one launch's LDS */
+static int seg_fits(const kqk_seg* g) {
+    int a, b, c;
+    const long l = kqk_segs_lds(g, 1, plan_grid(), &a, &b, &c);
+    return l > 0 && l <= g_kq.lds_max;
+}
+
 static int check_shape(int type, int N, int K) {
     if (!block_bytes(type)) return kq_fail("unsupported type %d", type);
     if (N <= 0 || K <= 0 || K % 256) return kq_fail("bad shape N=%d K=%d (K %% 256 must be 0)", N, K);
@@ -570,6 +577,7 @@ static size_t mfma_prepare(const char* who, int type, const void* w, const float
     if (B < 1) { kq_fail("%s: B=%d", who, B); return 0; }
     if (check_shape(type, N, K) || kq_ready()) return 0;
     if (!w || !xs || !ys) { kq_fail("%s: NULL pointer", who); return 0; }
+    if ((uintptr_t)xs & 15) { kq_fail("%s: xs must be 16-byte aligned", who); return 0; }
     long pl, xsb, pt;
     if (kqk_mfma_workspace(type, B, N, K, g_kq.n_cu, &pl, &xsb, &pt)) {
         kq_fail("%s: bad shape", who);
@@ -925,7 +933,51 @@ static int moe_one_token_ffn(const kq_moe_op* op, const int* sel, int k, int E,
         g->cx = cx;
         g->cw = cw;
     }
-    return launch_segs(h, nh, st);
+    int fit = 1;
+    for (int i = 0; i < nh; i++) fit = fit && seg_fits(&h[i]);
+    if (fit || act || cx) return launch_segs(h, nh, st);   /* the fused forms: checked by the caller */
+    /* A segment too large for LDS (k per-part x of a long row, or many
+     * rows per workgroup): its parts go in several segments of m parts, m
+     * a divisor of k, so each sub-segment's parts are consecutive ranks of
+     * one tensor (part i uses sel[q0 + i]).  Routed in the launch, the
+     * top-k is taken by a launch of its own first. */
+    if (probs) {
+        const int e = kqk_launch_moe_topk(probs, 1, E, k, (int*)sel, selw, st);
+        if (e) return kq_fail("moe topk launch: %s", hipGetErrorString((hipError_t)e));
+    }
+    kqk_seg out[KQ_MAX_SEGMENTS];
+    int no = 0;
+    for (int i = 0; i < nh; i++) {
+        kqk_seg g = h[i];
+        g.probs = NULL; g.sel_out = NULL; g.selw_out = NULL; g.logits = 0;
+        int m = k;
+        for (; m > 1; m--) {
+            if (k % m) continue;
+            kqk_seg t = g;
+            t.nparts = m;
+            if (seg_fits(&t)) break;
+        }
+        for (int q0 = 0; q0 < g.nparts; q0 += m) {
+            kqk_seg t;
+            memset(&t, 0, sizeof t);
+            for (int p = 0; p < m; p++) {
+                t.w[p] = g.w[q0 + p];
+                t.y[p] = g.y[q0 + p];
+                t.rows[p] = g.rows[q0 + p];
+            }
+            t.type = g.type; t.K = g.K; t.nparts = m;
+            t.x = g.x_stride ? g.x + (size_t)q0 * g.x_stride : g.x;
+            t.x_stride = m > 1 ? g.x_stride : 0;
+            t.sel = sel + q0 % k;
+            t.estride = g.estride; t.ksel = m; t.emax = g.emax;
+            out[no++] = t;
+            if (no == KQ_MAX_SEGMENTS) {
+                if (launch_segs(out, no, st)) return -1;
+                no = 0;
+            }
+        }
+    }
+    return no ? launch_segs(out, no, st) : 0;
 }
 
 static int moe_one_token(const kq_moe_op* op, const int* sel, int k, int E, const float* probs,
@@ -971,7 +1023,22 @@ typedef struct {
     int* out;
     const int* in;
     int mch, stored;
+    /* where the grouping launch writes its records and their count (the
+     * fallback when the runs are not built in the multi-x launch); NULL:
+     * the library's scratch, grown on demand */
+    void* grp;
+    size_t grp_bytes;
+    int grp_used;          /* set when the grouping launch ran */
+    int runs_loaded;       /* set when a launch loaded the stored tables */
 } moe_runs_io;
+
+/* Bytes of the grouping launch's records and count for nt tensors, nm
+ * members over E experts cut into runs of at most mch members. */
+static size_t moe_group_bytes(int nt, int nm, int E, int mch) {
+    const int dmax = E < nm ? E : nm;
+    const long ngmax = (long)nt * (dmax + (nm + mch - 1) / mch);
+    return (size_t)ngmax * (size_t)kqk_mx_group_bytes() + 64;
+}
 
 static int moe_batch(const kq_moe_op* op, int* sel, const float* probs, float* selw, int B, int k,
                      int E, moe_runs_io* io, hipStream_t st) {
@@ -1001,6 +1068,7 @@ static int moe_batch(const kq_moe_op* op, int* sel, const float* probs, float* s
                 io->stored = 1;
                 io->mch = plan[7];
             }
+            if (rin) io->runs_loaded = 1;
             return 0;
         }
     }
@@ -1011,9 +1079,20 @@ static int moe_batch(const kq_moe_op* op, int* sel, const float* probs, float* s
     const int mch = plan[7];
     const int ngmax = nt * (dmax + (nm + mch - 1) / mch);
     const size_t gbytes = (size_t)kqk_mx_group_bytes();
-    if (grow(&g_kq.d_moe, &g_kq.cap_moe, (ngmax * gbytes + 64) / sizeof(float) + 1)) return -1;
-    void* groups = g_kq.d_moe;
-    int* ng = (int*)((uint8_t*)g_kq.d_moe + ngmax * gbytes);
+    const size_t need = moe_group_bytes(nt, nm, E, mch);
+    uint8_t* gbase;
+    if (io && io->grp) {           /* the caller's workspace: no allocation */
+        if (need > io->grp_bytes)
+            return kq_fail("moe grouping: %zu bytes of group records, %zu in the workspace", need,
+                           io->grp_bytes);
+        gbase = (uint8_t*)io->grp;
+        io->grp_used = 1;
+    } else {
+        if (grow(&g_kq.d_moe, &g_kq.cap_moe, need / sizeof(float) + 1)) return -1;
+        gbase = (uint8_t*)g_kq.d_moe;
+    }
+    void* groups = gbase;
+    int* ng = (int*)(gbase + (size_t)ngmax * gbytes);
     int e = kqk_launch_moe_group(sel, nm, E, nt, op->x_div, mch, op->w[0], op->w[nt - 1], op->y[0],
                                  op->y[nt - 1], (long)op->expert_stride, groups, ng, st);
     if (e) return kq_fail("moe group launch: %s", hipGetErrorString((hipError_t)e));
@@ -1035,37 +1114,48 @@ static int moe_per_token(const kq_moe_op* op, const int* sel, int B, int k, int 
     return 0;
 }
 
-int kq_moe_gemv_routed_dev(const kq_moe_op* op, const float* probs, int B, int k, int E, int* sel,
-                           float* selw, kq_stream stream) {
+/* kq_moe_gemv_routed_dev with the grouping records in io->grp when io is
+ * given (the FFN step's workspace), else in the library's scratch */
+static int moe_gemv_routed(const kq_moe_op* op, const float* probs, int B, int k, int E, int* sel,
+                           float* selw, moe_runs_io* io, hipStream_t st) {
     if (!op || !probs || !sel || !selw) return kq_fail("kq_moe_gemv_routed_dev: NULL argument");
     if (B < 1 || B > KQ_MOE_MAX_TOKENS || k < 1 || k > KQ_MAX_GROUPS || E < 1 || E > 1024)
         return kq_fail("kq_moe_gemv_routed_dev: B=%d k=%d E=%d (E <= 1024)", B, k, E);
     if (moe_check_op(op, k, E, "kq_moe_gemv_routed_dev")) return -1;
-    hipStream_t st = pick(stream);
     if (B == 1) return moe_one_token(op, sel, k, E, probs, selw, st);
     if (!is_core(op->type)) {
         const int e = kqk_launch_moe_topk(probs, B, E, k, sel, selw, st);
         if (e) return kq_fail("moe topk launch: %s", hipGetErrorString((hipError_t)e));
         return moe_per_token(op, sel, B, k, E, st);
     }
-    const int r = moe_batch(op, sel, probs, selw, B, k, E, NULL, st);
+    const int r = moe_batch(op, sel, probs, selw, B, k, E, io, st);
     if (r <= 0) return r;
     /* the router weights do not fit beside the plan: route separately */
     const int e = kqk_launch_moe_topk(probs, B, E, k, sel, selw, st);
     if (e) return kq_fail("moe topk launch: %s", hipGetErrorString((hipError_t)e));
-    return moe_batch(op, sel, NULL, NULL, B, k, E, NULL, st);
+    return moe_batch(op, sel, NULL, NULL, B, k, E, io, st);
 }
 
-int kq_moe_gemv_dev(const kq_moe_op* op, const int* sel, int B, int k, int E, kq_stream stream) {
+int kq_moe_gemv_routed_dev(const kq_moe_op* op, const float* probs, int B, int k, int E, int* sel,
+                           float* selw, kq_stream stream) {
+    return moe_gemv_routed(op, probs, B, k, E, sel, selw, NULL, pick(stream));
+}
+
+/* kq_moe_gemv_dev with the grouping records in io->grp when io is given */
+static int moe_gemv(const kq_moe_op* op, const int* sel, int B, int k, int E, moe_runs_io* io,
+                    hipStream_t st) {
     if (!op || !sel) return kq_fail("kq_moe_gemv_dev: NULL argument");
     if (B < 1 || B > KQ_MOE_MAX_TOKENS || k < 1 || k > KQ_MAX_GROUPS || E < 1 ||
         E > KQ_MOE_MAX_EXPERTS)
         return kq_fail("kq_moe_gemv_dev: B=%d k=%d E=%d", B, k, E);
     if (moe_check_op(op, k, E, "kq_moe_gemv_dev")) return -1;
-    hipStream_t st = pick(stream);
     if (B == 1) return moe_one_token(op, sel, k, E, NULL, NULL, st);
     if (!is_core(op->type)) return moe_per_token(op, sel, B, k, E, st);
-    return moe_batch(op, (int*)sel, NULL, NULL, B, k, E, NULL, st);
+    return moe_batch(op, (int*)sel, NULL, NULL, B, k, E, io, st);
+}
+
+int kq_moe_gemv_dev(const kq_moe_op* op, const int* sel, int B, int k, int E, kq_stream stream) {
+    return moe_gemv(op, sel, B, k, E, NULL, pick(stream));
 }
 
 /* ------------------------------------------------------ MoE FFN step */
@@ -1105,15 +1195,20 @@ int kq_moe_combine_dev(const float* o, const int* sel, const float* selw, const 
 }
 
 /* workspace of one step: probs B x E, g / u / act B*k x F, down outputs
- * B*k x H, the run tables of the batch launches, each 256-byte aligned */
-static int64_t ffn_layout(const kq_moe_ffn* f, int B, int64_t off[6]) {
+ * B*k x H, the run tables of the batch launches, and the records of the
+ * grouping launch (used when the runs cannot be built inside the multi-x
+ * launch: sized for gate+up together and runs of one member, the most any
+ * launch of the step needs), each 256-byte aligned */
+#define FFN_REGIONS 7
+static int64_t ffn_layout(const kq_moe_ffn* f, int B, int64_t off[FFN_REGIONS]) {
     const int64_t bk = (int64_t)B * f->k;
     const int dmax = f->n_experts < bk ? f->n_experts : (int)bk;
-    const int64_t sz[6] = {(int64_t)B * f->n_experts * 4, bk * f->n_ff * 4, bk * f->n_ff * 4,
-                           bk * f->n_ff * 4, bk * f->n_embed * 4,
-                           4 * kqk_moe_runs_words((int)bk, f->n_experts, dmax + (int)bk)};
+    const int64_t sz[FFN_REGIONS] = {
+        (int64_t)B * f->n_experts * 4, bk * f->n_ff * 4, bk * f->n_ff * 4, bk * f->n_ff * 4,
+        bk * f->n_embed * 4, 4 * kqk_moe_runs_words((int)bk, f->n_experts, dmax + (int)bk),
+        (int64_t)moe_group_bytes(2, (int)bk, f->n_experts, 1)};
     int64_t t = 0;
-    for (int i = 0; i < 6; i++) {
+    for (int i = 0; i < FFN_REGIONS; i++) {
         off[i] = t;
         t += (sz[i] + 255) & ~(int64_t)255;
     }
@@ -1134,23 +1229,61 @@ static int ffn_check(const kq_moe_ffn* f, int B, const char* who) {
 
 int64_t kq_moe_ffn_workspace_bytes(const kq_moe_ffn* f, int B) {
     if (ffn_check(f, B, "kq_moe_ffn_workspace_bytes")) return -1;
-    int64_t off[6];
+    int64_t off[FFN_REGIONS];
     return ffn_layout(f, B, off);
 }
+
+/* Whether the batch-1 three-launch form fits this layer: the launches'
+ * LDS plans, and the conditions the fused epilogues put on them (each
+ * workgroup's outputs of all parts fit the x region it no longer needs,
+ * and the combine has a lane per output row of a part). */
+static int ffn_fused_fits(const kq_moe_ffn* f) {
+    const int grid = plan_grid(), H = f->n_embed, F = f->n_ff, k = f->k;
+    if (F % grid || H % grid) return 0;
+    static const float dummy[4];
+    static int dsel[KQ_MAX_GROUPS];
+    kqk_seg s;
+    int xo, to, so;
+    /* gate + up: 2k parts of F rows on one x of H, routed in the launch */
+    memset(&s, 0, sizeof s);
+    s.type = f->gate_type; s.K = H; s.nparts = 2 * k; s.x = dummy;
+    for (int p = 0; p < 2 * k; p++) s.rows[p] = F;
+    s.sel = dsel; s.ksel = k; s.emax = f->n_experts;
+    s.probs = dummy; s.sel_out = dsel; s.selw_out = (float*)dummy;
+    long l = kqk_segs_lds(&s, 1, grid, &xo, &to, &so);
+    if (l < 0 || l > g_kq.lds_max || (long)2 * k * (F / grid) * 4 > xo) return 0;
+    /* down: k parts of H rows, each on its own x of F */
+    memset(&s, 0, sizeof s);
+    s.type = f->down_type; s.K = F; s.nparts = k; s.x = dummy;
+    s.x_stride = k > 1 ? F : 0;
+    for (int p = 0; p < k; p++) s.rows[p] = H;
+    s.sel = dsel; s.ksel = k; s.emax = f->n_experts;
+    l = kqk_segs_lds(&s, 1, grid, &xo, &to, &so);
+    if (l < 0 || l > g_kq.lds_max || (long)k * (H / grid) * 4 > xo ||
+        H / grid > plan_threads(&s, 1, grid))
+        return 0;
+    return 1;
+}
+
+static int g_ffn_path;     /* what the last kq_moe_ffn_dev call did (KQ_FFN_* bits) */
+
+int kq_moe_ffn_last_path(void) { return g_ffn_path; }
 
 /* The expert FFN step of moe_forward_one_token / moe_forward_b
  * (stratum_arch_moe.inc.c:689-743, 1107-1226) after the norm: router GEMV,
  * softmax, top-k, gate and up of the selected slices, SwiGLU, down, and
- * the rank-ordered weighted accumulate plus the residual -- six launches
- * on one stream, no allocation. */
+ * the rank-ordered weighted accumulate plus the residual -- on one stream,
+ * with every intermediate and every device-side table in the caller's
+ * workspace (no allocation). */
 int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* sel, float* selw,
                    void* work, int64_t work_bytes, kq_stream stream) {
     static const char who[] = "kq_moe_ffn_dev";
+    g_ffn_path = 0;
     if (ffn_check(f, B, who) || kq_ready()) return -1;
     if (!xn || !x || !sel || !selw || !work) return kq_fail("%s: NULL pointer", who);
     if (((uintptr_t)xn | (uintptr_t)x | (uintptr_t)work) & 15)
         return kq_fail("%s: xn, x and work must be 16-byte aligned", who);
-    int64_t off[6];
+    int64_t off[FFN_REGIONS];
     const int64_t need = ffn_layout(f, B, off);
     if (work_bytes < need)
         return kq_fail("%s: workspace of %lld bytes, %lld needed", who, (long long)work_bytes,
@@ -1161,9 +1294,15 @@ int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* s
     float* u = (float*)(w8 + off[2]);
     float* act = (float*)(w8 + off[3]);
     float* ffo = (float*)(w8 + off[4]);
-    moe_runs_io rio = {(int*)(w8 + off[5]), NULL, 0, 0};
+    void* grp = w8 + off[6];
+    const size_t grp_bytes = (size_t)(need - off[6]);
+    /* rio: the gate+up launch's run tables for the down launch; gio: group
+     * records only (every other launch that may group) */
+    moe_runs_io rio = {(int*)(w8 + off[5]), NULL, 0, 0, grp, grp_bytes, 0, 0};
+    moe_runs_io gio = {NULL, NULL, 0, 0, grp, grp_bytes, 0, 0};
     const int H = f->n_embed, F = f->n_ff, E = f->n_experts, k = f->k;
     const int pair = f->gate_type == f->up_type && f->gate_stride == f->up_stride;
+    hipStream_t st = pick(stream);
 
     /* One token in three launches: router logits; gate and up of the
      * selected slices with the softmax and top-k taken in that launch and
@@ -1171,11 +1310,12 @@ int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* s
      * residual in its epilogue.  The same arithmetic as the six-launch form
      * below (the tests hold the two bit-identical; KQ_MOE_FFN_SPLIT=1 forces
      * that form).  Needs one gate+up segment (2k <= KQ_MAX_GROUPS), E <= 256
-     * (every logit in a lane), a core down type, and n_ff and n_embed
-     * multiples of the grid (a workgroup then holds a rank's gate and up
-     * row, and all k ranks' down rows, of the same index). */
-    if (B == 1 && pair && 2 * k <= KQ_MAX_GROUPS && E <= 256 && is_core(f->down_type) &&
-        F % plan_grid() == 0 && H % plan_grid() == 0 && !g_kq.env_ffn_split) {
+     * (every logit in a lane), a core down type, n_ff and n_embed multiples
+     * of the grid (a workgroup then holds a rank's gate and up row, and all
+     * k ranks' down rows, of the same index), and the fused epilogues'
+     * room (ffn_fused_fits). */
+    if (B == 1 && pair && 2 * k <= KQ_MAX_GROUPS && E <= 256 && is_core(f->gate_type) &&
+        is_core(f->down_type) && !g_kq.env_ffn_split && ffn_fused_fits(f)) {
         if (kq_gemv_dev(f->router_type, f->router, xn, NULL, probs, E, H, stream)) return -1;
         kq_moe_op gu;
         memset(&gu, 0, sizeof gu);
@@ -1185,13 +1325,13 @@ int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* s
         gu.w[1] = f->up; gu.y[1] = u;
         gu.expert_stride = f->gate_stride;
         if (moe_check_op(&gu, k, E, who)) return -1;
-        hipStream_t st = pick(stream);
         if (moe_one_token_ffn(&gu, sel, k, E, probs, selw, 1, act, NULL, NULL, st)) return -1;
         kq_moe_op dn;
         memset(&dn, 0, sizeof dn);
         dn.type = f->down_type; dn.n_out = H; dn.k_in = F; dn.x = act; dn.x_div = 1;
         dn.ntensors = 1; dn.w[0] = f->down; dn.y[0] = ffo; dn.expert_stride = f->down_stride;
         if (moe_check_op(&dn, k, E, who)) return -1;
+        g_ffn_path = KQ_FFN_FUSED_B1;
         return moe_one_token_ffn(&dn, sel, k, E, NULL, NULL, 0, NULL, x, selw, st);
     }
 
@@ -1216,7 +1356,6 @@ int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* s
         /* a batch: the grouped gate+up launch stores its run tables for the
          * down launch (routed inside it when that fits, else after a top-k
          * launch) */
-        hipStream_t st = pick(stream);
         if (moe_check_op(&gu, k, E, who)) return -1;
         int r = moe_batch(&gu, sel, probs, selw, B, k, E, &rio, st);
         if (r == 1) {
@@ -1225,12 +1364,12 @@ int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* s
             r = moe_batch(&gu, sel, NULL, NULL, B, k, E, &rio, st);
         }
         if (r < 0) return -1;
-        if (r > 0 && kq_moe_gemv_dev(&gu, sel, B, k, E, stream)) return -1;
+        if (r > 0 && moe_gemv(&gu, sel, B, k, E, &gio, st)) return -1;
     } else if (E <= 1024) {
-        if (kq_moe_gemv_routed_dev(&gu, probs, B, k, E, sel, selw, stream)) return -1;
+        if (moe_gemv_routed(&gu, probs, B, k, E, sel, selw, &gio, st)) return -1;
     } else {
         if (kq_moe_topk_dev(probs, B, E, k, sel, selw, stream) ||
-            kq_moe_gemv_dev(&gu, sel, B, k, E, stream))
+            moe_gemv(&gu, sel, B, k, E, &gio, st))
             return -1;
     }
     if (!pair) {
@@ -1238,7 +1377,7 @@ int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* s
         memset(&up, 0, sizeof up);
         up.type = f->up_type; up.n_out = F; up.k_in = H; up.x = xn; up.x_div = k;
         up.ntensors = 1; up.w[0] = f->up; up.y[0] = u; up.expert_stride = f->up_stride;
-        if (kq_moe_gemv_dev(&up, sel, B, k, E, stream)) return -1;
+        if (moe_gemv(&up, sel, B, k, E, &gio, st)) return -1;
     }
 
     /* SwiGLU, down, weighted accumulate + residual */
@@ -1252,12 +1391,14 @@ int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* s
         rio.in = rio.out;
         rio.out = NULL;
         if (moe_check_op(&dn, k, E, who)) return -1;
-        const int r = moe_batch(&dn, sel, NULL, NULL, B, k, E, &rio, pick(stream));
+        const int r = moe_batch(&dn, sel, NULL, NULL, B, k, E, &rio, st);
         if (r < 0) return -1;
-        if (r > 0 && kq_moe_gemv_dev(&dn, sel, B, k, E, stream)) return -1;
-    } else if (kq_moe_gemv_dev(&dn, sel, B, k, E, stream)) {
+        if (r > 0 && moe_gemv(&dn, sel, B, k, E, &gio, st)) return -1;
+    } else if (moe_gemv(&dn, sel, B, k, E, &gio, st)) {
         return -1;
     }
+    g_ffn_path = (rio.stored ? KQ_FFN_RUNS_STORED : 0) | (rio.runs_loaded ? KQ_FFN_RUNS_LOADED : 0) |
+                 (rio.grp_used || gio.grp_used ? KQ_FFN_GROUP_LAUNCH : 0);
     return kq_moe_combine_dev(ffo, sel, selw, x, x, B, k, H, stream);
 }
 

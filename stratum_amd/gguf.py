@@ -79,12 +79,22 @@ class Index:
         except Exception:
             pass
 
+    # The descriptors kq_gguf_open builds live in C memory that
+    # kq_gguf_close frees (names included).  tensors() and find() return
+    # copies that hold a reference to this Index, so the C memory their
+    # name pointers use stays alive as long as any of them does; close()
+    # must not be called while they are still in use.
+    def _own(self, t: KqTensor) -> KqTensor:
+        c = KqTensor.from_buffer_copy(t)
+        c._index = self
+        return c
+
     def tensors(self) -> list[KqTensor]:
-        return [self.g.tensors[i] for i in range(self.g.n_tensors)]
+        return [self._own(self.g.tensors[i]) for i in range(self.g.n_tensors)]
 
     def find(self, name: str) -> KqTensor | None:
         p = glib().kq_gguf_find_tensor(ctypes.byref(self.g), name.encode())
-        return p.contents if p else None
+        return self._own(p.contents) if p else None
 
     def u32(self, key: str) -> int | None:
         v = ctypes.c_uint32()

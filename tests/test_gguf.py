@@ -149,6 +149,25 @@ def test_model_index_and_metadata():
     ix.close()
 
 
+def test_descriptors_outlive_the_index_object():
+    """tensors() and find() return copies that keep their Index (and the C
+    memory their names point into) alive: dropping the Index object first
+    leaves them valid."""
+    import gc
+    r = synth.rng(81)
+    ts = [("blk.0.attn_q.weight", [768, 2], 12, synth.q4k_blocks(r, 6).tobytes()),
+          ("norm", [40], 0, np.arange(40, dtype=np.float32).tobytes())]
+    buf = G.model(ts, [G.kv_str("general.architecture", "qwen3")])
+    got = KG.Index(buf).tensors()
+    q = KG.Index(buf).find("blk.0.attn_q.weight")
+    gc.collect()
+    junk = [KG.Index(buf) for _ in range(4)]       # reuse freed memory, if any
+    assert [t.name for t in got] == [b"blk.0.attn_q.weight", b"norm"]
+    assert got[0].type == 12 and got[1].nelem == 40
+    assert q.name == b"blk.0.attn_q.weight" and q.nbytes == 6 * 144
+    del junk
+
+
 def test_type_table():
     for t, (b, e) in {0: (4, 1), 1: (2, 1), 8: (34, 32), 10: (84, 256), 11: (110, 256),
                       12: (144, 256), 13: (176, 256), 14: (210, 256), 42: (148, 256),

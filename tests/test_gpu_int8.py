@@ -20,6 +20,7 @@ import pytest
 
 import stratum_amd as K
 from conftest import same_values
+from i8_cases import reciprocal_groups
 from stratum_amd import INT8_ACT, TYPE_Q4_K, TYPE_Q6_K, synth
 
 pytestmark = pytest.mark.gpu
@@ -84,6 +85,9 @@ def test_quantize_bit_exact(port, G, Kd):
     x[0:G] = 0.0                                    # a zero group
     x[G:G + 8] = [127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5]   # ties
     x[G + 8:2 * G] = 0.25
+    # groups where fl(x * fl(1 / scale)) and fl(x / scale) round apart
+    rx, _ = reciprocal_groups(G, min(8, Kd // G - 2))
+    x[2 * G:2 * G + rx.size] = rx
     dx = dev(x)
     ng = Kd // G
     xq = torch.empty(Kd, dtype=torch.int8, device="cuda")

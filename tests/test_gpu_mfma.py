@@ -165,6 +165,13 @@ def test_mfma_repeatable_and_other_types_refused():
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     with pytest.raises(RuntimeError, match="no MFMA path"):
         run(K.gemv_multix_mfma_dev, 10, dw, xs, B, N, Kd)
+    # an xs that is not 16-byte aligned is refused before any launch (the
+    # split kernel reads x as float4)
+    dx = torch.from_numpy(np.ascontiguousarray(xs.reshape(-1))).cuda()
+    dy = torch.zeros(B * N, dtype=torch.float32, device="cuda")
+    for fn in (K.lib().kq_gemv_multix_mfma_dev, K.lib().kq_gemv_multix_mfma_noalloc_dev):
+        rc = fn(qtype, dw.data_ptr(), dx.data_ptr() + 4, dy.data_ptr(), B - 1, N, Kd, None)
+        assert rc == -1 and b"16-byte aligned" in K.lib().kq_last_error()
 
 
 def test_mfma_reserved_workspace_allocates_nothing():

@@ -194,7 +194,15 @@ def run_step(d, xn, x0, B):
     sizes = {"probs": B * E, "g": B * k * F, "u": B * k * F, "act": B * k * F, "ffo": B * k * H}
     out = {n: wk[off[n] // 4:off[n] // 4 + sizes[n]] for n in sizes}
     out.update(x=dx.cpu().numpy(), sel=sel.cpu().numpy(), selw=selw.cpu().numpy())
+    # what the step ran, and the first word of the run-table region (the
+    # run count when the gate+up launch stored its tables; the workspace was
+    # filled with NaN bits before the call)
+    out["path"] = K.moe_ffn_last_path()
+    out["runs0"] = int(wk[off["runs"] // 4:off["runs"] // 4 + 1].view(np.int32)[0])
     return out
+
+
+NAN_BITS = int(np.array([np.nan], np.float32).view(np.int32)[0])
 
 
 @pytest.mark.parametrize("B", [1, 16])
@@ -256,18 +264,20 @@ def test_moe_ffn_step_config(port, B, kq_env):
     assert err <= 1e-4 * contrib
 
 
-@pytest.mark.parametrize("case", ["config", "q6k_down", "parts16", "grid37", "e512"])
+@pytest.mark.parametrize("case", ["config", "q6k_down", "parts16", "grid37", "e512", "wide_ff"])
 def test_moe_ffn_fused_matches_split(port, case, kq_env):
     """Batch 1 in three launches (softmax and top-k inside the gate+up
     launch and SwiGLU in its epilogue; the rank-ordered combine plus residual
     in the down launch's epilogue) against the six-launch form: x, sel, selw
     and the activations bit-identical, and x against the oracle.  grid37 (37
-    workgroups: the rows per part are not a multiple) and e512 (512 experts:
-    more than 256 logits) take the six-launch form inside kq_moe_ffn_dev and
-    must give the same bits too."""
+    workgroups: the rows per part are not a multiple), e512 (512 experts:
+    more than 256 logits) and wide_ff (n_ff 32x n_embed: a workgroup's gate
+    and up outputs overflow the x region the fused epilogue keeps them in)
+    take the six-launch form inside kq_moe_ffn_dev and must give the same
+    bits too; kq_moe_ffn_last_path tells which form ran."""
     H, F, E, k = {"config": (2048, 768, 128, 8), "q6k_down": (1024, 512, 64, 4),
                   "parts16": (1024, 256, 32, 8), "grid37": (2048, 768, 128, 8),
-                  "e512": (1024, 256, 512, 4)}[case]
+                  "e512": (1024, 256, 512, 4), "wide_ff": (256, 8192, 16, 8)}[case]
     d = make_layer(H, F, E, k, 9700)
     if case == "q6k_down":
         d["down_type"] = 14
@@ -279,8 +289,11 @@ def test_moe_ffn_fused_matches_split(port, case, kq_env):
         kq_env(KQ_GRID=37)
     print(f"moe ffn fused vs split: {case}", flush=True)
     fused = run_step(d, xn, x0, 1)
+    want_fused = case in ("config", "q6k_down", "parts16")
+    assert bool(fused["path"] & K.FFN_FUSED_B1) == want_fused, fused["path"]
     kq_env(KQ_MOE_FFN_SPLIT=1)
     split = run_step(d, xn, x0, 1)
+    assert not split["path"] & K.FFN_FUSED_B1
     for n in ("sel", "selw", "act", "x"):
         assert same_values(fused[n], split[n]), n
     full = port.moe_ffn(d, xn, x0, 1)
@@ -306,14 +319,57 @@ def test_moe_ffn_batch_shared_runs_match_split(port, case, kq_env):
     x0 = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
     print(f"moe ffn batch shared run tables vs split: {case}", flush=True)
     fused = run_step(d, xn, x0, B)
+    # the tables were stored (run count written over the NaN fill) and the
+    # down launch loaded them
+    assert fused["path"] & K.FFN_RUNS_STORED and fused["path"] & K.FFN_RUNS_LOADED, fused["path"]
+    assert fused["runs0"] != NAN_BITS and 0 < fused["runs0"] <= B * k, fused["runs0"]
     kq_env(KQ_MOE_FFN_SPLIT=1)
     split = run_step(d, xn, x0, B)
+    assert not split["path"] & (K.FFN_RUNS_STORED | K.FFN_RUNS_LOADED)
     for n in ("sel", "selw", "g", "u", "act", "ffo", "x"):
         assert same_values(fused[n], split[n]), n
     full = port.moe_ffn(d, xn, x0, B)
     assert np.array_equal(full["sel"], fused["sel"])
     contrib = np.abs(full["x"] - x0).max()
     assert np.abs(fused["x"] - full["x"]).max() <= 1e-4 * contrib
+
+
+@pytest.mark.parametrize("case", ["group_launch_b16", "e4096_b4", "e4096_b4_group_launch"])
+def test_moe_ffn_never_grows_library_scratch(port, case, kq_env):
+    """No allocation in the step, also where a launch groups the selection
+    in a launch of its own: group_launch_b16 and e4096_b4_group_launch force
+    that form (KQ_MOE_GROUP_LAUNCH); e4096_b4 is the largest expert count,
+    routed by a separate top-k launch.  With the library's scratch emptied
+    first (kq_linear_shutdown), kq_scratch_bytes() stays 0 across the step,
+    the forced group records went to the workspace (KQ_FFN_GROUP_LAUNCH),
+    and x agrees with the oracle (group_launch_b16: bit-identical to the
+    step with the runs built in the launch)."""
+    B, H, F, E, k = {"group_launch_b16": (16, 2048, 768, 128, 8),
+                     "e4096_b4": (4, 256, 256, 4096, 8),
+                     "e4096_b4_group_launch": (4, 256, 256, 4096, 8)}[case]
+    forced = case != "e4096_b4"
+    d = make_layer(H, F, E, k, 9900)
+    r = synth.rng(9901)
+    xn = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
+    x0 = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
+    print(f"moe ffn scratch: {case}", flush=True)
+    if case == "group_launch_b16":
+        base = run_step(d, xn, x0, B)
+    if forced:
+        kq_env(KQ_MOE_GROUP_LAUNCH=1)
+    K.lib().kq_linear_shutdown()
+    assert K.lib().kq_scratch_bytes() == 0
+    got = run_step(d, xn, x0, B)
+    assert K.lib().kq_scratch_bytes() == 0
+    if forced:
+        assert got["path"] & K.FFN_GROUP_LAUNCH, got["path"]
+    if case == "group_launch_b16":
+        for n in ("sel", "selw", "g", "u", "act", "ffo", "x"):
+            assert same_values(got[n], base[n]), n
+    full = port.moe_ffn(d, xn, x0, B)
+    assert np.array_equal(full["sel"], got["sel"])
+    contrib = np.abs(full["x"] - x0).max()
+    assert np.abs(got["x"] - full["x"]).max() <= 1e-4 * contrib
 
 
 def test_moe_ffn_step_f16_router_mixed_types(port):

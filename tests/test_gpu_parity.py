@@ -505,18 +505,35 @@ def test_multix_member_chunks(port, B):
         assert same_values(got[s], gpu_gemv(qtype, w, xs[s], N, Kd)), f"stream {s}"
 
 
-@pytest.mark.parametrize("qtype,N,Kd", [(12, 17408, 5120), (14, 5120, 17408)])
-def test_multix_27b_sampled(port, qtype, N, Kd):
-    """27B gate / down with B = 8: sampled rows against the oracle, all rows
-    against single-stream launches."""
-    B = 8
-    w = synth.tensor(qtype, N, Kd, 850 + qtype)
+@pytest.mark.parametrize("tensor,B", [("gate", 8), ("down", 8), ("gate", 16), ("up", 16),
+                                      ("down", 16), ("gate", 64), ("up", 64), ("down", 64)])
+def test_multix_27b_sampled(port, tensor, B):
+    """27B gate / up (Q4_K 17408 x 5120) and down (Q6_K 5120 x 17408) with
+    B = 8, 16 and 64 streams, the MULTISEQ shapes bench.py times (the
+    planner picks other member chunks and x tiles at each B): every stream
+    against its single-stream launch bit for bit, and 256 sampled rows of
+    two streams against the oracle."""
+    qtype, N, Kd, seed = {"gate": (12, 17408, 5120, 850), "up": (12, 17408, 5120, 851),
+                          "down": (14, 5120, 17408, 852)}[tensor]
+    w = synth.tensor(qtype, N, Kd, seed)
     xs = np.stack([synth.gaussian(synth.rng(860 + s), Kd) for s in range(B)])
-    got = gpu_multix(qtype, w, xs, N, Kd)
-    rows = np.random.default_rng(3).choice(N, 256, replace=False)
+    print(f"multix 27B {tensor} B={B}", flush=True)
+    dw, dx = dev(w), dev(xs.reshape(-1))
+    dy = torch.full((B * N,), float("nan"), dtype=torch.float32, device="cuda")
+    K.gemv_multix_dev(qtype, dw.data_ptr(), dx.data_ptr(), dy.data_ptr(), B, N, Kd,
+                      stream=stream())
+    d1 = torch.full((B * N,), float("nan"), dtype=torch.float32, device="cuda")
+    for s in range(B):
+        K.gemv_dev(qtype, dw.data_ptr(), dx.data_ptr() + 4 * s * Kd, d1.data_ptr() + 4 * s * N,
+                   N, Kd, stream=stream())
+    torch.cuda.synchronize()
+    got = dy.cpu().numpy().reshape(B, N)
+    single = d1.cpu().numpy().reshape(B, N)
+    for s in range(B):
+        assert same_values(got[s], single[s]), f"stream {s}"
+    rows = np.random.default_rng(3 + B).choice(N, 256, replace=False)
     rb = K.lib().kq_row_bytes(qtype, Kd)
     sub = np.concatenate([w[r * rb:(r + 1) * rb] for r in rows])
-    for s in (0, 5):
-        assert same_values(got[s], gpu_gemv(qtype, w, xs[s], N, Kd)), f"stream {s}"
+    for s in (0, B - 3):
         check_close(got[s][rows], port.gemv(qtype, sub, xs[s], len(rows), Kd),
-                    f"multix 27B {K.TYPE_NAMES[qtype]} s={s}")
+                    f"multix 27B {tensor} B={B} s={s}")

@@ -21,6 +21,7 @@ pins it instead:
 import numpy as np
 import pytest
 
+from i8_cases import reciprocal_groups
 from stratum_amd import TYPE_Q4_K, TYPE_Q6_K, synth
 
 I8_TYPES = [TYPE_Q4_K, TYPE_Q6_K]
@@ -61,6 +62,22 @@ def test_quantize_halfway_zero_sign(port, G):
     assert xq[G] == -127 and xq[G + 1] == 3
     assert xs[2] == 0.0 and not np.any(xq[2 * G:3 * G])
     assert np.all(xq[3 * G:4 * G] == 127)
+
+
+@pytest.mark.parametrize("G", [32, 16])
+def test_quantize_multiplies_by_the_rounded_reciprocal(port, G):
+    """q = rne(fl(x * fl(1 / scale))) as the reference writes it
+    (stratum_q4k_neon.h:262-276, stratum_q6k_neon.h:117-133), not
+    rne(fl(x / scale)): on 24 inputs where the two round to different
+    integers, the restatement gives the reciprocal form's value."""
+    x, want = reciprocal_groups(G, 24)
+    xq, xs = port.quantize_q8(x, G)
+    got = xq.reshape(-1, G)[:, 1].astype(np.int32)
+    assert np.array_equal(got, want)
+    amax = x.reshape(-1, G)[:, 0]
+    div = np.rint((x.reshape(-1, G)[:, 1] / (amax / np.float32(127.0))).astype(np.float32))
+    assert np.all(div.astype(np.int32) != want)
+    assert np.all(xq.reshape(-1, G)[:, 0] == 127)
 
 
 @pytest.mark.parametrize("G", [32, 16])
