@@ -49,21 +49,24 @@ extern "C" {
 #define KQ_TYPE_Q6_K    14
 #define KQ_TYPE_Q2K_NIB 42
 
-/* Int8-activation mode of Q4_K and Q6_K: `type | KQ_INT8_ACT` on
- * kq_gemv_dev, kq_gemv_multix_dev and kq_gemv_segments_dev computes the
- * reference's SDOT path (g_st.use_sdot, stratum_linear.h:376-404,
- * 581-603, 643-690): x quantized to int8 per 32 (Q4_K,
- * q4k_quantize_x_q8, stratum_q4k_neon.h:229-275) or per 16 (Q6_K,
- * q6k_quantize_x_q8_g16, stratum_q6k_neon.h:117-133), exact integer dot
- * products per sub-block, and the terms of q4k_dot_row_sdot_f /
- * q6k_dot_row_sdot_f (stratum_q4k_neon.h:365-407, q6k_neon.h:265-317):
- * coefficient fl(fl(d*sc)*xscale) times the integer sum.  The quantized x,
- * the integer parts and the coefficients are bit-identical to the
- * reference's; the terms are summed in binary64 instead of the reference's
- * four binary32 FMA lanes, so y differs from q*_dot_row_sdot_f by at most
- * 2^-22 * sum|term| (the lanes' own rounding) and is independent of the
- * launch shape.  The weights are unchanged: kq_row_bytes is the base
- * type's.  No MoE or matrix-core form. */
+/* Int8-activation mode of Q4_K, Q6_K, Q5_K, Q3_K and Q8_0:
+ * `type | KQ_INT8_ACT` on kq_gemv_dev, kq_gemv_multix_dev and
+ * kq_gemv_segments_dev computes the reference's SDOT path (g_st.use_sdot,
+ * stratum_linear.h:376-489, 581-603, 643-690): x quantized to int8 per 16
+ * (Q6_K, q6k_quantize_x_q8_g16, stratum_q6k_neon.h:117-133) or per 32 (the
+ * others, q4k_quantize_x_q8, stratum_q4k_neon.h:229-275), exact integer
+ * dot products per sub-block, group or block, and the terms of
+ * q4k_dot_row_sdot_f / q6k_dot_row_sdot_f / q5k_dot_row_sdot_f /
+ * q3k_dot_row_sdot_f / q8_0_dot_row_sdot_f (stratum_q4k_neon.h:365-407,
+ * q6k_neon.h:265-317, q5k_neon.h:158-204, q3k_neon.h:84-125,
+ * stratum_q8_0.h:112-145): coefficient fl(fl(d*sc)*xscale) (Q8_0:
+ * fl(d*xscale)) times the integer sum.  The quantized x, the integer parts
+ * and the coefficients are bit-identical to the reference's; the terms are
+ * summed in binary64 instead of the reference's four binary32 FMA lanes,
+ * so y differs from q*_dot_row_sdot_f by at most 2^-22 * sum|term| (the
+ * lanes' own rounding) and is independent of the launch shape.  The
+ * weights are unchanged: kq_row_bytes is the base type's.  No MoE or
+ * matrix-core form. */
 #define KQ_INT8_ACT     0x100
 
 /* Layout-compatible with GgufTensor (stratum_gguf.h:129-137): a caller may
@@ -118,9 +121,10 @@ const char* kq_last_error(void);
 int kq_tuning_reload(void);
 
 /* g_st.use_sdot for the host-pointer entry points (kq_linear_dispatch*,
- * kq_linear_multix, kq_q4k_group): on != 0 routes Q4_K and Q6_K through
- * the int8-activation mode (KQ_INT8_ACT), as st_linear_q4k / _q6k do when
- * use_sdot is set (stratum_linear.h:376-404).  Off at start-up: the
+ * kq_linear_multix, kq_q4k_group): on != 0 routes Q4_K, Q6_K, Q5_K, Q3_K
+ * and Q8_0 through the int8-activation mode (KQ_INT8_ACT), as
+ * st_linear_q4k / _q6k / _q5k / _q3k / _q8_0 do when use_sdot is set
+ * (stratum_linear.h:376-489).  Off at start-up: the
  * reference turns it on by default only where its NEON kernels exist
  * (stratum_linear.h:133-137).  Returns the previous setting. */
 int kq_linear_set_sdot(int on);

@@ -560,14 +560,163 @@ static double q6k_i8_dot(const uint8_t* row, int K, const int8_t* xq, const floa
     return dot;
 }
 
+/* Q5_K with int8 activations per 32, q5k_dot_row_sdot_f
+ * (stratum_q5k_neon.h:158-204): Q4_K's lanes with the 5-bit values
+ * q5k_q (nibble plus 16 times the qh bit, 0..31) in the exact dots. */
+static float q5k_sdot_f(const uint8_t* row, int K, const int8_t* xq, const float* xs,
+                        const int32_t* xsum, double* mag) {
+    float f[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    double m_ = 0.0;
+    for (int b = 0; b < K / 256; b++) {
+        const uint8_t* blk = row + (size_t)b * 176;
+        const float d = ko_fp16_to_fp32(rd16(blk)), dmin = ko_fp16_to_fp32(rd16(blk + 2));
+        for (int j = 0; j < 4; j++) {
+            const int g0 = 8 * b + 2 * j, g1 = g0 + 1;
+            uint8_t sc1, mn1, sc2, mn2;
+            ko_q4k_scale_min(2 * j, blk + 4, &sc1, &mn1);
+            ko_q4k_scale_min(2 * j + 1, blk + 4, &sc2, &mn2);
+            int32_t L = 0, H = 0;
+            for (int l = 0; l < 32; l++) {
+                L += (int32_t)q5k_q(blk, 2 * j, l) * xq[32 * g0 + l];
+                H += (int32_t)q5k_q(blk, 2 * j + 1, l) * xq[32 * g1 + l];
+            }
+            const float c[4] = {d * (float)sc1 * xs[g0], -dmin * (float)mn1 * xs[g0],
+                                d * (float)sc2 * xs[g1], -dmin * (float)mn2 * xs[g1]};
+            const int32_t t[4] = {L, xsum[g0], H, xsum[g1]};
+            for (int k = 0; k < 4; k++) {
+                f[k] = fmaf((float)t[k], c[k], f[k]);
+                m_ += fabs((double)t[k] * (double)c[k]);
+            }
+        }
+    }
+    if (mag) *mag = m_;
+    return (f[0] + f[1]) + (f[2] + f[3]);
+}
+
+/* Q3_K with int8 activations per 32, q3k_dot_row_sdot_f
+ * (stratum_q3k_neon.h:84-125): 16-weight group gg (positions 16 gg .. of
+ * its block, q3k_q's signed values -4..3) dotted exactly with the
+ * quantized x there; coefficient fl(fl(d * (sc - 32)) * xs) with the
+ * scale of the 32-group holding it; four binary32 fused multiply-add
+ * lanes t = gg % 4; then (f0 + f1) + (f2 + f3).  No min term. */
+static float q3k_sdot_f(const uint8_t* row, int K, const int8_t* xq, const float* xs,
+                        double* mag) {
+    float f[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    double m_ = 0.0;
+    for (int b = 0; b < K / 256; b++) {
+        const uint8_t* blk = row + (size_t)b * 110;
+        const float d = ko_fp16_to_fp32(rd16(blk + 108));
+        for (int gg = 0; gg < 16; gg++) {
+            const int g = 16 * b + gg;
+            int32_t acc = 0;
+            for (int l = 0; l < 16; l++) acc += (int32_t)q3k_q(blk, gg, l) * xq[16 * g + l];
+            const float c = d * (float)(q3k_scale(blk + 96, gg) - 32) * xs[g >> 1];
+            f[gg & 3] = fmaf((float)acc, c, f[gg & 3]);
+            m_ += fabs((double)acc * (double)c);
+        }
+    }
+    if (mag) *mag = m_;
+    return (f[0] + f[1]) + (f[2] + f[3]);
+}
+
+/* Q8_0 with int8 activations per 32 (one scale per block),
+ * q8_0_dot_row_sdot_f (stratum_q8_0.h:112-145): block i's exact dot with
+ * the quantized x, coefficient fl(d * xs[i]), lane i % 4 of four binary32
+ * fused multiply-add chains (K % 256 == 0, so no tail), then
+ * (f0 + f1) + (f2 + f3). */
+static float q8_0_sdot_f(const uint8_t* row, int K, const int8_t* xq, const float* xs,
+                         double* mag) {
+    float f[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    double m_ = 0.0;
+    for (int i = 0; i < K / 32; i++) {
+        const uint8_t* blk = row + (size_t)i * 34;
+        int32_t acc = 0;
+        for (int l = 0; l < 32; l++) acc += (int32_t)(int8_t)blk[2 + l] * xq[32 * i + l];
+        const float c = ko_fp16_to_fp32(rd16(blk)) * xs[i];
+        f[i & 3] = fmaf((float)acc, c, f[i & 3]);
+        m_ += fabs((double)acc * (double)c);
+    }
+    if (mag) *mag = m_;
+    return (f[0] + f[1]) + (f[2] + f[3]);
+}
+
+/* The same three as the GPU computes them: the identical integer dots and
+ * binary32 coefficients, each term formed in binary64 (Q5_K: c1*L + c2*xsum
+ * with one rounding, as Q4_K; Q3_K, Q8_0: c * dot, exact) and summed in
+ * binary64. */
+static double q5k_i8_dot(const uint8_t* row, int K, const int8_t* xq, const float* xs,
+                         const int32_t* xsum) {
+    double dot = 0.0;
+    for (int b = 0; b < K / 256; b++) {
+        const uint8_t* blk = row + (size_t)b * 176;
+        const float d = ko_fp16_to_fp32(rd16(blk)), dmin = ko_fp16_to_fp32(rd16(blk + 2));
+        for (int s = 0; s < 8; s++) {
+            const int g = 8 * b + s;
+            uint8_t sc, mn;
+            ko_q4k_scale_min(s, blk + 4, &sc, &mn);
+            int32_t L = 0;
+            for (int l = 0; l < 32; l++) L += (int32_t)q5k_q(blk, s, l) * xq[32 * g + l];
+            const float c1 = d * (float)sc * xs[g], c2 = -dmin * (float)mn * xs[g];
+            dot += fma((double)c1, (double)L, (double)c2 * (double)xsum[g]);
+        }
+    }
+    return dot;
+}
+
+static double q3k_i8_dot(const uint8_t* row, int K, const int8_t* xq, const float* xs) {
+    double dot = 0.0;
+    for (int b = 0; b < K / 256; b++) {
+        const uint8_t* blk = row + (size_t)b * 110;
+        const float d = ko_fp16_to_fp32(rd16(blk + 108));
+        for (int gg = 0; gg < 16; gg++) {
+            const int g = 16 * b + gg;
+            int32_t acc = 0;
+            for (int l = 0; l < 16; l++) acc += (int32_t)q3k_q(blk, gg, l) * xq[16 * g + l];
+            const float c = d * (float)(q3k_scale(blk + 96, gg) - 32) * xs[g >> 1];
+            dot += (double)c * (double)acc;
+        }
+    }
+    return dot;
+}
+
+static double q8_0_i8_dot(const uint8_t* row, int K, const int8_t* xq, const float* xs) {
+    double dot = 0.0;
+    for (int i = 0; i < K / 32; i++) {
+        const uint8_t* blk = row + (size_t)i * 34;
+        int32_t acc = 0;
+        for (int l = 0; l < 32; l++) acc += (int32_t)(int8_t)blk[2 + l] * xq[32 * i + l];
+        dot += (double)(ko_fp16_to_fp32(rd16(blk)) * xs[i]) * (double)acc;
+    }
+    return dot;
+}
+
+/* one row of the int8 mode: the reference's order (sdot_f) or the GPU's */
+static float i8_row(int type, const uint8_t* row, int K, const int8_t* xq, const float* xs,
+                    const int32_t* xsum, int sdot_f, double* mag) {
+    switch (type) {
+    case KO_Q4_K: return sdot_f ? q4k_sdot_f(row, K, xq, xs, xsum, mag)
+                                : (float)q4k_i8_dot(row, K, xq, xs, xsum);
+    case KO_Q6_K: return sdot_f ? q6k_sdot_f(row, K, xq, xs, xsum, mag)
+                                : (float)q6k_i8_dot(row, K, xq, xs, xsum);
+    case KO_Q5_K: return sdot_f ? q5k_sdot_f(row, K, xq, xs, xsum, mag)
+                                : (float)q5k_i8_dot(row, K, xq, xs, xsum);
+    case KO_Q3_K: return sdot_f ? q3k_sdot_f(row, K, xq, xs, mag)
+                                : (float)q3k_i8_dot(row, K, xq, xs);
+    default: return sdot_f ? q8_0_sdot_f(row, K, xq, xs, mag)
+                           : (float)q8_0_i8_dot(row, K, xq, xs);
+    }
+}
+
 /* y[r] (+ add[r]) for the int8-activation mode: x quantized once per call
- * (per 32 for Q4_K, per 16 for Q6_K), then each row in the reference's
- * order (sdot_f != 0) or the GPU's (binary64 terms).  mag (optional)
- * receives each row's sum of |term|. */
+ * (per 16 for Q6_K, per 32 for Q4_K, Q5_K, Q3_K and Q8_0), then each row
+ * in the reference's order (sdot_f != 0) or the GPU's (binary64 terms).
+ * mag (optional) receives each row's sum of |term|. */
 int ko_gemv_i8(int type, const uint8_t* w, const float* x, const float* add, float* y,
                double* mag, int N, int K, int sdot_f) {
-    if ((type != KO_Q4_K && type != KO_Q6_K) || K % 256) return -1;
-    const int G = type == KO_Q4_K ? 32 : 16;
+    if ((type != KO_Q4_K && type != KO_Q6_K && type != KO_Q5_K && type != KO_Q3_K &&
+         type != KO_Q8_0) || K % 256)
+        return -1;
+    const int G = type == KO_Q6_K ? 16 : 32;
     int8_t* xq = malloc((size_t)K);
     float* xs = malloc((size_t)(K / G) * sizeof(float));
     int32_t* xsum = malloc((size_t)(K / G) * sizeof(int32_t));
@@ -578,19 +727,11 @@ int ko_gemv_i8(int type, const uint8_t* w, const float* x, const float* add, flo
     for (int r = 0; r < N; r++) {
         const uint8_t* row = w + (size_t)r * rb;
         double m_ = 0.0;
-        float v;
-        if (sdot_f)
-            v = type == KO_Q4_K ? q4k_sdot_f(row, K, xq, xs, xsum, &m_)
-                                : q6k_sdot_f(row, K, xq, xs, xsum, &m_);
-        else
-            v = (float)(type == KO_Q4_K ? q4k_i8_dot(row, K, xq, xs, xsum)
-                                        : q6k_i8_dot(row, K, xq, xs, xsum));
+        float v = i8_row(type, row, K, xq, xs, xsum, sdot_f, &m_);
         if (add) v = add[r] + v;
         y[r] = v;
         if (mag) {
-            if (!sdot_f)
-                (void)(type == KO_Q4_K ? q4k_sdot_f(row, K, xq, xs, xsum, &m_)
-                                       : q6k_sdot_f(row, K, xq, xs, xsum, &m_));
+            if (!sdot_f) (void)i8_row(type, row, K, xq, xs, xsum, 1, &m_);
             mag[r] = m_;
         }
     }

@@ -33,7 +33,8 @@ TYPE_Q4_K = 12
 TYPE_Q5_K = 13
 TYPE_Q6_K = 14
 TYPE_Q2K_NIB = 42
-# int8-activation mode flag (KQ_INT8_ACT): TYPE_Q4_K | INT8_ACT, TYPE_Q6_K | INT8_ACT
+# int8-activation mode flag (KQ_INT8_ACT): TYPE_Q4_K | INT8_ACT, and likewise for
+# Q6_K, Q5_K, Q3_K and Q8_0
 INT8_ACT = 0x100
 
 # bytes per 256 weights (stratum_gguf.h:57-79; Q8_0: eight 34-byte blocks)

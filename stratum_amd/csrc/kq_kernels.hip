@@ -59,11 +59,14 @@ constexpr int T_Q4K = 12;
 constexpr int T_Q5K = 13;
 constexpr int T_Q6K = 14;
 constexpr int T_NIB = 42;
-// the int8-activation mode of Q4_K / Q6_K (the reference's SDOT path):
-// the type id with this bit set
+// the int8-activation mode (the reference's SDOT path) of Q4_K, Q6_K,
+// Q5_K, Q3_K and Q8_0: the type id with this bit set
 constexpr int T_I8 = 0x100;
 constexpr int T_Q4K_I8 = T_I8 | T_Q4K;
 constexpr int T_Q6K_I8 = T_I8 | T_Q6K;
+constexpr int T_Q5K_I8 = T_I8 | T_Q5K;
+constexpr int T_Q3K_I8 = T_I8 | T_Q3K;
+constexpr int T_Q80_I8 = T_I8 | T_Q80;
 // float4 slots per chunk in the int8 x layout: 64 bytes padded to 80
 // (chunk c at byte 80c; 16-byte reads by consecutive chunks hit distinct
 // banks)
@@ -85,6 +88,9 @@ template <int TYPE> struct TypeInfo;
 template <> struct TypeInfo<T_Q4K> { static constexpr int BB = 144; static constexpr bool LINEAR = true;  static constexpr int XS_PER_CHUNK = 2; static constexpr bool SCALED = true; };
 template <> struct TypeInfo<T_Q4K_I8> { static constexpr int BB = 144; static constexpr bool LINEAR = true;  static constexpr int XS_PER_CHUNK = 4; static constexpr bool SCALED = false; };
 template <> struct TypeInfo<T_Q6K_I8> { static constexpr int BB = 210; static constexpr bool LINEAR = false; static constexpr int XS_PER_CHUNK = 8; static constexpr bool SCALED = false; };
+template <> struct TypeInfo<T_Q5K_I8> { static constexpr int BB = 176; static constexpr bool LINEAR = true;  static constexpr int XS_PER_CHUNK = 4; static constexpr bool SCALED = false; };
+template <> struct TypeInfo<T_Q80_I8> { static constexpr int BB = 272; static constexpr bool LINEAR = true;  static constexpr int XS_PER_CHUNK = 4; static constexpr bool SCALED = false; };
+template <> struct TypeInfo<T_Q3K_I8> { static constexpr int BB = 110; static constexpr bool LINEAR = false; static constexpr int XS_PER_CHUNK = 8; static constexpr bool SCALED = false; };
 template <> struct TypeInfo<T_Q6K> { static constexpr int BB = 210; static constexpr bool LINEAR = false; static constexpr int XS_PER_CHUNK = 0; static constexpr bool SCALED = false; };
 template <> struct TypeInfo<T_Q2K> { static constexpr int BB = 84;  static constexpr bool LINEAR = false; static constexpr int XS_PER_CHUNK = 4; static constexpr bool SCALED = true; };
 template <> struct TypeInfo<T_NIB> { static constexpr int BB = 148; static constexpr bool LINEAR = true;  static constexpr int XS_PER_CHUNK = 4; static constexpr bool SCALED = true; };
@@ -232,8 +238,9 @@ constexpr uint32_t KSC_SPAN = 117 - 24;
 template <int TYPE> struct XGroup {
     // float4 per group: 32 values for the types with 32-weight sub-blocks
     // (and the int8 mode's per-32 quantization), else 16
-    static constexpr int G4 =
-        (TYPE == T_Q4K || TYPE == T_Q5K || TYPE == T_Q80 || TYPE == T_Q4K_I8) ? 8 : 4;
+    static constexpr int G4 = (TYPE == T_Q4K || TYPE == T_Q5K || TYPE == T_Q80 ||
+                               TYPE == T_Q4K_I8 || TYPE == T_Q5K_I8 || TYPE == T_Q80_I8 ||
+                               TYPE == T_Q3K_I8) ? 8 : 4;
     static constexpr bool SUMS = TypeInfo<TYPE>::XS_PER_CHUNK != 0;
     static constexpr bool I8 = (TYPE & T_I8) != 0;
     static constexpr int XSTRIDE = I8 ? XPAD_I8 : XPAD;   // float4 slots per chunk
@@ -345,10 +352,17 @@ __device__ __forceinline__ void resum(int K, int ngx, int tid, int T, const floa
 // q6k_quantize_x_q8_g16, stratum_q6k_neon.h:117-133, per 16): a lane
 // quantizes the group it loaded -- amax = max |x|, scale = fl(amax / 127),
 // inv = scale > 0 ? fl(1 / scale) : 0, q = clamp(rne(fl(x * inv)), -128,
-// 127) -- and writes the int8 values to the chunk's slot (Q4_K: sub-block
-// gi at byte 80(gi/2) + 32(gi&1); Q6_K: the 16-group at positions 16gi, run
-// t of chunk (block, half, is), at byte 80c + 16t) and {scale, sum} to the
-// group's two floats (Q4_K: 4 per chunk; Q6_K: 8).  x must be finite.
+// 127) -- and writes the int8 values to the chunk's slot and {scale, sum}
+// to the group's two floats:
+//  Q4_K, Q5_K, Q8_0 (linear chunks, per 32): group gi at byte 80(gi/2) +
+//    32(gi&1), floats 4 per chunk;
+//  Q6_K (strided chunks, per 16): the 16-group at positions 16gi is run t
+//    of chunk (block, half, is), at byte 80c + 16t, floats 8 per chunk;
+//  Q3_K (strided chunks, per 32): the group's first 16 values are run j of
+//    chunk (block, s, 0), its last 16 run j of chunk (block, s, 1) (the
+//    group covers positions 128s + 32j ..), and both chunks get its
+//    {scale, sum} in their run-j floats.
+// x must be finite.
 template <int TYPE>
 __device__ __forceinline__ void store_i8(int gidx, int per, int NC, const f32x4* v, uint8_t* xq,
                                          float* xs) {
@@ -375,19 +389,32 @@ __device__ __forceinline__ void store_i8(int gidx, int per, int NC, const f32x4*
         }
         packed[q] = w;
     }
+    constexpr int XPC = TypeInfo<TYPE>::XS_PER_CHUNK;
+    float* xsx = xs + (size_t)gx * NC * XPC;
+    if (TYPE == T_Q3K_I8) {
+        const int bi = gi >> 3, s = (gi >> 2) & 1, j = gi & 3, c0 = 4 * bi + 2 * s;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            uint4* dst = reinterpret_cast<uint4*>(xq + (size_t)(gx * NC + c0 + h) * 80 + 16 * j);
+            *dst = make_uint4(packed[4 * h], packed[4 * h + 1], packed[4 * h + 2],
+                              packed[4 * h + 3]);
+            *reinterpret_cast<float2*>(xsx + XPC * (c0 + h) + 2 * j) =
+                make_float2(scale, (float)sum);
+        }
+        return;
+    }
     int c, off, slot;
-    if (TYPE == T_Q4K_I8) {
-        c = gi >> 1; off = 32 * (gi & 1); slot = 2 * gi;
-    } else {
+    if (TYPE == T_Q6K_I8) {
         const int p = 16 * gi, bi = p >> 8, h = (p >> 7) & 1, t = (p >> 5) & 3, is = (p >> 4) & 1;
         c = 4 * bi + 2 * h + is; off = 16 * t; slot = 8 * c + 2 * t;
+    } else {
+        c = gi >> 1; off = 32 * (gi & 1); slot = 2 * gi;
     }
     uint4* dst = reinterpret_cast<uint4*>(xq + (size_t)(gx * NC + c) * 80 + off);
 #pragma unroll
     for (int q = 0; q < G4; q += 4)
         dst[q / 4] = make_uint4(packed[q], packed[q + 1], packed[q + 2], packed[q + 3]);
-    float2* xs2 = reinterpret_cast<float2*>(xs + (size_t)gx * NC * TypeInfo<TYPE>::XS_PER_CHUNK + slot);
-    *xs2 = make_float2(scale, (float)sum);
+    *reinterpret_cast<float2*>(xsx + slot) = make_float2(scale, (float)sum);
 }
 
 // ------------------------------------------------------------ raw loads
@@ -1076,8 +1103,139 @@ __device__ __forceinline__ double term_q6k_i8(const RawQ6& r, int u, const uint3
     return t;
 }
 
+// Q5_K chunk j with int8 activations (q5k_dot_row_sdot_f,
+// stratum_q5k_neon.h:158-204): Q4_K's form with the 5-bit values (nibble
+// plus 16 times the qh bit, 0..31) in the exact dots.
+__device__ __forceinline__ double term_q5k_i8(const RawQ5& r, int j, const uint32_t* xq,
+                                              float4 xs4) {
+    const float d = f16_bits_to_f32(r.hd.x & 0xffffu);
+    const float dmin = f16_bits_to_f32(r.hd.x >> 16);
+    uint32_t sc1, mn1, sc2, mn2;
+    scale_min_pair(r.hd.y, r.hd.z, r.hd.w, j, sc1, mn1, sc2, mn2);
+    const uint4 xa = reinterpret_cast<const uint4*>(xq)[0], xb = reinterpret_cast<const uint4*>(xq)[1];
+    const uint4 xc = reinterpret_cast<const uint4*>(xq)[2], xd = reinterpret_cast<const uint4*>(xq)[3];
+    const uint32_t lo_x[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+    const uint32_t hi_x[8] = {xc.x, xc.y, xc.z, xc.w, xd.x, xd.y, xd.z, xd.w};
+    const uint32_t b1 = 2u * (uint32_t)j;
+    int L = 0, H = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const uint32_t v = k < 4 ? dw_of(r.qa, k) : dw_of(r.qb, k - 4);
+        const uint32_t h = k < 4 ? dw_of(r.h0, k) : dw_of(r.h1, k - 4);
+        const uint32_t vl = (v & 0x0f0f0f0fu) | (((h >> b1) & 0x01010101u) << 4);
+        const uint32_t vh = ((v >> 4) & 0x0f0f0f0fu) | (((h >> (b1 + 1)) & 0x01010101u) << 4);
+        L = __builtin_amdgcn_sdot4((int)vl, (int)lo_x[k], L, false);
+        H = __builtin_amdgcn_sdot4((int)vh, (int)hi_x[k], H, false);
+    }
+    const float c1 = d * (float)sc1 * xs4.x, c2 = -dmin * (float)mn1 * xs4.x;
+    const float c3 = d * (float)sc2 * xs4.z, c4 = -dmin * (float)mn2 * xs4.z;
+    const double t1 = fma((double)c1, (double)L, (double)c2 * (double)xs4.y);
+    const double t2 = fma((double)c3, (double)H, (double)c4 * (double)xs4.w);
+    return t1 + t2;
+}
+
+// Q3_K chunk u = (s, h) with int8 activations per 32 (q3k_dot_row_sdot_f,
+// stratum_q3k_neon.h:84-125): group j's 16 signed 3-bit values, built as
+// the int8 32 q3 (term_q3k's bytes) so v_dot4 gives 32 times the exact dot,
+// which an arithmetic shift undoes; coefficient fl(fl(d (sc - 32)) xs) with
+// the scale of the 32-group holding the run (xs8[2j]); term c * dot exact
+// in binary64, summed over j in order.  No min term.
+__device__ __forceinline__ double term_q3k_i8(const RawQ3& r, int u, const uint32_t* xq,
+                                              const float* xs8) {
+    const int s = u >> 1, h = u & 1;
+    const uint32_t sh = r.sh;
+    const float d = f16_bits_to_f32(r.d);
+    const uint32_t S0 = __builtin_amdgcn_alignbit(r.s[1], r.s[0], sh);
+    const uint32_t S1 = __builtin_amdgcn_alignbit(r.s[2], r.s[1], sh);
+    const uint32_t S2 = __builtin_amdgcn_alignbit(r.s[3], r.s[2], sh);
+    uint32_t Q[4], M[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        Q[k] = __builtin_amdgcn_alignbit(r.q[k + 1], r.q[k], sh);
+        M[k] = __builtin_amdgcn_alignbit(r.m[k + 1], r.m[k], sh);
+    }
+    double t = 0.0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t bi = 8u * (uint32_t)(2 * (j & 1) + h);
+        const uint32_t w = (uint32_t)(2 * s + (j >> 1));
+        const uint32_t nib = bfe((w & 1u) ? S1 : S0, bi + ((w & 2u) ? 4u : 0u), 4);
+        const uint32_t hi2 = bfe(S2, bi + 2u * w, 2);
+        const float c = d * (float)((int)(nib | (hi2 << 4)) - 32) * xs8[2 * j];
+        int acc = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t lo2 = (Q[k] >> (2 * j)) & 0x03030303u;
+            const uint32_t neg = ((~M[k] >> (4 * s + j)) & 0x01010101u) << 2;
+            acc = __builtin_amdgcn_sdot4((int)((lo2 | neg) << 5), (int)xq[4 * j + k], acc, false);
+        }
+        t = t + (double)c * (double)(acc >> 5);
+    }
+    return t;
+}
+
+// Q8_0 chunk u (blocks 2u, 2u+1) with int8 activations per 32
+// (q8_0_dot_row_sdot_f, stratum_q8_0.h:112-145): per block the exact dot
+// of its int8 quants with the block's quantized x, coefficient fl(d * xs),
+// term c * dot exact in binary64; the chunk's two terms added.
+__device__ __forceinline__ double term_q80_i8(const RawQ8& r, const uint32_t* xq, float4 xs4) {
+    double t = 0.0;
+#pragma unroll
+    for (int half = 0; half < 2; half++) {
+        const float d = f16_bits_to_f32(half ? (r.w[8] >> 16) : (r.w[0] & 0xffffu));
+        int acc = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t v = half ? r.w[9 + k] : __builtin_amdgcn_alignbit(r.w[k + 1], r.w[k], 16);
+            acc = __builtin_amdgcn_sdot4((int)v, (int)xq[8 * half + k], acc, false);
+        }
+        const float c = d * (half ? xs4.z : xs4.x);
+        t = t + (double)c * (double)acc;
+    }
+    return t;
+}
+
 // ------------------------------------------------------ per-type dispatch
 template <int TYPE> struct Chunk;
+template <> struct Chunk<T_Q5K_I8> {
+    using Raw = RawQ5;
+    static __device__ __forceinline__ Raw load(wptr blk, int u) { return load_q5k(blk, u); }
+    static __device__ __forceinline__ void drain(const Raw& r) {
+        asm volatile("" ::"v"(r.hd.x), "v"(r.h0.x), "v"(r.h1.x), "v"(r.qa.x), "v"(r.qb.x));
+    }
+    template <bool SC, bool LOWREG = false>
+    static __device__ __forceinline__ double term(const Raw& r, int u, const float4* xc,
+                                                  const float* xs, int c, float, double) {
+        return term_q5k_i8(r, u, reinterpret_cast<const uint32_t*>(xc),
+                           reinterpret_cast<const float4*>(xs)[c]);
+    }
+};
+template <> struct Chunk<T_Q3K_I8> {
+    using Raw = RawQ3;
+    static __device__ __forceinline__ Raw load(wptr blk, int u) { return load_q3k(blk, u); }
+    static __device__ __forceinline__ void drain(const Raw& r) {
+        asm volatile("" ::"v"(r.q[0]), "v"(r.q[4]), "v"(r.m[0]), "v"(r.m[4]), "v"(r.s[0]),
+                     "v"(r.s[3]), "v"(r.d));
+    }
+    template <bool SC, bool LOWREG = false>
+    static __device__ __forceinline__ double term(const Raw& r, int u, const float4* xc,
+                                                  const float* xs, int c, float, double) {
+        return term_q3k_i8(r, u, reinterpret_cast<const uint32_t*>(xc), xs + 8 * c);
+    }
+};
+template <> struct Chunk<T_Q80_I8> {
+    using Raw = RawQ8;
+    static __device__ __forceinline__ Raw load(wptr blk, int u) { return load_q80(blk, u); }
+    static __device__ __forceinline__ void drain(const Raw& r) {
+        asm volatile("" ::"v"(r.w[0]), "v"(r.w[12]), "v"(r.w[16]));
+    }
+    template <bool SC, bool LOWREG = false>
+    static __device__ __forceinline__ double term(const Raw& r, int, const float4* xc,
+                                                  const float* xs, int c, float, double) {
+        return term_q80_i8(r, reinterpret_cast<const uint32_t*>(xc),
+                           reinterpret_cast<const float4*>(xs)[c]);
+    }
+};
 template <> struct Chunk<T_Q4K_I8> {
     using Raw = RawQ4;
     static __device__ __forceinline__ Raw load(wptr blk, int u) { return load_q4k(blk, u); }
@@ -1572,7 +1730,9 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
     constexpr bool SCTYPE = TI::SCALED;
     const int xst = ngx > 1 ? S.x_stride : 0;
     // x layouts: 0 strided fp32, 1 linear fp32, 2 / 3 int8 per 32 / per 16
-    constexpr int LAYOUT = XGroup<TYPE>::I8 ? (TYPE == T_Q4K_I8 ? 2 : 3) : (int)TI::LINEAR;
+    // (the int8 layouts: 2 linear chunks per 32, 3 strided per 16, 4 strided per 32)
+    constexpr int LAYOUT = !XGroup<TYPE>::I8 ? (int)TI::LINEAR
+                         : TYPE == T_Q6K_I8 ? 3 : TYPE == T_Q3K_I8 ? 4 : 2;
     // the MoE FFN step pieces of a one-segment gather launch (segment 0)
     const bool cmb = PM == PM_SEL && seg == 0 && A.cx != nullptr;   // uniform
     const bool swe = PM == PM_SEL && seg == 0 && A.act != nullptr;  // uniform
@@ -1830,6 +1990,7 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
 // four types); the host gives each of the other types launches of its own.
 constexpr int TB_Q4K = 1, TB_Q6K = 2, TB_Q2K = 4, TB_NIB = 8, TB_ALL = 15;
 constexpr int TB_Q5K = 32, TB_Q3K = 64, TB_Q80 = 128, TB_Q4K_I8 = 256, TB_Q6K_I8 = 512;
+constexpr int TB_Q5K_I8 = 1024, TB_Q3K_I8 = 2048, TB_Q80_I8 = 4096;
 // TB_SEL: the MoE gather instantiations (every segment has a selection)
 constexpr int TB_SEL = 16;
 
@@ -1862,7 +2023,8 @@ __global__ __launch_bounds__(1024) void kq_segs_kernel(SegsArg A) {
     constexpr int TYB = TYPES & ~TB_SEL;
     constexpr bool SINGLE = TYB == TB_Q4K || TYB == TB_Q6K || TYB == TB_Q2K || TYB == TB_NIB ||
                             TYB == TB_Q5K || TYB == TB_Q3K || TYB == TB_Q80 ||
-                            TYB == TB_Q4K_I8 || TYB == TB_Q6K_I8;
+                            TYB == TB_Q4K_I8 || TYB == TB_Q6K_I8 || TYB == TB_Q5K_I8 ||
+                            TYB == TB_Q3K_I8 || TYB == TB_Q80_I8;
     for (int i = 0; i < nseg; i++) {
         const Seg& S = A.s[i];
         if (i) prefetch_seg(S);
@@ -1877,7 +2039,9 @@ __global__ __launch_bounds__(1024) void kq_segs_kernel(SegsArg A) {
             constexpr int TY = TYB == TB_Q4K ? T_Q4K : TYB == TB_Q6K ? T_Q6K
                              : TYB == TB_Q2K ? T_Q2K : TYB == TB_NIB ? T_NIB
                              : TYB == TB_Q5K ? T_Q5K : TYB == TB_Q3K ? T_Q3K
-                             : TYB == TB_Q80 ? T_Q80 : TYB == TB_Q4K_I8 ? T_Q4K_I8 : T_Q6K_I8;
+                             : TYB == TB_Q80 ? T_Q80 : TYB == TB_Q4K_I8 ? T_Q4K_I8
+                             : TYB == TB_Q6K_I8 ? T_Q6K_I8 : TYB == TB_Q5K_I8 ? T_Q5K_I8
+                             : TYB == TB_Q3K_I8 ? T_Q3K_I8 : T_Q80_I8;
             KQ_RUN(TY)
         } else {
             switch (S.type) {
@@ -3668,6 +3832,9 @@ static int xs_per_chunk(int type) {
     case T_Q80: return TypeInfo<T_Q80>::XS_PER_CHUNK;
     case T_Q4K_I8: return TypeInfo<T_Q4K_I8>::XS_PER_CHUNK;
     case T_Q6K_I8: return TypeInfo<T_Q6K_I8>::XS_PER_CHUNK;
+    case T_Q5K_I8: return TypeInfo<T_Q5K_I8>::XS_PER_CHUNK;
+    case T_Q3K_I8: return TypeInfo<T_Q3K_I8>::XS_PER_CHUNK;
+    case T_Q80_I8: return TypeInfo<T_Q80_I8>::XS_PER_CHUNK;
     default: return -1;
     }
 }
@@ -3683,6 +3850,9 @@ static int block_bytes_of(int type) {
     case T_Q80: return TypeInfo<T_Q80>::BB;
     case T_Q4K_I8: return TypeInfo<T_Q4K_I8>::BB;
     case T_Q6K_I8: return TypeInfo<T_Q6K_I8>::BB;
+    case T_Q5K_I8: return TypeInfo<T_Q5K_I8>::BB;
+    case T_Q3K_I8: return TypeInfo<T_Q3K_I8>::BB;
+    case T_Q80_I8: return TypeInfo<T_Q80_I8>::BB;
     default: return 0;
     }
 }
@@ -3699,6 +3869,9 @@ static int type_slot(int type) {
     case T_Q80: return 7;
     case T_Q4K_I8: return 8;
     case T_Q6K_I8: return 9;
+    case T_Q5K_I8: return 10;
+    case T_Q3K_I8: return 11;
+    case T_Q80_I8: return 12;
     default: return -1;
     }
 }
@@ -3748,34 +3921,40 @@ long kqk_segs_lds(const kqk_seg* segs, int nseg, int grid, int* xs_off, int* ter
 }
 
 // Every instantiation, indexed by [multi][depth - 1][slot]: slots 0..3 and
-// 5..7 single types (type_slot), 4 the mixed-type kernel.
+// 5..7 single types (type_slot), 4 the mixed-type kernel, 8..12 the int8
+// mode of Q4_K, Q6_K, Q5_K, Q3_K and Q8_0.
+constexpr int NSLOT = 13;
 #define KQ_SEGS_ROW(D, M)                                                       \
     {&kq_segs_kernel<D, TB_Q4K, M>, &kq_segs_kernel<D, TB_Q6K, M>,              \
      &kq_segs_kernel<D, TB_Q2K, M>, &kq_segs_kernel<D, TB_NIB, M>,              \
      &kq_segs_kernel<D, TB_ALL, M>, &kq_segs_kernel<D, TB_Q5K, M>,              \
      &kq_segs_kernel<D, TB_Q3K, M>, &kq_segs_kernel<D, TB_Q80, M>,              \
-     &kq_segs_kernel<D, TB_Q4K_I8, M>, &kq_segs_kernel<D, TB_Q6K_I8, M>}
+     &kq_segs_kernel<D, TB_Q4K_I8, M>, &kq_segs_kernel<D, TB_Q6K_I8, M>,        \
+     &kq_segs_kernel<D, TB_Q5K_I8, M>, &kq_segs_kernel<D, TB_Q3K_I8, M>,        \
+     &kq_segs_kernel<D, TB_Q80_I8, M>}
 typedef void (*segs_fn)(SegsArg);
-static const segs_fn k_segs[2][2][10] = {{KQ_SEGS_ROW(1, false), KQ_SEGS_ROW(2, false)},
-                                        {KQ_SEGS_ROW(1, true), KQ_SEGS_ROW(2, true)}};
+static const segs_fn k_segs[2][2][NSLOT] = {{KQ_SEGS_ROW(1, false), KQ_SEGS_ROW(2, false)},
+                                           {KQ_SEGS_ROW(1, true), KQ_SEGS_ROW(2, true)}};
 #undef KQ_SEGS_ROW
-// the MoE gather (TB_SEL) instantiations, single type only (slots 4, 8
-// and 9 unused: the mixed kernel and the int8 mode have no gather form)
+// the MoE gather (TB_SEL) instantiations, single type only (slots 4 and
+// 8..12 unused: the mixed kernel and the int8 mode have no gather form)
 #define KQ_SEL_ROW(D, M)                                                                  \
     {&kq_segs_kernel<D, TB_Q4K | TB_SEL, M>, &kq_segs_kernel<D, TB_Q6K | TB_SEL, M>,       \
      &kq_segs_kernel<D, TB_Q2K | TB_SEL, M>, &kq_segs_kernel<D, TB_NIB | TB_SEL, M>,       \
      &kq_segs_kernel<D, TB_Q4K | TB_SEL, M>, &kq_segs_kernel<D, TB_Q5K | TB_SEL, M>,       \
      &kq_segs_kernel<D, TB_Q3K | TB_SEL, M>, &kq_segs_kernel<D, TB_Q80 | TB_SEL, M>,       \
-     &kq_segs_kernel<D, TB_Q4K | TB_SEL, M>, &kq_segs_kernel<D, TB_Q4K | TB_SEL, M>}
-static const segs_fn k_segs_sel[2][2][10] = {{KQ_SEL_ROW(1, false), KQ_SEL_ROW(2, false)},
-                                            {KQ_SEL_ROW(1, true), KQ_SEL_ROW(2, true)}};
+     &kq_segs_kernel<D, TB_Q4K | TB_SEL, M>, &kq_segs_kernel<D, TB_Q4K | TB_SEL, M>,       \
+     &kq_segs_kernel<D, TB_Q4K | TB_SEL, M>, &kq_segs_kernel<D, TB_Q4K | TB_SEL, M>,       \
+     &kq_segs_kernel<D, TB_Q4K | TB_SEL, M>}
+static const segs_fn k_segs_sel[2][2][NSLOT] = {{KQ_SEL_ROW(1, false), KQ_SEL_ROW(2, false)},
+                                               {KQ_SEL_ROW(1, true), KQ_SEL_ROW(2, true)}};
 #undef KQ_SEL_ROW
 
 int kqk_set_max_lds(int bytes) {
     for (int m = 0; m < 2; m++)
         for (int d = 0; d < 2; d++)
-            for (int t = 0; t < 20; t++) {
-                const segs_fn f = t < 10 ? k_segs[m][d][t] : k_segs_sel[m][d][t - 10];
+            for (int t = 0; t < 2 * NSLOT; t++) {
+                const segs_fn f = t < NSLOT ? k_segs[m][d][t] : k_segs_sel[m][d][t - NSLOT];
                 const hipError_t e =
                     hipFuncSetAttribute(reinterpret_cast<const void*>(f),
                                         hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
@@ -3839,11 +4018,14 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
         magic_for((uint32_t)(h.K >> 6), d.nc_m, d.nc_l);
         set |= h.type == T_Q4K ? TB_Q4K : h.type == T_Q6K ? TB_Q6K : h.type == T_Q2K ? TB_Q2K
              : h.type == T_NIB ? TB_NIB : h.type == T_Q5K ? TB_Q5K : h.type == T_Q3K ? TB_Q3K
-             : h.type == T_Q80 ? TB_Q80 : h.type == T_Q4K_I8 ? TB_Q4K_I8 : TB_Q6K_I8;
+             : h.type == T_Q80 ? TB_Q80 : h.type == T_Q4K_I8 ? TB_Q4K_I8
+             : h.type == T_Q6K_I8 ? TB_Q6K_I8 : h.type == T_Q5K_I8 ? TB_Q5K_I8
+             : h.type == T_Q3K_I8 ? TB_Q3K_I8 : TB_Q80_I8;
     }
     const int t = set == TB_Q4K ? 0 : set == TB_Q6K ? 1 : set == TB_Q2K ? 2 : set == TB_NIB ? 3
                 : set == TB_Q5K ? 5 : set == TB_Q3K ? 6 : set == TB_Q80 ? 7
-                : set == TB_Q4K_I8 ? 8 : set == TB_Q6K_I8 ? 9
+                : set == TB_Q4K_I8 ? 8 : set == TB_Q6K_I8 ? 9 : set == TB_Q5K_I8 ? 10
+                : set == TB_Q3K_I8 ? 11 : set == TB_Q80_I8 ? 12
                 : (set & ~TB_ALL) ? -1 : 4;
     if (t < 0) return (int)hipErrorInvalidValue;   // other types are never mixed in a launch
     if (t == 4) depth = 1;   // the all-types kernel fits 128 VGPRs at depth 1 only

@@ -71,11 +71,17 @@ __attribute__((visibility("hidden"))) int kq_fail(const char* fmt, ...) {
 
 const char* kq_last_error(void) { return g_kq.err; }
 
+/* the types with an int8-activation (SDOT) form: st_linear_q4k, _q6k,
+ * _q5k, _q3k and _q8_0 under g_st.use_sdot (stratum_linear.h:369-489) */
+static int has_sdot(int type) {
+    return type == KQ_TYPE_Q4_K || type == KQ_TYPE_Q6_K || type == KQ_TYPE_Q5_K ||
+           type == KQ_TYPE_Q3_K || type == KQ_TYPE_Q8_0;
+}
+
 /* bytes per 256 weights (stratum_gguf.h:57-79; Q8_0: eight 34-byte blocks);
- * the int8-activation mode of Q4_K / Q6_K (KQ_INT8_ACT) keeps the blocks */
+ * the int8-activation mode (KQ_INT8_ACT) keeps the blocks */
 static int block_bytes(int type) {
-    if (type == (KQ_INT8_ACT | KQ_TYPE_Q4_K)) return 144;
-    if (type == (KQ_INT8_ACT | KQ_TYPE_Q6_K)) return 210;
+    if ((type & KQ_INT8_ACT) && has_sdot(type & ~KQ_INT8_ACT)) type &= ~KQ_INT8_ACT;
     switch (type) {
     case KQ_TYPE_F32: return 1024;
     case KQ_TYPE_F16: return 512;
@@ -667,12 +673,11 @@ int kq_dequant_dev(int type, const void* w, float* y, int64_t nblocks, kq_stream
 
 /* --------------------------------------------------- host-pointer ABI */
 
-/* st_linear_q4k / st_linear_q6k take the SDOT (int8-activation) path when
- * g_st.use_sdot is set (stratum_linear.h:369-409): the same switch for the
- * host-pointer entry points */
+/* st_linear_q4k, _q6k, _q5k, _q3k and _q8_0 take the SDOT
+ * (int8-activation) path when g_st.use_sdot is set (stratum_linear.h:
+ * 369-489): the same switch for the host-pointer entry points */
 static int sdot_type(int type) {
-    return g_kq.use_sdot && (type == KQ_TYPE_Q4_K || type == KQ_TYPE_Q6_K) ? type | KQ_INT8_ACT
-                                                                          : type;
+    return g_kq.use_sdot && has_sdot(type) ? type | KQ_INT8_ACT : type;
 }
 
 int kq_linear_set_sdot(int on) {

@@ -1,5 +1,6 @@
-"""GPU parity of the int8-activation mode (type | KQ_INT8_ACT, Q4_K and
-Q6_K: the reference's SDOT path, stratum_linear.h:376-404) against the CPU
+"""GPU parity of the int8-activation mode (type | KQ_INT8_ACT, Q4_K, Q6_K,
+Q5_K, Q3_K and Q8_0: the reference's SDOT path, stratum_linear.h:376-489)
+against the CPU
 oracle's restatement (oracle/kq_oracle.c ko_gemv_i8, pinned by
 tests/test_oracle_i8.py).
 
@@ -21,13 +22,13 @@ import pytest
 import stratum_amd as K
 from conftest import same_values
 from i8_cases import reciprocal_groups
-from stratum_amd import INT8_ACT, TYPE_Q4_K, TYPE_Q6_K, synth
+from stratum_amd import INT8_ACT, TYPE_Q3_K, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0, synth
 
 pytestmark = pytest.mark.gpu
 
 torch = pytest.importorskip("torch")
-I8_TYPES = [TYPE_Q4_K, TYPE_Q6_K]
-GROUP = {TYPE_Q4_K: 32, TYPE_Q6_K: 16}
+I8_TYPES = [TYPE_Q4_K, TYPE_Q6_K, TYPE_Q5_K, TYPE_Q3_K, TYPE_Q8_0]
+GROUP = {TYPE_Q4_K: 32, TYPE_Q6_K: 16, TYPE_Q5_K: 32, TYPE_Q3_K: 32, TYPE_Q8_0: 32}
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -118,11 +119,16 @@ def test_gemv_shapes(port, qtype, N, Kd):
 
 def pow2_blocks(qtype, r, nblocks):
     b = synth.blocks(qtype, r, nblocks).reshape(nblocks, -1)
-    if qtype == TYPE_Q4_K:
-        b[:, 0:2] = np.array([2.0 ** -10], np.float16).view(np.uint8)
-        b[:, 2:4] = np.array([2.0 ** -12], np.float16).view(np.uint8)
+    f16 = lambda v: np.array([v], np.float16).view(np.uint8)   # noqa: E731
+    if qtype in (TYPE_Q4_K, TYPE_Q5_K):
+        b[:, 0:2] = f16(2.0 ** -10)
+        b[:, 2:4] = f16(2.0 ** -12)
+    elif qtype == TYPE_Q6_K:
+        b[:, 208:210] = f16(2.0 ** -10)
+    elif qtype == TYPE_Q3_K:
+        b[:, 108:110] = f16(2.0 ** -10)
     else:
-        b[:, 208:210] = np.array([2.0 ** -10], np.float16).view(np.uint8)
+        b.reshape(nblocks, 8, 34)[:, :, 0:2] = f16(2.0 ** -10)
     return b.reshape(-1)
 
 
@@ -142,7 +148,9 @@ def test_gemv_exact_inputs(port, qtype):
 
 
 @pytest.mark.parametrize("qtype,N,Kd", [(TYPE_Q4_K, 6144, 5120), (TYPE_Q4_K, 17408, 5120),
-                                        (TYPE_Q6_K, 5120, 17408), (TYPE_Q6_K, 1024, 5120)])
+                                        (TYPE_Q6_K, 5120, 17408), (TYPE_Q6_K, 1024, 5120),
+                                        (TYPE_Q5_K, 17408, 5120), (TYPE_Q3_K, 17408, 5120),
+                                        (TYPE_Q8_0, 5120, 17408)])
 def test_gemv_config_shapes(port, qtype, N, Kd, kq_env):
     """27B-class shapes: sampled rows against the oracle, a bit-identical
     rerun and the same bits under 37 workgroups of 256 lanes."""
@@ -230,10 +238,12 @@ def test_multix_equals_single_stream(qtype):
 
 def test_host_abi_sdot_switch(port):
     """kq_linear_set_sdot routes the host-pointer entry points through the
-    int8 mode for Q4_K and Q6_K (as g_st.use_sdot does) and leaves other
-    types alone; switching it off restores the exact path."""
+    int8 mode for Q4_K, Q6_K, Q5_K, Q3_K and Q8_0 (as g_st.use_sdot does,
+    stratum_linear.h:376-489) and leaves other types (Q2_K) alone;
+    switching it off restores the exact path."""
     Kd = 1024
-    specs = [(TYPE_Q4_K, 300), (TYPE_Q6_K, 200), (10, 64)]
+    specs = [(TYPE_Q4_K, 300), (TYPE_Q6_K, 200), (10, 64), (TYPE_Q5_K, 96), (TYPE_Q3_K, 80),
+             (TYPE_Q8_0, 72)]
     parts, tensors, off = [], [], 0
     for i, (t, N) in enumerate(specs):
         wb = synth.tensor(t, N, Kd, 8900 + i)
@@ -269,7 +279,8 @@ def test_host_abi_sdot_switch(port):
 
 
 def test_refused_forms():
-    """No MoE, matrix-core or non-Q4_K/Q6_K int8 form: refused with -1."""
+    """No matrix-core int8 form, and no int8 form of Q2_K, type 42, F16 or
+    F32: refused with -1."""
     N, Kd = 64, 512
     w = dev(synth.tensor(TYPE_Q4_K, N, Kd, 9000))
     x = dev(synth.gaussian(synth.rng(9001), 2 * Kd))
@@ -279,4 +290,7 @@ def test_refused_forms():
                                      y.data_ptr(), 2, N, Kd, None) == -1
     assert L.kq_gemv_dev(10 | INT8_ACT, w.data_ptr(), x.data_ptr(), None, y.data_ptr(), N, Kd,
                          None) == -1
-    assert L.kq_row_bytes(13 | INT8_ACT, Kd) == -1
+    for t in (10, 42, 0, 1):
+        assert L.kq_row_bytes(t | INT8_ACT, Kd) == -1, t
+    for t in (TYPE_Q5_K, TYPE_Q3_K, TYPE_Q8_0):
+        assert L.kq_row_bytes(t | INT8_ACT, Kd) == L.kq_row_bytes(t, Kd)

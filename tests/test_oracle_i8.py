@@ -22,10 +22,10 @@ import numpy as np
 import pytest
 
 from i8_cases import reciprocal_groups
-from stratum_amd import TYPE_Q4_K, TYPE_Q6_K, synth
+from stratum_amd import TYPE_Q3_K, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0, synth
 
-I8_TYPES = [TYPE_Q4_K, TYPE_Q6_K]
-GROUP = {TYPE_Q4_K: 32, TYPE_Q6_K: 16}
+I8_TYPES = [TYPE_Q4_K, TYPE_Q6_K, TYPE_Q5_K, TYPE_Q3_K, TYPE_Q8_0]
+GROUP = {TYPE_Q4_K: 32, TYPE_Q6_K: 16, TYPE_Q5_K: 32, TYPE_Q3_K: 32, TYPE_Q8_0: 32}
 
 
 def exact_x(r, K, G, e):
@@ -100,19 +100,32 @@ def test_quantize_error_bound(port, G):
 
 def pow2_blocks(qtype, r, nblocks, small=False):
     """random blocks with d = 2^-10 (and dmin = 2^-12), so every product is
-    exact; small: scales (and mins) limited to 3 bits, so that the
-    reference's binary32 lanes stay exact too over one block"""
+    exact; small: scales (and mins) limited to 3 bits (Q3_K: sc - 32 in
+    0..3; Q8_0: quants in -8..7), so that the reference's binary32 lanes
+    stay exact too over one block"""
     b = synth.blocks(qtype, r, nblocks).reshape(nblocks, -1)
-    if qtype == TYPE_Q4_K:
-        b[:, 0:2] = np.array([2.0 ** -10], np.float16).view(np.uint8)
-        b[:, 2:4] = np.array([2.0 ** -12], np.float16).view(np.uint8)
+    f16 = lambda v: np.array([v], np.float16).view(np.uint8)   # noqa: E731
+    if qtype in (TYPE_Q4_K, TYPE_Q5_K):
+        b[:, 0:2] = f16(2.0 ** -10)
+        b[:, 2:4] = f16(2.0 ** -12)
         if small:
             b[:, 4:16] = synth.pack_q4k_scales(r.integers(0, 8, (nblocks, 8)),
                                                r.integers(0, 8, (nblocks, 8)))
-    else:
-        b[:, 208:210] = np.array([2.0 ** -10], np.float16).view(np.uint8)
+    elif qtype == TYPE_Q6_K:
+        b[:, 208:210] = f16(2.0 ** -10)
         if small:
             b[:, 192:208] = r.integers(-4, 4, (nblocks, 16)).astype(np.int8).view(np.uint8)
+    elif qtype == TYPE_Q3_K:
+        b[:, 108:110] = f16(2.0 ** -10)
+        if small:   # every 6-bit scale 32 + (0..3): low nibbles 0..3, top bits 2
+            lo = r.integers(0, 4, (nblocks, 8, 2))
+            b[:, 96:104] = (lo[:, :, 0] | (lo[:, :, 1] << 4)).astype(np.uint8)
+            b[:, 104:108] = 0xAA
+    else:            # Q8_0: eight 34-byte blocks per 256 weights
+        u = b.reshape(nblocks, 8, 34)
+        u[:, :, 0:2] = f16(2.0 ** -10)
+        if small:
+            u[:, :, 2:34] = r.integers(-8, 8, (nblocks, 8, 32)).astype(np.int8).view(np.uint8)
     return b.reshape(-1)
 
 
@@ -135,22 +148,37 @@ def test_i8_exact_against_dequant(port, qtype, case):
 
 @pytest.mark.parametrize("qtype", I8_TYPES)
 def test_i8_reference_quant_test_case(port, qtype):
-    """quant_test.c:95-122 (Q4_K) / :196-237 (Q6_K) data, rel err <= 5e-2"""
+    """quant_test.c's data and relation for each type's SDOT form, rel err
+    <= 5e-2 against the exact dot: Q4_K :95-122, Q6_K :196-237, Q5_K
+    :150-187 (d 0.01, dmin 0.001), Q3_K :245-275 (d 0.01), Q8_0 :45-88
+    (d 0.01 + U(0, 1), random int8 quants); random bytes elsewhere.  The
+    reference asserts the relation on one dot of its own seed; over several
+    rows, the signed types (Q3_K, Q8_0) can cancel to a dot far below its
+    terms, so the relative error is taken against max(|dot|, 0.1 sum |w x|)."""
     r = synth.rng(7400 + qtype)
     N, K = 8, 1024
-    b = r.integers(0, 256, (N * K // 256, 144 if qtype == TYPE_Q4_K else 210), dtype=np.uint8)
-    if qtype == TYPE_Q4_K:
-        b[:, 0:2] = np.array([0.01], np.float16).view(np.uint8)
-        b[:, 2:4] = np.array([0.001], np.float16).view(np.uint8)
+    bb = K // 256 * synth.row_bytes(qtype, 256)
+    b = r.integers(0, 256, (N * K // 256, bb // (K // 256)), dtype=np.uint8)
+    f16 = lambda v: np.array(v, np.float16).view(np.uint8)   # noqa: E731
+    if qtype in (TYPE_Q4_K, TYPE_Q5_K):
+        b[:, 0:2] = f16([0.01])
+        b[:, 2:4] = f16([0.001])
+    elif qtype == TYPE_Q6_K:
+        b[:, 208:210] = f16([0.01])
+    elif qtype == TYPE_Q3_K:
+        b[:, 108:110] = f16([0.01])
     else:
-        b[:, 208:210] = np.array([0.01], np.float16).view(np.uint8)
+        u = b.reshape(-1, 8, 34)
+        d = (0.01 + r.integers(0, 0x10000, (u.shape[0], 8)) / 65535.0).astype(np.float16)
+        u[:, :, 0:2] = d.view(np.uint8).reshape(u.shape[0], 8, 2)
     w = b.reshape(-1)
     x = (r.integers(0, 0x10000, K) / 32768.0 - 0.5).astype(np.float32)
     deq = port.dequant(qtype, w, N, K).reshape(N, K).astype(np.float64)
     ref = (deq * x.astype(np.float64)).sum(axis=1).astype(np.float32)
+    mag = (np.abs(deq) * np.abs(x.astype(np.float64))).sum(axis=1)
     for sdot_f in (True, False):
         y = port.gemv_i8(qtype, w, x, N, K, sdot_f=sdot_f)
-        rel = np.abs(y - ref) / np.maximum(np.abs(ref), 1e-6)
+        rel = np.abs(y - ref) / np.maximum(np.maximum(np.abs(ref), 0.1 * mag), 1e-6)
         assert rel.max() <= 5e-2, (sdot_f, rel.max())
 
 
