@@ -177,7 +177,18 @@ int kq_quantize_x_q8_dev(const float* x, int K, int group, int8_t* xq, float* xs
 int kq_gemv_dev(int type, const void* w, const float* x, const float* add, float* y,
                 int N, int K, kq_stream stream);
 
-/* Contiguous multix: ys[s*N + r] = row r . xs[s*K ...] for s < B. */
+/* Contiguous multix: ys[s*N + r] = row r . xs[s*K ...] for s < B, one
+ * weight pass; each stream equals its kq_gemv_dev result bit for bit.
+ * Exception, as in the reference: Q4_K and Q6_K in the int8 mode at B >= 2
+ * compute st_linear_multix's int8 arithmetic under use_sdot
+ * (stratum_linear.h:732-907, q4k_dot_rows2_sdot_multix_pack /
+ * q6k_dot_rows2_sdot_multix_pack, stratum_q4k_neon.h:870-948,
+ * stratum_q6k_neon.h:627-700) bit for bit: one binary32 term per Q4_K
+ * sub-block (binary64 per Q6_K 16-group) summed in binary64 in element
+ * order, which differs from the single-stream SDOT form's rounding (the
+ * reference's own quant_test.c holds the two within 1e-4).  That path
+ * runs the integer dots on the matrix cores and uses the library's
+ * matrix-core workspace (grown on demand, see kq_reserve_mfma_workspace). */
 int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,
                        int B, int N, int K, kq_stream stream);
 

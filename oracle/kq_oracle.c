@@ -739,6 +739,80 @@ int ko_gemv_i8(int type, const uint8_t* w, const float* x, const float* add, flo
     return 0;
 }
 
+/* The int8 MULTISEQ of st_linear_multix under g_st.use_sdot, B >= 2
+ * (stratum_linear.h:732-907): every stream quantized as the single-stream
+ * form quantizes it (per 32, q4k_quantize_x_q8_1b, stratum_q4k_neon.h:
+ * 185-226, the same rule as q4k_quantize_x_q8; per 16 for Q6_K,
+ * q6k_quantize_x_q8_g16), then per (row, stream) a binary64 sum in element
+ * order of one term per sub-block / 16-group:
+ *   Q4_K (q4k_dot_rows2_sdot_multix_pack, stratum_q4k_neon.h:870-948):
+ *     fl(fl(fl(d*sc) * fl(fl(L) * scl)) - fl(fl(dmin*m) * fl(fl(S) * scl)))
+ *     with L the exact dot of the 4-bit values and S the group's int8 sum;
+ *   Q6_K (q6k_dot_rows2_sdot_multix_pack, stratum_q6k_neon.h:627-700):
+ *     (((double)d * sc) * (double)scl) * (double)A, binary64, with A the
+ *     exact dot of the signed values q - 32.
+ * The rows2 kernels take every row pair (the i8mm rows4 path keeps their
+ * merge order, stratum_q4k_neon.h:1066-1071); the single-row multix_pack
+ * form, used for an odd last row, is the same arithmetic except at B = 7,
+ * where it takes a binary32-accumulating variant (q4k_dot_row_sdot_pack_b7)
+ * that is not restated here. */
+int ko_gemv_i8_multix(int type, const uint8_t* w, const float* xs, float* ys, int B, int N,
+                      int K) {
+    if ((type != KO_Q4_K && type != KO_Q6_K) || K % 256 || B < 1) return -1;
+    const int G = type == KO_Q4_K ? 32 : 16, ng = K / G;
+    int8_t* xq = malloc((size_t)B * K);
+    float* sc = malloc((size_t)B * ng * sizeof(float));
+    int32_t* sm = malloc((size_t)B * ng * sizeof(int32_t));
+    if (!xq || !sc || !sm) { free(xq); free(sc); free(sm); return -1; }
+    for (int s = 0; s < B; s++) {
+        ko_quantize_x_q8(xs + (size_t)s * K, K, G, xq + (size_t)s * K, sc + (size_t)s * ng);
+        xsums(xq + (size_t)s * K, K, G, sm + (size_t)s * ng);
+    }
+    const size_t rb = (size_t)(K / 256) * (size_t)ko_block_bytes(type);
+    for (int r = 0; r < N; r++) {
+        const uint8_t* row = w + (size_t)r * rb;
+        for (int s = 0; s < B; s++) {
+            const int8_t* x8 = xq + (size_t)s * K;
+            const float* scl = sc + (size_t)s * ng;
+            const int32_t* S = sm + (size_t)s * ng;
+            double dot = 0.0;
+            for (int b = 0; b < K / 256; b++) {
+                if (type == KO_Q4_K) {
+                    const uint8_t* blk = row + (size_t)b * 144;
+                    const float d = ko_fp16_to_fp32(rd16(blk)), dmin = ko_fp16_to_fp32(rd16(blk + 2));
+                    for (int sb = 0; sb < 8; sb++) {
+                        const int g = 8 * b + sb;
+                        uint8_t scv, mn;
+                        ko_q4k_scale_min(sb, blk + 4, &scv, &mn);
+                        const float d_sc = d * (float)scv, dmin_m = dmin * (float)mn;
+                        int32_t L = 0;
+                        for (int l = 0; l < 32; l++) L += (int32_t)q4k_q(blk, sb, l) * x8[32 * g + l];
+                        const float s_f = (float)S[g];
+                        dot += (double)(d_sc * ((float)L * scl[g]) - dmin_m * (s_f * scl[g]));
+                    }
+                } else {
+                    const uint8_t* blk = row + (size_t)b * 210;
+                    const float d = ko_fp16_to_fp32(rd16(blk + 208));
+                    const int8_t* sc8 = (const int8_t*)(blk + 192);
+                    for (int h = 0; h < 2; h++)
+                        for (int is = 0; is < 2; is++)
+                            for (int t = 0; t < 4; t++) {
+                                const int gl = 8 * h + is + 2 * t, g = 16 * b + gl;
+                                int32_t acc = 0;
+                                for (int l = 0; l < 16; l++)
+                                    acc += (int32_t)q6k_q(blk, h, t, 16 * is + l) * x8[16 * g + l];
+                                const double ds = (double)d * (double)sc8[gl];
+                                dot += ds * (double)scl[g] * (double)acc;
+                            }
+                }
+            }
+            ys[(size_t)s * N + r] = (float)dot;
+        }
+    }
+    free(xq); free(sc); free(sm);
+    return 0;
+}
+
 /* ------------------------------------------------------------ dispatch */
 void ko_dequant_row(int type, const uint8_t* row, int K, float* y) {
     const int bb = ko_block_bytes(type);

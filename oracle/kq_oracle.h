@@ -108,6 +108,10 @@ int ko_gemv_multix(int type, const uint8_t* w, const float* xs, float* ys,
 void ko_quantize_x_q8(const float* x, int K, int G, int8_t* xq, float* xscale);
 int ko_gemv_i8(int type, const uint8_t* w, const float* x, const float* add, float* y,
                double* mag, int N, int K, int sdot_f);
+/* int8 MULTISEQ (st_linear_multix under use_sdot, B >= 2; Q4_K / Q6_K):
+ * ys[s * N + r], the reference's multix_pack arithmetic. 0, or -1. */
+int ko_gemv_i8_multix(int type, const uint8_t* w, const float* xs, float* ys, int B, int N,
+                      int K);
 
 /* type-42 permutation (148-byte blocks) and its inverse */
 void ko_q2k_to_nib(const uint8_t* q2k, uint8_t* nib, int64_t nblocks);

@@ -81,6 +81,7 @@ class Port:
         L.ko_quantize_x_q8.argtypes = [_F, I, I, ctypes.POINTER(ctypes.c_int8), _F]
         L.ko_quantize_x_q8.restype = None
         L.ko_gemv_i8.argtypes = [I, _U8, _F, _F, _F, ctypes.POINTER(ctypes.c_double), I, I, I]
+        L.ko_gemv_i8_multix.argtypes = [I, _U8, _F, _F, I, I, I]
         L.ko_softmax.argtypes = [_F, I]
         L.ko_softmax.restype = None
         L.ko_swiglu.argtypes = [_F, _F, _F, ctypes.c_int64]
@@ -156,6 +157,15 @@ class Port:
                                if with_mag else None, N, K, int(sdot_f))
         assert rc == 0
         return (y, mag) if with_mag else y
+
+    def gemv_i8_multix(self, qtype, w, xs, N, K):
+        """int8 MULTISEQ (the reference's multix_pack arithmetic): ys [B, N]"""
+        xs = np.ascontiguousarray(xs, np.float32)
+        B = xs.shape[0]
+        ys = np.empty((B, N), np.float32)
+        rc = self.L.ko_gemv_i8_multix(qtype, _u8(w), _f(xs), _f(ys), B, N, K)
+        assert rc == 0
+        return ys
 
     def softmax(self, x: np.ndarray) -> np.ndarray:
         """softmax of each row of x (copied)"""

@@ -45,6 +45,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "kq_launch.h"
 
 
@@ -3364,6 +3366,346 @@ int launch_mfma_t(const float* x, const void* w, float* y, int B, int N, int K, 
 }
 
 // --------------------------------------------------------------- dequant
+// ------------------------------------------------- int8 MULTISEQ (MFMA)
+// st_linear_multix under g_st.use_sdot for Q4_K / Q6_K, B >= 2
+// (stratum_linear.h:732-907): every stream's x quantized as the
+// single-stream int8 mode quantizes it (kq_mi8_prep_kernel), then per
+// (row, stream) the reference's multix_pack arithmetic, bit for bit:
+//  Q4_K (q4k_dot_rows2_sdot_multix_pack, stratum_q4k_neon.h:870-948): per
+//    sub-block the binary32 term fl(fl(fl(d*sc) * fl(fl(L) * scl)) -
+//    fl(fl(dmin*m) * fl(fl(S) * scl))), added to a binary64 sum in element
+//    order (L the exact dot of the 4-bit values, S the group's int8 sum);
+//  Q6_K (q6k_dot_rows2_sdot_multix_pack, stratum_q6k_neon.h:627-700): per
+//    16-group ((double)d * sc * (double)scl) * (double)A in binary64, A the
+//    exact dot of q - 32.
+// The integer dots run on the matrix cores (v_mfma_i32_16x16x64_i8, exact
+// in int32), the terms and the sequential binary64 sums on the VALU.
+//
+// Operands.  One MFMA: A = 16 rows of x operands (i), B = 16 weight rows
+// (j), 64 k-values: lane l gives A[l % 16][16 (l/16) .. +15] and
+// B[..][l % 16] for the same 16 k-values, so any assignment of the chunk's
+// positions to (l / 16, byte) is summed correctly as long as A and B use the
+// same one: here byte b of lane group q is chunk position 16q + b.
+//  Q4_K: A row i = (stream i/2, sub-block i&1) holds that stream's x only
+//    at the sub-block's positions (q >> 1 == i & 1), zero elsewhere, so
+//    D[i][j] is the sub-block's dot: 8 streams x both sub-blocks per MFMA.
+//  Q6_K: A row i = (stream i/4, run i&3) holds x only at run i&3's 16
+//    positions (q == i & 3): 4 streams x the chunk's 4 runs per MFMA.
+// D[i][j] lands in lane j + 16 (i/4), register i % 4: a lane holds its
+// weight row's dots for 2 streams x 2 sub-blocks (Q4_K) or 1 stream x 4
+// runs (Q6_K), in the order its binary64 sums need them.
+//
+// Work.  A wave owns 16 rows and SW streams for the whole row (the sums are
+// sequential in k); a workgroup's 4 waves take 4 neighbouring row blocks
+// with the same streams, whose quantized x and coefficients for one
+// super-block are staged in LDS (double-buffered, one barrier per
+// super-block) and read by all four.  Weights and staging data are loaded
+// P super-blocks ahead into registers: the x, coefficient and weight loads
+// of a super-block are issued together, so the in-order wait for one never
+// waits on data needed later.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+struct Mi8Arg {
+    const uint8_t* w;         // N rows of K weights (Q4_K / Q6_K blocks)
+    const int8_t* xq;         // [B][K] quantized streams
+    const uint8_t* zp;        // 64 zero bytes
+    const uint8_t* cf;        // per (stream, group) coefficients: Q4_K float2
+                              // {scl, fl(fl(S) * scl)} [B][K/32]; Q6_K double
+                              // scl [B][K/16]
+    float* y;                 // y[s * y_stride + r]
+    long y_stride;
+    int N, K, B;
+};
+
+// x -> int8 per group (the single-stream rule, kq_quantize_kernel's) and
+// the coefficients the main kernel needs, one thread per (stream, group).
+// Streams B .. bpad - 1 (the padding up to the main kernel's stream
+// count) get zero values and coefficients, so their terms are 0.
+// It also zeroes the 256-byte zero page zp.
+template <int G>
+__global__ __launch_bounds__(256) void kq_mi8_prep_kernel(const float* x, long x_stride, int K,
+                                                          int B, int bpad, int8_t* xq,
+                                                          uint8_t* cf, uint8_t* zp) {
+    const int ng = K / G;
+    const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+    if (gid < 16) reinterpret_cast<uint4*>(zp)[gid] = make_uint4(0, 0, 0, 0);
+    if (gid >= (long)ng * bpad) return;
+    const int s = (int)(gid / ng), g = (int)(gid - (long)s * ng);
+    const f32x4* src =
+        reinterpret_cast<const f32x4*>(x + (size_t)min(s, B - 1) * x_stride) + (size_t)g * (G / 4);
+    f32x4 v[G / 4];
+#pragma unroll
+    for (int k = 0; k < G / 4; k++) v[k] = s < B ? src[k] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < G / 4; k++)
+        amax = fmaxf(fmaxf(fmaxf(amax, fabsf(v[k].x)), fmaxf(fabsf(v[k].y), fabsf(v[k].z))),
+                     fabsf(v[k].w));
+    const float scale = __fdiv_rn(amax, 127.0f);
+    const float inv = scale > 0.0f ? __fdiv_rn(1.0f, scale) : 0.0f;
+    int sum = 0;
+    uint32_t* dst = reinterpret_cast<uint32_t*>(xq + (size_t)s * K + (size_t)g * G);
+#pragma unroll
+    for (int k = 0; k < G / 4; k++) {
+        const float e[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+        uint32_t w = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int iv = min(127, max(-128, __float2int_rn(e[i] * inv)));
+            sum += iv;
+            w |= ((uint32_t)iv & 0xffu) << (8 * i);
+        }
+        dst[k] = w;
+    }
+    if (G == 32)
+        reinterpret_cast<float2*>(cf)[gid] = make_float2(scale, (float)sum * scale);
+    else
+        reinterpret_cast<double*>(cf)[gid] = (double)scale;
+}
+
+// Weight registers of one super-block of one lane's row.
+//  Q4_K: the header and, of each chunk's 32 quant bytes, the half lane
+//    group q reads (16 (q & 1) ..).
+//  Q6_K (lane group q = run t): for each chunk u = (half h, is) the 16 ql
+//    bytes run t takes its nibbles from (64h + 16is + 32 (t & 1)) and the
+//    16 qh bytes (128 + 32h + 16is), each as 5 dwords from the dword-aligned
+//    address below (realigned by sh: 210-byte blocks are only 2-byte
+//    aligned); the 16 scale bytes and d.
+struct Mi8W4 { uint4 hd, qv[4]; };
+struct Mi8W6 { uint32_t l[4][5], h[4][5], s[5]; uint32_t d, sh; };
+
+// Shape of one launch: SW streams per wave (8 streams x 2 sub-blocks per
+// Q4_K MFMA, 4 streams x 4 runs per Q6_K MFMA), P super-blocks of loads in
+// flight, and a workgroup of KS waves on one 16-row block, one K-part each.
+// A wave needs no other wave until the end: its weights, its A operands
+// (loaded per lane straight from the quantized streams; lanes whose A row
+// is zero at their positions read the workspace's zero page) and its
+// coefficients all come through its own register ring, and it stages the
+// coefficients in its own LDS region (LDS operations of one wave complete
+// in order, so no barrier).  The KS partial sums of a row are added in LDS
+// in K-part order at the end: the binary64 sum is grouped by K-part -- a
+// fixed order, like the single-stream kernel's phases (the result equals
+// the reference's strictly sequential sum unless a binary64 re-association
+// crosses a binary32 rounding boundary).
+template <int TYPE, int SW, int P, int KS>
+__global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
+    constexpr bool Q4 = TYPE == T_Q4K_I8;
+    constexpr int NM = Q4 ? SW / 8 : SW / 4;        // MFMAs per chunk
+    constexpr int NACC = Q4 ? 2 * NM : NM;          // binary64 sums per lane
+    constexpr int CB = Q4 ? 64 : 128;               // coefficient bytes per stream and super-block
+    constexpr int CU = SW * CB / 16, CPT = (CU + 63) / 64;
+    constexpr int DEC = Q4 ? 16 * 4 * 16 : 0;       // Q4_K: decoded d*sc, dmin*m per (chunk, row)
+    constexpr int WL = SW * CB + DEC;               // LDS bytes per wave
+    constexpr int STAGE = KS * WL, COMB = KS * 64 * NACC * 8;
+    __shared__ __align__(16) uint8_t lds[STAGE > COMB ? STAGE : COMB];
+    using W = typename std::conditional<Q4, Mi8W4, Mi8W6>::type;
+
+    const int tid = threadIdx.x, lane = tid & 63, kp = tid >> 6;
+    const int q = lane >> 4, jr = lane & 15;
+    const int N = A.N, K = A.K, nb = K >> 8;
+    const int ng = Q4 ? K >> 5 : K >> 4;            // coefficient groups per stream
+    const int rb = blockIdx.x, s0 = blockIdx.y * SW;
+    const int row = min(rb * 16 + jr, N - 1);
+    constexpr int BB = Q4 ? 144 : 210;
+    const wptr wr = to_global(A.w) + (size_t)row * (size_t)nb * BB;
+    const int nbp = (nb + KS - 1) / KS;             // super-blocks per K-part
+    const int kb0 = kp * nbp, kb1 = min(nb, kb0 + nbp);
+    uint8_t* wl = lds + kp * WL;                    // this wave's LDS
+    // (xq and cf hold a multiple of 16 streams: streams past B are zero;
+    // zp is 64 zero bytes)
+    const uint8_t* cf = A.cf;
+    // this lane's A row holds x at its positions: Q4_K row (stream jr/2,
+    // sub-block jr&1) at lane groups q >> 1 == jr & 1; Q6_K row (stream
+    // jr/4, run jr&3) at lane group q == jr & 3.  Its x: stream sa + NS m,
+    // chunk position offset qo; else the zero page.
+    const bool on = Q4 ? (q >> 1) == (jr & 1) : q == (jr & 3);
+    const int sa = s0 + (Q4 ? jr >> 1 : jr >> 2), NS = Q4 ? 8 : 4;
+    const uint8_t* xa0 = reinterpret_cast<const uint8_t*>(A.xq) + (size_t)sa * K;
+    const uint8_t* zp = A.zp;
+
+    struct Slot { W w; i32x4 a[4][NM]; uint4 c[CPT]; };
+    auto load = [&](int b, Slot& sl) {
+        const wptr blk = wr + (size_t)b * BB;
+        if constexpr (Q4) {
+            sl.w.hd = ld16(blk);
+#pragma unroll
+            for (int j = 0; j < 4; j++) sl.w.qv[j] = ld16(blk + 16 + 32 * j + 16 * (q & 1));
+        } else {
+            const uint32_t mis = (uint32_t)reinterpret_cast<uintptr_t>(blk) & 3u;
+            sl.w.sh = mis * 8u;
+            const wptr b4 = blk - mis;
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int h = u >> 1, is = u & 1;
+                load5(b4 + 64 * h + 16 * is + 32 * (q & 1), sl.w.l[u]);
+                load5(b4 + 128 + 32 * h + 16 * is, sl.w.h[u]);
+            }
+            // the scales' fifth dword only when 2 bytes off (else dword 3
+            // again: the last block is never read past its 210 bytes)
+            sl.w.s[0] = ld4(b4 + 192); sl.w.s[1] = ld4(b4 + 196);
+            sl.w.s[2] = ld4(b4 + 200); sl.w.s[3] = ld4(b4 + 204);
+            sl.w.s[4] = ld4(b4 + (mis ? 208 : 204));
+            sl.w.d = ld2(blk + 208);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int m = 0; m < NM; m++) {
+                // chunk j's positions of this lane: Q4_K 64j + 16q; Q6_K run
+                // q of chunk (h, is) at 128h + 32q + 16is
+                const int qo = Q4 ? 64 * j + 16 * q : 128 * (j >> 1) + 32 * q + 16 * (j & 1);
+                const uint8_t* src = on ? xa0 + (size_t)NS * m * K + 256 * (size_t)b + qo : zp;
+                sl.a[j][m] = *reinterpret_cast<const i32x4*>(src);
+            }
+        constexpr int CPS = CB / 16;                // uint4 of coefficients per stream
+#pragma unroll
+        for (int k = 0; k < CPT; k++) {
+            const int v = min(lane + 64 * k, CU - 1), sc = s0 + v / CPS;
+            sl.c[k] = *reinterpret_cast<const uint4*>(
+                cf + ((size_t)sc * ng + (size_t)b * (CB / 8)) * 8 + 16 * (v % CPS));
+        }
+    };
+
+    double acc[NACC];
+#pragma unroll
+    for (int a = 0; a < NACC; a++) acc[a] = 0.0;
+    const i32x4 zero = {0, 0, 0, 0};
+    // A ring of R = P + 1 register slots: step i computes slot i % R and
+    // reloads slot (i + P) % R, which step i - 1 finished with, for
+    // super-block i + P.  The loop body is R steps with no exit (the steps
+    // past the K-part only reload), so every slot keeps its registers around
+    // the loop and no load in flight is waited for early to move one.
+    constexpr int R = P + 1;
+    Slot ring[R];
+#pragma unroll
+    for (int p = 0; p < P; p++) load(min(kb0 + p, nb - 1), ring[p]);
+    const int nit = (nbp + R - 1) / R * R;
+    for (int i0 = 0; i0 < nit; i0 += R) {
+#pragma unroll
+        for (int p = 0; p < R; p++) {
+            const int b = kb0 + i0 + p;
+            const Slot& cur = ring[p];
+            const bool go = b < kb1;                 // uniform
+            // the next loads go out first: waiting for this step's slot
+            // then leaves them in flight
+            load(min(b + P, nb - 1), ring[(p + P) % R]);
+            if (go) {
+                // the coefficients into this wave's LDS (unconditional
+                // stores: a lane past the last piece stores it again)
+                constexpr int CPS = CB / 16;
+#pragma unroll
+                for (int k = 0; k < CPT; k++) {
+                    const int v = min(lane + 64 * k, CU - 1);
+                    *reinterpret_cast<uint4*>(wl + CB * (v / CPS) + 16 * (v % CPS)) = cur.c[k];
+                }
+                if constexpr (Q4) {
+                    // lane group q decodes chunk q of its row: d*sc, dmin*m of
+                    // sub-blocks 2q, 2q+1 (shared with the other groups)
+                    const float d = f16_bits_to_f32(cur.w.hd.x & 0xffffu);
+                    const float dmin = f16_bits_to_f32(cur.w.hd.x >> 16);
+                    uint32_t sc1, mn1, sc2, mn2;
+                    scale_min_pair(cur.w.hd.y, cur.w.hd.z, cur.w.hd.w, q, sc1, mn1, sc2, mn2);
+                    *reinterpret_cast<float4*>(wl + SW * CB + 16 * (16 * q + jr)) =
+                        make_float4(d * (float)sc1, dmin * (float)mn1, d * (float)sc2,
+                                    dmin * (float)mn2);
+                }
+            }
+            if (!go) continue;
+            if constexpr (Q4) {
+                const uint32_t sh = 4u * (uint32_t)(q >> 1);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float4 dm = *reinterpret_cast<const float4*>(wl + SW * CB + 16 * (16 * j + jr));
+                    const uint4 qv = cur.w.qv[j];
+                    const i32x4 bop = {(int)((qv.x >> sh) & 0x0f0f0f0fu),
+                                       (int)((qv.y >> sh) & 0x0f0f0f0fu),
+                                       (int)((qv.z >> sh) & 0x0f0f0f0fu),
+                                       (int)((qv.w >> sh) & 0x0f0f0f0fu)};
+#pragma unroll
+                    for (int m = 0; m < NM; m++) {
+                        const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.a[j][m], bop, zero,
+                                                                              0, 0, 0);
+                        // D[2e + sb]: stream 8m + 2q + e, sub-block sb
+#pragma unroll
+                        for (int e = 0; e < 2; e++) {
+                            const float4 c = *reinterpret_cast<const float4*>(
+                                wl + 64 * (8 * m + 2 * q + e) + 16 * j);
+                            const float tl = dm.x * ((float)D[2 * e] * c.x) - dm.y * c.y;
+                            acc[2 * m + e] = acc[2 * m + e] + (double)tl;
+                            const float th = dm.z * ((float)D[2 * e + 1] * c.z) - dm.w * c.w;
+                            acc[2 * m + e] = acc[2 * m + e] + (double)th;
+                        }
+                    }
+                    // one chunk at a time: hoisting the next chunk's LDS
+                    // reads over this one only costs registers
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            } else {
+                const double d = (double)f16_bits_to_f32(cur.w.d);
+                uint32_t S[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    S[k] = __builtin_amdgcn_alignbit(cur.w.s[k + 1], cur.w.s[k], cur.w.sh);
+                const uint32_t tsh = 4u * (uint32_t)(q >> 1), hsh = 2u * (uint32_t)q;
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int h = u >> 1, is = u & 1;
+                    // this row's d * sc for the chunk's four runs (scale 8h + is + 2t)
+                    double ds[4];
+#pragma unroll
+                    for (int t = 0; t < 4; t++) {
+                        const int g = 8 * h + is + 2 * t;
+                        ds[t] = d * (double)(int8_t)(uint8_t)(S[g >> 2] >> (8 * (g & 3)));
+                    }
+                    uint32_t bw[4];
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        const uint32_t L = __builtin_amdgcn_alignbit(cur.w.l[u][k + 1], cur.w.l[u][k], cur.w.sh);
+                        const uint32_t H = __builtin_amdgcn_alignbit(cur.w.h[u][k + 1], cur.w.h[u][k], cur.w.sh);
+                        const uint32_t v = ((L >> tsh) & 0x0f0f0f0fu) | (((H >> hsh) & 0x03030303u) << 4);
+                        bw[k] = ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u;   // bytes v - 32
+                    }
+                    const i32x4 bop = {(int)bw[0], (int)bw[1], (int)bw[2], (int)bw[3]};
+#pragma unroll
+                    for (int m = 0; m < NM; m++) {
+                        const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.a[u][m], bop, zero,
+                                                                              0, 0, 0);
+                        // D[t]: stream 4m + q, run t
+                        const double* cs = reinterpret_cast<const double*>(wl + 128 * (4 * m + q));
+#pragma unroll
+                        for (int t = 0; t < 4; t++)
+                            acc[m] = acc[m] + ds[t] * cs[8 * h + is + 2 * t] * (double)D[t];
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        }
+    }
+    // the K-parts' partial sums, added in K-part order
+    double* part = reinterpret_cast<double*>(lds);
+    if (KS > 1) {
+        __syncthreads();
+#pragma unroll
+        for (int a = 0; a < NACC; a++) part[(kp * 64 + lane) * NACC + a] = acc[a];
+        __syncthreads();
+        if (kp != 0) return;
+#pragma unroll
+        for (int a = 0; a < NACC; a++) {
+            double v = part[lane * NACC + a];
+#pragma unroll
+            for (int k = 1; k < KS; k++) v = v + part[(k * 64 + lane) * NACC + a];
+            acc[a] = v;
+        }
+    }
+    const int r = rb * 16 + jr;
+    if (r >= N) return;
+#pragma unroll
+    for (int a = 0; a < NACC; a++) {
+        const int so = Q4 ? s0 + 8 * (a >> 1) + 2 * q + (a & 1) : s0 + 4 * a + q;
+        if (so < A.B) A.y[(size_t)so * A.y_stride + r] = (float)acc[a];
+    }
+}
+
 // Bit-exact dequantization, one lane per 64-weight chunk (64 floats out).
 template <int TYPE>
 __global__ __launch_bounds__(256) void kq_dequant_kernel(const uint8_t* __restrict__ w,
@@ -4426,6 +4768,81 @@ int kqk_launch_dense(int type, const void* w, const float* x, const float* add, 
     if (sb == 1) { KQ_DENSE_SB(1) } else { KQ_DENSE_SB(DENSE_SB) }
 #undef KQ_DENSE_SB
 #undef KQ_DENSE_GO
+    return (int)hipGetLastError();
+}
+
+// int8 MULTISEQ on the matrix cores: workspace bytes (quantized streams,
+// then their coefficients, 256-byte aligned), and the launches (prep, main).
+int kqk_mi8_parts(int K) {
+    // measured over 1, 2, 4 and 8 parts at B = 8, 16, 64: the 27B gate
+    // (20 super-blocks) is fastest with 2 (1 at B = 8 by 10 %), the down
+    // projection (68) with 4 (2 at B = 16 by 9 %); 8 was never fastest
+    const int nb = K >> 8;
+    return nb >= 48 ? 4 : nb >= 12 ? 2 : 1;
+}
+
+// (streams padded to a multiple of 16, the widest wave's stream count)
+long kqk_mi8_workspace(int type, int B, int K, long* cf_off) {
+    if ((type != T_Q4K_I8 && type != T_Q6K_I8) || B < 1 || K < 256 || (K & 255)) return -1;
+    const long bp = (B + 15) & ~15L;
+    const long xb = (bp * K + 255) & ~255L;
+    const long cb = bp * (type == T_Q4K_I8 ? K / 32 : K / 16) * 8;
+    *cf_off = xb;
+    return xb + ((cb + 255) & ~255L) + 256;     // + the zero page
+}
+
+int kqk_launch_mi8(int type, const float* xs, long x_stride, const void* w, float* ys,
+                   long y_stride, int B, int N, int K, void* ws, int ks, hipStream_t st) {
+    long cf_off = 0;
+    const long wsb = kqk_mi8_workspace(type, B, K, &cf_off);
+    if (wsb < 0 || N < 1 || B < 2 || (x_stride & 3) || x_stride < K || y_stride < N ||
+        ((uintptr_t)xs & 15) || ((uintptr_t)ws & 255))
+        return (int)hipErrorInvalidValue;
+    int8_t* xq = static_cast<int8_t*>(ws);
+    uint8_t* cf = static_cast<uint8_t*>(ws) + cf_off;
+    uint8_t* zp = static_cast<uint8_t*>(ws) + wsb - 256;   // zeroed by the prep kernel
+    const int G = type == T_Q4K_I8 ? 32 : 16;
+    const int bpad = (B + 15) & ~15;
+    const long groups = (long)bpad * (K / G);
+    if (G == 32)
+        hipLaunchKernelGGL(kq_mi8_prep_kernel<32>, dim3((unsigned)((groups + 255) / 256)), dim3(256),
+                           0, st, xs, x_stride, K, B, bpad, xq, cf, zp);
+    else
+        hipLaunchKernelGGL(kq_mi8_prep_kernel<16>, dim3((unsigned)((groups + 255) / 256)), dim3(256),
+                           0, st, xs, x_stride, K, B, bpad, xq, cf, zp);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    Mi8Arg a;
+    a.w = static_cast<const uint8_t*>(w);
+    a.xq = xq;
+    a.zp = zp;
+    a.cf = cf;
+    a.y = ys;
+    a.y_stride = y_stride;
+    a.N = N; a.K = K; a.B = B;
+    // Q4_K: 8 or 16 streams per wave; Q6_K: 8 (its A operands take
+    // 16 registers per MFMA and super-block)
+    const int SW = type == T_Q6K_I8 || B <= 8 ? 8 : 16;
+    const int nset = (B + SW - 1) / SW, nrb = (N + 15) / 16;
+    // K-parts: a function of the row length only (kqk_mi8_parts), so the
+    // binary64 grouping -- and with it the result -- does not depend on the
+    // batch or the row count
+    if (ks != 1 && ks != 2 && ks != 4 && ks != 8) ks = kqk_mi8_parts(K);
+#define KQ_MI8_GO(T_, S_, P_, K_)                                                            \
+    hipLaunchKernelGGL((kq_mi8_kernel<T_, S_, P_, K_>), dim3((unsigned)nrb, (unsigned)nset),  \
+                       dim3(64 * K_), 0, st, a)
+#define KQ_MI8_KS(T_, S_, P_)                                                                \
+    if (ks == 1) KQ_MI8_GO(T_, S_, P_, 1);                                                   \
+    else if (ks == 2) KQ_MI8_GO(T_, S_, P_, 2);                                              \
+    else if (ks == 4) KQ_MI8_GO(T_, S_, P_, 4);                                              \
+    else KQ_MI8_GO(T_, S_, P_, 8);
+    if (type == T_Q4K_I8) {
+        if (SW == 8) { KQ_MI8_KS(T_Q4K_I8, 8, 2) } else { KQ_MI8_KS(T_Q4K_I8, 16, 1) }
+    } else {
+        KQ_MI8_KS(T_Q6K_I8, 8, 1)
+    }
+#undef KQ_MI8_KS
+#undef KQ_MI8_GO
     return (int)hipGetLastError();
 }
 

@@ -94,6 +94,15 @@ int kqk_mfma_workspace(int type, int B, int N, int K, int grid, long* planes, lo
 int kqk_noalloc_scratch(void** ptr, long* bytes);
 int kqk_launch_mfma(int type, const float* x, const void* w, float* y, int B, int N, int K,
                     void* planes, float* xs, float* part, int grid, hipStream_t st);
+/* int8 MULTISEQ on the matrix cores (Q4_K / Q6_K | KQ_INT8_ACT, B >= 2):
+ * workspace bytes (*cf_off: offset of the coefficients), or -1; the
+ * launch (prep + main kernel) with ws 256-byte aligned; ks: K-parts per
+ * row block (1, 2, 4 or 8; anything else: kqk_mi8_parts(K), the rule the
+ * library uses -- the grouping of the binary64 sums follows it) */
+long kqk_mi8_workspace(int type, int B, int K, long* cf_off);
+int kqk_mi8_parts(int K);
+int kqk_launch_mi8(int type, const float* xs, long x_stride, const void* w, float* ys,
+                   long y_stride, int B, int N, int K, void* ws, int ks, hipStream_t st);
 int kqk_launch_moe_group(const int* sel, int nm, int E, int nt, int x_div, int mch,
                          const void* w0, const void* w1, float* y0, float* y1, long estride,
                          void* groups, int* ng, hipStream_t st);

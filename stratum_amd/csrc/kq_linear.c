@@ -527,9 +527,26 @@ static long mx_plan(int type, int N, int K, int mmax, int ngmax, int grid, const
     return lds;
 }
 
+static int mfma_reserve(size_t need);
+
+/* The int8 MULTISEQ of st_linear_multix under use_sdot (Q4_K / Q6_K, B >= 2,
+ * stratum_linear.h:732-907): streams quantized into the library's
+ * matrix-core workspace, then one weight pass on the matrix cores with the
+ * reference's multix_pack arithmetic. */
+static int mi8_multix(int type, const void* w, const float* xs, float* ys, int B, int N, int K,
+                      hipStream_t st) {
+    long cf_off = 0;
+    const long need = kqk_mi8_workspace(type, B, K, &cf_off);
+    if (need < 0) return kq_fail("int8 multix: bad shape B=%d K=%d", B, K);
+    if (mfma_reserve((size_t)need)) return -1;
+    const int e = kqk_launch_mi8(type, xs, K, w, ys, N, B, N, K, g_kq.d_mf, 0, st);
+    if (e) return kq_fail("int8 multix launch: %s", hipGetErrorString((hipError_t)e));
+    return 0;
+}
+
 /* B streams with one pass over the weights per group of up to 64 streams
  * (the multi-x kernel); each stream's y equals its single-stream result bit
- * for bit. */
+ * for bit, except in the int8 mode of Q4_K / Q6_K (mi8_multix). */
 int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,
                        int B, int N, int K, kq_stream stream) {
     if (B < 1) return kq_fail("kq_gemv_multix_dev: B=%d", B);
@@ -537,6 +554,8 @@ int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,
     if (!w || !xs || !ys) return kq_fail("kq_gemv_multix_dev: NULL pointer");
     if ((uintptr_t)xs & 15) return kq_fail("kq_gemv_multix_dev: xs must be 16-byte aligned");
     if (is_dense(type) && B > 1) return dense_gemv(type, w, xs, NULL, ys, N, K, B, pick(stream));
+    if (B > 1 && (type == (KQ_INT8_ACT | KQ_TYPE_Q4_K) || type == (KQ_INT8_ACT | KQ_TYPE_Q6_K)))
+        return mi8_multix(type, w, xs, ys, B, N, K, pick(stream));
     if (B == 1 || !is_core(type)) {   /* per-stream launches: the same bits as single calls */
         for (int s = 0; s < B; s++)
             if (kq_gemv_dev(type, w, xs + (size_t)s * K, NULL, ys + (size_t)s * N, N, K, stream))

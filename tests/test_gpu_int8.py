@@ -221,8 +221,10 @@ def test_segments_groups_strided_x(port, qtype):
         assert same_values(y[g], gpu_gemv(qtype | INT8_ACT, ws[g], xs[g], N, H)), g
 
 
-@pytest.mark.parametrize("qtype", I8_TYPES)
+@pytest.mark.parametrize("qtype", [TYPE_Q5_K, TYPE_Q3_K, TYPE_Q8_0])
 def test_multix_equals_single_stream(qtype):
+    """the int8 types without a matrix-core MULTISEQ form: per-stream
+    launches, each stream bit-identical to its single-stream result"""
     N, Kd, B = 100, 1024, 5
     w = synth.tensor(qtype, N, Kd, 8800)
     xs = np.stack([synth.gaussian(synth.rng(8801 + s), Kd) for s in range(B)])
@@ -266,6 +268,11 @@ def test_host_abi_sdot_switch(port):
             assert same_values(K.linear_dispatch_add(d, x, add, N, Kd), add + y), t
             xs = [synth.gaussian(synth.rng(8970 + s), Kd) for s in range(3)]
             ys = K.linear_multix(d, xs, N, Kd)
+            if t in (TYPE_Q4_K, TYPE_Q6_K):      # st_linear_multix's int8 arithmetic
+                want = port.gemv_i8_multix(t, wb, np.stack(xs), N, Kd)
+                for s in range(3):
+                    assert same_values(ys[s], want[s]), (t, s)
+                continue
             for s in range(3):
                 assert same_values(ys[s], K.linear_dispatch(d, xs[s], N, Kd)), (t, s)
         (d0, _, _, n0), (d1, _, _, n1) = tensors[:2]
@@ -294,3 +301,70 @@ def test_refused_forms():
         assert L.kq_row_bytes(t | INT8_ACT, Kd) == -1, t
     for t in (TYPE_Q5_K, TYPE_Q3_K, TYPE_Q8_0):
         assert L.kq_row_bytes(t | INT8_ACT, Kd) == L.kq_row_bytes(t, Kd)
+
+
+# ------------------------------------ int8 MULTISEQ on the matrix cores
+MX_TYPES = [TYPE_Q4_K, TYPE_Q6_K]
+
+
+def gpu_multix_i8(qtype, dw, dx, B, N, Kd):
+    dy = torch.full((B * N,), float("nan"), dtype=torch.float32, device="cuda")
+    K.gemv_multix_dev(qtype | INT8_ACT, dw.data_ptr(), dx.data_ptr(), dy.data_ptr(), B, N, Kd,
+                      stream=stream())
+    torch.cuda.synchronize()
+    return dy.cpu().numpy().reshape(B, N)
+
+
+@pytest.mark.parametrize("qtype", MX_TYPES)
+@pytest.mark.parametrize("B,N,Kd", [(2, 100, 1024), (5, 33, 512), (8, 130, 2048), (16, 64, 4096),
+                                    (17, 70, 768), (33, 96, 1280), (64, 200, 2048)])
+def test_multix_i8_matches_reference_pack(port, qtype, B, N, Kd):
+    """Q4_K / Q6_K int8 MULTISEQ (B >= 2) on the matrix cores: every stream
+    bit-identical to the oracle's restatement of the reference's
+    q*_dot_rows2_sdot_multix_pack arithmetic (streams not a multiple of the
+    wave's 8/16/32, rows not a multiple of 16 or 64)"""
+    w = synth.tensor(qtype, N, Kd, 9100 + B)
+    xs = np.stack([synth.gaussian(synth.rng(9110 + s), Kd) for s in range(B)])
+    print(f"int8 mfma multix type={qtype} B={B} N={N} K={Kd}", flush=True)
+    got = gpu_multix_i8(qtype, dev(w), dev(xs.reshape(-1)), B, N, Kd)
+    want = port.gemv_i8_multix(qtype, w, xs, N, Kd)
+    exact = int(np.sum(got.view(np.uint32) == want.view(np.uint32)))
+    print(f"  bit-identical {exact}/{want.size}", flush=True)
+    assert same_values(got, want)
+
+
+@pytest.mark.parametrize("qtype,N,Kd,B", [(TYPE_Q4_K, 17408, 5120, 8), (TYPE_Q4_K, 17408, 5120, 16),
+                                          (TYPE_Q4_K, 17408, 5120, 64), (TYPE_Q6_K, 5120, 17408, 16),
+                                          (TYPE_Q6_K, 5120, 17408, 64)])
+def test_multix_i8_27b_sampled(port, qtype, N, Kd, B):
+    """configs[3] shapes (27B gate / down) at B = 8, 16, 64: 256 sampled rows
+    of every stream bit-identical to the oracle's pack arithmetic, and two
+    streams within the terms' rounding bound of the single-stream int8 form"""
+    w = synth.tensor(qtype, N, Kd, 9200 + qtype)
+    xs = np.stack([synth.gaussian(synth.rng(9210 + s), Kd) for s in range(B)])
+    print(f"int8 mfma multix 27B type={qtype} B={B}", flush=True)
+    dw, dx = dev(w), dev(xs.reshape(-1))
+    got = gpu_multix_i8(qtype, dw, dx, B, N, Kd)
+    rows = np.random.default_rng(5 + B).choice(N, 256, replace=False)
+    rb = K.lib().kq_row_bytes(qtype, Kd)
+    sub = np.concatenate([w[r * rb:(r + 1) * rb] for r in rows])
+    want = port.gemv_i8_multix(qtype, sub, xs, rows.size, Kd)
+    assert same_values(got[:, rows], want)
+    for s in (0, B - 1):
+        y1 = gpu_gemv(qtype | INT8_ACT, w, xs[s], N, Kd)
+        _, mag = port.gemv_i8(qtype, sub, xs[s], rows.size, Kd, sdot_f=True, with_mag=True)
+        d = np.abs(got[s, rows].astype(np.float64) - y1[rows].astype(np.float64))
+        assert np.all(d <= 5 * 2.0 ** -24 * mag + np.spacing(np.abs(y1[rows]))), s
+
+
+def test_multix_i8_repeatable_and_strided_launch_shapes(port):
+    """two launches give the same bits; B = 1 stays the single-stream form"""
+    qtype, N, Kd, B = TYPE_Q4_K, 300, 3072, 24
+    w = synth.tensor(qtype, N, Kd, 9300)
+    xs = np.stack([synth.gaussian(synth.rng(9310 + s), Kd) for s in range(B)])
+    dw, dx = dev(w), dev(xs.reshape(-1))
+    a = gpu_multix_i8(qtype, dw, dx, B, N, Kd)
+    b = gpu_multix_i8(qtype, dw, dx, B, N, Kd)
+    assert same_values(a, b)
+    one = gpu_multix_i8(qtype, dw, dx, 1, N, Kd)
+    assert same_values(one[0], gpu_gemv(qtype | INT8_ACT, w, xs[0], N, Kd))

@@ -208,3 +208,67 @@ def test_i8_add(port, qtype):
     y = port.gemv_i8(qtype, w, x, N, K)
     ya = port.gemv_i8(qtype, w, x, N, K, add=add)
     assert np.array_equal(ya, add + y)
+
+
+# ------------------------------------------------- int8 MULTISEQ (pack form)
+MX_TYPES = [TYPE_Q4_K, TYPE_Q6_K]
+
+
+@pytest.mark.parametrize("qtype", MX_TYPES)
+def test_i8_multix_exact_against_dequant(port, qtype):
+    """the multix_pack arithmetic on exact inputs (power-of-two d / dmin,
+    3-bit scales and mins, exactly quantizable x): every term is exact, so
+    each stream's y == fl(sum dequant(w) * x)"""
+    r = synth.rng(7700 + qtype)
+    N, K, B = 20, 512, 3
+    w = pow2_blocks(qtype, r, N * K // 256, small=True)
+    xs = np.stack([exact_x(r, K, GROUP[qtype], -7 + s)[0] for s in range(B)])
+    deq = port.dequant(qtype, w, N, K).reshape(N, K).astype(np.float64)
+    want = (xs.astype(np.float64) @ deq.T).astype(np.float32)
+    assert np.array_equal(port.gemv_i8_multix(qtype, w, xs, N, K), want)
+
+
+@pytest.mark.parametrize("qtype", MX_TYPES)
+def test_i8_multix_reference_relation(port, qtype):
+    """quant_test.c:126-145 (Q4_K) / :228-238 (Q6_K): on the reference's
+    data (d 0.01, dmin 0.001, x uniform in [-0.5, 0.5)), B = 4 streams of
+    the pack form within 1e-4 relative of q*_dot_row_sdot_f (the
+    single-stream lanes), and within 5e-2 of the exact dot (relative to
+    max(|dot|, 0.1 sum |w x|), as random signed Q6_K rows can cancel)"""
+    r = synth.rng(7800 + qtype)
+    N, K, B = 8, 1024, 4
+    b = r.integers(0, 256, (N * K // 256, 144 if qtype == TYPE_Q4_K else 210), dtype=np.uint8)
+    if qtype == TYPE_Q4_K:
+        b[:, 0:2] = np.array([0.01], np.float16).view(np.uint8)
+        b[:, 2:4] = np.array([0.001], np.float16).view(np.uint8)
+    else:
+        b[:, 208:210] = np.array([0.01], np.float16).view(np.uint8)
+    w = b.reshape(-1)
+    xs = (r.integers(0, 0x10000, (B, K)) / 32768.0 - 0.5).astype(np.float32)
+    ys = port.gemv_i8_multix(qtype, w, xs, N, K)
+    deq = port.dequant(qtype, w, N, K).reshape(N, K).astype(np.float64)
+    for s in range(B):
+        fy = port.gemv_i8(qtype, w, xs[s], N, K, sdot_f=True)
+        assert np.all(np.abs(ys[s] - fy) <= 1e-4 * np.maximum(np.abs(fy), 1e-6)), s
+        ref = deq @ xs[s].astype(np.float64)
+        mag = np.abs(deq) @ np.abs(xs[s].astype(np.float64))
+        assert np.all(np.abs(ys[s] - ref) <= 5e-2 * np.maximum(np.abs(ref), 0.1 * mag)), s
+
+
+@pytest.mark.parametrize("qtype", MX_TYPES)
+def test_i8_multix_within_term_bound_of_binary64_terms(port, qtype):
+    """each pack term rounds at most four times in binary32 (Q4_K; Q6_K's
+    are binary64): against the exact-term binary64 order of the
+    single-stream form the difference stays within 5 2^-24 sum|term| plus
+    one ulp"""
+    r = synth.rng(7900 + qtype)
+    N, K, B = 48, 4096, 5
+    w = synth.blocks(qtype, r, N * K // 256)
+    xs = np.stack([synth.gaussian(r, K) for _ in range(B)])
+    ys = port.gemv_i8_multix(qtype, w, xs, N, K)
+    for s in range(B):
+        yg = port.gemv_i8(qtype, w, xs[s], N, K)
+        _, mag = port.gemv_i8(qtype, w, xs[s], N, K, sdot_f=True, with_mag=True)
+        d = np.abs(ys[s].astype(np.float64) - yg.astype(np.float64))
+        bound = 5 * 2.0 ** -24 * mag + np.spacing(np.abs(yg)).astype(np.float64)
+        assert np.all(d <= bound), s
