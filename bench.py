@@ -305,6 +305,53 @@ def multiseq_mfma(L, torch, stream, host_w) -> dict:
     return res
 
 
+MFMA_I8_PEAK_TOPS = 5000.0
+
+
+def multiseq_int8(L, torch, stream, host_w) -> dict:
+    """configs[3] in the int8-activation mode: kq_gemv_multix_dev(type |
+    KQ_INT8_ACT), which for Q4_K / Q6_K at B >= 2 computes st_linear_multix's
+    use_sdot arithmetic (the reference's multix_pack: a binary32 term per
+    Q4_K sub-block, binary64 per Q6_K 16-group, summed in binary64) with the
+    integer dots on the matrix cores (v_mfma_i32_16x16x64_i8).
+    Time per call (quantization launch included) with HIP events; TOP/s
+    counts the product's 2*N*K*B integer ops; mfma_util the int8 MFMA ops
+    the kernel issues (operand rows masked to one sub-block (Q4_K) or one
+    16-run (Q6_K) of the 64 k-values: 2x and 4x the product's) against the
+    dense int8 peak.  Distance to the single-stream int8 form
+    (kq_gemv_dev(type | KQ_INT8_ACT)): max |a - b| / max(|b|, 1e-6)."""
+    sh = stream.cuda_stream
+    res = {}
+    for name, t, N, K in (("ffn_gate", 12, 17408, 5120), ("ffn_up", 12, 17408, 5120),
+                          ("ffn_down", 14, 5120, 17408)):
+        cm = _copies(torch, host_w[name])
+        for B in (8, 16, 32, 64):
+            xs = torch.from_numpy(np.stack([synth.gaussian(synth.rng(4100 + s), K)
+                                            for s in range(B)])).cuda()
+            ym = torch.empty(B * N, dtype=torch.float32, device="cuda")
+            us = _events_us(torch, stream, lambda i: _check(L, L.kq_gemv_multix_dev(
+                t | KQ.INT8_ACT, cm[i % len(cm)].data_ptr(), xs.data_ptr(), ym.data_ptr(), B,
+                N, K, sh)), 20)
+            _check(L, L.kq_gemv_multix_dev(t | KQ.INT8_ACT, cm[0].data_ptr(), xs.data_ptr(),
+                                           ym.data_ptr(), B, N, K, sh))
+            y1 = torch.empty(N, dtype=torch.float32, device="cuda")
+            _check(L, L.kq_gemv_dev(t | KQ.INT8_ACT, cm[0].data_ptr(), xs.data_ptr(), None,
+                                    y1.data_ptr(), N, K, sh))
+            torch.cuda.synchronize()
+            rel = ((ym[:N] - y1).abs() / y1.abs().clamp_min(1e-6)).max().item()
+            ops = 2.0 * N * K * B
+            issued = ops * (2 if t == 12 else 4) * ((B + 7) // 8 * 8) / B
+            nb = algo_bytes(t, N, K, B)
+            res[f"{name}_B{B}"] = {
+                "us_per_call": round(us, 2), "us_per_stream": round(us / B, 2),
+                "GB/s": round(nb / us / 1e3, 1), "TOP/s": round(ops / us / 1e6, 2),
+                "mfma_util": round(issued / us / 1e6 / MFMA_I8_PEAK_TOPS, 4),
+                "max_rel_vs_single_stream_int8": float(f"{rel:.3e}")}
+            del xs, ym, y1
+        del cm
+    return res
+
+
 def cfg1(L, torch, stream, host_w) -> dict:
     """one Q4_K GEMV, W 1024 x 1024 (4096 blocks), batch 1."""
     sh = stream.cuda_stream
@@ -644,11 +691,27 @@ def cfg_int8(L, torch, stream, host_w) -> dict:
             "port", "the seven matvecs in q*_dot_row_sdot_f's order, one thread")
         res["layer_set"]["cpu"]["cores"] = 1
     del copies
+    # the other SDOT types (st_linear_q5k / _q3k / _q8_0 under use_sdot) on
+    # the 27B gate shape, int8 against the exact path, weights rotated
+    N, K = 17408, 5120
+    xg = xs["h"]
+    yt = torch.empty(N, dtype=torch.float32, device="cuda")
+    for t, tname in ((KQ.TYPE_Q5_K, "Q5_K"), (KQ.TYPE_Q3_K, "Q3_K"), (KQ.TYPE_Q8_0, "Q8_0")):
+        tc = _copies(torch, synth.tensor(t, N, K, 4200 + t), COPIES)
+        nb = algo_bytes(t, N, K)
+        res[f"{tname}_17408x5120"] = {"bytes": nb}
+        for flag, key in ((KQ.INT8_ACT, "int8"), (0, "exact")):
+            tus = _events_us(torch, stream, lambda i: _check(L, L.kq_gemv_dev(
+                t | flag, tc[i % len(tc)].data_ptr(), xg.data_ptr(), None, yt.data_ptr(), N, K,
+                sh)), 50)
+            res[f"{tname}_17408x5120"][key] = {"us": round(tus, 2), "GB/s": round(nb / tus / 1e3, 1)}
+        del tc
     return res
 
 
 OTHER = {"cfg1_q4k_1024x1024": cfg1, "cfg2_qwen3_0.6b": cfg2, "cfg3_gate_up_q2k_type42": cfg3,
          "cfg4_multiseq_exact": cfg4, "cfg4_multiseq_mfma": multiseq_mfma,
+         "cfg4_multiseq_int8": multiseq_int8,
          "cfg5_moe_128e_top8": cfg5, "cfg3_int8_activations": cfg_int8}
 
 

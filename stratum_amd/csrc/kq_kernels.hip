@@ -4278,16 +4278,16 @@ typedef void (*segs_fn)(SegsArg);
 static const segs_fn k_segs[2][2][NSLOT] = {{KQ_SEGS_ROW(1, false), KQ_SEGS_ROW(2, false)},
                                            {KQ_SEGS_ROW(1, true), KQ_SEGS_ROW(2, true)}};
 #undef KQ_SEGS_ROW
-// the MoE gather (TB_SEL) instantiations, single type only (slots 4 and
-// 8..12 unused: the mixed kernel and the int8 mode have no gather form)
+// the MoE gather (TB_SEL) instantiations, single type only (slot 4
+// unused: the mixed kernel has no gather form; the int8 mode's at depth 1)
 #define KQ_SEL_ROW(D, M)                                                                  \
     {&kq_segs_kernel<D, TB_Q4K | TB_SEL, M>, &kq_segs_kernel<D, TB_Q6K | TB_SEL, M>,       \
      &kq_segs_kernel<D, TB_Q2K | TB_SEL, M>, &kq_segs_kernel<D, TB_NIB | TB_SEL, M>,       \
      &kq_segs_kernel<D, TB_Q4K | TB_SEL, M>, &kq_segs_kernel<D, TB_Q5K | TB_SEL, M>,       \
      &kq_segs_kernel<D, TB_Q3K | TB_SEL, M>, &kq_segs_kernel<D, TB_Q80 | TB_SEL, M>,       \
-     &kq_segs_kernel<D, TB_Q4K | TB_SEL, M>, &kq_segs_kernel<D, TB_Q4K | TB_SEL, M>,       \
-     &kq_segs_kernel<D, TB_Q4K | TB_SEL, M>, &kq_segs_kernel<D, TB_Q4K | TB_SEL, M>,       \
-     &kq_segs_kernel<D, TB_Q4K | TB_SEL, M>}
+     &kq_segs_kernel<1, TB_Q4K_I8 | TB_SEL, M>, &kq_segs_kernel<1, TB_Q6K_I8 | TB_SEL, M>, \
+     &kq_segs_kernel<1, TB_Q5K_I8 | TB_SEL, M>, &kq_segs_kernel<1, TB_Q3K_I8 | TB_SEL, M>, \
+     &kq_segs_kernel<1, TB_Q80_I8 | TB_SEL, M>}
 static const segs_fn k_segs_sel[2][2][NSLOT] = {{KQ_SEL_ROW(1, false), KQ_SEL_ROW(2, false)},
                                                {KQ_SEL_ROW(1, true), KQ_SEL_ROW(2, true)}};
 #undef KQ_SEL_ROW
@@ -4373,13 +4373,13 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
     if (t == 4) depth = 1;   // the all-types kernel fits 128 VGPRs at depth 1 only
     int nsel = 0;
     for (int i = 0; i < nseg; i++) nsel += segs[i].sel != nullptr;
-    if (nsel && (nsel != nseg || t == 4 || t >= 8)) return (int)hipErrorInvalidValue;
+    if (nsel && (nsel != nseg || t == 4)) return (int)hipErrorInvalidValue;
     // the MoE FFN step pieces: one selection segment; the combine needs
     // equal parts whose rows are a multiple of the grid and its outputs in
     // the x region; in-launch softmax needs every logit in a lane
     const kqk_seg& h0 = segs[0];
     if (h0.act || h0.cx || h0.logits) {
-        if (nseg != 1 || !h0.sel || t == 4 || t >= 8 || (h0.act && h0.cx))
+        if (nseg != 1 || !h0.sel || t == 4 || (h0.act && h0.cx))
             return (int)hipErrorInvalidValue;
         if (h0.act || h0.cx) {   // equal parts, rows a multiple of the grid, outputs in the x region
             const int pn = h0.rows[0];

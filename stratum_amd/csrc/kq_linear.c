@@ -1012,7 +1012,8 @@ static int moe_one_token(const kq_moe_op* op, const int* sel, int k, int E, cons
 static int moe_check_op(const kq_moe_op* op, int k, int E, const char* who) {
     if (check_shape(op->type, op->n_out, op->k_in) || kq_ready()) return -1;
     if (is_dense(op->type)) return kq_fail("%s: dense (F16/F32) experts are not supported", who);
-    if (op->type & KQ_INT8_ACT) return kq_fail("%s: the int8-activation mode has no MoE form", who);
+    if ((op->type & KQ_INT8_ACT) && !has_sdot(op->type & ~KQ_INT8_ACT))
+        return kq_fail("%s: type %d has no int8-activation form", who, op->type & ~KQ_INT8_ACT);
     const int nt = op->ntensors;
     if (nt < 1 || nt > 2) return kq_fail("%s: ntensors=%d", who, nt);
     if (op->x_div != 1 && op->x_div != k) return kq_fail("%s: x_div must be 1 or k", who);

@@ -369,3 +369,49 @@ def test_moe_config_full_layer_routed(port, B):
     act = np.stack([synth.gaussian(r, F) for _ in range(B * k)]).reshape(-1)
     dn = run_moe(qtype, [down], sel.reshape(B, k), act, 1, B, k, n_exp, H, F)
     check_members(port, qtype, [down], sel, act, 1, dn, H, F, n_oracle=4)
+
+
+# --------------------------------------------------- int8-activation mode
+def check_ulp1(got, want, what):
+    d = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    assert np.all(d <= np.spacing(np.abs(want)).astype(np.float64)), what
+
+
+@pytest.mark.parametrize("qtype", [12, 14, 13, 11, 8])
+@pytest.mark.parametrize("B", [1, 3])
+def test_moe_int8_members_equal_single_slice(port, qtype, B):
+    """The int8-activation mode (type | KQ_INT8_ACT: the per-slice
+    st_linear_dispatch of moe_forward_one_token under use_sdot,
+    stratum_arch_moe.inc.c:596-603): gate and up routed in one launch at
+    batch 1 (per token at B > 1), down on the written sel; every member
+    bit-identical to its slice's single int8 GEMV and within one ulp of the
+    oracle's int8 form."""
+    qi = qtype | K.INT8_ACT
+    n_exp, H, F, k = 32, 512, 256, 8
+    gate, up = experts(qtype, n_exp, F, H, 61), experts(qtype, n_exp, F, H, 62)
+    down = experts(qtype, n_exp, H, F, 63)
+    r = np.random.default_rng(64 + B + qtype)
+    probs = softmax_rows(r.standard_normal((B, n_exp)).astype(np.float32))
+    x = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
+    print(f"moe int8 type={qtype} B={B}", flush=True)
+    got, sel, selw = run_routed(qi, [gate, up], probs if B > 1 else probs[0], x, k, k, F, H)
+    for s_ in range(B):
+        ws, ww = port.topk(probs[s_], k)
+        assert list(sel[s_ * k:(s_ + 1) * k]) == ws
+    rb = K.lib().kq_row_bytes(qtype, H)
+    for t, w in enumerate((gate, up)):
+        for m, e in enumerate(sel):
+            xm = x[(m // k) * H:(m // k + 1) * H]
+            ws_ = w[e * F * rb:(e + 1) * F * rb]
+            assert same_values(got[t][m], single(qi, ws_, xm, F, H)), (t, m)
+            if m < 3:
+                check_ulp1(got[t][m], port.gemv_i8(qtype, ws_, xm, F, H), (t, m))
+    act = np.stack([synth.gaussian(r, F) for _ in range(B * k)]).reshape(-1)
+    dn = run_moe(qi, [down], sel.reshape(B, k), act, 1, B, k, n_exp, H, F)
+    rbd = K.lib().kq_row_bytes(qtype, F)
+    for m, e in enumerate(sel):
+        ws_ = down[e * H * rbd:(e + 1) * H * rbd]
+        am = act[m * F:(m + 1) * F]
+        assert same_values(dn[0][m], single(qi, ws_, am, H, F)), m
+        if m < 3:
+            check_ulp1(dn[0][m], port.gemv_i8(qtype, ws_, am, H, F), m)

@@ -372,6 +372,48 @@ def test_moe_ffn_never_grows_library_scratch(port, case, kq_env):
     assert np.abs(got["x"] - full["x"]).max() <= 1e-4 * contrib
 
 
+@pytest.mark.parametrize("B", [1, 3])
+def test_moe_ffn_step_int8(port, B):
+    """The step with Q4_K experts in the int8-activation mode (gate, up and
+    down types | KQ_INT8_ACT; F32 router): sel is the oracle's top-k of the
+    step's own probabilities, every gate, up and down member is
+    bit-identical to its slice's single int8 GEMV on the step's own inputs,
+    SwiGLU within 4 ulps and the combine bit for bit."""
+    H, F, E, k = 1024, 512, 32, 4
+    d = make_layer(H, F, E, k, 9950)
+    qi = TYPE_Q4_K | K.INT8_ACT
+    d["gate_type"] = d["up_type"] = d["down_type"] = qi
+    r = synth.rng(9951 + B)
+    xn = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
+    x0 = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
+    print(f"moe ffn int8 B={B}", flush=True)
+    got = run_step(d, xn, x0, B)
+    rb_in, rb_ff = synth.row_bytes(TYPE_Q4_K, H), synth.row_bytes(TYPE_Q4_K, F)
+
+    def single(w, xv, N, Kd):
+        dw, dx = dev(w), dev(xv)
+        dy = torch.empty(N, dtype=torch.float32, device="cuda")
+        K.gemv_dev(qi, dw.data_ptr(), dx.data_ptr(), dy.data_ptr(), N, Kd, stream=stream())
+        torch.cuda.synchronize()
+        return dy.cpu().numpy()
+    for s in range(B):
+        p = got["probs"][s * E:(s + 1) * E]
+        sel, selw = port.topk(p, k)
+        assert list(got["sel"][s * k:(s + 1) * k]) == sel, s
+        for r_, e in enumerate(sel):
+            m = s * k + r_
+            xs = xn[s * H:(s + 1) * H]
+            g, u = got["g"][m * F:(m + 1) * F], got["u"][m * F:(m + 1) * F]
+            a = got["act"][m * F:(m + 1) * F]
+            assert same_values(g, single(d["gate"][e * F * rb_in:(e + 1) * F * rb_in], xs, F, H))
+            assert same_values(u, single(d["up"][e * F * rb_in:(e + 1) * F * rb_in], xs, F, H))
+            assert ulps(a, port.swiglu(g, u)).max() <= 4.0
+            o = got["ffo"][m * H:(m + 1) * H]
+            assert same_values(o, single(d["down"][e * H * rb_ff:(e + 1) * H * rb_ff], a, H, F))
+    assert same_values(got["x"], port.moe_combine(got["ffo"], got["sel"], got["selw"], x0, B, k,
+                                                  H))
+
+
 def test_moe_ffn_step_f16_router_mixed_types(port):
     """An F16 router and gate/up/down of different types (Q4_K gate/up,
     Q6_K down): gate and up still share one routed launch, down has its
