@@ -551,6 +551,20 @@ def cfg5(L, torch, stream, host_w) -> dict:
                                                B, k, E, sel.data_ptr(), selw.data_ptr(), sh))
             _check(L, L.kq_moe_gemv_dev(ctypes.byref(dn), sel.data_ptr(), B, k, E, sh))
         us = _events_us(torch, stream, moe_step, 2 * MOE_SETS * NCOPY)
+        # the same step in the int8-activation mode (Q4_K | KQ_INT8_ACT)
+        def as_int8(op):
+            o = KQ.KqMoeOp.from_buffer_copy(op)
+            o.type = 12 | KQ.INT8_ACT
+            return o
+        ops8 = [[(as_int8(gu), as_int8(dn)) for gu, dn in per] for per in ops]
+
+        def moe_step8(i):
+            j = i % MOE_SETS
+            gu, dn = ops8[(i // MOE_SETS) % NCOPY][j]
+            _check(L, L.kq_moe_gemv_routed_dev(ctypes.byref(gu), probs.data_ptr() + 4 * j * B * E,
+                                               B, k, E, sel.data_ptr(), selw.data_ptr(), sh))
+            _check(L, L.kq_moe_gemv_dev(ctypes.byref(dn), sel.data_ptr(), B, k, E, sh))
+        us8 = _events_us(torch, stream, moe_step8, 2 * MOE_SETS * NCOPY)
         nb = distinct * (2 * gsl + dsl) + 4 * (B * H + 2 * B * k * F + B * k * F + B * k * H)
         per_rot = sum(len(t) for t in sets) * NCOPY * (2 * gsl + dsl)
         res[f"B{B}"] = {"us_per_layer": round(us, 2), "distinct_experts": round(distinct, 2),
@@ -559,7 +573,9 @@ def cfg5(L, torch, stream, host_w) -> dict:
                         "route": "kq_moe_gemv_routed_dev",
                         "rotation": f"{MOE_SETS} routing sets x {NCOPY} weight copies: "
                                     f"{per_rot / 2 ** 20:.0f} MiB of selected slices per "
-                                    "rotation"}
+                                    "rotation",
+                        "int8": {"us_per_layer": round(us8, 2), "GB/s": round(nb / us8 / 1e3, 1),
+                                 "what": "the same gather with Q4_K | KQ_INT8_ACT"}}
         # the whole expert FFN step (kq_moe_ffn_dev): F32 router GEMV, softmax,
         # routed gate+up, SwiGLU, down, rank-ordered combine + residual
         router = torch.from_numpy(synth.tensor(KQ.TYPE_F32, E, H, 3703)).cuda()

@@ -364,6 +364,20 @@ def moe_pack_offset(data_off: int, n_experts: int, gate: int, up: int, down: int
     return off
 
 
+def moe_tickets(sel, n_experts: int, ch: int = 8):
+    """The expert tickets of moe_forward_b (stratum_arch_moe.inc.c:1136-1140,
+    1158-1178): member m = s * k + r with sel[m] >= 0 joins expert sel[m]'s
+    list (tokens s in order, ranks r in order, i.e. increasing m), and each
+    list is cut from its start into tickets of at most CH = 8 members, each
+    one st_linear_multix call (stratum_arch_moe.inc.c:1194-1201).  Returns
+    [(e, [m, ...]), ...] in increasing expert order."""
+    lists = [[] for _ in range(n_experts)]
+    for m, e in enumerate(int(v) for v in sel):
+        if 0 <= e < n_experts:
+            lists[e].append(m)
+    return [(e, lst[j:j + ch]) for e, lst in enumerate(lists) for j in range(0, len(lst), ch)]
+
+
 # ------------------------------------------------------------ tolerances
 def rel_err(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     """Per-element |a-b| / max(|b|, 1e-6): ASSERT_REL of quant_test.c:34-43."""

@@ -3415,6 +3415,14 @@ struct Mi8Arg {
     float* y;                 // y[s * y_stride + r]
     long y_stride;
     int N, K, B;
+    // grouped launches (the int8 MoE batch): blockIdx.y is group g < *ng of
+    // the kq_moe_group_kernel records (runs of at most 8 members of one
+    // expert); member slot j reads quantized row xi[j] and writes row
+    // yi[j] of the group's y (stride y_stride); slots past M read row zrow
+    // (all zero).  w and y above are unused.
+    const MxGroup* groups;
+    const int* ng;
+    int zrow;
 };
 
 // x -> int8 per group (the single-stream rule, kq_quantize_kernel's) and
@@ -3487,7 +3495,19 @@ struct Mi8W6 { uint32_t l[4][5], h[4][5], s[5]; uint32_t d, sh; };
 // fixed order, like the single-stream kernel's phases (the result equals
 // the reference's strictly sequential sum unless a binary64 re-association
 // crosses a binary32 rounding boundary).
-template <int TYPE, int SW, int P, int KS>
+//
+// GR (the int8 MoE batch, moe_forward_b under use_sdot,
+// stratum_arch_moe.inc.c:1158-1201): one workgroup per (16-row block, run of
+// one expert's members).  A run of two or more members takes
+// st_linear_multix's pack arithmetic above, exactly as a kq_gemv_multix_dev
+// call on that expert's slice would.  A run of one member takes the
+// single-stream path (st_linear_multix at B = 1 is st_linear_dispatch): the
+// single-stream int8 kernel's chunk terms (term_q4k_i8 / term_q6k_i8, from
+// the same exact dots; the Q4_K x sums come from one more MFMA against a
+// B operand of ones), kept in LDS (dynamic, 16 rows x K/64 doubles) and
+// reduced in that kernel's phase order, so the member equals its
+// kq_gemv_dev(type | KQ_INT8_ACT) result bit for bit.
+template <int TYPE, int SW, int P, int KS, bool GR>
 __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
     constexpr bool Q4 = TYPE == T_Q4K_I8;
     constexpr int NM = Q4 ? SW / 8 : SW / 4;        // MFMAs per chunk
@@ -3504,10 +3524,25 @@ __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
     const int q = lane >> 4, jr = lane & 15;
     const int N = A.N, K = A.K, nb = K >> 8;
     const int ng = Q4 ? K >> 5 : K >> 4;            // coefficient groups per stream
-    const int rb = blockIdx.x, s0 = blockIdx.y * SW;
+    const int rb = blockIdx.x, s0 = GR ? 0 : blockIdx.y * SW;
     const int row = min(rb * 16 + jr, N - 1);
     constexpr int BB = Q4 ? 144 : 210;
-    const wptr wr = to_global(A.w) + (size_t)row * (size_t)nb * BB;
+    const MxGroup* gp = nullptr;
+    int M = SW;
+    const uint8_t* wbase = A.w;
+    if constexpr (GR) {
+        if ((int)blockIdx.y >= *A.ng) return;     // uniform over the workgroup
+        gp = A.groups + blockIdx.y;
+        M = gp->M;
+        wbase = gp->w;
+    }
+    // quantized row of member slot j (0 .. SW-1)
+    auto xrow = [&](int j) -> long {
+        if constexpr (GR) return j < M ? gp->xi[j] : A.zrow;
+        return s0 + j;
+    };
+    const bool single = GR && M == 1;             // uniform
+    const wptr wr = to_global(wbase) + (size_t)row * (size_t)nb * BB;
     const int nbp = (nb + KS - 1) / KS;             // super-blocks per K-part
     const int kb0 = kp * nbp, kb1 = min(nb, kb0 + nbp);
     uint8_t* wl = lds + kp * WL;                    // this wave's LDS
@@ -3519,9 +3554,16 @@ __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
     // jr/4, run jr&3) at lane group q == jr & 3.  Its x: stream sa + NS m,
     // chunk position offset qo; else the zero page.
     const bool on = Q4 ? (q >> 1) == (jr & 1) : q == (jr & 3);
-    const int sa = s0 + (Q4 ? jr >> 1 : jr >> 2), NS = Q4 ? 8 : 4;
-    const uint8_t* xa0 = reinterpret_cast<const uint8_t*>(A.xq) + (size_t)sa * K;
+    const int sa = Q4 ? jr >> 1 : jr >> 2, NS = Q4 ? 8 : 4;
+    const uint8_t* xa[NM];
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+        xa[m] = reinterpret_cast<const uint8_t*>(A.xq) + (size_t)xrow(sa + NS * m) * K;
     const uint8_t* zp = A.zp;
+    constexpr int CPS = CB / 16;                    // uint4 of coefficients per stream
+    long crow[CPT];                                 // coefficient row of this lane's pieces
+#pragma unroll
+    for (int k = 0; k < CPT; k++) crow[k] = xrow(min(lane + 64 * k, CU - 1) / CPS);
 
     struct Slot { W w; i32x4 a[4][NM]; uint4 c[CPT]; };
     auto load = [&](int b, Slot& sl) {
@@ -3554,17 +3596,19 @@ __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
                 // chunk j's positions of this lane: Q4_K 64j + 16q; Q6_K run
                 // q of chunk (h, is) at 128h + 32q + 16is
                 const int qo = Q4 ? 64 * j + 16 * q : 128 * (j >> 1) + 32 * q + 16 * (j & 1);
-                const uint8_t* src = on ? xa0 + (size_t)NS * m * K + 256 * (size_t)b + qo : zp;
+                const uint8_t* src = on ? xa[m] + 256 * (size_t)b + qo : zp;
                 sl.a[j][m] = *reinterpret_cast<const i32x4*>(src);
             }
-        constexpr int CPS = CB / 16;                // uint4 of coefficients per stream
 #pragma unroll
         for (int k = 0; k < CPT; k++) {
-            const int v = min(lane + 64 * k, CU - 1), sc = s0 + v / CPS;
+            const int v = min(lane + 64 * k, CU - 1);
             sl.c[k] = *reinterpret_cast<const uint4*>(
-                cf + ((size_t)sc * ng + (size_t)b * (CB / 8)) * 8 + 16 * (v % CPS));
+                cf + ((size_t)crow[k] * ng + (size_t)b * (CB / 8)) * 8 + 16 * (v % CPS));
         }
     };
+    // a run of one member: chunk terms of the 16 rows, [row][K/64]
+    extern __shared__ __align__(16) double mi8_terms[];
+    const int NCH = K >> 6;
 
     double acc[NACC];
 #pragma unroll
@@ -3621,6 +3665,25 @@ __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
                                        (int)((qv.y >> sh) & 0x0f0f0f0fu),
                                        (int)((qv.z >> sh) & 0x0f0f0f0fu),
                                        (int)((qv.w >> sh) & 0x0f0f0f0fu)};
+                    if (GR && single) {
+                        // slot 0 (lanes 0-15): the dots and x sums of both
+                        // sub-blocks, then term_q4k_i8's binary64 term
+                        const i32x4 ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+                        const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.a[j][0], bop, zero,
+                                                                              0, 0, 0);
+                        const i32x4 X = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.a[j][0], ones, zero,
+                                                                              0, 0, 0);
+                        if (q == 0) {
+                            const float4 c = *reinterpret_cast<const float4*>(wl + 16 * j);
+                            const float c1 = dm.x * c.x, c2 = -(dm.y * c.x);
+                            const float c3 = dm.z * c.z, c4 = -(dm.w * c.z);
+                            const double t1 = fma((double)c1, (double)D[0], (double)c2 * (double)X[0]);
+                            const double t2 = fma((double)c3, (double)D[1], (double)c4 * (double)X[1]);
+                            mi8_terms[jr * NCH + 4 * b + j] = t1 + t2;
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                        continue;
+                    }
 #pragma unroll
                     for (int m = 0; m < NM; m++) {
                         const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.a[j][m], bop, zero,
@@ -3666,6 +3729,27 @@ __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
                         bw[k] = ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u;   // bytes v - 32
                     }
                     const i32x4 bop = {(int)bw[0], (int)bw[1], (int)bw[2], (int)bw[3]};
+                    if (GR && single) {
+                        // slot 0 (lanes 0-15): the four runs' dots of q - 32,
+                        // then term_q6k_i8's binary64 term
+                        const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.a[u][0], bop, zero,
+                                                                              0, 0, 0);
+                        if (q == 0) {
+                            const double* cs = reinterpret_cast<const double*>(wl);
+                            const float df = f16_bits_to_f32(cur.w.d);
+                            double t = 0.0;
+#pragma unroll
+                            for (int r4 = 0; r4 < 4; r4++) {
+                                const int g = 8 * h + is + 2 * r4;
+                                const float sc = (float)(int8_t)(uint8_t)(S[g >> 2] >> (8 * (g & 3)));
+                                const float c = df * sc * (float)cs[g];
+                                t = t + (double)c * (double)D[r4];
+                            }
+                            mi8_terms[jr * NCH + 4 * b + u] = t;
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                        continue;
+                    }
 #pragma unroll
                     for (int m = 0; m < NM; m++) {
                         const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.a[u][m], bop, zero,
@@ -3680,6 +3764,23 @@ __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
                 }
             }
         }
+    }
+    if (GR && single) {
+        // the single-stream kernel's row reduction: GP = kq_phases(K/64)
+        // lanes per row, lane p sums chunks p, p+GP, ... in order from 0,
+        // then phase_tree (16 GP tasks, whole waves)
+        __syncthreads();
+        const int GP = kq_phases(NCH), lgp = GP == 32 ? 5 : 3;
+        for (int task = tid; task < 16 * GP; task += 64 * KS) {
+            const int rho = task >> lgp, p = task & (GP - 1);
+            const double* tr = mi8_terms + rho * NCH;
+            double v = 0.0;
+            for (int i = p; i < NCH; i += GP) v = v + tr[i];
+            v = phase_tree(v, GP);
+            const int r = rb * 16 + rho;
+            if (p == 0 && r < N) gp->y[(size_t)gp->yi[0] * A.y_stride + r] = (float)v;
+        }
+        return;
     }
     // the K-parts' partial sums, added in K-part order
     double* part = reinterpret_cast<double*>(lds);
@@ -3701,8 +3802,12 @@ __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
     if (r >= N) return;
 #pragma unroll
     for (int a = 0; a < NACC; a++) {
-        const int so = Q4 ? s0 + 8 * (a >> 1) + 2 * q + (a & 1) : s0 + 4 * a + q;
-        if (so < A.B) A.y[(size_t)so * A.y_stride + r] = (float)acc[a];
+        const int so = Q4 ? 8 * (a >> 1) + 2 * q + (a & 1) : 4 * a + q;   // member slot
+        if constexpr (GR) {
+            if (so < M) gp->y[(size_t)gp->yi[so] * A.y_stride + r] = (float)acc[a];
+        } else if (s0 + so < A.B) {
+            A.y[(size_t)(s0 + so) * A.y_stride + r] = (float)acc[a];
+        }
     }
 }
 
@@ -4820,6 +4925,7 @@ int kqk_launch_mi8(int type, const float* xs, long x_stride, const void* w, floa
     a.y = ys;
     a.y_stride = y_stride;
     a.N = N; a.K = K; a.B = B;
+    a.groups = nullptr; a.ng = nullptr; a.zrow = 0;
     // Q4_K: 8 or 16 streams per wave; Q6_K: 8 (its A operands take
     // 16 registers per MFMA and super-block)
     const int SW = type == T_Q6K_I8 || B <= 8 ? 8 : 16;
@@ -4829,8 +4935,8 @@ int kqk_launch_mi8(int type, const float* xs, long x_stride, const void* w, floa
     // batch or the row count
     if (ks != 1 && ks != 2 && ks != 4 && ks != 8) ks = kqk_mi8_parts(K);
 #define KQ_MI8_GO(T_, S_, P_, K_)                                                            \
-    hipLaunchKernelGGL((kq_mi8_kernel<T_, S_, P_, K_>), dim3((unsigned)nrb, (unsigned)nset),  \
-                       dim3(64 * K_), 0, st, a)
+    hipLaunchKernelGGL((kq_mi8_kernel<T_, S_, P_, K_, false>), dim3((unsigned)nrb,           \
+                       (unsigned)nset), dim3(64 * K_), 0, st, a)
 #define KQ_MI8_KS(T_, S_, P_)                                                                \
     if (ks == 1) KQ_MI8_GO(T_, S_, P_, 1);                                                   \
     else if (ks == 2) KQ_MI8_GO(T_, S_, P_, 2);                                              \
@@ -4843,6 +4949,61 @@ int kqk_launch_mi8(int type, const float* xs, long x_stride, const void* w, floa
     }
 #undef KQ_MI8_KS
 #undef KQ_MI8_GO
+    return (int)hipGetLastError();
+}
+
+// The int8 MoE batch: workspace bytes for nx quantized x rows (plus the
+// zero row) and the launches (prep over the nx rows; the grouped main
+// kernel over up to ngmax groups, *ng of them live, each a run of at most 8
+// members built by kq_moe_group_kernel).  K-parts as kqk_launch_mi8 takes
+// them, so a run's members equal a kq_gemv_multix_dev call over them.
+long kqk_mi8_moe_workspace(int type, int nx, int K) {
+    long cf_off = 0;
+    return nx < 1 ? -1 : kqk_mi8_workspace(type, nx + 1, K, &cf_off);
+}
+
+int kqk_launch_mi8_moe(int type, const float* x, int nx, int K, const void* groups,
+                       const int* ng, int ngmax, int N, long y_stride, void* ws, hipStream_t st) {
+    long cf_off = 0;
+    const long wsb = kqk_mi8_workspace(type, nx + 1, K, &cf_off);
+    const long tl = 16L * (K >> 6) * 8;          // a single member's chunk terms
+    if (wsb < 0 || nx < 1 || N < 1 || ngmax < 1 || ngmax > 65535 || y_stride < N || !groups ||
+        !ng || ((uintptr_t)x & 15) || ((uintptr_t)ws & 15) || tl > 65536)
+        return (int)hipErrorInvalidValue;
+    int8_t* xq = static_cast<int8_t*>(ws);
+    uint8_t* cf = static_cast<uint8_t*>(ws) + cf_off;
+    uint8_t* zp = static_cast<uint8_t*>(ws) + wsb - 256;
+    const int G = type == T_Q4K_I8 ? 32 : 16;
+    const int bpad = (nx + 1 + 15) & ~15;        // rows nx .. bpad-1 zero
+    const long gq = (long)bpad * (K / G);
+    if (G == 32)
+        hipLaunchKernelGGL(kq_mi8_prep_kernel<32>, dim3((unsigned)((gq + 255) / 256)), dim3(256), 0,
+                           st, x, (long)K, K, nx, bpad, xq, cf, zp);
+    else
+        hipLaunchKernelGGL(kq_mi8_prep_kernel<16>, dim3((unsigned)((gq + 255) / 256)), dim3(256), 0,
+                           st, x, (long)K, K, nx, bpad, xq, cf, zp);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    Mi8Arg a;
+    a.w = nullptr;
+    a.xq = xq; a.zp = zp; a.cf = cf;
+    a.y = nullptr;
+    a.y_stride = y_stride;
+    a.N = N; a.K = K; a.B = 8;
+    a.groups = static_cast<const MxGroup*>(groups);
+    a.ng = ng;
+    a.zrow = nx;
+    const int nrb = (N + 15) / 16, ks = kqk_mi8_parts(K);
+#define KQ_MI8G_GO(T_, P_, K_)                                                               \
+    hipLaunchKernelGGL((kq_mi8_kernel<T_, 8, P_, K_, true>), dim3((unsigned)nrb,             \
+                       (unsigned)ngmax), dim3(64 * K_), (size_t)tl, st, a)
+#define KQ_MI8G_KS(T_, P_)                                                                   \
+    if (ks == 1) KQ_MI8G_GO(T_, P_, 1);                                                      \
+    else if (ks == 2) KQ_MI8G_GO(T_, P_, 2);                                                 \
+    else KQ_MI8G_GO(T_, P_, 4);
+    if (type == T_Q4K_I8) { KQ_MI8G_KS(T_Q4K_I8, 2) } else { KQ_MI8G_KS(T_Q6K_I8, 1) }
+#undef KQ_MI8G_KS
+#undef KQ_MI8G_GO
     return (int)hipGetLastError();
 }
 

@@ -1127,6 +1127,61 @@ static int moe_batch(const kq_moe_op* op, int* sel, const float* probs, float* s
     return 0;
 }
 
+/* Q4_K / Q6_K in the int8 mode: the types whose st_linear_multix under
+ * use_sdot has its own (pack) arithmetic at B >= 2 */
+static int is_i8mx(int type) {
+    return type == (KQ_INT8_ACT | KQ_TYPE_Q4_K) || type == (KQ_INT8_ACT | KQ_TYPE_Q6_K);
+}
+
+/* Bytes of moe_i8_batch's workspace for nx x rows of K, nt tensors and nm
+ * members over E experts: the quantized rows, their coefficients and the
+ * zero page (kqk_mi8_moe_workspace), then the runs' group records; 0 for a
+ * bad shape. */
+static size_t moe_i8_bytes(int type, int nx, int K, int nt, int nm, int E) {
+    const long xw = kqk_mi8_moe_workspace(type, nx, K);
+    if (xw < 0) return 0;
+    return (((size_t)xw + 255) & ~(size_t)255) + moe_group_bytes(nt, nm, E, 8);
+}
+
+/* Several tokens in the int8 mode, Q4_K / Q6_K.  moe_forward_b under
+ * use_sdot (stratum_arch_moe.inc.c:1136-1201) runs each expert's members,
+ * in increasing member order, in tickets of at most CH = 8 through
+ * st_linear_multix: a ticket of two or more members takes the multix pack
+ * arithmetic, a ticket of one the single-stream path.  Here the same runs
+ * are cut on the device (kq_moe_group_kernel, run length 8), every x row
+ * is quantized once, and one grouped matrix-core launch computes all runs
+ * (kq_mi8_kernel, GR): each member equals kq_gemv_multix_dev over its run
+ * (kq_gemv_dev for a run of one) bit for bit.  The workspace is io->grp
+ * when given (the FFN step's), else the library's matrix-core scratch. */
+static int moe_i8_batch(const kq_moe_op* op, const int* sel, int B, int k, int E,
+                        moe_runs_io* io, hipStream_t st) {
+    const int nm = B * k, nt = op->ntensors, nx = nm / op->x_div, K = op->k_in;
+    const size_t need = moe_i8_bytes(op->type, nx, K, nt, nm, E);
+    if (!need) return kq_fail("int8 moe batch: bad shape K=%d", K);
+    uint8_t* base;
+    if (io && io->grp) {
+        if (need > io->grp_bytes)
+            return kq_fail("int8 moe batch: %zu workspace bytes, %zu given", need, io->grp_bytes);
+        base = (uint8_t*)io->grp;
+        io->grp_used = 1;
+    } else {
+        if (mfma_reserve(need)) return -1;
+        base = g_kq.d_mf;
+    }
+    const size_t xwa = ((size_t)kqk_mi8_moe_workspace(op->type, nx, K) + 255) & ~(size_t)255;
+    const int dmax = E < nm ? E : nm;
+    const int ngmax = nt * (dmax + (nm + 7) / 8);
+    void* groups = base + xwa;
+    int* ng = (int*)(base + xwa + (size_t)ngmax * (size_t)kqk_mx_group_bytes());
+    int e = kqk_launch_moe_group(sel, nm, E, nt, op->x_div, 8, op->w[0], op->w[nt - 1], op->y[0],
+                                 op->y[nt - 1], (long)op->expert_stride, groups, ng, st);
+    if (e) return kq_fail("moe group launch: %s", hipGetErrorString((hipError_t)e));
+    e = kqk_launch_mi8_moe(op->type, op->x, nx, K, groups, ng, ngmax, op->n_out, op->n_out, base,
+                           st);
+    if (e) return kq_fail("int8 moe launch: %s", hipGetErrorString((hipError_t)e));
+    return 0;
+}
+
 /* B tokens of a type the multi-x kernel does not cover: one launch per
  * token, each with its k selections (the same bits as the batched path). */
 static int moe_per_token(const kq_moe_op* op, const int* sel, int B, int k, int E, hipStream_t st) {
@@ -1151,7 +1206,8 @@ static int moe_gemv_routed(const kq_moe_op* op, const float* probs, int B, int k
     if (!is_core(op->type)) {
         const int e = kqk_launch_moe_topk(probs, B, E, k, sel, selw, st);
         if (e) return kq_fail("moe topk launch: %s", hipGetErrorString((hipError_t)e));
-        return moe_per_token(op, sel, B, k, E, st);
+        return is_i8mx(op->type) ? moe_i8_batch(op, sel, B, k, E, io, st)
+                                 : moe_per_token(op, sel, B, k, E, st);
     }
     const int r = moe_batch(op, sel, probs, selw, B, k, E, io, st);
     if (r <= 0) return r;
@@ -1175,6 +1231,7 @@ static int moe_gemv(const kq_moe_op* op, const int* sel, int B, int k, int E, mo
         return kq_fail("kq_moe_gemv_dev: B=%d k=%d E=%d", B, k, E);
     if (moe_check_op(op, k, E, "kq_moe_gemv_dev")) return -1;
     if (B == 1) return moe_one_token(op, sel, k, E, NULL, NULL, st);
+    if (is_i8mx(op->type)) return moe_i8_batch(op, sel, B, k, E, io, st);
     if (!is_core(op->type)) return moe_per_token(op, sel, B, k, E, st);
     return moe_batch(op, (int*)sel, NULL, NULL, B, k, E, io, st);
 }
@@ -1228,10 +1285,20 @@ int kq_moe_combine_dev(const float* o, const int* sel, const float* selw, const 
 static int64_t ffn_layout(const kq_moe_ffn* f, int B, int64_t off[FFN_REGIONS]) {
     const int64_t bk = (int64_t)B * f->k;
     const int dmax = f->n_experts < bk ? f->n_experts : (int)bk;
+    /* the group records, or a batch's int8 (pack) workspace when larger */
+    const int E = f->n_experts, pair = f->gate_type == f->up_type && f->gate_stride == f->up_stride;
+    size_t g6 = moe_group_bytes(2, (int)bk, E, 1);
+    if (B > 1) {
+        const size_t i8[3] = {
+            is_i8mx(f->gate_type) ? moe_i8_bytes(f->gate_type, B, f->n_embed, pair ? 2 : 1, (int)bk, E) : 0,
+            is_i8mx(f->up_type) ? moe_i8_bytes(f->up_type, B, f->n_embed, 1, (int)bk, E) : 0,
+            is_i8mx(f->down_type) ? moe_i8_bytes(f->down_type, (int)bk, f->n_ff, 1, (int)bk, E) : 0};
+        for (int i = 0; i < 3; i++) g6 = i8[i] > g6 ? i8[i] : g6;
+    }
     const int64_t sz[FFN_REGIONS] = {
         (int64_t)B * f->n_experts * 4, bk * f->n_ff * 4, bk * f->n_ff * 4, bk * f->n_ff * 4,
         bk * f->n_embed * 4, 4 * kqk_moe_runs_words((int)bk, f->n_experts, dmax + (int)bk),
-        (int64_t)moe_group_bytes(2, (int)bk, f->n_experts, 1)};
+        (int64_t)g6};
     int64_t t = 0;
     for (int i = 0; i < FFN_REGIONS; i++) {
         off[i] = t;

@@ -377,15 +377,58 @@ def check_ulp1(got, want, what):
     assert np.all(d <= np.spacing(np.abs(want)).astype(np.float64)), what
 
 
+def gpu_multix(qtype, w, xs, N, K_in):
+    """kq_gemv_multix_dev over the rows of xs: [B, N]"""
+    dw, dx = dev(w), dev(np.ascontiguousarray(xs, np.float32).reshape(-1))
+    B = xs.shape[0]
+    dy = torch.full((B * N,), float("nan"), dtype=torch.float32, device="cuda")
+    K.gemv_multix_dev(qtype, dw.data_ptr(), dx.data_ptr(), dy.data_ptr(), B, N, K_in,
+                      stream=stream())
+    torch.cuda.synchronize()
+    return dy.cpu().numpy().reshape(B, N)
+
+
+def check_i8_tickets(port, qtype, w, sel, x, x_div, got, N_out, K_in, n_exp, n_oracle=2):
+    """Every member of an int8 batch (type | KQ_INT8_ACT) against the
+    reference's tickets (moe_forward_b, stratum_arch_moe.inc.c:1136-1201,
+    restated by oracle.moe_tickets): a ticket of two or more members of a
+    Q4_K / Q6_K expert equals kq_gemv_multix_dev over the ticket's members
+    (the multix pack arithmetic) bit for bit, and the oracle's restatement of
+    that arithmetic on the first n_oracle such tickets; a ticket of one
+    member, and every member of the other types, equals its slice's single
+    int8 GEMV bit for bit.  Returns the ticket sizes seen."""
+    qi = qtype | K.INT8_ACT
+    rb = K.lib().kq_row_bytes(qtype, K_in)
+    sl = N_out * rb
+    xr = x.reshape(-1, K_in)
+    sizes, packed = [], 0
+    for e, mem in O.moe_tickets(np.asarray(sel).reshape(-1), n_exp):
+        ws = w[e * sl:(e + 1) * sl]
+        xs = np.stack([xr[m // x_div] for m in mem])
+        sizes.append(len(mem))
+        if len(mem) == 1 or qtype not in (12, 14):
+            for i, m in enumerate(mem):
+                assert same_values(got[m], single(qi, ws, xs[i], N_out, K_in)), (e, m)
+            continue
+        want = gpu_multix(qi, ws, xs, N_out, K_in)
+        for i, m in enumerate(mem):
+            assert same_values(got[m], want[i]), (e, m, len(mem))
+        if packed < n_oracle:
+            ref = port.gemv_i8_multix(qtype, ws, xs, N_out, K_in)
+            assert same_values(want, ref), (e, len(mem))
+            packed += 1
+    return sizes
+
+
 @pytest.mark.parametrize("qtype", [12, 14, 13, 11, 8])
 @pytest.mark.parametrize("B", [1, 3])
-def test_moe_int8_members_equal_single_slice(port, qtype, B):
-    """The int8-activation mode (type | KQ_INT8_ACT: the per-slice
-    st_linear_dispatch of moe_forward_one_token under use_sdot,
-    stratum_arch_moe.inc.c:596-603): gate and up routed in one launch at
-    batch 1 (per token at B > 1), down on the written sel; every member
-    bit-identical to its slice's single int8 GEMV and within one ulp of the
-    oracle's int8 form."""
+def test_moe_int8_members(port, qtype, B):
+    """The int8-activation mode (type | KQ_INT8_ACT).  Batch 1 is
+    moe_forward_one_token's per-slice st_linear_dispatch under use_sdot
+    (stratum_arch_moe.inc.c:596-603): every member bit-identical to its
+    slice's single int8 GEMV and within one ulp of the oracle's int8 form.
+    At B = 3, moe_forward_b's tickets (check_i8_tickets).  Gate and up
+    routed in one launch, down on the written sel."""
     qi = qtype | K.INT8_ACT
     n_exp, H, F, k = 32, 512, 256, 8
     gate, up = experts(qtype, n_exp, F, H, 61), experts(qtype, n_exp, F, H, 62)
@@ -398,6 +441,13 @@ def test_moe_int8_members_equal_single_slice(port, qtype, B):
     for s_ in range(B):
         ws, ww = port.topk(probs[s_], k)
         assert list(sel[s_ * k:(s_ + 1) * k]) == ws
+    act = np.stack([synth.gaussian(r, F) for _ in range(B * k)]).reshape(-1)
+    dn = run_moe(qi, [down], sel.reshape(B, k), act, 1, B, k, n_exp, H, F)
+    if B > 1:
+        for t, w in enumerate((gate, up)):
+            check_i8_tickets(port, qtype, w, sel, x, k, got[t], F, H, n_exp)
+        check_i8_tickets(port, qtype, down, sel, act, 1, dn[0], H, F, n_exp)
+        return
     rb = K.lib().kq_row_bytes(qtype, H)
     for t, w in enumerate((gate, up)):
         for m, e in enumerate(sel):
@@ -406,8 +456,6 @@ def test_moe_int8_members_equal_single_slice(port, qtype, B):
             assert same_values(got[t][m], single(qi, ws_, xm, F, H)), (t, m)
             if m < 3:
                 check_ulp1(got[t][m], port.gemv_i8(qtype, ws_, xm, F, H), (t, m))
-    act = np.stack([synth.gaussian(r, F) for _ in range(B * k)]).reshape(-1)
-    dn = run_moe(qi, [down], sel.reshape(B, k), act, 1, B, k, n_exp, H, F)
     rbd = K.lib().kq_row_bytes(qtype, F)
     for m, e in enumerate(sel):
         ws_ = down[e * H * rbd:(e + 1) * H * rbd]
@@ -415,3 +463,72 @@ def test_moe_int8_members_equal_single_slice(port, qtype, B):
         assert same_values(dn[0][m], single(qi, ws_, am, H, F)), m
         if m < 3:
             check_ulp1(dn[0][m], port.gemv_i8(qtype, ws_, am, H, F), m)
+
+
+def designed_sel(B, k, counts, n_exp, seed):
+    """A selection [B, k] (distinct experts per token) in which expert e is
+    chosen by counts[e] tokens; the other slots take experts past
+    len(counts); ranks shuffled per token."""
+    r = np.random.default_rng(seed)
+    rows = [[] for _ in range(B)]
+    for e, c in enumerate(counts):
+        toks = sorted(range(B), key=lambda s: (len(rows[s]), r.random()))[:c]
+        for s in toks:
+            rows[s].append(e)
+    rest = list(range(len(counts), n_exp))
+    for s in range(B):
+        extra = [int(e) for e in r.permutation(rest) if e not in rows[s]][:k - len(rows[s])]
+        rows[s] += extra
+        assert len(rows[s]) == k and len(set(rows[s])) == k
+        r.shuffle(rows[s])
+    return np.array(rows, np.int32)
+
+
+@pytest.mark.parametrize("qtype", [12, 14])
+def test_moe_int8_ticket_sizes(port, qtype):
+    """Experts chosen by 1, 2, 7, 8, 9, 16 and 17 tokens (tickets 1, 2, 7,
+    8, 8+1, 8+8, 8+8+1): a ticket of one member takes the single-stream int8
+    form, a longer one the pack arithmetic over exactly its members; gate
+    and up share x per token (x_div = k), down has one x per member; one
+    slot left empty (sel -1) is not written."""
+    n_exp, H, F, k, B = 48, 768, 512, 6, 20
+    sel = designed_sel(B, k, [1, 2, 7, 8, 9, 16, 17], n_exp, 70 + qtype)
+    hole = 3 * k + int(np.nonzero(sel[3] >= 7)[0][0])   # a slot of an unplanned expert
+    sel.reshape(-1)[hole] = -1
+    gate, up = experts(qtype, n_exp, F, H, 71), experts(qtype, n_exp, F, H, 72)
+    down = experts(qtype, n_exp, H, F, 73)
+    r = np.random.default_rng(74)
+    x = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
+    act = np.stack([synth.gaussian(r, F) for _ in range(B * k)]).reshape(-1)
+    qi = qtype | K.INT8_ACT
+    print(f"moe int8 tickets type={qtype}", flush=True)
+    got = run_moe(qi, [gate, up], sel, x, k, B, k, n_exp, F, H)
+    sizes = check_i8_tickets(port, qtype, gate, sel, x, k, got[0], F, H, n_exp, n_oracle=3)
+    check_i8_tickets(port, qtype, up, sel, x, k, got[1], F, H, n_exp, n_oracle=1)
+    assert {1, 2, 7, 8}.issubset(set(sizes)), sizes
+    assert np.isnan(got[0][hole]).all()
+    dn = run_moe(qi, [down], sel, act, 1, B, k, n_exp, H, F)
+    check_i8_tickets(port, qtype, down, sel, act, 1, dn[0], H, F, n_exp, n_oracle=2)
+
+
+def test_moe_int8_config_b16(port):
+    """configs[4] in the int8 mode at batch 16 (128 experts, top-8, hidden
+    2048, expert ffn 768, Q4_K): routed gate+up, then down; every member
+    against its ticket (check_i8_tickets)."""
+    n_exp, H, F, k, B = 128, 2048, 768, 8, 16
+    gate, up = experts(12, n_exp, F, H, 81), experts(12, n_exp, F, H, 82)
+    down = experts(12, n_exp, H, F, 83)
+    r = np.random.default_rng(84)
+    probs = softmax_rows(r.standard_normal((B, n_exp)).astype(np.float32))
+    x = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
+    qi = 12 | K.INT8_ACT
+    print("moe int8 configs[4] B=16", flush=True)
+    got, sel, _ = run_routed(qi, [gate, up], probs, x, k, k, F, H)
+    for s_ in range(B):
+        assert list(sel[s_ * k:(s_ + 1) * k]) == port.topk(probs[s_], k)[0]
+    sizes = check_i8_tickets(port, 12, gate, sel, x, k, got[0], F, H, n_exp)
+    assert 1 in sizes and max(sizes) >= 2, sizes
+    check_i8_tickets(port, 12, up, sel, x, k, got[1], F, H, n_exp, n_oracle=0)
+    act = np.stack([synth.gaussian(r, F) for _ in range(B * k)]).reshape(-1)
+    dn = run_moe(qi, [down], sel.reshape(B, k), act, 1, B, k, n_exp, H, F)
+    check_i8_tickets(port, 12, down, sel, act, 1, dn[0], H, F, n_exp, n_oracle=1)

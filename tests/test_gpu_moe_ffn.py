@@ -376,9 +376,12 @@ def test_moe_ffn_never_grows_library_scratch(port, case, kq_env):
 def test_moe_ffn_step_int8(port, B):
     """The step with Q4_K experts in the int8-activation mode (gate, up and
     down types | KQ_INT8_ACT; F32 router): sel is the oracle's top-k of the
-    step's own probabilities, every gate, up and down member is
-    bit-identical to its slice's single int8 GEMV on the step's own inputs,
-    SwiGLU within 4 ulps and the combine bit for bit."""
+    step's own probabilities; every gate, up and down member is
+    bit-identical, on the step's own inputs, to its ticket's int8 call
+    (moe_forward_b's tickets of at most 8 members, oracle.moe_tickets: a
+    single int8 GEMV for a ticket of one, kq_gemv_multix_dev over the
+    ticket otherwise; at B = 1 every ticket has one member); SwiGLU within 4
+    ulps and the combine bit for bit."""
     H, F, E, k = 1024, 512, 32, 4
     d = make_layer(H, F, E, k, 9950)
     qi = TYPE_Q4_K | K.INT8_ACT
@@ -396,20 +399,33 @@ def test_moe_ffn_step_int8(port, B):
         K.gemv_dev(qi, dw.data_ptr(), dx.data_ptr(), dy.data_ptr(), N, Kd, stream=stream())
         torch.cuda.synchronize()
         return dy.cpu().numpy()
+    def multix(w, xs, N, Kd):
+        dw, dx = dev(w), dev(np.ascontiguousarray(xs).reshape(-1))
+        dy = torch.empty(xs.shape[0] * N, dtype=torch.float32, device="cuda")
+        K.gemv_multix_dev(qi, dw.data_ptr(), dx.data_ptr(), dy.data_ptr(), xs.shape[0], N, Kd,
+                          stream=stream())
+        torch.cuda.synchronize()
+        return dy.cpu().numpy().reshape(xs.shape[0], N)
+
+    def ticket(w, xs, N, Kd):
+        # moe_forward_b's ticket: one member -> the single-stream form, more
+        # -> the multix pack arithmetic over exactly those members
+        return single(w, xs[0], N, Kd)[None] if len(xs) == 1 else multix(w, xs, N, Kd)
     for s in range(B):
         p = got["probs"][s * E:(s + 1) * E]
         sel, selw = port.topk(p, k)
         assert list(got["sel"][s * k:(s + 1) * k]) == sel, s
-        for r_, e in enumerate(sel):
-            m = s * k + r_
-            xs = xn[s * H:(s + 1) * H]
-            g, u = got["g"][m * F:(m + 1) * F], got["u"][m * F:(m + 1) * F]
-            a = got["act"][m * F:(m + 1) * F]
-            assert same_values(g, single(d["gate"][e * F * rb_in:(e + 1) * F * rb_in], xs, F, H))
-            assert same_values(u, single(d["up"][e * F * rb_in:(e + 1) * F * rb_in], xs, F, H))
-            assert ulps(a, port.swiglu(g, u)).max() <= 4.0
-            o = got["ffo"][m * H:(m + 1) * H]
-            assert same_values(o, single(d["down"][e * H * rb_ff:(e + 1) * H * rb_ff], a, H, F))
+    g, u = got["g"].reshape(B * k, F), got["u"].reshape(B * k, F)
+    a, o = got["act"].reshape(B * k, F), got["ffo"].reshape(B * k, H)
+    for m in range(B * k):
+        assert ulps(a[m], port.swiglu(g[m], u[m])).max() <= 4.0
+    xr = xn.reshape(B, H)
+    for e, mem in O.moe_tickets(got["sel"], E):
+        xs = np.stack([xr[m // k] for m in mem])
+        assert same_values(g[mem], ticket(d["gate"][e * F * rb_in:(e + 1) * F * rb_in], xs, F, H))
+        assert same_values(u[mem], ticket(d["up"][e * F * rb_in:(e + 1) * F * rb_in], xs, F, H))
+        assert same_values(o[mem], ticket(d["down"][e * H * rb_ff:(e + 1) * H * rb_ff], a[mem], H,
+                                          F))
     assert same_values(got["x"], port.moe_combine(got["ffo"], got["sel"], got["selw"], x0, B, k,
                                                   H))
 

@@ -22,6 +22,7 @@ import numpy as np
 import pytest
 
 from i8_cases import reciprocal_groups
+from oracle import oracle as O
 from stratum_amd import TYPE_Q3_K, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0, synth
 
 I8_TYPES = [TYPE_Q4_K, TYPE_Q6_K, TYPE_Q5_K, TYPE_Q3_K, TYPE_Q8_0]
@@ -272,3 +273,29 @@ def test_i8_multix_within_term_bound_of_binary64_terms(port, qtype):
         d = np.abs(ys[s].astype(np.float64) - yg.astype(np.float64))
         bound = 5 * 2.0 ** -24 * mag + np.spacing(np.abs(yg)).astype(np.float64)
         assert np.all(d <= bound), s
+
+
+def test_moe_tickets_rule():
+    """oracle.moe_tickets, moe_forward_b's expert tickets
+    (stratum_arch_moe.inc.c:1136-1140, 1158-1178): a worked case, the cut
+    at 8, and over random selections the invariants the reference's loops
+    fix -- every chosen member in exactly one ticket of its expert, members
+    in increasing order, experts in increasing order, every ticket but an
+    expert's last holding exactly 8."""
+    # B = 3, k = 2: members 0..5 choose experts 1,0 | 1,2 | 0,1
+    assert O.moe_tickets([1, 0, 1, 2, 0, 1], 3) == [(0, [1, 4]), (1, [0, 2, 5]), (2, [3])]
+    assert O.moe_tickets([-1, 2, -1], 4) == [(2, [1])]
+    assert [len(m) for _, m in O.moe_tickets([5] * 19, 6)] == [8, 8, 3]
+    rng = np.random.default_rng(11)
+    for _ in range(50):
+        B, k, E = int(rng.integers(1, 40)), int(rng.integers(1, 9)), int(rng.integers(8, 64))
+        sel = np.stack([rng.choice(E, k, replace=False) for _ in range(B)]).reshape(-1)
+        sel[rng.random(sel.size) < 0.05] = -1
+        t = O.moe_tickets(sel, E)
+        seen = sorted(m for _, mem in t for m in mem)
+        assert seen == [m for m in range(sel.size) if sel[m] >= 0]
+        assert [e for e, _ in t] == sorted(e for e, _ in t)
+        for i, (e, mem) in enumerate(t):
+            assert all(sel[m] == e for m in mem) and mem == sorted(mem) and 1 <= len(mem) <= 8
+            if i + 1 < len(t) and t[i + 1][0] == e:
+                assert len(mem) == 8 and mem[-1] < t[i + 1][1][0]
