@@ -2731,8 +2731,8 @@ struct MoeGroupArg {
     int* ng;
 };
 
-__global__ __launch_bounds__(1024) void kq_moe_group_kernel(MoeGroupArg a) {
-    extern __shared__ __align__(16) int lds_i[];
+// (the body, for one workgroup of 1024 lanes with the dynamic LDS lds_i)
+__device__ void moe_group_body(const MoeGroupArg& a, int* lds_i) {
     int* cnt = lds_i;                 // [E]
     int* gid = cnt + a.E;             // [E] group index of expert e
     // [4 ceil(nm/4)] the members' experts (-1: none), 16-byte aligned, the
@@ -2805,6 +2805,11 @@ __global__ __launch_bounds__(1024) void kq_moe_group_kernel(MoeGroupArg a) {
             }
         }
     }
+}
+
+__global__ __launch_bounds__(1024) void kq_moe_group_kernel(MoeGroupArg a) {
+    extern __shared__ __align__(16) int lds_i[];
+    moe_group_body(a, lds_i);
 }
 
 // ------------------------------------------------------- MFMA multi-x
@@ -3423,6 +3428,8 @@ struct Mi8Arg {
     const MxGroup* groups;
     const int* ng;
     int zrow;
+    int rbw;                  // 16-row blocks per workgroup (1 unless KS = 1)
+    const float2* sm;         // grouped: {scale, sum} per (row, group)
 };
 
 // x -> int8 per group (the single-stream rule, kq_quantize_kernel's) and
@@ -3431,11 +3438,10 @@ struct Mi8Arg {
 // count) get zero values and coefficients, so their terms are 0.
 // It also zeroes the 256-byte zero page zp.
 template <int G>
-__global__ __launch_bounds__(256) void kq_mi8_prep_kernel(const float* x, long x_stride, int K,
-                                                          int B, int bpad, int8_t* xq,
-                                                          uint8_t* cf, uint8_t* zp) {
+__device__ __forceinline__ void mi8_prep_one(long gid, const float* x, long x_stride, int K,
+                                             int B, int bpad, int8_t* xq, uint8_t* cf,
+                                             uint8_t* zp, float2* sm) {
     const int ng = K / G;
-    const long gid = (long)blockIdx.x * 256 + threadIdx.x;
     if (gid < 16) reinterpret_cast<uint4*>(zp)[gid] = make_uint4(0, 0, 0, 0);
     if (gid >= (long)ng * bpad) return;
     const int s = (int)(gid / ng), g = (int)(gid - (long)s * ng);
@@ -3469,6 +3475,106 @@ __global__ __launch_bounds__(256) void kq_mi8_prep_kernel(const float* x, long x
         reinterpret_cast<float2*>(cf)[gid] = make_float2(scale, (float)sum * scale);
     else
         reinterpret_cast<double*>(cf)[gid] = (double)scale;
+    if (sm) sm[gid] = make_float2(scale, (float)sum);   // the single-stream form's {scale, sum}
+}
+
+template <int G>
+__global__ __launch_bounds__(256) void kq_mi8_prep_kernel(const float* x, long x_stride, int K,
+                                                          int B, int bpad, int8_t* xq,
+                                                          uint8_t* cf, uint8_t* zp, float2* sm) {
+    mi8_prep_one<G>((long)blockIdx.x * 256 + threadIdx.x, x, x_stride, K, B, bpad, xq, cf, zp, sm);
+}
+
+// The int8 MoE batch's set-up in one launch: workgroup 0 cuts the runs
+// (moe_group_body, as kq_moe_group_kernel), the others quantize the x rows
+// (1024 groups each, as kq_mi8_prep_kernel).
+template <int G>
+__global__ __launch_bounds__(1024) void kq_mi8_moe_prep_kernel(MoeGroupArg ga, const float* x,
+                                                               int K, int B, int bpad, int8_t* xq,
+                                                               uint8_t* cf, uint8_t* zp,
+                                                               float2* sm) {
+    extern __shared__ __align__(16) int lds_i[];
+    if (blockIdx.x == 0) {
+        moe_group_body(ga, lds_i);
+        return;
+    }
+    mi8_prep_one<G>((long)(blockIdx.x - 1) * 1024 + threadIdx.x, x, (long)K, K, B, bpad, xq, cf,
+                    zp, sm);
+}
+
+// A run of one member in a grouped launch (st_linear_multix at B = 1 is
+// st_linear_dispatch): the single-stream int8 kernel's arithmetic, so the
+// member equals kq_gemv_dev(type | KQ_INT8_ACT) bit for bit.  The T lanes
+// take the 64-weight chunks of rows r0 .. r0 + 16 nrw - 1 in row-major
+// order (neighbouring lanes read neighbouring chunks of a row), each chunk
+// term exactly as kq_segs_kernel forms it (term_q4k_i8 / term_q6k_i8, x
+// and {scale, sum} read from the quantized row xi), kept in LDS
+// ([row][K/64] doubles), then that kernel's row reduction: GP =
+// kq_phases(K/64) lanes per row, lane p sums chunks p, p+GP, ... in order
+// from 0, then phase_tree.  Output y[r] (y: the member's row).
+template <int TYPE>
+__device__ __forceinline__ void mi8_single(const Mi8Arg& A, const uint8_t* w, int xi, float* y,
+                                           int rb0, int nrw, double* terms, int tid, int T) {
+    using C = Chunk<TYPE>;
+    constexpr bool Q4 = TYPE == T_Q4K_I8;
+    constexpr int BB = Q4 ? 144 : 210;
+    const int N = A.N, K = A.K, NCH = K >> 6, nb = K >> 8;
+    const int r0 = rb0 * 16, nr = min(16 * nrw, N - r0), nchk = nr * NCH;
+    const uint8_t* xr = reinterpret_cast<const uint8_t*>(A.xq) + (size_t)xi * K;
+    const float2* sr = A.sm + (size_t)xi * (Q4 ? K >> 5 : K >> 4);
+    struct In { typename C::Raw r; uint4 x[4]; float s[8]; };
+    auto ld = [&](int f, In& in) {
+        const int fc = min(f, nchk - 1), rr = fc / NCH, c = fc - rr * NCH;
+        const wptr blk = to_global(w) + (size_t)(r0 + rr) * nb * BB + (size_t)(c >> 2) * BB;
+        in.r = C::load(blk, c & 3);
+        if constexpr (Q4) {
+            // chunk c: x[64c .. 64c+63], groups 2c, 2c+1
+#pragma unroll
+            for (int k = 0; k < 4; k++) in.x[k] = *reinterpret_cast<const uint4*>(xr + 64 * c + 16 * k);
+            const float4 s4 = *reinterpret_cast<const float4*>(sr + 2 * c);
+            in.s[0] = s4.x; in.s[1] = s4.y; in.s[2] = s4.z; in.s[3] = s4.w;
+        } else {
+            // chunk c = (block bi, half h, is): run t at 256 bi + 128 h + 32 t + 16 is
+            const int bi = c >> 2, h = (c >> 1) & 1, is = c & 1;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int pos = 256 * bi + 128 * h + 32 * t + 16 * is;
+                in.x[t] = *reinterpret_cast<const uint4*>(xr + pos);
+                const float2 v = sr[pos >> 4];
+                in.s[2 * t] = v.x; in.s[2 * t + 1] = v.y;
+            }
+        }
+    };
+    auto term = [&](int f, const In& in) {
+        const int fc = min(f, nchk - 1), rr = fc / NCH, c = fc - rr * NCH;
+        double t;
+        if constexpr (Q4)
+            t = term_q4k_i8(in.r, c & 3, reinterpret_cast<const uint32_t*>(in.x),
+                            make_float4(in.s[0], in.s[1], in.s[2], in.s[3]));
+        else
+            t = term_q6k_i8(in.r, c & 3, reinterpret_cast<const uint32_t*>(in.x), in.s);
+        if (f < nchk) terms[rr * NCH + c] = t;
+    };
+    // two batches in flight: the next one's loads go out before this one's term
+    const int nit = (nchk + T - 1) / T;
+    In a, b;
+    ld(tid, a);
+    for (int it = 0; it < nit; it += 2) {
+        ld(tid + (it + 1) * T, b);
+        term(tid + it * T, a);
+        ld(tid + (it + 2) * T, a);
+        if (it + 1 < nit) term(tid + (it + 1) * T, b);
+    }
+    __syncthreads();
+    const int GP = kq_phases(NCH), lgp = GP == 32 ? 5 : 3;
+    for (int task = tid; task < 16 * nrw * GP; task += T) {   // whole waves
+        const int rho = task >> lgp, p = task & (GP - 1);
+        const double* tr = terms + rho * NCH;
+        double v = 0.0;
+        for (int i = p; i < NCH; i += GP) v = v + tr[i];
+        v = phase_tree(v, GP);
+        if (p == 0 && rho < nr) y[r0 + rho] = (float)v;
+    }
 }
 
 // Weight registers of one super-block of one lane's row.
@@ -3501,11 +3607,7 @@ struct Mi8W6 { uint32_t l[4][5], h[4][5], s[5]; uint32_t d, sh; };
 // one expert's members).  A run of two or more members takes
 // st_linear_multix's pack arithmetic above, exactly as a kq_gemv_multix_dev
 // call on that expert's slice would.  A run of one member takes the
-// single-stream path (st_linear_multix at B = 1 is st_linear_dispatch): the
-// single-stream int8 kernel's chunk terms (term_q4k_i8 / term_q6k_i8, from
-// the same exact dots; the Q4_K x sums come from one more MFMA against a
-// B operand of ones), kept in LDS (dynamic, 16 rows x K/64 doubles) and
-// reduced in that kernel's phase order, so the member equals its
+// single-stream path (mi8_single): the member equals its
 // kq_gemv_dev(type | KQ_INT8_ACT) result bit for bit.
 template <int TYPE, int SW, int P, int KS, bool GR>
 __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
@@ -3524,25 +3626,36 @@ __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
     const int q = lane >> 4, jr = lane & 15;
     const int N = A.N, K = A.K, nb = K >> 8;
     const int ng = Q4 ? K >> 5 : K >> 4;            // coefficient groups per stream
-    const int rb = blockIdx.x, s0 = GR ? 0 : blockIdx.y * SW;
-    const int row = min(rb * 16 + jr, N - 1);
+    const int s0 = GR ? 0 : blockIdx.y * SW;
+    // row blocks rb0 .. rb0 + nrw - 1 (one after the other; KS = 1 only)
+    const int rbw = KS == 1 ? A.rbw : 1;
+    const int rb0 = blockIdx.x * rbw, nrw = min(rbw, (N + 15) / 16 - rb0);
     constexpr int BB = Q4 ? 144 : 210;
     const MxGroup* gp = nullptr;
     int M = SW;
     const uint8_t* wbase = A.w;
     if constexpr (GR) {
-        if ((int)blockIdx.y >= *A.ng) return;     // uniform over the workgroup
-        gp = A.groups + blockIdx.y;
+        gp = A.groups + blockIdx.y;               // read with the count (in bounds)
+        const int ngv = *A.ng;
         M = gp->M;
         wbase = gp->w;
+        if ((int)blockIdx.y >= ngv) return;       // uniform over the workgroup
     }
     // quantized row of member slot j (0 .. SW-1)
     auto xrow = [&](int j) -> long {
         if constexpr (GR) return j < M ? gp->xi[j] : A.zrow;
         return s0 + j;
     };
-    const bool single = GR && M == 1;             // uniform
-    const wptr wr = to_global(wbase) + (size_t)row * (size_t)nb * BB;
+    if (GR && M == 1) {                           // uniform
+        extern __shared__ __align__(16) double mi8_terms[];
+        mi8_single<TYPE>(A, wbase, gp->xi[0], gp->y + (size_t)gp->yi[0] * A.y_stride, rb0, nrw,
+                         mi8_terms, tid, 64 * KS);
+        return;
+    }
+    // this lane's weight row in row block rb0 + i
+    auto wrow = [&](int i) -> wptr {
+        return to_global(wbase) + (size_t)min((rb0 + i) * 16 + jr, N - 1) * (size_t)nb * BB;
+    };
     const int nbp = (nb + KS - 1) / KS;             // super-blocks per K-part
     const int kb0 = kp * nbp, kb1 = min(nb, kb0 + nbp);
     uint8_t* wl = lds + kp * WL;                    // this wave's LDS
@@ -3566,8 +3679,8 @@ __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
     for (int k = 0; k < CPT; k++) crow[k] = xrow(min(lane + 64 * k, CU - 1) / CPS);
 
     struct Slot { W w; i32x4 a[4][NM]; uint4 c[CPT]; };
-    auto load = [&](int b, Slot& sl) {
-        const wptr blk = wr + (size_t)b * BB;
+    auto load = [&](int i, int b, Slot& sl) {
+        const wptr blk = wrow(i) + (size_t)b * BB;
         if constexpr (Q4) {
             sl.w.hd = ld16(blk);
 #pragma unroll
@@ -3606,33 +3719,55 @@ __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
                 cf + ((size_t)crow[k] * ng + (size_t)b * (CB / 8)) * 8 + 16 * (v % CPS));
         }
     };
-    // a run of one member: chunk terms of the 16 rows, [row][K/64]
-    extern __shared__ __align__(16) double mi8_terms[];
-    const int NCH = K >> 6;
-
     double acc[NACC];
 #pragma unroll
     for (int a = 0; a < NACC; a++) acc[a] = 0.0;
     const i32x4 zero = {0, 0, 0, 0};
-    // A ring of R = P + 1 register slots: step i computes slot i % R and
-    // reloads slot (i + P) % R, which step i - 1 finished with, for
-    // super-block i + P.  The loop body is R steps with no exit (the steps
-    // past the K-part only reload), so every slot keeps its registers around
-    // the loop and no load in flight is waited for early to move one.
+    // A row block's end (KS = 1): its outputs, then the sums start again.
+    auto finish = [&](int ib) {
+        const int r = (rb0 + ib) * 16 + jr;
+#pragma unroll
+        for (int a = 0; a < NACC; a++) {
+            const int so = Q4 ? 8 * (a >> 1) + 2 * q + (a & 1) : 4 * a + q;   // member slot
+            if (r < N) {
+                if constexpr (GR) {
+                    if (so < M) gp->y[(size_t)gp->yi[so] * A.y_stride + r] = (float)acc[a];
+                } else if (s0 + so < A.B) {
+                    A.y[(size_t)(s0 + so) * A.y_stride + r] = (float)acc[a];
+                }
+            }
+            acc[a] = 0.0;
+        }
+    };
+    // A ring of R = P + 1 register slots: step t computes slot t % R and
+    // reloads slot (t + P) % R, which step t - 1 finished with, for step
+    // t + P.  Step t is row block t / nbp, super-block kb0 + t % nbp.  The
+    // loop body is R steps with no exit (the steps past the end only
+    // reload), so every slot keeps its registers around the loop and no
+    // load in flight is waited for early to move one.
     constexpr int R = P + 1;
+    const int nst = nrw * nbp;
+    int ci = 0, cb = kb0;                           // this step's row block, super-block
+    int li = 0, lb = kb0;                           // those of the step P ahead
     Slot ring[R];
 #pragma unroll
-    for (int p = 0; p < P; p++) load(min(kb0 + p, nb - 1), ring[p]);
-    const int nit = (nbp + R - 1) / R * R;
+    for (int p = 0; p < P; p++) {
+        load(min(li, nrw - 1), min(lb, nb - 1), ring[p]);
+        if (++lb == kb0 + nbp) { lb = kb0; li++; }
+    }
+    const int nit = (nst + R - 1) / R * R;
     for (int i0 = 0; i0 < nit; i0 += R) {
 #pragma unroll
         for (int p = 0; p < R; p++) {
-            const int b = kb0 + i0 + p;
+            const int b = cb, ib = ci;
             const Slot& cur = ring[p];
-            const bool go = b < kb1;                 // uniform
+            const bool go = i0 + p < nst && b < kb1;               // uniform
+            const bool last = KS == 1 && go && b == nb - 1;        // a row block's end
+            if (++cb == kb0 + nbp) { cb = kb0; ci++; }
             // the next loads go out first: waiting for this step's slot
             // then leaves them in flight
-            load(min(b + P, nb - 1), ring[(p + P) % R]);
+            load(min(li, nrw - 1), min(lb, nb - 1), ring[(p + P) % R]);
+            if (++lb == kb0 + nbp) { lb = kb0; li++; }
             if (go) {
                 // the coefficients into this wave's LDS (unconditional
                 // stores: a lane past the last piece stores it again)
@@ -3665,25 +3800,6 @@ __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
                                        (int)((qv.y >> sh) & 0x0f0f0f0fu),
                                        (int)((qv.z >> sh) & 0x0f0f0f0fu),
                                        (int)((qv.w >> sh) & 0x0f0f0f0fu)};
-                    if (GR && single) {
-                        // slot 0 (lanes 0-15): the dots and x sums of both
-                        // sub-blocks, then term_q4k_i8's binary64 term
-                        const i32x4 ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
-                        const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.a[j][0], bop, zero,
-                                                                              0, 0, 0);
-                        const i32x4 X = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.a[j][0], ones, zero,
-                                                                              0, 0, 0);
-                        if (q == 0) {
-                            const float4 c = *reinterpret_cast<const float4*>(wl + 16 * j);
-                            const float c1 = dm.x * c.x, c2 = -(dm.y * c.x);
-                            const float c3 = dm.z * c.z, c4 = -(dm.w * c.z);
-                            const double t1 = fma((double)c1, (double)D[0], (double)c2 * (double)X[0]);
-                            const double t2 = fma((double)c3, (double)D[1], (double)c4 * (double)X[1]);
-                            mi8_terms[jr * NCH + 4 * b + j] = t1 + t2;
-                        }
-                        __builtin_amdgcn_sched_barrier(0);
-                        continue;
-                    }
 #pragma unroll
                     for (int m = 0; m < NM; m++) {
                         const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.a[j][m], bop, zero,
@@ -3729,27 +3845,6 @@ __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
                         bw[k] = ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u;   // bytes v - 32
                     }
                     const i32x4 bop = {(int)bw[0], (int)bw[1], (int)bw[2], (int)bw[3]};
-                    if (GR && single) {
-                        // slot 0 (lanes 0-15): the four runs' dots of q - 32,
-                        // then term_q6k_i8's binary64 term
-                        const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.a[u][0], bop, zero,
-                                                                              0, 0, 0);
-                        if (q == 0) {
-                            const double* cs = reinterpret_cast<const double*>(wl);
-                            const float df = f16_bits_to_f32(cur.w.d);
-                            double t = 0.0;
-#pragma unroll
-                            for (int r4 = 0; r4 < 4; r4++) {
-                                const int g = 8 * h + is + 2 * r4;
-                                const float sc = (float)(int8_t)(uint8_t)(S[g >> 2] >> (8 * (g & 3)));
-                                const float c = df * sc * (float)cs[g];
-                                t = t + (double)c * (double)D[r4];
-                            }
-                            mi8_terms[jr * NCH + 4 * b + u] = t;
-                        }
-                        __builtin_amdgcn_sched_barrier(0);
-                        continue;
-                    }
 #pragma unroll
                     for (int m = 0; m < NM; m++) {
                         const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.a[u][m], bop, zero,
@@ -3763,25 +3858,11 @@ __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
+            if (last) finish(ib);
         }
     }
-    if (GR && single) {
-        // the single-stream kernel's row reduction: GP = kq_phases(K/64)
-        // lanes per row, lane p sums chunks p, p+GP, ... in order from 0,
-        // then phase_tree (16 GP tasks, whole waves)
-        __syncthreads();
-        const int GP = kq_phases(NCH), lgp = GP == 32 ? 5 : 3;
-        for (int task = tid; task < 16 * GP; task += 64 * KS) {
-            const int rho = task >> lgp, p = task & (GP - 1);
-            const double* tr = mi8_terms + rho * NCH;
-            double v = 0.0;
-            for (int i = p; i < NCH; i += GP) v = v + tr[i];
-            v = phase_tree(v, GP);
-            const int r = rb * 16 + rho;
-            if (p == 0 && r < N) gp->y[(size_t)gp->yi[0] * A.y_stride + r] = (float)v;
-        }
-        return;
-    }
+    if (KS == 1) return;
+    // KS > 1: one row block (rb0)
     // the K-parts' partial sums, added in K-part order
     double* part = reinterpret_cast<double*>(lds);
     if (KS > 1) {
@@ -3798,17 +3879,7 @@ __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
             acc[a] = v;
         }
     }
-    const int r = rb * 16 + jr;
-    if (r >= N) return;
-#pragma unroll
-    for (int a = 0; a < NACC; a++) {
-        const int so = Q4 ? 8 * (a >> 1) + 2 * q + (a & 1) : 4 * a + q;   // member slot
-        if constexpr (GR) {
-            if (so < M) gp->y[(size_t)gp->yi[so] * A.y_stride + r] = (float)acc[a];
-        } else if (s0 + so < A.B) {
-            A.y[(size_t)(s0 + so) * A.y_stride + r] = (float)acc[a];
-        }
-    }
+    finish(0);
 }
 
 // Bit-exact dequantization, one lane per 64-weight chunk (64 floats out).
@@ -4911,10 +4982,10 @@ int kqk_launch_mi8(int type, const float* xs, long x_stride, const void* w, floa
     const long groups = (long)bpad * (K / G);
     if (G == 32)
         hipLaunchKernelGGL(kq_mi8_prep_kernel<32>, dim3((unsigned)((groups + 255) / 256)), dim3(256),
-                           0, st, xs, x_stride, K, B, bpad, xq, cf, zp);
+                           0, st, xs, x_stride, K, B, bpad, xq, cf, zp, nullptr);
     else
         hipLaunchKernelGGL(kq_mi8_prep_kernel<16>, dim3((unsigned)((groups + 255) / 256)), dim3(256),
-                           0, st, xs, x_stride, K, B, bpad, xq, cf, zp);
+                           0, st, xs, x_stride, K, B, bpad, xq, cf, zp, nullptr);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
     Mi8Arg a;
@@ -4925,7 +4996,7 @@ int kqk_launch_mi8(int type, const float* xs, long x_stride, const void* w, floa
     a.y = ys;
     a.y_stride = y_stride;
     a.N = N; a.K = K; a.B = B;
-    a.groups = nullptr; a.ng = nullptr; a.zrow = 0;
+    a.groups = nullptr; a.ng = nullptr; a.zrow = 0; a.rbw = 1; a.sm = nullptr;
     // Q4_K: 8 or 16 streams per wave; Q6_K: 8 (its A operands take
     // 16 registers per MFMA and super-block)
     const int SW = type == T_Q6K_I8 || B <= 8 ? 8 : 16;
@@ -4953,35 +5024,74 @@ int kqk_launch_mi8(int type, const float* xs, long x_stride, const void* w, floa
 }
 
 // The int8 MoE batch: workspace bytes for nx quantized x rows (plus the
-// zero row) and the launches (prep over the nx rows; the grouped main
-// kernel over up to ngmax groups, *ng of them live, each a run of at most 8
-// members built by kq_moe_group_kernel).  K-parts as kqk_launch_mi8 takes
-// them, so a run's members equal a kq_gemv_multix_dev call over them.
-long kqk_mi8_moe_workspace(int type, int nx, int K) {
-    long cf_off = 0;
-    return nx < 1 ? -1 : kqk_mi8_workspace(type, nx + 1, K, &cf_off);
+// zero row: the MULTISEQ workspace of nx + 1 streams, then the rows'
+// {scale, sum} pairs) and the launches: the runs of at most 8 members of
+// one expert (kq_moe_group_kernel's rule; records in groups, their count
+// in *ng, at most ngmax) together with the quantized x rows (nx = nm /
+// x_div of them), then the grouped main kernel.  K-parts as kqk_launch_mi8
+// takes them, so a run's members equal a kq_gemv_multix_dev call over them.
+#ifndef KQ_MI8_RBW
+#define KQ_MI8_RBW 2
+#endif
+static long mi8_moe_layout(int type, int nx, int K, long* cf_off, long* sm_off, long* zp_off) {
+    const long base = nx < 1 ? -1 : kqk_mi8_workspace(type, nx + 1, K, cf_off);
+    if (base < 0) return -1;
+    const long bpad = (nx + 1 + 15) & ~15L;
+    *zp_off = base - 256;
+    *sm_off = base;
+    return base + ((bpad * (K / (type == T_Q4K_I8 ? 32 : 16)) * 8 + 255) & ~255L);
 }
 
-int kqk_launch_mi8_moe(int type, const float* x, int nx, int K, const void* groups,
-                       const int* ng, int ngmax, int N, long y_stride, void* ws, hipStream_t st) {
-    long cf_off = 0;
-    const long wsb = kqk_mi8_workspace(type, nx + 1, K, &cf_off);
-    const long tl = 16L * (K >> 6) * 8;          // a single member's chunk terms
+long kqk_mi8_moe_workspace(int type, int nx, int K) {
+    long a, b, c;
+    return mi8_moe_layout(type, nx, K, &a, &b, &c);
+}
+
+int kqk_launch_mi8_moe(int type, const int* sel, int nm, int E, int nt, int x_div,
+                       const void* w0, const void* w1, float* y0, float* y1, long estride,
+                       const float* x, int K, void* groups, int* ng, int ngmax, int N,
+                       void* ws, hipStream_t st) {
+    const int nx = x_div > 0 ? nm / x_div : 0;
+    const long y_stride = N;
+    if (nm < 1 || E < 1 || E > 4096 || nt < 1 || nt > 2 || x_div < 1 || nm % x_div)
+        return (int)hipErrorInvalidValue;
+    long cf_off = 0, sm_off = 0, zp_off = 0;
+    const long wsb = mi8_moe_layout(type, nx, K, &cf_off, &sm_off, &zp_off);
+    const int ks = kqk_mi8_parts(K);
+    // several row blocks per workgroup when the row is one K-part: a run's
+    // workgroup then streams one weight sequence instead of paying a
+    // launch-to-first-load latency per 16 rows
+    const int rbw = ks == 1 ? KQ_MI8_RBW : 1;
+    const long tl = 16L * rbw * (K >> 6) * 8;    // a single member's chunk terms
     if (wsb < 0 || nx < 1 || N < 1 || ngmax < 1 || ngmax > 65535 || y_stride < N || !groups ||
         !ng || ((uintptr_t)x & 15) || ((uintptr_t)ws & 15) || tl > 65536)
         return (int)hipErrorInvalidValue;
     int8_t* xq = static_cast<int8_t*>(ws);
     uint8_t* cf = static_cast<uint8_t*>(ws) + cf_off;
-    uint8_t* zp = static_cast<uint8_t*>(ws) + wsb - 256;
+    uint8_t* zp = static_cast<uint8_t*>(ws) + zp_off;
+    float2* sm = reinterpret_cast<float2*>(static_cast<uint8_t*>(ws) + sm_off);
     const int G = type == T_Q4K_I8 ? 32 : 16;
     const int bpad = (nx + 1 + 15) & ~15;        // rows nx .. bpad-1 zero
     const long gq = (long)bpad * (K / G);
+    // the runs (workgroup 0, kq_moe_group_kernel's rule with run length 8)
+    // and the quantized rows (the other workgroups) in one launch
+    MoeGroupArg ga;
+    ga.sel = sel; ga.nm = nm; ga.E = E; ga.nt = nt; ga.x_div = x_div; ga.mch = 8;
+    ga.w[0] = static_cast<const uint8_t*>(w0);
+    ga.w[1] = static_cast<const uint8_t*>(nt > 1 ? w1 : w0);
+    ga.y[0] = y0;
+    ga.y[1] = nt > 1 ? y1 : y0;
+    ga.estride = estride;
+    ga.groups = static_cast<MxGroup*>(groups);
+    ga.ng = ng;
+    const size_t glds = (size_t)(((2 * E + 3) & ~3) + 4 * ((nm + 3) / 4)) * sizeof(int);
+    const dim3 pg((unsigned)(1 + (gq + 1023) / 1024));
     if (G == 32)
-        hipLaunchKernelGGL(kq_mi8_prep_kernel<32>, dim3((unsigned)((gq + 255) / 256)), dim3(256), 0,
-                           st, x, (long)K, K, nx, bpad, xq, cf, zp);
+        hipLaunchKernelGGL(kq_mi8_moe_prep_kernel<32>, pg, dim3(1024), glds, st, ga, x, K, nx, bpad,
+                           xq, cf, zp, sm);
     else
-        hipLaunchKernelGGL(kq_mi8_prep_kernel<16>, dim3((unsigned)((gq + 255) / 256)), dim3(256), 0,
-                           st, x, (long)K, K, nx, bpad, xq, cf, zp);
+        hipLaunchKernelGGL(kq_mi8_moe_prep_kernel<16>, pg, dim3(1024), glds, st, ga, x, K, nx, bpad,
+                           xq, cf, zp, sm);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
     Mi8Arg a;
@@ -4993,7 +5103,9 @@ int kqk_launch_mi8_moe(int type, const float* x, int nx, int K, const void* grou
     a.groups = static_cast<const MxGroup*>(groups);
     a.ng = ng;
     a.zrow = nx;
-    const int nrb = (N + 15) / 16, ks = kqk_mi8_parts(K);
+    a.rbw = rbw;
+    a.sm = sm;
+    const int nrb = ((N + 15) / 16 + rbw - 1) / rbw;
 #define KQ_MI8G_GO(T_, P_, K_)                                                               \
     hipLaunchKernelGGL((kq_mi8_kernel<T_, 8, P_, K_, true>), dim3((unsigned)nrb,             \
                        (unsigned)ngmax), dim3(64 * K_), (size_t)tl, st, a)

@@ -104,8 +104,10 @@ int kqk_mi8_parts(int K);
 int kqk_launch_mi8(int type, const float* xs, long x_stride, const void* w, float* ys,
                    long y_stride, int B, int N, int K, void* ws, int ks, hipStream_t st);
 long kqk_mi8_moe_workspace(int type, int nx, int K);
-int kqk_launch_mi8_moe(int type, const float* x, int nx, int K, const void* groups,
-                       const int* ng, int ngmax, int N, long y_stride, void* ws, hipStream_t st);
+int kqk_launch_mi8_moe(int type, const int* sel, int nm, int E, int nt, int x_div,
+                       const void* w0, const void* w1, float* y0, float* y1, long estride,
+                       const float* x, int K, void* groups, int* ng, int ngmax, int N,
+                       void* ws, hipStream_t st);
 int kqk_launch_moe_group(const int* sel, int nm, int E, int nt, int x_div, int mch,
                          const void* w0, const void* w1, float* y0, float* y1, long estride,
                          void* groups, int* ng, hipStream_t st);

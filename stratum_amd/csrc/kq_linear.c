@@ -1148,8 +1148,9 @@ static size_t moe_i8_bytes(int type, int nx, int K, int nt, int nm, int E) {
  * in increasing member order, in tickets of at most CH = 8 through
  * st_linear_multix: a ticket of two or more members takes the multix pack
  * arithmetic, a ticket of one the single-stream path.  Here the same runs
- * are cut on the device (kq_moe_group_kernel, run length 8), every x row
- * is quantized once, and one grouped matrix-core launch computes all runs
+ * are cut on the device (kq_moe_group_kernel's rule, run length 8) in the
+ * launch that quantizes every x row once, and one grouped matrix-core
+ * launch computes all runs
  * (kq_mi8_kernel, GR): each member equals kq_gemv_multix_dev over its run
  * (kq_gemv_dev for a run of one) bit for bit.  The workspace is io->grp
  * when given (the FFN step's), else the library's matrix-core scratch. */
@@ -1173,11 +1174,9 @@ static int moe_i8_batch(const kq_moe_op* op, const int* sel, int B, int k, int E
     const int ngmax = nt * (dmax + (nm + 7) / 8);
     void* groups = base + xwa;
     int* ng = (int*)(base + xwa + (size_t)ngmax * (size_t)kqk_mx_group_bytes());
-    int e = kqk_launch_moe_group(sel, nm, E, nt, op->x_div, 8, op->w[0], op->w[nt - 1], op->y[0],
-                                 op->y[nt - 1], (long)op->expert_stride, groups, ng, st);
-    if (e) return kq_fail("moe group launch: %s", hipGetErrorString((hipError_t)e));
-    e = kqk_launch_mi8_moe(op->type, op->x, nx, K, groups, ng, ngmax, op->n_out, op->n_out, base,
-                           st);
+    const int e = kqk_launch_mi8_moe(op->type, sel, nm, E, nt, op->x_div, op->w[0], op->w[nt - 1],
+                                     op->y[0], op->y[nt - 1], (long)op->expert_stride, op->x, K,
+                                     groups, ng, ngmax, op->n_out, base, st);
     if (e) return kq_fail("int8 moe launch: %s", hipGetErrorString((hipError_t)e));
     return 0;
 }
