@@ -5033,6 +5033,12 @@ int kqk_launch_mi8(int type, const float* xs, long x_stride, const void* w, floa
 #ifndef KQ_MI8_RBW
 #define KQ_MI8_RBW 2
 #endif
+// (Q4_K super-blocks in flight per wave: 1 keeps the wave at 114 VGPRs,
+// four waves per SIMD; measured at configs[4] B = 4 / 16 / 64 against 2
+// and 3, and against 1 and 4 row blocks per workgroup)
+#ifndef KQ_MI8G_P
+#define KQ_MI8G_P 1
+#endif
 static long mi8_moe_layout(int type, int nx, int K, long* cf_off, long* sm_off, long* zp_off) {
     const long base = nx < 1 ? -1 : kqk_mi8_workspace(type, nx + 1, K, cf_off);
     if (base < 0) return -1;
@@ -5113,7 +5119,7 @@ int kqk_launch_mi8_moe(int type, const int* sel, int nm, int E, int nt, int x_di
     if (ks == 1) KQ_MI8G_GO(T_, P_, 1);                                                      \
     else if (ks == 2) KQ_MI8G_GO(T_, P_, 2);                                                 \
     else KQ_MI8G_GO(T_, P_, 4);
-    if (type == T_Q4K_I8) { KQ_MI8G_KS(T_Q4K_I8, 2) } else { KQ_MI8G_KS(T_Q6K_I8, 1) }
+    if (type == T_Q4K_I8) { KQ_MI8G_KS(T_Q4K_I8, KQ_MI8G_P) } else { KQ_MI8G_KS(T_Q6K_I8, 1) }
 #undef KQ_MI8G_KS
 #undef KQ_MI8G_GO
     return (int)hipGetLastError();
