@@ -1993,6 +1993,10 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
 constexpr int TB_Q4K = 1, TB_Q6K = 2, TB_Q2K = 4, TB_NIB = 8, TB_ALL = 15;
 constexpr int TB_Q5K = 32, TB_Q3K = 64, TB_Q80 = 128, TB_Q4K_I8 = 256, TB_Q6K_I8 = 512;
 constexpr int TB_Q5K_I8 = 1024, TB_Q3K_I8 = 2048, TB_Q80_I8 = 4096;
+// Q4_K and Q6_K in the int8 mode mixed in one launch (st_mixed_fused_sdot,
+// stratum_linear.h:1043-1085: one dispatch for a group whose tensors have
+// either type, e.g. Q, K, V with a Q6_K V)
+constexpr int TB_I8MIX = TB_Q4K_I8 | TB_Q6K_I8;
 // TB_SEL: the MoE gather instantiations (every segment has a selection)
 constexpr int TB_SEL = 16;
 
@@ -2051,6 +2055,8 @@ __global__ __launch_bounds__(1024) void kq_segs_kernel(SegsArg A) {
             case T_Q6K: if (TYPES & TB_Q6K) { KQ_RUN(T_Q6K) } break;
             case T_Q2K: if (TYPES & TB_Q2K) { KQ_RUN(T_Q2K) } break;
             case T_NIB: if (TYPES & TB_NIB) { KQ_RUN(T_NIB) } break;
+            case T_Q4K_I8: if (TYB == TB_I8MIX) { KQ_RUN(T_Q4K_I8) } break;
+            case T_Q6K_I8: if (TYB == TB_I8MIX) { KQ_RUN(T_Q6K_I8) } break;
             default: break;
             }
         }
@@ -4440,8 +4446,8 @@ long kqk_segs_lds(const kqk_seg* segs, int nseg, int grid, int* xs_off, int* ter
 
 // Every instantiation, indexed by [multi][depth - 1][slot]: slots 0..3 and
 // 5..7 single types (type_slot), 4 the mixed-type kernel, 8..12 the int8
-// mode of Q4_K, Q6_K, Q5_K, Q3_K and Q8_0.
-constexpr int NSLOT = 13;
+// mode of Q4_K, Q6_K, Q5_K, Q3_K and Q8_0, 13 int8 Q4_K and Q6_K mixed.
+constexpr int NSLOT = 14;
 #define KQ_SEGS_ROW(D, M)                                                       \
     {&kq_segs_kernel<D, TB_Q4K, M>, &kq_segs_kernel<D, TB_Q6K, M>,              \
      &kq_segs_kernel<D, TB_Q2K, M>, &kq_segs_kernel<D, TB_NIB, M>,              \
@@ -4449,13 +4455,14 @@ constexpr int NSLOT = 13;
      &kq_segs_kernel<D, TB_Q3K, M>, &kq_segs_kernel<D, TB_Q80, M>,              \
      &kq_segs_kernel<D, TB_Q4K_I8, M>, &kq_segs_kernel<D, TB_Q6K_I8, M>,        \
      &kq_segs_kernel<D, TB_Q5K_I8, M>, &kq_segs_kernel<D, TB_Q3K_I8, M>,        \
-     &kq_segs_kernel<D, TB_Q80_I8, M>}
+     &kq_segs_kernel<D, TB_Q80_I8, M>, &kq_segs_kernel<1, TB_I8MIX, M>}
 typedef void (*segs_fn)(SegsArg);
 static const segs_fn k_segs[2][2][NSLOT] = {{KQ_SEGS_ROW(1, false), KQ_SEGS_ROW(2, false)},
                                            {KQ_SEGS_ROW(1, true), KQ_SEGS_ROW(2, true)}};
 #undef KQ_SEGS_ROW
-// the MoE gather (TB_SEL) instantiations, single type only (slot 4
-// unused: the mixed kernel has no gather form; the int8 mode's at depth 1)
+// the MoE gather (TB_SEL) instantiations, single type only (slots 4 and
+// 13 unused: the mixed kernels have no gather form; the int8 mode's at
+// depth 1)
 #define KQ_SEL_ROW(D, M)                                                                  \
     {&kq_segs_kernel<D, TB_Q4K | TB_SEL, M>, &kq_segs_kernel<D, TB_Q6K | TB_SEL, M>,       \
      &kq_segs_kernel<D, TB_Q2K | TB_SEL, M>, &kq_segs_kernel<D, TB_NIB | TB_SEL, M>,       \
@@ -4463,7 +4470,7 @@ static const segs_fn k_segs[2][2][NSLOT] = {{KQ_SEGS_ROW(1, false), KQ_SEGS_ROW(
      &kq_segs_kernel<D, TB_Q3K | TB_SEL, M>, &kq_segs_kernel<D, TB_Q80 | TB_SEL, M>,       \
      &kq_segs_kernel<1, TB_Q4K_I8 | TB_SEL, M>, &kq_segs_kernel<1, TB_Q6K_I8 | TB_SEL, M>, \
      &kq_segs_kernel<1, TB_Q5K_I8 | TB_SEL, M>, &kq_segs_kernel<1, TB_Q3K_I8 | TB_SEL, M>, \
-     &kq_segs_kernel<1, TB_Q80_I8 | TB_SEL, M>}
+     &kq_segs_kernel<1, TB_Q80_I8 | TB_SEL, M>, &kq_segs_kernel<1, TB_Q4K_I8 | TB_SEL, M>}
 static const segs_fn k_segs_sel[2][2][NSLOT] = {{KQ_SEL_ROW(1, false), KQ_SEL_ROW(2, false)},
                                                {KQ_SEL_ROW(1, true), KQ_SEL_ROW(2, true)}};
 #undef KQ_SEL_ROW
@@ -4543,19 +4550,19 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
     const int t = set == TB_Q4K ? 0 : set == TB_Q6K ? 1 : set == TB_Q2K ? 2 : set == TB_NIB ? 3
                 : set == TB_Q5K ? 5 : set == TB_Q3K ? 6 : set == TB_Q80 ? 7
                 : set == TB_Q4K_I8 ? 8 : set == TB_Q6K_I8 ? 9 : set == TB_Q5K_I8 ? 10
-                : set == TB_Q3K_I8 ? 11 : set == TB_Q80_I8 ? 12
+                : set == TB_Q3K_I8 ? 11 : set == TB_Q80_I8 ? 12 : set == TB_I8MIX ? 13
                 : (set & ~TB_ALL) ? -1 : 4;
     if (t < 0) return (int)hipErrorInvalidValue;   // other types are never mixed in a launch
-    if (t == 4) depth = 1;   // the all-types kernel fits 128 VGPRs at depth 1 only
+    if (t == 4 || t == 13) depth = 1;   // the mixed kernels fit 128 VGPRs at depth 1 only
     int nsel = 0;
     for (int i = 0; i < nseg; i++) nsel += segs[i].sel != nullptr;
-    if (nsel && (nsel != nseg || t == 4)) return (int)hipErrorInvalidValue;
+    if (nsel && (nsel != nseg || t == 4 || t == 13)) return (int)hipErrorInvalidValue;
     // the MoE FFN step pieces: one selection segment; the combine needs
     // equal parts whose rows are a multiple of the grid and its outputs in
     // the x region; in-launch softmax needs every logit in a lane
     const kqk_seg& h0 = segs[0];
     if (h0.act || h0.cx || h0.logits) {
-        if (nseg != 1 || !h0.sel || t == 4 || (h0.act && h0.cx))
+        if (nseg != 1 || !h0.sel || t == 4 || t == 13 || (h0.act && h0.cx))
             return (int)hipErrorInvalidValue;
         if (h0.act || h0.cx) {   // equal parts, rows a multiple of the grid, outputs in the x region
             const int pn = h0.rows[0];
@@ -4999,7 +5006,16 @@ int kqk_launch_mi8(int type, const float* xs, long x_stride, const void* w, floa
     a.groups = nullptr; a.ng = nullptr; a.zrow = 0; a.rbw = 1; a.sm = nullptr;
     // Q4_K: 8 or 16 streams per wave; Q6_K: 8 (its A operands take
     // 16 registers per MFMA and super-block)
-    const int SW = type == T_Q6K_I8 || B <= 8 ? 8 : 16;
+    // (8 streams per wave up to B = 8, one super-block in flight; measured
+    // at the 27B gate, B = 8 .. 64, against 8 streams at every B and two
+    // super-blocks in flight)
+#ifndef KQ_MI8_SWB
+#define KQ_MI8_SWB 8
+#endif
+#ifndef KQ_MI8_P8
+#define KQ_MI8_P8 1
+#endif
+    const int SW = type == T_Q6K_I8 || B <= KQ_MI8_SWB ? 8 : 16;
     const int nset = (B + SW - 1) / SW, nrb = (N + 15) / 16;
     // K-parts: a function of the row length only (kqk_mi8_parts), so the
     // binary64 grouping -- and with it the result -- does not depend on the
@@ -5014,7 +5030,7 @@ int kqk_launch_mi8(int type, const float* xs, long x_stride, const void* w, floa
     else if (ks == 4) KQ_MI8_GO(T_, S_, P_, 4);                                              \
     else KQ_MI8_GO(T_, S_, P_, 8);
     if (type == T_Q4K_I8) {
-        if (SW == 8) { KQ_MI8_KS(T_Q4K_I8, 8, 2) } else { KQ_MI8_KS(T_Q4K_I8, 16, 1) }
+        if (SW == 8) { KQ_MI8_KS(T_Q4K_I8, 8, KQ_MI8_P8) } else { KQ_MI8_KS(T_Q4K_I8, 16, 1) }
     } else {
         KQ_MI8_KS(T_Q6K_I8, 8, 1)
     }

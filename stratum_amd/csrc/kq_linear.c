@@ -102,6 +102,13 @@ static int is_dense(int type) { return type == KQ_TYPE_F16 || type == KQ_TYPE_F3
 /* the types the multi-x (MULTISEQ, MoE batch) kernel and the mixed-type
  * segment kernel cover; the other block types run single-type launches and
  * per-stream calls */
+/* Q4_K / Q6_K in the int8 mode: the types whose st_linear_multix under
+ * use_sdot has its own (pack) arithmetic at B >= 2, and which share a
+ * launch in a group (st_mixed_fused_sdot) */
+static int is_i8mx(int type) {
+    return type == (KQ_INT8_ACT | KQ_TYPE_Q4_K) || type == (KQ_INT8_ACT | KQ_TYPE_Q6_K);
+}
+
 static int is_core(int type) {
     return type == KQ_TYPE_Q2_K || type == KQ_TYPE_Q4_K || type == KQ_TYPE_Q6_K ||
            type == KQ_TYPE_Q2K_NIB;
@@ -295,16 +302,23 @@ static int plan_depth(void) {
 
 static int launch_segs_one(const kqk_seg* segs, int nseg, hipStream_t st);
 
+/* Whether one kernel instantiation takes segments of types a and b
+ * together: any mix of the core types; Q4_K and Q6_K in the int8 mode (as
+ * st_mixed_fused_sdot, stratum_linear.h:1043-1085); else one type. */
+static int same_launch(int a, int b) {
+    if (is_core(a)) return is_core(b);
+    if (is_i8mx(a)) return is_i8mx(b);
+    return a == b;
+}
+
 /* One launch per run of consecutive segments that one kernel instantiation
- * takes: any mix of the core types, or one other block type.  The
- * segments are independent, so splitting changes no result. */
+ * takes (same_launch).  The segments are independent, so splitting changes
+ * no result. */
 static int launch_segs(const kqk_seg* segs, int nseg, hipStream_t st) {
     int i = 0;
     while (i < nseg) {
         int j = i + 1;
-        while (j < nseg && (is_core(segs[i].type) ? is_core(segs[j].type)
-                                                   : segs[j].type == segs[i].type))
-            j++;
+        while (j < nseg && same_launch(segs[i].type, segs[j].type)) j++;
         if (launch_segs_one(segs + i, j - i, st)) return -1;
         i = j;
     }
@@ -1125,12 +1139,6 @@ static int moe_batch(const kq_moe_op* op, int* sel, const float* probs, float* s
                       op->n_out, op->n_out, op->k_in, st);
     if (e) return kq_fail("moe gemv launch: %s", hipGetErrorString((hipError_t)e));
     return 0;
-}
-
-/* Q4_K / Q6_K in the int8 mode: the types whose st_linear_multix under
- * use_sdot has its own (pack) arithmetic at B >= 2 */
-static int is_i8mx(int type) {
-    return type == (KQ_INT8_ACT | KQ_TYPE_Q4_K) || type == (KQ_INT8_ACT | KQ_TYPE_Q6_K);
 }
 
 /* Bytes of moe_i8_batch's workspace for nx x rows of K, nt tensors and nm

@@ -202,6 +202,32 @@ def test_segments_share_x_with_exact_path(port):
             check_ulp(got, port.gemv_i8(t & 0xff, ws[i], x, N, H), f"seg {i}")
 
 
+@pytest.mark.parametrize("order", [(12, 12, 14), (14, 12, 14, 14, 12)])
+def test_segments_mixed_int8_q4k_q6k_one_launch(port, order):
+    """Q4_K and Q6_K in the int8 mode in one segment list (a Q, K, V group
+    with a Q6_K V): one launch of the mixed int8 kernel, as
+    st_mixed_fused_sdot dispatches the group once (stratum_linear.h:
+    1043-1085); each output equals its own single int8 launch."""
+    H = 2048
+    x = synth.gaussian(synth.rng(8650), H)
+    rows = [512, 128, 160, 96, 64]
+    dx = dev(x)
+    ws, dws, dys, segs = [], [], [], []
+    for i, t in enumerate(order):
+        N = rows[i]
+        ws.append(synth.tensor(t, N, H, 8660 + i))
+        dws.append(dev(ws[-1]))
+        dys.append(torch.full((N,), float("nan"), dtype=torch.float32, device="cuda"))
+        segs.append(K.segment(t | INT8_ACT, H, N, [dws[-1].data_ptr()], dx.data_ptr(),
+                              dys[-1].data_ptr()))
+    K.gemv_segments_dev(segs, stream=stream())
+    torch.cuda.synchronize()
+    for i, t in enumerate(order):
+        got = dys[i].cpu().numpy()
+        assert same_values(got, gpu_gemv(t | INT8_ACT, ws[i], x, rows[i], H)), (i, t)
+        check_ulp(got, port.gemv_i8(t, ws[i], x, rows[i], H), f"seg {i}")
+
+
 @pytest.mark.parametrize("qtype", I8_TYPES)
 def test_segments_groups_strided_x(port, qtype):
     """A segment of several groups, each with its own x (x_stride), as the
