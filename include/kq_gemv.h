@@ -65,8 +65,13 @@ extern "C" {
  * summed in binary64 instead of the reference's four binary32 FMA lanes,
  * so y differs from q*_dot_row_sdot_f by at most 2^-22 * sum|term| (the
  * lanes' own rounding) and is independent of the launch shape.  The
- * weights are unchanged: kq_row_bytes is the base type's.  No MoE or
- * matrix-core form. */
+ * weights are unchanged: kq_row_bytes is the base type's.  Batches take
+ * the reference's batch arithmetic: kq_gemv_multix_dev at B >= 2 for Q4_K
+ * and Q6_K the multix pack form (below), kq_moe_gemv_dev /
+ * kq_moe_gemv_routed_dev / kq_moe_ffn_dev at B > 1 moe_forward_b's
+ * tickets (at kq_moe_gemv_dev).  A segment list mixing Q4_K and Q6_K in
+ * this mode runs as one launch (st_mixed_fused_sdot,
+ * stratum_linear.h:1043-1085). */
 #define KQ_INT8_ACT     0x100
 
 /* Layout-compatible with GgufTensor (stratum_gguf.h:129-137): a caller may
@@ -362,7 +367,14 @@ int kq_moe_topk_dev(const float* probs, int B, int E, int k, int* sel, float* se
  * stratum_arch_moe.inc.c:1130-1205) and streams each selected slice once
  * for all of its tokens.  B <= KQ_MOE_MAX_TOKENS, k <= KQ_MAX_GROUPS.  No
  * counterpart as one call in the reference, which dispatches per slice
- * (moe_dispatch_slice / moe_multix_slice, :596-603, :808-815). */
+ * (moe_dispatch_slice / moe_multix_slice, :596-603, :808-815).
+ * Int8 mode (type | KQ_INT8_ACT) at B > 1, Q4_K / Q6_K: moe_forward_b's
+ * tickets under use_sdot (:1136-1201): each expert's members in increasing
+ * m, cut into tickets of at most 8; a member of a ticket of two or more
+ * equals kq_gemv_multix_dev over exactly that ticket's members (the multix
+ * pack arithmetic), a member of a ticket of one equals kq_gemv_dev.  This
+ * path uses the library's matrix-core scratch (grown on first use); the
+ * other int8 types run per token. */
 typedef struct kq_moe_op {
     int type, n_out, k_in;
     int ntensors;

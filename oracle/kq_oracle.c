@@ -9,6 +9,13 @@
  * The arithmetic follows the reference statement by statement; the code
  * is organised by 32- or 16-weight sub-block rather than by the
  * reference's pointer walks.  Reference lines are cited per function.
+ *
+ * Pinning (tests/test_oracle*.py): every function is checked against the
+ * reference build (oracle/_ref), golden vectors, closed forms or exact-input
+ * identities.  One point is parity unpinned: in ko_gemv_i8_multix the
+ * association of each Q4_K term's three binary32 products follows the
+ * reference source as read, and no independent check separates it from
+ * another association (the NEON source does not build here).
  */
 #define _GNU_SOURCE
 #include "kq_oracle.h"
@@ -755,7 +762,9 @@ int ko_gemv_i8(int type, const uint8_t* w, const float* x, const float* add, flo
  * merge order, stratum_q4k_neon.h:1066-1071); the single-row multix_pack
  * form, used for an odd last row, is the same arithmetic except at B = 7,
  * where it takes a binary32-accumulating variant (q4k_dot_row_sdot_pack_b7)
- * that is not restated here. */
+ * that is not restated here.  Parity unpinned for the association of the
+ * Q4_K term's products (see the header); indexing, signs, coefficients and
+ * magnitude are pinned by exact inputs and quant_test.c's relation. */
 int ko_gemv_i8_multix(int type, const uint8_t* w, const float* xs, float* ys, int B, int N,
                       int K) {
     if ((type != KO_Q4_K && type != KO_Q6_K) || K % 256 || B < 1) return -1;
