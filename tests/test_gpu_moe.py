@@ -532,3 +532,26 @@ def test_moe_int8_config_b16(port):
     act = np.stack([synth.gaussian(r, F) for _ in range(B * k)]).reshape(-1)
     dn = run_moe(qi, [down], sel.reshape(B, k), act, 1, B, k, n_exp, H, F)
     check_i8_tickets(port, 12, down, sel, act, 1, dn[0], H, F, n_exp, n_oracle=1)
+
+
+@pytest.mark.parametrize("qtype", [12, 14])
+@pytest.mark.parametrize("H,F", [(4096, 256), (256, 12288)])
+def test_moe_int8_tickets_long_rows(port, qtype, H, F):
+    """Rows of 16 and 48 super-blocks (gate/up K = 4096, down K = 12288),
+    where the ticket kernel splits each row over 2 and 4 waves (K-parts) and
+    takes one row block per workgroup: every member against its ticket, with
+    tickets of 1, 2, 7, 8 and 9 members."""
+    n_exp, k, B = 16, 4, 12
+    sel = designed_sel(B, k, [1, 2, 7, 9], n_exp, 90 + qtype)
+    gate = experts(qtype, n_exp, F, H, 91)
+    down = experts(qtype, n_exp, H, F, 93)
+    r = np.random.default_rng(94)
+    x = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
+    act = np.stack([synth.gaussian(r, F) for _ in range(B * k)]).reshape(-1)
+    qi = qtype | K.INT8_ACT
+    print(f"moe int8 long rows type={qtype} H={H} F={F}", flush=True)
+    got = run_moe(qi, [gate], sel, x, k, B, k, n_exp, F, H)
+    sizes = check_i8_tickets(port, qtype, gate, sel, x, k, got[0], F, H, n_exp, n_oracle=2)
+    assert {1, 2, 7, 8}.issubset(set(sizes)), sizes
+    dn = run_moe(qi, [down], sel, act, 1, B, k, n_exp, H, F)
+    check_i8_tickets(port, qtype, down, sel, act, 1, dn[0], H, F, n_exp, n_oracle=2)
