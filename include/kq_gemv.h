@@ -465,7 +465,9 @@ int64_t kq_moe_ffn_workspace_bytes(const kq_moe_ffn* f, int B);
  * instead of grouping the selection again, with the same results.  Where
  * a launch groups the selection in a launch of its own (run tables too
  * large for LDS, or KQ_MOE_GROUP_LAUNCH), the group records also go to the
- * workspace: the step never touches the library's scratch. */
+ * workspace; so do, for int8 Q4_K / Q6_K experts (type | KQ_INT8_ACT) at
+ * B > 1, the quantized rows and tickets of moe_forward_b's ticket batch
+ * (kq_moe_gemv_dev): the step never touches the library's scratch. */
 int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* sel, float* selw,
                    void* work, int64_t work_bytes, kq_stream stream);
 
