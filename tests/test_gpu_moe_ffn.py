@@ -381,7 +381,8 @@ def test_moe_ffn_step_int8(port, B):
     (moe_forward_b's tickets of at most 8 members, oracle.moe_tickets: a
     single int8 GEMV for a ticket of one, kq_gemv_multix_dev over the
     ticket otherwise; at B = 1 every ticket has one member); SwiGLU within 4
-    ulps and the combine bit for bit."""
+    ulps and the combine bit for bit; the library's scratch stays empty
+    across the step (the ticket batch's workspace is the step's)."""
     H, F, E, k = 1024, 512, 32, 4
     d = make_layer(H, F, E, k, 9950)
     qi = TYPE_Q4_K | K.INT8_ACT
@@ -390,7 +391,10 @@ def test_moe_ffn_step_int8(port, B):
     xn = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
     x0 = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
     print(f"moe ffn int8 B={B}", flush=True)
+    K.lib().kq_linear_shutdown()                  # the step allocates nothing
+    assert K.lib().kq_scratch_bytes() == 0
     got = run_step(d, xn, x0, B)
+    assert K.lib().kq_scratch_bytes() == 0
     rb_in, rb_ff = synth.row_bytes(TYPE_Q4_K, H), synth.row_bytes(TYPE_Q4_K, F)
 
     def single(w, xv, N, Kd):
