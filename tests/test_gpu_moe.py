@@ -555,3 +555,32 @@ def test_moe_int8_tickets_long_rows(port, qtype, H, F):
     assert {1, 2, 7, 8}.issubset(set(sizes)), sizes
     dn = run_moe(qi, [down], sel, act, 1, B, k, n_exp, H, F)
     check_i8_tickets(port, qtype, down, sel, act, 1, dn[0], H, F, n_exp, n_oracle=2)
+
+
+@pytest.mark.parametrize("B,E,k", [(5, 1000, 1), (4, 4096, 8), (64, 32, 2)])
+def test_moe_int8_tickets_shapes(port, B, E, k):
+    """Int8 batches at the edges of the ticket cut: one rank per token
+    (every member alone unless tokens share their expert), 4096 experts
+    (the grouping's LDS tables at their largest), and 64 tokens over 32
+    experts (tickets of eight and their remainders); Q4_K gate and up
+    routed, then down on the written sel, against check_i8_tickets."""
+    H, F = (256, 256) if E > 1024 else (512, 256)
+    gate, up = experts(12, E, F, H, 101), experts(12, E, F, H, 102)
+    down = experts(12, E, H, F, 103)
+    r = np.random.default_rng(104 + B)
+    probs = softmax_rows(r.standard_normal((B, E)).astype(np.float32))
+    x = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
+    act = np.stack([synth.gaussian(r, F) for _ in range(B * k)]).reshape(-1)
+    qi = 12 | K.INT8_ACT
+    print(f"moe int8 tickets B={B} E={E} k={k}", flush=True)
+    if E <= 1024:
+        got, sel, _ = run_routed(qi, [gate, up], probs, x, k, k, F, H)
+    else:
+        sel = np.stack([port.topk(probs[s], k)[0] for s in range(B)]).astype(np.int32).reshape(-1)
+        got = run_moe(qi, [gate, up], sel.reshape(B, k), x, k, B, k, E, F, H)
+    for s_ in range(B):
+        assert list(sel[s_ * k:(s_ + 1) * k]) == port.topk(probs[s_], k)[0]
+    for t, w in enumerate((gate, up)):
+        check_i8_tickets(port, 12, w, sel, x, k, got[t], F, H, E, n_oracle=1)
+    dn = run_moe(qi, [down], sel.reshape(B, k), act, 1, B, k, E, H, F)
+    check_i8_tickets(port, 12, down, sel, act, 1, dn[0], H, F, E, n_oracle=1)
