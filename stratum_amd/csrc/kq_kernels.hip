@@ -3509,37 +3509,33 @@ __global__ __launch_bounds__(1024) void kq_mi8_moe_prep_kernel(MoeGroupArg ga, c
 }
 
 // A run of one member in a grouped launch (st_linear_multix at B = 1 is
-// st_linear_dispatch): the single-stream int8 kernel's arithmetic, so the
-// member equals kq_gemv_dev(type | KQ_INT8_ACT) bit for bit.  The T lanes
-// take the 64-weight chunks of rows r0 .. r0 + 16 nrw - 1 in row-major
-// order (neighbouring lanes read neighbouring chunks of a row), each chunk
-// term exactly as kq_segs_kernel forms it (term_q4k_i8 / term_q6k_i8, x
-// and {scale, sum} read from the quantized row xi), kept in LDS
-// ([row][K/64] doubles), then that kernel's row reduction: GP =
-// kq_phases(K/64) lanes per row, lane p sums chunks p, p+GP, ... in order
-// from 0, then phase_tree.  Output y[r] (y: the member's row).
+// st_linear_dispatch; for Q5_K, Q3_K and Q8_0 every member is one): the
+// single-stream int8 kernel's arithmetic, so the member equals
+// kq_gemv_dev(type | KQ_INT8_ACT) bit for bit.  The T lanes take the
+// 64-weight chunks of rows r0 .. r0 + 16 nrw - 1 in row-major order
+// (neighbouring lanes read neighbouring chunks of a row); each chunk term is
+// kq_segs_kernel's (Chunk<TYPE>::term), with the chunk's x and {scale, sum}
+// pairs read from the quantized row xi in the order that kernel stages them
+// (store_i8), kept in LDS ([row][K/64] doubles); then that kernel's row
+// reduction: GP = kq_phases(K/64) lanes per row, lane p sums chunks p,
+// p+GP, ... in order from 0, then phase_tree.  Output y[r] (y: the member's
+// row).
 template <int TYPE>
 __device__ __forceinline__ void mi8_single(const Mi8Arg& A, const uint8_t* w, int xi, float* y,
                                            int rb0, int nrw, double* terms, int tid, int T) {
     using C = Chunk<TYPE>;
-    constexpr bool Q4 = TYPE == T_Q4K_I8;
-    constexpr int BB = Q4 ? 144 : 210;
+    constexpr int BB = TypeInfo<TYPE>::BB;
+    constexpr bool Q6 = TYPE == T_Q6K_I8, Q3 = TYPE == T_Q3K_I8;
     const int N = A.N, K = A.K, NCH = K >> 6, nb = K >> 8;
     const int r0 = rb0 * 16, nr = min(16 * nrw, N - r0), nchk = nr * NCH;
     const uint8_t* xr = reinterpret_cast<const uint8_t*>(A.xq) + (size_t)xi * K;
-    const float2* sr = A.sm + (size_t)xi * (Q4 ? K >> 5 : K >> 4);
-    struct In { typename C::Raw r; uint4 x[4]; float s[8]; };
+    const float2* sr = A.sm + (size_t)xi * (Q6 ? K >> 4 : K >> 5);
+    struct In { typename C::Raw r; uint4 x[4]; float4 s[2]; };
     auto ld = [&](int f, In& in) {
         const int fc = min(f, nchk - 1), rr = fc / NCH, c = fc - rr * NCH;
         const wptr blk = to_global(w) + (size_t)(r0 + rr) * nb * BB + (size_t)(c >> 2) * BB;
         in.r = C::load(blk, c & 3);
-        if constexpr (Q4) {
-            // chunk c: x[64c .. 64c+63], groups 2c, 2c+1
-#pragma unroll
-            for (int k = 0; k < 4; k++) in.x[k] = *reinterpret_cast<const uint4*>(xr + 64 * c + 16 * k);
-            const float4 s4 = *reinterpret_cast<const float4*>(sr + 2 * c);
-            in.s[0] = s4.x; in.s[1] = s4.y; in.s[2] = s4.z; in.s[3] = s4.w;
-        } else {
+        if constexpr (Q6) {
             // chunk c = (block bi, half h, is): run t at 256 bi + 128 h + 32 t + 16 is
             const int bi = c >> 2, h = (c >> 1) & 1, is = c & 1;
 #pragma unroll
@@ -3547,18 +3543,29 @@ __device__ __forceinline__ void mi8_single(const Mi8Arg& A, const uint8_t* w, in
                 const int pos = 256 * bi + 128 * h + 32 * t + 16 * is;
                 in.x[t] = *reinterpret_cast<const uint4*>(xr + pos);
                 const float2 v = sr[pos >> 4];
-                in.s[2 * t] = v.x; in.s[2 * t + 1] = v.y;
+                reinterpret_cast<float2*>(in.s)[t] = v;
             }
+        } else if constexpr (Q3) {
+            // chunk c = (block bi, s, h): part j holds the h-th 16 values of
+            // 32-group 8 bi + 4 s + j
+            const int bi = c >> 2, sg = (c >> 1) & 1, h = c & 1;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int gi = 8 * bi + 4 * sg + j;
+                in.x[j] = *reinterpret_cast<const uint4*>(xr + 32 * gi + 16 * h);
+                reinterpret_cast<float2*>(in.s)[j] = sr[gi];
+            }
+        } else {
+            // Q4_K, Q5_K, Q8_0: chunk c = x[64c .. 64c+63], groups 2c, 2c+1
+#pragma unroll
+            for (int k = 0; k < 4; k++) in.x[k] = *reinterpret_cast<const uint4*>(xr + 64 * c + 16 * k);
+            in.s[0] = *reinterpret_cast<const float4*>(sr + 2 * c);
         }
     };
     auto term = [&](int f, const In& in) {
         const int fc = min(f, nchk - 1), rr = fc / NCH, c = fc - rr * NCH;
-        double t;
-        if constexpr (Q4)
-            t = term_q4k_i8(in.r, c & 3, reinterpret_cast<const uint32_t*>(in.x),
-                            make_float4(in.s[0], in.s[1], in.s[2], in.s[3]));
-        else
-            t = term_q6k_i8(in.r, c & 3, reinterpret_cast<const uint32_t*>(in.x), in.s);
+        const double t = C::template term<false>(in.r, c & 3, reinterpret_cast<const float4*>(in.x),
+                                                 reinterpret_cast<const float*>(in.s), 0, 1.0f, 0.0);
         if (f < nchk) terms[rr * NCH + c] = t;
     };
     // two batches in flight: the next one's loads go out before this one's term
@@ -3581,6 +3588,21 @@ __device__ __forceinline__ void mi8_single(const Mi8Arg& A, const uint8_t* w, in
         v = phase_tree(v, GP);
         if (p == 0 && rho < nr) y[r0 + rho] = (float)v;
     }
+}
+
+// The int8 MoE batch of the types whose st_linear_multix is per stream
+// (Q5_K, Q3_K, Q8_0: every member alone, grouped with run length 1): one
+// workgroup of 256 lanes per (rbw 16-row blocks, member), mi8_single.
+template <int TYPE>
+__global__ __launch_bounds__(256) void kq_mi8s_kernel(Mi8Arg A) {
+    extern __shared__ __align__(16) double mi8s_terms[];
+    const MxGroup* gp = A.groups + blockIdx.y;    // read with the count (in bounds)
+    const int ngv = *A.ng;
+    const uint8_t* w = gp->w;
+    if ((int)blockIdx.y >= ngv) return;           // uniform over the workgroup
+    const int rb0 = blockIdx.x * A.rbw, nrw = min(A.rbw, (A.N + 15) / 16 - rb0);
+    mi8_single<TYPE>(A, w, gp->xi[0], gp->y + (size_t)gp->yi[0] * A.y_stride, rb0, nrw,
+                     mi8s_terms, threadIdx.x, 256);
 }
 
 // Weight registers of one super-block of one lane's row.
@@ -5056,12 +5078,17 @@ int kqk_launch_mi8(int type, const float* xs, long x_stride, const void* w, floa
 #define KQ_MI8G_P 1
 #endif
 static long mi8_moe_layout(int type, int nx, int K, long* cf_off, long* sm_off, long* zp_off) {
-    const long base = nx < 1 ? -1 : kqk_mi8_workspace(type, nx + 1, K, cf_off);
+    // the per-32 types share Q4_K's layout (their batches use only the
+    // quantized rows and the {scale, sum} pairs)
+    const int lt = type == T_Q6K_I8 ? T_Q6K_I8
+                 : type == T_Q4K_I8 || type == T_Q5K_I8 || type == T_Q3K_I8 || type == T_Q80_I8
+                 ? T_Q4K_I8 : -1;
+    const long base = nx < 1 || lt < 0 ? -1 : kqk_mi8_workspace(lt, nx + 1, K, cf_off);
     if (base < 0) return -1;
     const long bpad = (nx + 1 + 15) & ~15L;
     *zp_off = base - 256;
     *sm_off = base;
-    return base + ((bpad * (K / (type == T_Q4K_I8 ? 32 : 16)) * 8 + 255) & ~255L);
+    return base + ((bpad * (K / (lt == T_Q4K_I8 ? 32 : 16)) * 8 + 255) & ~255L);
 }
 
 long kqk_mi8_moe_workspace(int type, int nx, int K) {
@@ -5079,11 +5106,13 @@ int kqk_launch_mi8_moe(int type, const int* sel, int nm, int E, int nt, int x_di
         return (int)hipErrorInvalidValue;
     long cf_off = 0, sm_off = 0, zp_off = 0;
     const long wsb = mi8_moe_layout(type, nx, K, &cf_off, &sm_off, &zp_off);
+    const bool pack = type == T_Q4K_I8 || type == T_Q6K_I8;   // runs of up to 8, else of 1
     const int ks = kqk_mi8_parts(K);
     // several row blocks per workgroup when the row is one K-part: a run's
     // workgroup then streams one weight sequence instead of paying a
-    // launch-to-first-load latency per 16 rows
-    const int rbw = ks == 1 ? KQ_MI8_RBW : 1;
+    // launch-to-first-load latency per 16 rows (the per-stream types: four,
+    // 256 lanes on 64 rows, when their chunk terms fit)
+    const int rbw = pack ? (ks == 1 ? KQ_MI8_RBW : 1) : (K <= 8192 ? 4 : 1);
     const long tl = 16L * rbw * (K >> 6) * 8;    // a single member's chunk terms
     if (wsb < 0 || nx < 1 || N < 1 || ngmax < 1 || ngmax > 65535 || y_stride < N || !groups ||
         !ng || ((uintptr_t)x & 15) || ((uintptr_t)ws & 15) || tl > 65536)
@@ -5092,13 +5121,13 @@ int kqk_launch_mi8_moe(int type, const int* sel, int nm, int E, int nt, int x_di
     uint8_t* cf = static_cast<uint8_t*>(ws) + cf_off;
     uint8_t* zp = static_cast<uint8_t*>(ws) + zp_off;
     float2* sm = reinterpret_cast<float2*>(static_cast<uint8_t*>(ws) + sm_off);
-    const int G = type == T_Q4K_I8 ? 32 : 16;
+    const int G = type == T_Q6K_I8 ? 16 : 32;
     const int bpad = (nx + 1 + 15) & ~15;        // rows nx .. bpad-1 zero
     const long gq = (long)bpad * (K / G);
-    // the runs (workgroup 0, kq_moe_group_kernel's rule with run length 8)
-    // and the quantized rows (the other workgroups) in one launch
+    // the runs (workgroup 0, kq_moe_group_kernel's rule with run length 8,
+    // or 1) and the quantized rows (the other workgroups) in one launch
     MoeGroupArg ga;
-    ga.sel = sel; ga.nm = nm; ga.E = E; ga.nt = nt; ga.x_div = x_div; ga.mch = 8;
+    ga.sel = sel; ga.nm = nm; ga.E = E; ga.nt = nt; ga.x_div = x_div; ga.mch = pack ? 8 : 1;
     ga.w[0] = static_cast<const uint8_t*>(w0);
     ga.w[1] = static_cast<const uint8_t*>(nt > 1 ? w1 : w0);
     ga.y[0] = y0;
@@ -5128,6 +5157,16 @@ int kqk_launch_mi8_moe(int type, const int* sel, int nm, int E, int nt, int x_di
     a.rbw = rbw;
     a.sm = sm;
     const int nrb = ((N + 15) / 16 + rbw - 1) / rbw;
+    if (!pack) {
+        const dim3 g((unsigned)nrb, (unsigned)ngmax);
+        if (type == T_Q5K_I8)
+            hipLaunchKernelGGL(kq_mi8s_kernel<T_Q5K_I8>, g, dim3(256), (size_t)tl, st, a);
+        else if (type == T_Q3K_I8)
+            hipLaunchKernelGGL(kq_mi8s_kernel<T_Q3K_I8>, g, dim3(256), (size_t)tl, st, a);
+        else
+            hipLaunchKernelGGL(kq_mi8s_kernel<T_Q80_I8>, g, dim3(256), (size_t)tl, st, a);
+        return (int)hipGetLastError();
+    }
 #define KQ_MI8G_GO(T_, P_, K_)                                                               \
     hipLaunchKernelGGL((kq_mi8_kernel<T_, 8, P_, K_, true>), dim3((unsigned)nrb,             \
                        (unsigned)ngmax), dim3(64 * K_), (size_t)tl, st, a)

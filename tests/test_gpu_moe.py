@@ -584,3 +584,35 @@ def test_moe_int8_tickets_shapes(port, B, E, k):
         check_i8_tickets(port, 12, w, sel, x, k, got[t], F, H, E, n_oracle=1)
     dn = run_moe(qi, [down], sel.reshape(B, k), act, 1, B, k, E, H, F)
     check_i8_tickets(port, 12, down, sel, act, 1, dn[0], H, F, E, n_oracle=1)
+
+
+@pytest.mark.parametrize("qtype", [13, 11, 8])
+@pytest.mark.parametrize("H,F,N_g", [(768, 512, 512), (256, 12288, 12288), (512, 256, 200)])
+def test_moe_int8_per_stream_types(port, qtype, H, F, N_g):
+    """Q5_K, Q3_K and Q8_0 batches in the int8 mode: st_linear_multix is per
+    stream for them, so every member of every ticket equals its slice's
+    single int8 GEMV bit for bit (one grouped launch of single-member runs).
+    Experts chosen by 1, 2, 9 and 17 tokens with one slot left empty (sel
+    -1, not written); rows of 16 chunks up to 192 (down K = 12288: one row
+    block per workgroup), and a gate of 200 rows (a partial last row block,
+    gate only)."""
+    n_exp, k, B = 24, 4, 20
+    sel = designed_sel(B, k, [1, 2, 9, 17], n_exp, 110 + qtype)
+    hole = 5 * k + int(np.nonzero(sel[5] >= 4)[0][0])
+    sel.reshape(-1)[hole] = -1
+    gate = experts(qtype, n_exp, N_g, H, 111)
+    r = np.random.default_rng(112 + qtype)
+    x = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
+    qi = qtype | K.INT8_ACT
+    print(f"moe int8 per-stream type={qtype} H={H} F={F} N={N_g}", flush=True)
+    got = run_moe(qi, [gate], sel, x, k, B, k, n_exp, N_g, H)
+    sizes = check_i8_tickets(port, qtype, gate, sel, x, k, got[0], N_g, H, n_exp)
+    assert {1, 2, 8}.issubset(set(sizes)), sizes
+    assert np.isnan(got[0][hole]).all()
+    if N_g != F:
+        return
+    down = experts(qtype, n_exp, H, F, 113)
+    act = np.stack([synth.gaussian(r, F) for _ in range(B * k)]).reshape(-1)
+    dn = run_moe(qi, [down], sel, act, 1, B, k, n_exp, H, F)
+    check_i8_tickets(port, qtype, down, sel, act, 1, dn[0], H, F, n_exp)
+    assert np.isnan(dn[0][hole]).all()

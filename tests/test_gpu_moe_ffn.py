@@ -372,30 +372,32 @@ def test_moe_ffn_never_grows_library_scratch(port, case, kq_env):
     assert np.abs(got["x"] - full["x"]).max() <= 1e-4 * contrib
 
 
-@pytest.mark.parametrize("B", [1, 3])
-def test_moe_ffn_step_int8(port, B):
-    """The step with Q4_K experts in the int8-activation mode (gate, up and
-    down types | KQ_INT8_ACT; F32 router): sel is the oracle's top-k of the
+@pytest.mark.parametrize("qtype,B", [(TYPE_Q4_K, 1), (TYPE_Q4_K, 3), (14, 3), (13, 3), (8, 3)])
+def test_moe_ffn_step_int8(port, qtype, B):
+    """The step with experts in the int8-activation mode (gate, up and down
+    types | KQ_INT8_ACT; F32 router): sel is the oracle's top-k of the
     step's own probabilities; every gate, up and down member is
     bit-identical, on the step's own inputs, to its ticket's int8 call
-    (moe_forward_b's tickets of at most 8 members, oracle.moe_tickets: a
-    single int8 GEMV for a ticket of one, kq_gemv_multix_dev over the
-    ticket otherwise; at B = 1 every ticket has one member); SwiGLU within 4
-    ulps and the combine bit for bit; the library's scratch stays empty
-    across the step (the ticket batch's workspace is the step's)."""
+    (moe_forward_b's tickets of at most 8 members, oracle.moe_tickets: for
+    Q4_K / Q6_K a single int8 GEMV for a ticket of one, kq_gemv_multix_dev
+    over the ticket otherwise; for Q5_K / Q8_0, whose multix is per stream,
+    every member's single int8 GEMV; at B = 1 every ticket has one member);
+    SwiGLU within 4 ulps and the combine bit for bit; the library's scratch
+    stays empty across the step (the ticket batch's workspace is the
+    step's)."""
     H, F, E, k = 1024, 512, 32, 4
-    d = make_layer(H, F, E, k, 9950)
-    qi = TYPE_Q4_K | K.INT8_ACT
+    d = make_layer(H, F, E, k, 9950, qtype=qtype)
+    qi = qtype | K.INT8_ACT
     d["gate_type"] = d["up_type"] = d["down_type"] = qi
     r = synth.rng(9951 + B)
     xn = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
     x0 = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
-    print(f"moe ffn int8 B={B}", flush=True)
+    print(f"moe ffn int8 type={qtype} B={B}", flush=True)
     K.lib().kq_linear_shutdown()                  # the step allocates nothing
     assert K.lib().kq_scratch_bytes() == 0
     got = run_step(d, xn, x0, B)
     assert K.lib().kq_scratch_bytes() == 0
-    rb_in, rb_ff = synth.row_bytes(TYPE_Q4_K, H), synth.row_bytes(TYPE_Q4_K, F)
+    rb_in, rb_ff = synth.row_bytes(qtype, H), synth.row_bytes(qtype, F)
 
     def single(w, xv, N, Kd):
         dw, dx = dev(w), dev(xv)
@@ -413,8 +415,11 @@ def test_moe_ffn_step_int8(port, B):
 
     def ticket(w, xs, N, Kd):
         # moe_forward_b's ticket: one member -> the single-stream form, more
-        # -> the multix pack arithmetic over exactly those members
-        return single(w, xs[0], N, Kd)[None] if len(xs) == 1 else multix(w, xs, N, Kd)
+        # -> the multix pack arithmetic over exactly those members (per
+        # stream for the types without a pack)
+        if len(xs) > 1 and qtype in (TYPE_Q4_K, 14):
+            return multix(w, xs, N, Kd)
+        return np.stack([single(w, xv, N, Kd) for xv in xs])
     for s in range(B):
         p = got["probs"][s * E:(s + 1) * E]
         sel, selw = port.topk(p, k)
