@@ -368,13 +368,13 @@ int kq_moe_topk_dev(const float* probs, int B, int E, int k, int* sel, float* se
  * for all of its tokens.  B <= KQ_MOE_MAX_TOKENS, k <= KQ_MAX_GROUPS.  No
  * counterpart as one call in the reference, which dispatches per slice
  * (moe_dispatch_slice / moe_multix_slice, :596-603, :808-815).
- * Int8 mode (type | KQ_INT8_ACT) at B > 1, Q4_K / Q6_K: moe_forward_b's
- * tickets under use_sdot (:1136-1201): each expert's members in increasing
- * m, cut into tickets of at most 8; a member of a ticket of two or more
+ * Int8 mode (type | KQ_INT8_ACT) at B > 1: moe_forward_b's tickets under
+ * use_sdot (:1136-1201): each expert's members in increasing m, cut into
+ * tickets of at most 8; for Q4_K / Q6_K a member of a ticket of two or more
  * equals kq_gemv_multix_dev over exactly that ticket's members (the multix
- * pack arithmetic), a member of a ticket of one equals kq_gemv_dev.  This
- * path uses the library's matrix-core scratch (grown on first use); the
- * other int8 types run per token. */
+ * pack arithmetic), a member of a ticket of one equals kq_gemv_dev; for
+ * Q5_K, Q3_K and Q8_0 (per-stream multix) every member equals kq_gemv_dev.
+ * This path uses the library's matrix-core scratch (grown on first use). */
 typedef struct kq_moe_op {
     int type, n_out, k_in;
     int ntensors;
