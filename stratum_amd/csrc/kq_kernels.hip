@@ -1988,9 +1988,11 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
 // 2 Q2_K, 3 type 42, 5 Q5_K, 6 Q3_K, 7 Q8_0): the host launches the
 // instantiation with only the types present, so a single-type launch
 // carries one type's code and the register allocation is not constrained
-// by the others.  Launches that mix types run the TB_ALL kernel (the first
-// four types); the host gives each of the other types launches of its own.
-constexpr int TB_Q4K = 1, TB_Q6K = 2, TB_Q2K = 4, TB_NIB = 8, TB_ALL = 15;
+// by the others.  Launches that mix Q4_K and Q6_K run the TB_Q46 kernel;
+// the host gives every other type launches of its own.  (One kernel for all
+// four core types took 4 KB of scratch per lane and ran a Q4_K+Q6_K list
+// 16 times slower than the two single-type launches.)
+constexpr int TB_Q4K = 1, TB_Q6K = 2, TB_Q2K = 4, TB_NIB = 8, TB_Q46 = TB_Q4K | TB_Q6K;
 constexpr int TB_Q5K = 32, TB_Q3K = 64, TB_Q80 = 128, TB_Q4K_I8 = 256, TB_Q6K_I8 = 512;
 constexpr int TB_Q5K_I8 = 1024, TB_Q3K_I8 = 2048, TB_Q80_I8 = 4096;
 // Q4_K and Q6_K in the int8 mode mixed in one launch (st_mixed_fused_sdot,
@@ -2053,8 +2055,6 @@ __global__ __launch_bounds__(1024) void kq_segs_kernel(SegsArg A) {
             switch (S.type) {
             case T_Q4K: if (TYPES & TB_Q4K) { KQ_RUN(T_Q4K) } break;
             case T_Q6K: if (TYPES & TB_Q6K) { KQ_RUN(T_Q6K) } break;
-            case T_Q2K: if (TYPES & TB_Q2K) { KQ_RUN(T_Q2K) } break;
-            case T_NIB: if (TYPES & TB_NIB) { KQ_RUN(T_NIB) } break;
             case T_Q4K_I8: if (TYB == TB_I8MIX) { KQ_RUN(T_Q4K_I8) } break;
             case T_Q6K_I8: if (TYB == TB_I8MIX) { KQ_RUN(T_Q6K_I8) } break;
             default: break;
@@ -4467,13 +4467,13 @@ long kqk_segs_lds(const kqk_seg* segs, int nseg, int grid, int* xs_off, int* ter
 }
 
 // Every instantiation, indexed by [multi][depth - 1][slot]: slots 0..3 and
-// 5..7 single types (type_slot), 4 the mixed-type kernel, 8..12 the int8
+// 5..7 single types (type_slot), 4 Q4_K and Q6_K mixed, 8..12 the int8
 // mode of Q4_K, Q6_K, Q5_K, Q3_K and Q8_0, 13 int8 Q4_K and Q6_K mixed.
 constexpr int NSLOT = 14;
 #define KQ_SEGS_ROW(D, M)                                                       \
     {&kq_segs_kernel<D, TB_Q4K, M>, &kq_segs_kernel<D, TB_Q6K, M>,              \
      &kq_segs_kernel<D, TB_Q2K, M>, &kq_segs_kernel<D, TB_NIB, M>,              \
-     &kq_segs_kernel<D, TB_ALL, M>, &kq_segs_kernel<D, TB_Q5K, M>,              \
+     &kq_segs_kernel<1, TB_Q46, M>, &kq_segs_kernel<D, TB_Q5K, M>,              \
      &kq_segs_kernel<D, TB_Q3K, M>, &kq_segs_kernel<D, TB_Q80, M>,              \
      &kq_segs_kernel<D, TB_Q4K_I8, M>, &kq_segs_kernel<D, TB_Q6K_I8, M>,        \
      &kq_segs_kernel<D, TB_Q5K_I8, M>, &kq_segs_kernel<D, TB_Q3K_I8, M>,        \
@@ -4573,7 +4573,7 @@ int kqk_launch_segs(const kqk_seg* segs, int nseg, int grid, int threads, int de
                 : set == TB_Q5K ? 5 : set == TB_Q3K ? 6 : set == TB_Q80 ? 7
                 : set == TB_Q4K_I8 ? 8 : set == TB_Q6K_I8 ? 9 : set == TB_Q5K_I8 ? 10
                 : set == TB_Q3K_I8 ? 11 : set == TB_Q80_I8 ? 12 : set == TB_I8MIX ? 13
-                : (set & ~TB_ALL) ? -1 : 4;
+                : set == TB_Q46 ? 4 : -1;
     if (t < 0) return (int)hipErrorInvalidValue;   // other types are never mixed in a launch
     if (t == 4 || t == 13) depth = 1;   // the mixed kernels fit 128 VGPRs at depth 1 only
     int nsel = 0;

@@ -99,9 +99,6 @@ static int block_bytes(int type) {
 /* dense rows (their own kernel) */
 static int is_dense(int type) { return type == KQ_TYPE_F16 || type == KQ_TYPE_F32; }
 
-/* the types the multi-x (MULTISEQ, MoE batch) kernel and the mixed-type
- * segment kernel cover; the other block types run single-type launches and
- * per-stream calls */
 /* Q4_K / Q6_K in the int8 mode: the types whose st_linear_multix under
  * use_sdot has its own (pack) arithmetic at B >= 2, and which share a
  * launch in a group (st_mixed_fused_sdot) */
@@ -114,6 +111,8 @@ static int is_i8(int type) {
     return (type & KQ_INT8_ACT) && has_sdot(type & ~KQ_INT8_ACT);
 }
 
+/* the types the multi-x (MULTISEQ, MoE batch) kernel covers; the other
+ * block types run per-stream calls */
 static int is_core(int type) {
     return type == KQ_TYPE_Q2_K || type == KQ_TYPE_Q4_K || type == KQ_TYPE_Q6_K ||
            type == KQ_TYPE_Q2K_NIB;
@@ -308,10 +307,13 @@ static int plan_depth(void) {
 static int launch_segs_one(const kqk_seg* segs, int nseg, hipStream_t st);
 
 /* Whether one kernel instantiation takes segments of types a and b
- * together: any mix of the core types; Q4_K and Q6_K in the int8 mode (as
- * st_mixed_fused_sdot, stratum_linear.h:1043-1085); else one type. */
+ * together: Q4_K and Q6_K (a Q4_K_M layer's mix), in the exact or the int8
+ * mode (as st_mixed_fused_sdot, stratum_linear.h:1043-1085); else one
+ * type. */
+static int is_q46(int type) { return type == KQ_TYPE_Q4_K || type == KQ_TYPE_Q6_K; }
+
 static int same_launch(int a, int b) {
-    if (is_core(a)) return is_core(b);
+    if (is_q46(a)) return is_q46(b);
     if (is_i8mx(a)) return is_i8mx(b);
     return a == b;
 }

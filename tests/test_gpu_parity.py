@@ -257,6 +257,33 @@ def test_segments_layer_set_matches_single_launches(port):
         check_close(got, port.gemv(t, ws[name], xs[xn], N, Kd, threads=8), f"seg {name}")
 
 
+@pytest.mark.parametrize("order", [(12, 12, 14), (14, 12, 14, 14, 12), (14, 14, 12, 12, 14, 12, 12, 14)])
+def test_segments_mixed_q4k_q6k(port, order):
+    """Q4_K and Q6_K tensors on one x in one segment list (a Q4_K_M layer's
+    Q, K, V with a Q6_K V): one launch of the Q4_K+Q6_K kernel; every output
+    equals its own single launch bit for bit and the oracle within the GEMV
+    bound."""
+    H = 2048
+    x = synth.gaussian(synth.rng(8450), H)
+    rows = [1024, 128, 160, 96, 64, 300, 17, 256]
+    dx = dev(x)
+    ws, dws, dys, segs = [], [], [], []
+    for i, t in enumerate(order):
+        ws.append(synth.tensor(t, rows[i], H, 8460 + i))
+        dws.append(dev(ws[-1]))
+        dys.append(torch.full((rows[i],), float("nan"), dtype=torch.float32, device="cuda"))
+        segs.append(K.segment(t, H, rows[i], [dws[-1].data_ptr()], dx.data_ptr(),
+                              dys[-1].data_ptr()))
+    print(f"mixed q4k/q6k order={order}", flush=True)
+    K.gemv_segments_dev(segs, stream=stream())
+    torch.cuda.synchronize()
+    for i, t in enumerate(order):
+        got = dys[i].cpu().numpy()
+        assert same_values(got, gpu_gemv(t, ws[i], x, rows[i], H)), (i, t)
+        if i < 3:
+            check_close(got, port.gemv(t, ws[i], x, rows[i], H, threads=8), f"seg {i}")
+
+
 def test_segments_groups_expert_slices(port):
     """MoE-style segments: groups with separate weight bases; gate/up share
     x, down uses one x per group (x_stride)."""
