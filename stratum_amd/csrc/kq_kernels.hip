@@ -2415,11 +2415,18 @@ struct MoeRuns {
     }
 };
 
+// Workgroup size: 1024 lanes (128 VGPRs); Q5_K, Q3_K and Q8_0, whose
+// weight registers and terms do not fit 128 VGPRs with the next unit in
+// flight (40-400 bytes of spill per lane), take 512 (256 VGPRs, no spill).
+template <int TYPE> constexpr int mx_threads() {
+    return TYPE == T_Q5K || TYPE == T_Q3K || TYPE == T_Q80 ? 512 : 1024;
+}
+
 template <int TYPE, int S, bool WHOLE>
-__global__ __launch_bounds__(1024) void kq_mx_kernel(MxArg A) {
+__global__ __launch_bounds__(mx_threads<TYPE>()) void kq_mx_kernel(MxArg A) {
     using TI = TypeInfo<TYPE>;
     constexpr int G4 = XGroup<TYPE>::G4;
-    constexpr bool SCTYPE = TYPE != T_Q6K;
+    constexpr bool SCTYPE = TI::SCALED;           // the single-stream kernel's staging rule
     constexpr bool SUMS = XGroup<TYPE>::SUMS;
     extern __shared__ __align__(16) uint8_t smem[];
     // the wave index in a scalar register: task choice and the task loop's
@@ -4623,14 +4630,17 @@ long kqk_mx_plan(int type, int N, int K, int mmax, int ngmax, int grid, int lds_
     if (xpc < 0 || mmax < 1 || mmax > MX_MAXM || ngmax < 1 || N < 1 || K <= 0 || (K & 255) ||
         grid < 1)
         return -1;
-    const int T = 1024, W = T / 64;
+    const int T = type == T_Q5K || type == T_Q3K || type == T_Q80 ? 512 : 1024;   // mx_threads
+    const int W = T / 64;
     const int NC = K >> 6, GP = kq_phases(NC), RPT = 64 / GP;
     const int NCg = (NC + GP - 1) / GP * GP, nstep = NCg / GP;
-    const int G4 = type == T_Q4K ? 8 : 4;
+    const int G4 = type == T_Q4K || type == T_Q5K || type == T_Q80 ? 8 : 4;
     const long per = K / (4 * G4);
     const long head = 8L * MX_MAXM + 64;
-    const long rbytes = (long)(K >> 8) * (type == T_Q4K ? 144 : type == T_Q6K ? 210 : type == T_Q2K ? 84 : 148);
-    const double c0 = type == T_Q4K ? 45 : type == T_Q6K ? 170 : type == T_Q2K ? 30 : 35;
+    const long rbytes = (long)(K >> 8) * block_bytes_of(type);
+    // (Q5_K, Q3_K, Q8_0: estimated from their decode next to Q4_K's)
+    const double c0 = type == T_Q4K ? 45 : type == T_Q6K ? 170 : type == T_Q2K ? 30
+                    : type == T_Q5K ? 55 : type == T_Q3K ? 70 : type == T_Q80 ? 25 : 35;
     const double c1 = type == T_Q6K ? 140 : 150;
     // per-pass and per-tile overheads, fitted to timings of the 27B gate
     // and down shapes (a pass stages x and ramps the weight stream up)
@@ -4700,10 +4710,11 @@ int kqk_mx_set_max_lds(int bytes) {
     {&kq_mx_kernel<T_, 1, true>, &kq_mx_kernel<T_, 2, true>, &kq_mx_kernel<T_, 1, false>, \
      &kq_mx_kernel<T_, 2, false>}
     typedef void (*mx_fn)(MxArg);
-    const mx_fn fns[4][4] = {KQ_MX_ATTR(T_Q4K), KQ_MX_ATTR(T_Q6K), KQ_MX_ATTR(T_Q2K),
-                             KQ_MX_ATTR(T_NIB)};
+    const mx_fn fns[7][4] = {KQ_MX_ATTR(T_Q4K), KQ_MX_ATTR(T_Q6K), KQ_MX_ATTR(T_Q2K),
+                             KQ_MX_ATTR(T_NIB), KQ_MX_ATTR(T_Q5K), KQ_MX_ATTR(T_Q3K),
+                             KQ_MX_ATTR(T_Q80)};
 #undef KQ_MX_ATTR
-    for (int t = 0; t < 4; t++)
+    for (int t = 0; t < 7; t++)
         for (int i = 0; i < 4; i++) {
             const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fns[t][i]),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
@@ -4755,6 +4766,9 @@ int kqk_launch_mx(int type, const int* plan, long lds, int grid, const void* w, 
     case T_Q6K: return launch_mx_t<T_Q6K>(a, plan[1], whole, lds, st);
     case T_Q2K: return launch_mx_t<T_Q2K>(a, plan[1], whole, lds, st);
     case T_NIB: return launch_mx_t<T_NIB>(a, plan[1], whole, lds, st);
+    case T_Q5K: return launch_mx_t<T_Q5K>(a, plan[1], whole, lds, st);
+    case T_Q3K: return launch_mx_t<T_Q3K>(a, plan[1], whole, lds, st);
+    case T_Q80: return launch_mx_t<T_Q80>(a, plan[1], whole, lds, st);
     default: return (int)hipErrorInvalidValue;
     }
 }
@@ -4827,6 +4841,9 @@ int kqk_launch_mx_moe(int type, const int* plan, long plan_lds, long lds, int gr
     case T_Q6K: return launch_mx_t<T_Q6K>(a, plan[1], whole, lds, st);
     case T_Q2K: return launch_mx_t<T_Q2K>(a, plan[1], whole, lds, st);
     case T_NIB: return launch_mx_t<T_NIB>(a, plan[1], whole, lds, st);
+    case T_Q5K: return launch_mx_t<T_Q5K>(a, plan[1], whole, lds, st);
+    case T_Q3K: return launch_mx_t<T_Q3K>(a, plan[1], whole, lds, st);
+    case T_Q80: return launch_mx_t<T_Q80>(a, plan[1], whole, lds, st);
     default: return (int)hipErrorInvalidValue;
     }
 }

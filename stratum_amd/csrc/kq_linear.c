@@ -111,11 +111,16 @@ static int is_i8(int type) {
     return (type & KQ_INT8_ACT) && has_sdot(type & ~KQ_INT8_ACT);
 }
 
-/* the types the multi-x (MULTISEQ, MoE batch) kernel covers; the other
- * block types run per-stream calls */
+/* the four types of the fused batch-1 MoE FFN step */
 static int is_core(int type) {
     return type == KQ_TYPE_Q2_K || type == KQ_TYPE_Q4_K || type == KQ_TYPE_Q6_K ||
            type == KQ_TYPE_Q2K_NIB;
+}
+
+/* the types the exact multi-x (MULTISEQ, MoE batch) kernel covers: every
+ * block type; the int8 mode and the dense types have their own paths */
+static int is_mx(int type) {
+    return is_core(type) || type == KQ_TYPE_Q5_K || type == KQ_TYPE_Q3_K || type == KQ_TYPE_Q8_0;
 }
 
 int64_t kq_row_bytes(int type, int K) {
@@ -577,7 +582,7 @@ int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,
     if (is_dense(type) && B > 1) return dense_gemv(type, w, xs, NULL, ys, N, K, B, pick(stream));
     if (B > 1 && (type == (KQ_INT8_ACT | KQ_TYPE_Q4_K) || type == (KQ_INT8_ACT | KQ_TYPE_Q6_K)))
         return mi8_multix(type, w, xs, ys, B, N, K, pick(stream));
-    if (B == 1 || !is_core(type)) {   /* per-stream launches: the same bits as single calls */
+    if (B == 1 || !is_mx(type)) {     /* per-stream launches: the same bits as single calls */
         for (int s = 0; s < B; s++)
             if (kq_gemv_dev(type, w, xs + (size_t)s * K, NULL, ys + (size_t)s * N, N, K, stream))
                 return -1;
@@ -1220,7 +1225,7 @@ static int moe_gemv_routed(const kq_moe_op* op, const float* probs, int B, int k
         return kq_fail("kq_moe_gemv_routed_dev: B=%d k=%d E=%d (E <= 1024)", B, k, E);
     if (moe_check_op(op, k, E, "kq_moe_gemv_routed_dev")) return -1;
     if (B == 1) return moe_one_token(op, sel, k, E, probs, selw, st);
-    if (!is_core(op->type)) {
+    if (!is_mx(op->type)) {
         const int e = kqk_launch_moe_topk(probs, B, E, k, sel, selw, st);
         if (e) return kq_fail("moe topk launch: %s", hipGetErrorString((hipError_t)e));
         return is_i8(op->type) ? moe_i8_batch(op, sel, B, k, E, io, st)
@@ -1249,7 +1254,7 @@ static int moe_gemv(const kq_moe_op* op, const int* sel, int B, int k, int E, mo
     if (moe_check_op(op, k, E, "kq_moe_gemv_dev")) return -1;
     if (B == 1) return moe_one_token(op, sel, k, E, NULL, NULL, st);
     if (is_i8(op->type)) return moe_i8_batch(op, sel, B, k, E, io, st);
-    if (!is_core(op->type)) return moe_per_token(op, sel, B, k, E, st);
+    if (!is_mx(op->type)) return moe_per_token(op, sel, B, k, E, st);
     return moe_batch(op, (int*)sel, NULL, NULL, B, k, E, io, st);
 }
 
@@ -1459,7 +1464,7 @@ int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* s
     gu.w[0] = f->gate; gu.y[0] = g;
     gu.w[1] = pair ? f->up : NULL; gu.y[1] = pair ? u : NULL;
     gu.expert_stride = f->gate_stride;
-    const int share = B > 1 && is_core(f->gate_type) && is_core(f->down_type) && E <= 1024 &&
+    const int share = B > 1 && is_mx(f->gate_type) && is_mx(f->down_type) && E <= 1024 &&
                       !g_kq.env_ffn_split;
     if (share) {
         /* a batch: the grouped gate+up launch stores its run tables for the

@@ -259,7 +259,7 @@ def test_moe_routed_batch(port, qtype, B, E, k, case):
 
 
 @pytest.mark.parametrize("grouping", ["in_launch", "group_launch"])
-@pytest.mark.parametrize("qtype", [12, 14, 10])
+@pytest.mark.parametrize("qtype", [12, 14, 10, 13, 11, 8])
 @pytest.mark.parametrize("B,n_exp", [(16, 32), (16, 128), (3, 8), (64, 16)])
 def test_moe_batch_grouped(port, qtype, B, n_exp, grouping, kq_env):
     """Batches whose tokens share experts: each selected slice is streamed

@@ -302,18 +302,20 @@ def test_moe_ffn_fused_matches_split(port, case, kq_env):
     assert np.abs(fused["x"] - full["x"]).max() <= 1e-4 * contrib
 
 
-@pytest.mark.parametrize("case", ["config_b16", "routed_b4"])
+@pytest.mark.parametrize("case", ["config_b16", "routed_b4", "q5k_b16", "q3k_routed_b4"])
 def test_moe_ffn_batch_shared_runs_match_split(port, case, kq_env):
     """B > 1: the grouped gate+up launch stores its expert-run tables and
     the down launch loads them instead of grouping the selection again.
     config_b16 routes in a top-k launch first; routed_b4 (B E^2 <= 2^16)
-    inside the gate+up launch.  Every output (gate, up, activations, down
-    outputs, x, sel, selw) is bit-identical to the split form's
-    (KQ_MOE_FFN_SPLIT, where each launch groups for itself), and x agrees
-    with the oracle."""
-    B, H, F, E, k = {"config_b16": (16, 2048, 768, 128, 8),
-                     "routed_b4": (4, 1024, 512, 64, 4)}[case]
-    d = make_layer(H, F, E, k, 9800)
+    inside the gate+up launch; the q5k / q3k cases are the same with Q5_K
+    and Q3_K experts.  Every output (gate, up, activations, down outputs,
+    x, sel, selw) is bit-identical to the split form's (KQ_MOE_FFN_SPLIT,
+    where each launch groups for itself), and x agrees with the oracle."""
+    B, H, F, E, k, qt = {"config_b16": (16, 2048, 768, 128, 8, TYPE_Q4_K),
+                         "routed_b4": (4, 1024, 512, 64, 4, TYPE_Q4_K),
+                         "q5k_b16": (16, 2048, 768, 128, 8, 13),
+                         "q3k_routed_b4": (4, 1024, 512, 64, 4, 11)}[case]
+    d = make_layer(H, F, E, k, 9800, qtype=qt)
     r = synth.rng(9801)
     xn = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)
     x0 = np.stack([synth.gaussian(r, H) for _ in range(B)]).reshape(-1)

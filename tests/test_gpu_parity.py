@@ -477,12 +477,13 @@ def gpu_multix(qtype, w, xs, N, Kd):
     return dy.cpu().numpy().reshape(B, N)
 
 
-@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("qtype", TYPES + [13, 11, 8])
 @pytest.mark.parametrize("B,N,Kd", [(2, 300, 1024), (3, 129, 768), (8, 96, 3072),
                                     (16, 64, 1024), (19, 40, 2048)])
 def test_multix_bit_identical_to_single_stream(port, qtype, B, N, Kd):
-    """One weight pass for B streams: every stream equals its own
-    single-stream launch bit for bit, and the oracle within the bound."""
+    """One weight pass for B streams (every block type, Q5_K / Q3_K / Q8_0
+    included): every stream equals its own single-stream launch bit for
+    bit, and the oracle within the bound."""
     w = synth.tensor(qtype, N, Kd, 800 + qtype + B)
     xs = np.stack([synth.gaussian(synth.rng(810 + s), Kd) for s in range(B)])
     got = gpu_multix(qtype, w, xs, N, Kd)
@@ -492,7 +493,7 @@ def test_multix_bit_identical_to_single_stream(port, qtype, B, N, Kd):
         check_close(got[s], port.gemv(qtype, w, xs[s], N, Kd), f"multix {K.TYPE_NAMES[qtype]} B={B} s={s}")
 
 
-@pytest.mark.parametrize("qtype", [12, 10, 14])
+@pytest.mark.parametrize("qtype", [12, 10, 14, 13, 11, 8])
 def test_multix_window_fallback(port, qtype):
     """One stream with a value outside the scaled window sends the launch to
     the exact path; every stream still equals its single-stream result."""
@@ -506,7 +507,7 @@ def test_multix_window_fallback(port, qtype):
         check_close(got[s], port.gemv(qtype, w, xs[s], N, Kd), f"multix window s={s}")
 
 
-@pytest.mark.parametrize("qtype", [12, 10, 14, 42])
+@pytest.mark.parametrize("qtype", [12, 10, 14, 42, 13, 11, 8])
 def test_multix_tiled_window_fallback(port, qtype):
     """x too long to stage whole (tiles of a few chunks), with one stream
     outside the scaled window: the tiled exact path, still bit-identical."""
@@ -520,11 +521,12 @@ def test_multix_tiled_window_fallback(port, qtype):
     check_close(got[5], port.gemv(qtype, w, xs[5], N, Kd), "tiled window s=5")
 
 
-@pytest.mark.parametrize("B", [17, 40, 64, 70])
-def test_multix_member_chunks(port, B):
+@pytest.mark.parametrize("qtype,B", [(12, 17), (12, 40), (12, 64), (12, 70), (13, 40), (11, 64),
+                                     (8, 70)])
+def test_multix_member_chunks(port, qtype, B):
     """More than 16 streams: members staged 16 at a time within one weight
     pass (and more than 64 in two launches)."""
-    qtype, N, Kd = 12, 100, 1024
+    N, Kd = 100, 1024
     w = synth.tensor(qtype, N, Kd, 890 + B)
     xs = np.stack([synth.gaussian(synth.rng(900 + s), Kd) for s in range(B)])
     got = gpu_multix(qtype, w, xs, N, Kd)
@@ -533,15 +535,19 @@ def test_multix_member_chunks(port, B):
 
 
 @pytest.mark.parametrize("tensor,B", [("gate", 8), ("down", 8), ("gate", 16), ("up", 16),
-                                      ("down", 16), ("gate", 64), ("up", 64), ("down", 64)])
+                                      ("down", 16), ("gate", 64), ("up", 64), ("down", 64),
+                                      ("gate_q5k", 16), ("down_q3k", 16), ("down_q80", 64)])
 def test_multix_27b_sampled(port, tensor, B):
     """27B gate / up (Q4_K 17408 x 5120) and down (Q6_K 5120 x 17408) with
     B = 8, 16 and 64 streams, the MULTISEQ shapes bench.py times (the
-    planner picks other member chunks and x tiles at each B): every stream
-    against its single-stream launch bit for bit, and 256 sampled rows of
-    two streams against the oracle."""
+    planner picks other member chunks and x tiles at each B), and the same
+    shapes as Q5_K, Q3_K and Q8_0: every stream against its single-stream
+    launch bit for bit, and 256 sampled rows of two streams against the
+    oracle."""
     qtype, N, Kd, seed = {"gate": (12, 17408, 5120, 850), "up": (12, 17408, 5120, 851),
-                          "down": (14, 5120, 17408, 852)}[tensor]
+                          "down": (14, 5120, 17408, 852), "gate_q5k": (13, 17408, 5120, 853),
+                          "down_q3k": (11, 5120, 17408, 854),
+                          "down_q80": (8, 5120, 17408, 855)}[tensor]
     w = synth.tensor(qtype, N, Kd, seed)
     xs = np.stack([synth.gaussian(synth.rng(860 + s), Kd) for s in range(B)])
     print(f"multix 27B {tensor} B={B}", flush=True)

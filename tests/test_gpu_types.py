@@ -216,8 +216,8 @@ def test_multix_equals_single_stream(qtype, N, Kd, B):
 @pytest.mark.parametrize("B", [1, 3])
 def test_moe_gather_other_types(port, qtype, B):
     """MoE experts in Q5_K / Q8_0: one token through the device-selected
-    single-stream kernel, several tokens one launch per token; every member
-    equals its slice's single GEMV."""
+    single-stream kernel, several tokens through the multi-x kernel; every
+    member equals its slice's single GEMV."""
     n_exp, H, F, k = 16, 512, 256, 4
     gate = synth.tensor(qtype, n_exp * F, H, 720)
     r = np.random.default_rng(721 + B)
