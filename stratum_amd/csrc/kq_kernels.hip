@@ -1826,19 +1826,30 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
 
 
     // first DEPTH batches: static (wave w takes chunks 64w .., then
-    // 64(W + w) ..); their latency overlaps the staging
+    // 64(W + w) ..).  A segment that stages x issues them once its x has
+    // arrived (the wait below, after the first x stores are computed): all
+    // 256 workgroups' first batches together are about 13 MB, and issued
+    // ahead of the x arrival they queue in front of it in the memory system
+    // (x staged about 2 us after issue).  Measured on the 27B layer set in
+    // one process, against issuing them before the staging: 58.22 -> 57.07
+    // us ([down] 18.56 -> 18.09, [Q,K,V] 8.59 -> 8.45 us).
     int base[DEPTH], cx[DEPTH];
     typename C::Raw buf[DEPTH];
+    auto first_batches = [&]() {
+        if (restage) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
-    for (int k = 0; k < DEPTH; k++) {
-        base[k] = (k * (T >> 6) + wave) * 64;
-        buf[k] = C::load(W.locate(base[k], cx[k]), u);
-    }
+        for (int k = 0; k < DEPTH; k++) {
+            base[k] = (k * (T >> 6) + wave) * 64;
+            buf[k] = C::load(W.locate(base[k], cx[k]), u);
+        }
+    };
+    if (!restage) first_batches();
 
     if (XGroup<TYPE>::I8 && restage) {
         uint8_t* xq = reinterpret_cast<uint8_t*>(xl);
         const int per = xg.per;
         if (tid < xg.total) store_i8<TYPE>(tid, per, NC, xv, xq, xs);
+        first_batches();
         int gi0 = tid + T;
         if (PRE2 && two) {
             if (gi0 < xg.total) store_i8<TYPE>(gi0, per, NC, xv2, xq, xs);
@@ -1855,6 +1866,7 @@ __device__ void run_segment(const Seg& S, const SegsArg& A, int seg, Staged& st,
         st.bad = false;
     } else if (restage) {
         bool bad = xg.store(tid, xv, SCTYPE, true, xl, xs);
+        first_batches();
         int gi0 = tid + T;
         if (PRE2 && two) {
             bad |= xg.store(gi0, xv2, SCTYPE, true, xl, xs);

@@ -322,8 +322,11 @@ def test_moe_ffn_batch_shared_runs_match_split(port, case, kq_env):
     print(f"moe ffn batch shared run tables vs split: {case}", flush=True)
     fused = run_step(d, xn, x0, B)
     # the tables were stored (run count written over the NaN fill) and the
-    # down launch loaded them
-    assert fused["path"] & K.FFN_RUNS_STORED and fused["path"] & K.FFN_RUNS_LOADED, fused["path"]
+    # down launch loaded them (Q4_K: its down plan cuts runs as gate+up's;
+    # the q5k / q3k down plans may cut them otherwise and then regroup)
+    assert fused["path"] & K.FFN_RUNS_STORED, fused["path"]
+    if qt == TYPE_Q4_K:
+        assert fused["path"] & K.FFN_RUNS_LOADED, fused["path"]
     assert fused["runs0"] != NAN_BITS and 0 < fused["runs0"] <= B * k, fused["runs0"]
     kq_env(KQ_MOE_FFN_SPLIT=1)
     split = run_step(d, xn, x0, B)
