@@ -2190,8 +2190,10 @@ __device__ __forceinline__ void mx_sweep(const MxArg& A, const MxTasks& tk, wptr
     const int tid = threadIdx.x, T = A.threads, GP = tk.GP;
     const int p = tid & (GP - 1), u = p & 3, lrow = (tid & 63) >> tk.lgp;
     const int K = A.K, NC = K >> 6, nstep = (NC + GP - 1) >> tk.lgp, nsub = TC >> tk.lgp;
-    const int xmem = TC * XPAD;                   // float4 per member in a buffer
-    const int per2 = K / (4 * XGroup<TYPE>::G4);  // sums per member
+    constexpr int XS = XGroup<TYPE>::XSTRIDE;     // float4 slots per chunk
+    const int xmem = TC * XS;                     // float4 per member in a buffer
+    // floats of sums per member: one per group, or (int8) the chunks' {scale, sum} pairs
+    const int per2 = XGroup<TYPE>::I8 ? TC * TI::XS_PER_CHUNK : K / (4 * XGroup<TYPE>::G4);
     const int tq = MC * TC * 16;                  // float4 per tile
     const float f = SC ? ldexpf(1.0f, 149 - KSC) : 1.0f;
     const double f6 = 0.25;                       // Q6_K x is never scaled here
@@ -2263,7 +2265,7 @@ __device__ __forceinline__ void mx_sweep(const MxArg& A, const MxTasks& tk, wptr
                         for (int s = 0; s < S; s++) {
                             const int m = tk.sg[k] * S + s;
                             ok[s] = m < MC;
-                            xc[s] = xcur + min(m, MC - 1) * xmem + cl * XPAD;
+                            xc[s] = xcur + min(m, MC - 1) * xmem + cl * XS;
                         }
                         mx_term_q6k<S>(cur, u, xc, ok, f6, part[k]);
                     } else {
@@ -2271,7 +2273,7 @@ __device__ __forceinline__ void mx_sweep(const MxArg& A, const MxTasks& tk, wptr
                         for (int s = 0; s < S; s++) {
                             const int m = tk.sg[k] * S + s;
                             if (m < MC) {
-                                const float4* xc = xcur + m * xmem + cl * XPAD;
+                                const float4* xc = xcur + m * xmem + cl * XS;
                                 const float* xs = sums + m * per2;
                                 part[k][s] = part[k][s] +
                                              C::template term<SC, true>(cur, u, xc, xs, c, f, f6);
@@ -2427,11 +2429,15 @@ struct MoeRuns {
     }
 };
 
-// Workgroup size: 1024 lanes (128 VGPRs); Q5_K, Q3_K and Q8_0, whose
-// weight registers and terms do not fit 128 VGPRs with the next unit in
-// flight (40-400 bytes of spill per lane), take 512 (256 VGPRs, no spill).
+// Workgroup size: 1024 lanes (128 VGPRs); Q5_K, Q3_K and Q8_0 (exact and
+// int8), whose weight registers and terms do not fit 128 VGPRs with the
+// next unit in flight (40-400 bytes of spill per lane), take 512 (256
+// VGPRs, no spill).
 template <int TYPE> constexpr int mx_threads() {
-    return TYPE == T_Q5K || TYPE == T_Q3K || TYPE == T_Q80 ? 512 : 1024;
+    return TYPE == T_Q5K || TYPE == T_Q3K || TYPE == T_Q80 || TYPE == T_Q5K_I8 ||
+                   TYPE == T_Q3K_I8 || TYPE == T_Q80_I8
+               ? 512
+               : 1024;
 }
 
 template <int TYPE, int S, bool WHOLE>
@@ -2440,6 +2446,11 @@ __global__ __launch_bounds__(mx_threads<TYPE>()) void kq_mx_kernel(MxArg A) {
     constexpr int G4 = XGroup<TYPE>::G4;
     constexpr bool SCTYPE = TI::SCALED;           // the single-stream kernel's staging rule
     constexpr bool SUMS = XGroup<TYPE>::SUMS;
+    // the int8 mode of the types whose batches are per stream (Q5_K, Q3_K,
+    // Q8_0): x quantized per member as the single-stream kernel does
+    // (store_i8), staged whole (the host plans no tiles for them)
+    constexpr bool I8 = XGroup<TYPE>::I8;
+    static_assert(!I8 || WHOLE, "int8 members are staged whole");
     extern __shared__ __align__(16) uint8_t smem[];
     // the wave index in a scalar register: task choice and the task loop's
     // branches are then scalar (no exec masking around the weight loads)
@@ -2450,7 +2461,7 @@ __global__ __launch_bounds__(mx_threads<TYPE>()) void kq_mx_kernel(MxArg A) {
     const int GP = kq_phases(NC), lgp = GP == 32 ? 5 : 3, RPT = 64 / GP;
     const int TC = WHOLE ? (NC + GP - 1) & -GP : A.TC;
     const int ntile = WHOLE ? 1 : (NC + TC - 1) / TC;
-    const int xmem = TC * XPAD;
+    const int xmem = TC * XGroup<TYPE>::XSTRIDE;
 
     // LDS: member tables, flags, sums [mch][per], x buffer(s)
     int* d_xi = reinterpret_cast<int*>(smem);
@@ -2541,7 +2552,21 @@ __global__ __launch_bounds__(mx_threads<TYPE>()) void kq_mx_kernel(MxArg A) {
 
             // prologue: sums, window vote, and x itself when staged whole
             uint32_t dist = 0;
-            if (SUMS || WHOLE) {
+            if constexpr (I8) {
+                // member j's chunks at xb0 + j * xmem and its {scale, sum}
+                // floats at sums + j * TC * XS_PER_CHUNK (store_i8 with TC
+                // as the chunk stride)
+                for (int q = tid; q < MC * per; q += T) {
+                    const int j = q / per, gi = q - j * per;
+                    const f32x4* src = reinterpret_cast<const f32x4*>(
+                                           A.X + (size_t)d_xi[mc0 + j] * A.x_stride) +
+                                       (size_t)gi * G4;
+                    f32x4 v[G4];
+#pragma unroll
+                    for (int k = 0; k < G4; k++) v[k] = src[k];
+                    store_i8<TYPE>(q, per, TC, v, reinterpret_cast<uint8_t*>(xb0), sums);
+                }
+            } else if (SUMS || WHOLE) {
                 for (int q = tid; q < MC * per; q += T) {
                     const int j = q / per, gi = q - j * per;
                     const f32x4* src = reinterpret_cast<const f32x4*>(
@@ -2637,8 +2662,10 @@ int launch_mx_t(const MxArg& a, int s, bool whole, long lds, hipStream_t st) {
     hipLaunchKernelGGL((kq_mx_kernel<TYPE, S_, W_>), dim3(a.grid), dim3(a.threads), (size_t)lds, st, a)
     if (whole) {
         if (s == 1) KQ_MX_GO(1, true); else KQ_MX_GO(2, true);
-    } else {
+    } else if constexpr (!XGroup<TYPE>::I8) {
         if (s == 1) KQ_MX_GO(1, false); else KQ_MX_GO(2, false);
+    } else {
+        return (int)hipErrorInvalidValue;     // int8 members are staged whole
     }
 #undef KQ_MX_GO
     return (int)hipGetLastError();
@@ -3528,33 +3555,37 @@ __global__ __launch_bounds__(1024) void kq_mi8_moe_prep_kernel(MoeGroupArg ga, c
 }
 
 // A run of one member in a grouped launch (st_linear_multix at B = 1 is
-// st_linear_dispatch; for Q5_K, Q3_K and Q8_0 every member is one): the
-// single-stream int8 kernel's arithmetic, so the member equals
-// kq_gemv_dev(type | KQ_INT8_ACT) bit for bit.  The T lanes take the
-// 64-weight chunks of rows r0 .. r0 + 16 nrw - 1 in row-major order
-// (neighbouring lanes read neighbouring chunks of a row); each chunk term is
-// kq_segs_kernel's (Chunk<TYPE>::term), with the chunk's x and {scale, sum}
-// pairs read from the quantized row xi in the order that kernel stages them
-// (store_i8), kept in LDS ([row][K/64] doubles); then that kernel's row
-// reduction: GP = kq_phases(K/64) lanes per row, lane p sums chunks p,
-// p+GP, ... in order from 0, then phase_tree.  Output y[r] (y: the member's
-// row).
+// st_linear_dispatch): the single-stream int8 kernel's arithmetic, so the
+// member equals kq_gemv_dev(type | KQ_INT8_ACT) bit for bit.  The T lanes
+// take the 64-weight chunks of rows r0 .. r0 + 16 nrw - 1 in row-major
+// order (neighbouring lanes read neighbouring chunks of a row), each chunk
+// term exactly as kq_segs_kernel forms it (term_q4k_i8 / term_q6k_i8, x
+// and {scale, sum} read from the quantized row xi), kept in LDS
+// ([row][K/64] doubles), then that kernel's row reduction: GP =
+// kq_phases(K/64) lanes per row, lane p sums chunks p, p+GP, ... in order
+// from 0, then phase_tree.  Output y[r] (y: the member's row).
 template <int TYPE>
 __device__ __forceinline__ void mi8_single(const Mi8Arg& A, const uint8_t* w, int xi, float* y,
                                            int rb0, int nrw, double* terms, int tid, int T) {
     using C = Chunk<TYPE>;
-    constexpr int BB = TypeInfo<TYPE>::BB;
-    constexpr bool Q6 = TYPE == T_Q6K_I8, Q3 = TYPE == T_Q3K_I8;
+    constexpr bool Q4 = TYPE == T_Q4K_I8;
+    constexpr int BB = Q4 ? 144 : 210;
     const int N = A.N, K = A.K, NCH = K >> 6, nb = K >> 8;
     const int r0 = rb0 * 16, nr = min(16 * nrw, N - r0), nchk = nr * NCH;
     const uint8_t* xr = reinterpret_cast<const uint8_t*>(A.xq) + (size_t)xi * K;
-    const float2* sr = A.sm + (size_t)xi * (Q6 ? K >> 4 : K >> 5);
-    struct In { typename C::Raw r; uint4 x[4]; float4 s[2]; };
+    const float2* sr = A.sm + (size_t)xi * (Q4 ? K >> 5 : K >> 4);
+    struct In { typename C::Raw r; uint4 x[4]; float s[8]; };
     auto ld = [&](int f, In& in) {
         const int fc = min(f, nchk - 1), rr = fc / NCH, c = fc - rr * NCH;
         const wptr blk = to_global(w) + (size_t)(r0 + rr) * nb * BB + (size_t)(c >> 2) * BB;
         in.r = C::load(blk, c & 3);
-        if constexpr (Q6) {
+        if constexpr (Q4) {
+            // chunk c: x[64c .. 64c+63], groups 2c, 2c+1
+#pragma unroll
+            for (int k = 0; k < 4; k++) in.x[k] = *reinterpret_cast<const uint4*>(xr + 64 * c + 16 * k);
+            const float4 s4 = *reinterpret_cast<const float4*>(sr + 2 * c);
+            in.s[0] = s4.x; in.s[1] = s4.y; in.s[2] = s4.z; in.s[3] = s4.w;
+        } else {
             // chunk c = (block bi, half h, is): run t at 256 bi + 128 h + 32 t + 16 is
             const int bi = c >> 2, h = (c >> 1) & 1, is = c & 1;
 #pragma unroll
@@ -3562,29 +3593,18 @@ __device__ __forceinline__ void mi8_single(const Mi8Arg& A, const uint8_t* w, in
                 const int pos = 256 * bi + 128 * h + 32 * t + 16 * is;
                 in.x[t] = *reinterpret_cast<const uint4*>(xr + pos);
                 const float2 v = sr[pos >> 4];
-                reinterpret_cast<float2*>(in.s)[t] = v;
+                in.s[2 * t] = v.x; in.s[2 * t + 1] = v.y;
             }
-        } else if constexpr (Q3) {
-            // chunk c = (block bi, s, h): part j holds the h-th 16 values of
-            // 32-group 8 bi + 4 s + j
-            const int bi = c >> 2, sg = (c >> 1) & 1, h = c & 1;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int gi = 8 * bi + 4 * sg + j;
-                in.x[j] = *reinterpret_cast<const uint4*>(xr + 32 * gi + 16 * h);
-                reinterpret_cast<float2*>(in.s)[j] = sr[gi];
-            }
-        } else {
-            // Q4_K, Q5_K, Q8_0: chunk c = x[64c .. 64c+63], groups 2c, 2c+1
-#pragma unroll
-            for (int k = 0; k < 4; k++) in.x[k] = *reinterpret_cast<const uint4*>(xr + 64 * c + 16 * k);
-            in.s[0] = *reinterpret_cast<const float4*>(sr + 2 * c);
         }
     };
     auto term = [&](int f, const In& in) {
         const int fc = min(f, nchk - 1), rr = fc / NCH, c = fc - rr * NCH;
-        const double t = C::template term<false>(in.r, c & 3, reinterpret_cast<const float4*>(in.x),
-                                                 reinterpret_cast<const float*>(in.s), 0, 1.0f, 0.0);
+        double t;
+        if constexpr (Q4)
+            t = term_q4k_i8(in.r, c & 3, reinterpret_cast<const uint32_t*>(in.x),
+                            make_float4(in.s[0], in.s[1], in.s[2], in.s[3]));
+        else
+            t = term_q6k_i8(in.r, c & 3, reinterpret_cast<const uint32_t*>(in.x), in.s);
         if (f < nchk) terms[rr * NCH + c] = t;
     };
     // two batches in flight: the next one's loads go out before this one's term
@@ -3607,21 +3627,6 @@ __device__ __forceinline__ void mi8_single(const Mi8Arg& A, const uint8_t* w, in
         v = phase_tree(v, GP);
         if (p == 0 && rho < nr) y[r0 + rho] = (float)v;
     }
-}
-
-// The int8 MoE batch of the types whose st_linear_multix is per stream
-// (Q5_K, Q3_K, Q8_0: every member alone, grouped with run length 1): one
-// workgroup of 256 lanes per (rbw 16-row blocks, member), mi8_single.
-template <int TYPE>
-__global__ __launch_bounds__(256) void kq_mi8s_kernel(Mi8Arg A) {
-    extern __shared__ __align__(16) double mi8s_terms[];
-    const MxGroup* gp = A.groups + blockIdx.y;    // read with the count (in bounds)
-    const int ngv = *A.ng;
-    const uint8_t* w = gp->w;
-    if ((int)blockIdx.y >= ngv) return;           // uniform over the workgroup
-    const int rb0 = blockIdx.x * A.rbw, nrw = min(A.rbw, (A.N + 15) / 16 - rb0);
-    mi8_single<TYPE>(A, w, gp->xi[0], gp->y + (size_t)gp->yi[0] * A.y_stride, rb0, nrw,
-                     mi8s_terms, threadIdx.x, 256);
 }
 
 // Weight registers of one super-block of one lane's row.
@@ -4642,18 +4647,19 @@ long kqk_mx_plan(int type, int N, int K, int mmax, int ngmax, int grid, int lds_
     if (xpc < 0 || mmax < 1 || mmax > MX_MAXM || ngmax < 1 || N < 1 || K <= 0 || (K & 255) ||
         grid < 1)
         return -1;
-    const int T = type == T_Q5K || type == T_Q3K || type == T_Q80 ? 512 : 1024;   // mx_threads
+    const bool i8 = type == T_Q5K_I8 || type == T_Q3K_I8 || type == T_Q80_I8;
+    const int T = type == T_Q5K || type == T_Q3K || type == T_Q80 || i8 ? 512 : 1024;   // mx_threads
     const int W = T / 64;
     const int NC = K >> 6, GP = kq_phases(NC), RPT = 64 / GP;
     const int NCg = (NC + GP - 1) / GP * GP, nstep = NCg / GP;
-    const int G4 = type == T_Q4K || type == T_Q5K || type == T_Q80 ? 8 : 4;
+    const int G4 = type == T_Q4K || type == T_Q5K || type == T_Q80 || i8 ? 8 : 4;
     const long per = K / (4 * G4);
     const long head = 8L * MX_MAXM + 64;
     const long rbytes = (long)(K >> 8) * block_bytes_of(type);
     // (Q5_K, Q3_K, Q8_0: estimated from their decode next to Q4_K's)
     const double c0 = type == T_Q4K ? 45 : type == T_Q6K ? 170 : type == T_Q2K ? 30
-                    : type == T_Q5K ? 55 : type == T_Q3K ? 70 : type == T_Q80 ? 25 : 35;
-    const double c1 = type == T_Q6K ? 140 : 150;
+                    : type == T_Q5K ? 55 : type == T_Q3K ? 70 : type == T_Q80 ? 25 : i8 ? 50 : 35;
+    const double c1 = type == T_Q6K ? 140 : i8 ? 60 : 150;
     // per-pass and per-tile overheads, fitted to timings of the 27B gate
     // and down shapes (a pass stages x and ramps the weight stream up)
     const double item_cost = 20000, tile_cost = 500;
@@ -4661,14 +4667,18 @@ long kqk_mx_plan(int type, int N, int K, int mmax, int ngmax, int grid, int lds_
     long best_lds = -1;
     const int m0 = mmax < MX_MC ? mmax : MX_MC;
     for (int mch = m0; mch >= 1; mch = mch > 1 ? (mch + 1) / 2 : 0) {
-        const long sums = xpc ? ((long)mch * per * 4 + 15) & ~15L : 0;
-        const long whole = (long)mch * NCg * XPAD * 16;
+        // int8 members: chunks of XPAD_I8 slots and XS_PER_CHUNK floats
+        const long sums = i8 ? ((long)mch * NCg * xpc * 4 + 15) & ~15L
+                        : xpc ? ((long)mch * per * 4 + 15) & ~15L : 0;
+        const long whole = (long)mch * NCg * (i8 ? XPAD_I8 : XPAD) * 16;
         long xt, lds;
         int TC;
         if (head + sums + whole <= lds_max) {
             TC = NCg;
             xt = whole;
             lds = head + sums + xt;
+        } else if (i8) {
+            continue;                           // int8 members are staged whole
         } else {
             TC = 0;
             for (int tc = GP; tc < NCg; tc += GP) {
@@ -4722,11 +4732,16 @@ int kqk_mx_set_max_lds(int bytes) {
     {&kq_mx_kernel<T_, 1, true>, &kq_mx_kernel<T_, 2, true>, &kq_mx_kernel<T_, 1, false>, \
      &kq_mx_kernel<T_, 2, false>}
     typedef void (*mx_fn)(MxArg);
-    const mx_fn fns[7][4] = {KQ_MX_ATTR(T_Q4K), KQ_MX_ATTR(T_Q6K), KQ_MX_ATTR(T_Q2K),
-                             KQ_MX_ATTR(T_NIB), KQ_MX_ATTR(T_Q5K), KQ_MX_ATTR(T_Q3K),
-                             KQ_MX_ATTR(T_Q80)};
+#define KQ_MX_ATTR8(T_)                                                                 \
+    {&kq_mx_kernel<T_, 1, true>, &kq_mx_kernel<T_, 2, true>, &kq_mx_kernel<T_, 1, true>,  \
+     &kq_mx_kernel<T_, 2, true>}
+    const mx_fn fns[10][4] = {KQ_MX_ATTR(T_Q4K), KQ_MX_ATTR(T_Q6K), KQ_MX_ATTR(T_Q2K),
+                              KQ_MX_ATTR(T_NIB), KQ_MX_ATTR(T_Q5K), KQ_MX_ATTR(T_Q3K),
+                              KQ_MX_ATTR(T_Q80), KQ_MX_ATTR8(T_Q5K_I8), KQ_MX_ATTR8(T_Q3K_I8),
+                              KQ_MX_ATTR8(T_Q80_I8)};
 #undef KQ_MX_ATTR
-    for (int t = 0; t < 7; t++)
+#undef KQ_MX_ATTR8
+    for (int t = 0; t < 10; t++)
         for (int i = 0; i < 4; i++) {
             const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fns[t][i]),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
@@ -4781,6 +4796,9 @@ int kqk_launch_mx(int type, const int* plan, long lds, int grid, const void* w, 
     case T_Q5K: return launch_mx_t<T_Q5K>(a, plan[1], whole, lds, st);
     case T_Q3K: return launch_mx_t<T_Q3K>(a, plan[1], whole, lds, st);
     case T_Q80: return launch_mx_t<T_Q80>(a, plan[1], whole, lds, st);
+    case T_Q5K_I8: return launch_mx_t<T_Q5K_I8>(a, plan[1], whole, lds, st);
+    case T_Q3K_I8: return launch_mx_t<T_Q3K_I8>(a, plan[1], whole, lds, st);
+    case T_Q80_I8: return launch_mx_t<T_Q80_I8>(a, plan[1], whole, lds, st);
     default: return (int)hipErrorInvalidValue;
     }
 }
@@ -4856,6 +4874,9 @@ int kqk_launch_mx_moe(int type, const int* plan, long plan_lds, long lds, int gr
     case T_Q5K: return launch_mx_t<T_Q5K>(a, plan[1], whole, lds, st);
     case T_Q3K: return launch_mx_t<T_Q3K>(a, plan[1], whole, lds, st);
     case T_Q80: return launch_mx_t<T_Q80>(a, plan[1], whole, lds, st);
+    case T_Q5K_I8: return launch_mx_t<T_Q5K_I8>(a, plan[1], whole, lds, st);
+    case T_Q3K_I8: return launch_mx_t<T_Q3K_I8>(a, plan[1], whole, lds, st);
+    case T_Q80_I8: return launch_mx_t<T_Q80_I8>(a, plan[1], whole, lds, st);
     default: return (int)hipErrorInvalidValue;
     }
 }
@@ -5107,17 +5128,12 @@ int kqk_launch_mi8(int type, const float* xs, long x_stride, const void* w, floa
 #define KQ_MI8G_P 1
 #endif
 static long mi8_moe_layout(int type, int nx, int K, long* cf_off, long* sm_off, long* zp_off) {
-    // the per-32 types share Q4_K's layout (their batches use only the
-    // quantized rows and the {scale, sum} pairs)
-    const int lt = type == T_Q6K_I8 ? T_Q6K_I8
-                 : type == T_Q4K_I8 || type == T_Q5K_I8 || type == T_Q3K_I8 || type == T_Q80_I8
-                 ? T_Q4K_I8 : -1;
-    const long base = nx < 1 || lt < 0 ? -1 : kqk_mi8_workspace(lt, nx + 1, K, cf_off);
+    const long base = nx < 1 ? -1 : kqk_mi8_workspace(type, nx + 1, K, cf_off);
     if (base < 0) return -1;
     const long bpad = (nx + 1 + 15) & ~15L;
     *zp_off = base - 256;
     *sm_off = base;
-    return base + ((bpad * (K / (lt == T_Q4K_I8 ? 32 : 16)) * 8 + 255) & ~255L);
+    return base + ((bpad * (K / (type == T_Q4K_I8 ? 32 : 16)) * 8 + 255) & ~255L);
 }
 
 long kqk_mi8_moe_workspace(int type, int nx, int K) {
@@ -5135,13 +5151,11 @@ int kqk_launch_mi8_moe(int type, const int* sel, int nm, int E, int nt, int x_di
         return (int)hipErrorInvalidValue;
     long cf_off = 0, sm_off = 0, zp_off = 0;
     const long wsb = mi8_moe_layout(type, nx, K, &cf_off, &sm_off, &zp_off);
-    const bool pack = type == T_Q4K_I8 || type == T_Q6K_I8;   // runs of up to 8, else of 1
     const int ks = kqk_mi8_parts(K);
     // several row blocks per workgroup when the row is one K-part: a run's
     // workgroup then streams one weight sequence instead of paying a
-    // launch-to-first-load latency per 16 rows (the per-stream types: four,
-    // 256 lanes on 64 rows, when their chunk terms fit)
-    const int rbw = pack ? (ks == 1 ? KQ_MI8_RBW : 1) : (K <= 8192 ? 4 : 1);
+    // launch-to-first-load latency per 16 rows
+    const int rbw = ks == 1 ? KQ_MI8_RBW : 1;
     const long tl = 16L * rbw * (K >> 6) * 8;    // a single member's chunk terms
     if (wsb < 0 || nx < 1 || N < 1 || ngmax < 1 || ngmax > 65535 || y_stride < N || !groups ||
         !ng || ((uintptr_t)x & 15) || ((uintptr_t)ws & 15) || tl > 65536)
@@ -5153,10 +5167,10 @@ int kqk_launch_mi8_moe(int type, const int* sel, int nm, int E, int nt, int x_di
     const int G = type == T_Q6K_I8 ? 16 : 32;
     const int bpad = (nx + 1 + 15) & ~15;        // rows nx .. bpad-1 zero
     const long gq = (long)bpad * (K / G);
-    // the runs (workgroup 0, kq_moe_group_kernel's rule with run length 8,
-    // or 1) and the quantized rows (the other workgroups) in one launch
+    // the runs (workgroup 0, kq_moe_group_kernel's rule with run length 8)
+    // and the quantized rows (the other workgroups) in one launch
     MoeGroupArg ga;
-    ga.sel = sel; ga.nm = nm; ga.E = E; ga.nt = nt; ga.x_div = x_div; ga.mch = pack ? 8 : 1;
+    ga.sel = sel; ga.nm = nm; ga.E = E; ga.nt = nt; ga.x_div = x_div; ga.mch = 8;
     ga.w[0] = static_cast<const uint8_t*>(w0);
     ga.w[1] = static_cast<const uint8_t*>(nt > 1 ? w1 : w0);
     ga.y[0] = y0;
@@ -5186,16 +5200,6 @@ int kqk_launch_mi8_moe(int type, const int* sel, int nm, int E, int nt, int x_di
     a.rbw = rbw;
     a.sm = sm;
     const int nrb = ((N + 15) / 16 + rbw - 1) / rbw;
-    if (!pack) {
-        const dim3 g((unsigned)nrb, (unsigned)ngmax);
-        if (type == T_Q5K_I8)
-            hipLaunchKernelGGL(kq_mi8s_kernel<T_Q5K_I8>, g, dim3(256), (size_t)tl, st, a);
-        else if (type == T_Q3K_I8)
-            hipLaunchKernelGGL(kq_mi8s_kernel<T_Q3K_I8>, g, dim3(256), (size_t)tl, st, a);
-        else
-            hipLaunchKernelGGL(kq_mi8s_kernel<T_Q80_I8>, g, dim3(256), (size_t)tl, st, a);
-        return (int)hipGetLastError();
-    }
 #define KQ_MI8G_GO(T_, P_, K_)                                                               \
     hipLaunchKernelGGL((kq_mi8_kernel<T_, 8, P_, K_, true>), dim3((unsigned)nrb,             \
                        (unsigned)ngmax), dim3(64 * K_), (size_t)tl, st, a)

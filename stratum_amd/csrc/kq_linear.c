@@ -106,21 +106,21 @@ static int is_i8mx(int type) {
     return type == (KQ_INT8_ACT | KQ_TYPE_Q4_K) || type == (KQ_INT8_ACT | KQ_TYPE_Q6_K);
 }
 
-/* every type in the int8 mode (the five SDOT types) */
-static int is_i8(int type) {
-    return (type & KQ_INT8_ACT) && has_sdot(type & ~KQ_INT8_ACT);
-}
-
 /* the four types of the fused batch-1 MoE FFN step */
 static int is_core(int type) {
     return type == KQ_TYPE_Q2_K || type == KQ_TYPE_Q4_K || type == KQ_TYPE_Q6_K ||
            type == KQ_TYPE_Q2K_NIB;
 }
 
-/* the types the exact multi-x (MULTISEQ, MoE batch) kernel covers: every
- * block type; the int8 mode and the dense types have their own paths */
+/* the types the multi-x (MULTISEQ, MoE batch) kernel covers: every block
+ * type, and the int8 mode of Q5_K, Q3_K and Q8_0 (whose batches are per
+ * stream in the reference, so every member takes the single-stream int8
+ * values); int8 Q4_K / Q6_K and the dense types have their own paths */
 static int is_mx(int type) {
-    return is_core(type) || type == KQ_TYPE_Q5_K || type == KQ_TYPE_Q3_K || type == KQ_TYPE_Q8_0;
+    const int t = type & ~KQ_INT8_ACT;
+    if (type & KQ_INT8_ACT)
+        return t == KQ_TYPE_Q5_K || t == KQ_TYPE_Q3_K || t == KQ_TYPE_Q8_0;
+    return is_core(t) || t == KQ_TYPE_Q5_K || t == KQ_TYPE_Q3_K || t == KQ_TYPE_Q8_0;
 }
 
 int64_t kq_row_bytes(int type, int K) {
@@ -1160,23 +1160,23 @@ static int moe_batch(const kq_moe_op* op, int* sel, const float* probs, float* s
 static size_t moe_i8_bytes(int type, int nx, int K, int nt, int nm, int E) {
     const long xw = kqk_mi8_moe_workspace(type, nx, K);
     if (xw < 0) return 0;
-    return (((size_t)xw + 255) & ~(size_t)255) + moe_group_bytes(nt, nm, E, is_i8mx(type) ? 8 : 1);
+    return (((size_t)xw + 255) & ~(size_t)255) + moe_group_bytes(nt, nm, E, 8);
 }
 
-/* Several tokens in the int8 mode.  moe_forward_b under use_sdot
- * (stratum_arch_moe.inc.c:1136-1201) runs each expert's members, in
- * increasing member order, in tickets of at most CH = 8 through
- * st_linear_multix: for Q4_K / Q6_K a ticket of two or more members takes
- * the multix pack arithmetic and a ticket of one the single-stream path;
- * for Q5_K, Q3_K and Q8_0 every member gets the single-stream values
- * (st_linear_multix is per stream for Q5_K / Q3_K, and Q8_0's pack equals
- * its single-stream path, stratum_q8_0.h:145-149).  Here the runs are cut
- * on the device (kq_moe_group_kernel's rule, run length 8, or 1 for the
- * per-stream types) in the launch that quantizes every x row once, and one
- * grouped launch computes all runs (kq_mi8_kernel GR, kq_mi8s_kernel):
- * each member equals kq_gemv_multix_dev over its run (kq_gemv_dev for a run
- * of one) bit for bit.  The workspace is io->grp when given (the FFN
- * step's), else the library's matrix-core scratch. */
+/* Several tokens in the int8 mode, Q4_K / Q6_K.  moe_forward_b under
+ * use_sdot (stratum_arch_moe.inc.c:1136-1201) runs each expert's members,
+ * in increasing member order, in tickets of at most CH = 8 through
+ * st_linear_multix: a ticket of two or more members takes the multix pack
+ * arithmetic, a ticket of one the single-stream path.  Here the same runs
+ * are cut on the device (kq_moe_group_kernel's rule, run length 8) in the
+ * launch that quantizes every x row once, and one grouped matrix-core
+ * launch computes all runs (kq_mi8_kernel, GR): each member equals
+ * kq_gemv_multix_dev over its run (kq_gemv_dev for a run of one) bit for
+ * bit.  (For Q5_K, Q3_K and Q8_0 st_linear_multix is per stream -- Q8_0's
+ * pack equals its single-stream path, stratum_q8_0.h:145-149 -- so the
+ * tickets do not matter: their batches run in the multi-x kernel, moe_batch.)
+ * The workspace is io->grp when given (the FFN step's), else the library's
+ * matrix-core scratch. */
 static int moe_i8_batch(const kq_moe_op* op, const int* sel, int B, int k, int E,
                         moe_runs_io* io, hipStream_t st) {
     const int nm = B * k, nt = op->ntensors, nx = nm / op->x_div, K = op->k_in;
@@ -1193,8 +1193,8 @@ static int moe_i8_batch(const kq_moe_op* op, const int* sel, int B, int k, int E
         base = g_kq.d_mf;
     }
     const size_t xwa = ((size_t)kqk_mi8_moe_workspace(op->type, nx, K) + 255) & ~(size_t)255;
-    const int dmax = E < nm ? E : nm, mch = is_i8mx(op->type) ? 8 : 1;
-    const int ngmax = nt * (dmax + (nm + mch - 1) / mch);
+    const int dmax = E < nm ? E : nm;
+    const int ngmax = nt * (dmax + (nm + 7) / 8);
     void* groups = base + xwa;
     int* ng = (int*)(base + xwa + (size_t)ngmax * (size_t)kqk_mx_group_bytes());
     const int e = kqk_launch_mi8_moe(op->type, sel, nm, E, nt, op->x_div, op->w[0], op->w[nt - 1],
@@ -1228,8 +1228,8 @@ static int moe_gemv_routed(const kq_moe_op* op, const float* probs, int B, int k
     if (!is_mx(op->type)) {
         const int e = kqk_launch_moe_topk(probs, B, E, k, sel, selw, st);
         if (e) return kq_fail("moe topk launch: %s", hipGetErrorString((hipError_t)e));
-        return is_i8(op->type) ? moe_i8_batch(op, sel, B, k, E, io, st)
-                               : moe_per_token(op, sel, B, k, E, st);
+        return is_i8mx(op->type) ? moe_i8_batch(op, sel, B, k, E, io, st)
+                                 : moe_per_token(op, sel, B, k, E, st);
     }
     const int r = moe_batch(op, sel, probs, selw, B, k, E, io, st);
     if (r <= 0) return r;
@@ -1253,7 +1253,7 @@ static int moe_gemv(const kq_moe_op* op, const int* sel, int B, int k, int E, mo
         return kq_fail("kq_moe_gemv_dev: B=%d k=%d E=%d", B, k, E);
     if (moe_check_op(op, k, E, "kq_moe_gemv_dev")) return -1;
     if (B == 1) return moe_one_token(op, sel, k, E, NULL, NULL, st);
-    if (is_i8(op->type)) return moe_i8_batch(op, sel, B, k, E, io, st);
+    if (is_i8mx(op->type)) return moe_i8_batch(op, sel, B, k, E, io, st);
     if (!is_mx(op->type)) return moe_per_token(op, sel, B, k, E, st);
     return moe_batch(op, (int*)sel, NULL, NULL, B, k, E, io, st);
 }
@@ -1312,9 +1312,9 @@ static int64_t ffn_layout(const kq_moe_ffn* f, int B, int64_t off[FFN_REGIONS]) 
     size_t g6 = moe_group_bytes(2, (int)bk, E, 1);
     if (B > 1) {
         const size_t i8[3] = {
-            is_i8(f->gate_type) ? moe_i8_bytes(f->gate_type, B, f->n_embed, pair ? 2 : 1, (int)bk, E) : 0,
-            is_i8(f->up_type) ? moe_i8_bytes(f->up_type, B, f->n_embed, 1, (int)bk, E) : 0,
-            is_i8(f->down_type) ? moe_i8_bytes(f->down_type, (int)bk, f->n_ff, 1, (int)bk, E) : 0};
+            is_i8mx(f->gate_type) ? moe_i8_bytes(f->gate_type, B, f->n_embed, pair ? 2 : 1, (int)bk, E) : 0,
+            is_i8mx(f->up_type) ? moe_i8_bytes(f->up_type, B, f->n_embed, 1, (int)bk, E) : 0,
+            is_i8mx(f->down_type) ? moe_i8_bytes(f->down_type, (int)bk, f->n_ff, 1, (int)bk, E) : 0};
         for (int i = 0; i < 3; i++) g6 = i8[i] > g6 ? i8[i] : g6;
     }
     const int64_t sz[FFN_REGIONS] = {

@@ -248,12 +248,17 @@ def test_segments_groups_strided_x(port, qtype):
 
 
 @pytest.mark.parametrize("qtype", [TYPE_Q5_K, TYPE_Q3_K, TYPE_Q8_0])
-def test_multix_equals_single_stream(qtype):
-    """the int8 types without a matrix-core MULTISEQ form: per-stream
-    launches, each stream bit-identical to its single-stream result"""
-    N, Kd, B = 100, 1024, 5
-    w = synth.tensor(qtype, N, Kd, 8800)
+@pytest.mark.parametrize("B,N,Kd", [(5, 100, 1024), (2, 300, 768), (16, 64, 2048), (19, 40, 3072),
+                                    (40, 96, 1024), (70, 33, 512), (8, 200, 17408)])
+def test_multix_equals_single_stream(qtype, B, N, Kd):
+    """The int8 types whose reference batches are per stream (Q5_K, Q3_K,
+    Q8_0: st_linear_multix calls the single-stream form per stream): one
+    weight pass of the multi-x kernel for all streams, each stream
+    bit-identical to its single-stream result; ragged rows, member chunks
+    past 16 and 64 streams, and rows of 272 chunks."""
+    w = synth.tensor(qtype, N, Kd, 8800 + B)
     xs = np.stack([synth.gaussian(synth.rng(8801 + s), Kd) for s in range(B)])
+    print(f"int8 multix type={qtype} B={B} N={N} K={Kd}", flush=True)
     dw, dx = dev(w), dev(xs.reshape(-1))
     dy = torch.full((B * N,), float("nan"), dtype=torch.float32, device="cuda")
     K.gemv_multix_dev(qtype | INT8_ACT, dw.data_ptr(), dx.data_ptr(), dy.data_ptr(), B, N, Kd,

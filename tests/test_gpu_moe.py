@@ -591,11 +591,10 @@ def test_moe_int8_tickets_shapes(port, B, E, k):
 def test_moe_int8_per_stream_types(port, qtype, H, F, N_g):
     """Q5_K, Q3_K and Q8_0 batches in the int8 mode: st_linear_multix is per
     stream for them, so every member of every ticket equals its slice's
-    single int8 GEMV bit for bit (one grouped launch of single-member runs).
+    single int8 GEMV bit for bit (each slice streamed once for its members).
     Experts chosen by 1, 2, 9 and 17 tokens with one slot left empty (sel
-    -1, not written); rows of 16 chunks up to 192 (down K = 12288: one row
-    block per workgroup), and a gate of 200 rows (a partial last row block,
-    gate only)."""
+    -1, not written); rows of 4 to 192 chunks (down K = 12288), and a gate
+    of 200 rows (a partial last row block, gate only)."""
     n_exp, k, B = 24, 4, 20
     sel = designed_sel(B, k, [1, 2, 9, 17], n_exp, 110 + qtype)
     hole = 5 * k + int(np.nonzero(sel[5] >= 4)[0][0])
