@@ -217,8 +217,9 @@ __device__ __forceinline__ double phase_tree(double s, int G) {
 // binary32 order when the type has min terms (Q4_K: 32 values per
 // sub-block, stratum_q4k.h:115-122; Q2_K / type 42: 16 values,
 // stratum_q2k.h:65-68), scales, and writes to its LDS slots.  The first
-// round of x loads is issued before the weight prefetch and consumed after
-// it, so x arrives first and the weights' latency overlaps the staging.
+// weight batches are issued once the first round of x has arrived, so the
+// weight stream does not queue ahead of x; their latency overlaps the LDS
+// stores and the barrier.
 //
 // Scaled mode (Q4_K, Q2_K, type 42).  The byte-select multiply (bmul) needs
 // every nonzero product q * x' (q >= 1) in the binary32 normal range, so x
