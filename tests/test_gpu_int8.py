@@ -269,6 +269,30 @@ def test_multix_equals_single_stream(qtype, B, N, Kd):
         assert same_values(ys[s], gpu_gemv(qtype | INT8_ACT, w, xs[s], N, Kd)), s
 
 
+@pytest.mark.parametrize("qtype", [TYPE_Q5_K, TYPE_Q3_K, TYPE_Q8_0])
+def test_multix_edge_streams(qtype):
+    """The int8 multi-x path of the per-stream types on edge inputs: rows
+    of one super-block (K = 256) and a single row, a stream of zeros (scale
+    0: every quantized value 0), a stream with 1e30 and subnormal values,
+    and 65 streams (two launches): each stream bit-identical to its
+    single-stream result."""
+    for N, Kd, B in ((1, 256, 3), (37, 256, 65), (130, 512, 4)):
+        w = synth.tensor(qtype, N, Kd, 8900 + N)
+        xs = np.stack([synth.gaussian(synth.rng(8901 + s), Kd) for s in range(B)])
+        xs[1] = 0.0
+        xs[B - 1, ::7] = 1e30
+        xs[B - 1, 3::11] = 1e-40
+        print(f"int8 multix edges type={qtype} N={N} K={Kd} B={B}", flush=True)
+        dw, dx = dev(w), dev(xs.reshape(-1))
+        dy = torch.full((B * N,), float("nan"), dtype=torch.float32, device="cuda")
+        K.gemv_multix_dev(qtype | INT8_ACT, dw.data_ptr(), dx.data_ptr(), dy.data_ptr(), B, N, Kd,
+                          stream=stream())
+        torch.cuda.synchronize()
+        ys = dy.cpu().numpy().reshape(B, N)
+        for s in range(B):
+            assert same_values(ys[s], gpu_gemv(qtype | INT8_ACT, w, xs[s], N, Kd)), (N, Kd, s)
+
+
 def test_host_abi_sdot_switch(port):
     """kq_linear_set_sdot routes the host-pointer entry points through the
     int8 mode for Q4_K, Q6_K, Q5_K, Q3_K and Q8_0 (as g_st.use_sdot does,
