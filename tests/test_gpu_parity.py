@@ -284,6 +284,42 @@ def test_segments_mixed_q4k_q6k(port, order):
             check_close(got, port.gemv(t, ws[i], x, rows[i], H, threads=8), f"seg {i}")
 
 
+def test_segments_mixed_q4k_q6k_groups_and_add(port):
+    """The Q4_K+Q6_K kernel with the other part forms: a Q4_K segment of
+    three groups (separate weight bases, one x) with a residual add, a Q6_K
+    segment of two groups each on its own x (x_stride), and a plain Q4_K
+    one, in one list: every output equals its own single launch (with the
+    add as one binary32 add after the row)."""
+    H, N = 1024, 96
+    r = synth.rng(8480)
+    x = synth.gaussian(r, H)
+    xs2 = np.stack([synth.gaussian(r, H) for _ in range(2)])
+    add = synth.gaussian(r, 3 * N)
+    wa = [synth.tensor(12, N, H, 8481 + g) for g in range(3)]
+    wb = [synth.tensor(14, N, H, 8485 + g) for g in range(2)]
+    wc = synth.tensor(12, 40, H, 8488)
+    dx, dx2, dadd = dev(x), dev(xs2.reshape(-1)), dev(add)
+    dwa, dwb, dwc = [dev(w) for w in wa], [dev(w) for w in wb], dev(wc)
+    ya = torch.full((3 * N,), float("nan"), dtype=torch.float32, device="cuda")
+    yb = torch.full((2 * N,), float("nan"), dtype=torch.float32, device="cuda")
+    yc = torch.full((40,), float("nan"), dtype=torch.float32, device="cuda")
+    segs = [K.segment(12, H, N, [d.data_ptr() for d in dwa], dx.data_ptr(), ya.data_ptr(),
+                      add_ptr=dadd.data_ptr()),
+            K.segment(14, H, N, [d.data_ptr() for d in dwb], dx2.data_ptr(), yb.data_ptr(),
+                      x_stride=H),
+            K.segment(12, H, 40, [dwc.data_ptr()], dx.data_ptr(), yc.data_ptr())]
+    print("mixed q4k/q6k groups + add", flush=True)
+    K.gemv_segments_dev(segs, stream=stream())
+    torch.cuda.synchronize()
+    got_a, got_b, got_c = ya.cpu().numpy(), yb.cpu().numpy(), yc.cpu().numpy()
+    for g in range(3):
+        want = gpu_gemv(12, wa[g], x, N, H, add=add[g * N:(g + 1) * N])
+        assert same_values(got_a[g * N:(g + 1) * N], want), g
+    for g in range(2):
+        assert same_values(got_b[g * N:(g + 1) * N], gpu_gemv(14, wb[g], xs2[g], N, H)), g
+    assert same_values(got_c, gpu_gemv(12, wc, x, 40, H))
+
+
 def test_segments_groups_expert_slices(port):
     """MoE-style segments: groups with separate weight bases; gate/up share
     x, down uses one x per group (x_stride)."""
