@@ -166,9 +166,9 @@ int kq_q4k_group(const float* x, int K,
  * For a device-resident decode loop: all pointers are device pointers,
  * the call only enqueues work on `stream` (asynchronous).  x and xs must
  * be 16-byte aligned.  The MoE batch and matrix-core entries use scratch
- * buffers owned by the library (one per kind, grown on demand): calls of
- * the same kind on different streams that overlap in time race on it;
- * calls on one stream are ordered. */
+ * buffers owned by the library, one set per stream (up to 16 streams; a
+ * seventeenth returns -1), grown on demand: calls on different streams may
+ * overlap in time, calls on one stream are ordered. */
 
 /* The int8 quantizer of the int8-activation mode on its own: group 32 is
  * q4k_quantize_x_q8 (+ q4k_sum_i8_32 sums, stratum_q4k_neon.h:229-275,
@@ -193,7 +193,8 @@ int kq_gemv_dev(int type, const void* w, const float* x, const float* add, float
  * order, which differs from the single-stream SDOT form's rounding (the
  * reference's own quant_test.c holds the two within 1e-4).  That path
  * runs the integer dots on the matrix cores and uses the library's
- * matrix-core workspace (grown on demand, see kq_reserve_mfma_workspace). */
+ * matrix-core workspace of the call's stream (grown on demand, see
+ * kq_reserve_mfma_workspace). */
 int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,
                        int B, int N, int K, kq_stream stream);
 
@@ -208,10 +209,10 @@ int kq_gemv_multix_dev(int type, const void* w, const float* xs, float* ys,
  * No counterpart in the reference, whose multix must equal the
  * single-stream result (stratum_linear.h:963-966); this is the opt-in
  * dense-contraction path for large B.  x must be finite.  The workspace is
- * the library's, grown on the first call of a larger shape (hipMalloc /
- * hipFree, which synchronise the device) unless reserved beforehand
- * (kq_reserve_mfma_workspace); callers that cannot allocate at all use
- * kq_gemv_multix_mfma_noalloc_dev. */
+ * the library's, one per stream, grown on the first call of a larger shape
+ * on that stream (hipMalloc / hipFree, which synchronise the device) unless
+ * reserved beforehand (kq_reserve_mfma_workspace); callers that cannot
+ * allocate at all use kq_gemv_multix_mfma_noalloc_dev. */
 int kq_gemv_multix_mfma_dev(int type, const void* w, const float* xs, float* ys,
                             int B, int N, int K, kq_stream stream);
 
@@ -219,12 +220,15 @@ int kq_gemv_multix_mfma_dev(int type, const void* w, const float* xs, float* ys,
  * N, K), or -1.  No counterpart in the reference. */
 int64_t kq_gemv_multix_mfma_workspace_bytes(int type, int B, int N, int K);
 
-/* Grows the library's matrix-core workspace to at least `bytes` now (one
- * hipMalloc, which synchronises the device), so that later calls whose
+/* Grows the matrix-core workspace of the default stream (stream 0) and of
+ * every stream the library has run device entries on to at least `bytes`
+ * now (hipMalloc, which synchronises the device), so that later calls whose
  * workspace fits allocate nothing: for callers that set up once and then
- * enqueue only (graph capture of the calls, serving loops).  The workspace
- * is never shrunk before kq_linear_shutdown.  No counterpart in the
- * reference.  Returns 0, or -1 with a message. */
+ * enqueue only (graph capture of the calls, serving loops).  A stream first
+ * used later gets at least `bytes` at its first call, so such a caller makes
+ * one call on each of its streams before it stops allocating.  No workspace
+ * is shrunk before kq_linear_shutdown.  No counterpart in the reference.
+ * Returns 0, or -1 with a message. */
 int kq_reserve_mfma_workspace(int64_t bytes);
 
 /* Bytes of device scratch the library holds: the matrix-core workspace, the

@@ -26,6 +26,16 @@
 #include "kq_launch.h"
 
 #define KQ_MAX_REGIONS 16
+#define KQ_SCR_SLOTS 16    /* streams with their own device-entry scratch */
+
+/* one stream's scratch: MoE group records + their count; the matrix-core
+ * workspace (x planes, sums, partials; int8 rows and coefficients) */
+typedef struct {
+    hipStream_t st;
+    int used;
+    float* moe; size_t cap_moe;
+    uint8_t* mf; size_t cap_mf;
+} kq_scr;
 
 typedef struct {
     const uint8_t* host;
@@ -48,8 +58,8 @@ typedef struct {
     float* d_x; size_t cap_x;
     float* d_y; size_t cap_y;
     float* d_a; size_t cap_a;
-    float* d_moe; size_t cap_moe;   /* MoE expert groups + their count */
-    uint8_t* d_mf; size_t cap_mf;   /* MFMA multi-x: x planes, sums, partials */
+    kq_scr scr[KQ_SCR_SLOTS];       /* the device entries' scratch, per stream */
+    size_t mf_reserve;              /* kq_reserve_mfma_workspace: least mf size */
     /* launch overrides from the environment (0: unset), read by kq_ready
      * and again only by kq_tuning_reload: the planner runs on every call */
     int env_grid, env_threads, env_depth, env_moe_group_launch, env_ffn_split;
@@ -58,6 +68,7 @@ typedef struct {
 } kq_state;
 
 static kq_state g_kq;
+
 
 /* shared with kq_gguf.c; not exported */
 __attribute__((visibility("hidden"))) int kq_fail(const char* fmt, ...) {
@@ -70,6 +81,24 @@ __attribute__((visibility("hidden"))) int kq_fail(const char* fmt, ...) {
 }
 
 const char* kq_last_error(void) { return g_kq.err; }
+
+/* The scratch of the device entries that stream `st` runs on: calls on
+ * different streams get different buffers (they may overlap in time),
+ * calls on one stream are ordered.  NULL (message set) past
+ * KQ_SCR_SLOTS streams. */
+static kq_scr* scr_of(hipStream_t st) {
+    for (int i = 0; i < KQ_SCR_SLOTS; i++)
+        if (g_kq.scr[i].used && g_kq.scr[i].st == st) return &g_kq.scr[i];
+    for (int i = 0; i < KQ_SCR_SLOTS; i++)
+        if (!g_kq.scr[i].used) {
+            g_kq.scr[i].used = 1;
+            g_kq.scr[i].st = st;
+            return &g_kq.scr[i];
+        }
+    kq_fail("device entries used on more than %d streams: the library keeps scratch for "
+            "at most %d", KQ_SCR_SLOTS, KQ_SCR_SLOTS);
+    return NULL;
+}
 
 /* the types with an int8-activation (SDOT) form: st_linear_q4k, _q6k,
  * _q5k, _q3k and _q8_0 under g_st.use_sdot (stratum_linear.h:369-489) */
@@ -242,8 +271,10 @@ void kq_linear_shutdown(void) {
     if (g_kq.d_x) (void)hipFree(g_kq.d_x);
     if (g_kq.d_y) (void)hipFree(g_kq.d_y);
     if (g_kq.d_a) (void)hipFree(g_kq.d_a);
-    if (g_kq.d_moe) (void)hipFree(g_kq.d_moe);
-    if (g_kq.d_mf) (void)hipFree(g_kq.d_mf);
+    for (int i = 0; i < KQ_SCR_SLOTS; i++) {
+        if (g_kq.scr[i].moe) (void)hipFree(g_kq.scr[i].moe);
+        if (g_kq.scr[i].mf) (void)hipFree(g_kq.scr[i].mf);
+    }
     if (g_kq.stream_ready) (void)hipStreamDestroy(g_kq.stream);
     memset(&g_kq, 0, sizeof g_kq);
 }
@@ -553,7 +584,7 @@ static long mx_plan(int type, int N, int K, int mmax, int ngmax, int grid, const
     return lds;
 }
 
-static int mfma_reserve(size_t need);
+static int mfma_reserve(kq_scr* sc, size_t need);
 
 /* The int8 MULTISEQ of st_linear_multix under use_sdot (Q4_K / Q6_K, B >= 2,
  * stratum_linear.h:732-907): streams quantized into the library's
@@ -564,8 +595,9 @@ static int mi8_multix(int type, const void* w, const float* xs, float* ys, int B
     long cf_off = 0;
     const long need = kqk_mi8_workspace(type, B, K, &cf_off);
     if (need < 0) return kq_fail("int8 multix: bad shape B=%d K=%d", B, K);
-    if (mfma_reserve((size_t)need)) return -1;
-    const int e = kqk_launch_mi8(type, xs, K, w, ys, N, B, N, K, g_kq.d_mf, 0, st);
+    kq_scr* sc = scr_of(st);
+    if (!sc || mfma_reserve(sc, (size_t)need)) return -1;
+    const int e = kqk_launch_mi8(type, xs, K, w, ys, N, B, N, K, sc->mf, 0, st);
     if (e) return kq_fail("int8 multix launch: %s", hipGetErrorString((hipError_t)e));
     return 0;
 }
@@ -648,14 +680,16 @@ static int mfma_launch(int type, const void* w, const float* xs, float* ys, int 
     return 0;
 }
 
-/* Grows the library's matrix-core workspace to at least `need` bytes. */
-static int mfma_reserve(size_t need) {
-    if (g_kq.cap_mf >= need) return 0;
-    if (g_kq.d_mf) (void)hipFree(g_kq.d_mf);
-    g_kq.d_mf = NULL;
-    g_kq.cap_mf = 0;
-    if (hip_ok(hipMalloc((void**)&g_kq.d_mf, need), "hipMalloc(mfma workspace)")) return -1;
-    g_kq.cap_mf = need;
+/* Grows a stream's matrix-core workspace to at least `need` bytes (and at
+ * least what kq_reserve_mfma_workspace asked for). */
+static int mfma_reserve(kq_scr* sc, size_t need) {
+    if (need < g_kq.mf_reserve) need = g_kq.mf_reserve;
+    if (sc->cap_mf >= need) return 0;
+    if (sc->mf) (void)hipFree(sc->mf);
+    sc->mf = NULL;
+    sc->cap_mf = 0;
+    if (hip_ok(hipMalloc((void**)&sc->mf, need), "hipMalloc(mfma workspace)")) return -1;
+    sc->cap_mf = need;
     return 0;
 }
 
@@ -664,8 +698,10 @@ int kq_gemv_multix_mfma_dev(int type, const void* w, const float* xs, float* ys,
     size_t o_xs, o_pt;
     const size_t need = mfma_prepare("kq_gemv_multix_mfma_dev", type, w, xs, ys, B, N, K,
                                      &o_xs, &o_pt);
-    if (!need || mfma_reserve(need)) return -1;
-    return mfma_launch(type, w, xs, ys, B, N, K, g_kq.d_mf, o_xs, o_pt, stream);
+    if (!need) return -1;
+    kq_scr* sc = scr_of(pick(stream));
+    if (!sc || mfma_reserve(sc, need)) return -1;
+    return mfma_launch(type, w, xs, ys, B, N, K, sc->mf, o_xs, o_pt, stream);
 }
 
 int64_t kq_gemv_multix_mfma_workspace_bytes(int type, int B, int N, int K) {
@@ -679,12 +715,19 @@ int64_t kq_gemv_multix_mfma_workspace_bytes(int type, int B, int N, int K) {
 int kq_reserve_mfma_workspace(int64_t bytes) {
     if (bytes < 0) return kq_fail("kq_reserve_mfma_workspace: bytes=%lld", (long long)bytes);
     if (kq_ready()) return -1;
-    return mfma_reserve((size_t)bytes);
+    if ((size_t)bytes > g_kq.mf_reserve) g_kq.mf_reserve = (size_t)bytes;
+    kq_scr* sc = scr_of(NULL);
+    if (!sc) return -1;
+    for (int i = 0; i < KQ_SCR_SLOTS; i++)     /* the default stream and every stream seen */
+        if (g_kq.scr[i].used && mfma_reserve(&g_kq.scr[i], (size_t)bytes)) return -1;
+    return 0;
 }
 
 int64_t kq_scratch_bytes(void) {
-    return (int64_t)(g_kq.cap_mf + (g_kq.cap_moe + g_kq.cap_x + g_kq.cap_y + g_kq.cap_a) *
-                                       sizeof(float));
+    size_t n = (g_kq.cap_x + g_kq.cap_y + g_kq.cap_a) * sizeof(float);
+    for (int i = 0; i < KQ_SCR_SLOTS; i++)
+        n += g_kq.scr[i].cap_mf + g_kq.scr[i].cap_moe * sizeof(float);
+    return (int64_t)n;
 }
 
 /* The same launch with its workspace in the library's static device
@@ -1139,8 +1182,9 @@ static int moe_batch(const kq_moe_op* op, int* sel, const float* probs, float* s
         gbase = (uint8_t*)io->grp;
         io->grp_used = 1;
     } else {
-        if (grow(&g_kq.d_moe, &g_kq.cap_moe, need / sizeof(float) + 1)) return -1;
-        gbase = (uint8_t*)g_kq.d_moe;
+        kq_scr* sc = scr_of(st);
+        if (!sc || grow(&sc->moe, &sc->cap_moe, need / sizeof(float) + 1)) return -1;
+        gbase = (uint8_t*)sc->moe;
     }
     void* groups = gbase;
     int* ng = (int*)(gbase + (size_t)ngmax * gbytes);
@@ -1189,8 +1233,9 @@ static int moe_i8_batch(const kq_moe_op* op, const int* sel, int B, int k, int E
         base = (uint8_t*)io->grp;
         io->grp_used = 1;
     } else {
-        if (mfma_reserve(need)) return -1;
-        base = g_kq.d_mf;
+        kq_scr* sc = scr_of(st);
+        if (!sc || mfma_reserve(sc, need)) return -1;
+        base = sc->mf;
     }
     const size_t xwa = ((size_t)kqk_mi8_moe_workspace(op->type, nx, K) + 255) & ~(size_t)255;
     const int dmax = E < nm ? E : nm;
