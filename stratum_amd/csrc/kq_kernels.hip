@@ -2829,20 +2829,26 @@ __device__ void moe_group_body(const MoeGroupArg& a, int* lds_i) {
     // (the members before it with the same expert, so places follow
     // increasing m), then its slot j % mch of run j / mch; the first member
     // of a run writes the run's header.  The scan reads ms[] at the same
-    // index in every lane (broadcast), four entries per LDS read.
+    // index in every lane (broadcast), four entries per LDS read and four
+    // reads in flight.
+    const int4* ms4 = reinterpret_cast<const int4*>(ms);
+    auto count4 = [](int4 v, int b, int m, int e) {
+        return ((b + 0 < m) & (v.x == e)) + ((b + 1 < m) & (v.y == e)) +
+               ((b + 2 < m) & (v.z == e)) + ((b + 3 < m) & (v.w == e));
+    };
     for (int m0 = 0; m0 < a.nm; m0 += T) {
         const int m = m0 + tid;
         const int e = m < a.nm ? ms[m] : -1;
         int j = 0;
         const int lim = min(a.nm, m0 + T);               // uniform bound of the scan
-        for (int q = 0; q < min(nm4, (lim + 3) >> 2); q++) {
-            const int4 v = reinterpret_cast<const int4*>(ms)[q];
-            const int b = 4 * q;
-            j += (b + 0 < m) & (v.x == e);
-            j += (b + 1 < m) & (v.y == e);
-            j += (b + 2 < m) & (v.z == e);
-            j += (b + 3 < m) & (v.w == e);
+        const int nq = min(nm4, (lim + 3) >> 2);
+        int q = 0;
+        for (; q + 4 <= nq; q += 4) {
+            const int4 v0 = ms4[q], v1 = ms4[q + 1], v2 = ms4[q + 2], v3 = ms4[q + 3];
+            j += count4(v0, 4 * q, m, e) + count4(v1, 4 * q + 4, m, e) +
+                 count4(v2, 4 * q + 8, m, e) + count4(v3, 4 * q + 12, m, e);
         }
+        for (; q < nq; q++) j += count4(ms4[q], 4 * q, m, e);
         if (e >= 0) {
             const int r = j / a.mch, slot = j - r * a.mch;
             for (int t = 0; t < a.nt; t++) {
@@ -3540,9 +3546,11 @@ __global__ __launch_bounds__(256) void kq_mi8_prep_kernel(const float* x, long x
 
 // The int8 MoE batch's set-up in one launch: workgroup 0 cuts the runs
 // (moe_group_body, as kq_moe_group_kernel), the others quantize the x rows
-// (1024 groups each, as kq_mi8_prep_kernel).
+// (256 groups each, as kq_mi8_prep_kernel).  256-lane workgroups: the
+// quantizing is about 300 VALU instructions per group, so 1024-lane
+// workgroups (four waves per SIMD on a few CUs) made it the longer part.
 template <int G>
-__global__ __launch_bounds__(1024) void kq_mi8_moe_prep_kernel(MoeGroupArg ga, const float* x,
+__global__ __launch_bounds__(256) void kq_mi8_moe_prep_kernel(MoeGroupArg ga, const float* x,
                                                                int K, int B, int bpad, int8_t* xq,
                                                                uint8_t* cf, uint8_t* zp,
                                                                float2* sm) {
@@ -3551,7 +3559,7 @@ __global__ __launch_bounds__(1024) void kq_mi8_moe_prep_kernel(MoeGroupArg ga, c
         moe_group_body(ga, lds_i);
         return;
     }
-    mi8_prep_one<G>((long)(blockIdx.x - 1) * 1024 + threadIdx.x, x, (long)K, K, B, bpad, xq, cf,
+    mi8_prep_one<G>((long)(blockIdx.x - 1) * 256 + threadIdx.x, x, (long)K, K, B, bpad, xq, cf,
                     zp, sm);
 }
 
@@ -5180,12 +5188,12 @@ int kqk_launch_mi8_moe(int type, const int* sel, int nm, int E, int nt, int x_di
     ga.groups = static_cast<MxGroup*>(groups);
     ga.ng = ng;
     const size_t glds = (size_t)(((2 * E + 3) & ~3) + 4 * ((nm + 3) / 4)) * sizeof(int);
-    const dim3 pg((unsigned)(1 + (gq + 1023) / 1024));
+    const dim3 pg((unsigned)(1 + (gq + 255) / 256));
     if (G == 32)
-        hipLaunchKernelGGL(kq_mi8_moe_prep_kernel<32>, pg, dim3(1024), glds, st, ga, x, K, nx, bpad,
+        hipLaunchKernelGGL(kq_mi8_moe_prep_kernel<32>, pg, dim3(256), glds, st, ga, x, K, nx, bpad,
                            xq, cf, zp, sm);
     else
-        hipLaunchKernelGGL(kq_mi8_moe_prep_kernel<16>, pg, dim3(1024), glds, st, ga, x, K, nx, bpad,
+        hipLaunchKernelGGL(kq_mi8_moe_prep_kernel<16>, pg, dim3(256), glds, st, ga, x, K, nx, bpad,
                            xq, cf, zp, sm);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
