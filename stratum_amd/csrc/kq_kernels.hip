@@ -5153,7 +5153,7 @@ long kqk_mi8_moe_workspace(int type, int nx, int K) {
 int kqk_launch_mi8_moe(int type, const int* sel, int nm, int E, int nt, int x_div,
                        const void* w0, const void* w1, float* y0, float* y1, long estride,
                        const float* x, int K, void* groups, int* ng, int ngmax, int N,
-                       void* ws, hipStream_t st) {
+                       void* ws, int n_cu, hipStream_t st) {
     const int nx = x_div > 0 ? nm / x_div : 0;
     const long y_stride = N;
     if (nm < 1 || E < 1 || E > 4096 || nt < 1 || nt > 2 || x_div < 1 || nm % x_div)
@@ -5161,10 +5161,14 @@ int kqk_launch_mi8_moe(int type, const int* sel, int nm, int E, int nt, int x_di
     long cf_off = 0, sm_off = 0, zp_off = 0;
     const long wsb = mi8_moe_layout(type, nx, K, &cf_off, &sm_off, &zp_off);
     const int ks = kqk_mi8_parts(K);
-    // several row blocks per workgroup when the row is one K-part: a run's
-    // workgroup then streams one weight sequence instead of paying a
-    // launch-to-first-load latency per 16 rows
-    const int rbw = ks == 1 ? KQ_MI8_RBW : 1;
+    // several row blocks per workgroup when the row is one K-part and the
+    // runs' workgroups outnumber what the GPU holds at once (one wave each,
+    // four per SIMD): a workgroup then streams one weight sequence instead
+    // of paying a launch-to-first-load latency per 16 rows.  When they all
+    // fit (few members), the launch lasts one wave's chain of super-blocks,
+    // and one row block per workgroup halves it.
+    const long fit = (long)nt * (E < nm ? E : nm) * ((N + 15) / 16);
+    const int rbw = ks != 1 ? 1 : fit <= 16L * (n_cu > 0 ? n_cu : 256) ? 1 : KQ_MI8_RBW;
     const long tl = 16L * rbw * (K >> 6) * 8;    // a single member's chunk terms
     if (wsb < 0 || nx < 1 || N < 1 || ngmax < 1 || ngmax > 65535 || y_stride < N || !groups ||
         !ng || ((uintptr_t)x & 15) || ((uintptr_t)ws & 15) || tl > 65536)

@@ -107,7 +107,7 @@ long kqk_mi8_moe_workspace(int type, int nx, int K);
 int kqk_launch_mi8_moe(int type, const int* sel, int nm, int E, int nt, int x_div,
                        const void* w0, const void* w1, float* y0, float* y1, long estride,
                        const float* x, int K, void* groups, int* ng, int ngmax, int N,
-                       void* ws, hipStream_t st);
+                       void* ws, int n_cu, hipStream_t st);
 int kqk_launch_moe_group(const int* sel, int nm, int E, int nt, int x_div, int mch,
                          const void* w0, const void* w1, float* y0, float* y1, long estride,
                          void* groups, int* ng, hipStream_t st);

@@ -1244,7 +1244,7 @@ static int moe_i8_batch(const kq_moe_op* op, const int* sel, int B, int k, int E
     int* ng = (int*)(base + xwa + (size_t)ngmax * (size_t)kqk_mx_group_bytes());
     const int e = kqk_launch_mi8_moe(op->type, sel, nm, E, nt, op->x_div, op->w[0], op->w[nt - 1],
                                      op->y[0], op->y[nt - 1], (long)op->expert_stride, op->x, K,
-                                     groups, ng, ngmax, op->n_out, base, st);
+                                     groups, ng, ngmax, op->n_out, base, g_kq.n_cu, st);
     if (e) return kq_fail("int8 moe launch: %s", hipGetErrorString((hipError_t)e));
     return 0;
 }
