@@ -3489,6 +3489,7 @@ struct Mi8Arg {
     int zrow;
     int rbw;                  // 16-row blocks per workgroup (1 unless KS = 1)
     const float2* sm;         // grouped: {scale, sum} per (row, group)
+    int pack2;                // grouped Q4_K: runs of two members on the VALU
 };
 
 // x -> int8 per group (the single-stream rule, kq_quantize_kernel's) and
@@ -3638,6 +3639,91 @@ __device__ __forceinline__ void mi8_single(const Mi8Arg& A, const uint8_t* w, in
     }
 }
 
+// A Q4_K run of two members in a grouped launch (KS = 1): the same values as
+// the matrix-core form below (st_linear_multix's pack arithmetic), on the
+// VALU.  Each lane takes one (row, member) of rows r0 .. r0 + 16 nrw - 1
+// and walks the row's 64-weight chunks in order: the exact 4-bit x int8
+// dots of the two sub-blocks (sdot4), then per sub-block the binary32 term
+// fl(fl(d*sc) * fl(fl(L) * scl)) - fl(fl(dmin*m) * fl(fl(S)*scl)) added to
+// the lane's binary64 sum, in element order.  The matrix-core form leaves
+// three of its four lane groups on empty member slots for two members
+// (their epilogue instructions run anyway); here every lane's term is a
+// member's.  The two members' quantized rows and coefficients are staged in
+// LDS (2.5 K bytes), read by the lanes as broadcasts.
+__device__ __forceinline__ void mi8_pack2_q4k(const Mi8Arg& A, const MxGroup* gp, int rb0,
+                                              int nrw, uint8_t* lds, int tid) {
+    const int N = A.N, K = A.K, nb = K >> 8, ng = K >> 5;
+    const int xr[2] = {gp->xi[0], gp->xi[1]};
+    uint4* xs = reinterpret_cast<uint4*>(lds);                     // [2][K] int8
+    float4* cs = reinterpret_cast<float4*>(lds + 2 * (size_t)K);   // [2][K/64] {c0, c1}
+    const int s = tid & 1, rl = tid >> 1;
+    const int r = rb0 * 16 + rl;
+    const bool live = rl < 16 * nrw && r < N;
+    const wptr row = to_global(gp->w) + (size_t)min(r, N - 1) * (size_t)nb * 144;
+    // half a super-block per step (its header and 64 quant bytes: two
+    // chunks), the next half's loads issued before this one's terms
+    struct In { uint4 hd, q[4]; };
+    auto ld = [&](int hs, In& in) {
+        const int h = min(hs, 2 * nb - 1);
+        const wptr blk = row + (size_t)(h >> 1) * 144;
+        in.hd = ld16(blk);
+#pragma unroll
+        for (int i = 0; i < 4; i++) in.q[i] = ld16(blk + 16 + 64 * (h & 1) + 16 * i);
+    };
+    // the first half super-block's weights go out before the x staging,
+    // which does not hold them up
+    In a, b;
+    ld(0, a);
+    const int xq16 = K >> 4, nc2 = ng >> 1;
+    for (int i = tid; i < 2 * xq16; i += 64) {
+        const int m = i >= xq16, o = i - m * xq16;
+        xs[i] = reinterpret_cast<const uint4*>(A.xq + (size_t)xr[m] * K)[o];
+    }
+    for (int i = tid; i < 2 * nc2; i += 64) {
+        const int m = i >= nc2, o = i - m * nc2;
+        cs[i] = reinterpret_cast<const float4*>(A.cf + (size_t)xr[m] * ng * 8)[o];
+    }
+    __syncthreads();
+    const uint4* xm = xs + (size_t)s * xq16;
+    const float4* cm = cs + (size_t)s * nc2;
+    double acc = 0.0;
+    auto step = [&](int hs, const In& in) {
+        const float d = f16_bits_to_f32(in.hd.x & 0xffffu);
+        const float dmin = f16_bits_to_f32(in.hd.x >> 16);
+#pragma unroll
+        for (int jj = 0; jj < 2; jj++) {
+            const int j = 2 * (hs & 1) + jj, c = 2 * hs + jj;
+            uint32_t sc1, mn1, sc2, mn2;
+            scale_min_pair(in.hd.y, in.hd.z, in.hd.w, j, sc1, mn1, sc2, mn2);
+            const float4 dm = make_float4(d * (float)sc1, dmin * (float)mn1, d * (float)sc2,
+                                          dmin * (float)mn2);
+            const uint4 q0 = in.q[2 * jj], q1 = in.q[2 * jj + 1];
+            const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+            const uint4 x0 = xm[4 * c], x1 = xm[4 * c + 1], x2 = xm[4 * c + 2], x3 = xm[4 * c + 3];
+            const uint32_t xl[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            const uint32_t xh[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+            int L = 0, H = 0;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                L = __builtin_amdgcn_sdot4((int)(q[k] & 0x0f0f0f0fu), (int)xl[k], L, false);
+                H = __builtin_amdgcn_sdot4((int)((q[k] >> 4) & 0x0f0f0f0fu), (int)xh[k], H, false);
+            }
+            const float4 cf = cm[c];
+            const float tl = dm.x * ((float)L * cf.x) - dm.y * cf.y;
+            acc = acc + (double)tl;
+            const float th = dm.z * ((float)H * cf.z) - dm.w * cf.w;
+            acc = acc + (double)th;
+        }
+    };
+    for (int hs = 0; hs < 2 * nb; hs += 2) {
+        ld(hs + 1, b);
+        step(hs, a);
+        ld(hs + 2, a);
+        step(hs + 1, b);
+    }
+    if (live) gp->y[(size_t)gp->yi[s] * A.y_stride + r] = (float)acc;
+}
+
 // Weight registers of one super-block of one lane's row.
 //  Q4_K: the header and, of each chunk's 32 quant bytes, the half lane
 //    group q reads (16 (q & 1) ..).
@@ -3712,6 +3798,13 @@ __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
         mi8_single<TYPE>(A, wbase, gp->xi[0], gp->y + (size_t)gp->yi[0] * A.y_stride, rb0, nrw,
                          mi8_terms, tid, 64 * KS);
         return;
+    }
+    if constexpr (GR && Q4 && KS == 1) {
+        if (M == 2 && A.pack2) {                  // uniform
+            extern __shared__ __align__(16) double mi8_terms[];
+            mi8_pack2_q4k(A, gp, rb0, nrw, reinterpret_cast<uint8_t*>(mi8_terms), tid);
+            return;
+        }
     }
     // this lane's weight row in row block rb0 + i
     auto wrow = [&](int i) -> wptr {
@@ -5084,7 +5177,7 @@ int kqk_launch_mi8(int type, const float* xs, long x_stride, const void* w, floa
     a.y = ys;
     a.y_stride = y_stride;
     a.N = N; a.K = K; a.B = B;
-    a.groups = nullptr; a.ng = nullptr; a.zrow = 0; a.rbw = 1; a.sm = nullptr;
+    a.groups = nullptr; a.ng = nullptr; a.zrow = 0; a.rbw = 1; a.sm = nullptr; a.pack2 = 0;
     // Q4_K: 8 or 16 streams per wave; Q6_K: 8 (its A operands take
     // 16 registers per MFMA and super-block)
     // (8 streams per wave up to B = 8, one super-block in flight; measured
@@ -5169,7 +5262,15 @@ int kqk_launch_mi8_moe(int type, const int* sel, int nm, int E, int nt, int x_di
     // and one row block per workgroup halves it.
     const long fit = (long)nt * (E < nm ? E : nm) * ((N + 15) / 16);
     const int rbw = ks != 1 ? 1 : fit <= 16L * (n_cu > 0 ? n_cu : 256) ? 1 : KQ_MI8_RBW;
-    const long tl = 16L * rbw * (K >> 6) * 8;    // a single member's chunk terms
+    // runs of two Q4_K members on the VALU (mi8_pack2_q4k) when a workgroup
+    // has two row blocks, so that its 64 lanes are 32 rows x 2 members (with
+    // one row block half of them would idle: slower than the matrix-core
+    // form at configs[4] B = 4)
+    const int pack2 = type == T_Q4K_I8 && ks == 1 && rbw == 2;
+    // a single member's chunk terms; with pack2 also a run of two members'
+    // quantized rows and coefficients
+    long tl = 16L * rbw * (K >> 6) * 8;
+    if (pack2 && tl < 2L * K + K / 2) tl = 2L * K + K / 2;
     if (wsb < 0 || nx < 1 || N < 1 || ngmax < 1 || ngmax > 65535 || y_stride < N || !groups ||
         !ng || ((uintptr_t)x & 15) || ((uintptr_t)ws & 15) || tl > 65536)
         return (int)hipErrorInvalidValue;
@@ -5212,6 +5313,7 @@ int kqk_launch_mi8_moe(int type, const int* sel, int nm, int E, int nt, int x_di
     a.zrow = nx;
     a.rbw = rbw;
     a.sm = sm;
+    a.pack2 = pack2;
     const int nrb = ((N + 15) / 16 + rbw - 1) / rbw;
 #define KQ_MI8G_GO(T_, P_, K_)                                                               \
     hipLaunchKernelGGL((kq_mi8_kernel<T_, 8, P_, K_, true>), dim3((unsigned)nrb,             \
