@@ -3756,8 +3756,12 @@ struct Mi8W6 { uint32_t l[4][5], h[4][5], s[5]; uint32_t d, sh; };
 // call on that expert's slice would.  A run of one member takes the
 // single-stream path (mi8_single): the member equals its
 // kq_gemv_dev(type | KQ_INT8_ACT) result bit for bit.
+// (Q4_K: four waves per SIMD asked of the register allocator, which the
+// 16-stream forms reach with the A operands and coefficients out of the ring;
+// Q6_K reaches three by itself, and asking for them makes it spill)
 template <int TYPE, int SW, int P, int KS, bool GR>
-__global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
+__global__ __launch_bounds__(64 * KS) __attribute__((amdgpu_waves_per_eu(TYPE == T_Q4K_I8 ? 4 : 1)))
+void kq_mi8_kernel(Mi8Arg A) {
     constexpr bool Q4 = TYPE == T_Q4K_I8;
     constexpr int NM = Q4 ? SW / 8 : SW / 4;        // MFMAs per chunk
     constexpr int NACC = Q4 ? 2 * NM : NM;          // binary64 sums per lane
@@ -3832,7 +3836,30 @@ __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
 #pragma unroll
     for (int k = 0; k < CPT; k++) crow[k] = xrow(min(lane + 64 * k, CU - 1) / CPS);
 
-    struct Slot { W w; i32x4 a[4][NM]; uint4 c[CPT]; };
+    struct Slot { W w; };
+    // the A operands (this lane's x bytes, or the zero page) and the
+    // coefficients of super-block b: loaded at the step that uses them, not
+    // through the ring (they come from L2, and keeping them out of the
+    // ring's slots saves 2 x (4 x 4 NM + 4 CPT) registers a lane)
+    auto loada = [&](int b, i32x4 (&av)[4][NM], uint4 (&cv)[CPT]) {
+        const int bb = min(b, nb - 1);
+#pragma unroll
+        for (int k = 0; k < CPT; k++) {
+            const int v = min(lane + 64 * k, CU - 1);
+            cv[k] = *reinterpret_cast<const uint4*>(
+                cf + ((size_t)crow[k] * ng + (size_t)bb * (CB / 8)) * 8 + 16 * (v % CPS));
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int m = 0; m < NM; m++) {
+                // chunk j's positions of this lane: Q4_K 64j + 16q; Q6_K run
+                // q of chunk (h, is) at 128h + 32q + 16is
+                const int qo = Q4 ? 64 * j + 16 * q : 128 * (j >> 1) + 32 * q + 16 * (j & 1);
+                const uint8_t* src = on ? xa[m] + 256 * (size_t)bb + qo : zp;
+                av[j][m] = *reinterpret_cast<const i32x4*>(src);
+            }
+    };
     auto load = [&](int i, int b, Slot& sl) {
         const wptr blk = wrow(i) + (size_t)b * BB;
         if constexpr (Q4) {
@@ -3855,22 +3882,6 @@ __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
             sl.w.s[2] = ld4(b4 + 200); sl.w.s[3] = ld4(b4 + 204);
             sl.w.s[4] = ld4(b4 + (mis ? 208 : 204));
             sl.w.d = ld2(blk + 208);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-#pragma unroll
-            for (int m = 0; m < NM; m++) {
-                // chunk j's positions of this lane: Q4_K 64j + 16q; Q6_K run
-                // q of chunk (h, is) at 128h + 32q + 16is
-                const int qo = Q4 ? 64 * j + 16 * q : 128 * (j >> 1) + 32 * q + 16 * (j & 1);
-                const uint8_t* src = on ? xa[m] + 256 * (size_t)b + qo : zp;
-                sl.a[j][m] = *reinterpret_cast<const i32x4*>(src);
-            }
-#pragma unroll
-        for (int k = 0; k < CPT; k++) {
-            const int v = min(lane + 64 * k, CU - 1);
-            sl.c[k] = *reinterpret_cast<const uint4*>(
-                cf + ((size_t)crow[k] * ng + (size_t)b * (CB / 8)) * 8 + 16 * (v % CPS));
         }
     };
     double acc[NACC];
@@ -3918,8 +3929,11 @@ __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
             const bool go = i0 + p < nst && b < kb1;               // uniform
             const bool last = KS == 1 && go && b == nb - 1;        // a row block's end
             if (++cb == kb0 + nbp) { cb = kb0; ci++; }
-            // the next loads go out first: waiting for this step's slot
-            // then leaves them in flight
+            // this step's A operands, then the next slot's loads: waiting
+            // for this step's data then leaves the latter in flight
+            i32x4 av[4][NM];
+            uint4 cv[CPT];
+            loada(b, av, cv);
             load(min(li, nrw - 1), min(lb, nb - 1), ring[(p + P) % R]);
             if (++lb == kb0 + nbp) { lb = kb0; li++; }
             if (go) {
@@ -3929,7 +3943,7 @@ __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
 #pragma unroll
                 for (int k = 0; k < CPT; k++) {
                     const int v = min(lane + 64 * k, CU - 1);
-                    *reinterpret_cast<uint4*>(wl + CB * (v / CPS) + 16 * (v % CPS)) = cur.c[k];
+                    *reinterpret_cast<uint4*>(wl + CB * (v / CPS) + 16 * (v % CPS)) = cv[k];
                 }
                 if constexpr (Q4) {
                     // lane group q decodes chunk q of its row: d*sc, dmin*m of
@@ -3956,7 +3970,7 @@ __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
                                        (int)((qv.w >> sh) & 0x0f0f0f0fu)};
 #pragma unroll
                     for (int m = 0; m < NM; m++) {
-                        const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.a[j][m], bop, zero,
+                        const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[j][m], bop, zero,
                                                                               0, 0, 0);
                         // D[2e + sb]: stream 8m + 2q + e, sub-block sb
 #pragma unroll
@@ -4001,7 +4015,7 @@ __global__ __launch_bounds__(64 * KS) void kq_mi8_kernel(Mi8Arg A) {
                     const i32x4 bop = {(int)bw[0], (int)bw[1], (int)bw[2], (int)bw[3]};
 #pragma unroll
                     for (int m = 0; m < NM; m++) {
-                        const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.a[u][m], bop, zero,
+                        const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[u][m], bop, zero,
                                                                               0, 0, 0);
                         // D[t]: stream 4m + q, run t
                         const double* cs = reinterpret_cast<const double*>(wl + 128 * (4 * m + q));
