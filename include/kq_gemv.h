@@ -166,9 +166,11 @@ int kq_q4k_group(const float* x, int K,
  * For a device-resident decode loop: all pointers are device pointers,
  * the call only enqueues work on `stream` (asynchronous).  x and xs must
  * be 16-byte aligned.  The MoE batch and matrix-core entries use scratch
- * buffers owned by the library, one set per stream (up to 16 streams; a
- * seventeenth returns -1), grown on demand: calls on different streams may
- * overlap in time, calls on one stream are ordered. */
+ * buffers owned by the library, one set per stream, grown on demand: calls
+ * on different streams may overlap in time, calls on one stream are
+ * ordered.  The library keeps 16 sets; a seventeenth stream takes the least
+ * recently used stream's set, freeing its buffers first (hipFree, which
+ * waits for the device). */
 
 /* The int8 quantizer of the int8-activation mode on its own: group 32 is
  * q4k_quantize_x_q8 (+ q4k_sum_i8_32 sums, stratum_q4k_neon.h:229-275,

@@ -33,6 +33,7 @@
 typedef struct {
     hipStream_t st;
     int used;
+    unsigned long long last;   /* the call count at its last use */
     float* moe; size_t cap_moe;
     uint8_t* mf; size_t cap_mf;
 } kq_scr;
@@ -59,6 +60,7 @@ typedef struct {
     float* d_y; size_t cap_y;
     float* d_a; size_t cap_a;
     kq_scr scr[KQ_SCR_SLOTS];       /* the device entries' scratch, per stream */
+    unsigned long long scr_calls;   /* scr_of calls, for the least recently used */
     size_t mf_reserve;              /* kq_reserve_mfma_workspace: least mf size */
     /* launch overrides from the environment (0: unset), read by kq_ready
      * and again only by kq_tuning_reload: the planner runs on every call */
@@ -84,20 +86,33 @@ const char* kq_last_error(void) { return g_kq.err; }
 
 /* The scratch of the device entries that stream `st` runs on: calls on
  * different streams get different buffers (they may overlap in time),
- * calls on one stream are ordered.  NULL (message set) past
- * KQ_SCR_SLOTS streams. */
+ * calls on one stream are ordered.  A stream first seen when all
+ * KQ_SCR_SLOTS sets are taken gets the least recently used one, whose
+ * buffers are freed first (hipFree waits for the device, so no launch
+ * still reads them). */
 static kq_scr* scr_of(hipStream_t st) {
+    const unsigned long long now = ++g_kq.scr_calls;
     for (int i = 0; i < KQ_SCR_SLOTS; i++)
-        if (g_kq.scr[i].used && g_kq.scr[i].st == st) return &g_kq.scr[i];
-    for (int i = 0; i < KQ_SCR_SLOTS; i++)
-        if (!g_kq.scr[i].used) {
-            g_kq.scr[i].used = 1;
-            g_kq.scr[i].st = st;
+        if (g_kq.scr[i].used && g_kq.scr[i].st == st) {
+            g_kq.scr[i].last = now;
             return &g_kq.scr[i];
         }
-    kq_fail("device entries used on more than %d streams: the library keeps scratch for "
-            "at most %d", KQ_SCR_SLOTS, KQ_SCR_SLOTS);
-    return NULL;
+    int pick = -1;
+    for (int i = 0; i < KQ_SCR_SLOTS && pick < 0; i++)
+        if (!g_kq.scr[i].used) pick = i;
+    if (pick < 0) {
+        pick = 0;
+        for (int i = 1; i < KQ_SCR_SLOTS; i++)
+            if (g_kq.scr[i].last < g_kq.scr[pick].last) pick = i;
+        kq_scr* v = &g_kq.scr[pick];
+        if (v->moe) (void)hipFree(v->moe);
+        if (v->mf) (void)hipFree(v->mf);
+        memset(v, 0, sizeof *v);
+    }
+    g_kq.scr[pick].used = 1;
+    g_kq.scr[pick].st = st;
+    g_kq.scr[pick].last = now;
+    return &g_kq.scr[pick];
 }
 
 /* the types with an int8-activation (SDOT) form: st_linear_q4k, _q6k,

@@ -79,3 +79,36 @@ def test_scratch_entries_on_two_streams():
         for name, t, want in zip(("mfma", "int8 multix", "int8 moe"), o, alone[i]):
             assert np.array_equal(t.cpu().numpy().view(np.uint32), want), (name, i)
     assert L.kq_scratch_bytes() > held
+
+
+def test_more_streams_than_scratch_sets():
+    """Eighteen streams in turn through the matrix-core MULTISEQ entry: the
+    library keeps 16 scratch sets, so the seventeenth and eighteenth streams
+    take the least recently used sets (freed first); every call still gives
+    the default stream's bits, and the scratch held stays bounded."""
+    L = K.lib()
+    N, Kd, B = 256, 1024, 16
+    w = dev(synth.tensor(12, N, Kd, 9710))
+    r = synth.rng(9711)
+    x = dev(np.stack([synth.gaussian(r, Kd) for _ in range(B)]).reshape(-1))
+    want = torch.empty(B * N, device="cuda")
+    K.gemv_multix_mfma_dev(12, w.data_ptr(), x.data_ptr(), want.data_ptr(), B, N, Kd,
+                           stream=torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    want = want.cpu().numpy().view(np.uint32)
+    streams = [torch.cuda.Stream() for _ in range(18)]
+    print("eighteen streams, matrix-core multix", flush=True)
+    held = []
+    for rnd in range(2):
+        for i, s in enumerate(streams):
+            with torch.cuda.stream(s):
+                y = torch.full((B * N,), float("nan"), device="cuda")
+            K.gemv_multix_mfma_dev(12, w.data_ptr(), x.data_ptr(), y.data_ptr(), B, N, Kd,
+                                   stream=s.cuda_stream)
+            s.synchronize()
+            assert np.array_equal(y.cpu().numpy().view(np.uint32), want), (rnd, i)
+            held.append(L.kq_scratch_bytes())
+    # after the first round the 16 sets are the last 16 streams' (whatever
+    # earlier tests left): the second round only reassigns them, each one
+    # freed and taken again at the same size
+    assert all(h == held[17] for h in held[18:]), held
