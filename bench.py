@@ -599,10 +599,30 @@ def cfg5(L, torch, stream, host_w) -> dict:
                                        sel.data_ptr(), selw.data_ptr(), work.data_ptr(), wbytes,
                                        sh))
         fus = _events_us(torch, stream, ffn_step, 2 * MOE_SETS * NCOPY)
+        # the same step in the int8-activation mode (the reference's default
+        # arithmetic, use_sdot: expert GEMVs as Q4_K | KQ_INT8_ACT)
+        ffns8 = []
+        for f in ffns:
+            f8 = KQ.KqMoeFfn.from_buffer_copy(f)
+            f8.gate_type = f8.up_type = f8.down_type = 12 | KQ.INT8_ACT
+            ffns8.append(f8)
+        wbytes8 = KQ.moe_ffn_workspace_bytes(ffns8[0], B)
+        work8 = torch.empty(wbytes8, dtype=torch.uint8, device="cuda")
+
+        def ffn_step8(i):
+            j = i % MOE_SETS
+            _check(L, L.kq_moe_ffn_dev(ctypes.byref(ffns8[(i // MOE_SETS) % NCOPY]),
+                                       xm.data_ptr() + 4 * j * B * H, xres.data_ptr(), B,
+                                       sel.data_ptr(), selw.data_ptr(), work8.data_ptr(), wbytes8,
+                                       sh))
+        fus8 = _events_us(torch, stream, ffn_step8, 2 * MOE_SETS * NCOPY)
         res[f"B{B}"]["ffn_step"] = {
             "us_per_layer": round(fus, 2),
+            "int8_us_per_layer": round(fus8, 2),
             "what": "router GEMV (F32 128x2048), softmax, routed gate+up, SwiGLU, down, "
-                    f"combine + residual; {MOE_SETS} normed inputs x {NCOPY} weight copies"}
+                    f"combine + residual; {MOE_SETS} normed inputs x {NCOPY} weight copies; "
+                    "int8: the same step with the expert GEMVs as Q4_K | KQ_INT8_ACT"}
+        del work8
         del work, router
         if CPU["on"]:
             impl, kind = cpu_impl(12)

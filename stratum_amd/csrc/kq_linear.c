@@ -156,6 +156,14 @@ static int is_core(int type) {
            type == KQ_TYPE_Q2K_NIB;
 }
 
+/* the types the batch-1 three-launch FFN step takes: the four above and
+ * the int8 mode of Q4_K and Q6_K (moe_forward_one_token's per-slice
+ * st_linear_dispatch under use_sdot: the single-stream int8 forms, which
+ * the gather kernel's int8 instantiations compute) */
+static int is_ffn_b1(int type) {
+    return is_core(type) || is_i8mx(type);
+}
+
 /* the types the multi-x (MULTISEQ, MoE batch) kernel covers: every block
  * type, and the int8 mode of Q5_K, Q3_K and Q8_0 (whose batches are per
  * stream in the reference, so every member takes the single-stream int8
@@ -1484,12 +1492,12 @@ int kq_moe_ffn_dev(const kq_moe_ffn* f, const float* xn, float* x, int B, int* s
      * residual in its epilogue.  The same arithmetic as the six-launch form
      * below (the tests hold the two bit-identical; KQ_MOE_FFN_SPLIT=1 forces
      * that form).  Needs one gate+up segment (2k <= KQ_MAX_GROUPS), E <= 256
-     * (every logit in a lane), a core down type, n_ff and n_embed multiples
+     * (every logit in a lane), types of is_ffn_b1, n_ff and n_embed multiples
      * of the grid (a workgroup then holds a rank's gate and up row, and all
      * k ranks' down rows, of the same index), and the fused epilogues'
      * room (ffn_fused_fits). */
-    if (B == 1 && pair && 2 * k <= KQ_MAX_GROUPS && E <= 256 && is_core(f->gate_type) &&
-        is_core(f->down_type) && !g_kq.env_ffn_split && ffn_fused_fits(f)) {
+    if (B == 1 && pair && 2 * k <= KQ_MAX_GROUPS && E <= 256 && is_ffn_b1(f->gate_type) &&
+        is_ffn_b1(f->down_type) && !g_kq.env_ffn_split && ffn_fused_fits(f)) {
         if (kq_gemv_dev(f->router_type, f->router, xn, NULL, probs, E, H, stream)) return -1;
         kq_moe_op gu;
         memset(&gu, 0, sizeof gu);

@@ -264,7 +264,8 @@ def test_moe_ffn_step_config(port, B, kq_env):
     assert err <= 1e-4 * contrib
 
 
-@pytest.mark.parametrize("case", ["config", "q6k_down", "parts16", "grid37", "e512", "wide_ff"])
+@pytest.mark.parametrize("case", ["config", "q6k_down", "parts16", "grid37", "e512", "wide_ff",
+                                  "config_i8", "q6k_down_i8"])
 def test_moe_ffn_fused_matches_split(port, case, kq_env):
     """Batch 1 in three launches (softmax and top-k inside the gate+up
     launch and SwiGLU in its epilogue; the rank-ordered combine plus residual
@@ -274,28 +275,38 @@ def test_moe_ffn_fused_matches_split(port, case, kq_env):
     more than 256 logits) and wide_ff (n_ff 32x n_embed: a workgroup's gate
     and up outputs overflow the x region the fused epilogue keeps them in)
     take the six-launch form inside kq_moe_ffn_dev and must give the same
-    bits too; kq_moe_ffn_last_path tells which form ran."""
+    bits too; kq_moe_ffn_last_path tells which form ran.  The _i8 cases
+    take the experts in the int8-activation mode (Q4_K / Q6_K | KQ_INT8_ACT),
+    whose batch-1 step also runs in three launches; their values against
+    the oracle's int8 forms are test_moe_ffn_step_int8's."""
+    i8 = case.endswith("_i8")
+    base = case[:-3] if i8 else case
     H, F, E, k = {"config": (2048, 768, 128, 8), "q6k_down": (1024, 512, 64, 4),
                   "parts16": (1024, 256, 32, 8), "grid37": (2048, 768, 128, 8),
-                  "e512": (1024, 256, 512, 4), "wide_ff": (256, 8192, 16, 8)}[case]
+                  "e512": (1024, 256, 512, 4), "wide_ff": (256, 8192, 16, 8)}[base]
     d = make_layer(H, F, E, k, 9700)
-    if case == "q6k_down":
+    if base == "q6k_down":
         d["down_type"] = 14
         d["down"] = synth.tensor(14, E * H, F, 9704)
         d["down_stride"] = H * synth.row_bytes(14, F)
+    if i8:
+        for n in ("gate_type", "up_type", "down_type"):
+            d[n] |= K.INT8_ACT
     r = synth.rng(9701)
     xn, x0 = synth.gaussian(r, H), synth.gaussian(r, H)
     if case == "grid37":
         kq_env(KQ_GRID=37)
     print(f"moe ffn fused vs split: {case}", flush=True)
     fused = run_step(d, xn, x0, 1)
-    want_fused = case in ("config", "q6k_down", "parts16")
+    want_fused = base in ("config", "q6k_down", "parts16")
     assert bool(fused["path"] & K.FFN_FUSED_B1) == want_fused, fused["path"]
     kq_env(KQ_MOE_FFN_SPLIT=1)
     split = run_step(d, xn, x0, 1)
     assert not split["path"] & K.FFN_FUSED_B1
     for n in ("sel", "selw", "act", "x"):
         assert same_values(fused[n], split[n]), n
+    if i8:
+        return
     full = port.moe_ffn(d, xn, x0, 1)
     assert np.array_equal(full["sel"], fused["sel"])
     contrib = np.abs(full["x"] - x0).max()
@@ -429,19 +440,27 @@ def test_moe_ffn_step_int8(port, qtype, B):
         p = got["probs"][s * E:(s + 1) * E]
         sel, selw = port.topk(p, k)
         assert list(got["sel"][s * k:(s + 1) * k]) == sel, s
-    g, u = got["g"].reshape(B * k, F), got["u"].reshape(B * k, F)
-    a, o = got["act"].reshape(B * k, F), got["ffo"].reshape(B * k, H)
-    for m in range(B * k):
-        assert ulps(a[m], port.swiglu(g[m], u[m])).max() <= 4.0
+    # batch 1 runs in three launches (SwiGLU and the combine in the GEMV
+    # epilogues), which write no gate, up or per-member down outputs: those
+    # are then the tickets' own calls, and act and x are checked against them
+    fused = bool(got["path"] & K.FFN_FUSED_B1)
+    assert fused == (B == 1), got["path"]
+    a = got["act"].reshape(B * k, F)
     xr = xn.reshape(B, H)
+    g, u, o = (np.full((B * k, n), np.nan, np.float32) for n in (F, F, H))
     for e, mem in O.moe_tickets(got["sel"], E):
         xs = np.stack([xr[m // k] for m in mem])
-        assert same_values(g[mem], ticket(d["gate"][e * F * rb_in:(e + 1) * F * rb_in], xs, F, H))
-        assert same_values(u[mem], ticket(d["up"][e * F * rb_in:(e + 1) * F * rb_in], xs, F, H))
-        assert same_values(o[mem], ticket(d["down"][e * H * rb_ff:(e + 1) * H * rb_ff], a[mem], H,
-                                          F))
-    assert same_values(got["x"], port.moe_combine(got["ffo"], got["sel"], got["selw"], x0, B, k,
-                                                  H))
+        g[mem] = ticket(d["gate"][e * F * rb_in:(e + 1) * F * rb_in], xs, F, H)
+        u[mem] = ticket(d["up"][e * F * rb_in:(e + 1) * F * rb_in], xs, F, H)
+        o[mem] = ticket(d["down"][e * H * rb_ff:(e + 1) * H * rb_ff], a[mem], H, F)
+    if not fused:
+        assert same_values(got["g"].reshape(B * k, F), g)
+        assert same_values(got["u"].reshape(B * k, F), u)
+        assert same_values(got["ffo"].reshape(B * k, H), o)
+    for m in range(B * k):
+        assert ulps(a[m], port.swiglu(g[m], u[m])).max() <= 4.0
+    assert same_values(got["x"], port.moe_combine(o.reshape(-1), got["sel"], got["selw"], x0, B,
+                                                  k, H))
 
 
 def test_moe_ffn_step_f16_router_mixed_types(port):
