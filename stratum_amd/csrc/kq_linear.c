@@ -156,12 +156,15 @@ static int is_core(int type) {
            type == KQ_TYPE_Q2K_NIB;
 }
 
-/* the types the batch-1 three-launch FFN step takes: the four above and
- * the int8 mode of Q4_K and Q6_K (moe_forward_one_token's per-slice
+/* the types the batch-1 three-launch FFN step takes: every block type of
+ * the gather kernel (the four above, Q5_K, Q3_K, Q8_0) and the int8 mode
+ * of the five SDOT types (moe_forward_one_token's per-slice
  * st_linear_dispatch under use_sdot: the single-stream int8 forms, which
  * the gather kernel's int8 instantiations compute) */
 static int is_ffn_b1(int type) {
-    return is_core(type) || is_i8mx(type);
+    const int t = type & ~KQ_INT8_ACT;
+    if (type & KQ_INT8_ACT) return has_sdot(t);
+    return is_core(t) || t == KQ_TYPE_Q5_K || t == KQ_TYPE_Q3_K || t == KQ_TYPE_Q8_0;
 }
 
 /* the types the multi-x (MULTISEQ, MoE batch) kernel covers: every block

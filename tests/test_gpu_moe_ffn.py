@@ -265,7 +265,7 @@ def test_moe_ffn_step_config(port, B, kq_env):
 
 
 @pytest.mark.parametrize("case", ["config", "q6k_down", "parts16", "grid37", "e512", "wide_ff",
-                                  "config_i8", "q6k_down_i8"])
+                                  "config_i8", "q6k_down_i8", "q5k", "q3k_i8", "q80_i8"])
 def test_moe_ffn_fused_matches_split(port, case, kq_env):
     """Batch 1 in three launches (softmax and top-k inside the gate+up
     launch and SwiGLU in its epilogue; the rank-ordered combine plus residual
@@ -275,16 +275,20 @@ def test_moe_ffn_fused_matches_split(port, case, kq_env):
     more than 256 logits) and wide_ff (n_ff 32x n_embed: a workgroup's gate
     and up outputs overflow the x region the fused epilogue keeps them in)
     take the six-launch form inside kq_moe_ffn_dev and must give the same
-    bits too; kq_moe_ffn_last_path tells which form ran.  The _i8 cases
-    take the experts in the int8-activation mode (Q4_K / Q6_K | KQ_INT8_ACT),
-    whose batch-1 step also runs in three launches; their values against
-    the oracle's int8 forms are test_moe_ffn_step_int8's."""
+    bits too; kq_moe_ffn_last_path tells which form ran.  q5k takes Q5_K
+    experts; the _i8 cases take the experts in the int8-activation mode
+    (type | KQ_INT8_ACT), whose batch-1 step also runs in three launches;
+    their values against the oracle's int8 forms are
+    test_moe_ffn_step_int8's."""
     i8 = case.endswith("_i8")
     base = case[:-3] if i8 else case
+    qtype = {"q5k": 13, "q3k": 11, "q80": 8}.get(base, TYPE_Q4_K)
     H, F, E, k = {"config": (2048, 768, 128, 8), "q6k_down": (1024, 512, 64, 4),
                   "parts16": (1024, 256, 32, 8), "grid37": (2048, 768, 128, 8),
-                  "e512": (1024, 256, 512, 4), "wide_ff": (256, 8192, 16, 8)}[base]
-    d = make_layer(H, F, E, k, 9700)
+                  "e512": (1024, 256, 512, 4), "wide_ff": (256, 8192, 16, 8),
+                  "q5k": (1024, 512, 64, 4), "q3k": (1024, 512, 64, 4),
+                  "q80": (1024, 512, 64, 4)}[base]
+    d = make_layer(H, F, E, k, 9700, qtype=qtype)
     if base == "q6k_down":
         d["down_type"] = 14
         d["down"] = synth.tensor(14, E * H, F, 9704)
@@ -298,7 +302,7 @@ def test_moe_ffn_fused_matches_split(port, case, kq_env):
         kq_env(KQ_GRID=37)
     print(f"moe ffn fused vs split: {case}", flush=True)
     fused = run_step(d, xn, x0, 1)
-    want_fused = base in ("config", "q6k_down", "parts16")
+    want_fused = base in ("config", "q6k_down", "parts16", "q5k", "q3k", "q80")
     assert bool(fused["path"] & K.FFN_FUSED_B1) == want_fused, fused["path"]
     kq_env(KQ_MOE_FFN_SPLIT=1)
     split = run_step(d, xn, x0, 1)
