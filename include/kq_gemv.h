@@ -461,12 +461,14 @@ int64_t kq_moe_ffn_workspace_bytes(const kq_moe_ffn* f, int B);
  * steps as above.  No allocation: work is caller-provided device memory of
  * kq_moe_ffn_workspace_bytes.  B <= KQ_MOE_MAX_TOKENS, k <= KQ_MAX_GROUPS,
  * n_embed and n_ff multiples of 256.  Replaces the FFN half of
- * moe_forward_one_token / moe_forward_b after moe_rmsnorm.  At B = 1 (gate
- * and up of one type and stride, 2k <= KQ_MAX_GROUPS, n_experts <= 256,
- * n_embed and n_ff multiples of the CU count) the step runs in three
+ * moe_forward_one_token / moe_forward_b after moe_rmsnorm.  At B = 1 (gate,
+ * up and down of k-quant block types or Q8_0, exact or in the int8 mode;
+ * gate and up of one type and stride, 2k <= KQ_MAX_GROUPS, n_experts <=
+ * 256, n_embed and n_ff multiples of the CU count) the step runs in three
  * launches with the same results; the workspace then holds the
  * activations but not the probabilities or the gate, up and down outputs.
- * At B > 1 (core gate, up and down types) the grouped gate+up launch stores
+ * At B > 1 (block types of the multi-x kernel: every exact block type, and
+ * Q5_K, Q3_K, Q8_0 in the int8 mode) the grouped gate+up launch stores
  * its expert-run tables in the workspace and the down launch loads them
  * instead of grouping the selection again, with the same results.  Where
  * a launch groups the selection in a launch of its own (run tables too
