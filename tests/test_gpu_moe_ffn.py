@@ -392,7 +392,8 @@ def test_moe_ffn_never_grows_library_scratch(port, case, kq_env):
     assert np.abs(got["x"] - full["x"]).max() <= 1e-4 * contrib
 
 
-@pytest.mark.parametrize("qtype,B", [(TYPE_Q4_K, 1), (TYPE_Q4_K, 3), (14, 3), (13, 3), (8, 3)])
+@pytest.mark.parametrize("qtype,B", [(TYPE_Q4_K, 1), (TYPE_Q4_K, 3), (14, 3), (13, 3), (8, 3),
+                                     (14, 1), (13, 1), (11, 1), (8, 1)])
 def test_moe_ffn_step_int8(port, qtype, B):
     """The step with experts in the int8-activation mode (gate, up and down
     types | KQ_INT8_ACT; F32 router): sel is the oracle's top-k of the
